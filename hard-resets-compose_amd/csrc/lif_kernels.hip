@@ -1,0 +1,779 @@
+// Hard-reset LIF kernels for MI355X (gfx950): serial / replay forward, serial /
+// replay adjoint, chunk-map build, carry, on-device repair, affine-scan backward.
+//
+// Layout: I, U, S, GS, GU, Lam are time-major [T, N] fp32 (element (t, n) at
+// t*N + n).  One lane owns one neuron; a wave64 covers 64 consecutive neurons,
+// so every time row is one contiguous 256-byte access per wave.  Per-chunk
+// arrays are [M, N] and map slots [M, K, N] (neuron-contiguous, coalesced).
+#include "lsh_abi.h"
+#include "lsh_common.h"
+
+namespace lsh {
+
+// ---------------------------------------------------------------------------------------
+// workspace header reset: clears the counters and advances the look-back epoch.
+__global__ void k_ws_header_reset(WsHeader* h) {
+  unsigned int* w = reinterpret_cast<unsigned int*>(h);
+  const int epoch_word = (int)(offsetof(WsHeader, epoch) / 4);
+  const int t = threadIdx.x;
+  if (t < (int)(sizeof(WsHeader) / 4) && t != epoch_word) w[t] = 0u;
+  if (t == 0) h->epoch = h->epoch + 1u;
+}
+
+// ---------------------------------------------------------------------------------------
+// Forward over a segment of Ls steps from a given start state, D-step register tiles with
+// the next tile's loads in flight while the current tile is computed.
+//   serial forward: one segment (M = 1, Ls = T, starts = u0);
+//   scan replay   : M = T / C segments of Ls = C steps, starts = carried chunk entries.
+// Follows triton_lif.py:354-379 (fwd_tiled_kernel) and :152-165 (replay_kernel).
+template <int D>
+__global__ __launch_bounds__(64) void k_lif_fwd(const float* __restrict__ I,
+                                                const float* __restrict__ starts,
+                                                float* __restrict__ U, float* __restrict__ S,
+                                                float* __restrict__ ends, int64_t N, int64_t Ls,
+                                                int NB, float beta, float theta, float u_r) {
+  const int64_t m = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - m * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  if (n >= N) return;
+  float u = starts[m * N + n];
+  const size_t base = (size_t)m * (size_t)Ls * (size_t)N + (size_t)n;
+  const float* __restrict__ Ip = I + base;
+  float* __restrict__ Up = U + base;
+  float* __restrict__ Sp = S + base;
+  const int64_t nt = Ls / D;
+  float xa[D];
+  if (nt > 0) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) xa[j] = Ip[(size_t)j * N];
+  }
+  for (int64_t b = 0; b < nt; ++b) {
+    float xb[D];
+    const bool more = b + 1 < nt;
+    if (more) {
+      const float* __restrict__ In = Ip + (size_t)(b + 1) * D * N;
+#pragma unroll
+      for (int j = 0; j < D; ++j) xb[j] = In[(size_t)j * N];
+    }
+    float* __restrict__ Ub = Up + (size_t)b * D * N;
+    float* __restrict__ Sb = Sp + (size_t)b * D * N;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      bool s;
+      u = lif_step(u, xa[j], beta, theta, u_r, s);
+      st_nt(Ub + (size_t)j * N, u);
+      st_nt(Sb + (size_t)j * N, s ? 1.0f : 0.0f);
+    }
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) xa[j] = xb[j];
+    }
+  }
+  for (int64_t t = nt * D; t < Ls; ++t) {
+    bool s;
+    u = lif_step(u, Ip[(size_t)t * N], beta, theta, u_r, s);
+    st_nt(Up + (size_t)t * N, u);
+    st_nt(Sp + (size_t)t * N, s ? 1.0f : 0.0f);
+  }
+  if (ends) ends[m * N + n] = u;
+}
+
+// ---------------------------------------------------------------------------------------
+// Reverse sweep of the adjoint over a segment of Ls steps.
+//   COMPOSE = false: lam_t = b_t + a_t*lam_{t+1} from lam_end (or 0), writes Lam
+//                    (triton_lif.py:383-418 bwd_tiled_kernel, :1088-1127 bwd_tiled_pf_kernel);
+//   COMPOSE = true : composes the segment's affine map lam_start = P*lam_end + Q
+//                    (triton_lif.py:422-457 bwd_chunk_tiled_kernel).
+// Coefficients (triton_lif.py:43-50 _coef): v = beta*u_{t-1} + x_t, sg = surrogate'(v-theta),
+// J = 1 - s_t (+ (u_r - v)*sg when the reset is not detached), a = beta*J, b = gs*sg + J*gu.
+template <int D, bool COMPOSE, bool DETACH, bool HAS_GU>
+__global__ __launch_bounds__(64) void k_lif_bwd(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ U,
+    const float* __restrict__ S, const float* __restrict__ GS, const float* __restrict__ GU,
+    const float* __restrict__ lam_end, float* __restrict__ Lam, float* __restrict__ PA,
+    float* __restrict__ PB, int64_t N, int64_t Ls, int NB, float beta, float theta, float u_r,
+    float alpha) {
+  const int64_t m = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - m * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  if (n >= N) return;
+  const float u0n = u0[n];
+  float lam = (!COMPOSE && lam_end) ? lam_end[m * N + n] : 0.0f;
+  float P = 1.0f, Q = 0.0f;
+  const int64_t t_begin = m * Ls;
+  const int64_t nt = Ls / D;
+
+  auto coef = [&](float up, float x, float s, float gs, float gu, float& a, float& bb) {
+    const float v = lif_v(up, x, beta);
+    const float sg = surrogate(v, theta, alpha);
+    float J = 1.0f - s;
+    if (!DETACH) J = J + (u_r - v) * sg;
+    a = beta * J;
+    bb = HAS_GU ? gs * sg + J * gu : gs * sg;
+  };
+  auto uprev = [&](int64_t t) -> float { return t > 0 ? U[(size_t)(t - 1) * N + n] : u0n; };
+
+  // the highest `rem` steps first (segment lengths that are not a multiple of D)
+  for (int64_t t = t_begin + Ls - 1; t >= t_begin + nt * D; --t) {
+    const size_t o = (size_t)t * N + n;
+    float a, bb;
+    coef(uprev(t), I[o], S[o], GS[o], HAS_GU ? GU[o] : 0.0f, a, bb);
+    if (COMPOSE) {
+      Q = bb + a * Q;
+      P = a * P;
+    } else {
+      lam = bb + a * lam;
+      st_nt(Lam + o, lam);
+    }
+  }
+  if (nt == 0) {
+    if (COMPOSE) {
+      PA[m * N + n] = P;
+      PB[m * N + n] = Q;
+    }
+    return;
+  }
+  float xa[D], sa[D], ga[D], ha[D], pa[D];
+  auto load_tile = [&](int64_t b, float* x, float* s, float* g, float* h, float* p) {
+    const int64_t t0 = t_begin + b * D;
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      const size_t o = (size_t)(t0 + j) * N + n;
+      x[j] = I[o];
+      s[j] = S[o];
+      g[j] = GS[o];
+      h[j] = HAS_GU ? GU[o] : 0.0f;
+      p[j] = uprev(t0 + j);
+    }
+  };
+  load_tile(nt - 1, xa, sa, ga, ha, pa);
+  for (int64_t b = nt - 1; b >= 0; --b) {
+    float xb[D], sb[D], gb[D], hb[D], pb[D];
+    const bool more = b > 0;
+    if (more) load_tile(b - 1, xb, sb, gb, hb, pb);
+    const int64_t t0 = t_begin + b * D;
+#pragma unroll
+    for (int jj = 0; jj < D; ++jj) {
+      const int j = D - 1 - jj;
+      float a, bb;
+      coef(pa[j], xa[j], sa[j], ga[j], ha[j], a, bb);
+      if (COMPOSE) {
+        Q = bb + a * Q;
+        P = a * P;
+      } else {
+        lam = bb + a * lam;
+        st_nt(Lam + (size_t)(t0 + j) * N + n, lam);
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        xa[j] = xb[j];
+        sa[j] = sb[j];
+        ga[j] = gb[j];
+        ha[j] = hb[j];
+        pa[j] = pb[j];
+      }
+    }
+  }
+  if (COMPOSE) {
+    PA[m * N + n] = P;
+    PB[m * N + n] = Q;
+  }
+}
+
+// Reverse carry over chunk aggregates: LamEnd[m] = lam_{(m+1)C}; lam <- Q + P*lam
+// (triton_lif.py:198-208 bwd_carry_kernel).
+__global__ __launch_bounds__(64) void k_lif_bwd_carry(const float* __restrict__ PA,
+                                                      const float* __restrict__ PB,
+                                                      float* __restrict__ lam_end, int64_t N,
+                                                      int M) {
+  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
+  if (n >= N) return;
+  float lam = 0.0f;
+  for (int m = M - 1; m >= 0; --m) {
+    const size_t o = (size_t)m * N + n;
+    lam_end[o] = lam;
+    lam = PB[o] + PA[o] * lam;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Chunk-map build.  Per (chunk, neuron), one pass over the chunk's C inputs computes
+//   (a) the min-affine envelope map l -> min(c, a*l + b) of l -> min(u_r, beta*l + x)
+//       (triton_lif.py:699-719 env_chunk_kernel; lemma paper/main.tex:266-272), and
+//   (b) the piecewise map u_start -> u_end with capacity KMAX: affine part (A, B), breakpoints
+//       appended in descending order with their constants (triton_lif.py:737-779
+//       build3_kernel; fast.py:148-183).
+// The reference prunes a new breakpoint z unless z < xmin, z <= hi and xmin > lo, where lo
+// is the envelope bound of the chunk entry.  That bound depends on the preceding chunks, so
+// this pass prunes with hi only and records whether a (K+1)-th breakpoint appeared.  The
+// breakpoints form one descending sequence either way, so the reference's map is the prefix
+// of this one up to and including the first breakpoint <= lo, and its overflow flag is
+// "a (K+1)-th breakpoint appeared and all K stored ones are > lo"; the carry applies that
+// truncation once lo is known (k_lif_carry), which removes the separate envelope pass.
+template <int KMAX, int D>
+__global__ __launch_bounds__(64) void k_lif_build(
+    const float* __restrict__ I, const float* __restrict__ u0, float* __restrict__ EC,
+    float* __restrict__ EA, float* __restrict__ EB, float* __restrict__ MA, float* __restrict__ MB,
+    int* __restrict__ CNT, int* __restrict__ OVFRAW, float* __restrict__ MX, float* __restrict__ MC,
+    int64_t N, int C, int NB, int K, float beta, float theta, float u_r) {
+  const int64_t m = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - m * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  const bool valid = n < N;
+  const int64_t nn = valid ? n : 0;  // invalid lanes run on neuron 0 and store nothing
+  const float hi = fmaxf(u0[nn], fmaxf(theta, u_r));
+  float ec = INFINITY, ea = 1.0f, eb = 0.0f;
+  float A = 1.0f, B = 0.0f, xmin = INFINITY;
+  int cnt = 0;
+  bool ovf = false;
+  int wcnt = 0;  // wave-uniform upper bound of cnt
+  float xd[KMAX], cd[KMAX];
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) {
+    xd[i] = INFINITY;
+    cd[i] = 0.0f;
+  }
+  const float* __restrict__ Ip = I + (size_t)m * C * N + nn;
+
+  auto step = [&](float x) {
+    // (a) envelope
+    ec = fminf(u_r, lif_v(ec, x, beta));
+    ea = beta * ea;
+    eb = lif_v(eb, x, beta);
+    // (b) existing constants pushed through the step (same arithmetic as the serial step)
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+      if (i < wcnt) {
+        const float v = lif_v(cd[i], x, beta);
+        cd[i] = v >= theta ? u_r : v;
+      }
+    }
+    // preimage of the threshold under the affine part: beta*(A*u + B) + x >= theta
+    const float num = (theta - x) - beta * B;
+    const float den = beta * A;
+    const float z = den == 0.0f ? (num > 0.0f ? INFINITY : -INFINITY) : num / den;
+    bool nw = (z < xmin) && (z <= hi);
+    if (nw && cnt >= K) ovf = true;
+    nw = nw && (cnt < K);
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+      if (i <= wcnt && i < KMAX) {
+        const bool put = nw && (i == cnt);
+        xd[i] = put ? z : xd[i];
+        cd[i] = put ? u_r : cd[i];
+      }
+    }
+    if (__ballot(nw && cnt == wcnt) != 0ull) ++wcnt;
+    cnt += nw ? 1 : 0;
+    xmin = nw ? z : xmin;
+    A = beta * A;
+    B = lif_v(B, x, beta);
+  };
+
+  const int nt = C / D;
+  float xa[D];
+  if (nt > 0) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) xa[j] = Ip[(size_t)j * N];
+  }
+  for (int b = 0; b < nt; ++b) {
+    float xb[D];
+    const bool more = b + 1 < nt;
+    if (more) {
+      const float* __restrict__ In = Ip + (size_t)(b + 1) * D * N;
+#pragma unroll
+      for (int j = 0; j < D; ++j) xb[j] = In[(size_t)j * N];
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j) step(xa[j]);
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) xa[j] = xb[j];
+    }
+  }
+  for (int t = nt * D; t < C; ++t) step(Ip[(size_t)t * N]);
+
+  if (!valid) return;
+  const size_t o = (size_t)m * N + n;
+  EC[o] = ec;
+  EA[o] = ea;
+  EB[o] = eb;
+  MA[o] = A;
+  MB[o] = B;
+  CNT[o] = cnt;
+  OVFRAW[o] = ovf ? 1 : 0;
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) {
+    if (i < K) {
+      const size_t os = ((size_t)m * K + i) * N + n;
+      MX[os] = xd[i];
+      MC[os] = cd[i];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Sequential carry over the M chunks of each neuron (triton_lif.py:579-606 carry2_kernel,
+// :723-733 env_carry_kernel):
+//   Lo[m] = l - 1e-5*(|l| + 1), l <- min(c, a*l + b)         (envelope bound of chunk entry)
+//   (or one caller-given bound per neuron: the v1/v2 scans prune with the loose global
+//    state_bounds, triton_lif.py:238-243, :262-295, :609-642)
+//   map m truncated at the first breakpoint <= Lo[m] (see k_lif_build), overflow if none
+//   Starts[m] = u;  u <- (#{xd > u} == n) ? A*u + B : cd[#{xd > u}]
+//   overflowed map: u <- C serial steps from u (same arithmetic as the replay)
+// Accumulates the overflow count and kept-breakpoint sum / max for the stats.
+template <int KMAX>
+__global__ __launch_bounds__(64) void k_lif_carry(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ EC,
+    const float* __restrict__ EA, const float* __restrict__ EB, const float* __restrict__ MA,
+    const float* __restrict__ MB, const int* __restrict__ CNT, const int* __restrict__ OVFRAW,
+    const float* __restrict__ MX, const float* __restrict__ MC,
+    const float* __restrict__ lo_neuron, float* __restrict__ LO, int* __restrict__ MN,
+    int* __restrict__ OVF, float* __restrict__ starts, WsHeader* hdr, int64_t N, int M, int C,
+    int K, float beta, float theta, float u_r) {
+  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
+  const bool valid = n < N;
+  unsigned long long ovf_acc = 0, pcs_acc = 0;
+  int pmax = 0;
+  if (valid) {
+    const float margin = 1e-5f;
+    float l = u0[n];
+    float u = l;
+    for (int m = 0; m < M; ++m) {
+      const size_t o = (size_t)m * N + n;
+      const float lo = lo_neuron ? lo_neuron[n] : l - margin * (fabsf(l) + 1.0f);
+      LO[o] = lo;
+      l = fminf(EC[o], __fadd_rn(__fmul_rn(EA[o], l), EB[o]));
+      starts[o] = u;
+      const int cnt = CNT[o];
+      const bool ovfr = OVFRAW[o] != 0;
+      float xd[KMAX], cd[KMAX];
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i) {
+        if (i < K) {
+          const size_t os = ((size_t)m * K + i) * N + n;
+          xd[i] = MX[os];
+          cd[i] = MC[os];
+        } else {
+          xd[i] = -INFINITY;
+          cd[i] = 0.0f;
+        }
+      }
+      int gt = 0;
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i) gt += (i < cnt && xd[i] > lo) ? 1 : 0;
+      const int ne = min(cnt, gt + 1);
+      const bool ovf = ovfr && gt == cnt;
+      MN[o] = ne;
+      OVF[o] = ovf ? 1 : 0;
+      int k = 0;
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i) k += (i < ne && xd[i] > u) ? 1 : 0;
+      float cval = 0.0f;
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i) cval = (i == k) ? cd[i] : cval;
+      float nu = (k == ne) ? __fadd_rn(__fmul_rn(MA[o], u), MB[o]) : cval;
+      if (ovf) {  // rare: serial fallback through this chunk
+        float w = u;
+        const float* __restrict__ Ip = I + (size_t)m * C * N + n;
+        for (int j = 0; j < C; ++j) {
+          bool s;
+          w = lif_step(w, Ip[(size_t)j * N], beta, theta, u_r, s);
+        }
+        nu = w;
+      }
+      u = nu;
+      ovf_acc += ovf ? 1ull : 0ull;
+      pcs_acc += (unsigned long long)ne;
+      pmax = max(pmax, ne);
+    }
+  }
+  ovf_acc = wave_sum_u64(ovf_acc);
+  pcs_acc = wave_sum_u64(pcs_acc);
+  pmax = wave_max_i(pmax);
+  if (threadIdx.x == 0) {
+    atomicAdd(&hdr->ovf_count, ovf_acc);
+    atomicAdd(&hdr->pieces_sum, pcs_acc);
+    atomicMax(&hdr->pieces_max, (unsigned int)pmax);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// On-device repair (triton_lif.py:804-811): Jacobi rounds
+//   Starts[m] <- (m == 0 ? u0 : Ends[m-1]); replay the chunks whose start changed
+// until nothing changes or `R` rounds ran.  Neurons are independent, so one workgroup owns
+// the M chunks of 64 neurons and runs the rounds with workgroup barriers only, with no host
+// synchronization.  Only chunks whose start changed are replayed, and only successors of
+// chunks whose end changed are re-checked, through two work lists of (chunk, lane) entries.
+// Round r gives the same states as the reference's r-th full re-replay; the round count
+// (max over neurons) is the reference's repair_iters.
+__global__ __launch_bounds__(256) void k_lif_repair(const float* __restrict__ I,
+                                                    float* __restrict__ U, float* __restrict__ S,
+                                                    float* __restrict__ starts,
+                                                    float* __restrict__ ends, int* __restrict__ list0,
+                                                    int* __restrict__ list1, WsHeader* hdr,
+                                                    int64_t N, int M, int C, int64_t R,
+                                                    float beta, float theta, float u_r) {
+  __shared__ int s_nd, s_nc;
+  const int nb = blockIdx.x;
+  const int tid = threadIdx.x;
+  const size_t cap = (size_t)M * WAVE;
+  int* __restrict__ dl = list0 + (size_t)nb * cap;  // dirty chunks of the current round
+  int* __restrict__ cl = list1 + (size_t)nb * cap;  // successors of chunks whose end changed
+  if (tid == 0) s_nd = 0;
+  __syncthreads();
+  for (int e = tid + WAVE; e < M * WAVE; e += blockDim.x) {
+    const int m = e / WAVE;
+    const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
+    if (n < N && ends[(size_t)(m - 1) * N + n] != starts[(size_t)m * N + n]) {
+      dl[atomicAdd(&s_nd, 1)] = e;
+    }
+  }
+  __syncthreads();
+  int64_t rounds = 0;
+  while (true) {
+    const int nd = s_nd;
+    if (nd == 0 || rounds >= R) break;
+    ++rounds;
+    for (int i = tid; i < nd; i += blockDim.x) {
+      const int e = dl[i];
+      const int m = e / WAVE;
+      const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
+      starts[(size_t)m * N + n] = ends[(size_t)(m - 1) * N + n];
+    }
+    __syncthreads();
+    if (tid == 0) s_nc = 0;
+    __syncthreads();
+    for (int i = tid; i < nd; i += blockDim.x) {
+      const int e = dl[i];
+      const int m = e / WAVE;
+      const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
+      float u = starts[(size_t)m * N + n];
+      const size_t base = (size_t)m * C * N + n;
+      for (int j = 0; j < C; ++j) {
+        bool s;
+        u = lif_step(u, I[base + (size_t)j * N], beta, theta, u_r, s);
+        U[base + (size_t)j * N] = u;
+        S[base + (size_t)j * N] = s ? 1.0f : 0.0f;
+      }
+      const size_t oe = (size_t)m * N + n;
+      if (u != ends[oe]) {
+        ends[oe] = u;
+        if (m + 1 < M) cl[atomicAdd(&s_nc, 1)] = e + WAVE;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) s_nd = 0;
+    __syncthreads();
+    const int nc = s_nc;
+    for (int i = tid; i < nc; i += blockDim.x) {
+      const int e = cl[i];
+      const int m = e / WAVE;
+      const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
+      if (ends[(size_t)(m - 1) * N + n] != starts[(size_t)m * N + n]) dl[atomicAdd(&s_nd, 1)] = e;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) atomicMax(&hdr->repair_iters, (unsigned int)rounds);
+}
+
+// ---------------------------------------------------------------------------------------
+// host-side launch helpers
+template <int D>
+static void launch_fwd(const float* I, const float* starts, float* U, float* S, float* ends,
+                       int64_t N, int64_t Ls, int64_t M, float beta, float theta, float u_r,
+                       hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  hipLaunchKernelGGL(k_lif_fwd<D>, dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, starts, U, S,
+                     ends, N, Ls, NB, beta, theta, u_r);
+}
+
+static void launch_fwd_auto(const float* I, const float* starts, float* U, float* S, float* ends,
+                            int64_t N, int64_t Ls, int64_t M, float beta, float theta, float u_r,
+                            hipStream_t st) {
+  if (Ls >= 32)
+    launch_fwd<16>(I, starts, U, S, ends, N, Ls, M, beta, theta, u_r, st);
+  else
+    launch_fwd<4>(I, starts, U, S, ends, N, Ls, M, beta, theta, u_r, st);
+}
+
+template <bool COMPOSE, bool DETACH, bool HAS_GU>
+static void launch_bwd3(const float* I, const float* u0, const float* U, const float* S,
+                        const float* GS, const float* GU, const float* lam_end, float* Lam, float* PA,
+                        float* PB, int64_t N, int64_t Ls, int64_t M, float beta, float theta,
+                        float u_r, float alpha, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  constexpr int D = 4;
+  hipLaunchKernelGGL((k_lif_bwd<D, COMPOSE, DETACH, HAS_GU>), dim3((unsigned)(M * NB)), dim3(WAVE), 0,
+                     st, I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, N, Ls, NB, beta, theta, u_r, alpha);
+}
+
+template <bool COMPOSE>
+static void launch_bwd(const float* I, const float* u0, const float* U, const float* S,
+                       const float* GS, const float* GU, const float* lam_end, float* Lam, float* PA,
+                       float* PB, int64_t N, int64_t Ls, int64_t M, float beta, float theta,
+                       float u_r, float alpha, bool detach, hipStream_t st) {
+  const bool has_gu = GU != nullptr;
+  if (detach) {
+    if (has_gu)
+      launch_bwd3<COMPOSE, true, true>(I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, N, Ls, M, beta,
+                                       theta, u_r, alpha, st);
+    else
+      launch_bwd3<COMPOSE, true, false>(I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, N, Ls, M, beta,
+                                        theta, u_r, alpha, st);
+  } else {
+    if (has_gu)
+      launch_bwd3<COMPOSE, false, true>(I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, N, Ls, M, beta,
+                                        theta, u_r, alpha, st);
+    else
+      launch_bwd3<COMPOSE, false, false>(I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, N, Ls, M, beta,
+                                         theta, u_r, alpha, st);
+  }
+}
+
+static void v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3_layout* L) {
+  const int64_t M = T / C;
+  const size_t mn = (size_t)M * (size_t)N * 4;
+  const size_t nb = (size_t)((N + WAVE - 1) / WAVE);
+  Carver c;
+  L->EC = c.take(mn);
+  L->EA = c.take(mn);
+  L->EB = c.take(mn);
+  L->MA = c.take(mn);
+  L->MB = c.take(mn);
+  L->CNT = c.take(mn);
+  L->OVFRAW = c.take(mn);
+  L->MX = c.take(mn * (size_t)K);
+  L->MC = c.take(mn * (size_t)K);
+  L->LO = c.take(mn);
+  L->MN = c.take(mn);
+  L->OVF = c.take(mn);
+  L->STARTS = c.take(mn);
+  L->ENDS = c.take(mn);
+  L->LIST0 = c.take(nb * (size_t)M * WAVE * 4);
+  L->LIST1 = c.take(nb * (size_t)M * WAVE * 4);
+  L->total = c.off;
+}
+
+template <int KMAX>
+static void launch_build_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
+                               const lsh_v3_layout& L, int64_t N, int M, int C, int K, float beta,
+                               float theta, float u_r, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
+  auto Iq = [&](size_t off) { return reinterpret_cast<int*>(ws + off); };
+  if (C >= 16)
+    hipLaunchKernelGGL((k_lif_build<KMAX, 8>), dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, u0,
+                       F(L.EC), F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
+                       F(L.MC), N, C, NB, K, beta, theta, u_r);
+  else
+    hipLaunchKernelGGL((k_lif_build<KMAX, 1>), dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, u0,
+                       F(L.EC), F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
+                       F(L.MC), N, C, NB, K, beta, theta, u_r);
+  hipLaunchKernelGGL((k_lif_carry<KMAX>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, F(L.EC),
+                     F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX), F(L.MC),
+                     lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS), reinterpret_cast<WsHeader*>(ws), N,
+                     M, C, K, beta, theta, u_r);
+}
+
+}  // namespace lsh
+
+using namespace lsh;
+
+// ---------------------------------------------------------------------------------------
+// C ABI
+extern "C" int lsh_abi_version(void) { return LSH_ABI_VERSION; }
+extern "C" const char* lsh_arch(void) { return "gfx950"; }
+extern "C" const char* lsh_status_string(int status) {
+  switch (status) {
+    case LSH_OK: return "ok";
+    case LSH_ERR_ARG: return "invalid argument (null pointer or bad scalar)";
+    case LSH_ERR_SHAPE: return "unsupported shape (T, N, C, K or G out of range)";
+    case LSH_ERR_DIVISIBILITY: return "T must be divisible by the chunk length (and M by G)";
+    case LSH_ERR_WORKSPACE: return "workspace too small or not 256-byte aligned";
+    case LSH_ERR_HIP: return "HIP launch/runtime error";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int lsh_lif_serial_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
+                                  int64_t N, float beta, float theta, float u_r, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S)) return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  if (T >= 32)
+    launch_fwd<32>(I, u0, U, S, nullptr, N, T, 1, beta, theta, u_r, st);
+  else
+    launch_fwd<4>(I, u0, U, S, nullptr, N, T, 1, beta, theta, u_r, st);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" int lsh_lif_serial_bwd(const float* I, const float* u0, const float* U, const float* S,
+                                  const float* GS, const float* GU, float* Lam, int64_t T,
+                                  int64_t N, float beta, float theta, float u_r, float alpha,
+                                  int detach, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(Lam))
+    return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  launch_bwd<false>(I, u0, U, S, GS, GU, nullptr, Lam, nullptr, nullptr, N, T, 1, beta, theta, u_r,
+                    alpha, detach != 0, (hipStream_t)stream);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+static int v3_check(int64_t T, int64_t N, int C, int K) {
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C < 1 || K < 1 || K > 64) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  if ((T / C) * ((N + WAVE - 1) / WAVE) > ((int64_t)1 << 31) - 1) return LSH_ERR_SHAPE;
+  return LSH_OK;
+}
+
+extern "C" int lsh_lif_scan_v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3_layout* out) {
+  if (bad_ptr(out)) return LSH_ERR_ARG;
+  const int rc = v3_check(T, N, C, K);
+  if (rc != LSH_OK) return rc;
+  v3_layout(T, N, C, K, out);
+  return LSH_OK;
+}
+
+extern "C" size_t lsh_lif_scan_v3_workspace(int64_t T, int64_t N, int C, int K) {
+  if (v3_check(T, N, C, K) != LSH_OK) return 0;
+  lsh_v3_layout L;
+  v3_layout(T, N, C, K, &L);
+  return L.total;
+}
+
+static int scan2_fwd(const float* I, const float* u0, const float* lo_neuron, float* U, float* S,
+                     int64_t T, int64_t N, float beta, float theta, float u_r, int C, int K,
+                     int64_t repair, void* ws, size_t ws_bytes, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
+  if (repair < 0) return LSH_ERR_ARG;
+  int rc = v3_check(T, N, C, K);
+  if (rc != LSH_OK) return rc;
+  lsh_v3_layout L;
+  v3_layout(T, N, C, K, &L);
+  if (ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0) return LSH_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  char* w = static_cast<char*>(ws);
+  hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, reinterpret_cast<WsHeader*>(w));
+  if (T == 0 || N == 0) {
+    LSH_CHECK_LAUNCH();
+    return LSH_OK;
+  }
+  const int M = (int)(T / C);
+  if (K <= 4)
+    launch_build_carry<4>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
+  else if (K <= 8)
+    launch_build_carry<8>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
+  else if (K <= 16)
+    launch_build_carry<16>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
+  else if (K <= 32)
+    launch_build_carry<32>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
+  else
+    launch_build_carry<64>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
+  float* starts = reinterpret_cast<float*>(w + L.STARTS);
+  float* ends = reinterpret_cast<float*>(w + L.ENDS);
+  launch_fwd_auto(I, starts, U, S, ends, N, C, M, beta, theta, u_r, st);
+  if (repair > 0 && M > 1) {
+    const int NB = (int)((N + WAVE - 1) / WAVE);
+    hipLaunchKernelGGL(k_lif_repair, dim3((unsigned)NB), dim3(256), 0, st, I, U, S, starts, ends,
+                       reinterpret_cast<int*>(w + L.LIST0), reinterpret_cast<int*>(w + L.LIST1),
+                       reinterpret_cast<WsHeader*>(w), N, M, C, repair, beta, theta, u_r);
+  }
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" int lsh_lif_scan_v3_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
+                                   int64_t N, float beta, float theta, float u_r, int C, int K,
+                                   int64_t repair, void* ws, size_t ws_bytes, void* stream) {
+  return scan2_fwd(I, u0, nullptr, U, S, T, N, beta, theta, u_r, C, K, repair, ws, ws_bytes,
+                   stream);
+}
+
+extern "C" int lsh_lif_scan_lo_fwd(const float* I, const float* u0, const float* lo, float* U,
+                                   float* S, int64_t T, int64_t N, float beta, float theta,
+                                   float u_r, int C, int K, int64_t repair, void* ws,
+                                   size_t ws_bytes, void* stream) {
+  if (bad_ptr(lo)) return LSH_ERR_ARG;
+  return scan2_fwd(I, u0, lo, U, S, T, N, beta, theta, u_r, C, K, repair, ws, ws_bytes, stream);
+}
+
+extern "C" int lsh_scan_stats_read(const void* ws, int64_t chunk_neurons, int64_t super_neurons,
+                                   int alif, lsh_scan_stats* out, void* stream) {
+  if (bad_ptr(ws) || bad_ptr(out) || chunk_neurons < 0 || super_neurons < 0) return LSH_ERR_ARG;
+  WsHeader h;
+  hipStream_t st = (hipStream_t)stream;
+  if (hipMemcpyAsync(&h, ws, sizeof(h), hipMemcpyDeviceToHost, st) != hipSuccess) return LSH_ERR_HIP;
+  if (hipStreamSynchronize(st) != hipSuccess) return LSH_ERR_HIP;
+  const double cn = chunk_neurons > 0 ? (double)chunk_neurons : 1.0;
+  const double sn = super_neurons > 0 ? (double)super_neurons : 1.0;
+  out->repair_iters = (int64_t)h.repair_iters;
+  out->overflow_frac = (double)h.ovf_count / cn;
+  if (alif) {
+    const unsigned long long miss = ((unsigned long long)h.miss_count_hi << 32) | h.miss_count_lo;
+    out->mean_pieces = (double)h.alif_pieces_sum / cn;
+    out->max_pieces = (int64_t)h.alif_pieces_max;
+    out->miss_frac = (double)miss / cn;
+    out->mean_lines = (double)h.lines_sum / cn;
+  } else {
+    out->mean_pieces = (double)h.pieces_sum / cn + 1.0;
+    out->max_pieces = (int64_t)h.pieces_max + 1;
+    out->miss_frac = 0.0;
+    out->mean_lines = 0.0;
+  }
+  out->super_overflow_frac = (double)h.super_ovf_count / sn;
+  out->super_mean_pieces = (double)h.super_pieces_sum / sn + 1.0;
+  out->super_max_pieces = (int64_t)h.super_pieces_max + 1;
+  return LSH_OK;
+}
+
+static int bwd_check(int64_t T, int64_t N, int C) {
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C < 1) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  if ((T / C) * ((N + WAVE - 1) / WAVE) > ((int64_t)1 << 31) - 1) return LSH_ERR_SHAPE;
+  return LSH_OK;
+}
+
+extern "C" size_t lsh_lif_scan_bwd_workspace(int64_t T, int64_t N, int C) {
+  if (bwd_check(T, N, C) != LSH_OK) return 0;
+  const size_t mn = (size_t)(T / C) * (size_t)N * 4;
+  return kWsHeaderBytes + 3 * align_up(mn, 256);
+}
+
+extern "C" int lsh_lif_scan_bwd(const float* I, const float* u0, const float* U, const float* S,
+                                const float* GS, const float* GU, float* Lam, int64_t T, int64_t N,
+                                float beta, float theta, float u_r, float alpha, int detach, int C,
+                                void* ws, size_t ws_bytes, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(Lam) ||
+      bad_ptr(ws))
+    return LSH_ERR_ARG;
+  const int rc = bwd_check(T, N, C);
+  if (rc != LSH_OK) return rc;
+  if (ws_bytes < lsh_lif_scan_bwd_workspace(T, N, C) ||
+      (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+    return LSH_ERR_WORKSPACE;
+  if (T == 0 || N == 0) return LSH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t M = T / C;
+  const size_t mn = align_up((size_t)M * (size_t)N * 4, 256);
+  char* w = static_cast<char*>(ws) + kWsHeaderBytes;
+  float* PA = reinterpret_cast<float*>(w);
+  float* PB = reinterpret_cast<float*>(w + mn);
+  float* LE = reinterpret_cast<float*>(w + 2 * mn);
+  launch_bwd<true>(I, u0, U, S, GS, GU, nullptr, nullptr, PA, PB, N, C, M, beta, theta, u_r, alpha,
+                   detach != 0, st);
+  hipLaunchKernelGGL(k_lif_bwd_carry, dim3((unsigned)((N + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, PA,
+                     PB, LE, N, (int)M);
+  launch_bwd<false>(I, u0, U, S, GS, GU, LE, Lam, nullptr, nullptr, N, C, M, beta, theta, u_r,
+                    alpha, detach != 0, st);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}

@@ -1,0 +1,61 @@
+// Internal glue shared by the HIP translation units: status codes, argument
+// checks and the workspace header layout.  The public declarations live in
+// include/lifscan_hip.h; this header re-includes it so the definitions are
+// checked against the declarations by the compiler.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/lifscan_hip.h"
+
+namespace lsh {
+
+#define LSH_CHECK_LAUNCH()                          \
+  do {                                              \
+    hipError_t e_ = hipGetLastError();              \
+    if (e_ != hipSuccess) return LSH_ERR_HIP;       \
+  } while (0)
+
+// Workspace header (first 256 bytes of every scan workspace).  Counters are
+// cleared by a kernel at the start of each call, so a caller may capture the
+// call in a HIP graph (no memset node).
+struct WsHeader {
+  unsigned long long ovf_count;        // chunk-neuron pairs whose map overflowed
+  unsigned long long pieces_sum;       // sum over chunk-neuron pairs of breakpoints kept
+  unsigned int pieces_max;             // max breakpoints kept
+  unsigned int repair_iters;           // Jacobi repair rounds performed (max over neurons)
+  unsigned long long super_ovf_count;  // three-level scan: super-chunk overflows
+  unsigned long long super_pieces_sum;
+  unsigned int super_pieces_max;
+  unsigned int miss_count_lo;          // ALIF: box misses (low/high words of a u64)
+  unsigned int miss_count_hi;
+  unsigned int lines_max;
+  unsigned long long lines_sum;        // ALIF: first-spike lines kept
+  unsigned long long alif_pieces_sum;  // ALIF: post-spike x-pieces kept
+  unsigned int alif_pieces_max;
+  unsigned int pad0;
+  unsigned long long ticket;           // dynamic tile ticket (look-back kernels)
+  unsigned int epoch;                  // per-call epoch for look-back status words
+  unsigned int pad1;
+};
+static_assert(sizeof(WsHeader) <= 256, "workspace header must fit in 256 bytes");
+constexpr size_t kWsHeaderBytes = 256;
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Carves consecutive 256-byte aligned arrays out of a workspace.
+struct Carver {
+  size_t off = kWsHeaderBytes;
+  size_t take(size_t bytes) {
+    size_t o = off;
+    off = align_up(off + bytes, 256);
+    return o;
+  }
+};
+
+__global__ void k_ws_header_reset(WsHeader* h);
+
+inline bool bad_ptr(const void* p) { return p == nullptr; }
+
+}  // namespace lsh

@@ -1,0 +1,71 @@
+// Shared device helpers for the MI355X (gfx950) hard-reset LIF / ALIF scan kernels.
+//
+// Numerics contract (every kernel in this library):
+//   * one canonical step arithmetic, two IEEE round-to-nearest operations:
+//       v = fl(fl(beta * u) + x);  s = v >= theta;  u' = s ? u_r : v
+//     (triton_lif.py:21-25 `_step`, fast.py:76-79).  No FMA contraction anywhere
+//     (built with -ffp-contract=off and the pragma below), so the serial
+//     kernel, the scan's replay, the overflow fallback and the map constants
+//     execute the identical instruction sequence and a plain fp32 CPU loop
+//     reproduces every bit.
+//   * fp32 denormals are kept (built with -fno-gpu-flush-denormals-to-zero).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#pragma clang fp contract(off)
+
+namespace lsh {
+
+constexpr int WAVE = 64;
+
+// LIF membrane update before the threshold test (triton_lif.py:22).
+__device__ __forceinline__ float lif_v(float u, float x, float beta) {
+  return __fadd_rn(__fmul_rn(beta, u), x);
+}
+
+// One hard-reset LIF step; returns the new state and writes the spike.
+__device__ __forceinline__ float lif_step(float u, float x, float beta, float theta, float u_r,
+                                          bool& s) {
+  const float v = lif_v(u, x, beta);
+  s = v >= theta;
+  return s ? u_r : v;
+}
+
+// Surrogate derivative alpha*sig*(1-sig), sig = 1/(1+exp(-alpha*(v-theta)))
+// (triton_lif.py:45-46).  Gradients are compared within a tolerance, so the
+// library expf is used as is.
+__device__ __forceinline__ float surrogate(float v, float theta, float alpha) {
+  const float sig = 1.0f / (1.0f + expf(-(alpha * (v - theta))));
+  return alpha * sig * (1.0f - sig);
+}
+
+// Streaming (non-temporal) accesses: U, S and Lam are written once and not
+// re-read by the same kernel, so they should not evict the inputs from L2/MALL.
+template <typename T>
+__device__ __forceinline__ void st_nt(T* p, T v) { __builtin_nontemporal_store(v, p); }
+template <typename T>
+__device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
+
+// Wave-level reductions (wave64).
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, WAVE));
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+__device__ __forceinline__ unsigned long long wave_sum_u64(unsigned long long v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+
+__device__ __forceinline__ bool same_bits(float a, float b) {
+  return __float_as_uint(a) == __float_as_uint(b);
+}
+
+}  // namespace lsh

@@ -1,0 +1,121 @@
+"""ctypes binding of liblifscan_hip.so (the C ABI declared in include/lifscan_hip.h).
+
+torch is imported first so that the HIP runtime it loads (SONAME libamdhip64.so.7) is the
+one the library binds to: streams and device pointers handed over by torch are then valid
+in the library.  There is no fallback: if the library is missing, every call raises.
+"""
+import ctypes
+import os
+
+import torch
+
+from . import _build
+
+_LIB = None
+
+LSH_OK = 0
+LSH_ERR_ARG = -1
+LSH_ERR_SHAPE = -2
+LSH_ERR_DIVISIBILITY = -3
+LSH_ERR_WORKSPACE = -4
+LSH_ERR_HIP = -5
+
+c_p = ctypes.c_void_p
+c_i64 = ctypes.c_int64
+c_f = ctypes.c_float
+c_i = ctypes.c_int
+c_sz = ctypes.c_size_t
+
+
+class ScanStats(ctypes.Structure):
+    _fields_ = [
+        ("repair_iters", ctypes.c_int64),
+        ("overflow_frac", ctypes.c_double),
+        ("mean_pieces", ctypes.c_double),
+        ("max_pieces", ctypes.c_int64),
+        ("super_overflow_frac", ctypes.c_double),
+        ("super_mean_pieces", ctypes.c_double),
+        ("super_max_pieces", ctypes.c_int64),
+        ("miss_frac", ctypes.c_double),
+        ("mean_lines", ctypes.c_double),
+    ]
+
+
+class V3Layout(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in (
+        "EC", "EA", "EB", "MA", "MB", "CNT", "OVFRAW", "MX", "MC", "LO", "MN", "OVF", "STARTS",
+        "ENDS", "LIST0", "LIST1", "total")]
+
+
+# name -> (restype, argtypes); mirrors include/lifscan_hip.h
+SIGNATURES = {
+    "lsh_abi_version": (c_i, []),
+    "lsh_arch": (ctypes.c_char_p, []),
+    "lsh_status_string": (ctypes.c_char_p, [c_i]),
+    "lsh_lif_serial_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_p]),
+    "lsh_lif_serial_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,
+                                 c_f, c_i, c_p]),
+    "lsh_lif_scan_v3_workspace": (c_sz, [c_i64, c_i64, c_i, c_i]),
+    "lsh_lif_scan_v3_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i, c_i64,
+                                  c_p, c_sz, c_p]),
+    "lsh_lif_scan_lo_fwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i,
+                                  c_i64, c_p, c_sz, c_p]),
+    "lsh_scan_stats_read": (c_i, [c_p, c_i64, c_i64, c_i, ctypes.POINTER(ScanStats), c_p]),
+    "lsh_lif_scan_v3_layout": (c_i, [c_i64, c_i64, c_i, c_i, ctypes.POINTER(V3Layout)]),
+    "lsh_lif_scan_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
+    "lsh_lif_scan_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f,
+                               c_i, c_i, c_p, c_sz, c_p]),
+}
+
+
+def lib_path():
+    return _build.LIB_PATH
+
+
+def lib():
+    """Load (once) and return the ctypes handle of liblifscan_hip.so."""
+    global _LIB
+    if _LIB is None:
+        path = lib_path()
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"HIP extension not built ({path} missing): run `python -c \"import "
+                f"__graft_entry__ as g; g.build()\"` or `python {_build.__file__}`")
+        L = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _LIB = L
+    return _LIB
+
+
+def check(rc, what):
+    if rc == LSH_OK:
+        return
+    msg = f"{what}: {lib().lsh_status_string(rc).decode()} (status {rc})"
+    if rc in (LSH_ERR_ARG, LSH_ERR_SHAPE, LSH_ERR_DIVISIBILITY):
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def stream_of(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def workspace(nbytes, device):
+    """Caller-owned workspace (the library never allocates); 256-byte aligned by torch."""
+    ws = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+    assert ws.data_ptr() % 256 == 0
+    return ws
+
+
+def read_stats(ws, chunk_neurons, super_neurons=0, alif=False):
+    st = ScanStats()
+    check(lib().lsh_scan_stats_read(ptr(ws), int(chunk_neurons), int(super_neurons), int(alif),
+                                    ctypes.byref(st), stream_of(ws)), "lsh_scan_stats_read")
+    return st

@@ -1,0 +1,463 @@
+"""Hard-reset LIF on MI355X: serial kernels, exact two/three-level map scans, affine-scan
+backward and the autograd layers, with the call signatures of the reference's
+``lifscan/triton_lif.py`` so that callers (``shdnet``, ``fit``, experiments) drop in unchanged.
+
+Every op runs hand-written HIP kernels of ``liblifscan_hip.so`` through its C ABI; there is
+no CPU or PyTorch fallback.  Layout: I is [T, N] fp32 contiguous (N = batch * neurons),
+element (t, n) at t*N + n.
+
+Triton tile keywords of the reference (BN, nw, BNc, nwc, BNr, D, nwr, BNg, nwg, num_warps,
+STAGES, CSTAGES) are accepted for signature compatibility and ignored: the HIP kernels pick
+their own tiles (one lane per neuron, register-prefetched time tiles).
+
+Numerics: every path uses the same fp32 step v = fl(fl(beta*u) + x) (no FMA), so the
+serial kernel, the scan's replay and its fallbacks agree bit for bit, and after repair the
+scan equals the serial recurrence exactly.
+"""
+import math
+
+import torch
+
+from . import _native as _n
+
+BN_DEFAULT = 128
+
+# auto dispatch thresholds (serial vs scan per pass); see auto_modes
+AUTO_FWD_MAX_N = 1024
+AUTO_FWD_MIN_T = 16384
+AUTO_BWD_MAX_N = 1024
+AUTO_BWD_MIN_T = 1024
+
+
+# ----------------------------------------------------------------------------- helpers
+def _f32(x):
+    """Scalar parameter as a Python float (the kernels take fp32)."""
+    if torch.is_tensor(x):
+        return float(x.detach().item())
+    return float(x)
+
+
+def _input(I):
+    if not torch.is_tensor(I) or I.dim() != 2:
+        raise ValueError("I must be a 2-D [T, N] tensor")
+    if I.device.type != "cuda":
+        raise ValueError("I must be a GPU (HIP) tensor")
+    if I.dtype != torch.float32:
+        raise ValueError("I must be float32")
+    return I.contiguous()
+
+
+def _vec(v, N, like, name="u0"):
+    if not torch.is_tensor(v):
+        v = torch.full((N,), float(v), device=like.device, dtype=torch.float32)
+    v = v.detach()
+    if v.numel() != N:
+        raise ValueError(f"{name} must have N={N} elements")
+    if v.device != like.device:
+        raise ValueError(f"{name} must be on {like.device}")
+    return v.reshape(N).to(torch.float32).contiguous()
+
+
+def _same(t, like, name):
+    if t is None:
+        return None
+    if t.shape != like.shape or t.device != like.device or t.dtype != torch.float32:
+        raise ValueError(f"{name} must be float32 {tuple(like.shape)} on {like.device}")
+    return t.contiguous()
+
+
+def _fill_stats(stats, st, v4=False):
+    if stats is None:
+        return
+    stats["repair_iters"] = int(st.repair_iters)
+    stats["overflow_frac"] = float(st.overflow_frac)
+    stats["mean_pieces"] = float(st.mean_pieces)
+    if v4:
+        stats["super_overflow_frac"] = float(st.super_overflow_frac)
+        stats["super_mean_pieces"] = float(st.super_mean_pieces)
+        stats["super_max_pieces"] = int(st.super_max_pieces)
+    else:
+        stats["max_pieces"] = int(st.max_pieces)
+
+
+# ----------------------------------------------------------------------------- serial
+def serial_forward(I, beta, theta, u_r, u0, BN=BN_DEFAULT):
+    """Serial forward (triton_lif.py:246-251) -> (U, S), both [T, N] fp32."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    U = torch.empty_like(I)
+    S = torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        _n.check(_n.lib().lsh_lif_serial_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
+                                             _f32(beta), _f32(theta), _f32(u_r), _n.stream_of(I)),
+                 "lsh_lif_serial_fwd")
+    return U, S
+
+
+def serial_forward_tiled(I, beta, theta, u_r, u0, BN=32, D=4, num_warps=1):
+    """Time-tiled serial forward (triton_lif.py:460-466); same kernel as serial_forward."""
+    return serial_forward(I, beta, theta, u_r, u0)
+
+
+def serial_forward_auto(I, beta, theta, u_r, u0):
+    """Tuned serial forward (triton_lif.py:1221-1225)."""
+    return serial_forward(I, beta, theta, u_r, u0)
+
+
+def serial_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, BN=BN_DEFAULT):
+    """Serial adjoint (triton_lif.py:254-259) -> Lam [T, N] (= dL/dI).  GU may be None (zeros)."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    U, S, GS = _same(U, I, "U"), _same(S, I, "S"), _same(GS, I, "GS")
+    GU = _same(GU, I, "GU")
+    Lam = torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        _n.check(_n.lib().lsh_lif_serial_bwd(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS), _n.ptr(GU), _n.ptr(Lam), T, N,
+            _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), int(bool(detach)), _n.stream_of(I)),
+            "lsh_lif_serial_bwd")
+    return Lam
+
+
+def serial_backward_tiled(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True,
+                          BN=32, D=4, num_warps=1):
+    """triton_lif.py:469-476; same kernel as serial_backward."""
+    return serial_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach)
+
+
+def serial_backward_tiled_pf(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True,
+                             BN=32, D=4, num_warps=1):
+    """Prefetching serial adjoint (triton_lif.py:1130-1135); same kernel as serial_backward."""
+    return serial_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach)
+
+
+def serial_backward_auto(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True):
+    """Tuned serial adjoint (triton_lif.py:1199-1203)."""
+    return serial_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach)
+
+
+def serial_bwd_cfg(N):
+    """(BN, D, num_warps) table of the reference (triton_lif.py:1184-1189), kept for callers
+    that read it; the HIP kernels choose their own tiles."""
+    if N <= 8: return 16, 16, 1
+    if N <= 64: return 16, 2, 2
+    if N <= 16384: return 64, 16, 1
+    return 128, 2, 1
+
+
+def serial_fwd_cfg(N):
+    """(BN, D, num_warps) table of the reference (triton_lif.py:1213-1218); see serial_bwd_cfg."""
+    if N <= 8: return 16, 32, 1
+    if N <= 64: return 16, 4, 1
+    if N <= 512: return 128, 16, 1
+    return 64, 32, 1
+
+
+# ----------------------------------------------------------------------------- scan forward
+def state_bounds(I, beta, theta, u_r, u0):
+    """Loose per-neuron bounds [lo, hi] of every state (triton_lif.py:238-243)."""
+    Imin = I.min(0).values.clamp(max=0)
+    base = torch.minimum(u0, torch.full_like(u0, u_r)).clamp(max=0)
+    lo = base + (Imin / (1 - beta) if beta < 1 else I.clamp(max=0).sum(0))
+    hi = torch.maximum(u0, torch.full_like(u0, max(theta, u_r)))
+    return lo.contiguous(), hi.contiguous()
+
+
+class _ScanRun:
+    """Holds the workspace of one scan call (maps, starts, ends) for stats and tests."""
+
+    def __init__(self, ws, T, N, C, K):
+        self.ws, self.T, self.N, self.C, self.K = ws, T, N, C, K
+
+    def layout(self):
+        L = _n.V3Layout()
+        _n.check(_n.lib().lsh_lif_scan_v3_layout(self.T, self.N, self.C, self.K,
+                                                 _n.ctypes.byref(L)), "lsh_lif_scan_v3_layout")
+        return L
+
+    def view(self, name, dtype=torch.float32):
+        """[M, N] or [M, K, N] view of one workspace array (MX/MC are [M, K, N])."""
+        L = self.layout()
+        M = self.T // self.C
+        off = getattr(L, name)
+        shape = (M, self.K, self.N) if name in ("MX", "MC") else (M, self.N)
+        nbytes = 4 * math.prod(shape)
+        return self.ws[off:off + nbytes].view(dtype).view(*shape)
+
+
+_LAST_RUN = None
+
+
+def last_scan_run():
+    """Workspace of the most recent two-level scan on this process (diagnostics/tests)."""
+    return _LAST_RUN
+
+
+def _scan2(I, beta, theta, u_r, u0, C, K, repair, stats, lo=None):
+    global _LAST_RUN
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    C, K = int(C), int(K)
+    if C < 1 or T % C:
+        raise ValueError(f"T={T} must be divisible by the chunk length C={C}")
+    if not 1 <= K <= 64:
+        raise ValueError("map capacity K must be in [1, 64]")
+    repair = int(repair)
+    L = _n.lib()
+    nbytes = L.lsh_lif_scan_v3_workspace(T, N, C, K)
+    if nbytes == 0:
+        raise ValueError(f"unsupported scan shape T={T} N={N} C={C} K={K}")
+    ws = _n.workspace(nbytes, I.device)
+    U = torch.empty_like(I)
+    S = torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        st = _n.stream_of(I)
+        if lo is None:
+            rc = L.lsh_lif_scan_v3_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
+                                       _f32(beta), _f32(theta), _f32(u_r), C, K, repair,
+                                       _n.ptr(ws), nbytes, st)
+        else:
+            lo = _vec(lo, N, I, "lo")
+            rc = L.lsh_lif_scan_lo_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(lo), _n.ptr(U), _n.ptr(S), T,
+                                       N, _f32(beta), _f32(theta), _f32(u_r), C, K, repair,
+                                       _n.ptr(ws), nbytes, st)
+        _n.check(rc, "two-level scan forward")
+    _LAST_RUN = _ScanRun(ws, T, N, C, K)
+    if stats is not None:
+        _fill_stats(stats, _n.read_stats(ws, (T // C) * N))
+    return U, S
+
+
+def scan_forward_v3(I, beta, theta, u_r, u0, C=64, K=16, BN=32, nw=1, BNc=16, nwc=1, BNr=32, D=8,
+                    nwr=1, repair=0, stats=None):
+    """Two-level exact scan with per-chunk envelope bounds (triton_lif.py:782-817) -> (U, S).
+
+    Stricter than the reference: T % C != 0 raises ValueError (the reference leaves the tail
+    uninitialised).  stats receives repair_iters, overflow_frac, mean_pieces, max_pieces with
+    the reference's definitions (mean/max of kept breakpoints + 1)."""
+    return _scan2(I, beta, theta, u_r, u0, C, K, repair, stats)
+
+
+def scan_forward(I, beta, theta, u_r, u0, C=64, K=16, BN=BN_DEFAULT, repair=0, stats=None):
+    """Two-level scan pruned with the loose global state_bounds (triton_lif.py:262-295)."""
+    I = _input(I)
+    u0v = _vec(u0, I.shape[1], I)
+    lo, _ = state_bounds(I, _f32(beta), _f32(theta), _f32(u_r), u0v)
+    st = {} if stats is not None else None
+    U, S = _scan2(I, beta, theta, u_r, u0v, C, K, repair, st, lo=lo)
+    if stats is not None:
+        stats["repair_iters"] = st["repair_iters"]
+        stats["overflow_frac"] = st["overflow_frac"]
+        stats["max_pieces"] = st["max_pieces"]
+    return U, S
+
+
+def scan_forward_tiled(I, beta, theta, u_r, u0, C=64, K=16, BN=128, BNr=32, D=4, nw=4, nwr=1,
+                       repair=0, stats=None):
+    """triton_lif.py:479-509: same maps as scan_forward, tiled replay."""
+    st = {} if stats is not None else None
+    U, S = scan_forward(I, beta, theta, u_r, u0, C=C, K=K, repair=repair, stats=st)
+    if stats is not None:
+        stats["repair_iters"] = st["repair_iters"]
+        stats["overflow_frac"] = st["overflow_frac"]
+    return U, S
+
+
+def scan_forward_v2(I, beta, theta, u_r, u0, C=64, K=16, BN=128, nw=4, STAGES=3, CSTAGES=1,
+                    BNr=32, D=4, nwr=1, repair=0, stats=None, Imin=None):
+    """triton_lif.py:609-642: pruned with lo = min(u0, u_r, 0) + min(Imin, 0) * 1/(1-beta)
+    (or * T when beta == 1), computed in fp32 as the reference's build2 kernel does."""
+    I = _input(I)
+    T, N = I.shape
+    u0v = _vec(u0, N, I)
+    b = _f32(beta)
+    if Imin is None:
+        Imin = I.amin(0)
+    inv = 1.0 / (1.0 - b) if b < 1 else float(T)
+    imin = torch.minimum(Imin.float(), torch.zeros_like(u0v))
+    base = torch.minimum(torch.minimum(u0v, torch.full_like(u0v, _f32(u_r))), torch.zeros_like(u0v))
+    lo = (base + imin * torch.tensor(inv, dtype=torch.float32, device=I.device)).contiguous()
+    st = {} if stats is not None else None
+    U, S = _scan2(I, beta, theta, u_r, u0v, C, K, repair, st, lo=lo)
+    if stats is not None:
+        stats["repair_iters"] = st["repair_iters"]
+        stats["overflow_frac"] = st["overflow_frac"]
+    return U, S
+
+
+# ----------------------------------------------------------------------------- scan backward
+def scan_backward_tiled(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=64,
+                        BNr=32, D=4, nwr=1):
+    """Affine-scan adjoint (triton_lif.py:512-526) -> Lam.  GU may be None (zeros)."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    U, S, GS = _same(U, I, "U"), _same(S, I, "S"), _same(GS, I, "GS")
+    GU = _same(GU, I, "GU")
+    C = int(C)
+    if C < 1 or T % C:
+        raise ValueError(f"T={T} must be divisible by the chunk length C={C}")
+    L = _n.lib()
+    nbytes = L.lsh_lif_scan_bwd_workspace(T, N, C)
+    ws = _n.workspace(nbytes, I.device)
+    Lam = torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        _n.check(L.lsh_lif_scan_bwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS),
+                                    _n.ptr(GU), _n.ptr(Lam), T, N, _f32(beta), _f32(theta),
+                                    _f32(u_r), _f32(alpha), int(bool(detach)), C, _n.ptr(ws),
+                                    nbytes, _n.stream_of(I)), "lsh_lif_scan_bwd")
+    return Lam
+
+
+def scan_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=64,
+                  BN=BN_DEFAULT):
+    """triton_lif.py:298-312; same kernels as scan_backward_tiled."""
+    return scan_backward_tiled(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach, C=C)
+
+
+# ----------------------------------------------------------------------------- auto policies
+def _pick_C(T, D=8):
+    """Chunk length policy of the reference (triton_lif.py:647-651)."""
+    for C in (256, 128, 64, 32, 16, 8):
+        if T % C == 0 and C % D == 0 and C * C <= 4 * T:
+            return C
+    raise ValueError(f"T={T} needs a chunk length divisible by {D}")
+
+
+def scan_forward_auto(I, beta, theta, u_r, u0, K=16, repair=0):
+    """Two-level exact forward with the reference's default chunking (triton_lif.py:1228-1232)."""
+    T = I.shape[0]
+    C = _pick_C(T, D=16)
+    return scan_forward_v3(I, beta, theta, u_r, u0, C=C, K=K, repair=repair)
+
+
+def scan_backward_auto(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0):
+    """Affine-scan backward with the reference's default chunking (triton_lif.py:1235-1239)."""
+    T = I.shape[0]
+    C = min(128, _pick_C(T, D=2))
+    return scan_backward_tiled(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, C=C)
+
+
+def auto_modes(N, T):
+    """Serial or scan per pass from (N, T) (triton_lif.py:997-1000)."""
+    fwd = "scan" if (N <= AUTO_FWD_MAX_N and T >= AUTO_FWD_MIN_T) else "serial"
+    bwd = "scan" if (N <= AUTO_BWD_MAX_N and T >= AUTO_BWD_MIN_T) else "serial"
+    return fwd, bwd
+
+
+# ----------------------------------------------------------------------------- autograd layers
+def _beta_grad(Lam, U, u0, need):
+    """dL/dbeta = sum_t lam_t * u_{t-1} (fit.py:44)."""
+    if not need:
+        return None
+    uprev = torch.cat([u0[None], U[:-1]], 0)
+    return (Lam * uprev).sum().reshape(())
+
+
+class LIFFunction(torch.autograd.Function):
+    """Hard-reset LIF, mode in {"serial", "scan"} (triton_lif.py:315-339); returns S."""
+
+    @staticmethod
+    def forward(ctx, I, u0, beta, theta, u_r, alpha, mode, C, K, repair):
+        I = I.contiguous()
+        b = _f32(beta)
+        if mode == "serial":
+            U, S = serial_forward(I, b, theta, u_r, u0)
+        else:
+            U, S = scan_forward(I, b, theta, u_r, u0, C=C, K=K, repair=repair)
+        ctx.save_for_backward(I, u0, U, S)
+        ctx.cfg = (b, theta, u_r, alpha, mode, C)
+        return S
+
+    @staticmethod
+    def backward(ctx, gS):
+        I, u0, U, S = ctx.saved_tensors
+        b, theta, u_r, alpha, mode, C = ctx.cfg
+        gS = gS.contiguous()
+        if mode == "serial":
+            Lam = serial_backward(I, u0, U, S, gS, None, b, theta, u_r, alpha)
+        else:
+            Lam = scan_backward(I, u0, U, S, gS, None, b, theta, u_r, alpha, C=C)
+        return (Lam, b * Lam[0], _beta_grad(Lam, U, u0, ctx.needs_input_grad[2]),
+                None, None, None, None, None, None, None)
+
+
+def lif(I, u0, beta=0.9, theta=1.0, u_r=0.0, alpha=4.0, mode="scan", C=64, K=16, repair=0):
+    return LIFFunction.apply(I, u0, beta, theta, u_r, alpha, mode, C, K, repair)
+
+
+class LIFTuned(torch.autograd.Function):
+    """Hard-reset LIF (detached reset, sigmoid surrogate), mode in {"serial", "scan"}
+    (triton_lif.py:654-683).  Returns S; gradients for I and u0 as the reference, plus
+    dL/dbeta when beta is passed as a 0-d tensor that requires grad (the reference returns
+    None for beta).  The backward reads no GU array (it is identically zero here)."""
+
+    @staticmethod
+    def forward(ctx, I, u0, beta, theta, u_r, alpha, mode, K, repair):
+        I = I.contiguous()
+        b = _f32(beta)
+        if mode == "serial":
+            U, S = serial_forward_auto(I, b, theta, u_r, u0)
+        else:
+            U, S = scan_forward_auto(I, b, theta, u_r, u0, K=K, repair=repair)
+        ctx.save_for_backward(I, u0, U, S)
+        ctx.cfg = (b, theta, u_r, alpha, mode)
+        return S
+
+    @staticmethod
+    def backward(ctx, gS):
+        I, u0, U, S = ctx.saved_tensors
+        b, theta, u_r, alpha, mode = ctx.cfg
+        gS = gS.contiguous()
+        if mode == "serial":
+            Lam = serial_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
+        else:
+            Lam = scan_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
+        return (Lam, b * Lam[0], _beta_grad(Lam, U, u0, ctx.needs_input_grad[2]),
+                None, None, None, None, None, None)
+
+
+def lif_tuned(I, u0, beta=0.9, theta=1.0, u_r=0.0, alpha=4.0, mode="scan", K=16, repair=0):
+    return LIFTuned.apply(I, u0, beta, theta, u_r, alpha, mode, K, repair)
+
+
+class LIFAuto(torch.autograd.Function):
+    """Serial or scan chosen per pass (triton_lif.py:1003-1026)."""
+
+    @staticmethod
+    def forward(ctx, I, u0, beta, theta, u_r, alpha, K, repair, fwd_mode, bwd_mode):
+        I = I.contiguous()
+        b = _f32(beta)
+        if fwd_mode == "scan":
+            U, S = scan_forward_auto(I, b, theta, u_r, u0, K=K, repair=repair)
+        else:
+            U, S = serial_forward_auto(I, b, theta, u_r, u0)
+        ctx.save_for_backward(I, u0, U, S)
+        ctx.cfg = (b, theta, u_r, alpha, bwd_mode)
+        return S
+
+    @staticmethod
+    def backward(ctx, gS):
+        I, u0, U, S = ctx.saved_tensors
+        b, theta, u_r, alpha, bwd_mode = ctx.cfg
+        gS = gS.contiguous()
+        if bwd_mode == "scan":
+            Lam = scan_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
+        else:
+            Lam = serial_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
+        return (Lam, b * Lam[0], _beta_grad(Lam, U, u0, ctx.needs_input_grad[2]),
+                None, None, None, None, None, None, None)
+
+
+def lif_auto(I, u0, beta=0.9, theta=1.0, u_r=0.0, alpha=4.0, K=16, repair=0):
+    fwd, bwd = auto_modes(I.shape[1], I.shape[0])
+    return LIFAuto.apply(I, u0, beta, theta, u_r, alpha, K, repair, fwd, bwd)
+
+
+def surrogate_grad(x, alpha):
+    """Derivative of sigmoid(alpha*x) (fast.py:48-51); used by fit.lif_param."""
+    sg = torch.sigmoid(alpha * x)
+    return alpha * sg * (1 - sg)

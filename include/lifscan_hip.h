@@ -1,0 +1,122 @@
+/*
+ * lifscan_hip.h — C ABI of the MI355X (gfx950) exact hard-reset LIF / ALIF scan library
+ * (liblifscan_hip.so).
+ *
+ * Conventions (every entry point):
+ *   - All arrays are device pointers to fp32 (or int32 where stated), time-major [T, N]
+ *     with element (t, n) at t*N + n, neurons contiguous.  Per-chunk arrays are [M, N]
+ *     and per-chunk map slots [M, K, N] with M = T / C.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the default stream).  Kernels are
+ *     launched asynchronously on it; no entry point synchronizes unless stated.
+ *   - The library never allocates or frees device memory.  Scan entry points take a
+ *     caller-provided workspace whose size is given by the matching *_workspace() query.
+ *   - Return value: LSH_OK (0) or a negative LSH_ERR_* code; nothing is launched when an
+ *     argument check fails.
+ *   - Scalars beta, theta, u_r, alpha, rho, q, theta0 are fp32 (the reference passes
+ *     Python floats, which its kernels use as fp32).
+ *   - Step arithmetic: v = fl(fl(beta*u) + x), two IEEE round-to-nearest operations, no
+ *     FMA contraction; spikes s = v >= theta; u' = s ? u_r : v.
+ */
+#ifndef LIFSCAN_HIP_H
+#define LIFSCAN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LSH_ABI_VERSION 1
+
+#define LSH_OK 0
+#define LSH_ERR_ARG (-1)          /* null pointer or bad scalar argument */
+#define LSH_ERR_SHAPE (-2)        /* T, N, C, K, G out of the supported range */
+#define LSH_ERR_DIVISIBILITY (-3) /* T % C != 0 (or M % G != 0) */
+#define LSH_ERR_WORKSPACE (-4)    /* workspace too small or misaligned */
+#define LSH_ERR_HIP (-5)          /* HIP launch / runtime error */
+
+/* Library identity. */
+int lsh_abi_version(void);
+const char* lsh_arch(void);                /* "gfx950" */
+const char* lsh_status_string(int status); /* static string for a status code */
+
+/* Serial hard-reset LIF forward, one lane per neuron, time-tiled with register prefetch.
+ * Replaces triton_lif.py:460-466 (serial_forward_tiled), :246-251 (serial_forward) and
+ * :1221-1225 (serial_forward_auto).  U, S: [T, N] outputs. */
+int lsh_lif_serial_fwd(const float* I, const float* u0, float* U, float* S, int64_t T, int64_t N,
+                       float beta, float theta, float u_r, void* stream);
+
+/* Serial surrogate-gradient adjoint lam_t = gs_t*sg_t + J_t*(gu_t + beta*lam_{t+1}), lam_T = 0.
+ * Replaces triton_lif.py:1130-1135 (serial_backward_tiled_pf), :254-259 (serial_backward),
+ * :469-476 (serial_backward_tiled) and :1199-1203 (serial_backward_auto).
+ * GU may be NULL (treated as all zeros: LIFTuned.backward, triton_lif.py:678).
+ * detach != 0: J = 1 - s; detach == 0: J = 1 - s + (u_r - v)*sg (triton_lif.py:47-49). */
+int lsh_lif_serial_bwd(const float* I, const float* u0, const float* U, const float* S,
+                       const float* GS, const float* GU, float* Lam, int64_t T, int64_t N,
+                       float beta, float theta, float u_r, float alpha, int detach, void* stream);
+
+/* Two-level exact scan forward (envelope bound + capacity-K chunk maps, sequential carry
+ * with overflow-to-serial fallback, replay, Jacobi repair on device).
+ * Replaces triton_lif.py:782-817 (scan_forward_v3) and :1228-1232 (scan_forward_auto).
+ * repair: maximum number of repair rounds (0 = none; the result is bit-identical to the
+ * serial recurrence once the rounds converge, at most T/C rounds).  Requires T % C == 0,
+ * 1 <= K <= 64, C >= 1. */
+size_t lsh_lif_scan_v3_workspace(int64_t T, int64_t N, int C, int K);
+int lsh_lif_scan_v3_fwd(const float* I, const float* u0, float* U, float* S, int64_t T, int64_t N,
+                        float beta, float theta, float u_r, int C, int K, int64_t repair,
+                        void* ws, size_t ws_bytes, void* stream);
+
+/* Two-level scan pruned with one caller-given lower bound per neuron (lo[N], e.g. the loose
+ * state_bounds of triton_lif.py:238-243) instead of the per-chunk envelope.  Replaces
+ * triton_lif.py:262-295 (scan_forward), :479-509 (scan_forward_tiled) and :609-642
+ * (scan_forward_v2).  Same workspace as lsh_lif_scan_v3_fwd. */
+int lsh_lif_scan_lo_fwd(const float* I, const float* u0, const float* lo, float* U, float* S,
+                        int64_t T, int64_t N, float beta, float theta, float u_r, int C, int K,
+                        int64_t repair, void* ws, size_t ws_bytes, void* stream);
+
+/* Diagnostics of the last scan run in `ws` (synchronizes `stream`).  Same definitions as
+ * the reference's stats dict: triton_lif.py:812-816 (v3), :976-982 (v4),
+ * triton_alif.py:351-357 (ALIF). */
+typedef struct lsh_scan_stats {
+  int64_t repair_iters;
+  double overflow_frac;
+  double mean_pieces; /* mean(kept breakpoints) + 1 for LIF; mean(x-pieces) for ALIF */
+  int64_t max_pieces; /* max(kept breakpoints) + 1 for LIF; max(x-pieces) for ALIF */
+  double super_overflow_frac;
+  double super_mean_pieces;
+  int64_t super_max_pieces;
+  double miss_frac;  /* ALIF only */
+  double mean_lines; /* ALIF only */
+} lsh_scan_stats;
+int lsh_scan_stats_read(const void* ws, int64_t chunk_neurons, int64_t super_neurons,
+                        int alif, lsh_scan_stats* out, void* stream);
+
+/* Byte offsets of the arrays inside a v3 workspace (for tests and diagnostics). */
+typedef struct lsh_v3_layout {
+  size_t EC, EA, EB;   /* envelope chunk maps [M,N] */
+  size_t MA, MB;       /* affine part of the chunk maps [M,N] */
+  size_t CNT, OVFRAW;  /* breakpoints stored / capacity overflow before lower-bound pruning [M,N] int32 */
+  size_t MX, MC;       /* breakpoints (descending) and constants [M,K,N] */
+  size_t LO;           /* envelope lower bound of every chunk entry [M,N] */
+  size_t MN, OVF;      /* breakpoints kept after pruning with LO, final overflow flag [M,N] int32 */
+  size_t STARTS, ENDS; /* chunk entry / replayed exit states [M,N] */
+  size_t LIST0, LIST1; /* repair work lists */
+  size_t total;
+} lsh_v3_layout;
+int lsh_lif_scan_v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3_layout* out);
+
+/* Affine-scan backward: chunk composition of lam_t = a_t*lam_{t+1} + b_t, reverse carry,
+ * reverse replay.  Replaces triton_lif.py:512-526 (scan_backward_tiled), :298-312
+ * (scan_backward) and :1235-1239 (scan_backward_auto).  GU may be NULL (zeros). */
+size_t lsh_lif_scan_bwd_workspace(int64_t T, int64_t N, int C);
+int lsh_lif_scan_bwd(const float* I, const float* u0, const float* U, const float* S,
+                     const float* GS, const float* GU, float* Lam, int64_t T, int64_t N, float beta,
+                     float theta, float u_r, float alpha, int detach, int C, void* ws,
+                     size_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LIFSCAN_HIP_H */

@@ -1,0 +1,232 @@
+"""GPU parity of the HIP LIF kernels against the CPU oracle (through the C ABI).
+
+Bars: spikes and membrane potentials bit-exact (integer/byte-level equality of fp32 arrays)
+for every forward path; the adjoint within 1e-5 relative of the fp32 oracle (the reference's
+own scan-vs-serial bar, tests/test_triton.py:47) and 1e-4 relative of the fp64 adjoint
+(north-star gradient bar).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import lif_oracle as O
+from tests._inputs import gpu, host, normal, uniform
+
+pytestmark = pytest.mark.gpu
+
+REL_FP32 = 1e-5
+REL_FP64 = 1e-4
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from lifscan import triton_lif
+    return triton_lif
+
+
+@pytest.mark.parametrize("T,N,beta,u_r,mu,sd", [
+    (1024, 4096, 0.9, 0.0, 0.12, 0.25),   # cfg1 shape
+    (777, 333, 0.99, -0.1, 0.012, 0.08),  # ragged: N % 64 != 0, T % tile != 0
+    (3, 65, 0.5, -0.2, 0.4, 0.3),
+    (1, 1, 0.9, 0.0, 1.5, 0.1),
+    (2048, 200, 1.0, -0.1, 0.05, 0.3),
+])
+def test_serial_forward_bitexact(L, dev, T, N, beta, u_r, mu, sd):
+    I = normal(T, N, mu, sd, 1)
+    u0 = uniform(N, -0.3, 0.9, 2)
+    print(f"serial fwd T={T} N={N} beta={beta}", flush=True)
+    U, S = L.serial_forward(gpu(I, dev), beta, 1.0, u_r, gpu(u0, dev))
+    Uo, So = O.serial_forward(I, beta, 1.0, u_r, u0)
+    assert np.array_equal(host(U), Uo)
+    assert np.array_equal(host(S), So)
+
+
+@pytest.mark.parametrize("detach,with_gu", [(True, False), (True, True), (False, True)])
+def test_serial_backward(L, dev, detach, with_gu):
+    T, N = 1000, 300
+    I = normal(T, N, 0.15, 0.4, 3)
+    u0 = uniform(N, -0.2, 0.5, 4)
+    GS = normal(T, N, 0.0, 1.0, 5)
+    GU = normal(T, N, 0.0, 1.0, 6) if with_gu else None
+    U, S = O.serial_forward(I, 0.9, 1.0, -0.1, u0)
+    print(f"serial bwd detach={detach} gu={with_gu}", flush=True)
+    Lam = L.serial_backward(gpu(I, dev), gpu(u0, dev), gpu(U, dev), gpu(S, dev), gpu(GS, dev),
+                            gpu(GU, dev) if with_gu else None, 0.9, 1.0, -0.1, 4.0, detach)
+    ref32 = O.serial_backward(I, u0, U, S, GS, GU, 0.9, 1.0, -0.1, 4.0, detach)
+    ref64 = O.serial_backward(I, u0, U, S, GS, GU, 0.9, 1.0, -0.1, 4.0, detach, dtype=np.float64)
+    assert rel(host(Lam), ref32) < REL_FP32
+    assert rel(host(Lam), ref64) < REL_FP64
+
+
+REGIMES = [(b, mu, sd) for b in (0.5, 0.9, 0.99, 1.0) for (mu, sd) in ((0.15, 0.4), (-0.1, 0.6), (0.4, 0.2))]
+
+
+@pytest.mark.parametrize("beta,mu,sd", REGIMES)
+def test_scan_v3_matches_oracle(L, dev, beta, mu, sd):
+    """repair=0: U, S, chunk starts, kept maps and stats equal the oracle's v3 bit for bit;
+    repair on: U, S equal the serial recurrence (test_v3.py's N=777, not a multiple of 64)."""
+    T, N, C = 1024, 777, 64
+    I = normal(T, N, mu, sd, 7)
+    u0 = uniform(N, -0.3, 0.3, 8)
+    Ig, u0g = gpu(I, dev), gpu(u0, dev)
+    Us, Ss = O.serial_forward(I, beta, 1.0, -0.1, u0)
+    for K in (4, 16):
+        print(f"v3 beta={beta} mu={mu} K={K}", flush=True)
+        st, sto, keep = {}, {}, {}
+        U, S = L.scan_forward_v3(Ig, beta, 1.0, -0.1, u0g, C=C, K=K, stats=st)
+        run = L.last_scan_run()
+        Uo, So = O.scan_forward_v3(I, beta, 1.0, -0.1, u0, C=C, K=K, stats=sto, keep=keep)
+        assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+        assert np.array_equal(host(run.view("LO")), keep["Lo"])
+        assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+        n = host(run.view("MN", torch.int32))
+        assert np.array_equal(n, keep["n"])
+        assert np.array_equal(host(run.view("OVF", torch.int32)), keep["ovf"])
+        assert np.array_equal(host(run.view("MA")), keep["A"])
+        assert np.array_equal(host(run.view("MB")), keep["B"])
+        valid = np.arange(K)[None, :, None] < n[:, None, :]
+        assert np.array_equal(host(run.view("MX"))[valid], keep["xd"][valid])
+        assert np.array_equal(host(run.view("MC"))[valid], keep["cd"][valid])
+        assert st["overflow_frac"] == pytest.approx(sto["overflow_frac"], abs=0)
+        assert st["mean_pieces"] == pytest.approx(sto["mean_pieces"], rel=1e-12)
+        assert st["max_pieces"] == sto["max_pieces"]
+        st2 = {}
+        U2, S2 = L.scan_forward_v3(Ig, beta, 1.0, -0.1, u0g, C=C, K=K, repair=10 ** 6, stats=st2)
+        assert np.array_equal(host(U2), Us) and np.array_equal(host(S2), Ss)
+        sto2 = {}
+        O.scan_forward_v3(I, beta, 1.0, -0.1, u0, C=C, K=K, repair=10 ** 6, stats=sto2)
+        assert st2["repair_iters"] == sto2["repair_iters"]
+
+
+@pytest.mark.parametrize("R", [1, 2, 3])
+def test_scan_v3_finite_repair_rounds(L, dev, R):
+    T, N, C = 2048, 300, 64
+    I = normal(T, N, 0.012, 0.08, 9)
+    u0 = np.zeros(N, np.float32)
+    print(f"v3 finite repair R={R}", flush=True)
+    st, sto = {}, {}
+    U, S = L.scan_forward_v3(gpu(I, dev), 0.99, 1.0, 0.0, gpu(u0, dev), C=C, K=4, repair=R, stats=st)
+    Uo, So = O.scan_forward_v3(I, 0.99, 1.0, 0.0, u0, C=C, K=4, repair=R, stats=sto)
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+    assert st["repair_iters"] == sto["repair_iters"]
+
+
+def test_scan_v1_global_bounds(L, dev):
+    """scan_forward prunes with the loose global state_bounds (triton_lif.py:262-295)."""
+    T, N = 1024, 500
+    I = normal(T, N, 0.15, 0.4, 10)
+    u0 = uniform(N, -0.3, 0.3, 11)
+    Ig, u0g = gpu(I, dev), gpu(u0, dev)
+    lo_g, _ = L.state_bounds(Ig, 0.9, 1.0, -0.1, u0g)
+    lo = host(lo_g)
+    print("v1 scan", flush=True)
+    for K in (4, 16, 64):
+        st, sto = {}, {}
+        U, S = L.scan_forward(Ig, 0.9, 1.0, -0.1, u0g, C=64, K=K, stats=st)
+        Uo, So = O.scan_forward_v3(I, 0.9, 1.0, -0.1, u0, C=64, K=K, lo=lo, stats=sto)
+        assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+        assert st["overflow_frac"] == pytest.approx(sto["overflow_frac"], abs=0)
+        assert st["max_pieces"] == sto["max_pieces"]
+
+
+@pytest.mark.parametrize("C,K", [(8, 1), (16, 2), (128, 64), (1024, 8)])
+def test_scan_v3_edge_shapes(L, dev, C, K):
+    T, N = 1024, 65
+    I = normal(T, N, 0.12, 0.25, 12)
+    u0 = np.zeros(N, np.float32)
+    print(f"v3 edge C={C} K={K}", flush=True)
+    U, S = L.scan_forward_v3(gpu(I, dev), 0.9, 1.0, 0.0, gpu(u0, dev), C=C, K=K, repair=10 ** 6)
+    Us, Ss = O.serial_forward(I, 0.9, 1.0, 0.0, u0)
+    assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+
+
+def test_scan_v3_rejects_bad_shapes(L, dev):
+    I = torch.zeros(100, 8, device=dev)
+    u0 = torch.zeros(8, device=dev)
+    with pytest.raises(ValueError):
+        L.scan_forward_v3(I, 0.9, 1.0, 0.0, u0, C=64)
+    with pytest.raises(ValueError):
+        L.scan_forward_v3(I, 0.9, 1.0, 0.0, u0, C=10, K=65)
+
+
+@pytest.mark.parametrize("C", [32, 64, 128])
+def test_scan_backward(L, dev, C):
+    T, N = 1024, 333
+    I = normal(T, N, 0.15, 0.4, 13)
+    u0 = uniform(N, -0.2, 0.2, 14)
+    GS = normal(T, N, 0.0, 1.0, 15)
+    U, S = O.serial_forward(I, 0.9, 1.0, 0.0, u0)
+    print(f"scan bwd C={C}", flush=True)
+    Lam = L.scan_backward_tiled(gpu(I, dev), gpu(u0, dev), gpu(U, dev), gpu(S, dev), gpu(GS, dev),
+                                None, 0.9, 1.0, 0.0, 4.0, C=C)
+    ref32 = O.scan_backward(I, u0, U, S, GS, None, 0.9, 1.0, 0.0, 4.0, True, C=C)
+    ref64 = O.serial_backward(I, u0, U, S, GS, None, 0.9, 1.0, 0.0, 4.0, dtype=np.float64)
+    assert rel(host(Lam), ref32) < REL_FP32
+    assert rel(host(Lam), ref64) < REL_FP64
+    GU = normal(T, N, 0.0, 1.0, 16)
+    Lam2 = L.scan_backward_tiled(gpu(I, dev), gpu(u0, dev), gpu(U, dev), gpu(S, dev), gpu(GS, dev),
+                                 gpu(GU, dev), 0.9, 1.0, 0.0, 4.0, detach=False, C=C)
+    ref = O.serial_backward(I, u0, U, S, GS, GU, 0.9, 1.0, 0.0, 4.0, False, dtype=np.float64)
+    assert rel(host(Lam2), ref) < REL_FP64
+
+
+@pytest.mark.parametrize("mode", ["serial", "scan"])
+def test_lif_tuned_gradients(L, dev, mode):
+    """Gradients w.r.t. I, u0 and beta within 1e-4 relative of the fp64 adjoint."""
+    T, N = 1024, 256
+    I = normal(T, N, 0.15, 0.4, 17)
+    u0 = uniform(N, -0.2, 0.2, 18)
+    W = normal(T, N, 0.0, 1.0, 19)
+    Ig = gpu(I, dev).requires_grad_(True)
+    u0g = gpu(u0, dev).requires_grad_(True)
+    beta = torch.tensor(0.95, device=dev, requires_grad=True)
+    print(f"lif_tuned mode={mode}", flush=True)
+    S = L.lif_tuned(Ig, u0g, beta, 1.0, 0.0, 4.0, mode=mode, K=16, repair=10 ** 6)
+    (gpu(W, dev) * S).sum().backward()
+    Uo, So = O.serial_forward(I, 0.95, 1.0, 0.0, u0)
+    assert np.array_equal(host(S), So)
+    Lam = O.serial_backward(I, u0, Uo, So, W, None, 0.95, 1.0, 0.0, 4.0, dtype=np.float64)
+    assert rel(host(Ig.grad), Lam) < REL_FP64
+    assert rel(host(u0g.grad), np.float64(np.float32(0.95)) * Lam[0]) < REL_FP64
+    uprev = np.concatenate([u0[None], Uo[:-1]], 0).astype(np.float64)
+    dbeta = float((Lam * uprev).sum())
+    assert abs(beta.grad.item() - dbeta) <= REL_FP64 * abs(dbeta)
+
+
+def test_lif_auto_matches_serial(L, dev):
+    T, N = 1024, 128
+    I = normal(T, N, 0.15, 0.4, 20)
+    Ig = gpu(I, dev)
+    u0 = torch.zeros(N, device=dev)
+    S = L.lif_auto(Ig, u0, 0.9, 1.0, 0.0, 4.0)
+    _, So = O.serial_forward(I, 0.9, 1.0, 0.0, np.zeros(N, np.float32))
+    assert np.array_equal(host(S), So)
+
+
+def test_cfg2_scan_equals_serial_full_size(L, dev):
+    """BASELINE cfg2 at full size (65,536 x 4,096, beta in {0.9, 0.99}, K=8, repair on):
+    spikes and potentials of the scan equal the serial kernel's everywhere, and 512 columns
+    equal the oracle (the serial kernel itself is pinned to the oracle above)."""
+    T, N = 4096, 65536
+    for beta, mu, sd in ((0.9, 0.12, 0.25), (0.99, 0.012, 0.08)):
+        print(f"cfg2 beta={beta}", flush=True)
+        g = torch.Generator().manual_seed(0)
+        I = (mu + sd * torch.randn(T, N, generator=g)).to(dev)
+        u0 = torch.zeros(N, device=dev)
+        Us, Ss = L.serial_forward(I, beta, 1.0, 0.0, u0)
+        for C in (32, 128):
+            st = {}
+            U, S = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=8, repair=10 ** 6, stats=st)
+            assert torch.equal(U, Us) and torch.equal(S, Ss)
+            print(f"  C={C} stats={st}", flush=True)
+        cols = np.arange(0, N, N // 512)
+        Uo, So = O.serial_forward(host(I[:, cols]), beta, 1.0, 0.0, np.zeros(len(cols), np.float32))
+        assert np.array_equal(host(Us[:, cols]), Uo) and np.array_equal(host(Ss[:, cols]), So)
+        del I, Us, Ss, U, S
+        torch.cuda.empty_cache()

@@ -681,10 +681,13 @@ static int scan2_fwd(const float* I, const float* u0, const float* lo_neuron, fl
   float* ends = reinterpret_cast<float*>(w + L.ENDS);
   launch_fwd_auto(I, starts, U, S, ends, N, C, M, beta, theta, u_r, st);
   if (repair > 0 && M > 1) {
+    // Round r makes the starts of chunks 0..r exact, so M rounds always converge; the cap
+    // only bounds the work when NaN inputs make the comparison fail forever.
+    const int64_t rounds = repair < (int64_t)M ? repair : (int64_t)M;
     const int NB = (int)((N + WAVE - 1) / WAVE);
     hipLaunchKernelGGL(k_lif_repair, dim3((unsigned)NB), dim3(256), 0, st, I, U, S, starts, ends,
                        reinterpret_cast<int*>(w + L.LIST0), reinterpret_cast<int*>(w + L.LIST1),
-                       reinterpret_cast<WsHeader*>(w), N, M, C, repair, beta, theta, u_r);
+                       reinterpret_cast<WsHeader*>(w), N, M, C, rounds, beta, theta, u_r);
   }
   LSH_CHECK_LAUNCH();
   return LSH_OK;

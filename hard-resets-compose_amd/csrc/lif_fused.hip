@@ -1,0 +1,382 @@
+// Single-pass fused scans for MI355X: one workgroup owns a block of 64 neurons and walks
+// the time axis in rounds of W chunks, one chunk per wave.  Inputs are read from HBM once;
+// everything that crosses chunks (maps, chunk ends, affine aggregates) goes through LDS, so
+// no workgroup waits on another one.
+//
+// Forward (exact, i.e. the reference's two-level scan with repair run to convergence,
+// triton_lif.py:782-817):
+//   1. each wave loads its chunk's C inputs into registers and builds the chunk's
+//      capacity-K map (the same fold as triton_lif.py:737-779, hi-pruned) into LDS;
+//   2. each wave evaluates the maps of the earlier chunks of the round, from the round's
+//      exact entry state, to a speculative entry state, and replays its chunk (compute only)
+//      to a speculative exit state;
+//   3. exact exit states are handed from wave to wave through an LDS flag chain: a wave whose
+//      speculative entry equals the exact one (bit for bit) passes its speculative exit on at
+//      once, otherwise it replays from the exact entry first;
+//   4. every wave replays its chunk from the exact entry once more, storing U and S.
+//   The stored trajectory is therefore the serial recurrence bit for bit; the maps decide
+//   only how long the hand-off chain waits.
+// Backward (the affine scan of triton_lif.py:512-526 in one pass): each wave turns its chunk
+// into per-step coefficients (a_t, b_t) kept in registers, composes them to (P, Q) in LDS,
+// takes the adjoint at its chunk end from the later chunks' aggregates, and replays.
+#include "lsh_abi.h"
+#include "lsh_common.h"
+#include "lsh_map.h"
+
+namespace lsh {
+
+// Bounded LDS spin: waits until *flag == want.  The chain cannot deadlock (wave 0 never
+// waits), so the bound only guarantees termination if that reasoning were ever broken.
+__device__ __forceinline__ bool lds_wait(int* flag, int want) {
+  for (int it = 0; it < (1 << 24); ++it) {
+    if (__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) == want) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
+template <int KMAX, int C, int W, bool SPEC>
+__global__ __launch_bounds__(WAVE* W) void k_lif_fwd_fused(const float* __restrict__ I,
+                                                           const float* __restrict__ u0,
+                                                           float* __restrict__ U,
+                                                           float* __restrict__ S, WsHeader* hdr,
+                                                           int64_t N, int M, int K, float beta,
+                                                           float theta, float u_r) {
+  constexpr int KL = SPEC ? KMAX : 1;
+  __shared__ float sA[W][WAVE], sB[W][WAVE];
+  __shared__ float sXd[W][KL][WAVE], sCd[W][KL][WAVE];
+  __shared__ int sCnt[W][WAVE];
+  __shared__ float sEnd[W][WAVE];
+  __shared__ float sStart[WAVE];
+  __shared__ int sFlag[W];
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const unsigned lane = threadIdx.x % WAVE;
+  const int64_t nb0 = (int64_t)blockIdx.x * WAVE;
+  const bool valid = nb0 + lane < N;
+  // inactive lanes of the last block read a valid column and store nothing
+  const unsigned ln = valid ? lane : (unsigned)(N - 1 - nb0);
+  const unsigned lb = ln * 4u, sb = lane * 4u;  // load / store byte offsets within a row
+  const float* __restrict__ Ib = I + nb0;
+  float* __restrict__ Ub = U + nb0;
+  float* __restrict__ Sb = S + nb0;
+  const float hi = fmaxf(u0[nb0 + ln], fmaxf(theta, u_r));
+  if (w == 0) sStart[lane] = u0[nb0 + ln];
+  if (lane == 0) sFlag[w] = 0;
+  __syncthreads();
+
+  unsigned long long fixups = 0, unknown = 0;
+  unsigned int timeouts = 0;
+  const int rounds = (M + W - 1) / W;
+  for (int r = 0; r < rounds; ++r) {
+    const int m = r * W + w;
+    const bool active = m < M;  // wave-uniform
+    const size_t row0 = (size_t)m * C;
+    const unsigned rstride = (unsigned)(N * 4);  // bytes per time row (C*N*4 < 2^31 checked on host)
+    float x[C];
+    if (active) {
+      const Buf bi(Ib + row0 * N);
+#pragma unroll
+      for (int j = 0; j < C; ++j) x[j] = bi.ld(lb, j * rstride);
+      if (SPEC) {
+        MapBuilder<KMAX> mb;
+        mb.init();
+#pragma unroll
+        for (int j = 0; j < C; ++j) mb.step(x[j], beta, theta, u_r, hi, K);
+        sA[w][lane] = mb.A;
+        sB[w][lane] = mb.B;
+        sCnt[w][lane] = mb.cnt | (mb.ovf ? (1 << 16) : 0);
+#pragma unroll
+        for (int i = 0; i < KL; ++i) {
+          sXd[w][i][lane] = mb.xd[i];
+          sCd[w][i][lane] = mb.cd[i];
+        }
+      }
+    }
+    __syncthreads();
+    float e = 0.0f;
+    if (active) {
+      // (2) speculative entry through the earlier chunks' maps, speculative exit
+      float u_spec = sStart[lane];
+      bool known = SPEC;
+      float e_spec = 0.0f;
+      if (SPEC) {
+        for (int v = 0; v < w; ++v) {
+          const int cw = sCnt[v][lane];
+          const int cnt = cw & 0xffff;
+          int k = 0;
+#pragma unroll
+          for (int i = 0; i < KL; ++i) k += (i < cnt && sXd[v][i][lane] > u_spec) ? 1 : 0;
+          float cval = 0.0f;
+#pragma unroll
+          for (int i = 0; i < KL; ++i) cval = (i == k) ? sCd[v][i][lane] : cval;
+          if (k == cnt) {
+            if (cw >> 16) known = false;  // overflowed map, state below its stored pieces
+            u_spec = __fadd_rn(__fmul_rn(sA[v][lane], u_spec), sB[v][lane]);
+          } else {
+            u_spec = cval;
+          }
+        }
+        e_spec = u_spec;
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+          bool s;
+          e_spec = lif_step(e_spec, x[j], beta, theta, u_r, s);
+        }
+      }
+      // (3) exact entry from the previous wave of the chain
+      float start;
+      if (w == 0) {
+        start = sStart[lane];
+      } else {
+        if (!lds_wait(&sFlag[w - 1], r + 1)) ++timeouts;
+        start = sEnd[w - 1][lane];
+      }
+      const bool hit = known && same_bits(u_spec, start);
+      if (hit) {
+        e = e_spec;
+      } else {
+        e = start;
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+          bool s;
+          e = lif_step(e, x[j], beta, theta, u_r, s);
+        }
+      }
+      sEnd[w][lane] = e;
+      if (lane == 0)
+        __hip_atomic_store(&sFlag[w], r + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      fixups += (SPEC && known && !hit && valid) ? 1ull : 0ull;
+      unknown += (SPEC && !known && valid) ? 1ull : 0ull;
+      // (4) the stored trajectory, from the exact entry
+      if (valid) {
+        const Buf bu(Ub + row0 * N), bs(Sb + row0 * N);
+        float u = start;
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+          bool s;
+          u = lif_step(u, x[j], beta, theta, u_r, s);
+          bu.st_nt(sb, j * rstride, u);
+          bs.st_nt(sb, j * rstride, s ? 1.0f : 0.0f);
+        }
+      }
+    }
+    __syncthreads();
+    const int last = min(W, M - r * W) - 1;
+    if (w == last) sStart[lane] = e;
+    __syncthreads();
+  }
+  fixups = wave_sum_u64(fixups);
+  unknown = wave_sum_u64(unknown);
+  if (lane == 0) {
+    if (fixups) atomicAdd(&hdr->fused_fixups, fixups);
+    if (unknown) atomicAdd(&hdr->fused_unknown, unknown);
+    if (timeouts) atomicAdd(&hdr->spin_timeouts, timeouts);
+  }
+}
+
+template <int C, int W, bool DETACH, bool HAS_GU>
+__global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ U,
+    const float* __restrict__ S, const float* __restrict__ GS, const float* __restrict__ GU,
+    float* __restrict__ Lam, int64_t N, int M, float beta, float theta, float u_r, float alpha) {
+  __shared__ float sP[W][WAVE], sQ[W][WAVE];
+  __shared__ float sLam[WAVE];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const unsigned lane = threadIdx.x % WAVE;
+  const int64_t nb0 = (int64_t)blockIdx.x * WAVE;
+  const bool valid = nb0 + lane < N;
+  const unsigned ln = valid ? lane : (unsigned)(N - 1 - nb0);
+  const unsigned lb = ln * 4u, sb = lane * 4u;
+  const float* __restrict__ Ib = I + nb0;
+  const float* __restrict__ Sb = S + nb0;
+  const float* __restrict__ Gb = GS + nb0;
+  const float* __restrict__ Hb = HAS_GU ? GU + nb0 : nullptr;
+  const float* __restrict__ Ub = U + nb0;
+  float* __restrict__ Lb = Lam + nb0;
+  const float u0n = u0[nb0 + ln];
+  if (w == 0) sLam[lane] = 0.0f;
+  __syncthreads();
+  const int rounds = (M + W - 1) / W;
+  for (int r = 0; r < rounds; ++r) {
+    const int m = M - 1 - (r * W + w);  // wave 0 holds the latest chunk of the round
+    const bool active = m >= 0;
+    float a[C], b[C];
+    float lam = 0.0f;
+    const size_t row0 = (size_t)(active ? m : 0) * C;
+    const unsigned rstride = (unsigned)(N * 4);
+    if (active) {
+      const Buf bi(Ib + row0 * N), bs_(Sb + row0 * N), bg(Gb + row0 * N), bp(Ub + row0 * N);
+      // state before the chunk's first step: the previous chunk's last U row, or u0
+      const float up0 = row0 > 0 ? ld_row(Ub + (row0 - 1) * N, lb) : u0n;
+#pragma unroll
+      for (int j = 0; j < C; ++j) {
+        const unsigned so = j * rstride;
+        const float x = bi.ld(lb, so);
+        const float s = bs_.ld(lb, so);
+        const float gs = bg.ld(lb, so);
+        const float up = j == 0 ? up0 : bp.ld(lb, so - rstride);
+        const float v = lif_v(up, x, beta);
+        const float sg = surrogate(v, theta, alpha);
+        float J = 1.0f - s;
+        if (!DETACH) J = J + (u_r - v) * sg;
+        a[j] = beta * J;
+        b[j] = HAS_GU ? gs * sg + J * Buf(Hb + row0 * N).ld(lb, so) : gs * sg;
+      }
+      float P = 1.0f, Q = 0.0f;
+#pragma unroll
+      for (int j = C - 1; j >= 0; --j) {
+        Q = b[j] + a[j] * Q;
+        P = a[j] * P;
+      }
+      sP[w][lane] = P;
+      sQ[w][lane] = Q;
+    }
+    __syncthreads();
+    if (active) {
+      lam = sLam[lane];
+      for (int v = 0; v < w; ++v) lam = sQ[v][lane] + sP[v][lane] * lam;
+      const Buf bl(Lb + row0 * N);
+#pragma unroll
+      for (int j = C - 1; j >= 0; --j) {
+        lam = b[j] + a[j] * lam;
+        if (valid) bl.st_nt(sb, j * rstride, lam);
+      }
+    }
+    __syncthreads();
+    const int last = min(W, M - r * W) - 1;
+    if (w == last) sLam[lane] = lam;
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+template <int KMAX, int C, int W, bool SPEC>
+static void launch_fwd_fused(const float* I, const float* u0, float* U, float* S, WsHeader* h,
+                             int64_t N, int M, int K, float beta, float theta, float u_r,
+                             hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  hipLaunchKernelGGL((k_lif_fwd_fused<KMAX, C, W, SPEC>), dim3((unsigned)NB), dim3(WAVE * W), 0, st,
+                     I, u0, U, S, h, N, M, K, beta, theta, u_r);
+}
+
+template <int C, bool SPEC>
+static int fwd_fused_k(const float* I, const float* u0, float* U, float* S, WsHeader* h, int64_t N,
+                       int M, int K, float beta, float theta, float u_r, hipStream_t st) {
+  constexpr int W = 4;
+  if (!SPEC)
+    launch_fwd_fused<1, C, W, false>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+  else if (K <= 4)
+    launch_fwd_fused<4, C, W, true>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+  else if (K <= 8)
+    launch_fwd_fused<8, C, W, true>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+  else if (K <= 16)
+    launch_fwd_fused<16, C, W, true>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+  else
+    return LSH_ERR_SHAPE;
+  return LSH_OK;
+}
+
+template <bool SPEC>
+static int fwd_fused(const float* I, const float* u0, float* U, float* S, WsHeader* h, int64_t N,
+                     int M, int C, int K, float beta, float theta, float u_r, hipStream_t st) {
+  switch (C) {
+    case 16: return fwd_fused_k<16, SPEC>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+    case 32: return fwd_fused_k<32, SPEC>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+    case 64: return fwd_fused_k<64, SPEC>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+    case 128: return fwd_fused_k<128, SPEC>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+    default: return LSH_ERR_SHAPE;
+  }
+}
+
+template <int C, bool DETACH, bool HAS_GU>
+static void launch_bwd_fused(const float* I, const float* u0, const float* U, const float* S,
+                             const float* GS, const float* GU, float* Lam, int64_t N, int M,
+                             float beta, float theta, float u_r, float alpha, hipStream_t st) {
+  constexpr int W = 4;
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  hipLaunchKernelGGL((k_lif_bwd_fused<C, W, DETACH, HAS_GU>), dim3((unsigned)NB), dim3(WAVE * W), 0,
+                     st, I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha);
+}
+
+template <int C>
+static void bwd_fused_c(const float* I, const float* u0, const float* U, const float* S,
+                        const float* GS, const float* GU, float* Lam, int64_t N, int M, float beta,
+                        float theta, float u_r, float alpha, bool detach, hipStream_t st) {
+  if (detach) {
+    if (GU)
+      launch_bwd_fused<C, true, true>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
+    else
+      launch_bwd_fused<C, true, false>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
+  } else {
+    if (GU)
+      launch_bwd_fused<C, false, true>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
+    else
+      launch_bwd_fused<C, false, false>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
+  }
+}
+
+}  // namespace lsh
+
+using namespace lsh;
+
+extern "C" size_t lsh_lif_scan_exact_workspace(void) { return kWsHeaderBytes; }
+
+static int exact_fwd(bool spec, const float* I, const float* u0, float* U, float* S, int64_t T,
+                     int64_t N, float beta, float theta, float u_r, int C, int K, void* ws,
+                     size_t ws_bytes, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31 || K < 1 || K > 16) return LSH_ERR_SHAPE;
+  if (C != 16 && C != 32 && C != 64 && C != 128) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  // per-lane + per-row buffer byte offsets within one chunk must stay below 2^32
+  if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+  if (ws_bytes < kWsHeaderBytes || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+    return LSH_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  WsHeader* h = reinterpret_cast<WsHeader*>(ws);
+  hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, h);
+  if (T > 0 && N > 0) {
+    const int rc = spec ? fwd_fused<true>(I, u0, U, S, h, N, (int)(T / C), C, K, beta, theta, u_r, st)
+                        : fwd_fused<false>(I, u0, U, S, h, N, (int)(T / C), C, K, beta, theta, u_r, st);
+    if (rc != LSH_OK) return rc;
+  }
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" int lsh_lif_scan_exact_fwd(const float* I, const float* u0, float* U, float* S,
+                                      int64_t T, int64_t N, float beta, float theta, float u_r,
+                                      int C, int K, void* ws, size_t ws_bytes, void* stream) {
+  return exact_fwd(true, I, u0, U, S, T, N, beta, theta, u_r, C, K, ws, ws_bytes, stream);
+}
+
+extern "C" int lsh_lif_chunked_serial_fwd(const float* I, const float* u0, float* U, float* S,
+                                          int64_t T, int64_t N, float beta, float theta, float u_r,
+                                          int C, void* ws, size_t ws_bytes, void* stream) {
+  return exact_fwd(false, I, u0, U, S, T, N, beta, theta, u_r, C, 1, ws, ws_bytes, stream);
+}
+
+extern "C" int lsh_lif_scan_fused_bwd(const float* I, const float* u0, const float* U,
+                                      const float* S, const float* GS, const float* GU, float* Lam,
+                                      int64_t T, int64_t N, float beta, float theta, float u_r,
+                                      float alpha, int detach, int C, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(Lam))
+    return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C != 16 && C != 32 && C != 64) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  // per-lane + per-row buffer byte offsets within one chunk must stay below 2^32
+  if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int M = (int)(T / C);
+  const bool d = detach != 0;
+  switch (C) {
+    case 16: bwd_fused_c<16>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, d, st); break;
+    case 32: bwd_fused_c<32>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, d, st); break;
+    default: bwd_fused_c<64>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, d, st); break;
+  }
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}

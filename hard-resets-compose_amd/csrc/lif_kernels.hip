@@ -731,6 +731,9 @@ extern "C" int lsh_scan_stats_read(const void* ws, int64_t chunk_neurons, int64_
     out->miss_frac = 0.0;
     out->mean_lines = 0.0;
   }
+  out->fused_fixups = (int64_t)h.fused_fixups;
+  out->fused_unknown = (int64_t)h.fused_unknown;
+  out->spin_timeouts = (int64_t)h.spin_timeouts;
   out->super_overflow_frac = (double)h.super_ovf_count / sn;
   out->super_mean_pieces = (double)h.super_pieces_sum / sn + 1.0;
   out->super_max_pieces = (int64_t)h.super_pieces_max + 1;

@@ -35,9 +35,10 @@ struct WsHeader {
   unsigned long long alif_pieces_sum;  // ALIF: post-spike x-pieces kept
   unsigned int alif_pieces_max;
   unsigned int pad0;
-  unsigned long long ticket;           // dynamic tile ticket (look-back kernels)
-  unsigned int epoch;                  // per-call epoch for look-back status words
-  unsigned int pad1;
+  unsigned long long fused_fixups;     // fused scan: speculative chunk entries that missed
+  unsigned long long fused_unknown;    // fused scan: entries the maps could not predict
+  unsigned int spin_timeouts;          // bounded LDS waits that gave up (must stay 0)
+  unsigned int epoch;                  // advanced once per call
 };
 static_assert(sizeof(WsHeader) <= 256, "workspace header must fit in 256 bytes");
 constexpr size_t kWsHeaderBytes = 256;

@@ -47,6 +47,35 @@ __device__ __forceinline__ void st_nt(T* p, T v) { __builtin_nontemporal_store(v
 template <typename T>
 __device__ __forceinline__ T ld_nt(const T* p) { return __builtin_nontemporal_load(p); }
 
+// Row access with a wave-uniform row pointer and a 32-bit per-lane byte offset, so the
+// compiler can address with an SGPR base + VGPR offset instead of a 64-bit VGPR pair per
+// access (fewer VGPRs and address instructions in the unrolled time loops).
+__device__ __forceinline__ float ld_row(const float* __restrict__ row, unsigned boff) {
+  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(row) + boff);
+}
+__device__ __forceinline__ void st_row_nt(float* __restrict__ row, unsigned boff, float v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<float*>(reinterpret_cast<char*>(row) + boff));
+}
+
+// Raw buffer access (CDNA3/4): a 128-bit SGPR descriptor for a wave-uniform base address,
+// one per-lane VGPR byte offset shared by every access, and a wave-uniform SGPR byte offset
+// per time row.  The unrolled time loops then need no per-access address registers.
+// Descriptor word 3 (0x00020000) is the gfx9-family raw-buffer format (32-bit data).  The
+// record count is left at its maximum: callers keep every access in bounds themselves.
+struct Buf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ explicit Buf(const void* base)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)0xffffffff,
+                                            0x00020000)) {}
+  __device__ __forceinline__ float ld(unsigned voff, unsigned soff) const {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+  }
+  // non-temporal store (cache policy bit 1 = nt on gfx94x/gfx950)
+  __device__ __forceinline__ void st_nt(unsigned voff, unsigned soff, float v) const {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, voff, soff, 2);
+  }
+};
+
 // Wave-level reductions (wave64).
 __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll

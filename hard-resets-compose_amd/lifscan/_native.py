@@ -38,6 +38,9 @@ class ScanStats(ctypes.Structure):
         ("super_max_pieces", ctypes.c_int64),
         ("miss_frac", ctypes.c_double),
         ("mean_lines", ctypes.c_double),
+        ("fused_fixups", ctypes.c_int64),
+        ("fused_unknown", ctypes.c_int64),
+        ("spin_timeouts", ctypes.c_int64),
     ]
 
 
@@ -62,6 +65,13 @@ SIGNATURES = {
                                   c_i64, c_p, c_sz, c_p]),
     "lsh_scan_stats_read": (c_i, [c_p, c_i64, c_i64, c_i, ctypes.POINTER(ScanStats), c_p]),
     "lsh_lif_scan_v3_layout": (c_i, [c_i64, c_i64, c_i, c_i, ctypes.POINTER(V3Layout)]),
+    "lsh_lif_scan_exact_workspace": (c_sz, []),
+    "lsh_lif_scan_exact_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i, c_p,
+                                     c_sz, c_p]),
+    "lsh_lif_chunked_serial_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_p,
+                                         c_sz, c_p]),
+    "lsh_lif_scan_fused_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,
+                                     c_f, c_i, c_i, c_p]),
     "lsh_lif_scan_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
     "lsh_lif_scan_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f,
                                c_i, c_i, c_p, c_sz, c_p]),

@@ -237,7 +237,12 @@ def scan_forward_v3(I, beta, theta, u_r, u0, C=64, K=16, BN=32, nw=1, BNc=16, nw
 
     Stricter than the reference: T % C != 0 raises ValueError (the reference leaves the tail
     uninitialised).  stats receives repair_iters, overflow_frac, mean_pieces, max_pieces with
-    the reference's definitions (mean/max of kept breakpoints + 1)."""
+    the reference's definitions (mean/max of kept breakpoints + 1).  With the repair budget at
+    least T/C (converged) and no stats requested, the single-pass kernel computes the same
+    (serial-exact) result in one pass over I."""
+    I = _input(I)
+    if int(C) >= 1 and I.shape[0] % int(C) == 0 and _fused_fwd_ok(I.shape[0], C, K, repair, stats):
+        return scan_forward_exact(I, beta, theta, u_r, u0, K=K)
     return _scan2(I, beta, theta, u_r, u0, C, K, repair, stats)
 
 
@@ -288,10 +293,101 @@ def scan_forward_v2(I, beta, theta, u_r, u0, C=64, K=16, BN=128, nw=4, STAGES=3,
     return U, S
 
 
+# ----------------------------------------------------------------------------- single-pass exact scan
+# Internal chunk lengths of the single-pass kernels (their results do not depend on them:
+# the forward is bit-identical to the serial recurrence, the backward equals the two-level
+# affine scan up to fp32 association).
+FUSED_FWD_C = 32
+FUSED_BWD_C = 32
+FUSED_CHUNKS = (16, 32, 64, 128)
+
+_LAST_FUSED = None
+
+
+def last_fused_counters():
+    """Counters of the most recent single-pass forward: fused_fixups (chunk entries whose
+    map prediction missed), fused_unknown (entries the maps could not predict) and
+    spin_timeouts (must be 0).  Synchronizes."""
+    if _LAST_FUSED is None:
+        return None
+    st = _n.read_stats(_LAST_FUSED, 1)
+    return {"fused_fixups": int(st.fused_fixups), "fused_unknown": int(st.fused_unknown),
+            "spin_timeouts": int(st.spin_timeouts)}
+
+
+def scan_forward_exact(I, beta, theta, u_r, u0, C=None, K=8, maps=True):
+    """Single-pass exact two-level scan -> (U, S), bit-identical to the serial recurrence
+    (= scan_forward_v3 with the repair run to convergence), reading I once.  C is the
+    kernel's internal chunk length (16/32/64/128, default FUSED_FWD_C), K the map capacity
+    (<= 16).  maps=False hands chunk exits on without map predictions (chunked serial)."""
+    global _LAST_FUSED
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    C = int(C or FUSED_FWD_C)
+    if C not in FUSED_CHUNKS or T % C:
+        raise ValueError(f"single-pass scan needs C in {FUSED_CHUNKS} dividing T={T}")
+    if not 1 <= int(K) <= 16:
+        raise ValueError("single-pass scan supports map capacity K in [1, 16]")
+    L = _n.lib()
+    nbytes = L.lsh_lif_scan_exact_workspace()
+    ws = _n.workspace(nbytes, I.device)
+    U = torch.empty_like(I)
+    S = torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        st = _n.stream_of(I)
+        if maps:
+            rc = L.lsh_lif_scan_exact_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
+                                          _f32(beta), _f32(theta), _f32(u_r), C, int(K),
+                                          _n.ptr(ws), nbytes, st)
+        else:
+            rc = L.lsh_lif_chunked_serial_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
+                                              _f32(beta), _f32(theta), _f32(u_r), C, _n.ptr(ws),
+                                              nbytes, st)
+        _n.check(rc, "single-pass scan forward")
+    _LAST_FUSED = ws
+    return U, S
+
+
+def _fused_fwd_ok(T, C, K, repair, stats):
+    """The single-pass kernel gives the converged result; finite repair budgets and the
+    reference's stats (which describe the chunk-C maps) use the multi-kernel path."""
+    return stats is None and int(repair) >= T // int(C) and int(K) <= 16 and T % FUSED_FWD_C == 0
+
+
+def scan_backward_fused(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=None):
+    """Single-pass affine-scan adjoint -> Lam (I, U, S, GS read once)."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    U, S, GS = _same(U, I, "U"), _same(S, I, "S"), _same(GS, I, "GS")
+    GU = _same(GU, I, "GU")
+    C = int(C or FUSED_BWD_C)
+    if C not in (16, 32, 64) or T % C:
+        raise ValueError(f"single-pass backward needs C in (16, 32, 64) dividing T={T}")
+    Lam = torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        _n.check(_n.lib().lsh_lif_scan_fused_bwd(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS), _n.ptr(GU), _n.ptr(Lam), T, N,
+            _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), int(bool(detach)), C, _n.stream_of(I)),
+            "lsh_lif_scan_fused_bwd")
+    return Lam
+
+
 # ----------------------------------------------------------------------------- scan backward
 def scan_backward_tiled(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=64,
                         BNr=32, D=4, nwr=1):
-    """Affine-scan adjoint (triton_lif.py:512-526) -> Lam.  GU may be None (zeros)."""
+    """Affine-scan adjoint (triton_lif.py:512-526) -> Lam.  GU may be None (zeros).
+    Runs the single-pass kernel when T is a multiple of its internal chunk, else the
+    three-kernel chunk scan with chunk C."""
+    I = _input(I)
+    if I.shape[0] % FUSED_BWD_C == 0 and int(C) >= 1 and I.shape[0] % int(C) == 0:
+        return scan_backward_fused(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach)
+    return scan_backward_chunked(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach, C)
+
+
+def scan_backward_chunked(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=64):
+    """Three-kernel affine scan: chunk aggregates, reverse carry, reverse replay."""
     I = _input(I)
     T, N = I.shape
     u0 = _vec(u0, N, I)

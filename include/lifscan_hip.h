@@ -75,6 +75,25 @@ int lsh_lif_scan_lo_fwd(const float* I, const float* u0, const float* lo, float*
                         int64_t T, int64_t N, float beta, float theta, float u_r, int C, int K,
                         int64_t repair, void* ws, size_t ws_bytes, void* stream);
 
+/* Single-pass exact two-level scan forward: the result of lsh_lif_scan_v3_fwd with the repair
+ * run to convergence (bit-identical to the serial recurrence), computed in one pass over I.
+ * One workgroup per 64 neurons walks the chunks in rounds of 4 (one chunk per wave): chunk
+ * maps of capacity K are built from registers into LDS, speculative chunk entries are read
+ * off the maps, exact chunk exits are handed on through LDS and the chunk is stored from its
+ * exact entry.  Replaces triton_lif.py:782-817 (scan_forward_v3 with repair >= T/C) and
+ * :1228-1232.  C in {16, 32, 64, 128}, 1 <= K <= 16, T % C == 0.  Workspace:
+ * lsh_lif_scan_exact_workspace() bytes (counters only). */
+size_t lsh_lif_scan_exact_workspace(void);
+int lsh_lif_scan_exact_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
+                           int64_t N, float beta, float theta, float u_r, int C, int K, void* ws,
+                           size_t ws_bytes, void* stream);
+
+/* The same kernel without maps: each chunk waits for the exact exit of the previous one (a
+ * serial recurrence tiled over chunks, in-house baseline).  Same constraints as above. */
+int lsh_lif_chunked_serial_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
+                               int64_t N, float beta, float theta, float u_r, int C, void* ws,
+                               size_t ws_bytes, void* stream);
+
 /* Diagnostics of the last scan run in `ws` (synchronizes `stream`).  Same definitions as
  * the reference's stats dict: triton_lif.py:812-816 (v3), :976-982 (v4),
  * triton_alif.py:351-357 (ALIF). */
@@ -88,6 +107,9 @@ typedef struct lsh_scan_stats {
   int64_t super_max_pieces;
   double miss_frac;  /* ALIF only */
   double mean_lines; /* ALIF only */
+  int64_t fused_fixups;  /* single-pass scans: chunk entries whose map prediction missed */
+  int64_t fused_unknown; /* single-pass scans: chunk entries the maps could not predict */
+  int64_t spin_timeouts; /* bounded waits that gave up; always 0 unless a kernel is broken */
 } lsh_scan_stats;
 int lsh_scan_stats_read(const void* ws, int64_t chunk_neurons, int64_t super_neurons,
                         int alif, lsh_scan_stats* out, void* stream);
@@ -114,6 +136,15 @@ int lsh_lif_scan_bwd(const float* I, const float* u0, const float* U, const floa
                      const float* GS, const float* GU, float* Lam, int64_t T, int64_t N, float beta,
                      float theta, float u_r, float alpha, int detach, int C, void* ws,
                      size_t ws_bytes, void* stream);
+
+/* Single-pass affine-scan backward: per-step coefficients kept in registers, chunk
+ * aggregates composed through LDS, I/U/S/GS read once (20 B per neuron-step).  Same result
+ * as lsh_lif_scan_bwd up to fp32 association.  Replaces triton_lif.py:512-526 and :1235-1239.
+ * C (internal chunk) in {16, 32, 64}, T % C == 0.  GU may be NULL.  No workspace. */
+int lsh_lif_scan_fused_bwd(const float* I, const float* u0, const float* U, const float* S,
+                           const float* GS, const float* GU, float* Lam, int64_t T, int64_t N,
+                           float beta, float theta, float u_r, float alpha, int detach, int C,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,134 @@
+"""GPU parity of the single-pass fused kernels (lsh_lif_scan_exact_fwd,
+lsh_lif_chunked_serial_fwd, lsh_lif_scan_fused_bwd) against the CPU oracle.
+
+Forward: U and S bit-exact to the serial recurrence for every internal chunk length, map
+capacity and regime, including partial rounds (fewer chunks than waves per workgroup) and
+ragged neuron counts.  Backward: within 1e-5 relative of the fp32 oracle affine scan and
+1e-4 relative of the fp64 adjoint.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import lif_oracle as O
+from tests._inputs import gpu, host, normal, uniform
+
+pytestmark = pytest.mark.gpu
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from lifscan import hip_lif
+    return hip_lif
+
+
+REGIMES = [(b, mu, sd) for b in (0.5, 0.9, 0.99, 1.0) for (mu, sd) in ((0.15, 0.4), (-0.1, 0.6), (0.4, 0.2))]
+
+
+@pytest.mark.parametrize("beta,mu,sd", REGIMES)
+def test_exact_forward_regimes(L, dev, beta, mu, sd):
+    T, N = 1024, 777
+    I = normal(T, N, mu, sd, 3)
+    u0 = uniform(N, -0.3, 0.3, 4)
+    Us, Ss = O.serial_forward(I, beta, 1.0, -0.1, u0)
+    Ig, u0g = gpu(I, dev), gpu(u0, dev)
+    for C, K in ((16, 4), (32, 8), (64, 16), (128, 8)):
+        print(f"exact fwd beta={beta} mu={mu} C={C} K={K}", flush=True)
+        U, S = L.scan_forward_exact(Ig, beta, 1.0, -0.1, u0g, C=C, K=K)
+        assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+        assert L.last_fused_counters()["spin_timeouts"] == 0
+
+
+@pytest.mark.parametrize("T,N,C", [(16, 1, 16), (48, 65, 16), (160, 130, 32), (320, 64, 64),
+                                   (640, 200, 128), (4096, 3, 32)])
+def test_exact_forward_partial_rounds_and_ragged(L, dev, T, N, C):
+    I = normal(T, N, 0.12, 0.25, 5)
+    u0 = uniform(N, 0.0, 0.9, 6)
+    Us, Ss = O.serial_forward(I, 0.9, 1.0, 0.0, u0)
+    for K in (1, 16):
+        for maps in (True, False):
+            print(f"exact fwd T={T} N={N} C={C} K={K} maps={maps}", flush=True)
+            U, S = L.scan_forward_exact(gpu(I, dev), 0.9, 1.0, 0.0, gpu(u0, dev), C=C, K=K, maps=maps)
+            assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+            assert L.last_fused_counters()["spin_timeouts"] == 0
+
+
+def test_exact_forward_dyadic_ties(L, dev):
+    """beta = 1/2 on a 1/64 grid: exact ties v == theta (e2_float.py:30-41)."""
+    rng = np.random.default_rng(7)
+    T, N = 512, 256
+    I = (rng.integers(-40, 80, (T, N)) / 64.0).astype(np.float32)
+    u0 = (rng.integers(-64, 64, N) / 64.0).astype(np.float32)
+    Us, Ss = O.serial_forward(I, 0.5, 1.0, 0.0, u0)
+    U, S = L.scan_forward_exact(gpu(I, dev), 0.5, 1.0, 0.0, gpu(u0, dev), C=32, K=8)
+    assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+
+
+def test_v3_dispatches_to_single_pass_when_converged(L, dev):
+    T, N = 2048, 300
+    I = normal(T, N, 0.012, 0.08, 8)
+    u0 = np.zeros(N, np.float32)
+    Us, Ss = O.serial_forward(I, 0.99, 1.0, 0.0, u0)
+    U, S = L.scan_forward_v3(gpu(I, dev), 0.99, 1.0, 0.0, gpu(u0, dev), C=128, K=8, repair=10 ** 6)
+    assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+    c = L.last_fused_counters()
+    assert c["spin_timeouts"] == 0
+
+
+@pytest.mark.parametrize("C", [16, 32, 64])
+@pytest.mark.parametrize("detach,with_gu", [(True, False), (False, True)])
+def test_fused_backward(L, dev, C, detach, with_gu):
+    T, N = 1024, 333
+    I = normal(T, N, 0.15, 0.4, 9)
+    u0 = uniform(N, -0.2, 0.2, 10)
+    GS = normal(T, N, 0.0, 1.0, 11)
+    GU = normal(T, N, 0.0, 1.0, 12) if with_gu else None
+    U, S = O.serial_forward(I, 0.9, 1.0, -0.1, u0)
+    print(f"fused bwd C={C} detach={detach} gu={with_gu}", flush=True)
+    Lam = L.scan_backward_fused(gpu(I, dev), gpu(u0, dev), gpu(U, dev), gpu(S, dev), gpu(GS, dev),
+                                gpu(GU, dev) if with_gu else None, 0.9, 1.0, -0.1, 4.0, detach, C=C)
+    ref32 = O.scan_backward(I, u0, U, S, GS, GU, 0.9, 1.0, -0.1, 4.0, detach, C=C)
+    ref64 = O.serial_backward(I, u0, U, S, GS, GU, 0.9, 1.0, -0.1, 4.0, detach, dtype=np.float64)
+    assert rel(host(Lam), ref32) < 1e-5
+    assert rel(host(Lam), ref64) < 1e-4
+
+
+@pytest.mark.parametrize("T,N", [(16, 1), (48, 65), (4096, 3)])
+def test_fused_backward_partial_rounds(L, dev, T, N):
+    I = normal(T, N, 0.15, 0.4, 13)
+    u0 = np.zeros(N, np.float32)
+    GS = normal(T, N, 0.0, 1.0, 14)
+    U, S = O.serial_forward(I, 0.9, 1.0, 0.0, u0)
+    Lam = L.scan_backward_fused(gpu(I, dev), gpu(u0, dev), gpu(U, dev), gpu(S, dev), gpu(GS, dev),
+                                None, 0.9, 1.0, 0.0, 4.0, C=16)
+    ref64 = O.serial_backward(I, u0, U, S, GS, None, 0.9, 1.0, 0.0, 4.0, dtype=np.float64)
+    assert rel(host(Lam), ref64) < 1e-4
+
+
+def test_fused_cfg2_full_size(L, dev):
+    """cfg2 (65,536 x 4,096, beta = 0.9 and 0.99): single-pass forward == serial kernel bit for
+    bit; single-pass backward within 1e-5 of the three-kernel affine scan."""
+    T, N = 4096, 65536
+    for beta, mu, sd in ((0.9, 0.12, 0.25), (0.99, 0.012, 0.08)):
+        print(f"cfg2 fused beta={beta}", flush=True)
+        g = torch.Generator().manual_seed(0)
+        I = (mu + sd * torch.randn(T, N, generator=g)).to(dev)
+        g1 = torch.Generator().manual_seed(1)
+        GS = torch.randn(T, N, generator=g1).to(dev)
+        u0 = torch.zeros(N, device=dev)
+        Us, Ss = L.serial_forward(I, beta, 1.0, 0.0, u0)
+        for C in (32, 128):
+            U, S = L.scan_forward_exact(I, beta, 1.0, 0.0, u0, C=C, K=8)
+            assert torch.equal(U, Us) and torch.equal(S, Ss)
+            print(f"  C={C} counters={L.last_fused_counters()}", flush=True)
+        L1 = L.scan_backward_fused(I, u0, Us, Ss, GS, None, beta, 1.0, 0.0, 4.0)
+        L2 = L.scan_backward_chunked(I, u0, Us, Ss, GS, None, beta, 1.0, 0.0, 4.0, C=128)
+        assert ((L1 - L2).norm() / L2.norm()).item() < 1e-5
+        del I, GS, Us, Ss, U, S, L1, L2
+        torch.cuda.empty_cache()

@@ -4,14 +4,18 @@
 Workload ("cfg2"): 65,536 neurons x T = 4,096, fp32, beta = 0.9,
 x ~ N(0.12, 0.25^2) (seeded CPU generator, copied to HBM before timing), u0 = 0, theta = 1,
 u_r = 0, upstream gradient gS ~ N(0, 1).  One step = lif_tuned(mode="scan", K=8, repair on)
-forward + backward (autograd), i.e. the two-level exact scan (chunk C = 128 from the
-reference's _pick_C) and the affine-scan adjoint; spikes are bit-identical to the serial
-recurrence.  value = neuron-steps/s of that fwd+bwd step.
+forward + backward through autograd: the exact two-level scan (single pass, bit-identical to
+the serial recurrence) and the single-pass affine-scan adjoint.  value = neuron-steps/s of
+that fwd+bwd step.
 
-Printed JSON (one line on stdout) also carries: the forward-only throughput, the in-house
-tuned HIP serial baseline (fwd, fwd+bwd), the beta = 0.99 variant, scan stats, the roofline
-of the dominant kernel and the CPU baseline (PyTorch-CPU port of the reference's fast.py,
-timed on a bounded sample on this host).
+The JSON line also carries the forward-only rate, the scan with map speculation forced on,
+the in-house HIP serial baseline, the beta = 0.99 variant, the map statistics of the
+reference's chunking (C = 128, K = 8), the roofline of the dominant kernel (HIP events on the
+stream it runs on) and the CPU baseline (PyTorch-CPU port of the reference's fast.py on a
+bounded sample, timed on this host).
+
+  python bench.py [--steps K] [--warmup W] [--no-cpu]
+  python bench.py --dominant-only    # short run for rocprofv3 --pmc passes (copy + kernel)
 """
 import argparse
 import json
@@ -26,7 +30,8 @@ for p in (os.path.join(REPO, "hard-resets-compose_amd"), REPO):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
-B_FWD, B_BWD = 12, 20  # algorithmic bytes per neuron-step (read I; write U, S | read I, U, S, gS; write dI)
+B_FWD, B_BWD = 12, 20  # algorithmic bytes per neuron-step: read I; write U, S | read I, U, S, gS; write dI
+T_CFG, N_CFG = 4096, 65536
 
 
 def log(*a):
@@ -34,8 +39,8 @@ def log(*a):
 
 
 def ev_time(fn, reps, warm=1):
-    """Median ms of fn() over reps, HIP events on torch's current stream (the stream every
-    library call launches on)."""
+    """Median ms of fn() over reps with HIP events on torch's current stream, the stream
+    every library call launches on."""
     import torch
     for _ in range(warm):
         fn()
@@ -52,10 +57,20 @@ def ev_time(fn, reps, warm=1):
     return statistics.median(ts)
 
 
+def inputs(beta, dev):
+    import torch
+    mu, sd = (0.12, 0.25) if beta == 0.9 else (0.012, 0.08)
+    g = torch.Generator().manual_seed(0)
+    I_cpu = (mu + sd * torch.randn(T_CFG, N_CFG, generator=g)).float()
+    g1 = torch.Generator().manual_seed(1)
+    gS = torch.randn(T_CFG, N_CFG, generator=g1).float().to(dev)
+    return I_cpu, I_cpu.to(dev), gS
+
+
 def cpu_baseline(I_cpu, beta, n_cols):
     """PyTorch-CPU port of fast.py: two-level pruned scan forward (C=64, K=8, repair on) and
     the Hillis-Steele affine-scan backward, plus the serial pair, on the first n_cols neurons
-    of the same workload."""
+    of the same workload; median of 3 after one warm-up."""
     import torch
     from oracle import fast_port as F
     torch.set_num_threads(os.cpu_count() or 1)
@@ -75,7 +90,7 @@ def cpu_baseline(I_cpu, beta, n_cols):
 
     out = {}
     for name, fn in (("scan", scan_fb), ("serial", serial_fb)):
-        fn()  # warm-up
+        fn()
         ts = []
         for _ in range(3):
             t0 = time.perf_counter()
@@ -85,6 +100,24 @@ def cpu_baseline(I_cpu, beta, n_cols):
     return out
 
 
+def dominant_only(L, torch, dev):
+    """Short program for counter passes: a 256 MiB copy (FETCH/WRITE calibration), then the
+    dominant kernel (single-pass backward, cfg2) three times."""
+    x = torch.empty(64 * 2 ** 20, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    I_cpu, I, gS = inputs(0.9, dev)
+    u0 = torch.zeros(N_CFG, device=dev)
+    U, S = L.scan_forward_exact(I, 0.9, 1.0, 0.0, u0, K=8)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        L.scan_backward_fused(I, u0, U, S, gS, None, 0.9, 1.0, 0.0, 4.0)
+    torch.cuda.synchronize()
+    print(json.dumps({"dominant_only": True, "copy_bytes_each_way": 4 * x.numel(),
+                      "kernel": "k_lif_bwd_fused", "launches": 3}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -92,6 +125,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-cols", type=int, default=8192)
+    ap.add_argument("--dominant-only", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the exact LIF scan shards along neurons with no "
@@ -100,21 +134,20 @@ def main():
         sys.exit(2)
 
     import torch
-    from lifscan import triton_lif as L
+    from lifscan import hip_lif as L
+    from lifscan import triton_lif as TL
 
     dev = torch.device("cuda:0")
-    T, N, beta = 4096, 65536, 0.9
-    g = torch.Generator().manual_seed(0)
-    I_cpu = (0.12 + 0.25 * torch.randn(T, N, generator=g)).float()
-    g1 = torch.Generator().manual_seed(1)
-    gS = torch.randn(T, N, generator=g1).float().to(dev)
-    I = I_cpu.to(dev)
+    if args.dominant_only:
+        dominant_only(L, torch, dev)
+        return
+    T, N, beta, K = T_CFG, N_CFG, 0.9, 8
+    I_cpu, I, gS = inputs(beta, dev)
     u0 = torch.zeros(N, device=dev)
-    K = 8
 
     def step():
         Ig = I.detach().requires_grad_(True)
-        S = L.lif_tuned(Ig, u0, beta, 1.0, 0.0, 4.0, mode="scan", K=K, repair=10 ** 6)
+        S = TL.lif_tuned(Ig, u0, beta, 1.0, 0.0, 4.0, mode="scan", K=K, repair=10 ** 6)
         S.backward(gS)
         return Ig.grad
 
@@ -131,50 +164,58 @@ def main():
     value = N * T / (ms_step / 1000.0)
     log(f"fwd+bwd {ms_step:.3f} ms/step  {value / 1e9:.1f} G neuron-steps/s")
 
-    # component timings (HIP events, median)
+    # components (HIP events, median of 10)
     C = L._pick_C(T, D=16)
-    Cb = min(128, L._pick_C(T, D=2))
+    reps = 10
+    U, S = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6)
+    ms = {}
+    ms["scan_fwd"] = ev_time(lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6), reps)
+    ms["scan_fwd_maps_forced_C16"] = ev_time(
+        lambda: L.scan_forward_exact(I, beta, 1.0, 0.0, u0, C=16, K=K, maps=True), reps)
+    L.scan_forward_exact(I, beta, 1.0, 0.0, u0, C=16, K=K, maps=True)
+    maps_ctr = L.last_fused_counters()
+    ms["scan_bwd"] = ev_time(lambda: L.scan_backward_tiled(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0, C=C), reps)
+    ms["multikernel_scan_fwd_C128"] = ev_time(
+        lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6, stats={}), 3)
+    ms["serial_fwd"] = ev_time(lambda: L.serial_forward(I, beta, 1.0, 0.0, u0), reps)
+    ms["serial_bwd"] = ev_time(lambda: L.serial_backward(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), reps)
     st = {}
     L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6, stats=st)
-    U, S = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6)
-    t_fwd = ev_time(lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6), 10)
-    t_bwd = ev_time(lambda: L.scan_backward_tiled(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0, C=Cb), 10)
-    t_sf = ev_time(lambda: L.serial_forward(I, beta, 1.0, 0.0, u0), 10)
-    t_sb = ev_time(lambda: L.serial_backward(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), 10)
-    log(f"scan fwd {t_fwd:.3f} ms, scan bwd {t_bwd:.3f} ms, serial fwd {t_sf:.3f}, serial bwd {t_sb:.3f}")
+    # dominant kernel: the single-pass backward is one launch of k_lif_bwd_fused per call
+    t_dom = ev_time(lambda: L.scan_backward_fused(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), 20)
+    log("ms " + json.dumps({k: round(v, 4) for k, v in ms.items()}) + f" dominant {t_dom:.4f}")
     del U, S
 
     # beta = 0.99 variant of cfg2
-    g2 = torch.Generator().manual_seed(0)
-    I99 = (0.012 + 0.08 * torch.randn(T, N, generator=g2)).float().to(dev)
+    _, I99, _ = inputs(0.99, dev)
+    U99, S99 = L.scan_forward_v3(I99, 0.99, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6)
+    ms["scan_fwd_beta0.99"] = ev_time(lambda: L.scan_forward_v3(I99, 0.99, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6), reps)
+    ms["scan_bwd_beta0.99"] = ev_time(lambda: L.scan_backward_tiled(I99, u0, U99, S99, gS, None, 0.99, 1.0, 0.0, 4.0, C=C), reps)
+    ms["scan_fwd_maps_forced_C16_beta0.99"] = ev_time(
+        lambda: L.scan_forward_exact(I99, 0.99, 1.0, 0.0, u0, C=16, K=K, maps=True), reps)
     st99 = {}
     L.scan_forward_v3(I99, 0.99, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6, stats=st99)
-    U99, S99 = L.scan_forward_v3(I99, 0.99, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6)
-    t_fwd99 = ev_time(lambda: L.scan_forward_v3(I99, 0.99, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6), 10)
-    t_bwd99 = ev_time(lambda: L.scan_backward_tiled(I99, u0, U99, S99, gS, None, 0.99, 1.0, 0.0, 4.0, C=Cb), 10)
     del U99, S99, I99
 
-    # dominant cost: the larger of the two passes, priced on its algorithmic bytes
-    if t_bwd >= t_fwd:
-        dom, dom_ms, dom_b = "scan backward (lsh_lif_scan_bwd)", t_bwd, B_BWD
-    else:
-        dom, dom_ms, dom_b = "scan forward (lsh_lif_scan_v3_fwd)", t_fwd, B_FWD
-    achieved = dom_b * N * T / (dom_ms / 1000.0) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": dom, "bytes_per_neuron_step": dom_b}
+    achieved = B_BWD * N * T / (t_dom / 1000.0) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "k_lif_bwd_fused (single-pass affine-scan adjoint, C=32, W=4)",
+                "algorithmic_bytes_per_launch": B_BWD * N * T, "avg_launch_ms": round(t_dom, 4)}
 
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline on {args.cpu_cols} neurons x T={T}")
         r = cpu_baseline(I_cpu, beta, args.cpu_cols)
-        ns = args.cpu_cols * T
-        cpu = {"value": round(ns / r["scan"], 1), "unit": "neuron-steps/s", "cores": torch.get_num_threads(),
-               "kind": "port",
-               "sample": f"fast.py two-level pruned scan (C=64,K=8,repair on) + affine-scan bwd, "
-                         f"{args.cpu_cols} of {N} neurons x T={T}, median of 3",
-               "serial_value": round(ns / r["serial"], 1), "os_cpu_count": os.cpu_count()}
+        nsteps = args.cpu_cols * T
+        cpu = {"value": round(nsteps / r["scan"], 1), "unit": "neuron-steps/s",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"fast.py two-level pruned scan fwd (C=64,K=8,repair on) + Hillis-Steele "
+                         f"affine-scan bwd on {args.cpu_cols} of {N} neurons x T={T}, median of 3",
+               "serial_fwd_bwd_value": round(nsteps / r["serial"], 1),
+               "os_cpu_count": os.cpu_count()}
 
+    pct = lambda b, t: round(100 * b * N * T / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
     out = {
         "metric": "neuron-steps/s fwd and fwd+bwd (LIF, 65536xT4096 fp32); % of HBM roofline",
         "value": round(value, 1),
@@ -187,18 +228,18 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (seeded CPU generator, x~N(0.12,0.25^2), gS~N(0,1))",
-        "config": {"workload": "cfg2: lif_tuned scan fwd+bwd, N=65536 (256x256), T=4096, beta=0.9, "
-                               "theta=1, u_r=0, u0=0, C=128, K=8, repair on",
+        "data": "synthetic (seeded CPU generator: x~N(0.12,0.25^2), gS~N(0,1))",
+        "config": {"workload": "cfg2: lif_tuned(mode=scan, K=8, repair on) fwd+bwd, N=65536 "
+                               "(256x256), T=4096, beta=0.9, theta=1, u_r=0, u0=0",
                    "N": N, "T": T, "beta": beta, "C": C, "K": K},
-        "fwd_value": round(N * T / (t_fwd / 1000.0), 1),
-        "pct_roofline_fwd_bwd": round(100 * (B_FWD + B_BWD) * N * T / (ms_step / 1000.0) / 1e9 / HBM_PEAK_GBS, 2),
-        "pct_roofline_fwd": round(100 * B_FWD * N * T / (t_fwd / 1000.0) / 1e9 / HBM_PEAK_GBS, 2),
-        "ms": {"scan_fwd": round(t_fwd, 4), "scan_bwd": round(t_bwd, 4), "serial_fwd": round(t_sf, 4),
-               "serial_bwd": round(t_sb, 4), "scan_fwd_beta0.99": round(t_fwd99, 4),
-               "scan_bwd_beta0.99": round(t_bwd99, 4)},
-        "serial_hip_value": round(N * T / ((t_sf + t_sb) / 1000.0), 1),
-        "stats": {"beta0.9": st, "beta0.99": st99},
+        "pct_roofline_fwd_bwd": pct(B_FWD + B_BWD, ms_step),
+        "fwd_value": round(N * T / (ms["scan_fwd"] / 1000.0), 1),
+        "pct_roofline_fwd": pct(B_FWD, ms["scan_fwd"]),
+        "pct_roofline_bwd": pct(B_BWD, ms["scan_bwd"]),
+        "ms": {k: round(v, 4) for k, v in ms.items()},
+        "serial_hip_fwd_bwd_value": round(N * T / ((ms["serial_fwd"] + ms["serial_bwd"]) / 1000.0), 1),
+        "maps_forced_counters": maps_ctr,
+        "stats_C128_K8": {"beta0.9": st, "beta0.99": st99},
         "roofline": roofline,
         "cpu_baseline": cpu,
     }

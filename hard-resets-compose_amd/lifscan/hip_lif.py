@@ -300,6 +300,9 @@ def scan_forward_v2(I, beta, theta, u_r, u0, C=64, K=16, BN=128, nw=4, STAGES=3,
 FUSED_FWD_C = 32
 FUSED_BWD_C = 32
 FUSED_CHUNKS = (16, 32, 64, 128)
+# Map speculation shortens the in-workgroup hand-off chain; it pays when few neuron blocks
+# run (the chain latency is exposed), and costs VALU time otherwise (many blocks hide it).
+FUSED_MAPS_MAX_N = 8192
 
 _LAST_FUSED = None
 
@@ -315,11 +318,12 @@ def last_fused_counters():
             "spin_timeouts": int(st.spin_timeouts)}
 
 
-def scan_forward_exact(I, beta, theta, u_r, u0, C=None, K=8, maps=True):
+def scan_forward_exact(I, beta, theta, u_r, u0, C=None, K=8, maps="auto"):
     """Single-pass exact two-level scan -> (U, S), bit-identical to the serial recurrence
     (= scan_forward_v3 with the repair run to convergence), reading I once.  C is the
     kernel's internal chunk length (16/32/64/128, default FUSED_FWD_C), K the map capacity
-    (<= 16).  maps=False hands chunk exits on without map predictions (chunked serial)."""
+    (<= 16).  maps=False hands chunk exits on without map predictions (chunked serial);
+    "auto" builds maps when N <= FUSED_MAPS_MAX_N."""
     global _LAST_FUSED
     I = _input(I)
     T, N = I.shape
@@ -329,6 +333,8 @@ def scan_forward_exact(I, beta, theta, u_r, u0, C=None, K=8, maps=True):
         raise ValueError(f"single-pass scan needs C in {FUSED_CHUNKS} dividing T={T}")
     if not 1 <= int(K) <= 16:
         raise ValueError("single-pass scan supports map capacity K in [1, 16]")
+    if maps == "auto":
+        maps = N <= FUSED_MAPS_MAX_N
     L = _n.lib()
     nbytes = L.lsh_lif_scan_exact_workspace()
     ws = _n.workspace(nbytes, I.device)

@@ -57,6 +57,19 @@ def ev_time(fn, reps, warm=1):
     return statistics.median(ts)
 
 
+def profiled_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed counter summary
+    (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled on a copy kernel)."""
+    path = os.path.join(REPO, "profiles", "k_lif_bwd_fused_cfg2_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def inputs(beta, dev):
     import torch
     mu, sd = (0.12, 0.25) if beta == 0.9 else (0.012, 0.08)
@@ -199,7 +212,9 @@ def main():
 
     achieved = B_BWD * N * T / (t_dom / 1000.0) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
+                "traffic_source": "profiles/k_lif_bwd_fused_cfg2_traffic.txt (rocprofv3 --pmc FETCH_SIZE, "
+                                  "WRITE_SIZE; bytes per launch)",
                 "kernel": "k_lif_bwd_fused (single-pass affine-scan adjoint, C=32, W=4)",
                 "algorithmic_bytes_per_launch": B_BWD * N * T, "avg_launch_ms": round(t_dom, 4)}
 

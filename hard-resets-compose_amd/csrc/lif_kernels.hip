@@ -533,7 +533,7 @@ static void launch_bwd(const float* I, const float* u0, const float* U, const fl
   }
 }
 
-static void v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3_layout* L) {
+void v3_layout_fill(int64_t T, int64_t N, int C, int K, lsh_v3_layout* L) {
   const int64_t M = T / C;
   const size_t mn = (size_t)M * (size_t)N * 4;
   const size_t nb = (size_t)((N + WAVE - 1) / WAVE);
@@ -558,9 +558,9 @@ static void v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3_layout* L) {
 }
 
 template <int KMAX>
-static void launch_build_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
-                               const lsh_v3_layout& L, int64_t N, int M, int C, int K, float beta,
-                               float theta, float u_r, hipStream_t st) {
+static void launch_build(const float* I, const float* u0, char* ws, const lsh_v3_layout& L,
+                         int64_t N, int M, int C, int K, float beta, float theta, float u_r,
+                         hipStream_t st) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(ws + off); };
@@ -572,10 +572,47 @@ static void launch_build_carry(const float* I, const float* u0, const float* lo_
     hipLaunchKernelGGL((k_lif_build<KMAX, 1>), dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, u0,
                        F(L.EC), F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
                        F(L.MC), N, C, NB, K, beta, theta, u_r);
+}
+
+template <int KMAX>
+static void launch_build_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
+                               const lsh_v3_layout& L, int64_t N, int M, int C, int K, float beta,
+                               float theta, float u_r, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
+  auto Iq = [&](size_t off) { return reinterpret_cast<int*>(ws + off); };
+  launch_build<KMAX>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
   hipLaunchKernelGGL((k_lif_carry<KMAX>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, F(L.EC),
                      F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX), F(L.MC),
-                     lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS), reinterpret_cast<WsHeader*>(ws), N,
-                     M, C, K, beta, theta, u_r);
+                     lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS),
+                     reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r);
+}
+
+// Build kernel alone (used by the three-level scan).
+int lif_build_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L, int64_t N,
+                     int M, int C, int K, float beta, float theta, float u_r, hipStream_t st) {
+  if (K <= 4) launch_build<4>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
+  else if (K <= 8) launch_build<8>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
+  else if (K <= 16) launch_build<16>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
+  else if (K <= 32) launch_build<32>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
+  else launch_build<64>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
+  return LSH_OK;
+}
+
+// Replay of every chunk from its carried start, then the device repair rounds.
+void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* S, float* starts,
+                              float* ends, int* list0, int* list1, WsHeader* hdr, int64_t N, int M,
+                              int C, int64_t repair, float beta, float theta, float u_r,
+                              hipStream_t st) {
+  launch_fwd_auto(I, starts, U, S, ends, N, C, M, beta, theta, u_r, st);
+  if (repair > 0 && M > 1) {
+    // Round r makes the starts of chunks 0..r exact, so M rounds always converge; the cap
+    // only bounds the work when NaN inputs make the comparison fail forever.
+    const int64_t rounds = repair < (int64_t)M ? repair : (int64_t)M;
+    const int NB = (int)((N + WAVE - 1) / WAVE);
+    hipLaunchKernelGGL(k_lif_repair, dim3((unsigned)NB), dim3(256), 0, st, I, U, S, starts, ends,
+                       list0, list1, hdr, N, M, C, rounds, beta, theta, u_r);
+  }
 }
 
 }  // namespace lsh
@@ -638,14 +675,14 @@ extern "C" int lsh_lif_scan_v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3
   if (bad_ptr(out)) return LSH_ERR_ARG;
   const int rc = v3_check(T, N, C, K);
   if (rc != LSH_OK) return rc;
-  v3_layout(T, N, C, K, out);
+  v3_layout_fill(T, N, C, K, out);
   return LSH_OK;
 }
 
 extern "C" size_t lsh_lif_scan_v3_workspace(int64_t T, int64_t N, int C, int K) {
   if (v3_check(T, N, C, K) != LSH_OK) return 0;
   lsh_v3_layout L;
-  v3_layout(T, N, C, K, &L);
+  v3_layout_fill(T, N, C, K, &L);
   return L.total;
 }
 
@@ -657,7 +694,7 @@ static int scan2_fwd(const float* I, const float* u0, const float* lo_neuron, fl
   int rc = v3_check(T, N, C, K);
   if (rc != LSH_OK) return rc;
   lsh_v3_layout L;
-  v3_layout(T, N, C, K, &L);
+  v3_layout_fill(T, N, C, K, &L);
   if (ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0) return LSH_ERR_WORKSPACE;
   hipStream_t st = (hipStream_t)stream;
   char* w = static_cast<char*>(ws);
@@ -677,18 +714,10 @@ static int scan2_fwd(const float* I, const float* u0, const float* lo_neuron, fl
     launch_build_carry<32>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
   else
     launch_build_carry<64>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
-  float* starts = reinterpret_cast<float*>(w + L.STARTS);
-  float* ends = reinterpret_cast<float*>(w + L.ENDS);
-  launch_fwd_auto(I, starts, U, S, ends, N, C, M, beta, theta, u_r, st);
-  if (repair > 0 && M > 1) {
-    // Round r makes the starts of chunks 0..r exact, so M rounds always converge; the cap
-    // only bounds the work when NaN inputs make the comparison fail forever.
-    const int64_t rounds = repair < (int64_t)M ? repair : (int64_t)M;
-    const int NB = (int)((N + WAVE - 1) / WAVE);
-    hipLaunchKernelGGL(k_lif_repair, dim3((unsigned)NB), dim3(256), 0, st, I, U, S, starts, ends,
-                       reinterpret_cast<int*>(w + L.LIST0), reinterpret_cast<int*>(w + L.LIST1),
-                       reinterpret_cast<WsHeader*>(w), N, M, C, rounds, beta, theta, u_r);
-  }
+  lif_replay_repair_launch(I, u0, U, S, reinterpret_cast<float*>(w + L.STARTS),
+                           reinterpret_cast<float*>(w + L.ENDS), reinterpret_cast<int*>(w + L.LIST0),
+                           reinterpret_cast<int*>(w + L.LIST1), reinterpret_cast<WsHeader*>(w), N,
+                           M, C, repair, beta, theta, u_r, st);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }

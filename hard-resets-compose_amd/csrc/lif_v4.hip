@@ -1,0 +1,458 @@
+// Three-level exact scan for long sequences (reference: triton_lif.py:935-983,
+// scan_forward_v4): chunk maps are composed in groups of G into super-chunk maps of capacity
+// K2, the carry runs over the M/G super maps, then inside every super map in parallel, then
+// every chunk is replayed.  Sequential depth ~ C + G (compose) + M/G + G + C instead of
+// C + M + C.
+//
+// Kernels (one lane per neuron, one wave per 64 neurons):
+//   k_lif_env_trunc   sequential over chunks: envelope bound Lo[m] of every chunk entry and
+//                     the reference's lo-pruned map (breakpoint count, overflow flag) by
+//                     truncating the hi-pruned map of k_lif_build (see that kernel);
+//   k_lif_compose     per (super, neuron): G-1 compositions (triton_lif.py:829-899);
+//   k_map_carry       sequential over super maps with overflow-to-serial fallback
+//                     (triton_lif.py:579-606 with K = K2 and fallback length C*G);
+//   k_lif_carry_inner per (super, neuron): G chunk-map evaluations (triton_lif.py:903-932).
+#include "lsh_abi.h"
+#include "lsh_common.h"
+
+namespace lsh {
+
+// Map evaluation (triton_lif.py:592-599): k = #{i < n : xd[i] > u}; k == n -> A*u + B,
+// else cd[k].
+template <int KMAX>
+__device__ __forceinline__ float eval_slots(const float* xd, const float* cd, int n, float A,
+                                            float B, float u) {
+  int k = 0;
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) k += (i < n && xd[i] > u) ? 1 : 0;
+  float c = 0.0f;
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) c = (i == k) ? cd[i] : c;
+  return k == n ? __fadd_rn(__fmul_rn(A, u), B) : c;
+}
+
+// Serial fallback over L steps of column n from row r0 (same step arithmetic as the replay).
+__device__ __forceinline__ float serial_rows(const float* __restrict__ I, int64_t N, int64_t n,
+                                             int64_t r0, int64_t L, float u, float beta,
+                                             float theta, float u_r) {
+  const float* __restrict__ Ip = I + (size_t)r0 * N + n;
+  for (int64_t j = 0; j < L; ++j) {
+    bool s;
+    u = lif_step(u, Ip[(size_t)j * N], beta, theta, u_r, s);
+  }
+  return u;
+}
+
+template <int KMAX>
+__global__ __launch_bounds__(64) void k_lif_env_trunc(
+    const float* __restrict__ u0, const float* __restrict__ EC, const float* __restrict__ EA,
+    const float* __restrict__ EB, const int* __restrict__ CNT, const int* __restrict__ OVFRAW,
+    const float* __restrict__ MX, float* __restrict__ LO, int* __restrict__ MN,
+    int* __restrict__ OVF, WsHeader* hdr, int64_t N, int M, int K) {
+  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
+  const bool valid = n < N;
+  unsigned long long ovf_acc = 0, pcs_acc = 0;
+  int pmax = 0;
+  if (valid) {
+    const float margin = 1e-5f;
+    float l = u0[n];
+    for (int m = 0; m < M; ++m) {
+      const size_t o = (size_t)m * N + n;
+      const float lo = l - margin * (fabsf(l) + 1.0f);
+      LO[o] = lo;
+      l = fminf(EC[o], __fadd_rn(__fmul_rn(EA[o], l), EB[o]));
+      const int cnt = CNT[o];
+      int gt = 0;
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i)
+        if (i < K && i < cnt) gt += MX[((size_t)m * K + i) * N + n] > lo ? 1 : 0;
+      const int ne = min(cnt, gt + 1);
+      const bool ovf = OVFRAW[o] != 0 && gt == cnt;
+      MN[o] = ne;
+      OVF[o] = ovf ? 1 : 0;
+      ovf_acc += ovf ? 1ull : 0ull;
+      pcs_acc += (unsigned long long)ne;
+      pmax = max(pmax, ne);
+    }
+  }
+  ovf_acc = wave_sum_u64(ovf_acc);
+  pcs_acc = wave_sum_u64(pcs_acc);
+  pmax = wave_max_i(pmax);
+  if (threadIdx.x == 0) {
+    atomicAdd(&hdr->ovf_count, ovf_acc);
+    atomicAdd(&hdr->pieces_sum, pcs_acc);
+    atomicMax(&hdr->pieces_max, (unsigned int)pmax);
+  }
+}
+
+template <int KMAX, int K2MAX>
+__global__ __launch_bounds__(64) void k_lif_compose(
+    const float* __restrict__ MA, const float* __restrict__ MB, const int* __restrict__ MN,
+    const int* __restrict__ OVF, const float* __restrict__ MX, const float* __restrict__ MC,
+    const float* __restrict__ LO, const float* __restrict__ u0, float* __restrict__ SA,
+    float* __restrict__ SB, int* __restrict__ SN, int* __restrict__ SOVF, float* __restrict__ SX,
+    float* __restrict__ SC, WsHeader* hdr, int64_t N, int NB, int G, int K, int K2, float theta,
+    float u_r) {
+  const int64_t s = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - s * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  const bool valid = n < N;
+  const int64_t nn = valid ? n : N - 1;
+  const int64_t m0 = s * G;
+  const float lo = LO[(size_t)m0 * N + nn];
+  const float hi = fmaxf(u0[nn], fmaxf(theta, u_r));
+  float A = MA[(size_t)m0 * N + nn], B = MB[(size_t)m0 * N + nn];
+  int nH = MN[(size_t)m0 * N + nn];
+  int ov = OVF[(size_t)m0 * N + nn];
+  float X[K2MAX], Cc[K2MAX];
+#pragma unroll
+  for (int i = 0; i < K2MAX; ++i) {
+    const bool in = i < K && i < K2;
+    X[i] = in ? MX[((size_t)m0 * K + i) * N + nn] : INFINITY;
+    Cc[i] = in ? MC[((size_t)m0 * K + i) * N + nn] : 0.0f;
+  }
+  float xmin = INFINITY;
+#pragma unroll
+  for (int i = 0; i < K2MAX; ++i) xmin = (i < nH) ? fminf(xmin, X[i]) : xmin;
+  int wnH = wave_max_i(nH);
+  for (int jj = 1; jj < G; ++jj) {
+    const int64_t m = m0 + jj;
+    const size_t o = (size_t)m * N + nn;
+    const float Ag = MA[o], Bg = MB[o];
+    const int ng = MN[o];
+    ov |= OVF[o];
+    const int wng = wave_max_i(ng);
+    float yd[KMAX], dd[KMAX];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j < wng) {
+        yd[j] = MX[((size_t)m * K + j) * N + nn];
+        dd[j] = MC[((size_t)m * K + j) * N + nn];
+      } else {
+        yd[j] = INFINITY;
+        dd[j] = 0.0f;
+      }
+    }
+    // (1) the left map's constants pushed through the right map
+#pragma unroll
+    for (int i = 0; i < K2MAX; ++i) {
+      if (i < wnH) {
+        int c = 0;
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j)
+          if (j < wng) c += (j < ng && yd[j] > Cc[i]) ? 1 : 0;
+        float gc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j)
+          if (j < wng) gc = (c == j) ? dd[j] : gc;
+        Cc[i] = (c == ng) ? __fadd_rn(__fmul_rn(Ag, Cc[i]), Bg) : gc;
+      }
+    }
+    // (2) the right map's breakpoints pulled back through the left map's affine part
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      if (j < wng) {
+        const float num = yd[j] - B;
+        const float z = A == 0.0f ? (num > 0.0f ? INFINITY : -INFINITY) : num / A;
+        bool nw = (j < ng) && (z < xmin) && (z <= hi) && (xmin > lo);
+        if (nw && nH >= K2) ov = 1;
+        nw = nw && (nH < K2);
+#pragma unroll
+        for (int i = 0; i < K2MAX; ++i) {
+          if (i <= wnH) {
+            const bool put = nw && (i == nH);
+            X[i] = put ? z : X[i];
+            Cc[i] = put ? dd[j] : Cc[i];
+          }
+        }
+        if (__ballot(nw && nH == wnH) != 0ull) ++wnH;
+        nH += nw ? 1 : 0;
+        xmin = nw ? z : xmin;
+      }
+    }
+    // (3) affine parts
+    B = __fadd_rn(__fmul_rn(Ag, B), Bg);
+    A = Ag * A;
+  }
+  unsigned long long so = 0, sp = 0;
+  int smax = 0;
+  if (valid) {
+    const size_t o = (size_t)s * N + n;
+    SA[o] = A;
+    SB[o] = B;
+    SN[o] = nH;
+    SOVF[o] = ov;
+#pragma unroll
+    for (int i = 0; i < K2MAX; ++i) {
+      if (i < K2) {
+        SX[((size_t)s * K2 + i) * N + n] = X[i];
+        SC[((size_t)s * K2 + i) * N + n] = Cc[i];
+      }
+    }
+    so = ov ? 1ull : 0ull;
+    sp = (unsigned long long)nH;
+    smax = nH;
+  }
+  so = wave_sum_u64(so);
+  sp = wave_sum_u64(sp);
+  smax = wave_max_i(smax);
+  if (threadIdx.x == 0) {
+    atomicAdd(&hdr->super_ovf_count, so);
+    atomicAdd(&hdr->super_pieces_sum, sp);
+    atomicMax(&hdr->super_pieces_max, (unsigned int)smax);
+  }
+}
+
+// Sequential carry over pre-pruned maps (n and ovf final) with the next map's loads issued
+// before the current evaluation; overflowed maps fall back to L serial steps.
+template <int KMAX>
+__global__ __launch_bounds__(64) void k_map_carry(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ MA,
+    const float* __restrict__ MB, const int* __restrict__ MN, const int* __restrict__ OVF,
+    const float* __restrict__ MX, const float* __restrict__ MC, float* __restrict__ starts,
+    int64_t N, int M, int K, int64_t L, float beta, float theta, float u_r) {
+  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
+  if (n >= N) return;
+  float u = u0[n];
+  float xd[KMAX], cd[KMAX], A, B;
+  int cnt, ovf;
+  auto load = [&](int m, float* x, float* c, float& a, float& b, int& k, int& f) {
+    const size_t o = (size_t)m * N + n;
+    a = MA[o];
+    b = MB[o];
+    k = MN[o];
+    f = OVF[o];
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+      x[i] = i < K ? MX[((size_t)m * K + i) * N + n] : INFINITY;
+      c[i] = i < K ? MC[((size_t)m * K + i) * N + n] : 0.0f;
+    }
+  };
+  if (M > 0) load(0, xd, cd, A, B, cnt, ovf);
+  for (int m = 0; m < M; ++m) {
+    float xd2[KMAX], cd2[KMAX], A2 = 1.0f, B2 = 0.0f;
+    int cnt2 = 0, ovf2 = 0;
+    if (m + 1 < M) load(m + 1, xd2, cd2, A2, B2, cnt2, ovf2);
+    starts[(size_t)m * N + n] = u;
+    float nu = eval_slots<KMAX>(xd, cd, cnt, A, B, u);
+    if (ovf) nu = serial_rows(I, N, n, (int64_t)m * L, L, u, beta, theta, u_r);
+    u = nu;
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+      xd[i] = xd2[i];
+      cd[i] = cd2[i];
+    }
+    A = A2;
+    B = B2;
+    cnt = cnt2;
+    ovf = ovf2;
+  }
+}
+
+template <int KMAX>
+__global__ __launch_bounds__(64) void k_lif_carry_inner(
+    const float* __restrict__ I, const float* __restrict__ sstarts, const float* __restrict__ MA,
+    const float* __restrict__ MB, const int* __restrict__ MN, const int* __restrict__ OVF,
+    const float* __restrict__ MX, const float* __restrict__ MC, float* __restrict__ starts,
+    int64_t N, int NB, int G, int C, int K, float beta, float theta, float u_r) {
+  const int64_t s = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - s * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  if (n >= N) return;
+  float u = sstarts[(size_t)s * N + n];
+  for (int jj = 0; jj < G; ++jj) {
+    const int64_t m = s * G + jj;
+    const size_t o = (size_t)m * N + n;
+    starts[o] = u;
+    float xd[KMAX], cd[KMAX];
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+      xd[i] = i < K ? MX[((size_t)m * K + i) * N + n] : INFINITY;
+      cd[i] = i < K ? MC[((size_t)m * K + i) * N + n] : 0.0f;
+    }
+    float nu = eval_slots<KMAX>(xd, cd, MN[o], MA[o], MB[o], u);
+    if (OVF[o]) nu = serial_rows(I, N, n, m * C, C, u, beta, theta, u_r);
+    u = nu;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// entry point plumbing (the build, replay and repair kernels live in lif_kernels.hip)
+int lif_build_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L, int64_t N,
+                     int M, int C, int K, float beta, float theta, float u_r, hipStream_t st);
+void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* S, float* starts,
+                              float* ends, int* list0, int* list1, WsHeader* hdr, int64_t N, int M,
+                              int C, int64_t repair, float beta, float theta, float u_r,
+                              hipStream_t st);
+
+static int kcap(int k) { return k <= 4 ? 4 : k <= 8 ? 8 : k <= 16 ? 16 : k <= 32 ? 32 : 64; }
+
+template <int KMAX, int K2MAX>
+static void launch_compose(char* w, const lsh_v4_layout& L, const float* u0, int64_t N, int M2,
+                           int G, int K, int K2, float theta, float u_r, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
+  auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  hipLaunchKernelGGL((k_lif_compose<KMAX, K2MAX>), dim3((unsigned)((int64_t)M2 * NB)), dim3(WAVE), 0,
+                     st, F(L.v3.MA), F(L.v3.MB), Iq(L.v3.MN), Iq(L.v3.OVF), F(L.v3.MX), F(L.v3.MC),
+                     F(L.v3.LO), u0, F(L.SA), F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC),
+                     reinterpret_cast<WsHeader*>(w), N, NB, G, K, K2, theta, u_r);
+}
+
+template <int KMAX>
+static int launch_compose_k2(char* w, const lsh_v4_layout& L, const float* u0, int64_t N, int M2,
+                             int G, int K, int K2, float theta, float u_r, hipStream_t st) {
+  switch (kcap(K2)) {
+    case 4: if (KMAX <= 4) { launch_compose<KMAX, 4>(w, L, u0, N, M2, G, K, K2, theta, u_r, st); return LSH_OK; } break;
+    case 8: if (KMAX <= 8) { launch_compose<KMAX, 8>(w, L, u0, N, M2, G, K, K2, theta, u_r, st); return LSH_OK; } break;
+    case 16: if (KMAX <= 16) { launch_compose<KMAX, 16>(w, L, u0, N, M2, G, K, K2, theta, u_r, st); return LSH_OK; } break;
+    case 32: if (KMAX <= 32) { launch_compose<KMAX, 32>(w, L, u0, N, M2, G, K, K2, theta, u_r, st); return LSH_OK; } break;
+    default: launch_compose<KMAX, 64>(w, L, u0, N, M2, G, K, K2, theta, u_r, st); return LSH_OK;
+  }
+  return LSH_ERR_SHAPE;
+}
+
+template <int KMAX>
+static void launch_chunk_kernels(const float* I, const float* u0, char* w, const lsh_v4_layout& L,
+                                 int64_t N, int M, int G, int C, int K, float beta, float theta,
+                                 float u_r, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
+  auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  hipLaunchKernelGGL((k_lif_env_trunc<KMAX>), dim3((unsigned)NB), dim3(WAVE), 0, st, u0, F(L.v3.EC),
+                     F(L.v3.EA), F(L.v3.EB), Iq(L.v3.CNT), Iq(L.v3.OVFRAW), F(L.v3.MX), F(L.v3.LO),
+                     Iq(L.v3.MN), Iq(L.v3.OVF), reinterpret_cast<WsHeader*>(w), N, M, K);
+}
+
+template <int KMAX>
+static void launch_inner(const float* I, char* w, const lsh_v4_layout& L, int64_t N, int M2, int G,
+                         int C, int K, float beta, float theta, float u_r, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
+  auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  hipLaunchKernelGGL((k_lif_carry_inner<KMAX>), dim3((unsigned)((int64_t)M2 * NB)), dim3(WAVE), 0, st,
+                     I, F(L.SSTARTS), F(L.v3.MA), F(L.v3.MB), Iq(L.v3.MN), Iq(L.v3.OVF), F(L.v3.MX),
+                     F(L.v3.MC), F(L.v3.STARTS), N, NB, G, C, K, beta, theta, u_r);
+}
+
+template <int K2MAX>
+static void launch_super_carry(const float* I, const float* u0, char* w, const lsh_v4_layout& L,
+                               int64_t N, int M2, int K2, int64_t Lsteps, float beta, float theta,
+                               float u_r, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
+  auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  hipLaunchKernelGGL((k_map_carry<K2MAX>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, F(L.SA),
+                     F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC), F(L.SSTARTS), N, M2, K2,
+                     Lsteps, beta, theta, u_r);
+}
+
+void v3_layout_fill(int64_t T, int64_t N, int C, int K, lsh_v3_layout* L);
+
+static int v4_check(int64_t T, int64_t N, int C, int G, int K, int K2) {
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C < 1 || G < 1 || K < 1 || K > 32 || K2 < 1 || K2 > 64 || K > K2) return LSH_ERR_SHAPE;
+  if (T % C != 0 || (T / C) % G != 0) return LSH_ERR_DIVISIBILITY;
+  if ((T / C) * ((N + WAVE - 1) / WAVE) > ((int64_t)1 << 31) - 1) return LSH_ERR_SHAPE;
+  return LSH_OK;
+}
+
+static void v4_layout(int64_t T, int64_t N, int C, int G, int K, int K2, lsh_v4_layout* L) {
+  v3_layout_fill(T, N, C, K, &L->v3);
+  const int64_t M2 = (T / C) / G;
+  const size_t sn = (size_t)M2 * (size_t)N * 4;
+  Carver c;
+  c.off = L->v3.total;
+  L->SA = c.take(sn);
+  L->SB = c.take(sn);
+  L->SN = c.take(sn);
+  L->SOVF = c.take(sn);
+  L->SX = c.take(sn * (size_t)K2);
+  L->SC = c.take(sn * (size_t)K2);
+  L->SSTARTS = c.take(sn);
+  L->total = c.off;
+}
+
+}  // namespace lsh
+
+using namespace lsh;
+
+extern "C" int lsh_lif_scan_v4_layout(int64_t T, int64_t N, int C, int G, int K, int K2,
+                                      lsh_v4_layout* out) {
+  if (bad_ptr(out)) return LSH_ERR_ARG;
+  const int rc = v4_check(T, N, C, G, K, K2);
+  if (rc != LSH_OK) return rc;
+  v4_layout(T, N, C, G, K, K2, out);
+  return LSH_OK;
+}
+
+extern "C" size_t lsh_lif_scan_v4_workspace(int64_t T, int64_t N, int C, int G, int K, int K2) {
+  if (v4_check(T, N, C, G, K, K2) != LSH_OK) return 0;
+  lsh_v4_layout L;
+  v4_layout(T, N, C, G, K, K2, &L);
+  return L.total;
+}
+
+extern "C" int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
+                                   int64_t N, float beta, float theta, float u_r, int C, int G,
+                                   int K, int K2, int64_t repair, void* ws, size_t ws_bytes,
+                                   void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
+  if (repair < 0) return LSH_ERR_ARG;
+  const int rc = v4_check(T, N, C, G, K, K2);
+  if (rc != LSH_OK) return rc;
+  lsh_v4_layout L;
+  v4_layout(T, N, C, G, K, K2, &L);
+  if (ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0) return LSH_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  char* w = static_cast<char*>(ws);
+  WsHeader* h = reinterpret_cast<WsHeader*>(w);
+  hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, h);
+  if (T == 0 || N == 0) {
+    LSH_CHECK_LAUNCH();
+    return LSH_OK;
+  }
+  const int M = (int)(T / C);
+  const int M2 = M / G;
+  int r = lif_build_launch(I, u0, w, L.v3, N, M, C, K, beta, theta, u_r, st);
+  if (r != LSH_OK) return r;
+  switch (kcap(K)) {
+    case 4:
+      launch_chunk_kernels<4>(I, u0, w, L, N, M, G, C, K, beta, theta, u_r, st);
+      r = launch_compose_k2<4>(w, L, u0, N, M2, G, K, K2, theta, u_r, st);
+      break;
+    case 8:
+      launch_chunk_kernels<8>(I, u0, w, L, N, M, G, C, K, beta, theta, u_r, st);
+      r = launch_compose_k2<8>(w, L, u0, N, M2, G, K, K2, theta, u_r, st);
+      break;
+    case 16:
+      launch_chunk_kernels<16>(I, u0, w, L, N, M, G, C, K, beta, theta, u_r, st);
+      r = launch_compose_k2<16>(w, L, u0, N, M2, G, K, K2, theta, u_r, st);
+      break;
+    default:
+      launch_chunk_kernels<32>(I, u0, w, L, N, M, G, C, K, beta, theta, u_r, st);
+      r = launch_compose_k2<32>(w, L, u0, N, M2, G, K, K2, theta, u_r, st);
+      break;
+  }
+  if (r != LSH_OK) return r;
+  switch (kcap(K2)) {
+    case 4: launch_super_carry<4>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
+    case 8: launch_super_carry<8>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
+    case 16: launch_super_carry<16>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
+    case 32: launch_super_carry<32>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
+    default: launch_super_carry<64>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
+  }
+  switch (kcap(K)) {
+    case 4: launch_inner<4>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st); break;
+    case 8: launch_inner<8>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st); break;
+    case 16: launch_inner<16>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st); break;
+    default: launch_inner<32>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st); break;
+  }
+  lif_replay_repair_launch(I, u0, U, S, reinterpret_cast<float*>(w + L.v3.STARTS),
+                           reinterpret_cast<float*>(w + L.v3.ENDS),
+                           reinterpret_cast<int*>(w + L.v3.LIST0),
+                           reinterpret_cast<int*>(w + L.v3.LIST1), h, N, M, C, repair, beta, theta,
+                           u_r, st);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}

@@ -50,6 +50,11 @@ class V3Layout(ctypes.Structure):
         "ENDS", "LIST0", "LIST1", "total")]
 
 
+class V4Layout(ctypes.Structure):
+    _fields_ = [("v3", V3Layout)] + [(n, ctypes.c_size_t) for n in (
+        "SA", "SB", "SN", "SOVF", "SX", "SC", "SSTARTS", "total")]
+
+
 # name -> (restype, argtypes); mirrors include/lifscan_hip.h
 SIGNATURES = {
     "lsh_abi_version": (c_i, []),
@@ -72,6 +77,10 @@ SIGNATURES = {
                                          c_sz, c_p]),
     "lsh_lif_scan_fused_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,
                                      c_f, c_i, c_i, c_p]),
+    "lsh_lif_scan_v4_workspace": (c_sz, [c_i64, c_i64, c_i, c_i, c_i, c_i]),
+    "lsh_lif_scan_v4_layout": (c_i, [c_i64, c_i64, c_i, c_i, c_i, c_i, ctypes.POINTER(V4Layout)]),
+    "lsh_lif_scan_v4_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i, c_i, c_i,
+                                  c_i64, c_p, c_sz, c_p]),
     "lsh_lif_scan_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
     "lsh_lif_scan_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f,
                                c_i, c_i, c_p, c_sz, c_p]),

@@ -293,6 +293,65 @@ def scan_forward_v2(I, beta, theta, u_r, u0, C=64, K=16, BN=128, nw=4, STAGES=3,
     return U, S
 
 
+class _ScanRunV4(_ScanRun):
+    """Workspace of one three-level scan call: chunk arrays as in v3, plus super maps."""
+
+    def __init__(self, ws, T, N, C, G, K, K2):
+        super().__init__(ws, T, N, C, K)
+        self.G, self.K2 = G, K2
+
+    def layout(self):
+        L = _n.V4Layout()
+        _n.check(_n.lib().lsh_lif_scan_v4_layout(self.T, self.N, self.C, self.G, self.K, self.K2,
+                                                 _n.ctypes.byref(L)), "lsh_lif_scan_v4_layout")
+        return L
+
+    def view(self, name, dtype=torch.float32):
+        L = self.layout()
+        M = self.T // self.C
+        M2 = M // self.G
+        if name in ("SA", "SB", "SN", "SOVF", "SX", "SC", "SSTARTS"):
+            off = getattr(L, name)
+            shape = (M2, self.K2, self.N) if name in ("SX", "SC") else (M2, self.N)
+        else:
+            off = getattr(L.v3, name)
+            shape = (M, self.K, self.N) if name in ("MX", "MC") else (M, self.N)
+        nbytes = 4 * math.prod(shape)
+        return self.ws[off:off + nbytes].view(dtype).view(*shape)
+
+
+def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=1, BNg=16, nwg=1,
+                    BNc=16, nwc=1, BNr=32, D=8, nwr=1, repair=0, stats=None):
+    """Three-level exact scan (triton_lif.py:935-983) -> (U, S).  T must be divisible by C*G
+    (ValueError, the reference asserts).  stats receives repair_iters, overflow_frac,
+    super_overflow_frac, mean_pieces, super_mean_pieces, super_max_pieces (:976-982)."""
+    global _LAST_RUN
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    C, G, K, K2 = int(C), int(G), int(K), int(K2)
+    if C < 1 or G < 1 or T % C or (T // C) % G:
+        raise ValueError(f"T={T} must be divisible by C*G={C * G}")
+    if not (1 <= K <= 32 and K <= K2 <= 64):
+        raise ValueError("three-level scan needs 1 <= K <= 32 and K <= K2 <= 64")
+    L = _n.lib()
+    nbytes = L.lsh_lif_scan_v4_workspace(T, N, C, G, K, K2)
+    if nbytes == 0:
+        raise ValueError(f"unsupported three-level scan shape T={T} N={N} C={C} G={G}")
+    ws = _n.workspace(nbytes, I.device)
+    U = torch.empty_like(I)
+    S = torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        _n.check(L.lsh_lif_scan_v4_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
+                                       _f32(beta), _f32(theta), _f32(u_r), C, G, K, K2,
+                                       int(repair), _n.ptr(ws), nbytes, _n.stream_of(I)),
+                 "lsh_lif_scan_v4_fwd")
+    _LAST_RUN = _ScanRunV4(ws, T, N, C, G, K, K2)
+    if stats is not None:
+        _fill_stats(stats, _n.read_stats(ws, (T // C) * N, (T // C // G) * N), v4=True)
+    return U, S
+
+
 # ----------------------------------------------------------------------------- single-pass exact scan
 # Internal chunk lengths of the single-pass kernels (their results do not depend on them:
 # the forward is bit-identical to the serial recurrence, the backward equals the two-level

@@ -128,6 +128,25 @@ typedef struct lsh_v3_layout {
 } lsh_v3_layout;
 int lsh_lif_scan_v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3_layout* out);
 
+/* Three-level exact scan for long sequences: capacity-K chunk maps composed in groups of G
+ * into capacity-K2 super maps, carry over the super maps, carry inside every super map in
+ * parallel, replay, Jacobi repair on device.  Replaces triton_lif.py:935-983
+ * (scan_forward_v4), :829-899 (compose_group_kernel), :903-932 (carry_inner_kernel).
+ * Requires T % C == 0, (T / C) % G == 0, 1 <= K <= K2, K <= 32, K2 <= 64. */
+typedef struct lsh_v4_layout {
+  lsh_v3_layout v3;     /* chunk-level arrays, as for lsh_lif_scan_v3_fwd */
+  size_t SA, SB, SN, SOVF; /* super maps [M/G, N] */
+  size_t SX, SC;        /* super breakpoints / constants [M/G, K2, N] */
+  size_t SSTARTS;       /* super-chunk entry states [M/G, N] */
+  size_t total;
+} lsh_v4_layout;
+size_t lsh_lif_scan_v4_workspace(int64_t T, int64_t N, int C, int G, int K, int K2);
+int lsh_lif_scan_v4_layout(int64_t T, int64_t N, int C, int G, int K, int K2,
+                           lsh_v4_layout* out);
+int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, float* S, int64_t T, int64_t N,
+                        float beta, float theta, float u_r, int C, int G, int K, int K2,
+                        int64_t repair, void* ws, size_t ws_bytes, void* stream);
+
 /* Affine-scan backward: chunk composition of lam_t = a_t*lam_{t+1} + b_t, reverse carry,
  * reverse replay.  Replaces triton_lif.py:512-526 (scan_backward_tiled), :298-312
  * (scan_backward) and :1235-1239 (scan_backward_auto).  GU may be NULL (zeros). */

@@ -254,6 +254,125 @@ def state_bounds(I, beta, theta, u_r, u0):
     return lo.astype(f32), hi.astype(f32)
 
 
+# ----------------------------------------------------------------------------- three-level scan
+def compose_groups(A, B, xd, cd, n, ovf, Lo, u0, theta, u_r, G, K2):
+    """Compose G consecutive chunk maps into super maps of capacity K2
+    (triton_lif.py:829-899 compose_group_kernel): (1) push the left map's constants through
+    the right map, (2) pull the right map's breakpoints back through the left map's affine
+    part, appended iff z < xmin, z <= hi and xmin > lo (lo of the group's first chunk),
+    overflow past K2, (3) compose the affine parts.  Returns SA, SB, SX, SC, SN, SOVF."""
+    M, K, N = xd.shape
+    M2 = M // G
+    th, ur = _s(theta), _s(u_r)
+    hi = np.maximum(np.asarray(u0, dtype=f32), np.maximum(th, ur))
+    SA = np.empty((M2, N), f32)
+    SB = np.empty((M2, N), f32)
+    SX = np.full((M2, K2, N), INF, f32)
+    SC = np.zeros((M2, K2, N), f32)
+    SN = np.empty((M2, N), np.int32)
+    SOVF = np.empty((M2, N), np.int32)
+    k2 = np.arange(K2)[:, None]
+    for s_ in range(M2):
+        m0 = s_ * G
+        lo = Lo[m0]
+        Ah, Bh = A[m0].copy(), B[m0].copy()
+        nH = n[m0].astype(np.int32).copy()
+        ov = ovf[m0].astype(np.int32).copy()
+        X = np.full((K2, N), INF, f32)
+        Cc = np.zeros((K2, N), f32)
+        kk = min(K, K2)
+        X[:kk] = xd[m0, :kk]
+        Cc[:kk] = cd[m0, :kk]
+        xmin = np.where(k2 < nH[None], X, INF).min(0).astype(f32)
+        for jj in range(1, G):
+            m = m0 + jj
+            Ag, Bg, ng = A[m], B[m], n[m]
+            yd, dd = xd[m], cd[m]
+            ov = ov | ovf[m]
+            cnt = np.zeros((K2, N), np.int32)
+            for j in range(K):
+                cnt += ((yd[j][None] > Cc) & (j < ng)[None]).astype(np.int32)
+            gc = np.zeros((K2, N), f32)
+            for j in range(K):
+                gc = np.where(cnt == j, dd[j][None], gc)
+            Cc = np.where(cnt == ng[None], Ag[None] * Cc + Bg[None], gc).astype(f32)
+            for j in range(K):
+                num = yd[j] - Bh
+                z = _safe_div(num, Ah)
+                new = (j < ng) & (z < xmin) & (z <= hi) & (xmin > lo)
+                ov = np.where(new & (nH >= K2), 1, ov).astype(np.int32)
+                new = new & (nH < K2)
+                slot = (k2 == nH[None]) & new[None]
+                X = np.where(slot, z[None], X)
+                Cc = np.where(slot, dd[j][None], Cc).astype(f32)
+                nH = nH + new.astype(np.int32)
+                xmin = np.where(new, z, xmin).astype(f32)
+            Bh = Ag * Bh + Bg
+            Ah = Ag * Ah
+        SA[s_], SB[s_], SX[s_], SC[s_], SN[s_], SOVF[s_] = Ah, Bh, X, Cc, nH, ov
+    return SA, SB, SX, SC, SN, SOVF
+
+
+def carry_inner(I, sstarts, A, B, xd, cd, n, ovf, beta, theta, u_r, C, G):
+    """Carry the G chunk maps of every super map in parallel from its start
+    (triton_lif.py:903-932 carry_inner_kernel)."""
+    M, N = A.shape
+    M2 = M // G
+    starts = np.empty((M, N), f32)
+    u = sstarts.astype(f32).copy()  # [M2, N]
+    for jj in range(G):
+        ms = np.arange(M2) * G + jj
+        starts[ms] = u
+        nu = np.empty_like(u)
+        for s_ in range(M2):
+            m = s_ * G + jj
+            v = eval_map(A[m], B[m], xd[m], cd[m], n[m], u[s_])
+            if ovf[m].any():
+                w = serial_segment(I[m * C:(m + 1) * C], beta, theta, u_r, u[s_])
+                v = np.where(ovf[m] > 0, w, v).astype(f32)
+            nu[s_] = v
+        u = nu
+    return starts
+
+
+def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, repair=0, stats=None,
+                    keep=None):
+    """Three-level scan (triton_lif.py:935-983): envelope -> chunk maps -> group composition
+    -> carry over super maps -> inner carry -> replay -> repair; stats as :976-982."""
+    I = np.ascontiguousarray(I, dtype=f32)
+    T, N = I.shape
+    M = T // C
+    assert T % C == 0 and M % G == 0, "T must be divisible by C*G"
+    u0 = np.asarray(u0, dtype=f32).reshape(N)
+    hi = np.maximum(u0, np.maximum(_s(theta), _s(u_r)))
+    EC, EA, EB = envelope_chunks(I, beta, u_r, C)
+    Lo = envelope_carry(u0, EC, EA, EB)
+    A, B, xd, cd, n, ovf = build_maps(I, beta, theta, u_r, Lo, hi, C, K)
+    SA, SB, SX, SC, SN, SOVF = compose_groups(A, B, xd, cd, n, ovf, Lo, u0, theta, u_r, G, K2)
+    sstarts = carry(I, u0, SA, SB, SX, SC, SN, SOVF, beta, theta, u_r, C * G)
+    starts = carry_inner(I, sstarts, A, B, xd, cd, n, ovf, beta, theta, u_r, C, G)
+    U, S, ends = replay(I, starts, beta, theta, u_r, C)
+    it = 0
+    for it in range(1, repair + 1):
+        new = np.concatenate([u0[None], ends[:-1]], 0)
+        if np.array_equal(new, starts):
+            it -= 1
+            break
+        starts = new
+        U, S, ends = replay(I, starts, beta, theta, u_r, C)
+    if stats is not None:
+        stats["repair_iters"] = it
+        stats["overflow_frac"] = float(ovf.astype(np.float64).mean())
+        stats["super_overflow_frac"] = float(SOVF.astype(np.float64).mean())
+        stats["mean_pieces"] = float(n.astype(np.float64).mean()) + 1
+        stats["super_mean_pieces"] = float(SN.astype(np.float64).mean()) + 1
+        stats["super_max_pieces"] = int(SN.max()) + 1
+    if keep is not None:
+        keep.update(Lo=Lo, A=A, B=B, xd=xd, cd=cd, n=n, ovf=ovf, SA=SA, SB=SB, SX=SX, SC=SC,
+                    SN=SN, SOVF=SOVF, sstarts=sstarts, starts=starts)
+    return U, S
+
+
 # ----------------------------------------------------------------------------- scan backward
 def scan_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=64):
     """Two-level affine scan of the adjoint (triton_lif.py:422-457, :198-208, :383-418), fp32."""

@@ -230,3 +230,49 @@ def test_cfg2_scan_equals_serial_full_size(L, dev):
         assert np.array_equal(host(Us[:, cols]), Uo) and np.array_equal(host(Ss[:, cols]), So)
         del I, Us, Ss, U, S
         torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("beta,mu,sd", [(0.5, 0.15, 0.4), (0.9, 0.15, 0.4), (0.99, 0.012, 0.08),
+                                        (1.0, -0.1, 0.6), (0.9, 0.4, 0.2)])
+def test_scan_v4_matches_oracle(L, dev, beta, mu, sd):
+    """Three-level scan (experiments/test_v4.py shapes: N=777): chunk and super maps, starts,
+    U, S and stats equal the oracle bit for bit at repair=0; repair on gives the serial
+    recurrence."""
+    T, N, C, G = 2048, 777, 64, 8
+    I = normal(T, N, mu, sd, 25)
+    u0 = uniform(N, -0.3, 0.3, 26)
+    Ig, u0g = gpu(I, dev), gpu(u0, dev)
+    Us, Ss = O.serial_forward(I, beta, 1.0, -0.1, u0)
+    for K, K2 in ((16, 32), (8, 16), (4, 4)):
+        print(f"v4 beta={beta} mu={mu} K={K} K2={K2}", flush=True)
+        st, sto, keep = {}, {}, {}
+        U, S = L.scan_forward_v4(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, stats=st)
+        run = L.last_scan_run()
+        Uo, So = O.scan_forward_v4(I, beta, 1.0, -0.1, u0, C=C, G=G, K=K, K2=K2, stats=sto, keep=keep)
+        assert np.array_equal(host(run.view("LO")), keep["Lo"])
+        assert np.array_equal(host(run.view("MN", torch.int32)), keep["n"])
+        assert np.array_equal(host(run.view("OVF", torch.int32)), keep["ovf"])
+        SN = host(run.view("SN", torch.int32))
+        assert np.array_equal(SN, keep["SN"])
+        assert np.array_equal(host(run.view("SOVF", torch.int32)), keep["SOVF"])
+        assert np.array_equal(host(run.view("SA")), keep["SA"])
+        assert np.array_equal(host(run.view("SB")), keep["SB"])
+        valid = np.arange(K2)[None, :, None] < SN[:, None, :]
+        assert np.array_equal(host(run.view("SX"))[valid], keep["SX"][valid])
+        assert np.array_equal(host(run.view("SC"))[valid], keep["SC"][valid])
+        assert np.array_equal(host(run.view("SSTARTS")), keep["sstarts"])
+        assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+        assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+        for k in sto:
+            assert st[k] == pytest.approx(sto[k], rel=1e-12), k
+        U2, S2 = L.scan_forward_v4(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
+        assert np.array_equal(host(U2), Us) and np.array_equal(host(S2), Ss)
+
+
+def test_scan_v4_rejects_bad_shapes(L, dev):
+    I = torch.zeros(64 * 5, 8, device=dev)
+    u0 = torch.zeros(8, device=dev)
+    with pytest.raises(ValueError):
+        L.scan_forward_v4(I, 0.9, 1.0, 0.0, u0, C=64, G=2)
+    with pytest.raises(ValueError):
+        L.scan_forward_v4(I, 0.9, 1.0, 0.0, u0, C=64, G=5, K=16, K2=8)

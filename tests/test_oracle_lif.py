@@ -336,3 +336,52 @@ def test_pick_C_policy():
     assert O.pick_C(4096, 16) == 128 and O.pick_C(1024, 16) == 64 and O.pick_C(2 ** 20, 16) == 256
     with pytest.raises(ValueError):
         O.pick_C(100, 16)
+
+
+def test_group_composition_equals_map_of_concatenation():
+    """Maps are closed under composition (paper/main.tex:132-140; exact.py:108-131): on exact
+    inputs, composing G chunk maps (unpruned) gives the Theorem-1 map of the G*C-step segment."""
+    rng = np.random.default_rng(21)
+    C, G, N = 4, 4, 48
+    cols = [_dyadic_case(rng, C * G, -12, 20) for _ in range(N)]
+    I = np.array([[float(c[t]) for c in cols] for t in range(C * G)], dtype=np.float32)
+    M = G
+    lo = np.full((M, N), -np.inf, np.float32)
+    hi = np.full(N, np.inf, np.float32)
+    A, B, xd, cd, n, ovf = O.build_maps(I, 0.5, 1.0, 0.0, lo, hi, C, C)
+    SA, SB, SX, SC, SN, SOVF = O.compose_groups(A, B, xd, cd, n, ovf, lo, np.zeros(N, np.float32) - 1e30,
+                                                1e30, 0.0, G, C * G)
+    for j in range(N):
+        Ae, Be, xs, cs = _closed_form(cols[j], Fr(1, 2), Fr(1), Fr(0))
+        assert Fr(float(SA[0, j])) == Ae and Fr(float(SB[0, j])) == Be
+        assert SN[0, j] == len(xs) and SOVF[0, j] == 0
+        assert [Fr(float(v)) for v in SX[0, :SN[0, j], j]] == xs
+        assert [Fr(float(v)) for v in SC[0, :SN[0, j], j]] == cs
+
+
+@pytest.mark.parametrize("beta,mu,sd", [(0.9, 0.15, 0.4), (0.99, 0.012, 0.08), (0.5, -0.1, 0.6), (1.0, 0.4, 0.2)])
+def test_scan_v4_with_repair_equals_serial(beta, mu, sd):
+    T, N = 2048, 64
+    I = normal(T, N, mu, sd, 22)
+    u0 = uniform(N, -0.3, 0.3, 23)
+    Us, Ss = O.serial_forward(I, beta, 1.0, -0.1, u0)
+    for K, K2 in ((16, 32), (8, 16), (2, 4)):
+        st = {}
+        U, S = O.scan_forward_v4(I, beta, 1.0, -0.1, u0, C=64, G=8, K=K, K2=K2, repair=10 ** 6, stats=st)
+        assert np.array_equal(U, Us) and np.array_equal(S, Ss)
+        assert set(st) == {"repair_iters", "overflow_frac", "super_overflow_frac", "mean_pieces",
+                           "super_mean_pieces", "super_max_pieces"}
+
+
+def test_scan_v4_super_starts_match_serial_where_maps_are_exact():
+    """Super-chunk starts read off the composed maps equal the serial states at super
+    boundaries except where a map's affine piece or overflow makes them approximate."""
+    T, N, C, G = 4096, 128, 64, 8
+    I = normal(T, N, 0.15, 0.4, 24)
+    u0 = np.zeros(N, np.float32)
+    keep = {}
+    O.scan_forward_v4(I, 0.9, 1.0, 0.0, u0, C=C, G=G, K=16, K2=32, keep=keep)
+    Us, _ = O.serial_forward(I, 0.9, 1.0, 0.0, u0)
+    exact = np.concatenate([u0[None], Us[C * G - 1:-1:C * G]], 0)
+    frac = (keep["sstarts"] == exact).mean()
+    assert frac > 0.99

@@ -1,0 +1,952 @@
+// Adaptive-threshold LIF (ALIF) kernels for MI355X (gfx950).  Reference: lifscan/triton_alif.py.
+//
+//   v = fl(fl(beta*u) + x);  s = v >= fl(theta0 + w);  u' = s ? u_r : v;
+//   w' = s ? fl(fl(rho*w) + q) : fl(rho*w)                          (triton_alif.py:26-31)
+//
+// Forward: serial / replay (k_alif_fwd), warm-up predictor (k_alif_warm), and the exact
+// box scan: chunk maps over an entry box [lu, hu) x [lw, hw] (k_alif_build), verified carry
+// with serial fallback (k_alif_carry), replay, Jacobi repair on device (k_alif_repair).
+// Backward: the adjoint as two affine recurrences (triton_alif.py:361-365)
+//   lw_{t-1} = (rho - q*sg_t)*lw_t - sg_t*g_t        LW[t] = lw_t = dL/dw_t
+//   lv_t     = (1 - s_t)*beta*lv_{t+1} + sg_t*(g_t + q*lw_t)   LV[t] = dL/dv_t = dL/dI_t
+// solved serially, as chunked two-level scans, or in one fused pass.
+//
+// Map layout (workspace): per-chunk scalars [M, N]; line and piece slots [M, N, K]
+// (slot-contiguous, so the 32 lanes of one neuron store 128 contiguous bytes).
+#include "lsh_abi.h"
+#include "lsh_common.h"
+
+namespace lsh {
+
+__device__ __forceinline__ float alif_step(float u, float& w, float x, float beta, float rho,
+                                           float q, float theta0, float u_r, bool& s) {
+  const float v = lif_v(u, x, beta);
+  s = v >= theta0 + w;
+  const float rw = rho * w;
+  w = s ? rw + q : rw;
+  return s ? u_r : v;
+}
+
+// numpy-style min/max (a NaN operand gives NaN), as the oracle evaluates them
+__device__ __forceinline__ float nmin(float a, float b) {
+  return (a != a) ? a : ((b != b) ? b : (a < b ? a : b));
+}
+__device__ __forceinline__ float nmax(float a, float b) {
+  return (a != a) ? a : ((b != b) ? b : (a > b ? a : b));
+}
+
+// ---------------------------------------------------------------------------------------
+// Serial / replay forward over segments of Ls steps from (su, sw) (triton_alif.py:46-71).
+template <int D>
+__global__ __launch_bounds__(64) void k_alif_fwd(const float* __restrict__ I,
+                                                 const float* __restrict__ su,
+                                                 const float* __restrict__ sw, float* __restrict__ U,
+                                                 float* __restrict__ W, float* __restrict__ S,
+                                                 float* __restrict__ eu, float* __restrict__ ew,
+                                                 int64_t N, int64_t Ls, int NB, float beta, float rho,
+                                                 float q, float theta0, float u_r) {
+  const int64_t m = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - m * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  if (n >= N) return;
+  float u = su[m * N + n], w = sw[m * N + n];
+  const size_t base = (size_t)m * (size_t)Ls * (size_t)N + (size_t)n;
+  const float* __restrict__ Ip = I + base;
+  const int64_t nt = Ls / D;
+  float xa[D];
+  if (nt > 0) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) xa[j] = Ip[(size_t)j * N];
+  }
+  for (int64_t b = 0; b < nt; ++b) {
+    float xb[D];
+    const bool more = b + 1 < nt;
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) xb[j] = Ip[(size_t)((b + 1) * D + j) * N];
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      bool s;
+      u = alif_step(u, w, xa[j], beta, rho, q, theta0, u_r, s);
+      const size_t o = base + (size_t)(b * D + j) * N;
+      st_nt(U + o, u);
+      st_nt(W + o, w);
+      st_nt(S + o, s ? 1.0f : 0.0f);
+    }
+    if (more) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) xa[j] = xb[j];
+    }
+  }
+  for (int64_t t = nt * D; t < Ls; ++t) {
+    bool s;
+    u = alif_step(u, w, Ip[(size_t)t * N], beta, rho, q, theta0, u_r, s);
+    const size_t o = base + (size_t)t * N;
+    st_nt(U + o, u);
+    st_nt(W + o, w);
+    st_nt(S + o, s ? 1.0f : 0.0f);
+  }
+  if (eu) {
+    eu[m * N + n] = u;
+    ew[m * N + n] = w;
+  }
+}
+
+// Warm-up predictor (triton_alif.py:75-92): chunk m simulates chunks max(m-Wn,0)..m-1.
+__global__ __launch_bounds__(64) void k_alif_warm(const float* __restrict__ I,
+                                                  const float* __restrict__ u0,
+                                                  const float* __restrict__ w0,
+                                                  const float* __restrict__ UI,
+                                                  const float* __restrict__ WI, float* __restrict__ WP,
+                                                  int64_t N, int NB, int C, int Wn, float u_init,
+                                                  float w_init, float beta, float rho, float q,
+                                                  float theta0, float u_r) {
+  const int64_t m = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - m * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  if (n >= N) return;
+  const int64_t s0 = m - Wn > 0 ? m - Wn : 0;
+  float u, w;
+  if (s0 == 0) {
+    u = u0[n];
+    w = w0[n];
+  } else if (UI) {
+    u = UI[s0 * N + n];
+    w = WI[s0 * N + n];
+  } else {
+    u = u_init;
+    w = w_init;
+  }
+  for (int64_t t = s0 * C; t < m * C; ++t) {
+    bool s;
+    u = alif_step(u, w, I[(size_t)t * N + n], beta, rho, q, theta0, u_r, s);
+  }
+  WP[m * N + n] = w;
+}
+
+// Chunk envelope maps (triton_lif.py:699-719) and the sequential carry to per-chunk lower
+// bounds (:723-733): the hard-reset envelope also bounds ALIF potentials from below.
+__global__ __launch_bounds__(64) void k_env_chunks(const float* __restrict__ I,
+                                                   float* __restrict__ EC, float* __restrict__ EA,
+                                                   float* __restrict__ EB, int64_t N, int NB, int C,
+                                                   float beta, float u_r) {
+  const int64_t m = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - m * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  if (n >= N) return;
+  float c = INFINITY, a = 1.0f, b = 0.0f;
+  const float* __restrict__ Ip = I + (size_t)m * C * N + n;
+  for (int j = 0; j < C; ++j) {
+    const float x = Ip[(size_t)j * N];
+    c = fminf(u_r, lif_v(c, x, beta));
+    a = beta * a;
+    b = lif_v(b, x, beta);
+  }
+  EC[m * N + n] = c;
+  EA[m * N + n] = a;
+  EB[m * N + n] = b;
+}
+
+__global__ __launch_bounds__(64) void k_env_carry(const float* __restrict__ u0,
+                                                  const float* __restrict__ EC,
+                                                  const float* __restrict__ EA,
+                                                  const float* __restrict__ EB,
+                                                  float* __restrict__ LO, int64_t N, int M) {
+  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
+  if (n >= N) return;
+  const float margin = 1e-5f;
+  float l = u0[n];
+  for (int m = 0; m < M; ++m) {
+    const size_t o = (size_t)m * N + n;
+    LO[o] = l - margin * (fabsf(l) + 1.0f);
+    l = fminf(EC[o], __fadd_rn(__fmul_rn(EA[o], l), EB[o]));
+  }
+}
+
+// Entry box of every chunk (triton_alif.py:315-318), from the prediction Wp (Wp[0] = w0):
+// lw = max(Wp - dw, 0), hw = Wp + dw, hu = max(theta0 + hw/rho, u_r) + 1e-5(|.| + 1).
+__global__ __launch_bounds__(64) void k_alif_box(const float* __restrict__ Wpred,
+                                                 const float* __restrict__ w0,
+                                                 float* __restrict__ LW, float* __restrict__ HW,
+                                                 float* __restrict__ HU, int64_t N, int NB,
+                                                 float dw, float rho, float theta0, float u_r) {
+  const int64_t m = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - m * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  if (n >= N) return;
+  const size_t o = (size_t)m * N + n;
+  const float wp = m == 0 ? w0[n] : Wpred[o];
+  LW[o] = nmax(wp - dw, 0.0f);
+  const float hw = wp + dw;
+  HW[o] = hw;
+  float hu = nmax(theta0 + hw / rho, u_r);
+  HU[o] = hu + 1e-5f * (fabsf(hu) + 1.0f);
+}
+
+// ---------------------------------------------------------------------------------------
+// Box-scan chunk map (triton_alif.py:96-186).  32 lanes per neuron (two neurons per wave):
+// lane i holds first-spike line slot i (< K1) and post-spike piece slot i (< K2).  Per step:
+//  1. every piece is advanced; pieces cut by the threshold are split and the list compacted
+//     (exclusive prefix sum of the output counts, binary search of every output slot's
+//     source, gathers: all as shuffles within the neuron's 32 lanes).  The split runs for
+//     all neurons of a block of BLK neurons when any of them has a cut (the reference's
+//     Triton block); blocks wider than one wave agree through LDS.
+//  2. the step's first-spike line u0 >= sj*w0 + cj is added unless an existing line dominates
+//     it on [wlo, whi]; its post-spike piece x in [cx*wlo + q, cx*whi + q] (widened) is added.
+template <int BLK>
+__global__ __launch_bounds__(WAVE*(BLK > 2 ? BLK / 2 : 1)) void k_alif_build(
+    const float* __restrict__ I, const float* __restrict__ LU, const float* __restrict__ HU,
+    const float* __restrict__ LWb, const float* __restrict__ HWb, float* __restrict__ MA,
+    float* __restrict__ MB, int* __restrict__ NL, int* __restrict__ NP, int* __restrict__ OVF,
+    float* __restrict__ LS, float* __restrict__ LC, float* __restrict__ LX, int* __restrict__ POWN,
+    float* __restrict__ PXL, float* __restrict__ PXR, float* __restrict__ PU, float* __restrict__ PA,
+    float* __restrict__ POF, int64_t N, int NBLK, int C, int K1, int K2, int logk2, float beta,
+    float rho, float q, float theta0, float u_r) {
+  constexpr int WPB = BLK > 2 ? BLK / 2 : 1;  // waves per workgroup
+  __shared__ int s_cut[WPB];
+  const int64_t m = blockIdx.x / NBLK;
+  const int blk = (int)(blockIdx.x - m * NBLK);
+  const int wv = threadIdx.x / WAVE;
+  const int lane = threadIdx.x % WAVE;
+  const int half = lane >> 5;
+  const int i = lane & 31;  // slot
+  const int hb = half << 5;
+  const int64_t n = ((int64_t)blk * WPB + wv) * 2 + half;
+  const bool valid_n = n < N;
+  const int64_t nn = valid_n ? n : N - 1;
+  const size_t o = (size_t)m * N + nn;
+  const float lu = LU[o], hu = HU[o], hw = HWb[o];
+  float wlo = LWb[o];
+  float A = 1.0f, B = 0.0f, R = 1.0f;
+  float ls = 0.0f, lc = INFINITY, lx = 0.0f;
+  int nl = 0;
+  int pown = -1;
+  float pxl = INFINITY, pxr = INFINITY, pu = 0.0f, pa = 1.0f, pof = 0.0f;
+  int npc = 0;
+  int ovf = 0;
+  const unsigned long long hmask = 0xffffffffull << hb;
+  const float* __restrict__ Ip = I + (size_t)m * C * N + nn;
+  for (int j = 0; j < C; ++j) {
+    const float x = Ip[(size_t)j * N];
+    // 1. advance the post-spike pieces; a piece spikes for x <= (v - theta0 - pof)/pa
+    const bool valid = i < npc;
+    const float v = lif_v(pu, x, beta);
+    const float rr = (v - theta0) - pof;
+    const bool es = valid && rr > pa * pxl;
+    const bool en = valid && rr < pa * pxr;
+    const unsigned long long cb = __ballot(es && en);
+    bool cut;
+    if (BLK == 1) {
+      cut = (cb & hmask) != 0ull;
+    } else if (BLK == 2) {
+      cut = cb != 0ull;
+    } else {
+      if (lane == 0) s_cut[wv] = cb != 0ull ? 1 : 0;
+      __syncthreads();
+      int any = 0;
+#pragma unroll
+      for (int k = 0; k < WPB; ++k) any |= s_cut[k];
+      __syncthreads();
+      cut = any != 0;
+    }
+    if (cut) {
+      const float z = rr / pa;
+      const int nout = (es ? 1 : 0) + (en ? 1 : 0);
+      int incl = nout;  // inclusive prefix sum over the neuron's 32 slots
+#pragma unroll
+      for (int off = 1; off < 32; off <<= 1) {
+        const int y = __shfl_up(incl, off, 32);
+        if (i >= off) incl += y;
+      }
+      const int p = incl - nout;
+      const int ntot = __shfl(incl, 31, 32);
+      if (ntot > K2) ovf = 1;
+      int lo_i = 0, hi_i = K2 - 1;
+      for (int it = 0; it < logk2; ++it) {
+        const int mid = (lo_i + hi_i + 1) >> 1;
+        const bool le = __shfl(p, mid, 32) <= i;
+        lo_i = le ? mid : lo_i;
+        hi_i = le ? hi_i : mid - 1;
+      }
+      const int idx = lo_i;
+      const int d = i - __shfl(p, idx, 32);
+      const bool is_s = d == 0 && __shfl(es ? 1 : 0, idx, 32) != 0;
+      const float g_xl = __shfl(pxl, idx, 32), g_xr = __shfl(pxr, idx, 32);
+      const float g_z = __shfl(z, idx, 32), g_v = __shfl(v, idx, 32);
+      const float g_pa = __shfl(pa, idx, 32), g_po = __shfl(pof, idx, 32);
+      const int g_own = __shfl(pown, idx, 32);
+      const int n_new = min(ntot, K2);
+      const bool keep = i < n_new;
+      pxl = keep ? (is_s ? g_xl : nmax(g_xl, g_z)) : INFINITY;
+      pxr = keep ? (is_s ? nmin(g_xr, g_z) : g_xr) : INFINITY;
+      pu = keep ? (is_s ? u_r : g_v) : 0.0f;
+      pa = keep ? rho * g_pa : 1.0f;
+      pof = keep ? (is_s ? rho * g_po + q : rho * g_po) : 0.0f;
+      pown = keep ? g_own : -1;
+      npc = n_new;
+    } else if (valid) {
+      pu = es ? u_r : v;
+      pof = es ? rho * pof + q : rho * pof;
+      pa = rho * pa;
+    }
+    // 2. first-spike line of this step
+    A = beta * A;
+    B = lif_v(B, x, beta);
+    const float sj = R / A;
+    const float cj = (theta0 - B) / A;
+    const float whi = nmin(hw, (hu - cj) / sj);
+    const bool dl = i < nl && (ls * wlo + lc <= sj * wlo + cj) && (ls * whi + lc <= sj * whi + cj);
+    const bool dom = (__ballot(dl) & hmask) != 0ull;
+    const bool newc = (wlo < whi) && !dom && valid_n;
+    const float cx = R * rho;
+    if (newc && i == nl && nl < K1) {
+      ls = sj;
+      lc = cj;
+      lx = cx;
+    }
+    if (newc && nl >= K1) ovf = 1;
+    const float xlo = cx * wlo + q;
+    const float xhi = cx * whi + q;
+    const float pd = 4e-7f * (fabsf(xhi) + 1.0f);
+    if (newc && i == npc && npc < K2) {
+      pxl = xlo - pd;
+      pxr = xhi + pd;
+      pu = u_r;
+      pa = 1.0f;
+      pof = 0.0f;
+      pown = nl;
+    }
+    if (newc && npc >= K2) ovf = 1;
+    if (newc) {
+      nl = min(nl + 1, K1);
+      npc = min(npc + 1, K2);
+    }
+    wlo = nmax(wlo, (lu - cj) / sj);
+    R = rho * R;
+  }
+  if (!valid_n) return;
+  if (i == 0) {
+    MA[o] = A;
+    MB[o] = B;
+    NL[o] = nl;
+    NP[o] = npc;
+    OVF[o] = ovf;
+  }
+  if (i < K1) {
+    const size_t os = o * K1 + i;
+    LS[os] = ls;
+    LC[os] = lc;
+    LX[os] = lx;
+  }
+  if (i < K2) {
+    const size_t os = o * K2 + i;
+    POWN[os] = pown;
+    PXL[os] = pxl;
+    PXR[os] = pxr;
+    PU[os] = pu;
+    PA[os] = pa;
+    POF[os] = pof;
+  }
+}
+
+// Verified carry (triton_alif.py:214-252): the first line that fires gives the first spike
+// step and x = lx*w + q; the unique piece of that line containing x gives (u, w) at the
+// chunk end.  Out of box, overflow or not exactly one piece: the chunk runs serially.
+__global__ __launch_bounds__(64) void k_alif_carry(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
+    const float* __restrict__ LU, const float* __restrict__ HU, const float* __restrict__ LWb,
+    const float* __restrict__ HWb, const float* __restrict__ MA, const float* __restrict__ MB,
+    const int* __restrict__ NL, const int* __restrict__ NP, const int* __restrict__ OVF,
+    const float* __restrict__ LS, const float* __restrict__ LC, const float* __restrict__ LX,
+    const int* __restrict__ POWN, const float* __restrict__ PXL, const float* __restrict__ PXR,
+    const float* __restrict__ PU, const float* __restrict__ PA, const float* __restrict__ POF,
+    float* __restrict__ SU, float* __restrict__ SW, int* __restrict__ MISS, WsHeader* hdr,
+    int64_t N, int M, int C, int K1, int K2, float beta, float rho, float q, float theta0,
+    float u_r, float rhoC) {
+  const int lane = threadIdx.x;
+  const int half = lane >> 5;
+  const int i = lane & 31;
+  const int hb = half << 5;
+  const int64_t n = (int64_t)blockIdx.x * 2 + half;
+  const bool valid_n = n < N;
+  const int64_t nn = valid_n ? n : N - 1;
+  const unsigned long long hmask = 0xffffffffull << hb;
+  float u = u0[nn], w = w0[nn];
+  unsigned long long miss_acc = 0, ovf_acc = 0, lines_acc = 0, pcs_acc = 0;
+  int pmax = 0;
+  for (int m = 0; m < M; ++m) {
+    const size_t o = (size_t)m * N + nn;
+    if (valid_n && i == 0) {
+      SU[o] = u;
+      SW[o] = w;
+    }
+    const int nl = NL[o], npc = NP[o], ovf = OVF[o];
+    const float ls = i < K1 ? LS[o * K1 + i] : 0.0f;
+    const float lc = i < K1 ? LC[o * K1 + i] : INFINITY;
+    const float lx = i < K1 ? LX[o * K1 + i] : 0.0f;
+    const bool fire = i < nl && u >= ls * w + lc;
+    const unsigned long long fm = (__ballot(fire) & hmask) >> hb;
+    const int first = fm ? __builtin_ctzll(fm) : K1;
+    const bool none_ = first == K1;
+    const float lxf = none_ ? 0.0f : __shfl(lx, first, 32);
+    const float xq = lxf * w + q;
+    const int pw = i < K2 ? POWN[o * K2 + i] : -1;
+    const float pl = i < K2 ? PXL[o * K2 + i] : INFINITY;
+    const float pr = i < K2 ? PXR[o * K2 + i] : INFINITY;
+    const bool hit = i < npc && pw == first && pl <= xq && xq < pr;
+    const unsigned long long hm = (__ballot(hit) & hmask) >> hb;
+    const int nh = __builtin_popcountll(hm);
+    const int hl = hm ? __builtin_ctzll(hm) : 0;
+    const float pu_i = i < K2 ? PU[o * K2 + i] : 0.0f;
+    const float pa_i = i < K2 ? PA[o * K2 + i] : 0.0f;
+    const float po_i = i < K2 ? POF[o * K2 + i] : 0.0f;
+    const float mu = nh ? __shfl(pu_i, hl, 32) : 0.0f;
+    const float mw = nh ? __shfl(pa_i * xq + po_i, hl, 32) : 0.0f;
+    float nu = none_ ? __fadd_rn(__fmul_rn(MA[o], u), MB[o]) : mu;
+    float nw = none_ ? rhoC * w : mw;
+    const bool inbox = (u >= LU[o]) && (u < HU[o]) && (w >= LWb[o]) && (w <= HWb[o]);
+    const bool bad = !inbox || ovf != 0 || (!none_ && nh != 1);
+    if (valid_n && i == 0) MISS[o] = bad ? 1 : 0;
+    if (bad) {
+      float uu = u, ww = w;
+      const float* __restrict__ Ip = I + (size_t)m * C * N + nn;
+      for (int j = 0; j < C; ++j) {
+        bool s;
+        uu = alif_step(uu, ww, Ip[(size_t)j * N], beta, rho, q, theta0, u_r, s);
+      }
+      nu = uu;
+      nw = ww;
+    }
+    u = nu;
+    w = nw;
+    if (valid_n && i == 0) {
+      miss_acc += bad ? 1ull : 0ull;
+      ovf_acc += ovf ? 1ull : 0ull;
+      lines_acc += (unsigned long long)nl;
+      pcs_acc += (unsigned long long)npc;
+      pmax = max(pmax, npc);
+    }
+  }
+  miss_acc = wave_sum_u64(miss_acc);
+  ovf_acc = wave_sum_u64(ovf_acc);
+  lines_acc = wave_sum_u64(lines_acc);
+  pcs_acc = wave_sum_u64(pcs_acc);
+  pmax = wave_max_i(pmax);
+  if (lane == 0) {
+    const unsigned long long old_lo =
+        atomicAdd(&hdr->miss_count_lo, (unsigned int)(miss_acc & 0xffffffffull));
+    const unsigned int carry = (old_lo + (miss_acc & 0xffffffffull)) > 0xffffffffull ? 1u : 0u;
+    atomicAdd(&hdr->miss_count_hi, (unsigned int)(miss_acc >> 32) + carry);
+    atomicAdd(&hdr->ovf_count, ovf_acc);
+    atomicAdd(&hdr->lines_sum, lines_acc);
+    atomicAdd(&hdr->alif_pieces_sum, pcs_acc);
+    atomicMax(&hdr->alif_pieces_max, (unsigned int)pmax);
+  }
+}
+
+// Jacobi repair of (u, w) chunk starts, as k_lif_repair (triton_alif.py:342-348).
+__global__ __launch_bounds__(256) void k_alif_repair(
+    const float* __restrict__ I, float* __restrict__ U, float* __restrict__ W,
+    float* __restrict__ S, float* __restrict__ su, float* __restrict__ sw, float* __restrict__ eu,
+    float* __restrict__ ew, int* __restrict__ list0, int* __restrict__ list1, WsHeader* hdr,
+    int64_t N, int M, int C, int64_t R, float beta, float rho, float q, float theta0, float u_r) {
+  __shared__ int s_nd, s_nc;
+  const int nb = blockIdx.x;
+  const int tid = threadIdx.x;
+  const size_t cap = (size_t)M * WAVE;
+  int* __restrict__ dl = list0 + (size_t)nb * cap;
+  int* __restrict__ cl = list1 + (size_t)nb * cap;
+  auto differs = [&](int m, int64_t n) {
+    const size_t a = (size_t)(m - 1) * N + n, b = (size_t)m * N + n;
+    return eu[a] != su[b] || ew[a] != sw[b];
+  };
+  if (tid == 0) s_nd = 0;
+  __syncthreads();
+  for (int e = tid + WAVE; e < M * WAVE; e += blockDim.x) {
+    const int m = e / WAVE;
+    const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
+    if (n < N && differs(m, n)) dl[atomicAdd(&s_nd, 1)] = e;
+  }
+  __syncthreads();
+  int64_t rounds = 0;
+  while (true) {
+    const int nd = s_nd;
+    if (nd == 0 || rounds >= R) break;
+    ++rounds;
+    for (int k = tid; k < nd; k += blockDim.x) {
+      const int e = dl[k];
+      const int m = e / WAVE;
+      const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
+      su[(size_t)m * N + n] = eu[(size_t)(m - 1) * N + n];
+      sw[(size_t)m * N + n] = ew[(size_t)(m - 1) * N + n];
+    }
+    __syncthreads();
+    if (tid == 0) s_nc = 0;
+    __syncthreads();
+    for (int k = tid; k < nd; k += blockDim.x) {
+      const int e = dl[k];
+      const int m = e / WAVE;
+      const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
+      float u = su[(size_t)m * N + n], w = sw[(size_t)m * N + n];
+      const size_t base = (size_t)m * C * N + n;
+      for (int j = 0; j < C; ++j) {
+        bool s;
+        u = alif_step(u, w, I[base + (size_t)j * N], beta, rho, q, theta0, u_r, s);
+        U[base + (size_t)j * N] = u;
+        W[base + (size_t)j * N] = w;
+        S[base + (size_t)j * N] = s ? 1.0f : 0.0f;
+      }
+      const size_t oe = (size_t)m * N + n;
+      if (u != eu[oe] || w != ew[oe]) {
+        eu[oe] = u;
+        ew[oe] = w;
+        if (m + 1 < M) cl[atomicAdd(&s_nc, 1)] = e + WAVE;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) s_nd = 0;
+    __syncthreads();
+    const int nc = s_nc;
+    for (int k = tid; k < nc; k += blockDim.x) {
+      const int e = cl[k];
+      const int m = e / WAVE;
+      const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
+      if (differs(m, n)) dl[atomicAdd(&s_nd, 1)] = e;
+    }
+    __syncthreads();
+  }
+  if (tid == 0) atomicMax(&hdr->repair_iters, (unsigned int)rounds);
+}
+
+// ---------------------------------------------------------------------------------------
+// Backward.  Per step t: up = u_{t-1}, wp = w_{t-1} (u0, w0 at t = 0),
+// sg = alpha*sig*(1-sig), sig = 1/(1 + exp(-alpha*((beta*up + x - theta0) - wp)))
+// (triton_alif.py:367-370).
+__device__ __forceinline__ float alif_sg(float up, float wp, float x, float beta, float theta0,
+                                         float alpha) {
+  const float v = lif_v(up, x, beta);
+  const float sig = 1.0f / (1.0f + expf(-(alpha * ((v - theta0) - wp))));
+  return alpha * sig * (1.0f - sig);
+}
+
+// Reverse sweep over segments of Ls steps (triton_alif.py:374-440 PASS 0-4):
+//   PASS 0: compose the lw maps (P, Q)        PASS 1: lw replay from LamEnd, writes LW
+//   PASS 2: compose the lv maps (reads LW)    PASS 3: lv replay from LamEnd, writes LV
+//   PASS 4: fused serial sweep of both (one segment), writes LW and LV
+template <int PASS>
+__global__ __launch_bounds__(64) void k_alif_bwd(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
+    const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
+    const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
+    float* __restrict__ PA_, float* __restrict__ PB_, const float* __restrict__ lam_end,
+    int64_t N, int64_t Ls, int NB, float beta, float rho, float q, float theta0, float alpha) {
+  const int64_t m = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - m * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  if (n >= N) return;
+  const float u0n = u0[n], w0n = w0[n];
+  float lam = (PASS == 1 || PASS == 3) ? lam_end[m * N + n] : 0.0f;
+  float P = 1.0f, Q = 0.0f, lw = 0.0f, lv = 0.0f;
+  const int64_t t0 = m * Ls;
+  for (int64_t t = t0 + Ls - 1; t >= t0; --t) {
+    const size_t o = (size_t)t * N + n;
+    const float up = t > 0 ? U[o - N] : u0n;
+    const float wp = t > 0 ? W[o - N] : w0n;
+    const float x = I[o], s = S[o], gs = GS[o];
+    const float sg = alif_sg(up, wp, x, beta, theta0, alpha);
+    if (PASS == 0) {
+      const float a = rho - q * sg;
+      P = a * P;
+      Q = a * Q - sg * gs;
+    } else if (PASS == 1) {
+      st_nt(LW + o, lam);
+      lam = (rho - q * sg) * lam - sg * gs;
+    } else if (PASS == 2) {
+      const float a = (1.0f - s) * beta;
+      P = a * P;
+      Q = a * Q + sg * (gs + q * LW[o]);
+    } else if (PASS == 3) {
+      lam = (1.0f - s) * beta * lam + sg * (gs + q * LW[o]);
+      st_nt(LV + o, lam);
+    } else {
+      const float d = gs + q * lw;
+      lv = (1.0f - s) * beta * lv + sg * d;
+      st_nt(LW + o, lw);
+      st_nt(LV + o, lv);
+      lw = rho * lw - sg * d;
+    }
+  }
+  if (PASS == 0 || PASS == 2) {
+    PA_[m * N + n] = P;
+    PB_[m * N + n] = Q;
+  }
+}
+
+// Single-pass two-scan adjoint: one workgroup of W waves owns 64 neurons and walks the time
+// axis backwards in rounds of W chunks.  Each wave keeps its chunk's (sg_t, g_t, s_t) in
+// registers, composes the lw recurrence into (P1, Q1), takes lw at its chunk end from the
+// later chunks through LDS, replays lw (kept in registers), composes the lv recurrence
+// (which reads lw_t) into (P2, Q2), takes lv at its chunk end the same way and replays lv.
+template <int C, int WV>
+__global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
+    const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
+    const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV, int64_t N, int M,
+    float beta, float rho, float q, float theta0, float alpha) {
+  __shared__ float sP[WV][WAVE], sQ[WV][WAVE];
+  __shared__ float sLw[WAVE], sLv[WAVE];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const unsigned lane = threadIdx.x % WAVE;
+  const int64_t nb0 = (int64_t)blockIdx.x * WAVE;
+  const bool valid = nb0 + lane < N;
+  const unsigned ln = valid ? lane : (unsigned)(N - 1 - nb0);
+  const unsigned lb = ln * 4u, sb = lane * 4u;
+  const unsigned rstride = (unsigned)(N * 4);
+  const float u0n = u0[nb0 + ln], w0n = w0[nb0 + ln];
+  if (w == 0) {
+    sLw[lane] = 0.0f;
+    sLv[lane] = 0.0f;
+  }
+  __syncthreads();
+  const int rounds = (M + WV - 1) / WV;
+  for (int r = 0; r < rounds; ++r) {
+    const int m = M - 1 - (r * WV + w);
+    const bool active = m >= 0;
+    const size_t row0 = (size_t)(active ? m : 0) * C;
+    float sg[C], g[C], s1[C], lwv[C];
+    float lw_end = 0.0f, lv_end = 0.0f;
+    if (active) {
+      const Buf bi(I + nb0 + row0 * N), bs(S + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
+      const Buf bu(U + nb0 + row0 * N), bw(W + nb0 + row0 * N);
+      const float up0 = row0 > 0 ? ld_row(U + nb0 + (row0 - 1) * N, lb) : u0n;
+      const float wp0 = row0 > 0 ? ld_row(W + nb0 + (row0 - 1) * N, lb) : w0n;
+#pragma unroll
+      for (int j = 0; j < C; ++j) {
+        const unsigned so = j * rstride;
+        const float up = j == 0 ? up0 : bu.ld(lb, so - rstride);
+        const float wp = j == 0 ? wp0 : bw.ld(lb, so - rstride);
+        sg[j] = alif_sg(up, wp, bi.ld(lb, so), beta, theta0, alpha);
+        g[j] = bg.ld(lb, so);
+        s1[j] = 1.0f - bs.ld(lb, so);
+      }
+      float P = 1.0f, Q = 0.0f;
+#pragma unroll
+      for (int j = C - 1; j >= 0; --j) {
+        const float a = rho - q * sg[j];
+        P = a * P;
+        Q = a * Q - sg[j] * g[j];
+      }
+      sP[w][lane] = P;
+      sQ[w][lane] = Q;
+    }
+    __syncthreads();
+    if (active) {
+      float lam = sLw[lane];
+      for (int v = 0; v < w; ++v) lam = sQ[v][lane] + sP[v][lane] * lam;
+#pragma unroll
+      for (int j = C - 1; j >= 0; --j) {
+        lwv[j] = lam;
+        lam = (rho - q * sg[j]) * lam - sg[j] * g[j];
+      }
+      lw_end = lam;
+    }
+    __syncthreads();
+    if (active) {
+      float P = 1.0f, Q = 0.0f;
+#pragma unroll
+      for (int j = C - 1; j >= 0; --j) {
+        const float a = s1[j] * beta;
+        P = a * P;
+        Q = a * Q + sg[j] * (g[j] + q * lwv[j]);
+      }
+      sP[w][lane] = P;
+      sQ[w][lane] = Q;
+    }
+    __syncthreads();
+    if (active) {
+      float lam = sLv[lane];
+      for (int v = 0; v < w; ++v) lam = sQ[v][lane] + sP[v][lane] * lam;
+      const Buf bo(LW + nb0 + row0 * N), bv(LV + nb0 + row0 * N);
+#pragma unroll
+      for (int j = C - 1; j >= 0; --j) {
+        lam = s1[j] * beta * lam + sg[j] * (g[j] + q * lwv[j]);
+        if (valid) {
+          bo.st_nt(sb, j * rstride, lwv[j]);
+          bv.st_nt(sb, j * rstride, lam);
+        }
+      }
+      lv_end = lam;
+    }
+    __syncthreads();
+    const int last = min(WV, M - r * WV) - 1;
+    if (w == last) {
+      sLw[lane] = lw_end;
+      sLv[lane] = lv_end;
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(64) void k_rev_carry(const float* __restrict__ PA_,
+                                                  const float* __restrict__ PB_,
+                                                  float* __restrict__ lam_end, int64_t N, int M) {
+  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
+  if (n >= N) return;
+  float lam = 0.0f;
+  for (int m = M - 1; m >= 0; --m) {
+    const size_t o = (size_t)m * N + n;
+    lam_end[o] = lam;
+    lam = PB_[o] + PA_[o] * lam;
+  }
+}
+
+static void alif_scan_layout(int64_t T, int64_t N, int C, int K1, int K2, lsh_alif_layout* L) {
+  const int64_t M = T / C;
+  const size_t mn = (size_t)M * (size_t)N * 4;
+  const size_t nb = (size_t)((N + WAVE - 1) / WAVE);
+  Carver c;
+  L->EC = c.take(mn);
+  L->EA = c.take(mn);
+  L->EB = c.take(mn);
+  L->LU = c.take(mn);
+  L->HU = c.take(mn);
+  L->LW = c.take(mn);
+  L->HW = c.take(mn);
+  L->MA = c.take(mn);
+  L->MB = c.take(mn);
+  L->NL = c.take(mn);
+  L->NP = c.take(mn);
+  L->OVF = c.take(mn);
+  L->LS = c.take(mn * (size_t)K1);
+  L->LC = c.take(mn * (size_t)K1);
+  L->LX = c.take(mn * (size_t)K1);
+  L->POWN = c.take(mn * (size_t)K2);
+  L->PXL = c.take(mn * (size_t)K2);
+  L->PXR = c.take(mn * (size_t)K2);
+  L->PU = c.take(mn * (size_t)K2);
+  L->PA = c.take(mn * (size_t)K2);
+  L->POF = c.take(mn * (size_t)K2);
+  L->SU = c.take(mn);
+  L->SW = c.take(mn);
+  L->EU = c.take(mn);
+  L->EW = c.take(mn);
+  L->MISS = c.take(mn);
+  L->LIST0 = c.take(nb * (size_t)M * WAVE * 4);
+  L->LIST1 = c.take(nb * (size_t)M * WAVE * 4);
+  L->total = c.off;
+}
+
+static int alif_scan_check(int64_t T, int64_t N, int C, int K1, int K2, int block) {
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C < 1 || K1 < 1 || K1 > 32 || K2 < 1 || K2 > 32 || (K2 & (K2 - 1)) != 0) return LSH_ERR_SHAPE;
+  if (block != 1 && block != 2 && block != 4 && block != 8 && block != 16) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  if ((T / C) * ((N + WAVE - 1) / WAVE) > ((int64_t)1 << 31) - 1) return LSH_ERR_SHAPE;
+  return LSH_OK;
+}
+
+template <int BLK>
+static void launch_alif_build(const float* I, char* w, const lsh_alif_layout& L, int64_t N, int M,
+                              int C, int K1, int K2, float beta, float rho, float q, float theta0,
+                              float u_r, hipStream_t st) {
+  constexpr int WPB = BLK > 2 ? BLK / 2 : 1;
+  const int64_t per = (int64_t)WPB * 2;  // neurons per workgroup
+  const int NBLK = (int)((N + per - 1) / per);
+  int logk2 = 0;
+  while ((1 << logk2) < K2) ++logk2;
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
+  auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  hipLaunchKernelGGL((k_alif_build<BLK>), dim3((unsigned)((int64_t)M * NBLK)), dim3(WAVE * WPB), 0, st,
+                     I, F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
+                     Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),
+                     F(L.PA), F(L.POF), N, NBLK, C, K1, K2, logk2, beta, rho, q, theta0, u_r);
+}
+
+template <int D>
+static void launch_alif_fwd(const float* I, const float* su, const float* sw, float* U, float* W,
+                            float* S, float* eu, float* ew, int64_t N, int64_t Ls, int64_t M,
+                            float beta, float rho, float q, float theta0, float u_r, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  hipLaunchKernelGGL(k_alif_fwd<D>, dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, su, sw, U, W, S,
+                     eu, ew, N, Ls, NB, beta, rho, q, theta0, u_r);
+}
+
+}  // namespace lsh
+
+using namespace lsh;
+
+extern "C" int lsh_alif_serial_fwd(const float* I, const float* u0, const float* w0, float* U,
+                                   float* W, float* S, int64_t T, int64_t N, float beta, float rho,
+                                   float q, float theta0, float u_r, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(w0) || bad_ptr(U) || bad_ptr(W) || bad_ptr(S))
+    return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  launch_alif_fwd<16>(I, u0, w0, U, W, S, nullptr, nullptr, N, T, 1, beta, rho, q, theta0, u_r,
+                      (hipStream_t)stream);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" int lsh_alif_warm_predict(const float* I, const float* u0, const float* w0,
+                                     const float* UI, const float* WI, float* WP, int64_t T,
+                                     int64_t N, int C, int Wn, float u_init, float w_init,
+                                     float beta, float rho, float q, float theta0, float u_r,
+                                     void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(w0) || bad_ptr(WP)) return LSH_ERR_ARG;
+  if ((UI == nullptr) != (WI == nullptr)) return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || C < 1 || Wn < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  const int64_t M = T / C;
+  if (M == 0 || N == 0) return LSH_OK;
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  hipLaunchKernelGGL(k_alif_warm, dim3((unsigned)(M * NB)), dim3(WAVE), 0, (hipStream_t)stream, I, u0,
+                     w0, UI, WI, WP, N, NB, C, Wn, u_init, w_init, beta, rho, q, theta0, u_r);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" int lsh_alif_scan_layout(int64_t T, int64_t N, int C, int K1, int K2,
+                                    lsh_alif_layout* out) {
+  if (bad_ptr(out)) return LSH_ERR_ARG;
+  const int rc = alif_scan_check(T, N, C, K1, K2, 1);
+  if (rc != LSH_OK) return rc;
+  alif_scan_layout(T, N, C, K1, K2, out);
+  return LSH_OK;
+}
+
+extern "C" size_t lsh_alif_scan_workspace(int64_t T, int64_t N, int C, int K1, int K2) {
+  if (alif_scan_check(T, N, C, K1, K2, 1) != LSH_OK) return 0;
+  lsh_alif_layout L;
+  alif_scan_layout(T, N, C, K1, K2, &L);
+  return L.total;
+}
+
+extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w0,
+                                 const float* Wpred, float dw, float* U, float* W, float* S,
+                                 int64_t T, int64_t N, float beta, float rho, float q, float theta0,
+                                 float u_r, float rhoC, int C, int K1, int K2, int block,
+                                 int64_t repair, void* ws, size_t ws_bytes,
+                                 void* const* phase_events, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(w0) || bad_ptr(Wpred) || bad_ptr(U) || bad_ptr(W) ||
+      bad_ptr(S) || bad_ptr(ws))
+    return LSH_ERR_ARG;
+  if (repair < 0) return LSH_ERR_ARG;
+  const int rc = alif_scan_check(T, N, C, K1, K2, block);
+  if (rc != LSH_OK) return rc;
+  lsh_alif_layout L;
+  alif_scan_layout(T, N, C, K1, K2, &L);
+  if (ws_bytes < L.total || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0) return LSH_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  char* w = static_cast<char*>(ws);
+  WsHeader* h = reinterpret_cast<WsHeader*>(w);
+  hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, h);
+  if (T == 0 || N == 0) {
+    LSH_CHECK_LAUNCH();
+    return LSH_OK;
+  }
+  const int M = (int)(T / C);
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
+  auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  auto mark = [&](int k) {
+    if (phase_events && phase_events[k]) (void)hipEventRecord((hipEvent_t)phase_events[k], st);
+  };
+  mark(0);
+  hipLaunchKernelGGL(k_env_chunks, dim3((unsigned)((int64_t)M * NB)), dim3(WAVE), 0, st, I, F(L.EC),
+                     F(L.EA), F(L.EB), N, NB, C, beta, u_r);
+  hipLaunchKernelGGL(k_env_carry, dim3((unsigned)NB), dim3(WAVE), 0, st, u0, F(L.EC), F(L.EA),
+                     F(L.EB), F(L.LU), N, M);
+  hipLaunchKernelGGL(k_alif_box, dim3((unsigned)((int64_t)M * NB)), dim3(WAVE), 0, st, Wpred, w0,
+                     F(L.LW), F(L.HW), F(L.HU), N, NB, dw, rho, theta0, u_r);
+  mark(1);
+  switch (block) {
+    case 1: launch_alif_build<1>(I, w, L, N, M, C, K1, K2, beta, rho, q, theta0, u_r, st); break;
+    case 2: launch_alif_build<2>(I, w, L, N, M, C, K1, K2, beta, rho, q, theta0, u_r, st); break;
+    case 4: launch_alif_build<4>(I, w, L, N, M, C, K1, K2, beta, rho, q, theta0, u_r, st); break;
+    case 8: launch_alif_build<8>(I, w, L, N, M, C, K1, K2, beta, rho, q, theta0, u_r, st); break;
+    default: launch_alif_build<16>(I, w, L, N, M, C, K1, K2, beta, rho, q, theta0, u_r, st); break;
+  }
+  mark(2);
+  hipLaunchKernelGGL(k_alif_carry, dim3((unsigned)((N + 1) / 2)), dim3(WAVE), 0, st, I, u0, w0,
+                     F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
+                     Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),
+                     F(L.PA), F(L.POF), F(L.SU), F(L.SW), Iq(L.MISS), h, N, M, C, K1, K2, beta, rho,
+                     q, theta0, u_r, rhoC);
+  mark(3);
+  launch_alif_fwd<16>(I, F(L.SU), F(L.SW), U, W, S, F(L.EU), F(L.EW), N, C, M, beta, rho, q, theta0,
+                      u_r, st);
+  mark(4);
+  if (repair > 0 && M > 1) {
+    const int64_t rounds = repair < (int64_t)M ? repair : (int64_t)M;
+    hipLaunchKernelGGL(k_alif_repair, dim3((unsigned)NB), dim3(256), 0, st, I, U, W, S, F(L.SU),
+                       F(L.SW), F(L.EU), F(L.EW), Iq(L.LIST0), Iq(L.LIST1), h, N, M, C, rounds, beta,
+                       rho, q, theta0, u_r);
+  }
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" size_t lsh_alif_bwd_workspace(int64_t T, int64_t N, int C) {
+  if (T < 0 || N < 0 || C < 1 || T % C != 0) return 0;
+  const size_t mn = (size_t)(T / C) * (size_t)N * 4;
+  return kWsHeaderBytes + 3 * align_up(mn, 256);
+}
+
+extern "C" int lsh_alif_bwd(const float* I, const float* U, const float* W, const float* S,
+                            const float* GS, const float* u0, const float* w0, float* LV,
+                            float* LW, int64_t T, int64_t N, float beta, float rho, float q,
+                            float theta0, float alpha, int mode, int C, void* ws, size_t ws_bytes,
+                            void* stream) {
+  if (bad_ptr(I) || bad_ptr(U) || bad_ptr(W) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(u0) ||
+      bad_ptr(w0) || bad_ptr(LV) || bad_ptr(LW))
+    return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (mode < 0 || mode > 2) return LSH_ERR_ARG;
+  if (T == 0 || N == 0) return LSH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  if (mode == 0) {  // fused serial sweep (triton_alif.py:444-487)
+    hipLaunchKernelGGL(k_alif_bwd<4>, dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, w0, U, W, S, GS,
+                       LW, LV, nullptr, nullptr, nullptr, N, T, NB, beta, rho, q, theta0, alpha);
+    LSH_CHECK_LAUNCH();
+    return LSH_OK;
+  }
+  if (C < 1) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  const int M = (int)(T / C);
+  if (mode == 2) {  // single pass
+    if (C != 16 && C != 32) return LSH_ERR_SHAPE;
+    if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+    if (C == 16)
+      hipLaunchKernelGGL((k_alif_bwd_fused<16, 4>), dim3((unsigned)NB), dim3(WAVE * 4), 0, st, I, u0, w0,
+                         U, W, S, GS, LW, LV, N, M, beta, rho, q, theta0, alpha);
+    else
+      hipLaunchKernelGGL((k_alif_bwd_fused<32, 4>), dim3((unsigned)NB), dim3(WAVE * 4), 0, st, I, u0, w0,
+                         U, W, S, GS, LW, LV, N, M, beta, rho, q, theta0, alpha);
+    LSH_CHECK_LAUNCH();
+    return LSH_OK;
+  }
+  // chunked two-level scans (triton_alif.py:510-521)
+  if (bad_ptr(ws) || ws_bytes < lsh_alif_bwd_workspace(T, N, C) ||
+      (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+    return LSH_ERR_WORKSPACE;
+  const size_t mn = align_up((size_t)M * (size_t)N * 4, 256);
+  char* w = static_cast<char*>(ws) + kWsHeaderBytes;
+  float* PA_ = reinterpret_cast<float*>(w);
+  float* PB_ = reinterpret_cast<float*>(w + mn);
+  float* LE = reinterpret_cast<float*>(w + 2 * mn);
+  const dim3 g((unsigned)((int64_t)M * NB)), b(WAVE), gc((unsigned)NB);
+  hipLaunchKernelGGL(k_alif_bwd<0>, g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, nullptr, N,
+                     C, NB, beta, rho, q, theta0, alpha);
+  hipLaunchKernelGGL(k_rev_carry, gc, b, 0, st, PA_, PB_, LE, N, M);
+  hipLaunchKernelGGL(k_alif_bwd<1>, g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, LE, N, C,
+                     NB, beta, rho, q, theta0, alpha);
+  hipLaunchKernelGGL(k_alif_bwd<2>, g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, nullptr, N,
+                     C, NB, beta, rho, q, theta0, alpha);
+  hipLaunchKernelGGL(k_rev_carry, gc, b, 0, st, PA_, PB_, LE, N, M);
+  hipLaunchKernelGGL(k_alif_bwd<3>, g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, LE, N, C,
+                     NB, beta, rho, q, theta0, alpha);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}

@@ -55,6 +55,13 @@ class V4Layout(ctypes.Structure):
         "SA", "SB", "SN", "SOVF", "SX", "SC", "SSTARTS", "total")]
 
 
+class ALIFLayout(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in (
+        "EC", "EA", "EB", "LU", "HU", "LW", "HW", "MA", "MB", "NL", "NP", "OVF", "LS", "LC", "LX",
+        "POWN", "PXL", "PXR", "PU", "PA", "POF", "SU", "SW", "EU", "EW", "MISS", "LIST0", "LIST1",
+        "total")]
+
+
 # name -> (restype, argtypes); mirrors include/lifscan_hip.h
 SIGNATURES = {
     "lsh_abi_version": (c_i, []),
@@ -81,6 +88,18 @@ SIGNATURES = {
     "lsh_lif_scan_v4_layout": (c_i, [c_i64, c_i64, c_i, c_i, c_i, c_i, ctypes.POINTER(V4Layout)]),
     "lsh_lif_scan_v4_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i, c_i, c_i,
                                   c_i64, c_p, c_sz, c_p]),
+    "lsh_alif_serial_fwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f, c_f,
+                                  c_p]),
+    "lsh_alif_warm_predict": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_i, c_i, c_f, c_f,
+                                    c_f, c_f, c_f, c_f, c_f, c_p]),
+    "lsh_alif_scan_workspace": (c_sz, [c_i64, c_i64, c_i, c_i, c_i]),
+    "lsh_alif_scan_layout": (c_i, [c_i64, c_i64, c_i, c_i, c_i, ctypes.POINTER(ALIFLayout)]),
+    "lsh_alif_scan_fwd": (c_i, [c_p, c_p, c_p, c_p, c_f, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,
+                                c_f, c_f, c_f, c_i, c_i, c_i, c_i, c_i64, c_p, c_sz,
+                                ctypes.POINTER(c_p), c_p]),
+    "lsh_alif_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
+    "lsh_alif_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,
+                           c_f, c_f, c_i, c_i, c_p, c_sz, c_p]),
     "lsh_lif_scan_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
     "lsh_lif_scan_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f,
                                c_i, c_i, c_p, c_sz, c_p]),

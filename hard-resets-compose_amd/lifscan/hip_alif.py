@@ -1,0 +1,243 @@
+"""Adaptive-threshold LIF (ALIF) on MI355X with the call signatures of the reference's
+``lifscan/triton_alif.py``:
+
+    v = beta*u + I_t;  s = [v >= theta0 + w];  u <- u_r if s else v;  w <- rho*w + q*s
+
+Serial kernels, the warm-up predictor of chunk-entry adaptation, the exact box scan
+(first-spike lines + post-spike pieces, verified carry, serial fallback, replay and repair) and
+the adjoint as two affine recurrences, all in hand-written HIP kernels of liblifscan_hip.so.
+Triton tile keywords (BN for the serial kernels, nw, BNc, BNr, D) are accepted and ignored,
+except that alif_scan_forward's BN is the number of neurons that share the per-step piece
+split decision, as in the reference's Triton block.
+"""
+import math
+
+import torch
+
+from . import _native as _n
+from .hip_lif import _f32, _input, _vec, _same
+
+# single-pass backward (one workgroup per 64 neurons) pays off only with many neuron blocks
+ALIF_FUSED_BWD_MIN_N = 8192
+ALIF_FUSED_BWD_C = 16
+
+
+def alif_fwd_cfg(N):
+    """(BN, D, num_warps) table of the reference (triton_alif.py:255-260); kept for callers."""
+    if N <= 8: return 16, 16, 1
+    if N <= 64: return 16, 4, 1
+    if N <= 4096: return 32, 32, 1
+    return 128, 8, 1
+
+
+def alif_serial_forward(I, beta, rho, q, theta0, u_r, u0, w0, BN=32, D=0, num_warps=1):
+    """Serial ALIF (triton_alif.py:263-273) -> (U, W, S); plain and tiled are one kernel."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    w0 = _vec(w0, N, I, "w0")
+    U, W, S = torch.empty_like(I), torch.empty_like(I), torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        _n.check(_n.lib().lsh_alif_serial_fwd(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(U), _n.ptr(W), _n.ptr(S), T, N, _f32(beta),
+            _f32(rho), _f32(q), _f32(theta0), _f32(u_r), _n.stream_of(I)), "lsh_alif_serial_fwd")
+    return U, W, S
+
+
+def alif_warm_predict(I, beta, rho, q, theta0, u_r, u0, w0, C, Wn=4, u_init=0.0, w_init=0.0, BN=32,
+                      UI=None, WI=None):
+    """Predicted entry adaptation of every chunk (triton_alif.py:276-285) -> WP [T//C, N]."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    w0 = _vec(w0, N, I, "w0")
+    M = T // int(C)
+    if (UI is None) != (WI is None):
+        raise ValueError("UI and WI must be given together")
+    if UI is not None:
+        UI = UI.contiguous().float()
+        WI = WI.contiguous().float()
+        if UI.shape != (M, N) or WI.shape != (M, N):
+            raise ValueError(f"UI, WI must be [{M}, {N}]")
+    WP = torch.empty(M, N, device=I.device, dtype=torch.float32)
+    with torch.cuda.device(I.device):
+        _n.check(_n.lib().lsh_alif_warm_predict(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(UI), _n.ptr(WI), _n.ptr(WP), T, N, int(C),
+            int(Wn), float(u_init), float(w_init), _f32(beta), _f32(rho), _f32(q), _f32(theta0),
+            _f32(u_r), _n.stream_of(I)), "lsh_alif_warm_predict")
+    return WP
+
+
+class _ALIFRun:
+    """Workspace of one box-scan call (maps, box, chunk states) for stats and tests."""
+
+    def __init__(self, ws, T, N, C, K1, K2):
+        self.ws, self.T, self.N, self.C, self.K1, self.K2 = ws, T, N, C, K1, K2
+
+    def layout(self):
+        L = _n.ALIFLayout()
+        _n.check(_n.lib().lsh_alif_scan_layout(self.T, self.N, self.C, self.K1, self.K2,
+                                               _n.ctypes.byref(L)), "lsh_alif_scan_layout")
+        return L
+
+    def view(self, name, dtype=torch.float32):
+        """[M, N] arrays; LS/LC/LX as [M, K1, N] and piece arrays as [M, K2, N] (the reference's
+        layout; the workspace stores them slot-contiguous, [M, N, K])."""
+        L = self.layout()
+        M = self.T // self.C
+        off = getattr(L, name)
+        if name in ("LS", "LC", "LX"):
+            K = self.K1
+        elif name in ("POWN", "PXL", "PXR", "PU", "PA", "POF"):
+            K = self.K2
+        else:
+            return self.ws[off:off + 4 * M * self.N].view(dtype).view(M, self.N)
+        return self.ws[off:off + 4 * M * self.N * K].view(dtype).view(M, self.N, K).permute(0, 2, 1)
+
+
+_LAST_ALIF = None
+
+
+def last_alif_run():
+    return _LAST_ALIF
+
+
+def _rho_pow_c(rho, C):
+    """rho^C in fp32 exactly as the reference computes it (triton_alif.py:332)."""
+    return float(torch.tensor(_f32(rho), dtype=torch.float32) ** C)
+
+
+def alif_scan_forward(I, beta, rho, q, theta0, u_r, u0, w0, Wpred, dw, C=128, K1=16, K2=32, BN=16,
+                      nw=1, BNc=1, BNr=32, D=4, repair=0, stats=None, phases=None):
+    """Exact ALIF scan with a predicted adaptation box (triton_alif.py:301-358) -> (U, W, S).
+    Wpred: [T//C, N] predicted entry adaptation (row 0 is replaced by w0); dw: box half-width.
+    stats: repair_iters, miss_frac, overflow_frac, mean_lines, mean_pieces, max_pieces.
+    phases: per-phase GPU times in ms (envelope, build, carry, replay)."""
+    global _LAST_ALIF
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    w0 = _vec(w0, N, I, "w0")
+    C, K1, K2, BN = int(C), int(K1), int(K2), int(BN)
+    if T % C or C % int(D):
+        raise ValueError(f"T={T} must be divisible by C={C} and C by D={D}")
+    M = T // C
+    Wp = Wpred.detach().float().contiguous()
+    if Wp.shape != (M, N):
+        raise ValueError(f"Wpred must be [{M}, {N}]")
+    L = _n.lib()
+    nbytes = L.lsh_alif_scan_workspace(T, N, C, K1, K2)
+    if nbytes == 0:
+        raise ValueError("ALIF scan needs K1 <= 32 and K2 <= 32 a power of two")
+    ws = _n.workspace(nbytes, I.device)
+    U, W, S = torch.empty_like(I), torch.empty_like(I), torch.empty_like(I)
+    evs, ev_arr = None, None
+    if phases is not None:
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        for e in evs:
+            e.record()  # creates the underlying HIP event
+        ev_arr = (_n.c_p * 5)(*[e.cuda_event for e in evs])
+    with torch.cuda.device(I.device):
+        _n.check(L.lsh_alif_scan_fwd(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(Wp), _f32(dw), _n.ptr(U), _n.ptr(W), _n.ptr(S),
+            T, N, _f32(beta), _f32(rho), _f32(q), _f32(theta0), _f32(u_r), _rho_pow_c(rho, C), C, K1,
+            K2, BN, int(repair), _n.ptr(ws), nbytes, ev_arr, _n.stream_of(I)), "lsh_alif_scan_fwd")
+    _LAST_ALIF = _ALIFRun(ws, T, N, C, K1, K2)
+    if phases is not None:
+        torch.cuda.synchronize(I.device)
+        for k, name in enumerate(("envelope", "build", "carry", "replay")):
+            phases[name] = evs[k].elapsed_time(evs[k + 1])
+    if stats is not None:
+        st = _n.read_stats(ws, M * N, alif=True)
+        stats["repair_iters"] = int(st.repair_iters)
+        stats["miss_frac"] = float(st.miss_frac)
+        stats["overflow_frac"] = float(st.overflow_frac)
+        stats["mean_lines"] = float(st.mean_lines)
+        stats["mean_pieces"] = float(st.mean_pieces)
+        stats["max_pieces"] = int(st.max_pieces)
+    return U, W, S
+
+
+def alif_backward(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha=4.0, mode="scan", C=64,
+                  BN=32, D=4, nw=1):
+    """(LV, LW) with LV[t] = dL/dv_t (= dL/dI_t), LW[t] = dL/dw_t for dL/dS = GS
+    (triton_alif.py:490-521).  mode: serial_pf / serial_tuned / serial (fused serial sweep),
+    chunked (two-level affine scans over chunks of C), fused (single pass, C in {16, 32}) or
+    scan (fused when N is large, else chunked)."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    w0 = _vec(w0, N, I, "w0")
+    U, W, S, GS = (_same(a, I, nm) for a, nm in ((U, "U"), (W, "W"), (S, "S"), (GS, "GS")))
+    LV, LW = torch.empty_like(I), torch.empty_like(I)
+    ws, nbytes = None, 0
+    C = int(C)
+    if mode == "scan":
+        fused = N >= ALIF_FUSED_BWD_MIN_N and T % ALIF_FUSED_BWD_C == 0
+        mode = "fused" if fused else "chunked"
+        if fused:
+            C = ALIF_FUSED_BWD_C
+    if mode in ("serial_pf", "serial_tuned", "serial"):
+        code = 0
+    elif mode == "fused":  # single pass, C in {16, 32}
+        code = 2
+    elif mode == "chunked":
+        if T % C:
+            raise ValueError(f"T={T} must be divisible by C={C}")
+        code = 1
+        nbytes = _n.lib().lsh_alif_bwd_workspace(T, N, C)
+        ws = _n.workspace(nbytes, I.device)
+    else:
+        raise ValueError(f"unknown mode {mode!r}")
+    with torch.cuda.device(I.device):
+        _n.check(_n.lib().lsh_alif_bwd(
+            _n.ptr(I), _n.ptr(U), _n.ptr(W), _n.ptr(S), _n.ptr(GS), _n.ptr(u0), _n.ptr(w0), _n.ptr(LV),
+            _n.ptr(LW), T, N, _f32(beta), _f32(rho), _f32(q), _f32(theta0), _f32(alpha), code, C,
+            _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_alif_bwd")
+    return LV, LW
+
+
+class ALIFFn(torch.autograd.Function):
+    """S = ALIF(I; u0, w0, beta, rho, q, theta0) with u_r fixed (triton_alif.py:524-554).
+    Forward: serial, or the box scan with prediction Wpred (K1 = K2 = 32, block 4, no repair,
+    as the reference); backward: serial or scan.  Gradients for I, u0, w0, beta, rho, q, theta0."""
+
+    @staticmethod
+    def forward(ctx, I, u0, w0, beta, rho, q, theta0, u_r, alpha, fwd, bwd, Wpred, dw, C, Cb):
+        b, r, qq, th = _f32(beta), _f32(rho), _f32(q), _f32(theta0)
+        if fwd == "serial":
+            U, W, S = alif_serial_forward(I, b, r, qq, th, u_r, u0, w0)
+        else:
+            U, W, S = alif_scan_forward(I, b, r, qq, th, u_r, u0, w0, Wpred, dw, C=C, K1=32, K2=32,
+                                        BN=4, BNc=1, D=4)
+        ctx.save_for_backward(I, u0, w0, U, W, S)
+        ctx.c = (b, r, qq, th, u_r, alpha, bwd, Cb)
+        ctx.mark_non_differentiable(U, W)
+        return S, U, W
+
+    @staticmethod
+    def backward(ctx, gS, gU, gW):
+        I, u0, w0, U, W, S = ctx.saved_tensors
+        b, r, qq, th, u_r, alpha, bwd, Cb = ctx.c
+        GS = gS.contiguous()
+        LV, LW = alif_backward(I, U, W, S, GS, b, r, qq, th, u0, w0, alpha=alpha,
+                               mode="serial_tuned" if bwd == "serial" else bwd, C=Cb)
+        Up = torch.cat([u0[None], U[:-1]], 0)
+        Wp = torch.cat([w0[None], W[:-1]], 0)
+        V = b * Up + I
+        sig = torch.sigmoid(alpha * (V - th - Wp))
+        sg = alpha * sig * (1 - sig)
+        d = GS + qq * LW
+        lw_m1 = r * LW[0] - sg[0] * d[0]
+        return (LV, b * LV[0], lw_m1, (LV * Up).sum().reshape(()), (LW * Wp).sum().reshape(()),
+                (LW * S).sum().reshape(()), -(sg * d).sum().reshape(()), None, None, None, None,
+                None, None, None, None)
+
+
+def alif(I, u0, w0, beta, rho, q, theta0=1.0, u_r=0.0, alpha=4.0, fwd="serial", bwd="scan",
+         Wpred=None, dw=None, C=128, Cb=64):
+    """Differentiable ALIF layer -> (S, U, W) (triton_alif.py:557-560).  Parameters may be
+    0-d tensors (requires_grad) or floats."""
+    t = lambda v: v if torch.is_tensor(v) else torch.tensor(float(v), device=I.device)
+    return ALIFFn.apply(I, u0, w0, t(beta), t(rho), t(q), t(theta0), u_r, alpha, fwd, bwd, Wpred,
+                        dw, C, Cb)

@@ -165,6 +165,60 @@ int lsh_lif_scan_fused_bwd(const float* I, const float* u0, const float* U, cons
                            float beta, float theta, float u_r, float alpha, int detach, int C,
                            void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * ALIF: v = fl(fl(beta*u) + x); s = v >= fl(theta0 + w); u' = s ? u_r : v;
+ *       w' = s ? fl(fl(rho*w) + q) : fl(rho*w)          (triton_alif.py:26-31)
+ * U, W, S: [T, N] outputs. */
+
+/* Serial ALIF forward.  Replaces triton_alif.py:263-273 (alif_serial_forward, plain and tiled). */
+int lsh_alif_serial_fwd(const float* I, const float* u0, const float* w0, float* U, float* W,
+                        float* S, int64_t T, int64_t N, float beta, float rho, float q,
+                        float theta0, float u_r, void* stream);
+
+/* Predicted chunk-entry adaptation WP[T/C, N]: chunk m simulates chunks max(m-Wn, 0)..m-1 from
+ * (u_init, w_init), from (UI, WI)[max(m-Wn,0)] when both are given, or from (u0, w0) when the
+ * warm-up reaches t = 0.  Replaces triton_alif.py:75-92, :276-285 (alif_warm_predict). */
+int lsh_alif_warm_predict(const float* I, const float* u0, const float* w0, const float* UI,
+                          const float* WI, float* WP, int64_t T, int64_t N, int C, int Wn,
+                          float u_init, float w_init, float beta, float rho, float q,
+                          float theta0, float u_r, void* stream);
+
+/* Exact ALIF box scan: entry box [lu, hu) x [lw, hw] per chunk around the prediction Wpred
+ * [T/C, N] (Wpred[0] is replaced by w0) with half-width dw, chunk maps of K1 first-spike lines
+ * and K2 post-spike pieces, verified carry with serial fallback, replay, Jacobi repair on
+ * device.  `block` neurons share the per-step decision to split pieces (the reference's
+ * Triton BN; 1, 2, 4, 8 or 16).  rhoC = rho^C as fp32 (computed by the caller).  Replaces
+ * triton_alif.py:301-358 (alif_scan_forward), :96-186 (build), :214-252 (carry).
+ * K1 <= 32, K2 <= 32 and a power of two, T % C == 0. */
+typedef struct lsh_alif_layout {
+  size_t EC, EA, EB, LU, HU, LW, HW; /* envelope maps, box [M, N] */
+  size_t MA, MB, NL, NP, OVF;        /* per-chunk scalars [M, N] (NL, NP, OVF int32) */
+  size_t LS, LC, LX;                 /* first-spike lines [M, N, K1] */
+  size_t POWN, PXL, PXR, PU, PA, POF; /* post-spike pieces [M, N, K2] (POWN int32) */
+  size_t SU, SW, EU, EW, MISS;       /* chunk entry / exit states, carry misses [M, N] */
+  size_t LIST0, LIST1;               /* repair work lists */
+  size_t total;
+} lsh_alif_layout;
+size_t lsh_alif_scan_workspace(int64_t T, int64_t N, int C, int K1, int K2);
+int lsh_alif_scan_layout(int64_t T, int64_t N, int C, int K1, int K2, lsh_alif_layout* out);
+int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w0, const float* Wpred,
+                      float dw, float* U, float* W, float* S, int64_t T, int64_t N, float beta,
+                      float rho, float q, float theta0, float u_r, float rhoC, int C, int K1,
+                      int K2, int block, int64_t repair, void* ws, size_t ws_bytes,
+                      void* const* phase_events, void* stream);
+/* phase_events: NULL or 5 hipEvent_t recorded on `stream` at the start and after the
+ * envelope + box, the build, the carry and the first replay (the reference's `phases`). */
+
+/* ALIF adjoint: LW[t] = dL/dw_t, LV[t] = dL/dv_t (= dL/dI_t) for dL/dS = GS.
+ * mode 0: fused serial sweep (triton_alif.py:444-487); 1: chunked two-level affine scans of
+ * chunk C (triton_alif.py:510-521, needs lsh_alif_bwd_workspace(T, N, C) bytes); 2: single
+ * pass, internal chunk C in {16, 32} (no workspace).  Replaces triton_alif.py:490-521. */
+size_t lsh_alif_bwd_workspace(int64_t T, int64_t N, int C);
+int lsh_alif_bwd(const float* I, const float* U, const float* W, const float* S, const float* GS,
+                 const float* u0, const float* w0, float* LV, float* LW, int64_t T, int64_t N,
+                 float beta, float rho, float q, float theta0, float alpha, int mode, int C,
+                 void* ws, size_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

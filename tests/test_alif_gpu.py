@@ -1,0 +1,240 @@
+"""GPU parity of the HIP ALIF kernels against the CPU oracle (oracle/alif_oracle.py), through
+the C ABI.
+
+Bars: U, W, S bit-exact for serial, replay and the repaired box scan; every intermediate of the
+box scan (entry box, chunk maps, carried chunk states, miss flags) bit-exact at the same block
+size of the split decision; the adjoint within 1e-5 relative of the fp32 oracle and 1e-4 of the
+fp64 adjoint; parameter gradients within 1e-4 of the fp64 assembly.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import alif_oracle as A
+from tests._inputs import gpu, host, normal, uniform
+
+pytestmark = pytest.mark.gpu
+
+NEURONS = [("lsnn", 0.95, 0.995, 0.9), ("glif2", 0.99, 0.96, 0.2), ("appD-a", 0.9, 0.95, 0.5)]
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def _inputs(beta, mfree, T, N, seed):
+    g = torch.Generator().manual_seed(seed)
+    sig = 0.5
+    return ((1 - beta) * mfree + sig * math.sqrt(1 - beta * beta)
+            * torch.randn(T, N, generator=g)).float().numpy()
+
+
+@pytest.fixture(scope="module")
+def AL():
+    from lifscan import triton_alif
+    return triton_alif
+
+
+@pytest.mark.parametrize("name,beta,rho,q", NEURONS)
+@pytest.mark.parametrize("T,N", [(1024, 300), (37, 65), (1, 1)])
+def test_alif_serial_bitexact(AL, dev, name, beta, rho, q, T, N):
+    I = _inputs(beta, 2.0, T, N, 1)
+    u0 = uniform(N, -0.2, 0.8, 2)
+    w0 = uniform(N, 0.0, 0.3, 3)
+    print(f"alif serial {name} T={T} N={N}", flush=True)
+    U, W, S = AL.alif_serial_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev))
+    Uo, Wo, So = A.serial_forward(I, beta, rho, q, 1.0, 0.0, u0, w0)
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(W), Wo) and np.array_equal(host(S), So)
+
+
+@pytest.mark.parametrize("with_init", [False, True])
+def test_alif_warm_predict(AL, dev, with_init):
+    beta, rho, q = 0.99, 0.96, 0.2
+    T, N, C = 2048, 130, 64
+    I = _inputs(beta, 2.0, T, N, 4)
+    u0 = uniform(N, 0.0, 0.5, 5)
+    w0 = uniform(N, 0.0, 0.2, 6)
+    kw, kwo = {}, {}
+    if with_init:
+        UI = normal(T // C, N, 0.3, 0.1, 7)
+        WI = uniform(T // C * N, 0.0, 0.3, 8).reshape(T // C, N)
+        kw = dict(UI=gpu(UI, dev), WI=gpu(WI, dev))
+        kwo = dict(UI=UI, WI=WI)
+    print(f"alif warm init={with_init}", flush=True)
+    WP = AL.alif_warm_predict(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev), C, Wn=3,
+                              u_init=0.1, w_init=0.05, **kw)
+    WPo = A.warm_predict(I, beta, rho, q, 1.0, 0.0, u0, w0, C, Wn=3, u_init=0.1, w_init=0.05, **kwo)
+    assert np.array_equal(host(WP), WPo)
+
+
+def _preds(I, beta, rho, q, u0, w0, C):
+    Ur, Wr, Sr = A.serial_forward(I, beta, rho, q, 1.0, 0.0, u0, w0)
+    Wentry = np.concatenate([w0[None], Wr[C - 1:-1:C]], 0)
+    _, Wprev, _ = A.serial_forward((1.005 * I).astype(np.float32), beta, rho, q, 1.0, 0.0, u0, w0)
+    return (Ur, Wr, Sr), {
+        "oracle": Wentry,
+        "prev": np.concatenate([w0[None], Wprev[C - 1:-1:C]], 0),
+        "warm4": A.warm_predict(I, beta, rho, q, 1.0, 0.0, u0, w0, C, Wn=4),
+        "bad": (Wentry + 5 * q).astype(np.float32)}
+
+
+@pytest.mark.parametrize("name,beta,rho,q", NEURONS)
+@pytest.mark.parametrize("block", [1, 4])
+def test_alif_box_scan_matches_oracle(AL, dev, name, beta, rho, q, block):
+    """repair = 0: every intermediate of the box scan and the replayed outputs equal the
+    oracle's (same block of the split decision)."""
+    T, N, C, K1, K2 = 2048, 72, 128, 16, 32
+    I = _inputs(beta, 2.0, T, N, 9)
+    u0 = np.zeros(N, np.float32)
+    w0 = uniform(N, 0.0, 0.1, 10)
+    _, preds = _preds(I, beta, rho, q, u0, w0, C)
+    for tag in ("oracle", "warm4", "bad"):
+        Wp, dw = preds[tag], 0.1 * q
+        print(f"alif box {name} block={block} pred={tag}", flush=True)
+        st, sto, keep = {}, {}, {}
+        U, W, S = AL.alif_scan_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev),
+                                       gpu(Wp, dev), dw, C=C, K1=K1, K2=K2, BN=block, repair=0, stats=st)
+        run = AL.last_alif_run()
+        Uo, Wo, So = A.scan_forward(I, beta, rho, q, 1.0, 0.0, u0, w0, Wp, dw, C=C, K1=K1, K2=K2,
+                                    block=block, repair=0, stats=sto, keep=keep)
+        for g, o in (("LU", "Lu"), ("HU", "Hu"), ("LW", "Lw"), ("HW", "Hw"), ("MA", "A"), ("MB", "B"),
+                     ("SU", "SU"), ("SW", "SW")):
+            assert np.array_equal(host(run.view(g)), keep[o]), (tag, g)
+        for g, o in (("NL", "nl"), ("NP", "npc"), ("OVF", "ovf"), ("MISS", "MISS")):
+            assert np.array_equal(host(run.view(g, torch.int32)), keep[o]), (tag, g)
+        nl, npc = keep["nl"], keep["npc"]
+        lmask = np.arange(K1)[None, :, None] < nl[:, None]
+        pmask = np.arange(K2)[None, :, None] < npc[:, None]
+        for g, o in (("LS", "ls"), ("LC", "lc"), ("LX", "lx")):
+            assert np.array_equal(host(run.view(g))[lmask], keep[o][lmask]), (tag, g)
+        for g, o in (("PXL", "pxl"), ("PXR", "pxr"), ("PU", "pu"), ("PA", "pa"), ("POF", "pof")):
+            assert np.array_equal(host(run.view(g))[pmask], keep[o][pmask]), (tag, g)
+        assert np.array_equal(host(run.view("POWN", torch.int32))[pmask], keep["pown"][pmask])
+        assert np.array_equal(host(U), Uo) and np.array_equal(host(W), Wo) and np.array_equal(host(S), So)
+        for k in ("miss_frac", "overflow_frac", "mean_lines", "mean_pieces"):
+            assert st[k] == pytest.approx(sto[k], abs=1e-12), (tag, k)
+        assert st["max_pieces"] == sto["max_pieces"] and st["repair_iters"] == 0
+
+
+@pytest.mark.parametrize("name,beta,rho,q", NEURONS)
+@pytest.mark.parametrize("mfree", [0.5, 2.0])
+def test_alif_box_scan_with_repair_equals_serial(AL, dev, name, beta, rho, q, mfree):
+    """The reference's contract (tests/test_alif.py:10-39): with repair the box scan equals the
+    serial recurrence for any prediction, good or bad."""
+    T, N, C = 4096, 200, 128
+    I = _inputs(beta, mfree, T, N, 11)
+    u0 = np.zeros(N, np.float32)
+    w0 = uniform(N, 0.0, 0.1, 12)
+    (Ur, Wr, Sr), preds = _preds(I, beta, rho, q, u0, w0, C)
+    Ig, ug, wg = gpu(I, dev), gpu(u0, dev), gpu(w0, dev)
+    for tag, Wp in preds.items():
+        for block in (1, 4):
+            print(f"alif repair {name} mfree={mfree} pred={tag} block={block}", flush=True)
+            st, sto = {}, {}
+            U, W, S = AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, gpu(Wp, dev), 0.1 * q,
+                                           C=C, K1=16, K2=32, BN=block, repair=10 ** 6, stats=st)
+            assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), (tag, block)
+            assert np.array_equal(host(S), Sr), (tag, block)
+            if T * N <= 4096 * 200 and block == 4 and tag in ("oracle", "bad"):
+                A.scan_forward(I, beta, rho, q, 1.0, 0.0, u0, w0, Wp, 0.1 * q, C=C, K1=16, K2=32,
+                               block=block, repair=10 ** 6, stats=sto)
+                assert st["repair_iters"] == sto["repair_iters"]
+                assert st["miss_frac"] == pytest.approx(sto["miss_frac"], abs=1e-12)
+
+
+@pytest.mark.parametrize("R", [1, 2, 5])
+def test_alif_finite_repair_rounds(AL, dev, R):
+    beta, rho, q = 0.95, 0.995, 0.9
+    T, N, C = 2048, 64, 64
+    I = _inputs(beta, 2.0, T, N, 13)
+    u0 = np.zeros(N, np.float32)
+    w0 = np.zeros(N, np.float32)
+    _, preds = _preds(I, beta, rho, q, u0, w0, C)
+    Wp = preds["bad"]
+    print(f"alif finite repair R={R}", flush=True)
+    st, sto = {}, {}
+    U, W, S = AL.alif_scan_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev),
+                                   gpu(Wp, dev), 0.1 * q, C=C, K1=16, K2=32, BN=1, repair=R, stats=st)
+    Uo, Wo, So = A.scan_forward(I, beta, rho, q, 1.0, 0.0, u0, w0, Wp, 0.1 * q, C=C, K1=16, K2=32,
+                                block=1, repair=R, stats=sto)
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(W), Wo) and np.array_equal(host(S), So)
+    assert st["repair_iters"] == sto["repair_iters"]
+
+
+def test_alif_scan_phases_and_shapes(AL, dev):
+    beta, rho, q = 0.95, 0.995, 0.9
+    T, N, C = 1024, 64, 128
+    I = gpu(_inputs(beta, 2.0, T, N, 14), dev)
+    z = torch.zeros(N, device=dev)
+    Wp = torch.zeros(T // C, N, device=dev)
+    ph = {}
+    AL.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, Wp, 0.1, C=C, phases=ph)
+    assert set(ph) == {"envelope", "build", "carry", "replay"} and all(v >= 0 for v in ph.values())
+    with pytest.raises(ValueError):
+        AL.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, Wp, 0.1, C=100)
+    with pytest.raises(ValueError):
+        AL.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, Wp, 0.1, C=C, K2=24)
+    with pytest.raises(ValueError):
+        AL.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, Wp[1:], 0.1, C=C)
+
+
+@pytest.mark.parametrize("beta,rho,q", [(0.95, 0.995, 0.9), (0.99, 0.96, 0.2)])
+@pytest.mark.parametrize("mode,C", [("serial", 64), ("chunked", 64), ("chunked", 16), ("fused", 16),
+                                    ("fused", 32)])
+def test_alif_backward_modes(AL, dev, beta, rho, q, mode, C):
+    T, N = 1024, 130
+    x = _inputs(beta, 2.0, T, N, 15)
+    G = normal(T, N, 0.0, 1.0, 16)
+    u0 = uniform(N, -0.1, 0.3, 17)
+    w0 = uniform(N, 0.0, 0.2, 18)
+    U, W, S = A.serial_forward(x, beta, rho, q, 1.0, 0.0, u0, w0)
+    print(f"alif bwd {mode} C={C} beta={beta}", flush=True)
+    LV, LW = AL.alif_backward(gpu(x, dev), gpu(U, dev), gpu(W, dev), gpu(S, dev), gpu(G, dev), beta, rho, q,
+                              1.0, gpu(u0, dev), gpu(w0, dev), alpha=4.0, mode=mode, C=C)
+    LVo, LWo = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0)
+    LV6, LW6 = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0, dtype=np.float64)
+    assert rel(host(LV), LVo) < 1e-5 and rel(host(LW), LWo) < 1e-5
+    assert rel(host(LV), LV6) < 1e-4 and rel(host(LW), LW6) < 1e-4
+
+
+def test_alif_backward_rejects(AL, dev):
+    T, N = 100, 8
+    z = torch.zeros(T, N, device=dev)
+    v = torch.zeros(N, device=dev)
+    with pytest.raises(ValueError):
+        AL.alif_backward(z, z, z, z, z, 0.9, 0.95, 0.5, 1.0, v, v, mode="chunked", C=64)
+    with pytest.raises(ValueError):
+        AL.alif_backward(z, z, z, z, z, 0.9, 0.95, 0.5, 1.0, v, v, mode="fused", C=16)
+    with pytest.raises(ValueError):
+        AL.alif_backward(z, z, z, z, z, 0.9, 0.95, 0.5, 1.0, v, v, mode="nope")
+
+
+@pytest.mark.parametrize("fwd,bwd", [("serial", "serial"), ("serial", "scan"), ("scan", "scan")])
+def test_alif_layer_gradients(AL, dev, fwd, bwd):
+    """alif() gradients for I, u0, w0 and the four parameters against the fp64 adjoint and
+    ALIFFn's assembly (triton_alif.py:541-554)."""
+    beta, rho, q = 0.95, 0.995, 0.9
+    T, N, C = 1024, 96, 128
+    x = _inputs(beta, 2.0, T, N, 19)
+    G = normal(T, N, 0.0, 1.0, 20)
+    u0 = uniform(N, -0.1, 0.3, 21)
+    w0 = uniform(N, 0.0, 0.2, 22)
+    U, W, S = A.serial_forward(x, beta, rho, q, 1.0, 0.0, u0, w0)
+    Wentry = np.concatenate([w0[None], W[C - 1:-1:C]], 0)
+    xg = gpu(x, dev).requires_grad_(True)
+    ug = gpu(u0, dev).requires_grad_(True)
+    wg = gpu(w0, dev).requires_grad_(True)
+    ps = [torch.tensor(v, device=dev, requires_grad=True) for v in (beta, rho, q, 1.0)]
+    print(f"alif layer fwd={fwd} bwd={bwd}", flush=True)
+    Sg, Ug, Wg = AL.alif(xg, ug, wg, *ps, fwd=fwd, bwd=bwd, Wpred=gpu(Wentry, dev), dw=0.1 * q, C=C, Cb=64)
+    assert np.array_equal(host(Sg), S) and np.array_equal(host(Ug), U) and np.array_equal(host(Wg), W)
+    (Sg * gpu(G, dev)).sum().backward()
+    LV6, LW6 = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0, dtype=np.float64)
+    want = A.param_grads(x, U, W, S, G, LV6, LW6, beta, rho, q, 1.0, u0, w0, 4.0)
+    got = (xg.grad, ug.grad, wg.grad, *(p.grad for p in ps))
+    for k, (a, b) in enumerate(zip(got, want)):
+        assert rel(host(a), b) < 1e-4, k

@@ -270,8 +270,11 @@ __global__ __launch_bounds__(WAVE*(BLK > 2 ? BLK / 2 : 1)) void k_alif_build(
         hi_i = le ? hi_i : mid - 1;
       }
       const int idx = lo_i;
+      // every shuffle runs on all lanes of the neuron: a bpermute reads 0 from a lane that
+      // is switched off, so none may sit behind a per-lane condition
       const int d = i - __shfl(p, idx, 32);
-      const bool is_s = d == 0 && __shfl(es ? 1 : 0, idx, 32) != 0;
+      const int g_es = __shfl(es ? 1 : 0, idx, 32);
+      const bool is_s = d == 0 && g_es != 0;
       const float g_xl = __shfl(pxl, idx, 32), g_xr = __shfl(pxr, idx, 32);
       const float g_z = __shfl(z, idx, 32), g_v = __shfl(v, idx, 32);
       const float g_pa = __shfl(pa, idx, 32), g_po = __shfl(pof, idx, 32);
@@ -389,7 +392,8 @@ __global__ __launch_bounds__(64) void k_alif_carry(
     const unsigned long long fm = (__ballot(fire) & hmask) >> hb;
     const int first = fm ? __builtin_ctzll(fm) : K1;
     const bool none_ = first == K1;
-    const float lxf = none_ ? 0.0f : __shfl(lx, first, 32);
+    const float lx_first = __shfl(lx, first < K1 ? first : 0, 32);  // all lanes shuffle
+    const float lxf = none_ ? 0.0f : lx_first;
     const float xq = lxf * w + q;
     const int pw = i < K2 ? POWN[o * K2 + i] : -1;
     const float pl = i < K2 ? PXL[o * K2 + i] : INFINITY;
@@ -401,8 +405,10 @@ __global__ __launch_bounds__(64) void k_alif_carry(
     const float pu_i = i < K2 ? PU[o * K2 + i] : 0.0f;
     const float pa_i = i < K2 ? PA[o * K2 + i] : 0.0f;
     const float po_i = i < K2 ? POF[o * K2 + i] : 0.0f;
-    const float mu = nh ? __shfl(pu_i, hl, 32) : 0.0f;
-    const float mw = nh ? __shfl(pa_i * xq + po_i, hl, 32) : 0.0f;
+    const float pu_hit = __shfl(pu_i, hl, 32);
+    const float pw_hit = __shfl(pa_i * xq + po_i, hl, 32);
+    const float mu = nh ? pu_hit : 0.0f;
+    const float mw = nh ? pw_hit : 0.0f;
     float nu = none_ ? __fadd_rn(__fmul_rn(MA[o], u), MB[o]) : mu;
     float nw = none_ ? rhoC * w : mw;
     const bool inbox = (u >= LU[o]) && (u < HU[o]) && (w >= LWb[o]) && (w <= HWb[o]);

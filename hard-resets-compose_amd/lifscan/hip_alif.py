@@ -229,9 +229,12 @@ class ALIFFn(torch.autograd.Function):
         sg = alpha * sig * (1 - sig)
         d = GS + qq * LW
         lw_m1 = r * LW[0] - sg[0] * d[0]
-        return (LV, b * LV[0], lw_m1, (LV * Up).sum().reshape(()), (LW * Wp).sum().reshape(()),
-                (LW * S).sum().reshape(()), -(sg * d).sum().reshape(()), None, None, None, None,
-                None, None, None, None)
+        # parameter gradients are sums over T*N terms that largely cancel (dtheta0 above all):
+        # accumulate them in fp64
+        def tot(a):
+            return a.sum(dtype=torch.float64).float().reshape(())
+        return (LV, b * LV[0], lw_m1, tot(LV * Up), tot(LW * Wp), tot(LW * S), -tot(sg * d),
+                None, None, None, None, None, None, None, None)
 
 
 def alif(I, u0, w0, beta, rho, q, theta0=1.0, u_r=0.0, alpha=4.0, fwd="serial", bwd="scan",

@@ -515,7 +515,7 @@ def _beta_grad(Lam, U, u0, need):
     if not need:
         return None
     uprev = torch.cat([u0[None], U[:-1]], 0)
-    return (Lam * uprev).sum().reshape(())
+    return (Lam * uprev).sum(dtype=torch.float64).float().reshape(())
 
 
 class LIFFunction(torch.autograd.Function):

@@ -536,56 +536,164 @@ __device__ __forceinline__ float alif_sg(float up, float wp, float x, float beta
   return alpha * sig * (1.0f - sig);
 }
 
-// Reverse sweep over segments of Ls steps (triton_alif.py:374-440 PASS 0-4):
+// Parameter-gradient sums of ALIFFn.backward (triton_alif.py:541-554), accumulated in fp64
+// while the adjoint is swept: b = sum LV*u_{t-1} (dbeta), r = sum LW*w_{t-1} (drho),
+// q = sum LW*S (dq), t = sum sg*(g + q*LW) (-dtheta0).
+struct ParamAcc {
+  double b = 0.0, r = 0.0, q = 0.0, t = 0.0;
+  __device__ __forceinline__ void add(float lv, float up, float lw, float wp, float s, float sg,
+                                      float d) {
+    b += (double)lv * (double)up;
+    r += (double)lw * (double)wp;
+    q += (double)lw * (double)s;
+    t += (double)sg * (double)d;
+  }
+  __device__ __forceinline__ void wave_sum() {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      b += __shfl_xor(b, o, WAVE);
+      r += __shfl_xor(r, o, WAVE);
+      q += __shfl_xor(q, o, WAVE);
+      t += __shfl_xor(t, o, WAVE);
+    }
+  }
+  __device__ __forceinline__ void store(double* out) const {
+    out[0] = b;
+    out[1] = r;
+    out[2] = q;
+    out[3] = t;
+  }
+};
+
+// Reverse sweep over segments of Ls steps (triton_alif.py:374-440 PASS 0-3):
 //   PASS 0: compose the lw maps (P, Q)        PASS 1: lw replay from LamEnd, writes LW
 //   PASS 2: compose the lv maps (reads LW)    PASS 3: lv replay from LamEnd, writes LV
-//   PASS 4: fused serial sweep of both (one segment), writes LW and LV
-template <int PASS>
+// PASS 1 of the first segment also writes lw_{-1} = dL/dw0 to DW0 (if given); PASS 3 with PS
+// writes the block's parameter sums to partials[blockIdx.x].
+template <int PASS, bool PS>
 __global__ __launch_bounds__(64) void k_alif_bwd(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
     const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
     float* __restrict__ PA_, float* __restrict__ PB_, const float* __restrict__ lam_end,
-    int64_t N, int64_t Ls, int NB, float beta, float rho, float q, float theta0, float alpha) {
+    float* __restrict__ DW0, double* __restrict__ partials, int64_t N, int64_t Ls, int NB,
+    float beta, float rho, float q, float theta0, float alpha) {
   const int64_t m = blockIdx.x / NB;
   const int nb = (int)(blockIdx.x - m * NB);
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
-  if (n >= N) return;
-  const float u0n = u0[n], w0n = w0[n];
-  float lam = (PASS == 1 || PASS == 3) ? lam_end[m * N + n] : 0.0f;
-  float P = 1.0f, Q = 0.0f, lw = 0.0f, lv = 0.0f;
-  const int64_t t0 = m * Ls;
-  for (int64_t t = t0 + Ls - 1; t >= t0; --t) {
-    const size_t o = (size_t)t * N + n;
-    const float up = t > 0 ? U[o - N] : u0n;
-    const float wp = t > 0 ? W[o - N] : w0n;
-    const float x = I[o], s = S[o], gs = GS[o];
-    const float sg = alif_sg(up, wp, x, beta, theta0, alpha);
-    if (PASS == 0) {
-      const float a = rho - q * sg;
-      P = a * P;
-      Q = a * Q - sg * gs;
-    } else if (PASS == 1) {
-      st_nt(LW + o, lam);
-      lam = (rho - q * sg) * lam - sg * gs;
-    } else if (PASS == 2) {
-      const float a = (1.0f - s) * beta;
-      P = a * P;
-      Q = a * Q + sg * (gs + q * LW[o]);
-    } else if (PASS == 3) {
-      lam = (1.0f - s) * beta * lam + sg * (gs + q * LW[o]);
-      st_nt(LV + o, lam);
-    } else {
-      const float d = gs + q * lw;
-      lv = (1.0f - s) * beta * lv + sg * d;
-      st_nt(LW + o, lw);
-      st_nt(LV + o, lv);
-      lw = rho * lw - sg * d;
+  ParamAcc acc;
+  if (n < N) {
+    const float u0n = u0[n], w0n = w0[n];
+    float lam = (PASS == 1 || PASS == 3) ? lam_end[m * N + n] : 0.0f;
+    float P = 1.0f, Q = 0.0f;
+    const int64_t t0 = m * Ls;
+    for (int64_t t = t0 + Ls - 1; t >= t0; --t) {
+      const size_t o = (size_t)t * N + n;
+      const float up = t > 0 ? U[o - N] : u0n;
+      const float wp = t > 0 ? W[o - N] : w0n;
+      const float x = I[o], s = S[o], gs = GS[o];
+      const float sg = alif_sg(up, wp, x, beta, theta0, alpha);
+      if (PASS == 0) {
+        const float a = rho - q * sg;
+        P = a * P;
+        Q = a * Q - sg * gs;
+      } else if (PASS == 1) {
+        st_nt(LW + o, lam);
+        lam = (rho - q * sg) * lam - sg * gs;
+      } else if (PASS == 2) {
+        const float a = (1.0f - s) * beta;
+        P = a * P;
+        Q = a * Q + sg * (gs + q * LW[o]);
+      } else {
+        const float lw = LW[o];
+        const float d = gs + q * lw;
+        lam = (1.0f - s) * beta * lam + sg * d;
+        st_nt(LV + o, lam);
+        if (PS) acc.add(lam, up, lw, wp, s, sg, d);
+      }
     }
+    if (PASS == 0 || PASS == 2) {
+      PA_[m * N + n] = P;
+      PB_[m * N + n] = Q;
+    }
+    if (PASS == 1 && m == 0 && DW0) DW0[n] = lam;
   }
-  if (PASS == 0 || PASS == 2) {
-    PA_[m * N + n] = P;
-    PB_[m * N + n] = Q;
+  if (PS) {
+    acc.wave_sum();
+    if (threadIdx.x == 0) acc.store(partials + (size_t)blockIdx.x * 4);
+  }
+}
+
+// Fused serial sweep of both recurrences (triton_alif.py:444-487), one lane per neuron,
+// reverse tiles of D steps with the next tile's loads issued before the current tile's steps:
+//   d = g + q*lw;  lv = (1-s)*beta*lv + sg*d;  LW[t] = lw;  LV[t] = lv;  lw <- rho*lw - sg*d.
+// DW0 (if given) receives lw_{-1}; with PS, partials[blockIdx.x] the block's parameter sums.
+template <int D, bool WLW, bool PS>
+__global__ __launch_bounds__(64) void k_alif_bwd_serial(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
+    const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
+    const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
+    float* __restrict__ DW0, double* __restrict__ partials, int64_t N, int64_t T, float beta,
+    float rho, float q, float theta0, float alpha) {
+  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
+  ParamAcc acc;
+  if (n < N) {
+    const float u0n = u0[n], w0n = w0[n];
+    float lw = 0.0f, lv = 0.0f;
+    auto load = [&](int64_t t, float& x, float& s, float& g, float& up, float& wp) {
+      const size_t o = (size_t)t * N + n;
+      x = I[o];
+      s = S[o];
+      g = GS[o];
+      up = t > 0 ? U[o - N] : u0n;
+      wp = t > 0 ? W[o - N] : w0n;
+    };
+    auto step = [&](int64_t t, float x, float s, float g, float up, float wp) {
+      const size_t o = (size_t)t * N + n;
+      const float sg = alif_sg(up, wp, x, beta, theta0, alpha);
+      const float d = g + q * lw;
+      lv = (1.0f - s) * beta * lv + sg * d;
+      if (WLW) st_nt(LW + o, lw);
+      st_nt(LV + o, lv);
+      if (PS) acc.add(lv, up, lw, wp, s, sg, d);
+      lw = rho * lw - sg * d;
+    };
+    const int64_t nt = T / D;  // full tiles, from the end; the T % D first steps follow
+    float xa[D], sa[D], ga[D], ua[D], wa[D];
+    if (nt > 0) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) load(T - 1 - j, xa[j], sa[j], ga[j], ua[j], wa[j]);
+    }
+    for (int64_t b = 0; b < nt; ++b) {
+      float xb[D], sb[D], gb[D], ub[D], wb[D];
+      const bool more = b + 1 < nt;
+      if (more) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) load(T - 1 - (b + 1) * D - j, xb[j], sb[j], gb[j], ub[j], wb[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < D; ++j) step(T - 1 - b * D - j, xa[j], sa[j], ga[j], ua[j], wa[j]);
+      if (more) {
+#pragma unroll
+        for (int j = 0; j < D; ++j) {
+          xa[j] = xb[j];
+          sa[j] = sb[j];
+          ga[j] = gb[j];
+          ua[j] = ub[j];
+          wa[j] = wb[j];
+        }
+      }
+    }
+    for (int64_t t = T - nt * D - 1; t >= 0; --t) {
+      float x, s, g, up, wp;
+      load(t, x, s, g, up, wp);
+      step(t, x, s, g, up, wp);
+    }
+    if (DW0) DW0[n] = lw;
+  }
+  if (PS) {
+    acc.wave_sum();
+    if (threadIdx.x == 0) acc.store(partials + (size_t)blockIdx.x * 4);
   }
 }
 
@@ -594,14 +702,18 @@ __global__ __launch_bounds__(64) void k_alif_bwd(
 // registers, composes the lw recurrence into (P1, Q1), takes lw at its chunk end from the
 // later chunks through LDS, replays lw (kept in registers), composes the lv recurrence
 // (which reads lw_t) into (P2, Q2), takes lv at its chunk end the same way and replays lv.
-template <int C, int WV>
+// WLW: write LW.  PS: also keep u_{t-1}, w_{t-1} and sum the parameter gradients (one
+// partials row per workgroup).  DW0 (if given) receives lw_{-1} from the first chunk.
+template <int C, int WV, bool WLW, bool PS>
 __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
-    const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV, int64_t N, int M,
-    float beta, float rho, float q, float theta0, float alpha) {
+    const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
+    float* __restrict__ DW0, double* __restrict__ partials, int64_t N, int M, float beta,
+    float rho, float q, float theta0, float alpha) {
   __shared__ float sP[WV][WAVE], sQ[WV][WAVE];
   __shared__ float sLw[WAVE], sLv[WAVE];
+  __shared__ double sAcc[WV][4];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const unsigned lane = threadIdx.x % WAVE;
   const int64_t nb0 = (int64_t)blockIdx.x * WAVE;
@@ -610,6 +722,7 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
   const unsigned lb = ln * 4u, sb = lane * 4u;
   const unsigned rstride = (unsigned)(N * 4);
   const float u0n = u0[nb0 + ln], w0n = w0[nb0 + ln];
+  ParamAcc acc;
   if (w == 0) {
     sLw[lane] = 0.0f;
     sLv[lane] = 0.0f;
@@ -621,6 +734,7 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
     const bool active = m >= 0;
     const size_t row0 = (size_t)(active ? m : 0) * C;
     float sg[C], g[C], s1[C], lwv[C];
+    float upv[PS ? C : 1], wpv[PS ? C : 1];
     float lw_end = 0.0f, lv_end = 0.0f;
     if (active) {
       const Buf bi(I + nb0 + row0 * N), bs(S + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
@@ -635,6 +749,10 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
         sg[j] = alif_sg(up, wp, bi.ld(lb, so), beta, theta0, alpha);
         g[j] = bg.ld(lb, so);
         s1[j] = 1.0f - bs.ld(lb, so);
+        if (PS) {
+          upv[j] = up;
+          wpv[j] = wp;
+        }
       }
       float P = 1.0f, Q = 0.0f;
 #pragma unroll
@@ -656,6 +774,7 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
         lam = (rho - q * sg[j]) * lam - sg[j] * g[j];
       }
       lw_end = lam;
+      if (m == 0 && DW0 && valid) DW0[nb0 + lane] = lam;
     }
     __syncthreads();
     if (active) {
@@ -676,10 +795,12 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
       const Buf bo(LW + nb0 + row0 * N), bv(LV + nb0 + row0 * N);
 #pragma unroll
       for (int j = C - 1; j >= 0; --j) {
-        lam = s1[j] * beta * lam + sg[j] * (g[j] + q * lwv[j]);
+        const float d = g[j] + q * lwv[j];
+        lam = s1[j] * beta * lam + sg[j] * d;
         if (valid) {
-          bo.st_nt(sb, j * rstride, lwv[j]);
+          if (WLW) bo.st_nt(sb, j * rstride, lwv[j]);
           bv.st_nt(sb, j * rstride, lam);
+          if (PS) acc.add(lam, upv[j], lwv[j], wpv[j], 1.0f - s1[j], sg[j], d);
         }
       }
       lv_end = lam;
@@ -691,6 +812,21 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
       sLv[lane] = lv_end;
     }
     __syncthreads();
+  }
+  if (PS) {
+    acc.wave_sum();
+    if (lane == 0) acc.store(sAcc[w]);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      ParamAcc tot;
+      for (int v = 0; v < WV; ++v) {
+        tot.b += sAcc[v][0];
+        tot.r += sAcc[v][1];
+        tot.q += sAcc[v][2];
+        tot.t += sAcc[v][3];
+      }
+      tot.store(partials + (size_t)blockIdx.x * 4);
+    }
   }
 }
 
@@ -899,22 +1035,85 @@ extern "C" size_t lsh_alif_bwd_workspace(int64_t T, int64_t N, int C) {
   return kWsHeaderBytes + 3 * align_up(mn, 256);
 }
 
+extern "C" int64_t lsh_alif_bwd_partials(int64_t T, int64_t N, int mode, int C) {
+  if (T < 0 || N < 0 || mode < 0 || mode > 2) return -1;
+  const int64_t NB = (N + WAVE - 1) / WAVE;
+  if (mode != 1) return NB;
+  if (C < 1 || T % C != 0) return -1;
+  return (T / C) * NB;
+}
+
+template <int C, int W, bool WLW, bool PS>
+static void launch_alif_fused_w(const float* I, const float* u0, const float* w0, const float* U,
+                                const float* W_, const float* S, const float* GS, float* LW,
+                                float* LV, float* DW0, double* partials, int64_t N, int M, int NB,
+                                float beta, float rho, float q, float theta0, float alpha,
+                                hipStream_t st) {
+  hipLaunchKernelGGL((k_alif_bwd_fused<C, W, WLW, PS>), dim3((unsigned)NB), dim3(WAVE * W), 0, st, I,
+                     u0, w0, U, W_, S, GS, LW, LV, DW0, partials, N, M, beta, rho, q, theta0, alpha);
+}
+
+template <int C, bool WLW, bool PS>
+static void launch_alif_fused(const float* I, const float* u0, const float* w0, const float* U,
+                              const float* W, const float* S, const float* GS, float* LW, float* LV,
+                              float* DW0, double* partials, int64_t N, int M, int NB, float beta,
+                              float rho, float q, float theta0, float alpha, hipStream_t st) {
+  // registers allow 16 waves at C = 16 without the parameter sums, 4 at C = 32 with them, else 8
+  constexpr int WMAX = (C == 16 && !PS) ? 16 : ((C == 32 && PS) ? 4 : 8);
+  const int nw = fused_waves(NB, WMAX);
+  if constexpr (WMAX >= 16) {
+    if (nw == 16) {
+      launch_alif_fused_w<C, 16, WLW, PS>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB, beta,
+                                          rho, q, theta0, alpha, st);
+      return;
+    }
+  }
+  if (nw == 8)
+    launch_alif_fused_w<C, 8, WLW, PS>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB, beta,
+                                       rho, q, theta0, alpha, st);
+  else
+    launch_alif_fused_w<C, 4, WLW, PS>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB, beta,
+                                       rho, q, theta0, alpha, st);
+}
+
+template <bool WLW, bool PS>
+static void launch_alif_serial_bwd(const float* I, const float* u0, const float* w0, const float* U,
+                                   const float* W, const float* S, const float* GS, float* LW,
+                                   float* LV, float* DW0, double* partials, int64_t N, int64_t T,
+                                   int NB, float beta, float rho, float q, float theta0, float alpha,
+                                   hipStream_t st) {
+  hipLaunchKernelGGL((k_alif_bwd_serial<8, WLW, PS>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, w0,
+                     U, W, S, GS, LW, LV, DW0, partials, N, T, beta, rho, q, theta0, alpha);
+}
+
 extern "C" int lsh_alif_bwd(const float* I, const float* U, const float* W, const float* S,
                             const float* GS, const float* u0, const float* w0, float* LV,
-                            float* LW, int64_t T, int64_t N, float beta, float rho, float q,
-                            float theta0, float alpha, int mode, int C, void* ws, size_t ws_bytes,
-                            void* stream) {
+                            float* LW, float* DW0, double* partials, int64_t T, int64_t N,
+                            float beta, float rho, float q, float theta0, float alpha, int mode,
+                            int C, void* ws, size_t ws_bytes, void* stream) {
   if (bad_ptr(I) || bad_ptr(U) || bad_ptr(W) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(u0) ||
-      bad_ptr(w0) || bad_ptr(LV) || bad_ptr(LW))
+      bad_ptr(w0) || bad_ptr(LV))
     return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (mode < 0 || mode > 2) return LSH_ERR_ARG;
+  if (mode == 1 && bad_ptr(LW)) return LSH_ERR_ARG;  // the chunked scans keep LW in between
   if (T == 0 || N == 0) return LSH_OK;
   hipStream_t st = (hipStream_t)stream;
   const int NB = (int)((N + WAVE - 1) / WAVE);
-  if (mode == 0) {  // fused serial sweep (triton_alif.py:444-487)
-    hipLaunchKernelGGL(k_alif_bwd<4>, dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, w0, U, W, S, GS,
-                       LW, LV, nullptr, nullptr, nullptr, N, T, NB, beta, rho, q, theta0, alpha);
+  const bool wlw = LW != nullptr, ps = partials != nullptr;
+  if (mode == 0) {
+    if (wlw && ps)
+      launch_alif_serial_bwd<true, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, NB, beta,
+                                         rho, q, theta0, alpha, st);
+    else if (wlw)
+      launch_alif_serial_bwd<true, false>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, NB,
+                                          beta, rho, q, theta0, alpha, st);
+    else if (ps)
+      launch_alif_serial_bwd<false, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, NB,
+                                          beta, rho, q, theta0, alpha, st);
+    else
+      launch_alif_serial_bwd<false, false>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, NB,
+                                           beta, rho, q, theta0, alpha, st);
     LSH_CHECK_LAUNCH();
     return LSH_OK;
   }
@@ -924,12 +1123,26 @@ extern "C" int lsh_alif_bwd(const float* I, const float* U, const float* W, cons
   if (mode == 2) {  // single pass
     if (C != 16 && C != 32) return LSH_ERR_SHAPE;
     if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+#define LSH_FUSED(CC)                                                                              \
+  do {                                                                                             \
+    if (wlw && ps)                                                                                 \
+      launch_alif_fused<CC, true, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB,   \
+                                        beta, rho, q, theta0, alpha, st);                          \
+    else if (wlw)                                                                                  \
+      launch_alif_fused<CC, true, false>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB,  \
+                                         beta, rho, q, theta0, alpha, st);                         \
+    else if (ps)                                                                                   \
+      launch_alif_fused<CC, false, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB,  \
+                                         beta, rho, q, theta0, alpha, st);                         \
+    else                                                                                           \
+      launch_alif_fused<CC, false, false>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB, \
+                                          beta, rho, q, theta0, alpha, st);                        \
+  } while (0)
     if (C == 16)
-      hipLaunchKernelGGL((k_alif_bwd_fused<16, 4>), dim3((unsigned)NB), dim3(WAVE * 4), 0, st, I, u0, w0,
-                         U, W, S, GS, LW, LV, N, M, beta, rho, q, theta0, alpha);
+      LSH_FUSED(16);
     else
-      hipLaunchKernelGGL((k_alif_bwd_fused<32, 4>), dim3((unsigned)NB), dim3(WAVE * 4), 0, st, I, u0, w0,
-                         U, W, S, GS, LW, LV, N, M, beta, rho, q, theta0, alpha);
+      LSH_FUSED(32);
+#undef LSH_FUSED
     LSH_CHECK_LAUNCH();
     return LSH_OK;
   }
@@ -943,16 +1156,20 @@ extern "C" int lsh_alif_bwd(const float* I, const float* U, const float* W, cons
   float* PB_ = reinterpret_cast<float*>(w + mn);
   float* LE = reinterpret_cast<float*>(w + 2 * mn);
   const dim3 g((unsigned)((int64_t)M * NB)), b(WAVE), gc((unsigned)NB);
-  hipLaunchKernelGGL(k_alif_bwd<0>, g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, nullptr, N,
-                     C, NB, beta, rho, q, theta0, alpha);
+  hipLaunchKernelGGL((k_alif_bwd<0, false>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_,
+                     nullptr, nullptr, nullptr, N, C, NB, beta, rho, q, theta0, alpha);
   hipLaunchKernelGGL(k_rev_carry, gc, b, 0, st, PA_, PB_, LE, N, M);
-  hipLaunchKernelGGL(k_alif_bwd<1>, g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, LE, N, C,
-                     NB, beta, rho, q, theta0, alpha);
-  hipLaunchKernelGGL(k_alif_bwd<2>, g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, nullptr, N,
-                     C, NB, beta, rho, q, theta0, alpha);
+  hipLaunchKernelGGL((k_alif_bwd<1, false>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, LE,
+                     DW0, nullptr, N, C, NB, beta, rho, q, theta0, alpha);
+  hipLaunchKernelGGL((k_alif_bwd<2, false>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_,
+                     nullptr, nullptr, nullptr, N, C, NB, beta, rho, q, theta0, alpha);
   hipLaunchKernelGGL(k_rev_carry, gc, b, 0, st, PA_, PB_, LE, N, M);
-  hipLaunchKernelGGL(k_alif_bwd<3>, g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, LE, N, C,
-                     NB, beta, rho, q, theta0, alpha);
+  if (ps)
+    hipLaunchKernelGGL((k_alif_bwd<3, true>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_,
+                       LE, nullptr, partials, N, C, NB, beta, rho, q, theta0, alpha);
+  else
+    hipLaunchKernelGGL((k_alif_bwd<3, false>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_,
+                       LE, nullptr, nullptr, N, C, NB, beta, rho, q, theta0, alpha);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }

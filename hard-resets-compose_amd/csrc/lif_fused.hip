@@ -263,17 +263,32 @@ static void launch_fwd_fused(const float* I, const float* u0, float* U, float* S
 template <int C, bool SPEC>
 static int fwd_fused_k(const float* I, const float* u0, float* U, float* S, WsHeader* h, int64_t N,
                        int M, int K, float beta, float theta, float u_r, hipStream_t st) {
-  constexpr int W = 4;
-  if (!SPEC)
-    launch_fwd_fused<1, C, W, false>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
-  else if (K <= 4)
-    launch_fwd_fused<4, C, W, true>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
-  else if (K <= 8)
-    launch_fwd_fused<8, C, W, true>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
-  else if (K <= 16)
-    launch_fwd_fused<16, C, W, true>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
-  else
+  if (!SPEC) {
+    // registers allow 16 waves up to C = 32, 8 at C = 64
+    constexpr int WMAX = C <= 32 ? 16 : (C == 64 ? 8 : 4);
+    const int W = fused_waves((N + WAVE - 1) / WAVE, WMAX);
+    if constexpr (WMAX >= 16) {
+      if (W == 16) {
+        launch_fwd_fused<1, C, 16, false>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+        return LSH_OK;
+      }
+    }
+    if constexpr (WMAX >= 8) {
+      if (W == 8) {
+        launch_fwd_fused<1, C, 8, false>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+        return LSH_OK;
+      }
+    }
+    launch_fwd_fused<1, C, 4, false>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+  } else if (K <= 4) {  // map speculation keeps the maps of a round in LDS: 4 waves
+    launch_fwd_fused<4, C, 4, true>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+  } else if (K <= 8) {
+    launch_fwd_fused<8, C, 4, true>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+  } else if (K <= 16) {
+    launch_fwd_fused<16, C, 4, true>(I, u0, U, S, h, N, M, K, beta, theta, u_r, st);
+  } else {
     return LSH_ERR_SHAPE;
+  }
   return LSH_OK;
 }
 
@@ -289,31 +304,53 @@ static int fwd_fused(const float* I, const float* u0, float* U, float* S, WsHead
   }
 }
 
-template <int C, bool DETACH, bool HAS_GU>
+template <int C, int W, bool DETACH, bool HAS_GU>
 static void launch_bwd_fused(const float* I, const float* u0, const float* U, const float* S,
                              const float* GS, const float* GU, float* Lam, int64_t N, int M,
                              float beta, float theta, float u_r, float alpha, hipStream_t st) {
-  constexpr int W = 4;
   const int NB = (int)((N + WAVE - 1) / WAVE);
   hipLaunchKernelGGL((k_lif_bwd_fused<C, W, DETACH, HAS_GU>), dim3((unsigned)NB), dim3(WAVE * W), 0,
                      st, I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha);
+}
+
+template <int C, int W>
+static void bwd_fused_cw(const float* I, const float* u0, const float* U, const float* S,
+                         const float* GS, const float* GU, float* Lam, int64_t N, int M, float beta,
+                         float theta, float u_r, float alpha, bool detach, hipStream_t st) {
+  if (detach) {
+    if (GU)
+      launch_bwd_fused<C, W, true, true>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
+    else
+      launch_bwd_fused<C, W, true, false>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
+  } else {
+    if (GU)
+      launch_bwd_fused<C, W, false, true>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
+    else
+      launch_bwd_fused<C, W, false, false>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha,
+                                           st);
+  }
 }
 
 template <int C>
 static void bwd_fused_c(const float* I, const float* u0, const float* U, const float* S,
                         const float* GS, const float* GU, float* Lam, int64_t N, int M, float beta,
                         float theta, float u_r, float alpha, bool detach, hipStream_t st) {
-  if (detach) {
-    if (GU)
-      launch_bwd_fused<C, true, true>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
-    else
-      launch_bwd_fused<C, true, false>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
-  } else {
-    if (GU)
-      launch_bwd_fused<C, false, true>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
-    else
-      launch_bwd_fused<C, false, false>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, st);
+  // registers allow 16 waves at C = 16, 8 at C = 32
+  constexpr int WMAX = C == 16 ? 16 : (C == 32 ? 8 : 4);
+  const int W = fused_waves((N + WAVE - 1) / WAVE, WMAX);
+  if constexpr (WMAX >= 16) {
+    if (W == 16) {
+      bwd_fused_cw<C, 16>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, detach, st);
+      return;
+    }
   }
+  if constexpr (WMAX >= 8) {
+    if (W == 8) {
+      bwd_fused_cw<C, 8>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, detach, st);
+      return;
+    }
+  }
+  bwd_fused_cw<C, 4>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, detach, st);
 }
 
 }  // namespace lsh

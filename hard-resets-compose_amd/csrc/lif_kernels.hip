@@ -505,6 +505,12 @@ static void launch_bwd3(const float* I, const float* u0, const float* U, const f
                         float* PB, int64_t N, int64_t Ls, int64_t M, float beta, float theta,
                         float u_r, float alpha, hipStream_t st) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
+  if (M == 1 && !COMPOSE) {
+    // one segment: the serial adjoint, latency-bound with few neurons -> 16 steps in flight
+    hipLaunchKernelGGL((k_lif_bwd<16, COMPOSE, DETACH, HAS_GU>), dim3((unsigned)NB), dim3(WAVE), 0, st,
+                       I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, N, Ls, NB, beta, theta, u_r, alpha);
+    return;
+  }
   constexpr int D = 4;
   hipLaunchKernelGGL((k_lif_bwd<D, COMPOSE, DETACH, HAS_GU>), dim3((unsigned)(M * NB)), dim3(WAVE), 0,
                      st, I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, N, Ls, NB, beta, theta, u_r, alpha);

@@ -19,6 +19,15 @@ namespace lsh {
 
 constexpr int WAVE = 64;
 
+// Waves per workgroup of the single-pass (fused) kernels, where each wave owns one chunk of a
+// round: 4 when there are enough 64-neuron blocks to give every CU several workgroups, more
+// chunks in flight per workgroup when there are few.  wmax is what the kernel's registers allow
+// (16 waves of a workgroup need <= 128 VGPRs per lane, 8 waves <= 256).
+inline int fused_waves(int64_t nblocks, int wmax) {
+  const int w = nblocks >= 512 ? 4 : (nblocks >= 128 ? 8 : 16);
+  return w < wmax ? w : wmax;
+}
+
 // LIF membrane update before the threshold test (triton_lif.py:22).
 __device__ __forceinline__ float lif_v(float u, float x, float beta) {
   return __fadd_rn(__fmul_rn(beta, u), x);

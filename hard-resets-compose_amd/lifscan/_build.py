@@ -48,26 +48,57 @@ def hipcc():
     raise RuntimeError("hipcc not found: cannot build the HIP extension")
 
 
-def build_library(verbose=False, extra_flags=()):
-    """Compile every csrc/*.hip into lifscan/_lib/liblifscan_hip.so (always recompiles)."""
-    os.makedirs(LIB_DIR, exist_ok=True)
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), *HIP_FLAGS, *extra_flags, "-I", os.path.join(REPO, "include"), *sources(),
-           "-o", tmp]
+def _run(cmd, verbose):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout)
-        raise RuntimeError(f"hipcc failed (exit {res.returncode})")
+        raise RuntimeError(f"hipcc failed (exit {res.returncode}): {' '.join(cmd[-3:])}")
     if verbose and res.stdout.strip():
         # host pass warns about the gfx-only target feature; show anything else
         lines = [l for l in res.stdout.splitlines() if "packed-fp32-ops" not in l]
         if lines:
             print("\n".join(lines))
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+
+
+def _stale(obj, src):
+    """True when obj is missing or older than its source or any csrc header."""
+    if not os.path.exists(obj):
+        return True
+    deps = [src] + [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".h")]
+    deps.append(os.path.join(REPO, "include", "lifscan_hip.h"))
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(d) > t for d in deps if os.path.exists(d))
+
+
+def build_library(verbose=False, extra_flags=(), out=None, jobs=None, incremental=False):
+    """Compile every csrc/*.hip (one hipcc per source, in parallel) and link them into
+    lifscan/_lib/liblifscan_hip.so, or into `out`.  Recompiles everything unless
+    `incremental`, which skips sources whose object is newer than them and every header."""
+    from concurrent.futures import ThreadPoolExecutor
+    out = out or LIB_PATH
+    obj_dir = os.path.join(os.path.dirname(out), "_obj")
+    os.makedirs(obj_dir, exist_ok=True)
+    flags = [f for f in HIP_FLAGS if f != "-shared"] + list(extra_flags)
+    inc = ["-I", os.path.join(REPO, "include")]
+    objs = []
+    cmds = []
+    for src in sources():
+        obj = os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o")
+        objs.append(obj)
+        if incremental and not extra_flags and not _stale(obj, src):
+            continue
+        cmds.append([hipcc(), *flags, *inc, "-c", src, "-o", obj])
+    if cmds:
+        jobs = jobs or min(len(cmds), max(1, min(8, os.cpu_count() or 1)))
+        with ThreadPoolExecutor(jobs) as ex:
+            list(ex.map(lambda c: _run(c, verbose), cmds))
+    tmp = out + ".tmp"
+    _run([hipcc(), *HIP_FLAGS, *extra_flags, *objs, "-o", tmp], verbose)
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build_library(verbose=True))
+    print(build_library(verbose="-v" in sys.argv, incremental="-i" in sys.argv))

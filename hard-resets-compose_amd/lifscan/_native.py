@@ -98,8 +98,9 @@ SIGNATURES = {
                                 c_f, c_f, c_f, c_i, c_i, c_i, c_i, c_i64, c_p, c_sz,
                                 ctypes.POINTER(c_p), c_p]),
     "lsh_alif_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
-    "lsh_alif_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,
-                           c_f, c_f, c_i, c_i, c_p, c_sz, c_p]),
+    "lsh_alif_bwd_partials": (c_i64, [c_i64, c_i64, c_i, c_i]),
+    "lsh_alif_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f,
+                           c_f, c_f, c_f, c_f, c_i, c_i, c_p, c_sz, c_p]),
     "lsh_lif_scan_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
     "lsh_lif_scan_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f,
                                c_i, c_i, c_p, c_sz, c_p]),
@@ -107,7 +108,9 @@ SIGNATURES = {
 
 
 def lib_path():
-    return _build.LIB_PATH
+    """The in-tree build, or the library named by LIFSCAN_HIP_LIB (another build of the same
+    sources, e.g. with other tile constants)."""
+    return os.environ.get("LIFSCAN_HIP_LIB") or _build.LIB_PATH
 
 
 def lib():

@@ -158,19 +158,8 @@ def alif_scan_forward(I, beta, rho, q, theta0, u_r, u0, w0, Wpred, dw, C=128, K1
     return U, W, S
 
 
-def alif_backward(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha=4.0, mode="scan", C=64,
-                  BN=32, D=4, nw=1):
-    """(LV, LW) with LV[t] = dL/dv_t (= dL/dI_t), LW[t] = dL/dw_t for dL/dS = GS
-    (triton_alif.py:490-521).  mode: serial_pf / serial_tuned / serial (fused serial sweep),
-    chunked (two-level affine scans over chunks of C), fused (single pass, C in {16, 32}) or
-    scan (fused when N is large, else chunked)."""
-    I = _input(I)
-    T, N = I.shape
-    u0 = _vec(u0, N, I)
-    w0 = _vec(w0, N, I, "w0")
-    U, W, S, GS = (_same(a, I, nm) for a, nm in ((U, "U"), (W, "W"), (S, "S"), (GS, "GS")))
-    LV, LW = torch.empty_like(I), torch.empty_like(I)
-    ws, nbytes = None, 0
+def _bwd_mode(mode, T, N, C):
+    """Kernel mode code and chunk for an alif_backward mode name."""
     C = int(C)
     if mode == "scan":
         fused = N >= ALIF_FUSED_BWD_MIN_N and T % ALIF_FUSED_BWD_C == 0
@@ -178,29 +167,66 @@ def alif_backward(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha=4.0, mode=
         if fused:
             C = ALIF_FUSED_BWD_C
     if mode in ("serial_pf", "serial_tuned", "serial"):
-        code = 0
-    elif mode == "fused":  # single pass, C in {16, 32}
-        code = 2
-    elif mode == "chunked":
+        return 0, C
+    if mode == "fused":  # single pass, C in {16, 32}
+        return 2, C
+    if mode == "chunked":
         if T % C:
             raise ValueError(f"T={T} must be divisible by C={C}")
-        code = 1
-        nbytes = _n.lib().lsh_alif_bwd_workspace(T, N, C)
+        return 1, C
+    raise ValueError(f"unknown mode {mode!r}")
+
+
+def _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C, want_lw, want_params):
+    """One lsh_alif_bwd call -> (LV, LW or None, DW0 [N], param sums [4] fp64 or None)."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    w0 = _vec(w0, N, I, "w0")
+    U, W, S, GS = (_same(a, I, nm) for a, nm in ((U, "U"), (W, "W"), (S, "S"), (GS, "GS")))
+    code, C = _bwd_mode(mode, T, N, C)
+    L = _n.lib()
+    LV = torch.empty_like(I)
+    LW = torch.empty_like(I) if (want_lw or code == 1) else None
+    DW0 = torch.empty(N, device=I.device, dtype=torch.float32)
+    parts = None
+    if want_params:
+        P = L.lsh_alif_bwd_partials(T, N, code, C)
+        if P < 0:
+            raise ValueError("bad backward shape")
+        parts = torch.empty(max(P, 1), 4, device=I.device, dtype=torch.float64)
+        if T == 0 or N == 0:
+            parts.zero_()
+    ws, nbytes = None, 0
+    if code == 1:
+        nbytes = L.lsh_alif_bwd_workspace(T, N, C)
         ws = _n.workspace(nbytes, I.device)
-    else:
-        raise ValueError(f"unknown mode {mode!r}")
     with torch.cuda.device(I.device):
-        _n.check(_n.lib().lsh_alif_bwd(
+        _n.check(L.lsh_alif_bwd(
             _n.ptr(I), _n.ptr(U), _n.ptr(W), _n.ptr(S), _n.ptr(GS), _n.ptr(u0), _n.ptr(w0), _n.ptr(LV),
-            _n.ptr(LW), T, N, _f32(beta), _f32(rho), _f32(q), _f32(theta0), _f32(alpha), code, C,
-            _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_alif_bwd")
+            _n.ptr(LW), _n.ptr(DW0), _n.ptr(parts), T, N, _f32(beta), _f32(rho), _f32(q), _f32(theta0),
+            _f32(alpha), code, C, _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_alif_bwd")
+    sums = parts.sum(0) if parts is not None else None
+    return LV, (LW if want_lw else None), DW0, sums
+
+
+def alif_backward(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha=4.0, mode="scan", C=64,
+                  BN=32, D=4, nw=1):
+    """(LV, LW) with LV[t] = dL/dv_t (= dL/dI_t), LW[t] = dL/dw_t for dL/dS = GS
+    (triton_alif.py:490-521).  mode: serial_pf / serial_tuned / serial (fused serial sweep),
+    chunked (two-level affine scans over chunks of C), fused (single pass, C in {16, 32}) or
+    scan (fused when N is large, else chunked)."""
+    LV, LW, _, _ = _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C,
+                                  want_lw=True, want_params=False)
     return LV, LW
 
 
 class ALIFFn(torch.autograd.Function):
     """S = ALIF(I; u0, w0, beta, rho, q, theta0) with u_r fixed (triton_alif.py:524-554).
     Forward: serial, or the box scan with prediction Wpred (K1 = K2 = 32, block 4, no repair,
-    as the reference); backward: serial or scan.  Gradients for I, u0, w0, beta, rho, q, theta0."""
+    as the reference); backward: serial or scan.  Gradients for I, u0, w0, beta, rho, q, theta0:
+    the adjoint kernels also return dL/dw0 and the four parameter sums (fp64), so LW is never
+    written to memory."""
 
     @staticmethod
     def forward(ctx, I, u0, w0, beta, rho, q, theta0, u_r, alpha, fwd, bwd, Wpred, dw, C, Cb):
@@ -219,21 +245,17 @@ class ALIFFn(torch.autograd.Function):
     def backward(ctx, gS, gU, gW):
         I, u0, w0, U, W, S = ctx.saved_tensors
         b, r, qq, th, u_r, alpha, bwd, Cb = ctx.c
-        GS = gS.contiguous()
-        LV, LW = alif_backward(I, U, W, S, GS, b, r, qq, th, u0, w0, alpha=alpha,
-                               mode="serial_tuned" if bwd == "serial" else bwd, C=Cb)
-        Up = torch.cat([u0[None], U[:-1]], 0)
-        Wp = torch.cat([w0[None], W[:-1]], 0)
-        V = b * Up + I
-        sig = torch.sigmoid(alpha * (V - th - Wp))
-        sg = alpha * sig * (1 - sig)
-        d = GS + qq * LW
-        lw_m1 = r * LW[0] - sg[0] * d[0]
-        # parameter gradients are sums over T*N terms that largely cancel (dtheta0 above all):
-        # accumulate them in fp64
-        def tot(a):
-            return a.sum(dtype=torch.float64).float().reshape(())
-        return (LV, b * LV[0], lw_m1, tot(LV * Up), tot(LW * Wp), tot(LW * S), -tot(sg * d),
+        need = ctx.needs_input_grad
+        want_params = any(need[3:7])
+        LV, _, DW0, sums = _alif_bwd_call(I, U, W, S, gS.contiguous(), b, r, qq, th, u0, w0, alpha,
+                                          "serial_tuned" if bwd == "serial" else bwd, Cb,
+                                          want_lw=False, want_params=want_params)
+        if sums is None:
+            db = dr = dq = dth = None
+        else:
+            sums = sums.float()
+            db, dr, dq, dth = sums[0], sums[1], sums[2], -sums[3]
+        return (LV, b * LV[0], DW0.reshape(w0.shape) if w0.dim() else DW0, db, dr, dq, dth,
                 None, None, None, None, None, None, None, None)
 
 

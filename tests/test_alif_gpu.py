@@ -248,3 +248,33 @@ def test_alif_layer_gradients(AL, dev, fwd, bwd, beta, rho, q, T, N):
         # that cancel to a few 1e-3 of their magnitude (dtheta0 most), so they get the
         # reference's own bar, 1e-3 (tests/test_alif_grad.py:34)
         assert rel(host(a), b) < (1e-4 if k < 3 else 1e-3), k
+
+
+@pytest.mark.parametrize("mode,C", [("serial", 64), ("chunked", 64), ("fused", 16), ("fused", 32)])
+@pytest.mark.parametrize("T,N", [(1024, 130), (77 * 16, 33)])
+def test_alif_backward_param_sums_and_dw0(AL, dev, mode, C, T, N):
+    """The adjoint kernels' own reductions (dL/dw0 and the four parameter sums, one fp64 row per
+    block) against the fp64 assembly of ALIFFn.backward (triton_alif.py:541-554); LV the same
+    with and without LW written."""
+    from lifscan import hip_alif
+    beta, rho, q = 0.95, 0.995, 0.9
+    if mode != "serial" and T % C:
+        C = 16
+    x = _inputs(beta, 2.0, T, N, 23)
+    G = normal(T, N, 0.0, 1.0, 24)
+    u0 = uniform(N, -0.1, 0.3, 25)
+    w0 = uniform(N, 0.0, 0.2, 26)
+    U, W, S = A.serial_forward(x, beta, rho, q, 1.0, 0.0, u0, w0)
+    args = [gpu(a, dev) for a in (x, U, W, S, G)]
+    print(f"alif bwd sums {mode} C={C} T={T} N={N}", flush=True)
+    LV, LW, DW0, sums = hip_alif._alif_bwd_call(*args, beta, rho, q, 1.0, gpu(u0, dev), gpu(w0, dev), 4.0,
+                                                mode, C, want_lw=False, want_params=True)
+    LV2, LW2 = AL.alif_backward(*args, beta, rho, q, 1.0, gpu(u0, dev), gpu(w0, dev), mode=mode, C=C)
+    # the variant without LW may group chunks into rounds differently (another rounding order)
+    assert LW is None and rel(host(LV), host(LV2)) < 1e-6
+    LV6, LW6 = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0, dtype=np.float64)
+    want = A.param_grads(x, U, W, S, G, LV6, LW6, beta, rho, q, 1.0, u0, w0, 4.0)
+    assert rel(host(DW0), want[2]) < 1e-4
+    got = host(sums)
+    for k, w in enumerate((want[3], want[4], want[5], -want[6])):
+        assert rel(got[k], w) < 1e-3, k

@@ -175,13 +175,19 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_fwd_fused(const float* __restri
   }
 }
 
-template <int C, int W, bool DETACH, bool HAS_GU>
+// PS (detached, no GU): also sums the parameter gradients of fit.py:43-47 in fp64 (u_{t-1}
+// and the spike bits of the chunk stay in registers) and writes one partials row per
+// workgroup: sum lam_t*u_{t-1}, sum gs_t*sg_t, sum s_t*lam_{t+1}.
+template <int C, int W, bool DETACH, bool HAS_GU, bool PS = false>
 __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ U,
     const float* __restrict__ S, const float* __restrict__ GS, const float* __restrict__ GU,
-    float* __restrict__ Lam, int64_t N, int M, float beta, float theta, float u_r, float alpha) {
+    float* __restrict__ Lam, double* __restrict__ partials, int64_t N, int M, float beta,
+    float theta, float u_r, float alpha) {
+  static_assert(!PS || (DETACH && !HAS_GU && C <= 64), "parameter sums: detached, no GU");
   __shared__ float sP[W][WAVE], sQ[W][WAVE];
   __shared__ float sLam[WAVE];
+  __shared__ double sAcc[PS ? W : 1][3];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const unsigned lane = threadIdx.x % WAVE;
   const int64_t nb0 = (int64_t)blockIdx.x * WAVE;
@@ -195,6 +201,7 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
   const float* __restrict__ Ub = U + nb0;
   float* __restrict__ Lb = Lam + nb0;
   const float u0n = u0[nb0 + ln];
+  double acc_b = 0.0, acc_t = 0.0, acc_r = 0.0;
   if (w == 0) sLam[lane] = 0.0f;
   __syncthreads();
   const int rounds = (M + W - 1) / W;
@@ -202,6 +209,8 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
     const int m = M - 1 - (r * W + w);  // wave 0 holds the latest chunk of the round
     const bool active = m >= 0;
     float a[C], b[C];
+    float upk[PS ? C : 1];
+    unsigned long long sbits = 0;
     float lam = 0.0f;
     const size_t row0 = (size_t)(active ? m : 0) * C;
     const unsigned rstride = (unsigned)(N * 4);
@@ -222,6 +231,11 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
         if (!DETACH) J = J + (u_r - v) * sg;
         a[j] = beta * J;
         b[j] = HAS_GU ? gs * sg + J * Buf(Hb + row0 * N).ld(lb, so) : gs * sg;
+        if (PS) {
+          upk[j] = up;
+          if (s != 0.0f) sbits |= 1ull << j;
+          if (valid) acc_t += (double)b[j];
+        }
       }
       float P = 1.0f, Q = 0.0f;
 #pragma unroll
@@ -239,14 +253,47 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
       const Buf bl(Lb + row0 * N);
 #pragma unroll
       for (int j = C - 1; j >= 0; --j) {
+        const float lam_next = lam;
         lam = b[j] + a[j] * lam;
-        if (valid) bl.st_nt(sb, j * rstride, lam);
+        if (valid) {
+          bl.st_nt(sb, j * rstride, lam);
+          if (PS) {
+            acc_b += (double)lam * (double)upk[j];
+            if ((sbits >> j) & 1ull) acc_r += (double)lam_next;
+          }
+        }
       }
     }
     __syncthreads();
     const int last = min(W, M - r * W) - 1;
     if (w == last) sLam[lane] = lam;
     __syncthreads();
+  }
+  if (PS) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      acc_b += __shfl_xor(acc_b, o, WAVE);
+      acc_t += __shfl_xor(acc_t, o, WAVE);
+      acc_r += __shfl_xor(acc_r, o, WAVE);
+    }
+    if (lane == 0) {
+      sAcc[w][0] = acc_b;
+      sAcc[w][1] = acc_t;
+      sAcc[w][2] = acc_r;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double tb = 0.0, tt = 0.0, tr = 0.0;
+      for (int v = 0; v < W; ++v) {
+        tb += sAcc[v][0];
+        tt += sAcc[v][1];
+        tr += sAcc[v][2];
+      }
+      double* out = partials + (size_t)blockIdx.x * 3;
+      out[0] = tb;
+      out[1] = tt;
+      out[2] = tr;
+    }
   }
 }
 
@@ -310,7 +357,7 @@ static void launch_bwd_fused(const float* I, const float* u0, const float* U, co
                              float beta, float theta, float u_r, float alpha, hipStream_t st) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   hipLaunchKernelGGL((k_lif_bwd_fused<C, W, DETACH, HAS_GU>), dim3((unsigned)NB), dim3(WAVE * W), 0,
-                     st, I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha);
+                     st, I, u0, U, S, GS, GU, Lam, nullptr, N, M, beta, theta, u_r, alpha);
 }
 
 template <int C, int W>
@@ -351,6 +398,49 @@ static void bwd_fused_c(const float* I, const float* u0, const float* U, const f
     }
   }
   bwd_fused_cw<C, 4>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, detach, st);
+}
+
+template <int C, int W>
+static void launch_param_fused(const float* I, const float* u0, const float* U, const float* S,
+                               const float* GS, float* Lam, double* partials, int64_t N, int M,
+                               float beta, float theta, float u_r, float alpha, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  hipLaunchKernelGGL((k_lif_bwd_fused<C, W, true, false, true>), dim3((unsigned)NB), dim3(WAVE * W), 0,
+                     st, I, u0, U, S, GS, nullptr, Lam, partials, N, M, beta, theta, u_r, alpha);
+}
+
+template <int C>
+static void param_fused_c(const float* I, const float* u0, const float* U, const float* S,
+                          const float* GS, float* Lam, double* partials, int64_t N, int M, float beta,
+                          float theta, float u_r, float alpha, hipStream_t st) {
+  // u_{t-1} kept per step: 8 waves up to C = 32
+  constexpr int WMAX = C <= 32 ? 8 : 4;
+  const int W = fused_waves((N + WAVE - 1) / WAVE, WMAX);
+  if constexpr (WMAX >= 8) {
+    if (W == 8) {
+      launch_param_fused<C, 8>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st);
+      return;
+    }
+  }
+  launch_param_fused<C, 4>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st);
+}
+
+int lif_param_bwd_fused(const float* I, const float* u0, const float* U, const float* S,
+                        const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
+                        float beta, float theta, float u_r, float alpha, int C, hipStream_t st) {
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C != 16 && C != 32 && C != 64) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  const int M = (int)(T / C);
+  switch (C) {
+    case 16: param_fused_c<16>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st); break;
+    case 32: param_fused_c<32>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st); break;
+    default: param_fused_c<64>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st); break;
+  }
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
 }
 
 }  // namespace lsh

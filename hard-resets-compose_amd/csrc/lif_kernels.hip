@@ -86,17 +86,39 @@ __global__ __launch_bounds__(64) void k_lif_fwd(const float* __restrict__ I,
 //                    (triton_lif.py:422-457 bwd_chunk_tiled_kernel).
 // Coefficients (triton_lif.py:43-50 _coef): v = beta*u_{t-1} + x_t, sg = surrogate'(v-theta),
 // J = 1 - s_t (+ (u_r - v)*sg when the reset is not detached), a = beta*J, b = gs*sg + J*gu.
-template <int D, bool COMPOSE, bool DETACH, bool HAS_GU>
+// PS (replay, detached, no GU): also sums the parameter gradients of fit.py:43-47 in fp64 and
+// writes one partials row per block: sum lam_t*u_{t-1}, sum gs_t*sg_t, sum s_t*lam_{t+1}.
+template <int D, bool COMPOSE, bool DETACH, bool HAS_GU, bool PS>
 __global__ __launch_bounds__(64) void k_lif_bwd(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ U,
     const float* __restrict__ S, const float* __restrict__ GS, const float* __restrict__ GU,
     const float* __restrict__ lam_end, float* __restrict__ Lam, float* __restrict__ PA,
-    float* __restrict__ PB, int64_t N, int64_t Ls, int NB, float beta, float theta, float u_r,
-    float alpha) {
+    float* __restrict__ PB, double* __restrict__ partials, int64_t N, int64_t Ls, int NB,
+    float beta, float theta, float u_r, float alpha) {
+  static_assert(!PS || (!COMPOSE && DETACH && !HAS_GU), "parameter sums: detached replay only");
   const int64_t m = blockIdx.x / NB;
   const int nb = (int)(blockIdx.x - m * NB);
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
-  if (n >= N) return;
+  double acc_b = 0.0, acc_t = 0.0, acc_r = 0.0;
+  auto finish = [&]() {
+    if (!PS) return;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      acc_b += __shfl_xor(acc_b, o, WAVE);
+      acc_t += __shfl_xor(acc_t, o, WAVE);
+      acc_r += __shfl_xor(acc_r, o, WAVE);
+    }
+    if (threadIdx.x == 0) {
+      double* out = partials + (size_t)blockIdx.x * 3;
+      out[0] = acc_b;
+      out[1] = acc_t;
+      out[2] = acc_r;
+    }
+  };
+  if (n >= N) {
+    finish();
+    return;
+  }
   const float u0n = u0[n];
   float lam = (!COMPOSE && lam_end) ? lam_end[m * N + n] : 0.0f;
   float P = 1.0f, Q = 0.0f;
@@ -112,18 +134,29 @@ __global__ __launch_bounds__(64) void k_lif_bwd(
     bb = HAS_GU ? gs * sg + J * gu : gs * sg;
   };
   auto uprev = [&](int64_t t) -> float { return t > 0 ? U[(size_t)(t - 1) * N + n] : u0n; };
+  // one step of the replay: lam_{t+1} -> lam_t (bb = gs*sg when PS)
+  auto replay = [&](size_t o, float up, float s, float a, float bb) {
+    const float lam_next = lam;
+    lam = bb + a * lam;
+    st_nt(Lam + o, lam);
+    if (PS) {
+      acc_b += (double)lam * (double)up;
+      acc_t += (double)bb;
+      acc_r += s != 0.0f ? (double)lam_next : 0.0;
+    }
+  };
 
   // the highest `rem` steps first (segment lengths that are not a multiple of D)
   for (int64_t t = t_begin + Ls - 1; t >= t_begin + nt * D; --t) {
     const size_t o = (size_t)t * N + n;
     float a, bb;
-    coef(uprev(t), I[o], S[o], GS[o], HAS_GU ? GU[o] : 0.0f, a, bb);
+    const float up = uprev(t), s = S[o];
+    coef(up, I[o], s, GS[o], HAS_GU ? GU[o] : 0.0f, a, bb);
     if (COMPOSE) {
       Q = bb + a * Q;
       P = a * P;
     } else {
-      lam = bb + a * lam;
-      st_nt(Lam + o, lam);
+      replay(o, up, s, a, bb);
     }
   }
   if (nt == 0) {
@@ -131,6 +164,7 @@ __global__ __launch_bounds__(64) void k_lif_bwd(
       PA[m * N + n] = P;
       PB[m * N + n] = Q;
     }
+    finish();
     return;
   }
   float xa[D], sa[D], ga[D], ha[D], pa[D];
@@ -161,8 +195,7 @@ __global__ __launch_bounds__(64) void k_lif_bwd(
         Q = bb + a * Q;
         P = a * P;
       } else {
-        lam = bb + a * lam;
-        st_nt(Lam + (size_t)(t0 + j) * N + n, lam);
+        replay((size_t)(t0 + j) * N + n, pa[j], sa[j], a, bb);
       }
     }
     if (more) {
@@ -180,6 +213,7 @@ __global__ __launch_bounds__(64) void k_lif_bwd(
     PA[m * N + n] = P;
     PB[m * N + n] = Q;
   }
+  finish();
 }
 
 // Reverse carry over chunk aggregates: LamEnd[m] = lam_{(m+1)C}; lam <- Q + P*lam
@@ -499,21 +533,23 @@ static void launch_fwd_auto(const float* I, const float* starts, float* U, float
     launch_fwd<4>(I, starts, U, S, ends, N, Ls, M, beta, theta, u_r, st);
 }
 
-template <bool COMPOSE, bool DETACH, bool HAS_GU>
+template <bool COMPOSE, bool DETACH, bool HAS_GU, bool PS = false>
 static void launch_bwd3(const float* I, const float* u0, const float* U, const float* S,
                         const float* GS, const float* GU, const float* lam_end, float* Lam, float* PA,
                         float* PB, int64_t N, int64_t Ls, int64_t M, float beta, float theta,
-                        float u_r, float alpha, hipStream_t st) {
+                        float u_r, float alpha, hipStream_t st, double* partials = nullptr) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   if (M == 1 && !COMPOSE) {
     // one segment: the serial adjoint, latency-bound with few neurons -> 16 steps in flight
-    hipLaunchKernelGGL((k_lif_bwd<16, COMPOSE, DETACH, HAS_GU>), dim3((unsigned)NB), dim3(WAVE), 0, st,
-                       I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, N, Ls, NB, beta, theta, u_r, alpha);
+    hipLaunchKernelGGL((k_lif_bwd<16, COMPOSE, DETACH, HAS_GU, PS>), dim3((unsigned)NB), dim3(WAVE), 0,
+                       st, I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, partials, N, Ls, NB, beta, theta,
+                       u_r, alpha);
     return;
   }
   constexpr int D = 4;
-  hipLaunchKernelGGL((k_lif_bwd<D, COMPOSE, DETACH, HAS_GU>), dim3((unsigned)(M * NB)), dim3(WAVE), 0,
-                     st, I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, N, Ls, NB, beta, theta, u_r, alpha);
+  hipLaunchKernelGGL((k_lif_bwd<D, COMPOSE, DETACH, HAS_GU, PS>), dim3((unsigned)(M * NB)), dim3(WAVE),
+                     0, st, I, u0, U, S, GS, GU, lam_end, Lam, PA, PB, partials, N, Ls, NB, beta,
+                     theta, u_r, alpha);
 }
 
 template <bool COMPOSE>
@@ -815,6 +851,55 @@ extern "C" int lsh_lif_scan_bwd(const float* I, const float* u0, const float* U,
                      PB, LE, N, (int)M);
   launch_bwd<false>(I, u0, U, S, GS, GU, LE, Lam, nullptr, nullptr, N, C, M, beta, theta, u_r,
                     alpha, detach != 0, st);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" int64_t lsh_lif_param_partials(int64_t T, int64_t N, int mode, int C) {
+  if (T < 0 || N < 0 || mode < 0 || mode > 2) return -1;
+  const int64_t NB = (N + WAVE - 1) / WAVE;
+  if (mode != 1) return NB;
+  if (C < 1 || T % C != 0) return -1;
+  return (T / C) * NB;
+}
+
+extern "C" int lsh_lif_param_bwd(const float* I, const float* u0, const float* U, const float* S,
+                                 const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
+                                 float beta, float theta, float u_r, float alpha, int mode, int C,
+                                 void* ws, size_t ws_bytes, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(Lam) ||
+      bad_ptr(partials))
+    return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (mode < 0 || mode > 2) return LSH_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (mode == 0) {
+    if (T == 0 || N == 0) return LSH_OK;
+    launch_bwd3<false, true, false, true>(I, u0, U, S, GS, nullptr, nullptr, Lam, nullptr, nullptr, N,
+                                          T, 1, beta, theta, u_r, alpha, st, partials);
+    LSH_CHECK_LAUNCH();
+    return LSH_OK;
+  }
+  if (mode == 2) return lif_param_bwd_fused(I, u0, U, S, GS, Lam, partials, T, N, beta, theta, u_r,
+                                            alpha, C, st);
+  const int rc = bwd_check(T, N, C);
+  if (rc != LSH_OK) return rc;
+  if (bad_ptr(ws) || ws_bytes < lsh_lif_scan_bwd_workspace(T, N, C) ||
+      (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+    return LSH_ERR_WORKSPACE;
+  if (T == 0 || N == 0) return LSH_OK;
+  const int64_t M = T / C;
+  const size_t mn = align_up((size_t)M * (size_t)N * 4, 256);
+  char* w = static_cast<char*>(ws) + kWsHeaderBytes;
+  float* PA = reinterpret_cast<float*>(w);
+  float* PB = reinterpret_cast<float*>(w + mn);
+  float* LE = reinterpret_cast<float*>(w + 2 * mn);
+  launch_bwd3<true, true, false>(I, u0, U, S, GS, nullptr, nullptr, nullptr, PA, PB, N, C, M, beta,
+                                 theta, u_r, alpha, st);
+  hipLaunchKernelGGL(k_lif_bwd_carry, dim3((unsigned)((N + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, PA,
+                     PB, LE, N, (int)M);
+  launch_bwd3<false, true, false, true>(I, u0, U, S, GS, nullptr, LE, Lam, nullptr, nullptr, N, C, M,
+                                        beta, theta, u_r, alpha, st, partials);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }

@@ -59,4 +59,10 @@ __global__ void k_ws_header_reset(WsHeader* h);
 
 inline bool bad_ptr(const void* p) { return p == nullptr; }
 
+// Single-pass detached LIF adjoint with the fit.py parameter sums (lif_fused.hip); partials
+// gets one row of 3 doubles per 64-neuron block.  Returns an LSH_* status.
+int lif_param_bwd_fused(const float* I, const float* u0, const float* U, const float* S,
+                        const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
+                        float beta, float theta, float u_r, float alpha, int C, hipStream_t st);
+
 }  // namespace lsh

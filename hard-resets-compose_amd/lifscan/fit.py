@@ -1,0 +1,84 @@
+"""Differentiable hard-reset LIF with gradients w.r.t. the neuron parameters (beta, theta,
+u_r), the interface of the reference's ``lifscan/fit.py`` (LIFParamFn, lif_param):
+
+    dL/dbeta  = sum_t lambda_t u_{t-1}
+    dL/dtheta = -sum_t gS_t sigma'(v_t - theta)           (detached reset)
+    dL/du_r   = sum_t s_t beta lambda_{t+1}
+
+with lambda_t = dL/dv_t from the adjoint.  The three sums are accumulated in fp64 inside the
+adjoint kernel (lsh_lif_param_bwd), one row per block, so no [T, N] temporaries are formed.
+The reference's CPU prototype backend (LIFParamFnCPU) and the soft-reset layers are not part
+of this package.
+"""
+import torch
+
+from . import _native as _n
+from . import hip_lif as L
+from .hip_lif import _f32, _input, _vec, _same
+
+
+def _param_backward(I, u0, U, S, GS, beta, theta, u_r, alpha, mode):
+    """lsh_lif_param_bwd -> (Lam, sums [3] fp64)."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    U, S, GS = (_same(a, I, nm) for a, nm in ((U, "U"), (S, "S"), (GS, "GS")))
+    lib = _n.lib()
+    if mode == "scan":
+        if T % L.FUSED_BWD_C == 0:
+            code, C = 2, L.FUSED_BWD_C
+        else:
+            code, C = 1, min(128, L._pick_C(T, D=2))
+    else:
+        code, C = 0, 1
+    P = lib.lsh_lif_param_partials(T, N, code, C)
+    if P < 0:
+        raise ValueError(f"T={T} must be divisible by C={C}")
+    parts = torch.zeros(max(P, 1), 3, device=I.device, dtype=torch.float64)
+    Lam = torch.empty_like(I)
+    ws, nbytes = None, 0
+    if code == 1:
+        nbytes = lib.lsh_lif_scan_bwd_workspace(T, N, C)
+        ws = _n.workspace(nbytes, I.device)
+    with torch.cuda.device(I.device):
+        _n.check(lib.lsh_lif_param_bwd(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS), _n.ptr(Lam), _n.ptr(parts), T, N,
+            _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), code, C, _n.ptr(ws), nbytes,
+            _n.stream_of(I)), "lsh_lif_param_bwd")
+    return Lam, parts.sum(0)
+
+
+class LIFParamFn(torch.autograd.Function):
+    """S = LIF(I; u0, beta, theta, u_r) with gradients for I, u0 and the three parameters
+    (fit.py:15-48).  fwd_mode / bwd_mode: "serial" or "scan"."""
+
+    @staticmethod
+    def forward(ctx, I, u0, beta, theta, u_r, alpha, fwd_mode, bwd_mode, K):
+        b, th, ur = _f32(beta), _f32(theta), _f32(u_r)
+        I = I.contiguous()
+        if fwd_mode == "scan":
+            U, S = L.scan_forward_auto(I, b, th, ur, u0, K=K)
+        else:
+            U, S = L.serial_forward_auto(I, b, th, ur, u0)
+        ctx.save_for_backward(I, u0, U, S)
+        ctx.cfg = (b, th, ur, float(alpha), bwd_mode)
+        return S
+
+    @staticmethod
+    def backward(ctx, gS):
+        I, u0, U, S = ctx.saved_tensors
+        b, th, ur, alpha, bwd_mode = ctx.cfg
+        lam, sums = _param_backward(I, u0, U, S, gS.contiguous(), b, th, ur, alpha, bwd_mode)
+        sums = sums.float()
+        return (lam, b * lam[0], sums[0], -sums[1], b * sums[2], None, None, None, None)
+
+
+def lif_param(I, u0, beta, theta, u_r, alpha=4.0, mode="auto", K=16):
+    """fit.py:51-57: mode "auto" picks serial / scan per pass from (N, T)."""
+    T, N = I.shape
+    if mode == "auto":
+        fwd, bwd = L.auto_modes(N, T)
+    else:
+        fwd = bwd = mode
+    t = lambda v: v if torch.is_tensor(v) else torch.tensor(float(v), device=I.device)
+    return LIFParamFn.apply(I, u0, t(beta), t(theta), t(u_r), alpha, fwd, bwd, K)

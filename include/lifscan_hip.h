@@ -209,6 +209,18 @@ int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w0, const fl
 /* phase_events: NULL or 5 hipEvent_t recorded on `stream` at the start and after the
  * envelope + box, the build, the carry and the first replay (the reference's `phases`). */
 
+/* LIF adjoint with the neuron-parameter gradients of fit.py LIFParamFn.backward
+ * (fit.py:30-48): Lam as lsh_lif_*_bwd with the reset detached and no GU, plus per block
+ * partials[P][3] (fp64) = (sum lam_t*u_{t-1}, sum gs_t*sg_t, sum s_t*lam_{t+1}), whose column
+ * sums give dbeta, -dtheta and dL/du_r / beta.  mode 0: serial; 1: chunked scan of chunk C
+ * (workspace lsh_lif_scan_bwd_workspace(T, N, C)); 2: single pass, C in {16, 32, 64}.
+ * P = lsh_lif_param_partials(T, N, mode, C). */
+int64_t lsh_lif_param_partials(int64_t T, int64_t N, int mode, int C);
+int lsh_lif_param_bwd(const float* I, const float* u0, const float* U, const float* S,
+                      const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
+                      float beta, float theta, float u_r, float alpha, int mode, int C, void* ws,
+                      size_t ws_bytes, void* stream);
+
 /* ALIF adjoint: LW[t] = dL/dw_t, LV[t] = dL/dv_t (= dL/dI_t) for dL/dS = GS.
  * mode 0: fused serial sweep (triton_alif.py:444-487); 1: chunked two-level affine scans of
  * chunk C (triton_alif.py:510-521, needs lsh_alif_bwd_workspace(T, N, C) bytes); 2: single

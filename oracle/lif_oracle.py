@@ -83,6 +83,22 @@ def serial_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=Tru
     return Lam
 
 
+def param_grads(I, u0, U, S, GS, Lam, beta, theta, u_r, alpha=4.0):
+    """LIFParamFn.backward assembly (fit.py:36-48), fp64, detached reset:
+    (dI, du0, dbeta, dtheta, du_r) = (Lam, beta*Lam[0], sum Lam_t u_{t-1},
+    -sum gs_t sg(v_t - theta), sum s_t beta Lam_{t+1})."""
+    dt = np.float64
+    T, N = I.shape
+    Lam = np.asarray(Lam, dt)
+    Uprev = np.concatenate([np.asarray(u0, f32).reshape(1, N), U[:-1]], 0).astype(dt)
+    v = dt(beta) * Uprev + np.asarray(I, dt)
+    sig = 1.0 / (1.0 + np.exp(-(dt(alpha) * (v - dt(theta)))))
+    sg = dt(alpha) * sig * (1.0 - sig)
+    lam_next = np.concatenate([Lam[1:], np.zeros((1, N), dt)], 0)
+    return (Lam, dt(beta) * Lam[0], float((Lam * Uprev).sum()), float(-(np.asarray(GS, dt) * sg).sum()),
+            float((np.asarray(S, dt) * dt(beta) * lam_next).sum()))
+
+
 # ----------------------------------------------------------------------------- two-level scan
 def envelope_chunks(I, beta, u_r, C):
     """Per-chunk min-affine envelope map (c, a, b) (triton_lif.py:699-719)."""

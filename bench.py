@@ -14,7 +14,10 @@ reference's chunking (C = 128, K = 8), the roofline of the dominant kernel (HIP 
 stream it runs on) and the CPU baseline (PyTorch-CPU port of the reference's fast.py on a
 bounded sample, timed on this host).
 
-  python bench.py [--steps K] [--warmup W] [--no-cpu]
+The other BASELINE configurations (cfg3 network step, cfg4 long sequence, cfg5 ALIF) are
+measured after the headline and reported under "other_configs" (--headline-only skips them).
+
+  python bench.py [--steps K] [--warmup W] [--no-cpu] [--headline-only]
   python bench.py --dominant-only    # short run for rocprofv3 --pmc passes (copy + kernel)
 """
 import argparse
@@ -113,6 +116,141 @@ def cpu_baseline(I_cpu, beta, n_cols):
     return out
 
 
+def bench_cfg3(torch, dev, reps):
+    """cfg3: the 700-256-256-20 network, batch 64, T=1024, Bernoulli(0.015)
+    raster, beta=0.95, cross-entropy on random labels; one step = zero_grad + forward + loss +
+    backward (the reference's e7c_timing.py step).  Also the two LIF layers alone (fwd+bwd on
+    their [1024, 16384] currents, HIP events)."""
+    import torch.nn as nn
+    from lifscan.shdnet import Net
+    from lifscan import hip_lif as L
+    T, B = 1024, 64
+    g = torch.Generator().manual_seed(3)
+    x = (torch.rand(B, T, 700, generator=g) < 0.015).float().transpose(0, 1).contiguous().to(dev)
+    y = torch.randint(0, 20, (B,), generator=torch.Generator().manual_seed(5)).to(dev)
+    out = {}
+    for mode in ("scan", "serial", "auto"):
+        torch.manual_seed(4)
+        net = Net(mode).to(dev)
+
+        def step():
+            net.zero_grad()
+            logits, _ = net(x)
+            nn.functional.cross_entropy(logits, y).backward()
+        out[f"step_ms_{mode}"] = ev_time(step, reps, warm=3)
+    torch.manual_seed(4)
+    net = Net("scan").to(dev)
+    with torch.no_grad():
+        I1 = net.l1.fc(x).reshape(T, -1).contiguous()
+        s1 = L.lif_tuned(I1, torch.zeros(I1.shape[1], device=dev), beta=0.95, mode="scan", K=16,
+                         repair=10 ** 6).reshape(T, B, -1)
+        I2 = net.l2.fc(s1).reshape(T, -1).contiguous()
+    g2 = torch.randn(T, I1.shape[1], generator=torch.Generator().manual_seed(6)).to(dev)
+
+    def layers():
+        for I in (I1, I2):
+            Ig = I.detach().requires_grad_(True)
+            S = L.lif_tuned(Ig, torch.zeros(I.shape[1], device=dev), beta=0.95, mode="scan", K=16,
+                            repair=10 ** 6)
+            S.backward(g2)
+    out["lif_layers_fwd_bwd_ms"] = ev_time(layers, reps, warm=2)
+    nsteps = 2 * T * I1.shape[1]
+    out["lif_layers_pct_roofline"] = round(
+        100 * (B_FWD + B_BWD) * nsteps / (out["lif_layers_fwd_bwd_ms"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
+    out["config"] = "700-256-256-20, B=64, T=1024, beta=0.95, lif_tuned(scan, K=16, repair on)"
+    return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out.items()}
+
+
+def bench_cfg4(torch, dev, reps):
+    """cfg4: N=1024, T=2^20, beta=0.99, x~N(0.012,0.08^2), u0~U[0,1).
+    Exact single-pass forward, two-level scan_forward_v3 (C=512, K=32, repair on), three-level
+    scan_forward_v4 (C=64, G=16, K=16, K2=32, repair on, overflow statistics), serial forward,
+    and the affine-scan / serial backward; fwd+bwd = the faster exact forward + scan backward."""
+    from lifscan import hip_lif as L
+    T, N, beta = 2 ** 20, 1024, 0.99
+    I = (0.012 + 0.08 * torch.randn(T, N, generator=torch.Generator().manual_seed(0))).to(dev)
+    u0 = torch.rand(N, generator=torch.Generator().manual_seed(2)).to(dev)
+    gS = torch.randn(T, N, generator=torch.Generator().manual_seed(1)).to(dev)
+    out = {}
+    U, S = L.serial_forward(I, beta, 1.0, 0.0, u0)
+    U2, S2 = L.scan_forward_exact(I, beta, 1.0, 0.0, u0, K=8, maps=False)
+    out["exact_equals_serial"] = bool(torch.equal(U2, U) and torch.equal(S2, S))
+    del U2, S2
+    out["fwd_exact_ms"] = ev_time(lambda: L.scan_forward_exact(I, beta, 1.0, 0.0, u0, K=8, maps=False), reps)
+    out["fwd_serial_ms"] = ev_time(lambda: L.serial_forward(I, beta, 1.0, 0.0, u0), reps)
+    st3 = {}
+    U3, S3 = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=512, K=32, repair=10 ** 6, stats=st3)
+    out["v3_C512_K32_equals_serial"] = bool(torch.equal(U3, U) and torch.equal(S3, S))
+    del U3, S3
+    out["fwd_v3_C512_K32_ms"] = ev_time(lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=512, K=32,
+                                                                  repair=10 ** 6), 3)
+    out["v3_stats"] = st3
+    st = {}
+    U4, S4 = L.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=64, G=16, K=16, K2=32, repair=10 ** 6, stats=st)
+    out["v4_equals_serial"] = bool(torch.equal(U4, U) and torch.equal(S4, S))
+    del U4, S4
+    out["fwd_v4_ms"] = ev_time(lambda: L.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=64, G=16, K=16, K2=32,
+                                                         repair=10 ** 6), 2, warm=0)
+    out["v4_stats"] = st
+    out["bwd_scan_ms"] = ev_time(lambda: L.scan_backward_tiled(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), reps)
+    out["bwd_serial_ms"] = ev_time(lambda: L.serial_backward(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), 2)
+    ns = T * N
+    t_fb = min(out["fwd_exact_ms"], out["fwd_v3_C512_K32_ms"]) + out["bwd_scan_ms"]
+    out["fwd_bwd_ms"] = t_fb
+    out["fwd_bwd_value"] = round(ns / (t_fb / 1000.0), 1)
+    out["pct_roofline_fwd_bwd"] = round(100 * (B_FWD + B_BWD) * ns / (t_fb / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
+    out["config"] = "N=1024, T=1048576, beta=0.99, x~N(0.012,0.08^2), u0~U[0,1)"
+    del I, U, S, gS
+    torch.cuda.empty_cache()
+    return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out.items()}
+
+
+def bench_cfg5(torch, dev, reps):
+    """cfg5: ALIF, N=16384, T=4096, beta=0.95, rho=0.995, q=0.2,
+    theta0=1, u_r=0, x~N(0.15,0.3^2), u0=w0=0.  alif() fwd+bwd with the parameter gradients:
+    serial forward + scan adjoint, and the box scan (Wpred from alif_warm_predict(Wn=4), its
+    cost included, dw=0.1q, C=128, K1=K2=32) + scan adjoint; plus the exact box scan with repair
+    (statistics) and the serial forward."""
+    from lifscan import triton_alif as A
+    T, N, beta, rho, q, C = 4096, 16384, 0.95, 0.995, 0.2, 128
+    I = (0.15 + 0.3 * torch.randn(T, N, generator=torch.Generator().manual_seed(0))).to(dev)
+    gS = torch.randn(T, N, generator=torch.Generator().manual_seed(1)).to(dev)
+    z = torch.zeros(N, device=dev)
+    ps = [torch.tensor(v, device=dev, requires_grad=True) for v in (beta, rho, q, 1.0)]
+    Ig = I.clone().requires_grad_(True)
+    out = {}
+    for fwd in ("serial", "scan"):
+        def step():
+            Ig.grad = None
+            for p in ps:
+                p.grad = None
+            Wp = A.alif_warm_predict(I, beta, rho, q, 1.0, 0.0, z, z, C, Wn=4) if fwd == "scan" else None
+            S, _, _ = A.alif(Ig, z, z, *ps, fwd=fwd, bwd="scan", Wpred=Wp, dw=0.1 * q, C=C)
+            S.backward(gS)
+        out[f"alif_fwd_{fwd}_bwd_scan_ms"] = ev_time(step, reps, warm=2)
+    out["serial_fwd_ms"] = ev_time(lambda: A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z), reps)
+    U, W, S = A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z)
+    WP = A.alif_warm_predict(I, beta, rho, q, 1.0, 0.0, z, z, C, Wn=4)
+    st, ph = {}, {}
+    U2, W2, S2 = A.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, WP, 0.1 * q, C=C, K1=32, K2=32, BN=4,
+                                     repair=10 ** 6, stats=st, phases=ph)
+    out["box_scan_repair_equals_serial"] = bool(torch.equal(U2, U) and torch.equal(W2, W) and torch.equal(S2, S))
+    out["box_scan_repair_ms"] = ev_time(lambda: A.alif_scan_forward(
+        I, beta, rho, q, 1.0, 0.0, z, z, WP, 0.1 * q, C=C, K1=32, K2=32, BN=4, repair=10 ** 6), 3)
+    out["box_scan_stats"] = st
+    out["box_scan_phases_ms"] = {k: round(v, 4) for k, v in ph.items()}
+    out["bwd_scan_ms"] = ev_time(lambda: A.alif_backward(I, U, W, S, gS, beta, rho, q, 1.0, z, z), reps)
+    ns = T * N
+    t = out["alif_fwd_serial_bwd_scan_ms"]
+    out["fwd_bwd_value"] = round(ns / (t / 1000.0), 1)
+    # ALIF algorithmic bytes: fwd read I, write U, W, S (16); bwd read I, U, W, S, gS, write dI (24)
+    out["pct_roofline_fwd_bwd"] = round(100 * 40 * ns / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
+    out["config"] = "ALIF N=16384, T=4096, beta=0.95, rho=0.995, q=0.2, x~N(0.15,0.3^2)"
+    del I, gS, U, W, S, U2, W2, S2, Ig
+    torch.cuda.empty_cache()
+    return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out.items()}
+
+
 def dominant_only(L, torch, dev):
     """Short program for counter passes: a 256 MiB copy (FETCH/WRITE calibration), then the
     dominant kernel (single-pass backward, cfg2) three times."""
@@ -139,6 +277,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-cols", type=int, default=8192)
     ap.add_argument("--dominant-only", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="skip the cfg3 / cfg4 / cfg5 measurements")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the exact LIF scan shards along neurons with no "
@@ -218,6 +358,16 @@ def main():
                 "kernel": "k_lif_bwd_fused (single-pass affine-scan adjoint, C=32, W=4)",
                 "algorithmic_bytes_per_launch": B_BWD * N * T, "avg_launch_ms": round(t_dom, 4)}
 
+    others = None
+    if not args.headline_only:
+        del I
+        torch.cuda.empty_cache()
+        others = {}
+        for name, fn in (("cfg3", bench_cfg3), ("cfg5", bench_cfg5), ("cfg4", bench_cfg4)):
+            log(f"{name}")
+            others[name] = fn(torch, dev, 5)
+            log(f"{name} " + json.dumps(others[name]))
+
     cpu = None
     if not args.no_cpu:
         log(f"cpu baseline on {args.cpu_cols} neurons x T={T}")
@@ -257,6 +407,7 @@ def main():
         "stats_C128_K8": {"beta0.9": st, "beta0.99": st99},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "other_configs": others,
     }
     print(json.dumps(out))
 

@@ -416,11 +416,10 @@ __global__ __launch_bounds__(64) void k_alif_carry(
     if (valid_n && i == 0) MISS[o] = bad ? 1 : 0;
     if (bad) {
       float uu = u, ww = w;
-      const float* __restrict__ Ip = I + (size_t)m * C * N + nn;
-      for (int j = 0; j < C; ++j) {
+      stream_rows<16>(I + (size_t)m * C * N + nn, (size_t)N, C, [&](int64_t, float x) {
         bool s;
-        uu = alif_step(uu, ww, Ip[(size_t)j * N], beta, rho, q, theta0, u_r, s);
-      }
+        uu = alif_step(uu, ww, x, beta, rho, q, theta0, u_r, s);
+      });
       nu = uu;
       nw = ww;
     }
@@ -496,13 +495,13 @@ __global__ __launch_bounds__(256) void k_alif_repair(
       const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
       float u = su[(size_t)m * N + n], w = sw[(size_t)m * N + n];
       const size_t base = (size_t)m * C * N + n;
-      for (int j = 0; j < C; ++j) {
+      stream_rows<16>(I + base, (size_t)N, C, [&](int64_t j, float x) {
         bool s;
-        u = alif_step(u, w, I[base + (size_t)j * N], beta, rho, q, theta0, u_r, s);
+        u = alif_step(u, w, x, beta, rho, q, theta0, u_r, s);
         U[base + (size_t)j * N] = u;
         W[base + (size_t)j * N] = w;
         S[base + (size_t)j * N] = s ? 1.0f : 0.0f;
-      }
+      });
       const size_t oe = (size_t)m * N + n;
       if (u != eu[oe] || w != ew[oe]) {
         eu[oe] = u;

@@ -68,17 +68,29 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_fwd_fused(const float* __restri
   unsigned long long fixups = 0, unknown = 0;
   unsigned int timeouts = 0;
   const int rounds = (M + W - 1) / W;
+  const unsigned rstride = (unsigned)(N * 4);  // bytes per time row (C*N*4 < 2^31 checked on host)
+  // Without speculation the round's inputs are loaded one round ahead (xn), so the loads of
+  // round r+1 are in flight during round r's hand-off chain (barriers wait on LDS only).
+  float x[C], xn[SPEC ? 1 : C];
+  if (!SPEC && w < M) {
+    const Buf bi(Ib + (size_t)w * C * N);
+#pragma unroll
+    for (int j = 0; j < C; ++j) x[j] = bi.ld(lb, j * rstride);
+  }
   for (int r = 0; r < rounds; ++r) {
     const int m = r * W + w;
     const bool active = m < M;  // wave-uniform
     const size_t row0 = (size_t)m * C;
-    const unsigned rstride = (unsigned)(N * 4);  // bytes per time row (C*N*4 < 2^31 checked on host)
-    float x[C];
-    if (active) {
-      const Buf bi(Ib + row0 * N);
+    if (!SPEC && m + W < M) {
+      const Buf bn(Ib + (row0 + (size_t)W * C) * N);
 #pragma unroll
-      for (int j = 0; j < C; ++j) x[j] = bi.ld(lb, j * rstride);
+      for (int j = 0; j < C; ++j) xn[j] = bn.ld(lb, j * rstride);
+    }
+    if (active) {
       if (SPEC) {
+        const Buf bi(Ib + row0 * N);
+#pragma unroll
+        for (int j = 0; j < C; ++j) x[j] = bi.ld(lb, j * rstride);
         MapBuilder<KMAX> mb;
         mb.init();
 #pragma unroll
@@ -165,6 +177,10 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_fwd_fused(const float* __restri
     const int last = min(W, M - r * W) - 1;
     if (w == last) sStart[lane] = e;
     __syncthreads();
+    if (!SPEC && m + W < M) {
+#pragma unroll
+      for (int j = 0; j < C; ++j) x[j] = xn[j];
+    }
   }
   fixups = wave_sum_u64(fixups);
   unknown = wave_sum_u64(unknown);

@@ -411,11 +411,10 @@ __global__ __launch_bounds__(64) void k_lif_carry(
       float nu = (k == ne) ? __fadd_rn(__fmul_rn(MA[o], u), MB[o]) : cval;
       if (ovf) {  // rare: serial fallback through this chunk
         float w = u;
-        const float* __restrict__ Ip = I + (size_t)m * C * N + n;
-        for (int j = 0; j < C; ++j) {
+        stream_rows<16>(I + (size_t)m * C * N + n, (size_t)N, C, [&](int64_t, float x) {
           bool s;
-          w = lif_step(w, Ip[(size_t)j * N], beta, theta, u_r, s);
-        }
+          w = lif_step(w, x, beta, theta, u_r, s);
+        });
         nu = w;
       }
       u = nu;
@@ -486,12 +485,12 @@ __global__ __launch_bounds__(256) void k_lif_repair(const float* __restrict__ I,
       const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
       float u = starts[(size_t)m * N + n];
       const size_t base = (size_t)m * C * N + n;
-      for (int j = 0; j < C; ++j) {
+      stream_rows<16>(I + base, (size_t)N, C, [&](int64_t j, float x) {
         bool s;
-        u = lif_step(u, I[base + (size_t)j * N], beta, theta, u_r, s);
+        u = lif_step(u, x, beta, theta, u_r, s);
         U[base + (size_t)j * N] = u;
         S[base + (size_t)j * N] = s ? 1.0f : 0.0f;
-      }
+      });
       const size_t oe = (size_t)m * N + n;
       if (u != ends[oe]) {
         ends[oe] = u;

@@ -35,11 +35,10 @@ __device__ __forceinline__ float eval_slots(const float* xd, const float* cd, in
 __device__ __forceinline__ float serial_rows(const float* __restrict__ I, int64_t N, int64_t n,
                                              int64_t r0, int64_t L, float u, float beta,
                                              float theta, float u_r) {
-  const float* __restrict__ Ip = I + (size_t)r0 * N + n;
-  for (int64_t j = 0; j < L; ++j) {
+  stream_rows<16>(I + (size_t)r0 * N + n, (size_t)N, L, [&](int64_t, float x) {
     bool s;
-    u = lif_step(u, Ip[(size_t)j * N], beta, theta, u_r, s);
-  }
+    u = lif_step(u, x, beta, theta, u_r, s);
+  });
   return u;
 }
 

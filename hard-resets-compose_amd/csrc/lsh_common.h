@@ -86,6 +86,35 @@ struct Buf {
 };
 
 // Wave-level reductions (wave64).
+// f(j, p[j*stride]) for j = 0..n-1 in order, loading the rows in tiles of D with the next
+// tile's loads issued before the current tile is consumed (serial fallbacks and repairs run
+// one dependent chain per lane; without this every step waits for its own load).
+template <int D, class F>
+__device__ __forceinline__ void stream_rows(const float* __restrict__ p, size_t stride, int64_t n,
+                                            F&& f) {
+  const int64_t nt = n / D;
+  float a[D];
+  if (nt > 0) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) a[k] = p[(size_t)k * stride];
+  }
+  for (int64_t t = 0; t < nt; ++t) {
+    float b[D];
+    const bool more = t + 1 < nt;
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) b[k] = p[(size_t)((t + 1) * D + k) * stride];
+    }
+#pragma unroll
+    for (int k = 0; k < D; ++k) f(t * D + k, a[k]);
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) a[k] = b[k];
+    }
+  }
+  for (int64_t j = nt * D; j < n; ++j) f(j, p[(size_t)j * stride]);
+}
+
 __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, WAVE));

@@ -25,10 +25,10 @@ def _param_backward(I, u0, U, S, GS, beta, theta, u_r, alpha, mode):
     U, S, GS = (_same(a, I, nm) for a, nm in ((U, "U"), (S, "S"), (GS, "GS")))
     lib = _n.lib()
     if mode == "scan":
-        if T % L.FUSED_BWD_C == 0:
+        if N >= L.FUSED_BWD_MIN_N and T % L.FUSED_BWD_C == 0:
             code, C = 2, L.FUSED_BWD_C
         else:
-            code, C = 1, min(128, L._pick_C(T, D=2))
+            code, C = 1, L.chunked_bwd_C(T, N, min(128, L._pick_C(T, D=2)))
     else:
         code, C = 0, 1
     P = lib.lsh_lif_param_partials(T, N, code, C)

@@ -15,7 +15,7 @@ import math
 import torch
 
 from . import _native as _n
-from .hip_lif import _f32, _input, _vec, _same
+from .hip_lif import _f32, _input, _vec, _same, chunked_bwd_C
 
 # single-pass backward (one workgroup per 64 neurons) pays off only with many neuron blocks
 ALIF_FUSED_BWD_MIN_N = 8192
@@ -164,8 +164,7 @@ def _bwd_mode(mode, T, N, C):
     if mode == "scan":
         fused = N >= ALIF_FUSED_BWD_MIN_N and T % ALIF_FUSED_BWD_C == 0
         mode = "fused" if fused else "chunked"
-        if fused:
-            C = ALIF_FUSED_BWD_C
+        C = ALIF_FUSED_BWD_C if fused else chunked_bwd_C(T, N, C)
     if mode in ("serial_pf", "serial_tuned", "serial"):
         return 0, C
     if mode == "fused":  # single pass, C in {16, 32}

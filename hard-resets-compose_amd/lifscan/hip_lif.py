@@ -440,15 +440,35 @@ def scan_backward_fused(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach
 
 
 # ----------------------------------------------------------------------------- scan backward
+# The single-pass adjoint owns 64 neurons per workgroup: with fewer than this many neurons the
+# chip is not filled and the three-kernel chunk scan (parallel over chunks x neurons) wins.
+FUSED_BWD_MIN_N = 8192
+CHUNKED_BWD_MIN_BLOCKS = 2048  # chunk x 64-neuron blocks that keep every CU busy
+
+
+def chunked_bwd_C(T, N, C=64):
+    """Chunk of the three-kernel adjoint: the longest of 512..8 dividing T that still gives
+    CHUNKED_BWD_MIN_BLOCKS blocks (fewer, longer chunks cut the carry and aggregate traffic),
+    else the given C."""
+    nb = (N + 63) // 64
+    for c in (512, 256, 128, 64, 32, 16, 8):
+        if T % c == 0 and (T // c) * nb >= CHUNKED_BWD_MIN_BLOCKS:
+            return c
+    return int(C)
+
+
 def scan_backward_tiled(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=64,
                         BNr=32, D=4, nwr=1):
     """Affine-scan adjoint (triton_lif.py:512-526) -> Lam.  GU may be None (zeros).
-    Runs the single-pass kernel when T is a multiple of its internal chunk, else the
-    three-kernel chunk scan with chunk C."""
+    Runs the single-pass kernel when there are enough neurons to fill the chip and T is a
+    multiple of its internal chunk, else the three-kernel chunk scan (chunk from
+    chunked_bwd_C; the given C when none fits)."""
     I = _input(I)
-    if I.shape[0] % FUSED_BWD_C == 0 and int(C) >= 1 and I.shape[0] % int(C) == 0:
+    T, N = I.shape
+    if N >= FUSED_BWD_MIN_N and T % FUSED_BWD_C == 0:
         return scan_backward_fused(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach)
-    return scan_backward_chunked(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach, C)
+    return scan_backward_chunked(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach,
+                                 chunked_bwd_C(T, N, C))
 
 
 def scan_backward_chunked(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=64):

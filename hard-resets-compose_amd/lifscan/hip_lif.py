@@ -359,9 +359,11 @@ def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=
 FUSED_FWD_C = 32
 FUSED_BWD_C = 32
 FUSED_CHUNKS = (16, 32, 64, 128)
-# Map speculation shortens the in-workgroup hand-off chain; it pays when few neuron blocks
-# run (the chain latency is exposed), and costs VALU time otherwise (many blocks hide it).
-FUSED_MAPS_MAX_N = 8192
+# Map speculation shortens the in-workgroup hand-off chain but puts the map build on every
+# round's critical path; measured on MI355X it never beat the plain chain (at large N the
+# chain is hidden by other workgroups, at small N the build costs more than it saves), so
+# maps="auto" leaves it off.  maps=True still selects it.
+FUSED_MAPS_MAX_N = 0
 
 _LAST_FUSED = None
 

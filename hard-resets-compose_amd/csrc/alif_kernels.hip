@@ -998,9 +998,9 @@ extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w
                      F(L.EA), F(L.EB), N, NB, C, beta, u_r);
   hipLaunchKernelGGL(k_env_carry, dim3((unsigned)NB), dim3(WAVE), 0, st, u0, F(L.EC), F(L.EA),
                      F(L.EB), F(L.LU), N, M);
+  mark(1);  // the entry box belongs to the build phase, as in the reference (triton_alif.py:314-329)
   hipLaunchKernelGGL(k_alif_box, dim3((unsigned)((int64_t)M * NB)), dim3(WAVE), 0, st, Wpred, w0,
                      F(L.LW), F(L.HW), F(L.HU), N, NB, dw, rho, theta0, u_r);
-  mark(1);
   switch (block) {
     case 1: launch_alif_build<1>(I, w, L, N, M, C, K1, K2, beta, rho, q, theta0, u_r, st); break;
     case 2: launch_alif_build<2>(I, w, L, N, M, C, K1, K2, beta, rho, q, theta0, u_r, st); break;

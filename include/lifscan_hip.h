@@ -207,7 +207,8 @@ int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w0, const fl
                       int K2, int block, int64_t repair, void* ws, size_t ws_bytes,
                       void* const* phase_events, void* stream);
 /* phase_events: NULL or 5 hipEvent_t recorded on `stream` at the start and after the
- * envelope + box, the build, the carry and the first replay (the reference's `phases`). */
+ * envelope, the entry box + build, the carry and the first replay (the reference's `phases`,
+ * triton_alif.py:305-341). */
 
 /* LIF adjoint with the neuron-parameter gradients of fit.py LIFParamFn.backward
  * (fit.py:30-48): Lam as lsh_lif_*_bwd with the reset detached and no GU, plus per block

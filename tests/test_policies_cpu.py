@@ -1,0 +1,22 @@
+"""CPU: the MI355X dispatch policies (no GPU needed): auto_modes thresholds, the chunk of the
+three-kernel adjoint, and the reference's chunk policy kept verbatim."""
+import pytest
+
+
+def test_auto_modes_follow_mi355x_measurements():
+    from lifscan import hip_lif as L
+    assert L.auto_modes(1024, 65536) == ("scan", "scan")
+    assert L.auto_modes(4096, 65536) == ("serial", "scan")
+    assert L.auto_modes(65536, 4096) == ("serial", "scan")
+    assert L.auto_modes(1024, 4096) == ("serial", "scan")
+    assert L.auto_modes(65536, 128) == ("serial", "serial")
+
+
+def test_chunked_bwd_chunk_choice():
+    from lifscan import hip_lif as L
+    assert L.chunked_bwd_C(2 ** 20, 1024) == 512        # 2048 chunks x 16 blocks
+    assert L.chunked_bwd_C(65536, 1024) == 512          # 128 x 16 = 2048
+    assert L.chunked_bwd_C(16384, 4096) == 512          # 32 chunks x 64 blocks = 2048
+    assert L.chunked_bwd_C(1000, 64, C=8) == 8          # nothing gives 2048 blocks: the given C
+    with pytest.raises(ValueError):
+        L._pick_C(1001, D=2)

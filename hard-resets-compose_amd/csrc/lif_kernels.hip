@@ -276,12 +276,20 @@ __global__ __launch_bounds__(64) void k_lif_build(
     ec = fminf(u_r, lif_v(ec, x, beta));
     ea = beta * ea;
     eb = lif_v(eb, x, beta);
-    // (b) existing constants pushed through the step (same arithmetic as the serial step)
+    // (b) existing constants pushed through the step (same arithmetic as the serial step).
+    // wcnt is the same on every lane (it grows through a ballot): slots go in groups of 8
+    // behind one scalar branch per group, with no per-slot masks; a slot above a lane's cnt
+    // holds no breakpoint yet and is overwritten when one is added, so updating it is harmless.
+    const int wc = __builtin_amdgcn_readfirstlane(wcnt);
+    constexpr int G = KMAX < 8 ? KMAX : 8;
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-      if (i < wcnt) {
-        const float v = lif_v(cd[i], x, beta);
-        cd[i] = v >= theta ? u_r : v;
+    for (int g = 0; g < KMAX; g += G) {
+      if (g < wc) {
+#pragma unroll
+        for (int i = g; i < g + G; ++i) {
+          const float v = lif_v(cd[i], x, beta);
+          cd[i] = v >= theta ? u_r : v;
+        }
       }
     }
     // preimage of the threshold under the affine part: beta*(A*u + B) + x >= theta
@@ -291,15 +299,15 @@ __global__ __launch_bounds__(64) void k_lif_build(
     bool nw = (z < xmin) && (z <= hi);
     if (nw && cnt >= K) ovf = true;
     nw = nw && (cnt < K);
+    if (__ballot(nw) != 0ull) {  // few steps add a breakpoint anywhere in the wave
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-      if (i <= wcnt && i < KMAX) {
+      for (int i = 0; i < KMAX; ++i) {
         const bool put = nw && (i == cnt);
         xd[i] = put ? z : xd[i];
         cd[i] = put ? u_r : cd[i];
       }
+      if (__ballot(nw && cnt == wc) != 0ull) ++wcnt;
     }
-    if (__ballot(nw && cnt == wcnt) != 0ull) ++wcnt;
     cnt += nw ? 1 : 0;
     xmin = nw ? z : xmin;
     A = beta * A;
@@ -430,6 +438,147 @@ __global__ __launch_bounds__(64) void k_lif_carry(
     atomicAdd(&hdr->ovf_count, ovf_acc);
     atomicAdd(&hdr->pieces_sum, pcs_acc);
     atomicMax(&hdr->pieces_max, (unsigned int)pmax);
+  }
+}
+
+// The same carry with its map reads staged through LDS, for long chunk sequences (many M, few
+// neurons), where the one-wave carry above waits a full memory latency per chunk.  A workgroup
+// of 4 waves owns 64 neurons: waves 1-3 load the next R chunks' maps (7 + 2K rows of 64 lanes
+// each) into one LDS buffer while wave 0 runs the sequential carry over the R chunks already
+// in the other buffer; one barrier per stage.  Results are the same as k_lif_carry's.
+template <int KMAX>
+struct CarryStage {
+  static constexpr int ROWS = 7 + 2 * KMAX;                 // EC EA EB MA MB CNT OVFRAW, MX[K], MC[K]
+  static constexpr int R = (64 * 1024) / (ROWS * WAVE * 4);  // chunks per stage (<= 64 KB per buffer)
+};
+
+template <int KMAX>
+__global__ __launch_bounds__(256) void k_lif_carry_staged(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ EC,
+    const float* __restrict__ EA, const float* __restrict__ EB, const float* __restrict__ MA,
+    const float* __restrict__ MB, const int* __restrict__ CNT, const int* __restrict__ OVFRAW,
+    const float* __restrict__ MX, const float* __restrict__ MC,
+    const float* __restrict__ lo_neuron, float* __restrict__ LO, int* __restrict__ MN,
+    int* __restrict__ OVF, float* __restrict__ starts, WsHeader* hdr, int64_t N, int M, int C,
+    int K, float beta, float theta, float u_r) {
+  using CS = CarryStage<KMAX>;
+  constexpr int ROWS = CS::ROWS, R = CS::R;
+  __shared__ float sbuf[2][R * ROWS][WAVE];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const int lane = threadIdx.x % WAVE;
+  const int64_t n = (int64_t)blockIdx.x * WAVE + lane;
+  const bool valid = n < N;
+  const int64_t nn = valid ? n : N - 1;
+  const int stages = (M + R - 1) / R;
+  // stage s into buffer s & 1 by the loader waves 1-3, one whole chunk per wave at a time:
+  // every row index is a compile-time constant, all loads issued before the LDS writes
+  auto load_stage = [&](int s) {
+    const int m0 = s * R;
+    const int nch = min(R, M - m0);
+    for (int c = w - 1; c < nch; c += 3) {
+      const size_t o = (size_t)(m0 + c) * N + nn;
+      const size_t os = (size_t)(m0 + c) * K * N + nn;
+      float v[ROWS];
+      v[0] = EC[o];
+      v[1] = EA[o];
+      v[2] = EB[o];
+      v[3] = MA[o];
+      v[4] = MB[o];
+      v[5] = __int_as_float(CNT[o]);
+      v[6] = __int_as_float(OVFRAW[o]);
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i) {
+        if (i < K) {
+          v[7 + i] = MX[os + (size_t)i * N];
+          v[7 + KMAX + i] = MC[os + (size_t)i * N];
+        }
+      }
+      float* dst = &sbuf[s & 1][c * ROWS][0];
+#pragma unroll
+      for (int r = 0; r < 7; ++r) dst[r * WAVE + lane] = v[r];
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i) {
+        if (i < K) {
+          dst[(7 + i) * WAVE + lane] = v[7 + i];
+          dst[(7 + KMAX + i) * WAVE + lane] = v[7 + KMAX + i];
+        }
+      }
+    }
+  };
+  if (w >= 1) load_stage(0);
+  __syncthreads();
+
+  unsigned long long ovf_acc = 0, pcs_acc = 0;
+  int pmax = 0;
+  const float margin = 1e-5f;
+  float l = u0[nn];
+  float u = l;
+  for (int s = 0; s < stages; ++s) {
+    if (w >= 1) {
+      if (s + 1 < stages) load_stage(s + 1);
+    } else {
+      const int m0 = s * R;
+      const int nch = min(R, M - m0);
+      for (int c = 0; c < nch; ++c) {
+        const int m = m0 + c;
+        const float* row = &sbuf[s & 1][c * ROWS][0];
+        auto rd = [&](int r) { return row[r * WAVE + lane]; };
+        const size_t o = (size_t)m * N + nn;
+        const float lo = lo_neuron ? lo_neuron[nn] : l - margin * (fabsf(l) + 1.0f);
+        l = fminf(rd(0), __fadd_rn(__fmul_rn(rd(1), l), rd(2)));
+        const int cnt = __float_as_int(rd(5));
+        const bool ovfr = __float_as_int(rd(6)) != 0;
+        float xd[KMAX], cd[KMAX];
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) {
+          xd[i] = i < K ? rd(7 + i) : -INFINITY;
+          cd[i] = i < K ? rd(7 + KMAX + i) : 0.0f;
+        }
+        int gt = 0;
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) gt += (i < cnt && xd[i] > lo) ? 1 : 0;
+        const int ne = min(cnt, gt + 1);
+        const bool ovf = ovfr && gt == cnt;
+        int k = 0;
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) k += (i < ne && xd[i] > u) ? 1 : 0;
+        float cval = 0.0f;
+#pragma unroll
+        for (int i = 0; i < KMAX; ++i) cval = (i == k) ? cd[i] : cval;
+        float nu = (k == ne) ? __fadd_rn(__fmul_rn(rd(3), u), rd(4)) : cval;
+        if (valid) {
+          LO[o] = lo;
+          starts[o] = u;
+          MN[o] = ne;
+          OVF[o] = ovf ? 1 : 0;
+        }
+        if (ovf) {  // rare: serial fallback through this chunk
+          float wv = u;
+          stream_rows<16>(I + (size_t)m * C * N + nn, (size_t)N, C, [&](int64_t, float x) {
+            bool sp;
+            wv = lif_step(wv, x, beta, theta, u_r, sp);
+          });
+          nu = wv;
+        }
+        u = nu;
+        if (valid) {
+          ovf_acc += ovf ? 1ull : 0ull;
+          pcs_acc += (unsigned long long)ne;
+          pmax = max(pmax, ne);
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (w == 0) {
+    ovf_acc = wave_sum_u64(ovf_acc);
+    pcs_acc = wave_sum_u64(pcs_acc);
+    pmax = wave_max_i(pmax);
+    if (lane == 0) {
+      atomicAdd(&hdr->ovf_count, ovf_acc);
+      atomicAdd(&hdr->pieces_sum, pcs_acc);
+      atomicMax(&hdr->pieces_max, (unsigned int)pmax);
+    }
   }
 }
 
@@ -623,6 +772,14 @@ static void launch_build_carry(const float* I, const float* u0, const float* lo_
   auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(ws + off); };
   launch_build<KMAX>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
+  if (M >= 4 * CarryStage<KMAX>::R && KMAX <= 32) {
+    // long chunk sequences: map reads staged through LDS by three loader waves
+    hipLaunchKernelGGL((k_lif_carry_staged<KMAX>), dim3((unsigned)NB), dim3(256), 0, st, I, u0,
+                       F(L.EC), F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
+                       F(L.MC), lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS),
+                       reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r);
+    return;
+  }
   hipLaunchKernelGGL((k_lif_carry<KMAX>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, F(L.EC),
                      F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX), F(L.MC),
                      lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS),

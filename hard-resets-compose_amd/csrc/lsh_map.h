@@ -38,12 +38,21 @@ struct MapBuilder {
 
   // One step with input x (triton_lif.py:752-769): push every constant through the step,
   // then append the step's breakpoint, then advance the affine part.
+  // wcnt is the same on every lane (it only grows through a ballot), so it is read as a scalar:
+  // constants are pushed in groups of 8 slots behind one scalar branch per group (a slot above
+  // a lane's cnt holds no breakpoint yet and is overwritten when one is added), and the
+  // insertion, which few steps need, is skipped by the whole wave when no lane inserts.
   __device__ __forceinline__ void step(float x, float beta, float theta, float u_r, float hi, int K) {
+    const int wc = __builtin_amdgcn_readfirstlane(wcnt);
+    constexpr int G = KMAX < 8 ? KMAX : 8;
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-      if (i < wcnt) {
-        const float v = lif_v(cd[i], x, beta);
-        cd[i] = v >= theta ? u_r : v;
+    for (int g = 0; g < KMAX; g += G) {
+      if (g < wc) {
+#pragma unroll
+        for (int i = g; i < g + G; ++i) {
+          const float v = lif_v(cd[i], x, beta);
+          cd[i] = v >= theta ? u_r : v;
+        }
       }
     }
     const float num = (theta - x) - beta * B;
@@ -52,15 +61,15 @@ struct MapBuilder {
     bool nw = (z < xmin) && (z <= hi);
     if (nw && cnt >= K) ovf = true;
     nw = nw && (cnt < K);
+    if (__ballot(nw) != 0ull) {
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-      if (i <= wcnt) {
+      for (int i = 0; i < KMAX; ++i) {
         const bool put = nw && (i == cnt);
         xd[i] = put ? z : xd[i];
         cd[i] = put ? u_r : cd[i];
       }
+      if (__ballot(nw && cnt == wc) != 0ull) ++wcnt;
     }
-    if (__ballot(nw && cnt == wcnt) != 0ull) ++wcnt;
     cnt += nw ? 1 : 0;
     xmin = nw ? z : xmin;
     A = beta * A;

@@ -14,7 +14,7 @@ import torch
 
 from . import _native as _n
 from . import hip_lif as L
-from .hip_lif import _f32, _input, _vec, _same
+from .hip_lif import _f32, _f32s, _input, _vec, _same
 
 
 def _param_backward(I, u0, U, S, GS, beta, theta, u_r, alpha, mode):
@@ -54,7 +54,7 @@ class LIFParamFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, I, u0, beta, theta, u_r, alpha, fwd_mode, bwd_mode, K):
-        b, th, ur = _f32(beta), _f32(theta), _f32(u_r)
+        b, th, ur = _f32s(beta, theta, u_r)
         I = I.contiguous()
         if fwd_mode == "scan":
             U, S = L.scan_forward_auto(I, b, th, ur, u0, K=K)

@@ -15,7 +15,7 @@ import math
 import torch
 
 from . import _native as _n
-from .hip_lif import _f32, _input, _vec, _same, chunked_bwd_C
+from .hip_lif import _f32, _f32s, _input, _vec, _same, chunked_bwd_C
 
 # single-pass backward (one workgroup per 64 neurons) pays off only with many neuron blocks
 ALIF_FUSED_BWD_MIN_N = 8192
@@ -229,7 +229,8 @@ class ALIFFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, I, u0, w0, beta, rho, q, theta0, u_r, alpha, fwd, bwd, Wpred, dw, C, Cb):
-        b, r, qq, th = _f32(beta), _f32(rho), _f32(q), _f32(theta0)
+        b, r, qq, th = _f32s(beta, rho, q, theta0)
+        ctx.set_materialize_grads(False)  # U and W usually get no gradient: no zero fills
         if fwd == "serial":
             U, W, S = alif_serial_forward(I, b, r, qq, th, u_r, u0, w0)
         else:
@@ -242,6 +243,8 @@ class ALIFFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, gS, gU, gW):
+        if gS is None:  # S took no part in the loss
+            return (None,) * 15
         I, u0, w0, U, W, S = ctx.saved_tensors
         b, r, qq, th, u_r, alpha, bwd, Cb = ctx.c
         need = ctx.needs_input_grad

@@ -41,6 +41,21 @@ def _f32(x):
     return float(x)
 
 
+def _f32s(*xs):
+    """Several scalar parameters as Python floats with at most one device-to-host transfer
+    (each .item() on a GPU tensor is a synchronizing copy)."""
+    dev = [i for i, x in enumerate(xs) if torch.is_tensor(x) and x.device.type != "cpu"]
+    out = [float(x.detach().item()) if torch.is_tensor(x) and i not in dev else
+           (None if i in dev else float(x)) for i, x in enumerate(xs)]
+    if len(dev) == 1:
+        out[dev[0]] = float(xs[dev[0]].detach().item())
+    elif dev:
+        vals = torch.stack([xs[i].detach().reshape(()).to(torch.float64) for i in dev]).cpu().tolist()
+        for i, v in zip(dev, vals):
+            out[i] = float(v)
+    return tuple(out)
+
+
 def _input(I):
     if not torch.is_tensor(I) or I.dim() != 2:
         raise ValueError("I must be a 2-D [T, N] tensor")

@@ -104,6 +104,30 @@ def test_scan_v3_matches_oracle(L, dev, beta, mu, sd):
         assert st2["repair_iters"] == sto2["repair_iters"]
 
 
+@pytest.mark.parametrize("K", [4, 8, 16, 32])
+def test_scan_v3_long_sequence_staged_carry(L, dev, K):
+    """Many chunks per neuron (M = 1024): the carry stages its map reads through LDS
+    (k_lif_carry_staged); LO, starts, kept pieces, overflow flags and outputs equal the
+    oracle's bit for bit, including overflowed chunks (K = 4 at beta = 0.99)."""
+    T, N, C, beta = 16384, 130, 16, 0.99
+    I = normal(T, N, 0.012, 0.08, 21)
+    u0 = uniform(N, 0.0, 1.0, 22)
+    print(f"v3 staged carry K={K}", flush=True)
+    st, sto, keep = {}, {}, {}
+    U, S = L.scan_forward_v3(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=C, K=K, stats=st)
+    run = L.last_scan_run()
+    Uo, So = O.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, stats=sto, keep=keep)
+    assert np.array_equal(host(run.view("LO")), keep["Lo"])
+    assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+    assert np.array_equal(host(run.view("MN", torch.int32)), keep["n"])
+    assert np.array_equal(host(run.view("OVF", torch.int32)), keep["ovf"])
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+    assert st["overflow_frac"] == pytest.approx(sto["overflow_frac"], abs=0)
+    assert st["max_pieces"] == sto["max_pieces"]
+    if K == 4:
+        assert sto["overflow_frac"] > 0.01
+
+
 @pytest.mark.parametrize("R", [1, 2, 3])
 def test_scan_v3_finite_repair_rounds(L, dev, R):
     T, N, C = 2048, 300, 64

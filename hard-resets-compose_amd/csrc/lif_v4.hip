@@ -5,9 +5,10 @@
 // C + M + C.
 //
 // Kernels (one lane per neuron, one wave per 64 neurons):
-//   k_lif_env_trunc   sequential over chunks: envelope bound Lo[m] of every chunk entry and
-//                     the reference's lo-pruned map (breakpoint count, overflow flag) by
-//                     truncating the hi-pruned map of k_lif_build (see that kernel);
+//   k_lif_env_lo      sequential over chunks (three loads a chunk, tile-prefetched): the
+//                     envelope bound Lo[m] of every chunk entry;
+//   k_lif_trunc       per (chunk, neuron): the reference's lo-pruned map (breakpoint count,
+//                     overflow flag) by truncating the hi-pruned map of k_lif_build;
 //   k_lif_compose     per (super, neuron): G-1 compositions (triton_lif.py:829-899);
 //   k_map_carry       sequential over super maps with overflow-to-serial fallback
 //                     (triton_lif.py:579-606 with K = K2 and fallback length C*G);
@@ -42,43 +43,93 @@ __device__ __forceinline__ float serial_rows(const float* __restrict__ I, int64_
   return u;
 }
 
-template <int KMAX>
-__global__ __launch_bounds__(64) void k_lif_env_trunc(
-    const float* __restrict__ u0, const float* __restrict__ EC, const float* __restrict__ EA,
-    const float* __restrict__ EB, const int* __restrict__ CNT, const int* __restrict__ OVFRAW,
-    const float* __restrict__ MX, float* __restrict__ LO, int* __restrict__ MN,
-    int* __restrict__ OVF, WsHeader* hdr, int64_t N, int M, int K) {
+// Envelope bound of every chunk entry (triton_lif.py:723-733):
+//   LO[m] = l - 1e-5(|l| + 1),  l <- min(EC[m], EA[m]*l + EB[m]),  l = u0 at m = 0.
+// Sequential over the chunks of a neuron but only three loads a chunk, issued in tiles of D
+// ahead of their use.
+template <int D>
+__global__ __launch_bounds__(64) void k_lif_env_lo(const float* __restrict__ u0,
+                                                   const float* __restrict__ EC,
+                                                   const float* __restrict__ EA,
+                                                   const float* __restrict__ EB,
+                                                   float* __restrict__ LO, int64_t N, int M) {
   const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
-  const bool valid = n < N;
+  if (n >= N) return;
+  const float margin = 1e-5f;
+  float l = u0[n];
+  auto step = [&](int m, float c, float a, float b) {
+    LO[(size_t)m * N + n] = l - margin * (fabsf(l) + 1.0f);
+    l = fminf(c, __fadd_rn(__fmul_rn(a, l), b));
+  };
+  const int nt = M / D;
+  float ca[D], aa[D], ba[D];
+  auto load = [&](int t, float* c, float* a, float* b) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      const size_t o = (size_t)(t * D + k) * N + n;
+      c[k] = EC[o];
+      a[k] = EA[o];
+      b[k] = EB[o];
+    }
+  };
+  if (nt > 0) load(0, ca, aa, ba);
+  for (int t = 0; t < nt; ++t) {
+    float cb[D], ab[D], bb[D];
+    const bool more = t + 1 < nt;
+    if (more) load(t + 1, cb, ab, bb);
+#pragma unroll
+    for (int k = 0; k < D; ++k) step(t * D + k, ca[k], aa[k], ba[k]);
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        ca[k] = cb[k];
+        aa[k] = ab[k];
+        ba[k] = bb[k];
+      }
+    }
+  }
+  for (int m = nt * D; m < M; ++m) {
+    const size_t o = (size_t)m * N + n;
+    step(m, EC[o], EA[o], EB[o]);
+  }
+}
+
+// Truncation of every hi-only chunk map at its entry bound (in parallel over chunks and
+// neurons): the reference's map is the prefix up to the first breakpoint <= LO, and it
+// overflowed iff a (K+1)-th breakpoint appeared and all K stored ones are > LO.
+template <int KMAX>
+__global__ __launch_bounds__(64) void k_lif_trunc(const float* __restrict__ LO,
+                                                  const int* __restrict__ CNT,
+                                                  const int* __restrict__ OVFRAW,
+                                                  const float* __restrict__ MX,
+                                                  int* __restrict__ MN, int* __restrict__ OVF,
+                                                  WsHeader* hdr, int64_t N, int NB, int K) {
+  const int64_t m = blockIdx.x / NB;
+  const int nb = (int)(blockIdx.x - m * NB);
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
   unsigned long long ovf_acc = 0, pcs_acc = 0;
   int pmax = 0;
-  if (valid) {
-    const float margin = 1e-5f;
-    float l = u0[n];
-    for (int m = 0; m < M; ++m) {
-      const size_t o = (size_t)m * N + n;
-      const float lo = l - margin * (fabsf(l) + 1.0f);
-      LO[o] = lo;
-      l = fminf(EC[o], __fadd_rn(__fmul_rn(EA[o], l), EB[o]));
-      const int cnt = CNT[o];
-      int gt = 0;
+  if (n < N) {
+    const size_t o = (size_t)m * N + n;
+    const float lo = LO[o];
+    const int cnt = CNT[o];
+    int gt = 0;
 #pragma unroll
-      for (int i = 0; i < KMAX; ++i)
-        if (i < K && i < cnt) gt += MX[((size_t)m * K + i) * N + n] > lo ? 1 : 0;
-      const int ne = min(cnt, gt + 1);
-      const bool ovf = OVFRAW[o] != 0 && gt == cnt;
-      MN[o] = ne;
-      OVF[o] = ovf ? 1 : 0;
-      ovf_acc += ovf ? 1ull : 0ull;
-      pcs_acc += (unsigned long long)ne;
-      pmax = max(pmax, ne);
-    }
+    for (int i = 0; i < KMAX; ++i)
+      if (i < K && i < cnt) gt += MX[((size_t)m * K + i) * N + n] > lo ? 1 : 0;
+    const int ne = min(cnt, gt + 1);
+    const bool ovf = OVFRAW[o] != 0 && gt == cnt;
+    MN[o] = ne;
+    OVF[o] = ovf ? 1 : 0;
+    ovf_acc = ovf ? 1ull : 0ull;
+    pcs_acc = (unsigned long long)ne;
+    pmax = ne;
   }
   ovf_acc = wave_sum_u64(ovf_acc);
   pcs_acc = wave_sum_u64(pcs_acc);
   pmax = wave_max_i(pmax);
   if (threadIdx.x == 0) {
-    atomicAdd(&hdr->ovf_count, ovf_acc);
+    if (ovf_acc) atomicAdd(&hdr->ovf_count, ovf_acc);
     atomicAdd(&hdr->pieces_sum, pcs_acc);
     atomicMax(&hdr->pieces_max, (unsigned int)pmax);
   }
@@ -318,9 +369,11 @@ static void launch_chunk_kernels(const float* I, const float* u0, char* w, const
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
-  hipLaunchKernelGGL((k_lif_env_trunc<KMAX>), dim3((unsigned)NB), dim3(WAVE), 0, st, u0, F(L.v3.EC),
-                     F(L.v3.EA), F(L.v3.EB), Iq(L.v3.CNT), Iq(L.v3.OVFRAW), F(L.v3.MX), F(L.v3.LO),
-                     Iq(L.v3.MN), Iq(L.v3.OVF), reinterpret_cast<WsHeader*>(w), N, M, K);
+  hipLaunchKernelGGL((k_lif_env_lo<16>), dim3((unsigned)NB), dim3(WAVE), 0, st, u0, F(L.v3.EC),
+                     F(L.v3.EA), F(L.v3.EB), F(L.v3.LO), N, M);
+  hipLaunchKernelGGL((k_lif_trunc<KMAX>), dim3((unsigned)((int64_t)M * NB)), dim3(WAVE), 0, st,
+                     F(L.v3.LO), Iq(L.v3.CNT), Iq(L.v3.OVFRAW), F(L.v3.MX), Iq(L.v3.MN), Iq(L.v3.OVF),
+                     reinterpret_cast<WsHeader*>(w), N, NB, K);
 }
 
 template <int KMAX>

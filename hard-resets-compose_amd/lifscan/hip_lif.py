@@ -257,12 +257,40 @@ def scan_forward_v3(I, beta, theta, u_r, u0, C=64, K=16, BN=32, nw=1, BNc=16, nw
     Stricter than the reference: T % C != 0 raises ValueError (the reference leaves the tail
     uninitialised).  stats receives repair_iters, overflow_frac, mean_pieces, max_pieces with
     the reference's definitions (mean/max of kept breakpoints + 1).  With the repair budget at
-    least T/C (converged) and no stats requested, the single-pass kernel computes the same
-    (serial-exact) result in one pass over I."""
+    least T/C (converged) and no stats requested, the result is the serial recurrence and the
+    fastest exact path computes it: the single-pass kernel, or for few neurons and long T
+    the same two-level scan with long chunks (long_sequence_C)."""
     I = _input(I)
-    if int(C) >= 1 and I.shape[0] % int(C) == 0 and _fused_fwd_ok(I.shape[0], C, K, repair, stats):
+    T, N = I.shape
+    if int(C) >= 1 and T % int(C) == 0 and _fused_fwd_ok(T, C, K, repair, stats):
+        long_c = long_sequence_C(T, N)
+        if long_c:  # few neurons, long T: the multi-kernel scan with long chunks is faster
+            return _scan2(I, beta, theta, u_r, u0, long_c, LONG_K, T // long_c, None)
         return scan_forward_exact(I, beta, theta, u_r, u0, K=K)
     return _scan2(I, beta, theta, u_r, u0, C, K, repair, stats)
+
+
+# Converged exact forward for few neurons and long sequences: the single-pass kernel's hand-off
+# chain (T dependent steps per 64-neuron block) dominates there, while the two-level scan with
+# long chunks and capacity 32 keeps the whole chip busy in its build and replay.  Measured on
+# MI355X: N = 1024, T = 2^20: 24.2 ms single pass vs 8.0 ms (C = 4096); N = 256, T = 2^18:
+# 5.6 vs 1.6 ms (C = 1024); N = 1024, T = 65536: 1.42 vs 1.17 ms (C = 1024); from 4096 neurons
+# the single pass wins (N = 4096, T = 65536: 1.65 vs 2.24 ms).
+LONG_MAX_N = 1024
+LONG_MIN_T = 65536
+LONG_K = 32
+
+
+def long_sequence_C(T, N):
+    """Chunk of the long-sequence exact forward, or 0 when the single pass is used: the longest
+    of 4096, 2048, 1024 dividing T that leaves >= 1024 chunk x 64-neuron blocks."""
+    if N > LONG_MAX_N or T < LONG_MIN_T:
+        return 0
+    nb = (N + 63) // 64
+    for c in (4096, 2048, 1024):
+        if T % c == 0 and (T // c) * nb >= 1024:
+            return c
+    return 0
 
 
 def scan_forward(I, beta, theta, u_r, u0, C=64, K=16, BN=BN_DEFAULT, repair=0, stats=None):

@@ -128,6 +128,20 @@ def test_scan_v3_long_sequence_staged_carry(L, dev, K):
         assert sto["overflow_frac"] > 0.01
 
 
+def test_converged_v3_long_sequence_path(L, dev):
+    """Few neurons, long T, converged repair: scan_forward_v3 runs the two-level scan with
+    long chunks (C = 1024, K = 32) and returns the serial recurrence bit for bit."""
+    T, N, beta = 65536, 1000, 0.99
+    assert L.long_sequence_C(T, N) == 1024
+    I = normal(T, N, 0.012, 0.08, 23)
+    u0 = uniform(N, 0.0, 1.0, 24)
+    print("v3 long-sequence path", flush=True)
+    U, S = L.scan_forward_v3(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=256, K=16, repair=10 ** 6)
+    assert L.last_scan_run().C == 1024
+    Us, Ss = O.serial_forward(I, beta, 1.0, 0.0, u0)
+    assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+
+
 @pytest.mark.parametrize("R", [1, 2, 3])
 def test_scan_v3_finite_repair_rounds(L, dev, R):
     T, N, C = 2048, 300, 64

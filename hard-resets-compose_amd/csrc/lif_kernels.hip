@@ -1012,8 +1012,9 @@ extern "C" int lsh_lif_scan_bwd(const float* I, const float* u0, const float* U,
 }
 
 extern "C" int64_t lsh_lif_param_partials(int64_t T, int64_t N, int mode, int C) {
-  if (T < 0 || N < 0 || mode < 0 || mode > 2) return -1;
+  if (T < 0 || N < 0 || mode < 0 || mode > 3) return -1;
   const int64_t NB = (N + WAVE - 1) / WAVE;
+  if (mode == 3) return T % 256 == 0 ? (T / 256) * NB : -1;  // look-back: one row per tile
   if (mode != 1) return NB;
   if (C < 1 || T % C != 0) return -1;
   return (T / C) * NB;
@@ -1027,8 +1028,10 @@ extern "C" int lsh_lif_param_bwd(const float* I, const float* u0, const float* U
       bad_ptr(partials))
     return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
-  if (mode < 0 || mode > 2) return LSH_ERR_ARG;
+  if (mode < 0 || mode > 3) return LSH_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
+  if (mode == 3) return lif_param_bwd_lookback(I, u0, U, S, GS, Lam, partials, ws, ws_bytes, T, N,
+                                               beta, theta, u_r, alpha, st);
   if (mode == 0) {
     if (T == 0 || N == 0) return LSH_OK;
     launch_bwd3<false, true, false, true>(I, u0, U, S, GS, nullptr, nullptr, Lam, nullptr, nullptr, N,

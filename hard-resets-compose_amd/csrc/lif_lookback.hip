@@ -1,0 +1,316 @@
+// Single-pass affine-scan adjoint for few neurons (MI355X, gfx950): decoupled look-back across
+// workgroups.  Reference: triton_lif.py:512-526 (scan_backward_tiled), :43-50 (_coef).
+//
+//   lam_t = b_t + a_t * lam_{t+1},  lam_T = 0,   dI_t = lam_t
+//
+// The single-pass kernel of lif_fused.hip gives one workgroup all of T for 64 neurons, which
+// leaves most of the chip idle when there are few neurons.  Here a workgroup owns one segment
+// of W*C steps of 64 neurons (wave w: one chunk of C steps, wave 0 the latest), and
+// workgroups take segments latest-first through a ticket counter:
+//   1. every wave loads its chunk once (I, U_{t-1}, S, GS[, GU]) into registers and composes
+//      its affine map (P, Q);
+//   2. wave 0 composes the segment map and publishes it (flag 1);
+//   3. wave 0 looks back over the later segments, composing published segment maps until it
+//      meets a published inclusive value (flag 2), which gives lam at its segment end; it then
+//      publishes its own inclusive value (lam at the segment start, flag 2);
+//   4. every wave takes lam at its chunk end from the later chunks of the segment and replays,
+//      storing dI.
+// A workgroup only waits for segments whose tickets are smaller than its own, i.e. for
+// workgroups already running, so the waits end; each is bounded all the same (a give-up is
+// counted in the header and the result is then not valid).  Flags and aggregates cross XCDs;
+// they go through coherent vector atomics only (see ld_coh / st_coh / publish_flag).
+#include "lsh_abi.h"
+#include "lsh_common.h"
+
+namespace lsh {
+
+__global__ __launch_bounds__(64) void k_fill_i32(int* __restrict__ p, int64_t n, int v) {
+  const int64_t i = (int64_t)blockIdx.x * WAVE + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+// Cross-workgroup values are written and read with agent-scope relaxed atomics (coherent
+// vector loads/stores that bypass the non-coherent L2 of each XCD) instead of release/acquire
+// fences, which would write back or invalidate a whole L2 per hand-off.  Ordering: a producer
+// waits for its value stores to be acknowledged (s_waitcnt) before storing the flag; a consumer
+// issues its value loads only after the flag load has returned non-zero.
+__device__ __forceinline__ float ld_coh(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_flag(int* f, int v) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's value stores are acknowledged
+  if (__lane_id() == 0) __hip_atomic_store(f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// flag of (segment, block) -> value seen by the whole wave
+__device__ __forceinline__ int flag_wait(int* f, unsigned int* timeouts) {
+  for (int it = 0; it < (1 << 22); ++it) {
+    int v = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    v = __builtin_amdgcn_readfirstlane(v);
+    if (v != 0) return v;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  if (__lane_id() == 0) atomicAdd(timeouts, 1u);
+  return -1;
+}
+
+// PS (detached, no GU): the parameter sums of fit.py:43-47 in fp64, one partials row per
+// workgroup (tile): sum lam_t*u_{t-1}, sum gs_t*sg_t, sum s_t*lam_{t+1}.
+template <int C, int W, bool DETACH, bool HAS_GU, bool PS = false>
+__global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ U,
+    const float* __restrict__ S, const float* __restrict__ GS, const float* __restrict__ GU,
+    float* __restrict__ Lam, float* __restrict__ aggP, float* __restrict__ aggQ,
+    float* __restrict__ incl, int* __restrict__ flags, WsHeader* hdr, double* __restrict__ partials,
+    int64_t N, int NB, int NSEG, float beta, float theta, float u_r, float alpha) {
+  static_assert(!PS || (DETACH && !HAS_GU && C <= 64), "parameter sums: detached, no GU");
+  __shared__ float sP[W][WAVE], sQ[W][WAVE];
+  __shared__ float sLamEnd[WAVE];
+  __shared__ double sAcc[PS ? W : 1][3];
+  __shared__ int sTicket;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const unsigned lane = threadIdx.x % WAVE;
+  if (threadIdx.x == 0) sTicket = (int)atomicAdd(&hdr->ticket, 1u);
+  __syncthreads();
+  const int t = sTicket;
+  const int nb = t % NB;
+  const int seg = NSEG - 1 - t / NB;  // latest segments first
+  const int64_t nb0 = (int64_t)nb * WAVE;
+  const bool valid = nb0 + lane < N;
+  const unsigned ln = valid ? lane : (unsigned)(N - 1 - nb0);
+  const unsigned lb = ln * 4u, sb = lane * 4u;
+  const unsigned rstride = (unsigned)(N * 4);
+  const size_t row0 = ((size_t)seg * W + (W - 1 - w)) * C;  // wave 0 holds the latest chunk
+  const float u0n = u0[nb0 + ln];
+
+  // 1. coefficients of the chunk and its map
+  float a[C], b[C];
+  float upk[PS ? C : 1];
+  unsigned long long sbits = 0;
+  double acc_b = 0.0, acc_t = 0.0, acc_r = 0.0;
+  {
+    const Buf bi(I + nb0 + row0 * N), bs(S + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
+    const Buf bp(U + nb0 + row0 * N);
+    const float up0 = row0 > 0 ? ld_row(U + nb0 + (row0 - 1) * N, lb) : u0n;
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const unsigned so = j * rstride;
+      const float x = bi.ld(lb, so);
+      const float s = bs.ld(lb, so);
+      const float gs = bg.ld(lb, so);
+      const float up = j == 0 ? up0 : bp.ld(lb, so - rstride);
+      const float v = lif_v(up, x, beta);
+      const float sg = surrogate(v, theta, alpha);
+      float J = 1.0f - s;
+      if (!DETACH) J = J + (u_r - v) * sg;
+      a[j] = beta * J;
+      b[j] = HAS_GU ? gs * sg + J * Buf(GU + nb0 + row0 * N).ld(lb, so) : gs * sg;
+      if (PS) {
+        upk[j] = up;
+        if (s != 0.0f) sbits |= 1ull << j;
+        if (valid) acc_t += (double)b[j];
+      }
+    }
+  }
+  float P = 1.0f, Q = 0.0f;
+#pragma unroll
+  for (int j = C - 1; j >= 0; --j) {
+    Q = b[j] + a[j] * Q;
+    P = a[j] * P;
+  }
+  sP[w][lane] = P;
+  sQ[w][lane] = Q;
+  __syncthreads();
+
+  // 2.-3. segment map, look-back, inclusive value (wave 0)
+  if (w == 0) {
+    float Ps = 1.0f, Qs = 0.0f;  // lam_start(seg) = Qs + Ps * lam_end(seg)
+    for (int v = 0; v < W; ++v) {
+      Qs = sQ[v][lane] + sP[v][lane] * Qs;
+      Ps = sP[v][lane] * Ps;
+    }
+    const size_t so = (size_t)seg * N + nb0 + lane;
+    int* const myflag = flags + (size_t)seg * NB + nb;
+    float lam_end = 0.0f;
+    if (seg < NSEG - 1) {
+      if (valid) {
+        st_coh(aggP + so, Ps);
+        st_coh(aggQ + so, Qs);
+      }
+      publish_flag(myflag, 1);
+      // lam_end(seg) = F(lam_start(j)) with F the composition of segments seg+1 .. j-1
+      float Pa = 1.0f, Qa = 0.0f;
+      for (int j = seg + 1; j < NSEG; ++j) {
+        const int f = flag_wait(flags + (size_t)j * NB + nb, &hdr->spin_timeouts);
+        const size_t oj = (size_t)j * N + nb0 + ln;
+        if (f == 2 || f < 0) {
+          const float x = f == 2 ? ld_coh(incl + oj) : 0.0f;
+          lam_end = Qa + Pa * x;
+          break;
+        }
+        const float pj = ld_coh(aggP + oj), qj = ld_coh(aggQ + oj);
+        Qa = Qa + Pa * qj;
+        Pa = Pa * pj;
+      }
+    }
+    const float lam_start = Qs + Ps * lam_end;
+    if (valid) st_coh(incl + so, lam_start);
+    publish_flag(myflag, 2);
+    sLamEnd[lane] = lam_end;
+  }
+  __syncthreads();
+
+  // 4. replay of every chunk from lam at its end
+  float lam = sLamEnd[lane];
+  for (int v = 0; v < w; ++v) lam = sQ[v][lane] + sP[v][lane] * lam;
+  const Buf bl(Lam + nb0 + row0 * N);
+#pragma unroll
+  for (int j = C - 1; j >= 0; --j) {
+    const float lam_next = lam;
+    lam = b[j] + a[j] * lam;
+    if (valid) {
+      bl.st_nt(sb, j * rstride, lam);
+      if (PS) {
+        acc_b += (double)lam * (double)upk[j];
+        if ((sbits >> j) & 1ull) acc_r += (double)lam_next;
+      }
+    }
+  }
+  if (PS) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      acc_b += __shfl_xor(acc_b, o, WAVE);
+      acc_t += __shfl_xor(acc_t, o, WAVE);
+      acc_r += __shfl_xor(acc_r, o, WAVE);
+    }
+    if (lane == 0) {
+      sAcc[w][0] = acc_b;
+      sAcc[w][1] = acc_t;
+      sAcc[w][2] = acc_r;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      double tb = 0.0, tt = 0.0, tr = 0.0;
+      for (int v = 0; v < W; ++v) {
+        tb += sAcc[v][0];
+        tt += sAcc[v][1];
+        tr += sAcc[v][2];
+      }
+      double* out = partials + ((size_t)seg * NB + nb) * 3;
+      out[0] = tb;
+      out[1] = tt;
+      out[2] = tr;
+    }
+  }
+}
+
+template <int C, int W, bool DETACH, bool HAS_GU, bool PS = false>
+static void launch_lookback(const float* I, const float* u0, const float* U, const float* S,
+                            const float* GS, const float* GU, float* Lam, char* ws, int64_t N,
+                            int NSEG, float beta, float theta, float u_r, float alpha,
+                            hipStream_t st, double* partials = nullptr) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  const size_t sn = align_up((size_t)NSEG * (size_t)N * 4, 256);
+  float* aggP = reinterpret_cast<float*>(ws + kWsHeaderBytes);
+  float* aggQ = reinterpret_cast<float*>(ws + kWsHeaderBytes + sn);
+  float* incl = reinterpret_cast<float*>(ws + kWsHeaderBytes + 2 * sn);
+  int* flags = reinterpret_cast<int*>(ws + kWsHeaderBytes + 3 * sn);
+  const int64_t nflags = (int64_t)NSEG * NB;
+  hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, reinterpret_cast<WsHeader*>(ws));
+  hipLaunchKernelGGL(k_fill_i32, dim3((unsigned)((nflags + WAVE - 1) / WAVE)), dim3(WAVE), 0, st,
+                     flags, nflags, 0);
+  hipLaunchKernelGGL((k_lif_bwd_lookback<C, W, DETACH, HAS_GU, PS>), dim3((unsigned)nflags),
+                     dim3(WAVE * W), 0, st, I, u0, U, S, GS, GU, Lam, aggP, aggQ, incl, flags,
+                     reinterpret_cast<WsHeader*>(ws), partials, N, NB, NSEG, beta, theta, u_r,
+                     alpha);
+}
+
+template <int C, int W>
+static void lookback_cw(const float* I, const float* u0, const float* U, const float* S,
+                        const float* GS, const float* GU, float* Lam, char* ws, int64_t N, int NSEG,
+                        float beta, float theta, float u_r, float alpha, bool detach,
+                        hipStream_t st) {
+  if (detach) {
+    if (GU)
+      launch_lookback<C, W, true, true>(I, u0, U, S, GS, GU, Lam, ws, N, NSEG, beta, theta, u_r,
+                                        alpha, st);
+    else
+      launch_lookback<C, W, true, false>(I, u0, U, S, GS, GU, Lam, ws, N, NSEG, beta, theta, u_r,
+                                         alpha, st);
+  } else {
+    if (GU)
+      launch_lookback<C, W, false, true>(I, u0, U, S, GS, GU, Lam, ws, N, NSEG, beta, theta, u_r,
+                                         alpha, st);
+    else
+      launch_lookback<C, W, false, false>(I, u0, U, S, GS, GU, Lam, ws, N, NSEG, beta, theta, u_r,
+                                          alpha, st);
+  }
+}
+
+}  // namespace lsh
+
+using namespace lsh;
+
+// Segment = 256 steps: 16 waves of 16 steps (C = 16) or 8 waves of 32 steps (C = 32).
+static constexpr int kLookbackSeg = 256;
+
+extern "C" size_t lsh_lif_scan_lookback_bwd_workspace(int64_t T, int64_t N) {
+  if (T < 0 || N < 0 || T % kLookbackSeg != 0) return 0;
+  const int64_t NSEG = T / kLookbackSeg;
+  const int64_t NB = (N + WAVE - 1) / WAVE;
+  const size_t sn = align_up((size_t)NSEG * (size_t)N * 4, 256);
+  return kWsHeaderBytes + 3 * sn + align_up((size_t)NSEG * (size_t)NB * 4, 256);
+}
+
+extern "C" int lsh_lif_scan_lookback_bwd(const float* I, const float* u0, const float* U,
+                                         const float* S, const float* GS, const float* GU,
+                                         float* Lam, int64_t T, int64_t N, float beta, float theta,
+                                         float u_r, float alpha, int detach, int C, void* ws,
+                                         size_t ws_bytes, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(Lam) ||
+      bad_ptr(ws))
+    return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C != 16 && C != 32) return LSH_ERR_SHAPE;
+  if (T % kLookbackSeg != 0) return LSH_ERR_DIVISIBILITY;
+  if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+  if (ws_bytes < lsh_lif_scan_lookback_bwd_workspace(T, N) ||
+      (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+    return LSH_ERR_WORKSPACE;
+  const int64_t NSEG = T / kLookbackSeg;
+  const int64_t NB = (N + WAVE - 1) / WAVE;
+  if (NSEG * NB > ((int64_t)1 << 31) - 1) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  char* w = static_cast<char*>(ws);
+  if (C == 16)
+    lookback_cw<16, 16>(I, u0, U, S, GS, GU, Lam, w, N, (int)NSEG, beta, theta, u_r, alpha,
+                        detach != 0, st);
+  else
+    lookback_cw<32, 8>(I, u0, U, S, GS, GU, Lam, w, N, (int)NSEG, beta, theta, u_r, alpha,
+                       detach != 0, st);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+int lsh::lif_param_bwd_lookback(const float* I, const float* u0, const float* U, const float* S,
+                                const float* GS, float* Lam, double* partials, void* ws,
+                                size_t ws_bytes, int64_t T, int64_t N, float beta, float theta,
+                                float u_r, float alpha, hipStream_t st) {
+  if (bad_ptr(ws)) return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (T % kLookbackSeg != 0) return LSH_ERR_DIVISIBILITY;
+  if (ws_bytes < lsh_lif_scan_lookback_bwd_workspace(T, N) ||
+      (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+    return LSH_ERR_WORKSPACE;
+  const int64_t NSEG = T / kLookbackSeg;
+  if (NSEG * ((N + WAVE - 1) / WAVE) > ((int64_t)1 << 31) - 1) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  launch_lookback<16, 16, true, false, true>(I, u0, U, S, GS, nullptr, Lam, static_cast<char*>(ws),
+                                             N, (int)NSEG, beta, theta, u_r, alpha, st, partials);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}

@@ -37,8 +37,9 @@ struct WsHeader {
   unsigned int pad0;
   unsigned long long fused_fixups;     // fused scan: speculative chunk entries that missed
   unsigned long long fused_unknown;    // fused scan: entries the maps could not predict
-  unsigned int spin_timeouts;          // bounded LDS waits that gave up (must stay 0)
+  unsigned int spin_timeouts;          // bounded waits that gave up (must stay 0)
   unsigned int epoch;                  // advanced once per call
+  unsigned int ticket;                 // look-back scans: next tile in launch order
 };
 static_assert(sizeof(WsHeader) <= 256, "workspace header must fit in 256 bytes");
 constexpr size_t kWsHeaderBytes = 256;
@@ -64,5 +65,11 @@ inline bool bad_ptr(const void* p) { return p == nullptr; }
 int lif_param_bwd_fused(const float* I, const float* u0, const float* U, const float* S,
                         const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
                         float beta, float theta, float u_r, float alpha, int C, hipStream_t st);
+// The same with the look-back adjoint (lif_lookback.hip); one partials row per (256-step
+// segment, 64-neuron block); workspace as lsh_lif_scan_lookback_bwd.
+int lif_param_bwd_lookback(const float* I, const float* u0, const float* U, const float* S,
+                           const float* GS, float* Lam, double* partials, void* ws,
+                           size_t ws_bytes, int64_t T, int64_t N, float beta, float theta,
+                           float u_r, float alpha, hipStream_t st);
 
 }  // namespace lsh

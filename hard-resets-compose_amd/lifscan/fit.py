@@ -27,6 +27,8 @@ def _param_backward(I, u0, U, S, GS, beta, theta, u_r, alpha, mode):
     if mode == "scan":
         if N >= L.FUSED_BWD_MIN_N and T % L.FUSED_BWD_C == 0:
             code, C = 2, L.FUSED_BWD_C
+        elif L.LOOKBACK_BWD and T % L.LOOKBACK_SEG == 0:
+            code, C = 3, 16
         else:
             code, C = 1, L.chunked_bwd_C(T, N, min(128, L._pick_C(T, D=2)))
     else:
@@ -39,6 +41,9 @@ def _param_backward(I, u0, U, S, GS, beta, theta, u_r, alpha, mode):
     ws, nbytes = None, 0
     if code == 1:
         nbytes = lib.lsh_lif_scan_bwd_workspace(T, N, C)
+        ws = _n.workspace(nbytes, I.device)
+    elif code == 3:
+        nbytes = lib.lsh_lif_scan_lookback_bwd_workspace(T, N)
         ws = _n.workspace(nbytes, I.device)
     with torch.cuda.device(I.device):
         _n.check(lib.lsh_lif_param_bwd(

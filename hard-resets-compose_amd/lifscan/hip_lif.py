@@ -490,8 +490,11 @@ def scan_backward_fused(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach
 
 # ----------------------------------------------------------------------------- scan backward
 # The single-pass adjoint owns 64 neurons per workgroup: with fewer than this many neurons the
-# chip is not filled and the three-kernel chunk scan (parallel over chunks x neurons) wins.
-FUSED_BWD_MIN_N = 8192
+# chip is not filled, and the look-back adjoint (workgroups over 256-step segments chained by
+# a decoupled look-back) wins: N = 1024, T = 2^20: 3.63 ms vs 36.4 ms single pass and 8.13 ms
+# three-kernel chunk scan; N = 8192, T = 8192: 0.27 vs 0.38 / 0.47 ms.  From 16384 neurons
+# the single pass is as fast or faster (N = 16384, T = 1024: 0.068 vs 0.077 ms).
+FUSED_BWD_MIN_N = 16384
 CHUNKED_BWD_MIN_BLOCKS = 2048  # chunk x 64-neuron blocks that keep every CU busy
 
 
@@ -506,6 +509,41 @@ def chunked_bwd_C(T, N, C=64):
     return int(C)
 
 
+LOOKBACK_SEG = 256  # steps per workgroup segment of the look-back adjoint
+_LAST_LOOKBACK = None
+
+
+def scan_backward_lookback(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=16):
+    """Single-pass affine-scan adjoint with a decoupled look-back across workgroups -> Lam
+    (for few neurons; T % 256 == 0; C in {16, 32} steps per wave)."""
+    global _LAST_LOOKBACK
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    U, S, GS = _same(U, I, "U"), _same(S, I, "S"), _same(GS, I, "GS")
+    GU = _same(GU, I, "GU")
+    L = _n.lib()
+    nbytes = L.lsh_lif_scan_lookback_bwd_workspace(T, N)
+    if nbytes == 0:
+        raise ValueError(f"look-back adjoint needs T % {LOOKBACK_SEG} == 0 (T={T})")
+    ws = _n.workspace(nbytes, I.device)
+    Lam = torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        _n.check(L.lsh_lif_scan_lookback_bwd(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS), _n.ptr(GU), _n.ptr(Lam), T, N,
+            _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), int(bool(detach)), int(C), _n.ptr(ws),
+            nbytes, _n.stream_of(I)), "lsh_lif_scan_lookback_bwd")
+    _LAST_LOOKBACK = ws
+    return Lam
+
+
+def last_lookback_timeouts():
+    """Bounded waits of the most recent look-back adjoint that gave up (must be 0)."""
+    if _LAST_LOOKBACK is None:
+        return None
+    return int(_n.read_stats(_LAST_LOOKBACK, 1).spin_timeouts)
+
+
 def scan_backward_tiled(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=64,
                         BNr=32, D=4, nwr=1):
     """Affine-scan adjoint (triton_lif.py:512-526) -> Lam.  GU may be None (zeros).
@@ -516,8 +554,13 @@ def scan_backward_tiled(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach
     T, N = I.shape
     if N >= FUSED_BWD_MIN_N and T % FUSED_BWD_C == 0:
         return scan_backward_fused(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach)
+    if LOOKBACK_BWD and T % LOOKBACK_SEG == 0:
+        return scan_backward_lookback(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach)
     return scan_backward_chunked(I, u0, U, S, GS, GU, beta, theta, u_r, alpha, detach,
                                  chunked_bwd_C(T, N, C))
+
+
+LOOKBACK_BWD = True
 
 
 def scan_backward_chunked(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, C=64):

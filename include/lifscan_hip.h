@@ -210,11 +210,24 @@ int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w0, const fl
  * envelope, the entry box + build, the carry and the first replay (the reference's `phases`,
  * triton_alif.py:305-341). */
 
+/* Single-pass affine-scan adjoint for few neurons (replaces triton_lif.py:512-526 like
+ * lsh_lif_scan_fused_bwd): workgroups own 256-step segments of 64 neurons and chain them with
+ * a decoupled look-back, so every CU is busy even at N = 1024.  C in {16, 32} (steps per wave);
+ * T % 256 == 0; workspace lsh_lif_scan_lookback_bwd_workspace(T, N) bytes, 256-byte aligned,
+ * one call at a time.  A bounded wait that gave up is counted in the header's spin_timeouts
+ * (lsh_scan_stats_read); it must stay 0. */
+size_t lsh_lif_scan_lookback_bwd_workspace(int64_t T, int64_t N);
+int lsh_lif_scan_lookback_bwd(const float* I, const float* u0, const float* U, const float* S,
+                              const float* GS, const float* GU, float* Lam, int64_t T, int64_t N,
+                              float beta, float theta, float u_r, float alpha, int detach, int C,
+                              void* ws, size_t ws_bytes, void* stream);
+
 /* LIF adjoint with the neuron-parameter gradients of fit.py LIFParamFn.backward
  * (fit.py:30-48): Lam as lsh_lif_*_bwd with the reset detached and no GU, plus per block
  * partials[P][3] (fp64) = (sum lam_t*u_{t-1}, sum gs_t*sg_t, sum s_t*lam_{t+1}), whose column
  * sums give dbeta, -dtheta and dL/du_r / beta.  mode 0: serial; 1: chunked scan of chunk C
- * (workspace lsh_lif_scan_bwd_workspace(T, N, C)); 2: single pass, C in {16, 32, 64}.
+ * (workspace lsh_lif_scan_bwd_workspace(T, N, C)); 2: single pass, C in {16, 32, 64};
+ * 3: look-back (T % 256 == 0, workspace lsh_lif_scan_lookback_bwd_workspace(T, N)).
  * P = lsh_lif_param_partials(T, N, mode, C). */
 int64_t lsh_lif_param_partials(int64_t T, int64_t N, int mode, int C);
 int lsh_lif_param_bwd(const float* I, const float* u0, const float* U, const float* S,

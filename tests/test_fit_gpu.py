@@ -46,7 +46,7 @@ def test_lif_param_gradients(dev, mode, T, N):
         assert rel(p.grad.item(), want[2 + k]) < 1e-4, k
 
 
-@pytest.mark.parametrize("mode,C", [(0, 1), (1, 16), (1, 64), (2, 16), (2, 32), (2, 64)])
+@pytest.mark.parametrize("mode,C", [(0, 1), (1, 16), (1, 64), (2, 16), (2, 32), (2, 64), (3, 16)])
 def test_lif_param_partials(dev, mode, C):
     """lsh_lif_param_bwd directly: Lam and the three column sums of the per-block rows."""
     from lifscan import _native as nat
@@ -58,12 +58,16 @@ def test_lif_param_partials(dev, mode, C):
     U, S = O.serial_forward(I, beta, theta, u_r, u0)
     lib = nat.lib()
     P = lib.lsh_lif_param_partials(T, N, mode, C)
-    assert P == ((T // C) * ((N + 63) // 64) if mode == 1 else (N + 63) // 64)
+    nb = (N + 63) // 64
+    assert P == {1: (T // C) * nb, 3: (T // 256) * nb}.get(mode, nb)
     parts = torch.full((P, 3), float("nan"), device=dev, dtype=torch.float64)
     Lam = torch.empty(T, N, device=dev)
     ws, nb = None, 0
     if mode == 1:
         nb = lib.lsh_lif_scan_bwd_workspace(T, N, C)
+        ws = nat.workspace(nb, dev)
+    elif mode == 3:
+        nb = lib.lsh_lif_scan_lookback_bwd_workspace(T, N)
         ws = nat.workspace(nb, dev)
     args = [gpu(a, dev) for a in (I, u0, U, S, GS)]
     print(f"lif_param_bwd mode={mode} C={C}", flush=True)

@@ -18,6 +18,7 @@ The other BASELINE configurations (cfg3 network step, cfg4 long sequence, cfg5 A
 measured after the headline and reported under "other_configs" (--headline-only skips them).
 
   python bench.py [--steps K] [--warmup W] [--no-cpu] [--headline-only]
+  python bench.py --only cfg4        # one other configuration (profiling runs)
   python bench.py --dominant-only    # short run for rocprofv3 --pmc passes (copy + kernel)
 """
 import argparse
@@ -286,6 +287,9 @@ def main():
     ap.add_argument("--dominant-only", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
                     help="skip the cfg3 / cfg4 / cfg5 measurements")
+    ap.add_argument("--only", choices=("cfg3", "cfg4", "cfg5"),
+                    help="measure one of the other configurations only (for profiling runs); "
+                         "prints its JSON, not the headline line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the exact LIF scan shards along neurons with no "
@@ -300,6 +304,10 @@ def main():
     dev = torch.device("cuda:0")
     if args.dominant_only:
         dominant_only(L, torch, dev)
+        return
+    if args.only:
+        fn = {"cfg3": bench_cfg3, "cfg4": bench_cfg4, "cfg5": bench_cfg5}[args.only]
+        print(json.dumps({args.only: fn(torch, dev, 5)}))
         return
     T, N, beta, K = T_CFG, N_CFG, 0.9, 8
     I_cpu, I, gS = inputs(beta, dev)

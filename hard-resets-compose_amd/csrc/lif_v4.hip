@@ -13,6 +13,8 @@
 //   k_map_carry       sequential over super maps with overflow-to-serial fallback
 //                     (triton_lif.py:579-606 with K = K2 and fallback length C*G);
 //   k_lif_carry_inner per (super, neuron): G chunk-map evaluations (triton_lif.py:903-932).
+#include <algorithm>
+
 #include "lsh_abi.h"
 #include "lsh_common.h"
 
@@ -96,34 +98,39 @@ __global__ __launch_bounds__(64) void k_lif_env_lo(const float* __restrict__ u0,
 
 // Truncation of every hi-only chunk map at its entry bound (in parallel over chunks and
 // neurons): the reference's map is the prefix up to the first breakpoint <= LO, and it
-// overflowed iff a (K+1)-th breakpoint appeared and all K stored ones are > LO.
+// overflowed iff a (K+1)-th breakpoint appeared and all K stored ones are > LO.  A block of
+// 64 neurons takes every MB-th chunk (grid NB x MB), so the header counters see one atomic per
+// block rather than one per chunk.
 template <int KMAX>
 __global__ __launch_bounds__(64) void k_lif_trunc(const float* __restrict__ LO,
                                                   const int* __restrict__ CNT,
                                                   const int* __restrict__ OVFRAW,
                                                   const float* __restrict__ MX,
                                                   int* __restrict__ MN, int* __restrict__ OVF,
-                                                  WsHeader* hdr, int64_t N, int NB, int K) {
-  const int64_t m = blockIdx.x / NB;
-  const int nb = (int)(blockIdx.x - m * NB);
+                                                  WsHeader* hdr, int64_t N, int NB, int M, int MB,
+                                                  int K) {
+  const int nb = blockIdx.x % NB;
+  const int mb = blockIdx.x / NB;
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
   unsigned long long ovf_acc = 0, pcs_acc = 0;
   int pmax = 0;
   if (n < N) {
-    const size_t o = (size_t)m * N + n;
-    const float lo = LO[o];
-    const int cnt = CNT[o];
-    int gt = 0;
+    for (int m = mb; m < M; m += MB) {
+      const size_t o = (size_t)m * N + n;
+      const float lo = LO[o];
+      const int cnt = CNT[o];
+      int gt = 0;
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i)
-      if (i < K && i < cnt) gt += MX[((size_t)m * K + i) * N + n] > lo ? 1 : 0;
-    const int ne = min(cnt, gt + 1);
-    const bool ovf = OVFRAW[o] != 0 && gt == cnt;
-    MN[o] = ne;
-    OVF[o] = ovf ? 1 : 0;
-    ovf_acc = ovf ? 1ull : 0ull;
-    pcs_acc = (unsigned long long)ne;
-    pmax = ne;
+      for (int i = 0; i < KMAX; ++i)
+        if (i < K && i < cnt) gt += MX[((size_t)m * K + i) * N + n] > lo ? 1 : 0;
+      const int ne = min(cnt, gt + 1);
+      const bool ovf = OVFRAW[o] != 0 && gt == cnt;
+      MN[o] = ne;
+      OVF[o] = ovf ? 1 : 0;
+      ovf_acc += ovf ? 1ull : 0ull;
+      pcs_acc += (unsigned long long)ne;
+      pmax = max(pmax, ne);
+    }
   }
   ovf_acc = wave_sum_u64(ovf_acc);
   pcs_acc = wave_sum_u64(pcs_acc);
@@ -371,9 +378,11 @@ static void launch_chunk_kernels(const float* I, const float* u0, char* w, const
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
   hipLaunchKernelGGL((k_lif_env_lo<16>), dim3((unsigned)NB), dim3(WAVE), 0, st, u0, F(L.v3.EC),
                      F(L.v3.EA), F(L.v3.EB), F(L.v3.LO), N, M);
-  hipLaunchKernelGGL((k_lif_trunc<KMAX>), dim3((unsigned)((int64_t)M * NB)), dim3(WAVE), 0, st,
+  // ~8192 blocks in all: enough to fill the chip, few header atomics
+  const int MB = (int)std::max<int64_t>(1, std::min<int64_t>(M, 8192 / NB));
+  hipLaunchKernelGGL((k_lif_trunc<KMAX>), dim3((unsigned)((int64_t)MB * NB)), dim3(WAVE), 0, st,
                      F(L.v3.LO), Iq(L.v3.CNT), Iq(L.v3.OVFRAW), F(L.v3.MX), Iq(L.v3.MN), Iq(L.v3.OVF),
-                     reinterpret_cast<WsHeader*>(w), N, NB, K);
+                     reinterpret_cast<WsHeader*>(w), N, NB, M, MB, K);
 }
 
 template <int KMAX>

@@ -185,17 +185,33 @@ __global__ __launch_bounds__(64) void k_alif_box(const float* __restrict__ Wpred
 }
 
 // ---------------------------------------------------------------------------------------
-// Box-scan chunk map (triton_alif.py:96-186).  32 lanes per neuron (two neurons per wave):
-// lane i holds first-spike line slot i (< K1) and post-spike piece slot i (< K2).  Per step:
-//  1. every piece is advanced; pieces cut by the threshold are split and the list compacted
-//     (exclusive prefix sum of the output counts, binary search of every output slot's
-//     source, gathers: all as shuffles within the neuron's 32 lanes).  The split runs for
-//     all neurons of a block of BLK neurons when any of them has a cut (the reference's
+// Box-scan chunk map (triton_alif.py:96-186).  A workgroup owns 16 neurons (BLK neurons when
+// BLK >= 4: see AlifBuildShape); in the
+// piece loop 32 lanes serve one neuron (two neurons per wave): lane i holds first-spike line
+// slot i (< K1) and post-spike piece slot i (< K2).  Steps go in tiles of TS:
+//  0. the per-neuron line quantities of the tile, which do not depend on the pieces, are
+//     computed once per neuron instead of on 32 lanes, into LDS: (a) one thread per neuron runs
+//     the sequential recurrences A_j = beta*A, B_j = fl(fl(beta*B) + x_j) and R_j = rho^j;
+//     (b) all threads divide, sj = R_j/A_j, cj = (theta0 - B_j)/A_j, whi_j = min(hw, (hu - cj)/sj),
+//     (lu - cj)/sj; (c) one thread per neuron runs the running max wlo_j.  Same operations as
+//     the serial formulation, so the same bits.
+//  1. per step every piece is advanced; pieces cut by the threshold are split and the list
+//     compacted (exclusive prefix sum of the output counts, binary search of every output
+//     slot's source, gathers: all as shuffles within the neuron's 32 lanes).  The split runs
+//     for all neurons of a block of BLK neurons when any of them has a cut (the reference's
 //     Triton block); blocks wider than one wave agree through LDS.
 //  2. the step's first-spike line u0 >= sj*w0 + cj is added unless an existing line dominates
 //     it on [wlo, whi]; its post-spike piece x in [cx*wlo + q, cx*whi + q] (widened) is added.
+// Neurons per workgroup: 16 (8 waves) without a cross-wave split decision; a block of BLK >= 4
+// neurons is one workgroup of BLK/2 waves, so the per-step decision syncs only those waves.
 template <int BLK>
-__global__ __launch_bounds__(WAVE*(BLK > 2 ? BLK / 2 : 1)) void k_alif_build(
+struct AlifBuildShape {
+  static constexpr int NPW = BLK >= 4 ? BLK : 16;
+};
+constexpr int kAlifTS = 64;   // steps per tile
+
+template <int BLK, int kAlifNPW = AlifBuildShape<BLK>::NPW>
+__global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
     const float* __restrict__ I, const float* __restrict__ LU, const float* __restrict__ HU,
     const float* __restrict__ LWb, const float* __restrict__ HWb, float* __restrict__ MA,
     float* __restrict__ MB, int* __restrict__ NL, int* __restrict__ NP, int* __restrict__ OVF,
@@ -203,22 +219,38 @@ __global__ __launch_bounds__(WAVE*(BLK > 2 ? BLK / 2 : 1)) void k_alif_build(
     float* __restrict__ PXL, float* __restrict__ PXR, float* __restrict__ PU, float* __restrict__ PA,
     float* __restrict__ POF, int64_t N, int NBLK, int C, int K1, int K2, int logk2, float beta,
     float rho, float q, float theta0, float u_r) {
-  constexpr int WPB = BLK > 2 ? BLK / 2 : 1;  // waves per workgroup
-  __shared__ int s_cut[WPB];
+  constexpr int NW = kAlifNPW / 2;                // waves per workgroup
+  constexpr int GW = BLK > 2 ? BLK / 2 : 1;       // waves per split-decision block
+  static_assert(BLK <= 2 || GW == NW, "a split-decision block is one workgroup");
+  constexpr int TS = kAlifTS;
+  __shared__ float sX[kAlifNPW][TS], sS[kAlifNPW][TS], sC[kAlifNPW][TS], sHi[kAlifNPW][TS],
+      sLo[kAlifNPW][TS], sR[TS];
+  __shared__ float sA[kAlifNPW], sB[kAlifNPW], sLU[kAlifNPW], sHU[kAlifNPW], sHW[kAlifNPW];
+  __shared__ int s_cut[NW];
   const int64_t m = blockIdx.x / NBLK;
   const int blk = (int)(blockIdx.x - m * NBLK);
-  const int wv = threadIdx.x / WAVE;
-  const int lane = threadIdx.x % WAVE;
+  const int tid = threadIdx.x;
+  const int wv = tid / WAVE;
+  const int lane = tid % WAVE;
   const int half = lane >> 5;
   const int i = lane & 31;  // slot
   const int hb = half << 5;
-  const int64_t n = ((int64_t)blk * WPB + wv) * 2 + half;
+  const int ln = wv * 2 + half;  // neuron of this lane within the workgroup
+  const int64_t n = (int64_t)blk * kAlifNPW + ln;
   const bool valid_n = n < N;
   const int64_t nn = valid_n ? n : N - 1;
   const size_t o = (size_t)m * N + nn;
-  const float lu = LU[o], hu = HU[o], hw = HWb[o];
-  float wlo = LWb[o];
-  float A = 1.0f, B = 0.0f, R = 1.0f;
+  // per-neuron sequential state for phases (a) and (c): thread t < 16 serves neuron t
+  const int64_t pn = (int64_t)blk * kAlifNPW + (tid < kAlifNPW ? tid : 0);
+  const int64_t pnn = pn < N ? pn : N - 1;
+  const size_t po = (size_t)m * N + pnn;
+  float pA = 1.0f, pB = 0.0f, pR = 1.0f, pW = 0.0f;
+  if (tid < kAlifNPW) {
+    pW = LWb[po];
+    sLU[tid] = LU[po];
+    sHU[tid] = HU[po];
+    sHW[tid] = HWb[po];
+  }
   float ls = 0.0f, lc = INFINITY, lx = 0.0f;
   int nl = 0;
   int pown = -1;
@@ -226,108 +258,144 @@ __global__ __launch_bounds__(WAVE*(BLK > 2 ? BLK / 2 : 1)) void k_alif_build(
   int npc = 0;
   int ovf = 0;
   const unsigned long long hmask = 0xffffffffull << hb;
-  const float* __restrict__ Ip = I + (size_t)m * C * N + nn;
-  for (int j = 0; j < C; ++j) {
-    const float x = Ip[(size_t)j * N];
-    // 1. advance the post-spike pieces; a piece spikes for x <= (v - theta0 - pof)/pa
-    const bool valid = i < npc;
-    const float v = lif_v(pu, x, beta);
-    const float rr = (v - theta0) - pof;
-    const bool es = valid && rr > pa * pxl;
-    const bool en = valid && rr < pa * pxr;
-    const unsigned long long cb = __ballot(es && en);
-    bool cut;
-    if (BLK == 1) {
-      cut = (cb & hmask) != 0ull;
-    } else if (BLK == 2) {
-      cut = cb != 0ull;
-    } else {
-      if (lane == 0) s_cut[wv] = cb != 0ull ? 1 : 0;
-      __syncthreads();
-      int any = 0;
-#pragma unroll
-      for (int k = 0; k < WPB; ++k) any |= s_cut[k];
-      __syncthreads();
-      cut = any != 0;
-    }
-    if (cut) {
-      const float z = rr / pa;
-      const int nout = (es ? 1 : 0) + (en ? 1 : 0);
-      int incl = nout;  // inclusive prefix sum over the neuron's 32 slots
-#pragma unroll
-      for (int off = 1; off < 32; off <<= 1) {
-        const int y = __shfl_up(incl, off, 32);
-        if (i >= off) incl += y;
+  const float* __restrict__ Ipn = I + (size_t)m * C * N + pnn;
+  for (int j0 = 0; j0 < C; j0 += TS) {
+    const int ts = min(TS, C - j0);
+    // (a) sequential recurrences, inputs staged
+    if (tid < kAlifNPW) {
+      for (int k = 0; k < ts; ++k) {
+        const float x = Ipn[(size_t)(j0 + k) * N];
+        sX[tid][k] = x;
+        pA = beta * pA;
+        pB = lif_v(pB, x, beta);
+        sS[tid][k] = pA;  // A_j, replaced by sj in (b)
+        sC[tid][k] = pB;  // B_j, replaced by cj in (b)
+        if (tid == 0) sR[k] = pR;
+        pR = rho * pR;
       }
-      const int p = incl - nout;
-      const int ntot = __shfl(incl, 31, 32);
-      if (ntot > K2) ovf = 1;
-      int lo_i = 0, hi_i = K2 - 1;
-      for (int it = 0; it < logk2; ++it) {
-        const int mid = (lo_i + hi_i + 1) >> 1;
-        const bool le = __shfl(p, mid, 32) <= i;
-        lo_i = le ? mid : lo_i;
-        hi_i = le ? hi_i : mid - 1;
+      sA[tid] = pA;
+      sB[tid] = pB;
+    }
+    __syncthreads();
+    // (b) divisions, every (neuron, step) pair of the tile in parallel
+    for (int e = tid; e < kAlifNPW * ts; e += NW * WAVE) {
+      const int nu = e / ts, k = e - nu * ts;
+      const float Aj = sS[nu][k], Bj = sC[nu][k];
+      const float sj = sR[k] / Aj;
+      const float cj = (theta0 - Bj) / Aj;
+      sS[nu][k] = sj;
+      sC[nu][k] = cj;
+      sHi[nu][k] = nmin(sHW[nu], (sHU[nu] - cj) / sj);
+      sLo[nu][k] = (sLU[nu] - cj) / sj;  // candidate of the running max
+    }
+    __syncthreads();
+    // (c) running max of the lower w bound: sLo[k] becomes wlo before step k
+    if (tid < kAlifNPW) {
+      for (int k = 0; k < ts; ++k) {
+        const float cand = sLo[tid][k];
+        sLo[tid][k] = pW;
+        pW = nmax(pW, cand);
       }
-      const int idx = lo_i;
-      // every shuffle runs on all lanes of the neuron: a bpermute reads 0 from a lane that
-      // is switched off, so none may sit behind a per-lane condition
-      const int d = i - __shfl(p, idx, 32);
-      const int g_es = __shfl(es ? 1 : 0, idx, 32);
-      const bool is_s = d == 0 && g_es != 0;
-      const float g_xl = __shfl(pxl, idx, 32), g_xr = __shfl(pxr, idx, 32);
-      const float g_z = __shfl(z, idx, 32), g_v = __shfl(v, idx, 32);
-      const float g_pa = __shfl(pa, idx, 32), g_po = __shfl(pof, idx, 32);
-      const int g_own = __shfl(pown, idx, 32);
-      const int n_new = min(ntot, K2);
-      const bool keep = i < n_new;
-      pxl = keep ? (is_s ? g_xl : nmax(g_xl, g_z)) : INFINITY;
-      pxr = keep ? (is_s ? nmin(g_xr, g_z) : g_xr) : INFINITY;
-      pu = keep ? (is_s ? u_r : g_v) : 0.0f;
-      pa = keep ? rho * g_pa : 1.0f;
-      pof = keep ? (is_s ? rho * g_po + q : rho * g_po) : 0.0f;
-      pown = keep ? g_own : -1;
-      npc = n_new;
-    } else if (valid) {
-      pu = es ? u_r : v;
-      pof = es ? rho * pof + q : rho * pof;
-      pa = rho * pa;
     }
-    // 2. first-spike line of this step
-    A = beta * A;
-    B = lif_v(B, x, beta);
-    const float sj = R / A;
-    const float cj = (theta0 - B) / A;
-    const float whi = nmin(hw, (hu - cj) / sj);
-    const bool dl = i < nl && (ls * wlo + lc <= sj * wlo + cj) && (ls * whi + lc <= sj * whi + cj);
-    const bool dom = (__ballot(dl) & hmask) != 0ull;
-    const bool newc = (wlo < whi) && !dom && valid_n;
-    const float cx = R * rho;
-    if (newc && i == nl && nl < K1) {
-      ls = sj;
-      lc = cj;
-      lx = cx;
+    __syncthreads();
+    for (int k = 0; k < ts; ++k) {
+      const float x = sX[ln][k];
+      // 1. advance the post-spike pieces; a piece spikes for x <= (v - theta0 - pof)/pa
+      const bool valid = i < npc;
+      const float v = lif_v(pu, x, beta);
+      const float rr = (v - theta0) - pof;
+      const bool es = valid && rr > pa * pxl;
+      const bool en = valid && rr < pa * pxr;
+      const unsigned long long cb = __ballot(es && en);
+      bool cut;
+      if (BLK == 1) {
+        cut = (cb & hmask) != 0ull;
+      } else if (BLK == 2) {
+        cut = cb != 0ull;
+      } else {
+        if (lane == 0) s_cut[wv] = cb != 0ull ? 1 : 0;
+        __syncthreads();
+        int any = 0;
+#pragma unroll
+        for (int kk = 0; kk < GW; ++kk) any |= s_cut[kk];
+        __syncthreads();
+        cut = any != 0;
+      }
+      if (cut) {
+        const float z = rr / pa;
+        const int nout = (es ? 1 : 0) + (en ? 1 : 0);
+        int incl = nout;  // inclusive prefix sum over the neuron's 32 slots
+#pragma unroll
+        for (int off = 1; off < 32; off <<= 1) {
+          const int y = __shfl_up(incl, off, 32);
+          if (i >= off) incl += y;
+        }
+        const int p = incl - nout;
+        const int ntot = __shfl(incl, 31, 32);
+        if (ntot > K2) ovf = 1;
+        int lo_i = 0, hi_i = K2 - 1;
+        for (int it = 0; it < logk2; ++it) {
+          const int mid = (lo_i + hi_i + 1) >> 1;
+          const bool le = __shfl(p, mid, 32) <= i;
+          lo_i = le ? mid : lo_i;
+          hi_i = le ? hi_i : mid - 1;
+        }
+        const int idx = lo_i;
+        // every shuffle runs on all lanes of the neuron: a bpermute reads 0 from a lane that
+        // is switched off, so none may sit behind a per-lane condition
+        const int d = i - __shfl(p, idx, 32);
+        const int g_es = __shfl(es ? 1 : 0, idx, 32);
+        const bool is_s = d == 0 && g_es != 0;
+        const float g_xl = __shfl(pxl, idx, 32), g_xr = __shfl(pxr, idx, 32);
+        const float g_z = __shfl(z, idx, 32), g_v = __shfl(v, idx, 32);
+        const float g_pa = __shfl(pa, idx, 32), g_po = __shfl(pof, idx, 32);
+        const int g_own = __shfl(pown, idx, 32);
+        const int n_new = min(ntot, K2);
+        const bool keep = i < n_new;
+        pxl = keep ? (is_s ? g_xl : nmax(g_xl, g_z)) : INFINITY;
+        pxr = keep ? (is_s ? nmin(g_xr, g_z) : g_xr) : INFINITY;
+        pu = keep ? (is_s ? u_r : g_v) : 0.0f;
+        pa = keep ? rho * g_pa : 1.0f;
+        pof = keep ? (is_s ? rho * g_po + q : rho * g_po) : 0.0f;
+        pown = keep ? g_own : -1;
+        npc = n_new;
+      } else if (valid) {
+        pu = es ? u_r : v;
+        pof = es ? rho * pof + q : rho * pof;
+        pa = rho * pa;
+      }
+      // 2. first-spike line of this step
+      const float sj = sS[ln][k], cj = sC[ln][k], whi = sHi[ln][k], wlo = sLo[ln][k];
+      const bool dl = i < nl && (ls * wlo + lc <= sj * wlo + cj) && (ls * whi + lc <= sj * whi + cj);
+      const bool dom = (__ballot(dl) & hmask) != 0ull;
+      const bool newc = (wlo < whi) && !dom && valid_n;
+      const float cx = sR[k] * rho;
+      if (newc && i == nl && nl < K1) {
+        ls = sj;
+        lc = cj;
+        lx = cx;
+      }
+      if (newc && nl >= K1) ovf = 1;
+      const float xlo = cx * wlo + q;
+      const float xhi = cx * whi + q;
+      const float pd = 4e-7f * (fabsf(xhi) + 1.0f);
+      if (newc && i == npc && npc < K2) {
+        pxl = xlo - pd;
+        pxr = xhi + pd;
+        pu = u_r;
+        pa = 1.0f;
+        pof = 0.0f;
+        pown = nl;
+      }
+      if (newc && npc >= K2) ovf = 1;
+      if (newc) {
+        nl = min(nl + 1, K1);
+        npc = min(npc + 1, K2);
+      }
     }
-    if (newc && nl >= K1) ovf = 1;
-    const float xlo = cx * wlo + q;
-    const float xhi = cx * whi + q;
-    const float pd = 4e-7f * (fabsf(xhi) + 1.0f);
-    if (newc && i == npc && npc < K2) {
-      pxl = xlo - pd;
-      pxr = xhi + pd;
-      pu = u_r;
-      pa = 1.0f;
-      pof = 0.0f;
-      pown = nl;
-    }
-    if (newc && npc >= K2) ovf = 1;
-    if (newc) {
-      nl = min(nl + 1, K1);
-      npc = min(npc + 1, K2);
-    }
-    wlo = nmax(wlo, (lu - cj) / sj);
-    R = rho * R;
+    __syncthreads();  // the tile's LDS rows are rewritten next
   }
+  const float A = sA[ln], B = sB[ln];
   if (!valid_n) return;
   if (i == 0) {
     MA[o] = A;
@@ -891,14 +959,14 @@ template <int BLK>
 static void launch_alif_build(const float* I, char* w, const lsh_alif_layout& L, int64_t N, int M,
                               int C, int K1, int K2, float beta, float rho, float q, float theta0,
                               float u_r, hipStream_t st) {
-  constexpr int WPB = BLK > 2 ? BLK / 2 : 1;
-  const int64_t per = (int64_t)WPB * 2;  // neurons per workgroup
-  const int NBLK = (int)((N + per - 1) / per);
+  constexpr int kAlifNPW = AlifBuildShape<BLK>::NPW;
+  const int NBLK = (int)((N + kAlifNPW - 1) / kAlifNPW);
   int logk2 = 0;
   while ((1 << logk2) < K2) ++logk2;
   auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
-  hipLaunchKernelGGL((k_alif_build<BLK>), dim3((unsigned)((int64_t)M * NBLK)), dim3(WAVE * WPB), 0, st,
+  hipLaunchKernelGGL((k_alif_build<BLK>), dim3((unsigned)((int64_t)M * NBLK)), dim3(WAVE * kAlifNPW / 2),
+                     0, st,
                      I, F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
                      Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),
                      F(L.PA), F(L.POF), N, NBLK, C, K1, K2, logk2, beta, rho, q, theta0, u_r);

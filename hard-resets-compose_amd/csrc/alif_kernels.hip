@@ -227,6 +227,7 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
       sLo[kAlifNPW][TS], sR[TS];
   __shared__ float sA[kAlifNPW], sB[kAlifNPW], sLU[kAlifNPW], sHU[kAlifNPW], sHW[kAlifNPW];
   __shared__ int s_cut[NW];
+  __shared__ int s_slot[NW][WAVE];
   const int64_t m = blockIdx.x / NBLK;
   const int blk = (int)(blockIdx.x - m * NBLK);
   const int tid = threadIdx.x;
@@ -324,28 +325,27 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
       if (cut) {
         const float z = rr / pa;
         const int nout = (es ? 1 : 0) + (en ? 1 : 0);
-        int incl = nout;  // inclusive prefix sum over the neuron's 32 slots
-#pragma unroll
-        for (int off = 1; off < 32; off <<= 1) {
-          const int y = __shfl_up(incl, off, 32);
-          if (i >= off) incl += y;
-        }
+        // inclusive prefix sum of the output counts over the neuron's 32 slots: row shifts
+        // within 16-lane rows, then the last lane of rows 0 / 2 added to rows 1 / 3 (DPP)
+        int incl = nout;
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);  // row_shr:1
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);  // row_shr:2
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);  // row_shr:4
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);  // row_shr:8
+        incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xA, 0xF, false);  // row_bcast:15
         const int p = incl - nout;
         const int ntot = __shfl(incl, 31, 32);
         if (ntot > K2) ovf = 1;
-        int lo_i = 0, hi_i = K2 - 1;
-        for (int it = 0; it < logk2; ++it) {
-          const int mid = (lo_i + hi_i + 1) >> 1;
-          const bool le = __shfl(p, mid, 32) <= i;
-          lo_i = le ? mid : lo_i;
-          hi_i = le ? hi_i : mid - 1;
-        }
-        const int idx = lo_i;
+        // every output slot learns its source piece (and whether it is the spiking part)
+        // from a scatter through this wave's LDS row (same-wave LDS accesses stay in order)
+        int* slot = s_slot[wv] + hb;
+        if (nout >= 1 && p < K2) slot[p] = (i << 1) | (es ? 1 : 0);
+        if (nout == 2 && p + 1 < K2) slot[p + 1] = i << 1;
+        const int src = slot[i];
+        const int idx = (src >> 1) & 31;
+        const bool is_s = (src & 1) != 0;
         // every shuffle runs on all lanes of the neuron: a bpermute reads 0 from a lane that
         // is switched off, so none may sit behind a per-lane condition
-        const int d = i - __shfl(p, idx, 32);
-        const int g_es = __shfl(es ? 1 : 0, idx, 32);
-        const bool is_s = d == 0 && g_es != 0;
         const float g_xl = __shfl(pxl, idx, 32), g_xr = __shfl(pxr, idx, 32);
         const float g_z = __shfl(z, idx, 32), g_v = __shfl(v, idx, 32);
         const float g_pa = __shfl(pa, idx, 32), g_po = __shfl(pof, idx, 32);

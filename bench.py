@@ -218,7 +218,8 @@ def bench_cfg5(torch, dev, reps):
     theta0=1, u_r=0, x~N(0.15,0.3^2), u0=w0=0.  alif() fwd+bwd with the parameter gradients:
     serial forward + scan adjoint, and the box scan (Wpred from alif_warm_predict(Wn=4), its
     cost included, dw=0.1q, C=128, K1=K2=32) + scan adjoint; plus the exact box scan with repair
-    (statistics) and the serial forward."""
+    for both predictions (warm-up, previous iterate) and dw in {0.1q, 0.3q} (statistics), and
+    the serial forward."""
     from lifscan import triton_alif as A
     T, N, beta, rho, q, C = 4096, 16384, 0.95, 0.995, 0.2, 128
     I = (0.15 + 0.3 * torch.randn(T, N, generator=torch.Generator().manual_seed(0))).to(dev)
@@ -238,15 +239,26 @@ def bench_cfg5(torch, dev, reps):
         out[f"alif_fwd_{fwd}_bwd_scan_ms"] = ev_time(step, reps, warm=2)
     out["serial_fwd_ms"] = ev_time(lambda: A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z), reps)
     U, W, S = A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z)
-    WP = A.alif_warm_predict(I, beta, rho, q, 1.0, 0.0, z, z, C, Wn=4)
-    st, ph = {}, {}
-    U2, W2, S2 = A.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, WP, 0.1 * q, C=C, K1=32, K2=32, BN=4,
-                                     repair=10 ** 6, stats=st, phases=ph)
-    out["box_scan_repair_equals_serial"] = bool(torch.equal(U2, U) and torch.equal(W2, W) and torch.equal(S2, S))
-    out["box_scan_repair_ms"] = ev_time(lambda: A.alif_scan_forward(
-        I, beta, rho, q, 1.0, 0.0, z, z, WP, 0.1 * q, C=C, K1=32, K2=32, BN=4, repair=10 ** 6), 3)
-    out["box_scan_stats"] = st
-    out["box_scan_phases_ms"] = {k: round(v, 4) for k, v in ph.items()}
+    # Two predictions of the chunk-entry adaptation (experiments/e25d_alif_fwd.py:44-50): the
+    # warm-up predictor, and the previous fitting iterate emulated by a 1.005x input.
+    _, Wprev, _ = A.alif_serial_forward((1.005 * I).contiguous(), beta, rho, q, 1.0, 0.0, z, z)
+    preds = {"warm4": A.alif_warm_predict(I, beta, rho, q, 1.0, 0.0, z, z, C, Wn=4),
+             "prev": A.alif_prev_wpred(Wprev, z, C)}
+    box = {}
+    for pname, WP in preds.items():
+        for dwq in (0.1, 0.3):
+            st, ph = {}, {}
+            U2, W2, S2 = A.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, WP, dwq * q, C=C, K1=32, K2=32,
+                                             BN=4, repair=10 ** 6, stats=st, phases=ph)
+            ms = ev_time(lambda: A.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, WP, dwq * q, C=C, K1=32,
+                                                     K2=32, BN=4, repair=10 ** 6), 3)
+            box[f"{pname}_dw{dwq}q"] = {
+                "ms": round(ms, 4),
+                "equals_serial": bool(torch.equal(U2, U) and torch.equal(W2, W) and torch.equal(S2, S)),
+                "stats": st, "phases_ms": {k: round(v, 4) for k, v in ph.items()}}
+            del U2, W2, S2
+    out["box_scan_repair"] = box
+    del Wprev, preds
     out["bwd_scan_ms"] = ev_time(lambda: A.alif_backward(I, U, W, S, gS, beta, rho, q, 1.0, z, z), reps)
     ns = T * N
     t = out["alif_fwd_serial_bwd_scan_ms"]
@@ -254,7 +266,7 @@ def bench_cfg5(torch, dev, reps):
     # ALIF algorithmic bytes: fwd read I, write U, W, S (16); bwd read I, U, W, S, gS, write dI (24)
     out["pct_roofline_fwd_bwd"] = round(100 * 40 * ns / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
     out["config"] = "ALIF N=16384, T=4096, beta=0.95, rho=0.995, q=0.2, x~N(0.15,0.3^2)"
-    del I, gS, U, W, S, U2, W2, S2, Ig
+    del I, gS, U, W, S, Ig
     torch.cuda.empty_cache()
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out.items()}
 

@@ -191,16 +191,21 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_fwd_fused(const float* __restri
   }
 }
 
-// PS (detached, no GU): also sums the parameter gradients of fit.py:43-47 in fp64 (u_{t-1}
-// and the spike bits of the chunk stay in registers) and writes one partials row per
-// workgroup: sum lam_t*u_{t-1}, sum gs_t*sg_t, sum s_t*lam_{t+1}.
-template <int C, int W, bool DETACH, bool HAS_GU, bool PS = false>
+// PS (detached, no GU) also sums parameter gradients in fp64 (u_{t-1} and the spike bits of
+// the chunk stay in registers) and writes one partials row per workgroup:
+//   PS == 1, hard reset (fit.py:43-47): sum lam_t*u_{t-1}, sum gs_t*sg_t, sum s_t*lam_{t+1};
+//   PS == 2, affine reset u <- gamma*v + delta (triton_affine.py:229-242), `u_r` carrying
+//            gamma (a detached reset needs no u_r): J_t = s_t ? gamma : 1, and the sums
+//            lam_t*u_{t-1}, s_t*v_t*lam_{t+1}, s_t*lam_{t+1}.  a_t = beta*J_t follows from
+//            the spike bit, so v_t takes the registers a_t would.
+template <int C, int W, bool DETACH, bool HAS_GU, int PS = 0>
 __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ U,
     const float* __restrict__ S, const float* __restrict__ GS, const float* __restrict__ GU,
     float* __restrict__ Lam, double* __restrict__ partials, int64_t N, int M, float beta,
     float theta, float u_r, float alpha) {
   static_assert(!PS || (DETACH && !HAS_GU && C <= 64), "parameter sums: detached, no GU");
+  constexpr bool AFF = PS == 2;
   __shared__ float sP[W][WAVE], sQ[W][WAVE];
   __shared__ float sLam[WAVE];
   __shared__ double sAcc[PS ? W : 1][3];
@@ -218,15 +223,22 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
   float* __restrict__ Lb = Lam + nb0;
   const float u0n = u0[nb0 + ln];
   double acc_b = 0.0, acc_t = 0.0, acc_r = 0.0;
+  const float gbeta = beta * u_r;  // AFF: beta*gamma
   if (w == 0) sLam[lane] = 0.0f;
   __syncthreads();
   const int rounds = (M + W - 1) / W;
   for (int r = 0; r < rounds; ++r) {
     const int m = M - 1 - (r * W + w);  // wave 0 holds the latest chunk of the round
     const bool active = m >= 0;
-    float a[C], b[C];
+    float a[AFF ? 1 : C], b[C];
     float upk[PS ? C : 1];
+    float vpk[AFF ? C : 1];
     unsigned long long sbits = 0;
+    // a_j: from the spike bit for the affine reset
+    auto aj = [&](int j) -> float {
+      if constexpr (AFF) return ((sbits >> j) & 1ull) ? gbeta : beta;
+      else return a[j];
+    };
     float lam = 0.0f;
     const size_t row0 = (size_t)(active ? m : 0) * C;
     const unsigned rstride = (unsigned)(N * 4);
@@ -245,19 +257,20 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
         const float sg = surrogate(v, theta, alpha);
         float J = 1.0f - s;
         if (!DETACH) J = J + (u_r - v) * sg;
-        a[j] = beta * J;
+        if constexpr (!AFF) a[j] = beta * J;
         b[j] = HAS_GU ? gs * sg + J * Buf(Hb + row0 * N).ld(lb, so) : gs * sg;
         if (PS) {
           upk[j] = up;
           if (s != 0.0f) sbits |= 1ull << j;
-          if (valid) acc_t += (double)b[j];
+          if (PS == 1 && valid) acc_t += (double)b[j];
+          if constexpr (AFF) vpk[j] = v;
         }
       }
       float P = 1.0f, Q = 0.0f;
 #pragma unroll
       for (int j = C - 1; j >= 0; --j) {
-        Q = b[j] + a[j] * Q;
-        P = a[j] * P;
+        Q = b[j] + aj(j) * Q;
+        P = aj(j) * P;
       }
       sP[w][lane] = P;
       sQ[w][lane] = Q;
@@ -270,12 +283,15 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
 #pragma unroll
       for (int j = C - 1; j >= 0; --j) {
         const float lam_next = lam;
-        lam = b[j] + a[j] * lam;
+        lam = b[j] + aj(j) * lam;
         if (valid) {
           bl.st_nt(sb, j * rstride, lam);
           if (PS) {
             acc_b += (double)lam * (double)upk[j];
-            if ((sbits >> j) & 1ull) acc_r += (double)lam_next;
+            if ((sbits >> j) & 1ull) {
+              acc_r += (double)lam_next;
+              if constexpr (AFF) acc_t += (double)vpk[j] * (double)lam_next;
+            }
           }
         }
       }
@@ -419,31 +435,37 @@ static void bwd_fused_c(const float* I, const float* u0, const float* U, const f
 template <int C, int W>
 static void launch_param_fused(const float* I, const float* u0, const float* U, const float* S,
                                const float* GS, float* Lam, double* partials, int64_t N, int M,
-                               float beta, float theta, float u_r, float alpha, hipStream_t st) {
+                               float beta, float theta, float u_r, float alpha, int ps,
+                               hipStream_t st) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
-  hipLaunchKernelGGL((k_lif_bwd_fused<C, W, true, false, true>), dim3((unsigned)NB), dim3(WAVE * W), 0,
-                     st, I, u0, U, S, GS, nullptr, Lam, partials, N, M, beta, theta, u_r, alpha);
+  if (ps == 2)
+    hipLaunchKernelGGL((k_lif_bwd_fused<C, W, true, false, 2>), dim3((unsigned)NB), dim3(WAVE * W), 0,
+                       st, I, u0, U, S, GS, nullptr, Lam, partials, N, M, beta, theta, u_r, alpha);
+  else
+    hipLaunchKernelGGL((k_lif_bwd_fused<C, W, true, false, 1>), dim3((unsigned)NB), dim3(WAVE * W), 0,
+                       st, I, u0, U, S, GS, nullptr, Lam, partials, N, M, beta, theta, u_r, alpha);
 }
 
 template <int C>
 static void param_fused_c(const float* I, const float* u0, const float* U, const float* S,
                           const float* GS, float* Lam, double* partials, int64_t N, int M, float beta,
-                          float theta, float u_r, float alpha, hipStream_t st) {
+                          float theta, float u_r, float alpha, int ps, hipStream_t st) {
   // u_{t-1} kept per step: 8 waves up to C = 32
   constexpr int WMAX = C <= 32 ? 8 : 4;
   const int W = fused_waves((N + WAVE - 1) / WAVE, WMAX);
   if constexpr (WMAX >= 8) {
     if (W == 8) {
-      launch_param_fused<C, 8>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st);
+      launch_param_fused<C, 8>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, ps, st);
       return;
     }
   }
-  launch_param_fused<C, 4>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st);
+  launch_param_fused<C, 4>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, ps, st);
 }
 
 int lif_param_bwd_fused(const float* I, const float* u0, const float* U, const float* S,
                         const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
-                        float beta, float theta, float u_r, float alpha, int C, hipStream_t st) {
+                        float beta, float theta, float u_r, float alpha, int C, int ps,
+                        hipStream_t st) {
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (C != 16 && C != 32 && C != 64) return LSH_ERR_SHAPE;
   if (T % C != 0) return LSH_ERR_DIVISIBILITY;
@@ -451,9 +473,15 @@ int lif_param_bwd_fused(const float* I, const float* u0, const float* U, const f
   if (T == 0 || N == 0) return LSH_OK;
   const int M = (int)(T / C);
   switch (C) {
-    case 16: param_fused_c<16>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st); break;
-    case 32: param_fused_c<32>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st); break;
-    default: param_fused_c<64>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st); break;
+    case 16:
+      param_fused_c<16>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, ps, st);
+      break;
+    case 32:
+      param_fused_c<32>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, ps, st);
+      break;
+    default:
+      param_fused_c<64>(I, u0, U, S, GS, Lam, partials, N, M, beta, theta, u_r, alpha, ps, st);
+      break;
   }
   LSH_CHECK_LAUNCH();
   return LSH_OK;

@@ -86,22 +86,29 @@ __global__ __launch_bounds__(64) void k_lif_fwd(const float* __restrict__ I,
 //                    (triton_lif.py:422-457 bwd_chunk_tiled_kernel).
 // Coefficients (triton_lif.py:43-50 _coef): v = beta*u_{t-1} + x_t, sg = surrogate'(v-theta),
 // J = 1 - s_t (+ (u_r - v)*sg when the reset is not detached), a = beta*J, b = gs*sg + J*gu.
-// PS (replay, detached, no GU): also sums the parameter gradients of fit.py:43-47 in fp64 and
-// writes one partials row per block: sum lam_t*u_{t-1}, sum gs_t*sg_t, sum s_t*lam_{t+1}.
-template <int D, bool COMPOSE, bool DETACH, bool HAS_GU, bool PS>
+// PS (detached, no GU): PS == 1, the replay also sums the parameter gradients of
+// fit.py:43-47 in fp64 and writes one partials row per block: sum lam_t*u_{t-1},
+// sum gs_t*sg_t, sum s_t*lam_{t+1}.  PS == 2, the affine reset u <- gamma*v + delta
+// (triton_affine.py:229-242) with `u_r` carrying gamma: J_t = s_t ? gamma : 1 (compose and
+// replay), and the replay's sums lam_t*u_{t-1}, s_t*v_t*lam_{t+1}, s_t*lam_{t+1}.
+template <int D, bool COMPOSE, bool DETACH, bool HAS_GU, int PS>
 __global__ __launch_bounds__(64) void k_lif_bwd(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ U,
     const float* __restrict__ S, const float* __restrict__ GS, const float* __restrict__ GU,
     const float* __restrict__ lam_end, float* __restrict__ Lam, float* __restrict__ PA,
     float* __restrict__ PB, double* __restrict__ partials, int64_t N, int64_t Ls, int NB,
     float beta, float theta, float u_r, float alpha) {
-  static_assert(!PS || (!COMPOSE && DETACH && !HAS_GU), "parameter sums: detached replay only");
+  static_assert(!PS || (DETACH && !HAS_GU), "parameter sums: detached, no GU");
+  static_assert(PS != 1 || !COMPOSE, "hard-reset sums: replay only");
+  constexpr bool AFF = PS == 2;
+  constexpr bool SUMS = PS != 0 && !COMPOSE;
+  const float gbeta = beta * u_r;  // AFF: beta*gamma
   const int64_t m = blockIdx.x / NB;
   const int nb = (int)(blockIdx.x - m * NB);
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
   double acc_b = 0.0, acc_t = 0.0, acc_r = 0.0;
   auto finish = [&]() {
-    if (!PS) return;
+    if (!SUMS) return;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       acc_b += __shfl_xor(acc_b, o, WAVE);
@@ -125,23 +132,24 @@ __global__ __launch_bounds__(64) void k_lif_bwd(
   const int64_t t_begin = m * Ls;
   const int64_t nt = Ls / D;
 
-  auto coef = [&](float up, float x, float s, float gs, float gu, float& a, float& bb) {
-    const float v = lif_v(up, x, beta);
+  auto coef = [&](float up, float x, float s, float gs, float gu, float& a, float& bb, float& v) {
+    v = lif_v(up, x, beta);
     const float sg = surrogate(v, theta, alpha);
     float J = 1.0f - s;
     if (!DETACH) J = J + (u_r - v) * sg;
-    a = beta * J;
+    a = AFF ? (s != 0.0f ? gbeta : beta) : beta * J;
     bb = HAS_GU ? gs * sg + J * gu : gs * sg;
   };
   auto uprev = [&](int64_t t) -> float { return t > 0 ? U[(size_t)(t - 1) * N + n] : u0n; };
   // one step of the replay: lam_{t+1} -> lam_t (bb = gs*sg when PS)
-  auto replay = [&](size_t o, float up, float s, float a, float bb) {
+  auto replay = [&](size_t o, float up, float s, float a, float bb, float v) {
     const float lam_next = lam;
     lam = bb + a * lam;
     st_nt(Lam + o, lam);
-    if (PS) {
+    if (SUMS) {
       acc_b += (double)lam * (double)up;
-      acc_t += (double)bb;
+      if (PS == 1) acc_t += (double)bb;
+      if (AFF) acc_t += s != 0.0f ? (double)v * (double)lam_next : 0.0;
       acc_r += s != 0.0f ? (double)lam_next : 0.0;
     }
   };
@@ -149,14 +157,14 @@ __global__ __launch_bounds__(64) void k_lif_bwd(
   // the highest `rem` steps first (segment lengths that are not a multiple of D)
   for (int64_t t = t_begin + Ls - 1; t >= t_begin + nt * D; --t) {
     const size_t o = (size_t)t * N + n;
-    float a, bb;
+    float a, bb, v;
     const float up = uprev(t), s = S[o];
-    coef(up, I[o], s, GS[o], HAS_GU ? GU[o] : 0.0f, a, bb);
+    coef(up, I[o], s, GS[o], HAS_GU ? GU[o] : 0.0f, a, bb, v);
     if (COMPOSE) {
       Q = bb + a * Q;
       P = a * P;
     } else {
-      replay(o, up, s, a, bb);
+      replay(o, up, s, a, bb, v);
     }
   }
   if (nt == 0) {
@@ -189,13 +197,13 @@ __global__ __launch_bounds__(64) void k_lif_bwd(
 #pragma unroll
     for (int jj = 0; jj < D; ++jj) {
       const int j = D - 1 - jj;
-      float a, bb;
-      coef(pa[j], xa[j], sa[j], ga[j], ha[j], a, bb);
+      float a, bb, v;
+      coef(pa[j], xa[j], sa[j], ga[j], ha[j], a, bb, v);
       if (COMPOSE) {
         Q = bb + a * Q;
         P = a * P;
       } else {
-        replay((size_t)(t0 + j) * N + n, pa[j], sa[j], a, bb);
+        replay((size_t)(t0 + j) * N + n, pa[j], sa[j], a, bb, v);
       }
     }
     if (more) {
@@ -681,7 +689,7 @@ static void launch_fwd_auto(const float* I, const float* starts, float* U, float
     launch_fwd<4>(I, starts, U, S, ends, N, Ls, M, beta, theta, u_r, st);
 }
 
-template <bool COMPOSE, bool DETACH, bool HAS_GU, bool PS = false>
+template <bool COMPOSE, bool DETACH, bool HAS_GU, int PS = 0>
 static void launch_bwd3(const float* I, const float* u0, const float* U, const float* S,
                         const float* GS, const float* GU, const float* lam_end, float* Lam, float* PA,
                         float* PB, int64_t N, int64_t Ls, int64_t M, float beta, float theta,
@@ -946,7 +954,12 @@ extern "C" int lsh_scan_stats_read(const void* ws, int64_t chunk_neurons, int64_
   const double sn = super_neurons > 0 ? (double)super_neurons : 1.0;
   out->repair_iters = (int64_t)h.repair_iters;
   out->overflow_frac = (double)h.ovf_count / cn;
-  if (alif) {
+  if (alif == 2) {  // affine reset: pieces kept, no +1
+    out->mean_pieces = (double)h.pieces_sum / cn;
+    out->max_pieces = (int64_t)h.pieces_max;
+    out->miss_frac = 0.0;
+    out->mean_lines = 0.0;
+  } else if (alif) {
     const unsigned long long miss = ((unsigned long long)h.miss_count_hi << 32) | h.miss_count_lo;
     out->mean_pieces = (double)h.alif_pieces_sum / cn;
     out->max_pieces = (int64_t)h.alif_pieces_max;
@@ -1020,27 +1033,33 @@ extern "C" int64_t lsh_lif_param_partials(int64_t T, int64_t N, int mode, int C)
   return (T / C) * NB;
 }
 
-extern "C" int lsh_lif_param_bwd(const float* I, const float* u0, const float* U, const float* S,
-                                 const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
-                                 float beta, float theta, float u_r, float alpha, int mode, int C,
-                                 void* ws, size_t ws_bytes, void* stream) {
+// The detached adjoint with parameter sums; ps 1: hard reset (fit.py), ps 2: affine reset
+// with `ur_or_gamma` = gamma (triton_affine.py:229-242).
+template <int PS>
+static int param_bwd(const float* I, const float* u0, const float* U, const float* S,
+                     const float* GS, float* Lam, double* partials, int64_t T, int64_t N, float beta,
+                     float theta, float ur_or_gamma, float alpha, int mode, int C, void* ws,
+                     size_t ws_bytes, void* stream) {
   if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(Lam) ||
       bad_ptr(partials))
     return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (mode < 0 || mode > 3) return LSH_ERR_ARG;
   hipStream_t st = (hipStream_t)stream;
-  if (mode == 3) return lif_param_bwd_lookback(I, u0, U, S, GS, Lam, partials, ws, ws_bytes, T, N,
-                                               beta, theta, u_r, alpha, st);
+  const float g = ur_or_gamma;
+  if (mode == 3)
+    return lif_param_bwd_lookback(I, u0, U, S, GS, Lam, partials, ws, ws_bytes, T, N, beta, theta, g,
+                                  alpha, PS, st);
   if (mode == 0) {
     if (T == 0 || N == 0) return LSH_OK;
-    launch_bwd3<false, true, false, true>(I, u0, U, S, GS, nullptr, nullptr, Lam, nullptr, nullptr, N,
-                                          T, 1, beta, theta, u_r, alpha, st, partials);
+    launch_bwd3<false, true, false, PS>(I, u0, U, S, GS, nullptr, nullptr, Lam, nullptr, nullptr, N, T,
+                                        1, beta, theta, g, alpha, st, partials);
     LSH_CHECK_LAUNCH();
     return LSH_OK;
   }
-  if (mode == 2) return lif_param_bwd_fused(I, u0, U, S, GS, Lam, partials, T, N, beta, theta, u_r,
-                                            alpha, C, st);
+  if (mode == 2)
+    return lif_param_bwd_fused(I, u0, U, S, GS, Lam, partials, T, N, beta, theta, g, alpha, C, PS,
+                               st);
   const int rc = bwd_check(T, N, C);
   if (rc != LSH_OK) return rc;
   if (bad_ptr(ws) || ws_bytes < lsh_lif_scan_bwd_workspace(T, N, C) ||
@@ -1053,12 +1072,30 @@ extern "C" int lsh_lif_param_bwd(const float* I, const float* u0, const float* U
   float* PA = reinterpret_cast<float*>(w);
   float* PB = reinterpret_cast<float*>(w + mn);
   float* LE = reinterpret_cast<float*>(w + 2 * mn);
-  launch_bwd3<true, true, false>(I, u0, U, S, GS, nullptr, nullptr, nullptr, PA, PB, N, C, M, beta,
-                                 theta, u_r, alpha, st);
+  // the compose pass needs the affine reset's J, not the sums
+  launch_bwd3<true, true, false, PS == 2 ? 2 : 0>(I, u0, U, S, GS, nullptr, nullptr, nullptr, PA, PB,
+                                                  N, C, M, beta, theta, g, alpha, st);
   hipLaunchKernelGGL(k_lif_bwd_carry, dim3((unsigned)((N + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, PA,
                      PB, LE, N, (int)M);
-  launch_bwd3<false, true, false, true>(I, u0, U, S, GS, nullptr, LE, Lam, nullptr, nullptr, N, C, M,
-                                        beta, theta, u_r, alpha, st, partials);
+  launch_bwd3<false, true, false, PS>(I, u0, U, S, GS, nullptr, LE, Lam, nullptr, nullptr, N, C, M,
+                                      beta, theta, g, alpha, st, partials);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
+}
+
+extern "C" int lsh_lif_param_bwd(const float* I, const float* u0, const float* U, const float* S,
+                                 const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
+                                 float beta, float theta, float u_r, float alpha, int mode, int C,
+                                 void* ws, size_t ws_bytes, void* stream) {
+  return param_bwd<1>(I, u0, U, S, GS, Lam, partials, T, N, beta, theta, u_r, alpha, mode, C, ws,
+                      ws_bytes, stream);
+}
+
+extern "C" int lsh_aff_bwd(const float* I, const float* u0, const float* U, const float* S,
+                           const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
+                           float beta, float theta, float gamma, float alpha, int mode, int C,
+                           void* ws, size_t ws_bytes, void* stream) {
+  if (!(gamma >= 0.0f && gamma <= 1.0f)) return LSH_ERR_ARG;
+  return param_bwd<2>(I, u0, U, S, GS, Lam, partials, T, N, beta, theta, gamma, alpha, mode, C, ws,
+                      ws_bytes, stream);
 }

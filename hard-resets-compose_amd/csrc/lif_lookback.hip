@@ -57,9 +57,10 @@ __device__ __forceinline__ int flag_wait(int* f, unsigned int* timeouts) {
   return -1;
 }
 
-// PS (detached, no GU): the parameter sums of fit.py:43-47 in fp64, one partials row per
-// workgroup (tile): sum lam_t*u_{t-1}, sum gs_t*sg_t, sum s_t*lam_{t+1}.
-template <int C, int W, bool DETACH, bool HAS_GU, bool PS = false>
+// PS (detached, no GU): parameter sums in fp64, one partials row per workgroup (tile), as
+// k_lif_bwd_fused: PS == 1 the hard reset's (fit.py:43-47), PS == 2 the affine reset's
+// (triton_affine.py:229-242) with `u_r` carrying gamma.
+template <int C, int W, bool DETACH, bool HAS_GU, int PS = 0>
 __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ U,
     const float* __restrict__ S, const float* __restrict__ GS, const float* __restrict__ GU,
@@ -67,6 +68,7 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
     float* __restrict__ incl, int* __restrict__ flags, WsHeader* hdr, double* __restrict__ partials,
     int64_t N, int NB, int NSEG, float beta, float theta, float u_r, float alpha) {
   static_assert(!PS || (DETACH && !HAS_GU && C <= 64), "parameter sums: detached, no GU");
+  constexpr bool AFF = PS == 2;
   __shared__ float sP[W][WAVE], sQ[W][WAVE];
   __shared__ float sLamEnd[WAVE];
   __shared__ double sAcc[PS ? W : 1][3];
@@ -87,9 +89,15 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
   const float u0n = u0[nb0 + ln];
 
   // 1. coefficients of the chunk and its map
-  float a[C], b[C];
+  float a[AFF ? 1 : C], b[C];
   float upk[PS ? C : 1];
+  float vpk[AFF ? C : 1];
   unsigned long long sbits = 0;
+  const float gbeta = beta * u_r;  // AFF: beta*gamma
+  auto aj = [&](int j) -> float {
+    if constexpr (AFF) return ((sbits >> j) & 1ull) ? gbeta : beta;
+    else return a[j];
+  };
   double acc_b = 0.0, acc_t = 0.0, acc_r = 0.0;
   {
     const Buf bi(I + nb0 + row0 * N), bs(S + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
@@ -106,20 +114,21 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
       const float sg = surrogate(v, theta, alpha);
       float J = 1.0f - s;
       if (!DETACH) J = J + (u_r - v) * sg;
-      a[j] = beta * J;
+      if constexpr (!AFF) a[j] = beta * J;
       b[j] = HAS_GU ? gs * sg + J * Buf(GU + nb0 + row0 * N).ld(lb, so) : gs * sg;
       if (PS) {
         upk[j] = up;
         if (s != 0.0f) sbits |= 1ull << j;
-        if (valid) acc_t += (double)b[j];
+        if (PS == 1 && valid) acc_t += (double)b[j];
+        if constexpr (AFF) vpk[j] = v;
       }
     }
   }
   float P = 1.0f, Q = 0.0f;
 #pragma unroll
   for (int j = C - 1; j >= 0; --j) {
-    Q = b[j] + a[j] * Q;
-    P = a[j] * P;
+    Q = b[j] + aj(j) * Q;
+    P = aj(j) * P;
   }
   sP[w][lane] = P;
   sQ[w][lane] = Q;
@@ -170,12 +179,15 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
 #pragma unroll
   for (int j = C - 1; j >= 0; --j) {
     const float lam_next = lam;
-    lam = b[j] + a[j] * lam;
+    lam = b[j] + aj(j) * lam;
     if (valid) {
       bl.st_nt(sb, j * rstride, lam);
       if (PS) {
         acc_b += (double)lam * (double)upk[j];
-        if ((sbits >> j) & 1ull) acc_r += (double)lam_next;
+        if ((sbits >> j) & 1ull) {
+          acc_r += (double)lam_next;
+          if constexpr (AFF) acc_t += (double)vpk[j] * (double)lam_next;
+        }
       }
     }
   }
@@ -207,7 +219,7 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
   }
 }
 
-template <int C, int W, bool DETACH, bool HAS_GU, bool PS = false>
+template <int C, int W, bool DETACH, bool HAS_GU, int PS = 0>
 static void launch_lookback(const float* I, const float* u0, const float* U, const float* S,
                             const float* GS, const float* GU, float* Lam, char* ws, int64_t N,
                             int NSEG, float beta, float theta, float u_r, float alpha,
@@ -299,7 +311,7 @@ extern "C" int lsh_lif_scan_lookback_bwd(const float* I, const float* u0, const 
 int lsh::lif_param_bwd_lookback(const float* I, const float* u0, const float* U, const float* S,
                                 const float* GS, float* Lam, double* partials, void* ws,
                                 size_t ws_bytes, int64_t T, int64_t N, float beta, float theta,
-                                float u_r, float alpha, hipStream_t st) {
+                                float u_r, float alpha, int ps, hipStream_t st) {
   if (bad_ptr(ws)) return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (T % kLookbackSeg != 0) return LSH_ERR_DIVISIBILITY;
@@ -309,8 +321,12 @@ int lsh::lif_param_bwd_lookback(const float* I, const float* u0, const float* U,
   const int64_t NSEG = T / kLookbackSeg;
   if (NSEG * ((N + WAVE - 1) / WAVE) > ((int64_t)1 << 31) - 1) return LSH_ERR_SHAPE;
   if (T == 0 || N == 0) return LSH_OK;
-  launch_lookback<16, 16, true, false, true>(I, u0, U, S, GS, nullptr, Lam, static_cast<char*>(ws),
-                                             N, (int)NSEG, beta, theta, u_r, alpha, st, partials);
+  if (ps == 2)
+    launch_lookback<16, 16, true, false, 2>(I, u0, U, S, GS, nullptr, Lam, static_cast<char*>(ws), N,
+                                            (int)NSEG, beta, theta, u_r, alpha, st, partials);
+  else
+    launch_lookback<16, 16, true, false, 1>(I, u0, U, S, GS, nullptr, Lam, static_cast<char*>(ws), N,
+                                            (int)NSEG, beta, theta, u_r, alpha, st, partials);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }

@@ -60,16 +60,18 @@ __global__ void k_ws_header_reset(WsHeader* h);
 
 inline bool bad_ptr(const void* p) { return p == nullptr; }
 
-// Single-pass detached LIF adjoint with the fit.py parameter sums (lif_fused.hip); partials
-// gets one row of 3 doubles per 64-neuron block.  Returns an LSH_* status.
+// Single-pass detached adjoint with parameter sums (lif_fused.hip); partials gets one row of
+// 3 doubles per 64-neuron block.  ps 1: the hard reset's fit.py sums; ps 2: the affine
+// reset's (u_r carries gamma).  Returns an LSH_* status.
 int lif_param_bwd_fused(const float* I, const float* u0, const float* U, const float* S,
                         const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
-                        float beta, float theta, float u_r, float alpha, int C, hipStream_t st);
+                        float beta, float theta, float u_r, float alpha, int C, int ps,
+                        hipStream_t st);
 // The same with the look-back adjoint (lif_lookback.hip); one partials row per (256-step
 // segment, 64-neuron block); workspace as lsh_lif_scan_lookback_bwd.
 int lif_param_bwd_lookback(const float* I, const float* u0, const float* U, const float* S,
                            const float* GS, float* Lam, double* partials, void* ws,
                            size_t ws_bytes, int64_t T, int64_t N, float beta, float theta,
-                           float u_r, float alpha, hipStream_t st);
+                           float u_r, float alpha, int ps, hipStream_t st);
 
 }  // namespace lsh

@@ -55,6 +55,12 @@ class V4Layout(ctypes.Structure):
         "SA", "SB", "SN", "SOVF", "SX", "SC", "SSTARTS", "total")]
 
 
+class AffLayout(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in (
+        "EC", "EA", "EB", "HC", "HA", "HB", "LO", "HI", "PIECES", "NP", "OVF", "STARTS", "ENDS",
+        "LIST0", "LIST1", "total")]
+
+
 class ALIFLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in (
         "EC", "EA", "EB", "LU", "HU", "LW", "HW", "MA", "MB", "NL", "NP", "OVF", "LS", "LC", "LX",
@@ -107,6 +113,14 @@ SIGNATURES = {
                                 c_i, c_i, c_p, c_sz, c_p]),
     "lsh_alif_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f,
                            c_f, c_f, c_f, c_f, c_i, c_i, c_p, c_sz, c_p]),
+    "lsh_aff_serial_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f, c_p]),
+    "lsh_aff_scan_workspace": (c_sz, [c_i64, c_i64, c_i, c_i]),
+    "lsh_aff_scan_layout": (c_i, [c_i64, c_i64, c_i, c_i, ctypes.POINTER(AffLayout)]),
+    "lsh_aff_scan_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f, c_f, c_i, c_i,
+                               c_i64, c_p, c_sz, c_p]),
+    "lsh_aff_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f, c_i,
+                          c_i, c_p, c_sz, c_p]),
+    "lsh_reverse_affine_scan": (c_i, [c_p, c_p, c_p, c_i64, c_i64, c_p]),
     "lsh_lif_scan_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
     "lsh_lif_scan_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f,
                                c_i, c_i, c_p, c_sz, c_p]),
@@ -162,6 +176,7 @@ def workspace(nbytes, device):
 
 
 def read_stats(ws, chunk_neurons, super_neurons=0, alif=False):
+    """alif: False (LIF), True (ALIF) or 2 (affine reset)."""
     st = ScanStats()
     check(lib().lsh_scan_stats_read(ptr(ws), int(chunk_neurons), int(super_neurons), int(alif),
                                     ctypes.byref(st), stream_of(ws)), "lsh_scan_stats_read")

@@ -68,6 +68,19 @@ def alif_warm_predict(I, beta, rho, q, theta0, u_r, u0, w0, C, Wn=4, u_init=0.0,
     return WP
 
 
+def alif_prev_wpred(Wprev, w0, C):
+    """Chunk-entry adaptation taken from the previous fitting iterate's W [T, N]
+    (experiments/e28_allen_alif.py:36): row 0 is w0, row m the adaptation after step m*C - 1.
+    A strided device copy of M rows; nothing goes through the host."""
+    Wprev = _input(Wprev)
+    T, N = Wprev.shape
+    C = int(C)
+    if T % C:
+        raise ValueError(f"T={T} is not a multiple of C={C}")
+    w0 = _vec(w0, N, Wprev, "w0")
+    return torch.cat([w0[None], Wprev[C - 1:-1:C]], 0).contiguous()
+
+
 class _ALIFRun:
     """Workspace of one box-scan call (maps, box, chunk states) for stats and tests."""
 

@@ -96,12 +96,14 @@ int lsh_lif_chunked_serial_fwd(const float* I, const float* u0, float* U, float*
 
 /* Diagnostics of the last scan run in `ws` (synchronizes `stream`).  Same definitions as
  * the reference's stats dict: triton_lif.py:812-816 (v3), :976-982 (v4),
- * triton_alif.py:351-357 (ALIF). */
+ * triton_alif.py:351-357 (ALIF, alif = 1), triton_affine.py:195-198 (affine reset,
+ * alif = 2). */
 typedef struct lsh_scan_stats {
   int64_t repair_iters;
   double overflow_frac;
-  double mean_pieces; /* mean(kept breakpoints) + 1 for LIF; mean(x-pieces) for ALIF */
-  int64_t max_pieces; /* max(kept breakpoints) + 1 for LIF; max(x-pieces) for ALIF */
+  double mean_pieces; /* mean(kept breakpoints) + 1 for LIF; mean(x-pieces) for ALIF;
+                         mean(pieces) for the affine reset */
+  int64_t max_pieces; /* the same maxima */
   double super_overflow_frac;
   double super_mean_pieces;
   int64_t super_max_pieces;
@@ -234,6 +236,53 @@ int lsh_lif_param_bwd(const float* I, const float* u0, const float* U, const flo
                       const float* GS, float* Lam, double* partials, int64_t T, int64_t N,
                       float beta, float theta, float u_r, float alpha, int mode, int C, void* ws,
                       size_t ws_bytes, void* stream);
+
+/* ---- affine reset  u <- gamma*v + delta, 0 <= gamma <= 1 (triton_affine.py) -------------
+ *   v = fl(fl(beta*u) + x);  s = v >= theta;  u' = s ? fl(fl(gamma*v) + delta) : v
+ *                                                                  (triton_affine.py:19-23)
+ * gamma outside [0, 1] (or NaN) is LSH_ERR_ARG. */
+
+/* Serial forward.  Replaces triton_affine.py:143-162 (aff_run_kernel, aff_serial_forward). */
+int lsh_aff_serial_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
+                       int64_t N, float beta, float theta, float gamma, float delta, void* stream);
+
+/* Exact two-level scan.  Replaces triton_affine.py:165-199 (aff_scan_forward) with its
+ * kernels :26-48 (upper envelope), :51-111 (build), :114-140 (carry), :143-155 (replay) and
+ * the repair loop :188-194 (run on device; `repair` bounds the rounds as there).
+ * r_theta: the lower envelope's reset value gamma*theta + delta as the caller rounds it (the
+ * reference computes it in double and passes it as fp32, :171).  C >= 1, T % C == 0,
+ * 1 <= K <= 32.  Workspace lsh_aff_scan_workspace(T, N, C, K) bytes, 256-byte aligned; its
+ * arrays (for tests and diagnostics) at the offsets of lsh_aff_scan_layout: */
+typedef struct lsh_aff_layout {
+  size_t EC, EA, EB, HC, HA, HB; /* lower / upper chunk envelope maps [M, N] */
+  size_t LO, HI;                 /* envelope bounds at chunk starts [M, N] */
+  size_t PIECES;                 /* [M, N, K] float4 (xl, xr, a, c) */
+  size_t NP, OVF;                /* int32 [M, N]: pieces kept, overflow flag */
+  size_t STARTS, ENDS;           /* chunk start / end states [M, N] */
+  size_t LIST0, LIST1;           /* repair work lists */
+  size_t total;
+} lsh_aff_layout;
+size_t lsh_aff_scan_workspace(int64_t T, int64_t N, int C, int K);
+int lsh_aff_scan_layout(int64_t T, int64_t N, int C, int K, lsh_aff_layout* out);
+int lsh_aff_scan_fwd(const float* I, const float* u0, float* U, float* S, int64_t T, int64_t N,
+                     float beta, float theta, float gamma, float delta, float r_theta, int C,
+                     int K, int64_t repair, void* ws, size_t ws_bytes, void* stream);
+
+/* Adjoint of LIFAffineFn (triton_affine.py:229-242; the reference solves it with a torch
+ * Hillis-Steele scan, :202-211): lam_t = gs_t*sg_t + beta*J_t*lam_{t+1}, J_t = s_t ? gamma : 1
+ * (detached spike), Lam = lam = dL/dI, plus per block partials[P][3] (fp64) =
+ * (sum lam_t*u_{t-1}, sum s_t*v_t*lam_{t+1}, sum s_t*lam_{t+1}), whose column sums give
+ * dbeta, dgamma / beta and ddelta / beta.  mode, C, workspace and P as lsh_lif_param_bwd. */
+int lsh_aff_bwd(const float* I, const float* u0, const float* U, const float* S, const float* GS,
+                float* Lam, double* partials, int64_t T, int64_t N, float beta, float theta,
+                float gamma, float alpha, int mode, int C, void* ws, size_t ws_bytes,
+                void* stream);
+
+/* L[t] = A[t]*L[t+1] + B[t] with L[T] = 0, per column of [T, N] arrays (two roundings per
+ * step, rows from the last).  Replaces triton_affine.py:202-211 and fast.py:307-323
+ * (reverse_affine_scan; there a Hillis-Steele scan, so the bits differ by reassociation). */
+int lsh_reverse_affine_scan(const float* A, const float* B, float* L, int64_t T, int64_t N,
+                            void* stream);
 
 /* ALIF adjoint: LW[t] = dL/dw_t, LV[t] = dL/dv_t (= dL/dI_t) for dL/dS = GS.
  * mode 0: fused serial sweep (triton_alif.py:444-487); 1: chunked two-level affine scans of

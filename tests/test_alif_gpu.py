@@ -82,6 +82,21 @@ def _preds(I, beta, rho, q, u0, w0, C):
         "bad": (Wentry + 5 * q).astype(np.float32)}
 
 
+def test_alif_prev_wpred(AL, dev):
+    """The previous-iterate prediction (experiments/e28_allen_alif.py:36): row 0 = w0, row m =
+    W[m*C - 1]; non-multiple T is rejected."""
+    T, N, C = 1024, 70, 128
+    W = uniform(T * N, -1.0, 1.0, 21).reshape(T, N)
+    w0 = uniform(N, 0.0, 0.1, 22)
+    P = host(AL.alif_prev_wpred(gpu(W, dev), gpu(w0, dev), C))
+    assert P.shape == (T // C, N)
+    assert np.array_equal(P[0], w0)
+    for m in range(1, T // C):
+        assert np.array_equal(P[m], W[m * C - 1])
+    with pytest.raises(ValueError):
+        AL.alif_prev_wpred(gpu(W[:1000], dev), gpu(w0, dev), C)
+
+
 @pytest.mark.parametrize("name,beta,rho,q", NEURONS)
 @pytest.mark.parametrize("block", [1, 4])
 def test_alif_box_scan_matches_oracle(AL, dev, name, beta, rho, q, block):

@@ -64,3 +64,29 @@ def test_null_pointer_rejected_before_launch():
     rc = L.lsh_lif_scan_v3_fwd(None, None, None, None, 16, 16, 0.9, 1.0, 0.0, 8, 4, 0, None, 0,
                                None)
     assert rc == -1
+
+
+def test_affine_reset_host_checks():
+    """Affine-reset entry points: workspace and layout queries, and arguments rejected before
+    any launch (gamma outside [0, 1], null pointers)."""
+    from lifscan import _native
+    L = _native.lib()
+    assert L.lsh_aff_scan_workspace(8192, 200, 128, 32) > 0
+    assert L.lsh_aff_scan_workspace(8191, 200, 128, 32) == 0  # T % C
+    assert L.lsh_aff_scan_workspace(8192, 200, 128, 33) == 0  # K > 32
+    assert L.lsh_aff_scan_workspace(8192, 200, 128, 0) == 0
+    lay = _native.AffLayout()
+    assert L.lsh_aff_scan_layout(8192, 200, 128, 32, ctypes.byref(lay)) == 0
+    assert lay.total == L.lsh_aff_scan_workspace(8192, 200, 128, 32)
+    offs = [getattr(lay, f) for f, _ in _native.AffLayout._fields_ if f != "total"]
+    assert all(o % 256 == 0 for o in offs) and offs == sorted(offs)
+    # pieces: [M, N, K] float4
+    assert lay.NP - lay.PIECES >= 64 * 200 * 32 * 16
+    fake = ctypes.c_void_p(256)  # never dereferenced: the checks fail first
+    assert L.lsh_aff_serial_fwd(fake, fake, fake, fake, 16, 16, 0.9, 1.0, 1.5, 0.0, None) == -1
+    assert L.lsh_aff_serial_fwd(None, fake, fake, fake, 16, 16, 0.9, 1.0, 0.5, 0.0, None) == -1
+    assert L.lsh_aff_scan_fwd(fake, fake, fake, fake, 16, 16, 0.9, 1.0, -0.1, 0.0, 0.0, 8, 8, 0,
+                              fake, 1 << 20, None) == -1
+    assert L.lsh_aff_bwd(fake, fake, fake, fake, fake, fake, fake, 16, 16, 0.9, 1.0, 2.0, 4.0, 0, 1,
+                         None, 0, None) == -1
+    assert L.lsh_reverse_affine_scan(None, fake, fake, 4, 4, None) == -1

@@ -271,6 +271,62 @@ def bench_cfg5(torch, dev, reps):
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out.items()}
 
 
+def bench_affine(torch, dev, reps):
+    """Affine reset u <- gamma*v + delta (triton_affine.py; no published number).
+    (a) the reference's own test shape (tests/test_affine.py:7-18): T=8192, N=200, beta=0.9,
+        x~N(0.15,0.4^2), u0~N(0,0.2^2), C=128, K=32: serial forward vs the scan with repair
+        (bit-identical) for gamma, delta = (0.3, -0.1) and (1, -1);
+    (b) the cfg2 shape (65536 x T=4096, beta=0.9, x~N(0.12,0.25^2), u0=0) with gamma=0.5,
+        delta=-0.25: lif_affine fwd (serial) + bwd with the five gradients through autograd, and
+        the adjoint alone against its 20 B/neuron-step roofline."""
+    from lifscan import triton_affine as AF
+    out = {}
+    T, N = 8192, 200
+    g = torch.Generator().manual_seed(0)
+    I = (0.15 + 0.4 * torch.randn(T, N, generator=g)).to(dev)
+    u0 = (0.2 * torch.randn(N, generator=g)).to(dev)
+    for gamma, delta in ((0.3, -0.1), (1.0, -1.0)):
+        tag = f"small_g{gamma}_d{delta}"
+        Ur, Sr = AF.aff_serial_forward(I, 0.9, 1.0, gamma, delta, u0)
+        st = {}
+        U, S = AF.aff_scan_forward(I, 0.9, 1.0, gamma, delta, u0, C=128, K=32, repair=10 ** 6, stats=st)
+        out[tag] = {
+            "serial_fwd_ms": round(ev_time(lambda: AF.aff_serial_forward(I, 0.9, 1.0, gamma, delta, u0), reps), 4),
+            "scan_repair_ms": round(ev_time(lambda: AF.aff_scan_forward(
+                I, 0.9, 1.0, gamma, delta, u0, C=128, K=32, repair=10 ** 6), reps), 4),
+            "scan_equals_serial": bool(torch.equal(U, Ur) and torch.equal(S, Sr)),
+            "stats": st}
+    del I, u0, U, S, Ur, Sr
+    T, N = T_CFG, N_CFG
+    I = (0.12 + 0.25 * torch.randn(T, N, generator=torch.Generator().manual_seed(0))).to(dev)
+    gS = torch.randn(T, N, generator=torch.Generator().manual_seed(1)).to(dev)
+    z = torch.zeros(N, device=dev)
+    ps = [torch.tensor(v, device=dev, requires_grad=True) for v in (0.9, 0.5, -0.25)]
+    Ig = I.clone().requires_grad_(True)
+
+    def step():
+        Ig.grad = None
+        for p in ps:
+            p.grad = None
+        S = AF.lif_affine(Ig, z, *ps, mode="serial")
+        S.backward(gS)
+    t = ev_time(step, reps, warm=2)
+    U, S = AF.aff_serial_forward(I, 0.9, 1.0, 0.5, -0.25, z)
+    tb = ev_time(lambda: AF._aff_backward(I, z, U, S, gS, 0.9, 1.0, 0.5, 4.0), reps)
+    ns = T * N
+    out["cfg2_shape"] = {
+        "lif_affine_fwd_bwd_ms": round(t, 4),
+        "fwd_bwd_value": round(ns / (t / 1000.0), 1),
+        "pct_roofline_fwd_bwd": round(100 * (B_FWD + B_BWD) * ns / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2),
+        "serial_fwd_ms": round(ev_time(lambda: AF.aff_serial_forward(I, 0.9, 1.0, 0.5, -0.25, z), reps), 4),
+        "bwd_with_param_sums_ms": round(tb, 4),
+        "pct_roofline_bwd": round(100 * B_BWD * ns / (tb / 1000.0) / 1e9 / HBM_PEAK_GBS, 2),
+        "config": "65536 x 4096, beta=0.9, gamma=0.5, delta=-0.25, x~N(0.12,0.25^2)"}
+    del I, gS, U, S, Ig
+    torch.cuda.empty_cache()
+    return out
+
+
 def dominant_only(L, torch, dev):
     """Short program for counter passes: a 256 MiB copy (FETCH/WRITE calibration), then the
     dominant kernel (single-pass backward, cfg2) three times."""
@@ -298,8 +354,8 @@ def main():
     ap.add_argument("--cpu-cols", type=int, default=8192)
     ap.add_argument("--dominant-only", action="store_true")
     ap.add_argument("--headline-only", action="store_true",
-                    help="skip the cfg3 / cfg4 / cfg5 measurements")
-    ap.add_argument("--only", choices=("cfg3", "cfg4", "cfg5"),
+                    help="skip the cfg3 / cfg4 / cfg5 / affine-reset measurements")
+    ap.add_argument("--only", choices=("cfg3", "cfg4", "cfg5", "affine"),
                     help="measure one of the other configurations only (for profiling runs); "
                          "prints its JSON, not the headline line")
     args = ap.parse_args()
@@ -318,7 +374,8 @@ def main():
         dominant_only(L, torch, dev)
         return
     if args.only:
-        fn = {"cfg3": bench_cfg3, "cfg4": bench_cfg4, "cfg5": bench_cfg5}[args.only]
+        fn = {"cfg3": bench_cfg3, "cfg4": bench_cfg4, "cfg5": bench_cfg5,
+              "affine": bench_affine}[args.only]
         print(json.dumps({args.only: fn(torch, dev, 5)}))
         return
     T, N, beta, K = T_CFG, N_CFG, 0.9, 8
@@ -390,7 +447,8 @@ def main():
         del I
         torch.cuda.empty_cache()
         others = {}
-        for name, fn in (("cfg3", bench_cfg3), ("cfg5", bench_cfg5), ("cfg4", bench_cfg4)):
+        for name, fn in (("cfg3", bench_cfg3), ("cfg5", bench_cfg5), ("cfg4", bench_cfg4),
+                         ("affine", bench_affine)):
             log(f"{name}")
             others[name] = fn(torch, dev, 5)
             log(f"{name} " + json.dumps(others[name]))

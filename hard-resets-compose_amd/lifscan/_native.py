@@ -121,6 +121,10 @@ SIGNATURES = {
     "lsh_aff_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f, c_i,
                           c_i, c_p, c_sz, c_p]),
     "lsh_reverse_affine_scan": (c_i, [c_p, c_p, c_p, c_i64, c_i64, c_p]),
+    "lsh_soft_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
+    "lsh_soft_bwd_partials": (c_i64, [c_i64, c_i64, c_i]),
+    "lsh_soft_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, ctypes.c_double, c_f, c_f,
+                           c_i, c_p, c_sz, c_p]),
     "lsh_lif_scan_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
     "lsh_lif_scan_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f,
                                c_i, c_i, c_p, c_sz, c_p]),

@@ -7,8 +7,10 @@ u_r), the interface of the reference's ``lifscan/fit.py`` (LIFParamFn, lif_param
 
 with lambda_t = dL/dv_t from the adjoint.  The three sums are accumulated in fp64 inside the
 adjoint kernel (lsh_lif_param_bwd), one row per block, so no [T, N] temporaries are formed.
-The reference's CPU prototype backend (LIFParamFnCPU) and the soft-reset layers are not part
-of this package.
+
+The soft-reset layers (LIFSoftFn / lif_soft, LIFSoftScanFn / lif_soft_scan, fit.py:93-153) give
+gradients for I, u0 and beta; their adjoint is lsh_soft_bwd (float64 recurrence, dbeta summed in
+the kernel).  The reference's CPU prototype backend (LIFParamFnCPU) is not part of this package.
 """
 import torch
 
@@ -87,3 +89,66 @@ def lif_param(I, u0, beta, theta, u_r, alpha=4.0, mode="auto", K=16):
         fwd = bwd = mode
     t = lambda v: v if torch.is_tensor(v) else torch.tensor(float(v), device=I.device)
     return LIFParamFn.apply(I, u0, t(beta), t(theta), t(u_r), alpha, fwd, bwd, K)
+
+
+class LIFSoftFn(torch.autograd.Function):
+    """Soft (subtractive) reset LIF, serial forward; gradients for I, u0, beta (fit.py:93-114)."""
+
+    @staticmethod
+    def forward(ctx, I, u0, beta, theta, alpha):
+        from . import hip_soft as TS
+        b, th = _f32s(beta, theta)
+        I = I.contiguous()
+        U, S = TS.soft_serial_forward(I, b, th, u0)
+        ctx.save_for_backward(I, u0, U)
+        ctx.cfg = (b, th, float(alpha))
+        return S
+
+    @staticmethod
+    def backward(ctx, gS):
+        from . import hip_soft as TS
+        I, u0, U = ctx.saved_tensors
+        b, th, alpha = ctx.cfg
+        need_b = ctx.needs_input_grad[2]
+        lam, db = TS._soft_backward(I, u0, U, gS.contiguous(), b, th, alpha, need_b)
+        return lam, b * lam[0], (db.float().reshape(()) if need_b else None), None, None
+
+
+def lif_soft(I, u0, beta, theta=1.0, alpha=4.0):
+    """fit.py:117-118."""
+    return LIFSoftFn.apply(I, u0, beta, theta, alpha)
+
+
+class LIFSoftScanFn(torch.autograd.Function):
+    """Soft-reset LIF with the exact soft scan forward (mode "scan", the reference's default
+    repair = 0) or the serial forward; the adjoint is the float64 recurrence in both modes (the
+    reference: FFT convolution for "scan", the fp32 serial sweep otherwise); gradients for I,
+    u0, beta (fit.py:121-149)."""
+
+    @staticmethod
+    def forward(ctx, I, u0, beta, theta, alpha, mode, C, K):
+        from . import hip_soft as TS
+        b, th = _f32s(beta, theta)
+        I = I.contiguous()
+        if mode == "scan":
+            U, S = TS.soft_scan_forward(I, b, th, u0, C=C, K=K)
+        else:
+            U, S = TS.soft_serial_forward(I, b, th, u0)
+        ctx.save_for_backward(I, u0, U)
+        ctx.cfg = (b, th, float(alpha))
+        return S
+
+    @staticmethod
+    def backward(ctx, gS):
+        from . import hip_soft as TS
+        I, u0, U = ctx.saved_tensors
+        b, th, alpha = ctx.cfg
+        need_b = ctx.needs_input_grad[2]
+        lam, db = TS._soft_backward(I, u0, U, gS.contiguous(), b, th, alpha, need_b)
+        return (lam, b * lam[0], (db.float().reshape(()) if need_b else None), None, None, None, None,
+                None)
+
+
+def lif_soft_scan(I, u0, beta, theta=1.0, alpha=4.0, mode="scan", C=128, K=32):
+    """fit.py:152-153."""
+    return LIFSoftScanFn.apply(I, u0, beta, theta, alpha, mode, C, K)

@@ -734,3 +734,34 @@ def surrogate_grad(x, alpha):
     """Derivative of sigmoid(alpha*x) (fast.py:48-51); used by fit.lif_param."""
     sg = torch.sigmoid(alpha * x)
     return alpha * sg * (1 - sg)
+
+
+
+# Soft-reset serial functions the reference keeps in triton_lif.py (:1034-1083, :1139-1210);
+# implemented in hip_soft, imported at call time (hip_soft uses this module's helpers).
+def soft_serial_forward(I, beta, theta, u0, BN=32):
+    from . import hip_soft
+    return hip_soft.soft_serial_forward(I, beta, theta, u0)
+
+
+def soft_serial_backward(I, u0, U, GS, beta, theta, alpha=4.0, BN=32):
+    from . import hip_soft
+    return hip_soft.soft_serial_backward(I, u0, U, GS, beta, theta, alpha)
+
+
+def soft_serial_backward_pf(I, u0, U, GS, beta, theta, alpha=4.0, BN=32, D=4, num_warps=1):
+    from . import hip_soft
+    return hip_soft.soft_serial_backward(I, u0, U, GS, beta, theta, alpha)
+
+
+def soft_serial_backward_auto(I, u0, U, GS, beta, theta, alpha=4.0):
+    from . import hip_soft
+    return hip_soft.soft_serial_backward(I, u0, U, GS, beta, theta, alpha)
+
+
+def soft_bwd_cfg(N):
+    """(BN, D, num_warps) table of the reference (triton_lif.py:1192-1197); kept for callers."""
+    if N <= 8: return 16, 8, 1
+    if N <= 64: return 16, 4, 1
+    if N <= 16384: return 64, 16, 1
+    return 128, 4, 1

@@ -278,6 +278,27 @@ int lsh_aff_bwd(const float* I, const float* u0, const float* U, const float* S,
                 float gamma, float alpha, int mode, int C, void* ws, size_t ws_bytes,
                 void* stream);
 
+/* ---- soft reset  u <- v - theta (triton_soft.py) ----------------------------------------
+ * The forward is the affine reset with gamma = 1, delta = -theta (lsh_aff_serial_fwd,
+ * lsh_aff_scan_fwd with r_theta = 0): fl(fl(1*v) - theta) = fl(v - theta), the reference's
+ * rounding (triton_soft.py:106-110), and the soft scan's common-slope maps are the affine maps
+ * with every slope equal.
+ *
+ * Soft-reset adjoint, reset detached: lam_t = b_t + beta*lam_{t+1}, b_t = gS_t*alpha*sg*(1-sg),
+ * sg = sigmoid(alpha*(v_t - theta)) in fp32, the recurrence in float64, Lam stored as fp32.
+ * Replaces triton_soft.py:214-221 (soft_adjoint_fft: the same float64 recurrence by FFT
+ * convolution) and triton_lif.py:1052-1069, :1139-1210 (soft serial adjoints, fp32).
+ * V != NULL: v_t = V[t] (soft_adjoint_fft's input); I, u0, U unused and partials must be NULL.
+ * V == NULL: v_t = fl(fl(beta*u_{t-1}) + x_t) from I, u0 (t = 0) and U; partials NULL or
+ * [lsh_soft_bwd_partials(T, N, C)] doubles, one per block: sum lam_t*u_{t-1} (dbeta,
+ * fit.py:115, :149).  C: chunk length, T % C == 0 (C == T: one sweep per neuron, no
+ * workspace; otherwise lsh_soft_bwd_workspace(T, N, C) bytes, 256-byte aligned). */
+size_t lsh_soft_bwd_workspace(int64_t T, int64_t N, int C);
+int64_t lsh_soft_bwd_partials(int64_t T, int64_t N, int C);
+int lsh_soft_bwd(const float* I, const float* u0, const float* U, const float* V, const float* GS,
+                 float* Lam, double* partials, int64_t T, int64_t N, double beta, float theta,
+                 float alpha, int C, void* ws, size_t ws_bytes, void* stream);
+
 /* L[t] = A[t]*L[t+1] + B[t] with L[T] = 0, per column of [T, N] arrays (two roundings per
  * step, rows from the last).  Replaces triton_affine.py:202-211 and fast.py:307-323
  * (reverse_affine_scan; there a Hillis-Steele scan, so the bits differ by reassociation). */

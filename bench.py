@@ -278,7 +278,8 @@ def bench_affine(torch, dev, reps):
         (bit-identical) for gamma, delta = (0.3, -0.1) and (1, -1);
     (b) the cfg2 shape (65536 x T=4096, beta=0.9, x~N(0.12,0.25^2), u0=0) with gamma=0.5,
         delta=-0.25: lif_affine fwd (serial) + bwd with the five gradients through autograd, and
-        the adjoint alone against its 20 B/neuron-step roofline."""
+        the adjoint alone against its 20 B/neuron-step roofline;
+    (c) the soft reset on the reference's soft test shapes."""
     from lifscan import triton_affine as AF
     out = {}
     T, N = 8192, 200
@@ -324,6 +325,30 @@ def bench_affine(torch, dev, reps):
         "config": "65536 x 4096, beta=0.9, gamma=0.5, delta=-0.25, x~N(0.12,0.25^2)"}
     del I, gS, U, S, Ig
     torch.cuda.empty_cache()
+    # soft reset (triton_soft.py) on the reference's test shapes: the scan with repair vs serial
+    # (tests/test_soft_scan.py: T=8192, N=333, x~N(0.15,0.4^2), C=K=32), and the soft layer's
+    # float64 adjoint on the long narrow fitting shape (tests/test_soft_scan_grad.py: T=16384, N=8)
+    from lifscan import triton_soft as TS
+    from lifscan.hip_soft import _soft_backward
+    T, N = 8192, 333
+    g = torch.Generator().manual_seed(0)
+    I = (0.15 + 0.4 * torch.randn(T, N, generator=g)).to(dev)
+    u0 = (0.3 * torch.randn(N, generator=g)).to(dev)
+    Ur, Sr = TS.soft_serial_forward(I, 0.95, 1.0, u0)
+    st = {}
+    U, S = TS.soft_scan_forward(I, 0.95, 1.0, u0, C=32, K=32, repair=10 ** 6, stats=st)
+    out["soft_small"] = {
+        "serial_fwd_ms": round(ev_time(lambda: TS.soft_serial_forward(I, 0.95, 1.0, u0), reps), 4),
+        "scan_repair_ms": round(ev_time(lambda: TS.soft_scan_forward(I, 0.95, 1.0, u0, C=32, K=32,
+                                                                     repair=10 ** 6), reps), 4),
+        "scan_equals_serial": bool(torch.equal(U, Ur) and torch.equal(S, Sr)), "stats": st}
+    T, N = 16384, 8
+    I = (0.06 + 0.3 * torch.randn(T, N, generator=g)).to(dev)
+    gS = torch.randn(T, N, generator=g).to(dev)
+    z = torch.zeros(N, device=dev)
+    U, S = TS.soft_serial_forward(I, 0.95, 1.0, z)
+    out["soft_adjoint_T16384_N8_ms"] = round(ev_time(lambda: _soft_backward(I, z, U, gS, 0.95, 1.0, 4.0), reps), 4)
+    del I, gS, U, S, Ur, Sr
     return out
 
 

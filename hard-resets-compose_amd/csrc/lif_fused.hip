@@ -234,11 +234,6 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
     float upk[PS ? C : 1];
     float vpk[AFF ? C : 1];
     unsigned long long sbits = 0;
-    // a_j: from the spike bit for the affine reset
-    auto aj = [&](int j) -> float {
-      if constexpr (AFF) return ((sbits >> j) & 1ull) ? gbeta : beta;
-      else return a[j];
-    };
     float lam = 0.0f;
     const size_t row0 = (size_t)(active ? m : 0) * C;
     const unsigned rstride = (unsigned)(N * 4);
@@ -269,8 +264,14 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
       float P = 1.0f, Q = 0.0f;
 #pragma unroll
       for (int j = C - 1; j >= 0; --j) {
-        Q = b[j] + aj(j) * Q;
-        P = aj(j) * P;
+        if constexpr (AFF) {
+          const float aa = ((sbits >> j) & 1ull) ? gbeta : beta;
+          Q = b[j] + aa * Q;
+          P = aa * P;
+        } else {
+          Q = b[j] + a[j] * Q;
+          P = a[j] * P;
+        }
       }
       sP[w][lane] = P;
       sQ[w][lane] = Q;
@@ -283,7 +284,10 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
 #pragma unroll
       for (int j = C - 1; j >= 0; --j) {
         const float lam_next = lam;
-        lam = b[j] + aj(j) * lam;
+        if constexpr (AFF)
+          lam = b[j] + (((sbits >> j) & 1ull) ? gbeta : beta) * lam;
+        else
+          lam = b[j] + a[j] * lam;
         if (valid) {
           bl.st_nt(sb, j * rstride, lam);
           if (PS) {

@@ -94,10 +94,6 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
   float vpk[AFF ? C : 1];
   unsigned long long sbits = 0;
   const float gbeta = beta * u_r;  // AFF: beta*gamma
-  auto aj = [&](int j) -> float {
-    if constexpr (AFF) return ((sbits >> j) & 1ull) ? gbeta : beta;
-    else return a[j];
-  };
   double acc_b = 0.0, acc_t = 0.0, acc_r = 0.0;
   {
     const Buf bi(I + nb0 + row0 * N), bs(S + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
@@ -127,8 +123,14 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
   float P = 1.0f, Q = 0.0f;
 #pragma unroll
   for (int j = C - 1; j >= 0; --j) {
-    Q = b[j] + aj(j) * Q;
-    P = aj(j) * P;
+    if constexpr (AFF) {
+      const float aa = ((sbits >> j) & 1ull) ? gbeta : beta;
+      Q = b[j] + aa * Q;
+      P = aa * P;
+    } else {
+      Q = b[j] + a[j] * Q;
+      P = a[j] * P;
+    }
   }
   sP[w][lane] = P;
   sQ[w][lane] = Q;
@@ -179,7 +181,10 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
 #pragma unroll
   for (int j = C - 1; j >= 0; --j) {
     const float lam_next = lam;
-    lam = b[j] + aj(j) * lam;
+    if constexpr (AFF)
+      lam = b[j] + (((sbits >> j) & 1ull) ? gbeta : beta) * lam;
+    else
+      lam = b[j] + a[j] * lam;
     if (valid) {
       bl.st_nt(sb, j * rstride, lam);
       if (PS) {

@@ -104,17 +104,30 @@ __global__ __launch_bounds__(64) void k_soft_bwd(const float* __restrict__ I,
   }
 }
 
-// Reverse carry over chunks: lam_end[m] = lam after chunk m; lam <- Q[m] + beta^C*lam.
+// Reverse carry over chunks: lam_end[m] = lam after chunk m; lam <- Q[m] + beta^C*lam.  The
+// chunk offsets do not depend on lam, so they are loaded 8 chunks ahead.
 __global__ __launch_bounds__(64) void k_soft_bwd_carry(const double* __restrict__ Q,
                                                        double* __restrict__ lam_end, int64_t N,
                                                        int M, double betaC) {
+  constexpr int D = 8;
   const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
   if (n >= N) return;
+  auto row = [&](int m) { return (size_t)m * (size_t)N + (size_t)n; };
   double lam = 0.0;
-  for (int m = M - 1; m >= 0; --m) {
-    const size_t o = (size_t)m * N + n;
-    lam_end[o] = lam;
-    lam = Q[o] + betaC * lam;
+  int m = M - 1;
+  for (; m >= D - 1; m -= D) {
+    double q[D];
+#pragma unroll
+    for (int k = 0; k < D; ++k) q[k] = Q[row(m - k)];
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      lam_end[row(m - k)] = lam;
+      lam = q[k] + betaC * lam;
+    }
+  }
+  for (; m >= 0; --m) {
+    lam_end[row(m)] = lam;
+    lam = Q[row(m)] + betaC * lam;
   }
 }
 

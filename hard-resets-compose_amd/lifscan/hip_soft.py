@@ -11,6 +11,8 @@ coefficient recurrence lam_t = b_t + beta*lam_{t+1}; the reference solves it by 
 convolution (soft_adjoint_fft), here a HIP kernel solves the same recurrence directly in float64
 (lsh_soft_bwd).  Triton tile keywords are accepted and ignored.
 """
+import math
+
 import torch
 
 from . import _native as _n
@@ -49,13 +51,14 @@ def soft_scan_forward(I, beta, theta, u0, C=32, K=16, BN=16, nw=1, BNc=16, BNr=3
 
 def _soft_C(T, N, target_blocks=2048, min_C=32):
     """Chunk length of the soft adjoint: one sweep per neuron when the 64-neuron blocks alone
-    fill the chip, else the largest divisor of T of at least min_C steps giving about
-    target_blocks (chunk, block) pairs (one sweep when T has no such divisor)."""
+    fill the chip; otherwise the smallest divisor of T of at least T*NB/target_blocks steps (about
+    target_blocks (chunk, block) pairs) and at least max(min_C, sqrt(T)) steps, so that the
+    sequential carry over chunks stays short."""
     NB = (N + 63) // 64
     if T == 0 or NB >= target_blocks:
         return max(T, 1)
-    want = max(min_C, T * NB // target_blocks)
-    for C in range(min(want, T), min(min_C, T) - 1, -1):
+    want = max(min_C, math.isqrt(T), T * NB // target_blocks)
+    for C in range(min(want, T), T + 1):
         if T % C == 0:
             return C
     return T

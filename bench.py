@@ -5,8 +5,11 @@ Workload ("cfg2"): 65,536 neurons x T = 4,096, fp32, b
 x ~ N(0.12, 0.25^2) (seeded CPU generator, copied to HBM before timing), u0 = 0, theta = 1,
 u_r = 0, upstream gradient gS ~ N(0, 1).  One step = lif_tuned(mode="scan", K=8, repair on)
 forward + backward through autograd: the exact two-level scan (single pass, bit-identical to
-the serial recurrence) and the single-pass affine-scan adjoint.  value = neuron-steps/s of
-that fwd+bwd step.
+the serial recurrence) and the single-pass affine-scan adjoint.  lif_tuned keeps U only for its
+backward, so its forward stores S and the exact state at every 32-step chunk entry, and the
+adjoint replays each chunk's forward from that state in registers (same S, same gradients):
+20 bytes of HBM traffic per neuron-step instead of 32.  value = neuron-steps/s of that fwd+bwd
+step; the passes that store U are timed beside it ("stored_U_path").
 
 The JSON line also carries the forward-only rate, the scan with map speculation forced on,
 the in-house HIP serial baseline, the beta = 0.99 variant, the map statistics of the
@@ -34,7 +37,12 @@ for p in (os.path.join(REPO, "hard-resets-compose_amd"), REPO):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
-B_FWD, B_BWD = 12, 20  # algorithmic bytes per neuron-step: read I; write U, S | read I, U, S, gS; write dI
+# algorithmic bytes per neuron-step of the passes that store U (scan_forward_v3 returns it):
+# read I; write U, S | read I, U_{t-1}, S, gS; write dI
+B_FWD, B_BWD = 12, 20
+# lif_tuned keeps U only for its backward; its recomputing pair stores the chunk entry states
+# instead: read I; write S | read I, gS; write dI (the states are 1/32 of a row per step)
+B_FWD_RC, B_BWD_RC = 8, 12
 T_CFG, N_CFG = 4096, 65536
 
 
@@ -64,7 +72,7 @@ def ev_time(fn, reps, warm=1):
 def profiled_traffic():
     """HBM bytes per launch of the dominant kernel from the committed counter summary
     (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled on a copy kernel)."""
-    path = os.path.join(REPO, "profiles", "k_lif_bwd_fused_cfg2_traffic.txt")
+    path = os.path.join(REPO, "profiles", "k_lif_bwd_fused_rc_cfg2_traffic.txt")
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -361,13 +369,13 @@ def dominant_only(L, torch, dev):
         y.copy_(x)
     I_cpu, I, gS = inputs(0.9, dev)
     u0 = torch.zeros(N_CFG, device=dev)
-    U, S = L.scan_forward_exact(I, 0.9, 1.0, 0.0, u0, K=8)
+    S, ST = L.scan_forward_exact_starts(I, 0.9, 1.0, 0.0, u0)
     torch.cuda.synchronize()
     for _ in range(3):
-        L.scan_backward_fused(I, u0, U, S, gS, None, 0.9, 1.0, 0.0, 4.0)
+        L.scan_backward_fused_starts(I, ST, gS, 0.9, 1.0, 0.0, 4.0)
     torch.cuda.synchronize()
     print(json.dumps({"dominant_only": True, "copy_bytes_each_way": 4 * x.numel(),
-                      "kernel": "k_lif_bwd_fused", "launches": 3}))
+                      "kernel": "k_lif_bwd_fused<32, 4, true, false, 0, true>", "launches": 3}))
 
 
 def main():
@@ -443,10 +451,15 @@ def main():
     ms["serial_bwd"] = ev_time(lambda: L.serial_backward(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), reps)
     st = {}
     L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6, stats=st)
-    # dominant kernel: the single-pass backward is one launch of k_lif_bwd_fused per call
-    t_dom = ev_time(lambda: L.scan_backward_fused(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), 20)
-    log("ms " + json.dumps({k: round(v, 4) for k, v in ms.items()}) + f" dominant {t_dom:.4f}")
     del U, S
+    # the recomputing pair lif_tuned runs here: S + chunk entry states, adjoint from them
+    S_rc, ST = L.scan_forward_exact_starts(I, beta, 1.0, 0.0, u0)
+    ms["rc_fwd"] = ev_time(lambda: L.scan_forward_exact_starts(I, beta, 1.0, 0.0, u0), reps)
+    # dominant kernel: the recomputing adjoint is one launch of k_lif_bwd_fused<..., RC> per call
+    t_dom = ev_time(lambda: L.scan_backward_fused_starts(I, ST, gS, beta, 1.0, 0.0, 4.0), 20)
+    ms["rc_bwd"] = t_dom
+    log("ms " + json.dumps({k: round(v, 4) for k, v in ms.items()}) + f" dominant {t_dom:.4f}")
+    del S_rc, ST
 
     # beta = 0.99 variant of cfg2
     _, I99, _ = inputs(0.99, dev)
@@ -459,13 +472,14 @@ def main():
     L.scan_forward_v3(I99, 0.99, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6, stats=st99)
     del U99, S99, I99
 
-    achieved = B_BWD * N * T / (t_dom / 1000.0) / 1e9
+    achieved = B_BWD_RC * N * T / (t_dom / 1000.0) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(),
-                "traffic_source": "profiles/k_lif_bwd_fused_cfg2_traffic.txt (rocprofv3 --pmc FETCH_SIZE, "
-                                  "WRITE_SIZE; bytes per launch)",
-                "kernel": "k_lif_bwd_fused (single-pass affine-scan adjoint, C=32, W=4)",
-                "algorithmic_bytes_per_launch": B_BWD * N * T, "avg_launch_ms": round(t_dom, 4)}
+                "traffic_source": "profiles/k_lif_bwd_fused_rc_cfg2_traffic.txt (rocprofv3 --pmc "
+                                  "FETCH_SIZE, WRITE_SIZE; bytes per launch)",
+                "kernel": "k_lif_bwd_fused<32, 4, true, false, 0, true> (single-pass adjoint "
+                          "recomputing each chunk from its entry state)",
+                "algorithmic_bytes_per_launch": B_BWD_RC * N * T, "avg_launch_ms": round(t_dom, 4)}
 
     others = None
     if not args.headline_only:
@@ -507,10 +521,15 @@ def main():
         "config": {"workload": "cfg2: lif_tuned(mode=scan, K=8, repair on) fwd+bwd, N=65536 "
                                "(256x256), T=4096, beta=0.9, theta=1, u_r=0, u0=0",
                    "N": N, "T": T, "beta": beta, "C": C, "K": K},
-        "pct_roofline_fwd_bwd": pct(B_FWD + B_BWD, ms_step),
-        "fwd_value": round(N * T / (ms["scan_fwd"] / 1000.0), 1),
-        "pct_roofline_fwd": pct(B_FWD, ms["scan_fwd"]),
-        "pct_roofline_bwd": pct(B_BWD, ms["scan_bwd"]),
+        "bytes_per_neuron_step": B_FWD_RC + B_BWD_RC,
+        "pct_roofline_fwd_bwd": pct(B_FWD_RC + B_BWD_RC, ms_step),
+        "fwd_value": round(N * T / (ms["rc_fwd"] / 1000.0), 1),
+        "pct_roofline_fwd": pct(B_FWD_RC, ms["rc_fwd"]),
+        "pct_roofline_bwd": pct(B_BWD_RC, ms["rc_bwd"]),
+        "stored_U_path": {"fwd_bwd_ms": round(ms["scan_fwd"] + ms["scan_bwd"], 4),
+                          "pct_roofline_fwd": pct(B_FWD, ms["scan_fwd"]),
+                          "pct_roofline_bwd": pct(B_BWD, ms["scan_bwd"]),
+                          "bytes_per_neuron_step": B_FWD + B_BWD},
         "ms": {k: round(v, 4) for k, v in ms.items()},
         "serial_hip_fwd_bwd_value": round(N * T / ((ms["serial_fwd"] + ms["serial_bwd"]) / 1000.0), 1),
         "maps_forced_counters": maps_ctr,

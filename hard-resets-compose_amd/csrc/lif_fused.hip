@@ -35,7 +35,10 @@ __device__ __forceinline__ bool lds_wait(int* flag, int want) {
   return false;
 }
 
-template <int KMAX, int C, int W, bool SPEC>
+// SO (starts only): U is [M, N] and receives each chunk's exact entry state instead of the
+// trajectory, S as usual; the adjoint recomputes the trajectory from those states
+// (k_lif_bwd_fused<..., RC = true>), so the forward writes 4 B per neuron-step instead of 8.
+template <int KMAX, int C, int W, bool SPEC, bool SO = false>
 __global__ __launch_bounds__(WAVE* W) void k_lif_fwd_fused(const float* __restrict__ I,
                                                            const float* __restrict__ u0,
                                                            float* __restrict__ U,
@@ -161,7 +164,17 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_fwd_fused(const float* __restri
       fixups += (SPEC && known && !hit && valid) ? 1ull : 0ull;
       unknown += (SPEC && !known && valid) ? 1ull : 0ull;
       // (4) the stored trajectory, from the exact entry
-      if (valid) {
+      if (valid && SO) {
+        U[(size_t)m * N + nb0 + lane] = start;
+        const Buf bs(Sb + row0 * N);
+        float u = start;
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+          bool s;
+          u = lif_step(u, x[j], beta, theta, u_r, s);
+          bs.st_nt(sb, j * rstride, s ? 1.0f : 0.0f);
+        }
+      } else if (valid) {
         const Buf bu(Ub + row0 * N), bs(Sb + row0 * N);
         float u = start;
 #pragma unroll
@@ -198,13 +211,18 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_fwd_fused(const float* __restri
 //            gamma (a detached reset needs no u_r): J_t = s_t ? gamma : 1, and the sums
 //            lam_t*u_{t-1}, s_t*v_t*lam_{t+1}, s_t*lam_{t+1}.  a_t = beta*J_t follows from
 //            the spike bit, so v_t takes the registers a_t would.
-template <int C, int W, bool DETACH, bool HAS_GU, int PS = 0>
+// RC (recompute, detached, no GU): U is the [M, N] array of chunk entry states written by the
+// SO forward and S is not read; the wave replays its chunk's forward from the entry state in
+// registers (the forward's own arithmetic, so u_{t-1} and s_t are the forward's bits) while it
+// forms the coefficients: 8 B read per neuron-step instead of 16.
+template <int C, int W, bool DETACH, bool HAS_GU, int PS = 0, bool RC = false>
 __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ U,
     const float* __restrict__ S, const float* __restrict__ GS, const float* __restrict__ GU,
     float* __restrict__ Lam, double* __restrict__ partials, int64_t N, int M, float beta,
     float theta, float u_r, float alpha) {
   static_assert(!PS || (DETACH && !HAS_GU && C <= 64), "parameter sums: detached, no GU");
+  static_assert(!RC || (DETACH && !HAS_GU && PS != 2), "recompute: hard reset, detached, no GU");
   constexpr bool AFF = PS == 2;
   __shared__ float sP[W][WAVE], sQ[W][WAVE];
   __shared__ float sLam[WAVE];
@@ -239,15 +257,26 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
     const unsigned rstride = (unsigned)(N * 4);
     if (active) {
       const Buf bi(Ib + row0 * N), bs_(Sb + row0 * N), bg(Gb + row0 * N), bp(Ub + row0 * N);
-      // state before the chunk's first step: the previous chunk's last U row, or u0
-      const float up0 = row0 > 0 ? ld_row(Ub + (row0 - 1) * N, lb) : u0n;
+      // state before the chunk's first step: the previous chunk's last U row, or u0 (RC: the
+      // stored entry state of the chunk)
+      const float up0 = RC ? U[(size_t)m * N + nb0 + ln]
+                           : (row0 > 0 ? ld_row(Ub + (row0 - 1) * N, lb) : u0n);
+      float ur = up0;  // RC: the recomputed state
 #pragma unroll
       for (int j = 0; j < C; ++j) {
         const unsigned so = j * rstride;
         const float x = bi.ld(lb, so);
-        const float s = bs_.ld(lb, so);
+        float s, up;
+        if constexpr (RC) {
+          up = ur;
+          bool sb_;
+          ur = lif_step(ur, x, beta, theta, u_r, sb_);
+          s = sb_ ? 1.0f : 0.0f;
+        } else {
+          s = bs_.ld(lb, so);
+        }
         const float gs = bg.ld(lb, so);
-        const float up = j == 0 ? up0 : bp.ld(lb, so - rstride);
+        if constexpr (!RC) up = j == 0 ? up0 : bp.ld(lb, so - rstride);
         const float v = lif_v(up, x, beta);
         const float sg = surrogate(v, theta, alpha);
         float J = 1.0f - s;
@@ -334,13 +363,34 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_fused(
 }
 
 // ---------------------------------------------------------------------------------------
-template <int KMAX, int C, int W, bool SPEC>
+template <int KMAX, int C, int W, bool SPEC, bool SO = false>
 static void launch_fwd_fused(const float* I, const float* u0, float* U, float* S, WsHeader* h,
                              int64_t N, int M, int K, float beta, float theta, float u_r,
                              hipStream_t st) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
-  hipLaunchKernelGGL((k_lif_fwd_fused<KMAX, C, W, SPEC>), dim3((unsigned)NB), dim3(WAVE * W), 0, st,
-                     I, u0, U, S, h, N, M, K, beta, theta, u_r);
+  hipLaunchKernelGGL((k_lif_fwd_fused<KMAX, C, W, SPEC, SO>), dim3((unsigned)NB), dim3(WAVE * W), 0,
+                     st, I, u0, U, S, h, N, M, K, beta, theta, u_r);
+}
+
+// The chunked-serial exact forward (no maps) writing S and the chunk entry states only.
+template <int C>
+static void fwd_starts_c(const float* I, const float* u0, float* STARTS, float* S, WsHeader* h,
+                         int64_t N, int M, float beta, float theta, float u_r, hipStream_t st) {
+  constexpr int WMAX = C <= 32 ? 16 : (C == 64 ? 8 : 4);
+  const int W = fused_waves((N + WAVE - 1) / WAVE, WMAX);
+  if constexpr (WMAX >= 16) {
+    if (W == 16) {
+      launch_fwd_fused<1, C, 16, false, true>(I, u0, STARTS, S, h, N, M, 1, beta, theta, u_r, st);
+      return;
+    }
+  }
+  if constexpr (WMAX >= 8) {
+    if (W == 8) {
+      launch_fwd_fused<1, C, 8, false, true>(I, u0, STARTS, S, h, N, M, 1, beta, theta, u_r, st);
+      return;
+    }
+  }
+  launch_fwd_fused<1, C, 4, false, true>(I, u0, STARTS, S, h, N, M, 1, beta, theta, u_r, st);
 }
 
 template <int C, bool SPEC>
@@ -434,6 +484,46 @@ static void bwd_fused_c(const float* I, const float* u0, const float* U, const f
     }
   }
   bwd_fused_cw<C, 4>(I, u0, U, S, GS, GU, Lam, N, M, beta, theta, u_r, alpha, detach, st);
+}
+
+// Recomputing adjoint (RC): chunk entry states instead of U and S; ps 0 plain, ps 1 with the
+// fit.py parameter sums.
+template <int C, int W>
+static void launch_bwd_rc(const float* I, const float* STARTS, const float* GS, float* Lam,
+                          double* partials, int64_t N, int M, float beta, float theta, float u_r,
+                          float alpha, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  if (partials)
+    hipLaunchKernelGGL((k_lif_bwd_fused<C, W, true, false, 1, true>), dim3((unsigned)NB),
+                       dim3(WAVE * W), 0, st, I, STARTS, STARTS, nullptr, GS, nullptr, Lam, partials,
+                       N, M, beta, theta, u_r, alpha);
+  else
+    hipLaunchKernelGGL((k_lif_bwd_fused<C, W, true, false, 0, true>), dim3((unsigned)NB),
+                       dim3(WAVE * W), 0, st, I, STARTS, STARTS, nullptr, GS, nullptr, Lam, nullptr,
+                       N, M, beta, theta, u_r, alpha);
+}
+
+template <int C>
+static void bwd_rc_c(const float* I, const float* STARTS, const float* GS, float* Lam,
+                     double* partials, int64_t N, int M, float beta, float theta, float u_r,
+                     float alpha, hipStream_t st) {
+  // registers as the plain adjoint (with the sums as the parameter variant)
+  constexpr int WMAX = C == 16 ? 16 : (C == 32 ? 8 : 4);
+  const int wmax = partials ? (C <= 32 ? 8 : 4) : WMAX;
+  const int W = fused_waves((N + WAVE - 1) / WAVE, wmax);
+  if constexpr (WMAX >= 16) {
+    if (W == 16) {
+      launch_bwd_rc<C, 16>(I, STARTS, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st);
+      return;
+    }
+  }
+  if constexpr (WMAX >= 8) {
+    if (W == 8) {
+      launch_bwd_rc<C, 8>(I, STARTS, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st);
+      return;
+    }
+  }
+  launch_bwd_rc<C, 4>(I, STARTS, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st);
 }
 
 template <int C, int W>
@@ -530,6 +620,53 @@ extern "C" int lsh_lif_chunked_serial_fwd(const float* I, const float* u0, float
                                           int64_t T, int64_t N, float beta, float theta, float u_r,
                                           int C, void* ws, size_t ws_bytes, void* stream) {
   return exact_fwd(false, I, u0, U, S, T, N, beta, theta, u_r, C, 1, ws, ws_bytes, stream);
+}
+
+extern "C" int lsh_lif_scan_exact_fwd_starts(const float* I, const float* u0, float* STARTS,
+                                             float* S, int64_t T, int64_t N, float beta,
+                                             float theta, float u_r, int C, void* ws,
+                                             size_t ws_bytes, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(STARTS) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C != 16 && C != 32 && C != 64) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+  if (ws_bytes < kWsHeaderBytes || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+    return LSH_ERR_WORKSPACE;
+  hipStream_t st = (hipStream_t)stream;
+  WsHeader* h = reinterpret_cast<WsHeader*>(ws);
+  hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, h);
+  if (T > 0 && N > 0) {
+    const int M = (int)(T / C);
+    switch (C) {
+      case 16: fwd_starts_c<16>(I, u0, STARTS, S, h, N, M, beta, theta, u_r, st); break;
+      case 32: fwd_starts_c<32>(I, u0, STARTS, S, h, N, M, beta, theta, u_r, st); break;
+      default: fwd_starts_c<64>(I, u0, STARTS, S, h, N, M, beta, theta, u_r, st); break;
+    }
+  }
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" int lsh_lif_scan_fused_bwd_starts(const float* I, const float* STARTS, const float* GS,
+                                             float* Lam, double* partials, int64_t T, int64_t N,
+                                             float beta, float theta, float u_r, float alpha, int C,
+                                             void* stream) {
+  if (bad_ptr(I) || bad_ptr(STARTS) || bad_ptr(GS) || bad_ptr(Lam)) return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C != 16 && C != 32 && C != 64) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int M = (int)(T / C);
+  switch (C) {
+    case 16: bwd_rc_c<16>(I, STARTS, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st); break;
+    case 32: bwd_rc_c<32>(I, STARTS, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st); break;
+    default: bwd_rc_c<64>(I, STARTS, GS, Lam, partials, N, M, beta, theta, u_r, alpha, st); break;
+  }
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
 }
 
 extern "C" int lsh_lif_scan_fused_bwd(const float* I, const float* u0, const float* U,

@@ -90,6 +90,10 @@ SIGNATURES = {
                                          c_sz, c_p]),
     "lsh_lif_scan_fused_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,
                                      c_f, c_i, c_i, c_p]),
+    "lsh_lif_scan_exact_fwd_starts": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_p,
+                                            c_sz, c_p]),
+    "lsh_lif_scan_fused_bwd_starts": (c_i, [c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f,
+                                            c_i, c_p]),
     "lsh_lif_scan_v4_workspace": (c_sz, [c_i64, c_i64, c_i, c_i, c_i, c_i]),
     "lsh_lif_scan_v4_layout": (c_i, [c_i64, c_i64, c_i, c_i, c_i, c_i, ctypes.POINTER(V4Layout)]),
     "lsh_lif_scan_v4_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i, c_i, c_i,

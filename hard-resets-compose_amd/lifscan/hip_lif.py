@@ -488,6 +488,71 @@ def scan_backward_fused(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach
     return Lam
 
 
+# ----------------------------------------------------------------------------- recomputing pair
+# LIFTuned keeps U only for its backward.  When both passes run the single-pass kernels, the
+# forward writes S and the exact entry state of every FUSED_FWD_C-step chunk instead of U, and
+# the adjoint replays each chunk's forward from that state in registers: the same Lam (the
+# forward's own u_{t-1} and s_t bits), 20 instead of 32 bytes of HBM traffic per neuron-step.
+RECOMPUTE_BWD = True
+
+
+def scan_forward_exact_starts(I, beta, theta, u_r, u0, C=None):
+    """Single-pass exact forward -> (S, STARTS [T//C, N]): S as scan_forward_exact, and the
+    state before every C-step chunk (STARTS[0] = u0) in place of U."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    C = int(C or FUSED_FWD_C)
+    if C not in (16, 32, 64) or T % C:
+        raise ValueError(f"the starts-only forward needs C in (16, 32, 64) dividing T={T}")
+    L = _n.lib()
+    nbytes = L.lsh_lif_scan_exact_workspace()
+    ws = _n.workspace(nbytes, I.device)
+    S = torch.empty_like(I)
+    ST = torch.empty(T // C, N, device=I.device, dtype=torch.float32)
+    with torch.cuda.device(I.device):
+        _n.check(L.lsh_lif_scan_exact_fwd_starts(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(ST), _n.ptr(S), T, N, _f32(beta), _f32(theta), _f32(u_r), C,
+            _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_lif_scan_exact_fwd_starts")
+    return S, ST
+
+
+def scan_backward_fused_starts(I, STARTS, GS, beta, theta, u_r, alpha=4.0, want_sums=False):
+    """Single-pass adjoint from the chunk entry states (detached reset, no GU) -> (Lam, sums):
+    sums (fp64 [3]: sum lam*u_{t-1}, sum gS*sg, sum s*lam_{t+1}) when want_sums, else None."""
+    I = _input(I)
+    T, N = I.shape
+    GS = _same(GS, I, "GS")
+    M = STARTS.shape[0]
+    if M == 0 or T % M or STARTS.shape != (M, N):
+        raise ValueError(f"STARTS must be [T//C, {N}]")
+    C = T // M
+    STARTS = STARTS.contiguous()
+    Lam = torch.empty_like(I)
+    parts = None
+    if want_sums:
+        parts = torch.zeros((N + 63) // 64, 3, device=I.device, dtype=torch.float64)
+    with torch.cuda.device(I.device):
+        _n.check(_n.lib().lsh_lif_scan_fused_bwd_starts(
+            _n.ptr(I), _n.ptr(STARTS), _n.ptr(GS), _n.ptr(Lam), _n.ptr(parts), T, N,
+            _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), C, _n.stream_of(I)),
+            "lsh_lif_scan_fused_bwd_starts")
+    return Lam, (parts.sum(0) if want_sums else None)
+
+
+def _recompute_ok(T, N, K, repair):
+    """True when scan_forward_auto and scan_backward_auto would both take the single-pass
+    kernels (converged forward without maps, fused adjoint): then the recomputing pair gives
+    the same S and Lam."""
+    if not RECOMPUTE_BWD or FUSED_FWD_C != FUSED_BWD_C or T == 0 or N == 0:
+        return False
+    if T % _pick_C(T, D=16) or not _fused_fwd_ok(T, _pick_C(T, D=16), K, repair, None):
+        return False
+    if long_sequence_C(T, N) or N <= FUSED_MAPS_MAX_N:
+        return False
+    return N >= FUSED_BWD_MIN_N and T % FUSED_BWD_C == 0
+
+
 # ----------------------------------------------------------------------------- scan backward
 # The single-pass adjoint owns 64 neurons per workgroup: with fewer than this many neurons the
 # chip is not filled, and the look-back adjoint (workgroups over 256-step segments chained by
@@ -672,19 +737,33 @@ class LIFTuned(torch.autograd.Function):
     def forward(ctx, I, u0, beta, theta, u_r, alpha, mode, K, repair):
         I = I.contiguous()
         b = _f32(beta)
+        ctx.cfg = (b, theta, u_r, alpha, mode)
+        T, N = I.shape
+        if mode != "serial" and _recompute_ok(T, N, K, repair):
+            # U is kept only for the backward: store the chunk entry states instead
+            S, ST = scan_forward_exact_starts(I, b, theta, u_r, u0)
+            ctx.save_for_backward(I, u0, ST)
+            ctx.recompute = True
+            return S
         if mode == "serial":
             U, S = serial_forward_auto(I, b, theta, u_r, u0)
         else:
             U, S = scan_forward_auto(I, b, theta, u_r, u0, K=K, repair=repair)
         ctx.save_for_backward(I, u0, U, S)
-        ctx.cfg = (b, theta, u_r, alpha, mode)
+        ctx.recompute = False
         return S
 
     @staticmethod
     def backward(ctx, gS):
-        I, u0, U, S = ctx.saved_tensors
         b, theta, u_r, alpha, mode = ctx.cfg
         gS = gS.contiguous()
+        if ctx.recompute:
+            I, u0, ST = ctx.saved_tensors
+            need_b = ctx.needs_input_grad[2]
+            Lam, sums = scan_backward_fused_starts(I, ST, gS, b, theta, u_r, alpha, need_b)
+            db = sums[0].float().reshape(()) if need_b else None
+            return (Lam, b * Lam[0], db, None, None, None, None, None, None)
+        I, u0, U, S = ctx.saved_tensors
         if mode == "serial":
             Lam = serial_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
         else:

@@ -167,6 +167,23 @@ int lsh_lif_scan_fused_bwd(const float* I, const float* u0, const float* U, cons
                            float beta, float theta, float u_r, float alpha, int detach, int C,
                            void* stream);
 
+/* The autograd pair of LIFTuned / LIFAuto (triton_lif.py:654-683, :1003-1026) without the U
+ * tensor, which those layers only keep for their backward: the forward writes S and the exact
+ * entry state of every C-step chunk, STARTS[T/C][N] (STARTS[0] = u0), and the adjoint replays
+ * each chunk's forward from its entry state in registers while it forms the coefficients, so
+ * u_{t-1} and s_t are the forward's bits and Lam is the same as lsh_lif_scan_fused_bwd's with
+ * the reset detached and no GU.  HBM traffic: forward 8 B, adjoint 12 B per neuron-step
+ * (instead of 12 + 20).  C in {16, 32, 64}, the same C for both, T % C == 0; the forward is the
+ * single-pass exact forward without maps (workspace lsh_lif_scan_exact_workspace()).
+ * partials: NULL, or [ceil(N/64)] rows of 3 doubles as lsh_lif_param_bwd mode 2 (sum of
+ * lam_t*u_{t-1}, gs_t*sg_t, s_t*lam_{t+1}). */
+int lsh_lif_scan_exact_fwd_starts(const float* I, const float* u0, float* STARTS, float* S,
+                                  int64_t T, int64_t N, float beta, float theta, float u_r, int C,
+                                  void* ws, size_t ws_bytes, void* stream);
+int lsh_lif_scan_fused_bwd_starts(const float* I, const float* STARTS, const float* GS, float* Lam,
+                                  double* partials, int64_t T, int64_t N, float beta, float theta,
+                                  float u_r, float alpha, int C, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * ALIF: v = fl(fl(beta*u) + x); s = v >= fl(theta0 + w); u' = s ? u_r : v;
  *       w' = s ? fl(fl(rho*w) + q) : fl(rho*w)          (triton_alif.py:26-31)

@@ -154,3 +154,76 @@ def test_lookback_backward(dev, T, N, detach, with_gu, C):
     Lo = O.serial_backward(I, u0, U, S, GS, GU, beta, 1.0, -0.1, 4.0, detach)
     L6 = O.serial_backward(I, u0, U, S, GS, GU, beta, 1.0, -0.1, 4.0, detach, dtype=np.float64)
     assert rel(host(Lam), Lo) < 1e-5 and rel(host(Lam), L6) < 1e-4
+
+
+@pytest.mark.parametrize("C", [16, 32, 64])
+@pytest.mark.parametrize("T,N", [(1024, 777), (64, 65), (2048, 130)])
+def test_starts_forward_and_recomputing_adjoint(L, dev, C, T, N):
+    """The recomputing pair: S and the chunk entry states equal the serial recurrence's bits,
+    and the adjoint rebuilt from those states equals the single-pass adjoint that reads U and
+    S (same chunking, same arithmetic), with and without the parameter sums."""
+    if T % C:
+        pytest.skip("T % C")
+    beta, u_r = 0.9, -0.1
+    I = normal(T, N, 0.15, 0.4, 21)
+    u0 = uniform(N, -0.3, 0.3, 22)
+    GS = normal(T, N, 0.0, 1.0, 23)
+    Us, Ss = O.serial_forward(I, beta, 1.0, u_r, u0)
+    Ig, u0g, Gg = gpu(I, dev), gpu(u0, dev), gpu(GS, dev)
+    print(f"recompute pair C={C} T={T} N={N}", flush=True)
+    S, ST = L.scan_forward_exact_starts(Ig, beta, 1.0, u_r, u0g, C=C)
+    assert np.array_equal(host(S), Ss)
+    ref_st = np.concatenate([u0[None], Us[C - 1:-1:C]], 0)
+    assert np.array_equal(host(ST), ref_st)
+    Lam_ref = L.scan_backward_fused(Ig, u0g, gpu(Us, dev), gpu(Ss, dev), Gg, None, beta, 1.0, u_r,
+                                    4.0, C=C)
+    Lam, sums = L.scan_backward_fused_starts(Ig, ST, Gg, beta, 1.0, u_r, 4.0)
+    assert sums is None and torch.equal(Lam, Lam_ref)
+    Lam2, sums2 = L.scan_backward_fused_starts(Ig, ST, Gg, beta, 1.0, u_r, 4.0, want_sums=True)
+    # with the sums the kernel is the parameter variant (fewer waves per workgroup, so another
+    # association than Lam_ref): it equals lsh_lif_param_bwd's single pass bit for bit
+    from lifscan import _native as nat
+    lib = nat.lib()
+    Lam3 = torch.empty_like(Ig)
+    parts = torch.zeros(lib.lsh_lif_param_partials(T, N, 2, C), 3, device=dev, dtype=torch.float64)
+    Ug, Sg = gpu(Us, dev), gpu(Ss, dev)  # held: the call takes raw pointers
+    nat.check(lib.lsh_lif_param_bwd(nat.ptr(Ig), nat.ptr(u0g), nat.ptr(Ug), nat.ptr(Sg), nat.ptr(Gg),
+                                    nat.ptr(Lam3), nat.ptr(parts), T, N, beta, 1.0, u_r, 4.0, 2, C,
+                                    None, 0, nat.stream_of(Ig)), "lsh_lif_param_bwd")
+    assert torch.equal(Lam2, Lam3) and torch.equal(sums2, parts.sum(0))
+    assert rel(host(Lam2), host(Lam_ref)) < 1e-6
+    # the sums against the fp64 assembly of fit.py:44-47 on the serial trajectory and this Lam
+    _, _, dbeta, dtheta, du_r = O.param_grads(I, u0, Us, Ss, GS, host(Lam2).astype(np.float64),
+                                              beta, 1.0, u_r)
+    s2 = host(sums2)
+    bf = float(beta)  # param_grads scales by beta in fp64
+    assert abs(s2[0] - dbeta) <= 1e-9 * (abs(dbeta) + 1.0)
+    assert abs(-s2[1] - dtheta) <= 1e-5 * (abs(dtheta) + 1.0)
+    # s_t*lam_{t+1} takes lam_{t+1} at a chunk's last step from the composed chain, one fp32
+    # rounding away from the stored value
+    assert abs(bf * s2[2] - du_r) <= 1e-6 * (abs(du_r) + 1.0)
+
+
+@pytest.mark.parametrize("T,N", [(1024, 16384), (256, 17000)])
+def test_lif_tuned_recomputing_path_equals_stored_path(L, dev, T, N):
+    """lif_tuned in scan mode takes the recomputing pair at these shapes; S and every gradient
+    equal those of the path that stores U (switch off)."""
+    assert L._recompute_ok(T, N, 8, 10 ** 6)
+    I = gpu(normal(T, N, 0.15, 0.4, 31), dev)
+    GS = gpu(normal(T, N, 0.0, 1.0, 32), dev)
+    u0 = gpu(uniform(N, -0.3, 0.3, 33), dev)
+    out = []
+    for rc in (True, False):
+        L.RECOMPUTE_BWD = rc
+        try:
+            Ig = I.clone().requires_grad_(True)
+            ug = u0.clone().requires_grad_(True)
+            b = torch.tensor(0.9, device=dev, requires_grad=True)
+            S = L.lif_tuned(Ig, ug, b, 1.0, 0.0, 4.0, mode="scan", K=8, repair=10 ** 6)
+            S.backward(GS)
+            out.append((S.detach(), Ig.grad, ug.grad, b.grad.item()))
+        finally:
+            L.RECOMPUTE_BWD = True
+    (S1, g1, u1, b1), (S2, g2, u2, b2) = out
+    assert torch.equal(S1, S2) and torch.equal(g1, g2) and torch.equal(u1, u2)
+    assert abs(b1 - b2) <= 1e-6 * abs(b2)

@@ -164,8 +164,10 @@ def bench_cfg3(torch, dev, reps):
             S.backward(g2)
     out["lif_layers_fwd_bwd_ms"] = ev_time(layers, reps, warm=2)
     nsteps = 2 * T * I1.shape[1]
+    nbytes = (B_FWD_RC + B_BWD_RC) if L._recompute_ok(T, I1.shape[1], 16, 10 ** 6) else (B_FWD + B_BWD)
+    out["lif_layers_bytes_per_neuron_step"] = nbytes
     out["lif_layers_pct_roofline"] = round(
-        100 * (B_FWD + B_BWD) * nsteps / (out["lif_layers_fwd_bwd_ms"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
+        100 * nbytes * nsteps / (out["lif_layers_fwd_bwd_ms"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
     out["config"] = "700-256-256-20, B=64, T=1024, beta=0.95, lif_tuned(scan, K=16, repair on)"
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out.items()}
 

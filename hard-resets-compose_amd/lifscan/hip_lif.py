@@ -783,19 +783,35 @@ class LIFAuto(torch.autograd.Function):
     def forward(ctx, I, u0, beta, theta, u_r, alpha, K, repair, fwd_mode, bwd_mode):
         I = I.contiguous()
         b = _f32(beta)
+        ctx.cfg = (b, theta, u_r, alpha, bwd_mode)
+        T, N = I.shape
+        # the serial forward's bits are the single-pass exact forward's; with the fused adjoint
+        # behind it the recomputing pair applies (U is kept only for the backward)
+        if (fwd_mode == "serial" and bwd_mode == "scan"
+                and _recompute_ok(T, N, K, max(int(repair), T))):
+            S, ST = scan_forward_exact_starts(I, b, theta, u_r, u0)
+            ctx.save_for_backward(I, u0, ST)
+            ctx.recompute = True
+            return S
         if fwd_mode == "scan":
             U, S = scan_forward_auto(I, b, theta, u_r, u0, K=K, repair=repair)
         else:
             U, S = serial_forward_auto(I, b, theta, u_r, u0)
         ctx.save_for_backward(I, u0, U, S)
-        ctx.cfg = (b, theta, u_r, alpha, bwd_mode)
+        ctx.recompute = False
         return S
 
     @staticmethod
     def backward(ctx, gS):
-        I, u0, U, S = ctx.saved_tensors
         b, theta, u_r, alpha, bwd_mode = ctx.cfg
         gS = gS.contiguous()
+        if ctx.recompute:
+            I, u0, ST = ctx.saved_tensors
+            need_b = ctx.needs_input_grad[2]
+            Lam, sums = scan_backward_fused_starts(I, ST, gS, b, theta, u_r, alpha, need_b)
+            db = sums[0].float().reshape(()) if need_b else None
+            return (Lam, b * Lam[0], db, None, None, None, None, None, None, None)
+        I, u0, U, S = ctx.saved_tensors
         if bwd_mode == "scan":
             Lam = scan_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
         else:

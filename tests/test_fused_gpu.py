@@ -227,3 +227,25 @@ def test_lif_tuned_recomputing_path_equals_stored_path(L, dev, T, N):
     (S1, g1, u1, b1), (S2, g2, u2, b2) = out
     assert torch.equal(S1, S2) and torch.equal(g1, g2) and torch.equal(u1, u2)
     assert abs(b1 - b2) <= 1e-6 * abs(b2)
+
+
+def test_lif_auto_recomputing_path_equals_stored_path(L, dev):
+    """lif_auto at N = 16384 runs the serial forward and the scan adjoint; the recomputing pair
+    gives the same S and gradients."""
+    T, N = 1024, 16384
+    assert L.auto_modes(N, T) == ("serial", "scan")
+    I = gpu(normal(T, N, 0.15, 0.4, 41), dev)
+    GS = gpu(normal(T, N, 0.0, 1.0, 42), dev)
+    out = []
+    for rc in (True, False):
+        L.RECOMPUTE_BWD = rc
+        try:
+            Ig = I.clone().requires_grad_(True)
+            u0 = torch.zeros(N, device=dev, requires_grad=True)
+            S = L.lif_auto(Ig, u0, 0.95, 1.0, 0.0, 4.0)
+            S.backward(GS)
+            out.append((S.detach(), Ig.grad, u0.grad))
+        finally:
+            L.RECOMPUTE_BWD = True
+    (S1, g1, u1), (S2, g2, u2) = out
+    assert torch.equal(S1, S2) and torch.equal(g1, g2) and torch.equal(u1, u2)

@@ -63,19 +63,32 @@ class LIFParamFn(torch.autograd.Function):
     def forward(ctx, I, u0, beta, theta, u_r, alpha, fwd_mode, bwd_mode, K):
         b, th, ur = _f32s(beta, theta, u_r)
         I = I.contiguous()
+        ctx.cfg = (b, th, ur, float(alpha), bwd_mode)
+        T, N = I.shape
+        # the serial forward's bits are the single-pass exact forward's: with the single-pass
+        # adjoint behind it, keep the chunk entry states instead of U (same S and gradients)
+        if fwd_mode == "serial" and bwd_mode == "scan" and L._recompute_ok(T, N, K, T):
+            S, ST = L.scan_forward_exact_starts(I, b, th, ur, u0)
+            ctx.save_for_backward(I, u0, ST)
+            ctx.recompute = True
+            return S
         if fwd_mode == "scan":
             U, S = L.scan_forward_auto(I, b, th, ur, u0, K=K)
         else:
             U, S = L.serial_forward_auto(I, b, th, ur, u0)
         ctx.save_for_backward(I, u0, U, S)
-        ctx.cfg = (b, th, ur, float(alpha), bwd_mode)
+        ctx.recompute = False
         return S
 
     @staticmethod
     def backward(ctx, gS):
-        I, u0, U, S = ctx.saved_tensors
         b, th, ur, alpha, bwd_mode = ctx.cfg
-        lam, sums = _param_backward(I, u0, U, S, gS.contiguous(), b, th, ur, alpha, bwd_mode)
+        if ctx.recompute:
+            I, u0, ST = ctx.saved_tensors
+            lam, sums = L.scan_backward_fused_starts(I, ST, gS.contiguous(), b, th, ur, alpha, True)
+        else:
+            I, u0, U, S = ctx.saved_tensors
+            lam, sums = _param_backward(I, u0, U, S, gS.contiguous(), b, th, ur, alpha, bwd_mode)
         sums = sums.float()
         return (lam, b * lam[0], sums[0], -sums[1], b * sums[2], None, None, None, None)
 

@@ -80,3 +80,39 @@ def test_lif_param_partials(dev, mode, C):
     assert rel(sums[0], want[2]) < 1e-4
     assert rel(-sums[1], want[3]) < 1e-4
     assert rel(beta * sums[2], want[4]) < 1e-4
+
+
+def test_lif_param_auto_recomputing_path(dev):
+    """mode="auto" at N = 16384: serial forward and scan adjoint, which lif_param runs as the
+    recomputing pair; S, dI, du0 equal the stored path's, the parameter gradients agree to
+    fp64 summation order, and both match the fp64 assembly."""
+    from lifscan import hip_lif as L
+    from lifscan.fit import lif_param
+    T, N = 1024, 16384
+    beta, theta, u_r = 0.93, 1.0, -0.1
+    I = (np.float32(0.5) * normal(T, N, 0.0, 1.0, 51) + np.float32(0.08)).astype(np.float32)
+    W = normal(T, N, 0.0, 1.0, 52)
+    res = []
+    for rc in (True, False):
+        L.RECOMPUTE_BWD = rc
+        try:
+            Ig = gpu(I, dev).requires_grad_(True)
+            ug = torch.zeros(N, device=dev, requires_grad=True)
+            ps = [torch.tensor(v, device=dev, requires_grad=True) for v in (beta, theta, u_r)]
+            S = lif_param(Ig, ug, *ps, mode="auto")
+            (gpu(W, dev) * S).sum().backward()
+            res.append((S.detach(), Ig.grad, ug.grad, [p.grad.item() for p in ps]))
+        finally:
+            L.RECOMPUTE_BWD = True
+    (S1, g1, u1, p1), (S2, g2, u2, p2) = res
+    assert torch.equal(S1, S2) and torch.equal(g1, g2) and torch.equal(u1, u2)
+    for a, b in zip(p1, p2):
+        assert abs(a - b) <= 1e-6 * abs(b)
+    u0 = np.zeros(N, np.float32)
+    Uo, So = O.serial_forward(I, beta, theta, u_r, u0)
+    assert np.array_equal(host(S1), So)
+    Lam = O.serial_backward(I, u0, Uo, So, W, None, beta, theta, u_r, 4.0, True, dtype=np.float64)
+    want = O.param_grads(I, u0, Uo, So, W, Lam, beta, theta, u_r, 4.0)
+    assert rel(host(g1), want[0]) < 1e-4
+    for k in range(3):
+        assert rel(p1[k], want[2 + k]) < 1e-4, k

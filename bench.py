@@ -270,11 +270,22 @@ def bench_cfg5(torch, dev, reps):
     out["box_scan_repair"] = box
     del Wprev, preds
     out["bwd_scan_ms"] = ev_time(lambda: A.alif_backward(I, U, W, S, gS, beta, rho, q, 1.0, z, z), reps)
+    # the layer's adjoint (dI, dw0 and the parameter sums, LW not written): reading the stored
+    # states, and recomputing them inside each chunk from the row before it
+    from lifscan import hip_alif as H
+    for name, rc in (("stored", None), ("recompute", 0.0)):
+        out[f"bwd_layer_{name}_ms"] = ev_time(lambda: H._alif_bwd_call(
+            I, U, W, S, gS, beta, rho, q, 1.0, z, z, 4.0, "scan", 64, want_lw=False, want_params=True,
+            recompute_ur=rc), reps)
     ns = T * N
     t = out["alif_fwd_serial_bwd_scan_ms"]
     out["fwd_bwd_value"] = round(ns / (t / 1000.0), 1)
-    # ALIF algorithmic bytes: fwd read I, write U, W, S (16); bwd read I, U, W, S, gS, write dI (24)
-    out["pct_roofline_fwd_bwd"] = round(100 * 40 * ns / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
+    # ALIF algorithmic bytes: fwd read I, write U, W, S (16); bwd read I, U, W, S, gS, write dI
+    # (24), or with the recomputing adjoint read I, gS and U, W once per 16-step chunk, write dI
+    # (12.5)
+    bps = 16 + (12.5 if H.ALIF_RECOMPUTE_BWD else 24)
+    out["bytes_per_neuron_step"] = bps
+    out["pct_roofline_fwd_bwd"] = round(100 * bps * ns / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
     out["config"] = "ALIF N=16384, T=4096, beta=0.95, rho=0.995, q=0.2, x~N(0.15,0.3^2)"
     del I, gS, U, W, S, Ig
     torch.cuda.empty_cache()

@@ -27,6 +27,16 @@ __device__ __forceinline__ float alif_step(float u, float& w, float x, float bet
   return s ? u_r : v;
 }
 
+// The four parameters from device memory, [beta, rho, q, theta0] as fp32, for callers that keep
+// them on the device (a 0-d tensor per parameter): no device-to-host read before the launch.
+__device__ __forceinline__ void alif_params_from(const float* __restrict__ p, float& beta,
+                                                 float& rho, float& q, float& theta0) {
+  beta = p[0];
+  rho = p[1];
+  q = p[2];
+  theta0 = p[3];
+}
+
 // numpy-style min/max (a NaN operand gives NaN), as the oracle evaluates them
 __device__ __forceinline__ float nmin(float a, float b) {
   return (a != a) ? a : ((b != b) ? b : (a < b ? a : b));
@@ -44,7 +54,9 @@ __global__ __launch_bounds__(64) void k_alif_fwd(const float* __restrict__ I,
                                                  float* __restrict__ W, float* __restrict__ S,
                                                  float* __restrict__ eu, float* __restrict__ ew,
                                                  int64_t N, int64_t Ls, int NB, float beta, float rho,
-                                                 float q, float theta0, float u_r) {
+                                                 float q, float theta0, float u_r,
+                                                 const float* __restrict__ dpar) {
+  if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
   const int64_t m = blockIdx.x / NB;
   const int nb = (int)(blockIdx.x - m * NB);
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
@@ -644,7 +656,8 @@ __global__ __launch_bounds__(64) void k_alif_bwd(
     const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
     float* __restrict__ PA_, float* __restrict__ PB_, const float* __restrict__ lam_end,
     float* __restrict__ DW0, double* __restrict__ partials, int64_t N, int64_t Ls, int NB,
-    float beta, float rho, float q, float theta0, float alpha) {
+    float beta, float rho, float q, float theta0, float alpha, const float* __restrict__ dpar) {
+  if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
   const int64_t m = blockIdx.x / NB;
   const int nb = (int)(blockIdx.x - m * NB);
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
@@ -701,7 +714,8 @@ __global__ __launch_bounds__(64) void k_alif_bwd_serial(
     const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
     const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
     float* __restrict__ DW0, double* __restrict__ partials, int64_t N, int64_t T, float beta,
-    float rho, float q, float theta0, float alpha) {
+    float rho, float q, float theta0, float alpha, const float* __restrict__ dpar) {
+  if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
   const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
   ParamAcc acc;
   if (n < N) {
@@ -771,13 +785,18 @@ __global__ __launch_bounds__(64) void k_alif_bwd_serial(
 // (which reads lw_t) into (P2, Q2), takes lv at its chunk end the same way and replays lv.
 // WLW: write LW.  PS: also keep u_{t-1}, w_{t-1} and sum the parameter gradients (one
 // partials row per workgroup).  DW0 (if given) receives lw_{-1} from the first chunk.
-template <int C, int WV, bool WLW, bool PS>
+// RC: S is not read and U, W only at the row before each chunk; the chunk's u_{t-1}, w_{t-1}
+// and s_t are recomputed with the forward's own step (alif_step, reset value u_r) from that
+// entry state, which gives the stored bits when U, W, S come from one serial trajectory.  The
+// adjoint arithmetic is unchanged, so the outputs equal the stored-state variant's bit for bit.
+template <int C, int WV, bool WLW, bool PS, bool RC = false>
 __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
     const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
     float* __restrict__ DW0, double* __restrict__ partials, int64_t N, int M, float beta,
-    float rho, float q, float theta0, float alpha) {
+    float rho, float q, float theta0, float alpha, float u_r, const float* __restrict__ dpar) {
+  if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
   __shared__ float sP[WV][WAVE], sQ[WV][WAVE];
   __shared__ float sLw[WAVE], sLv[WAVE];
   __shared__ double sAcc[WV][4];
@@ -803,7 +822,29 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
     float sg[C], g[C], s1[C], lwv[C];
     float upv[PS ? C : 1], wpv[PS ? C : 1];
     float lw_end = 0.0f, lv_end = 0.0f;
-    if (active) {
+    if (active && RC) {
+      const Buf bi(I + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
+      float up = row0 > 0 ? ld_row(U + nb0 + (row0 - 1) * N, lb) : u0n;
+      float wp = row0 > 0 ? ld_row(W + nb0 + (row0 - 1) * N, lb) : w0n;
+      float xv[C];
+#pragma unroll
+      for (int j = 0; j < C; ++j) {
+        const unsigned so = j * rstride;
+        xv[j] = bi.ld(lb, so);
+        g[j] = bg.ld(lb, so);
+      }
+#pragma unroll
+      for (int j = 0; j < C; ++j) {
+        sg[j] = alif_sg(up, wp, xv[j], beta, theta0, alpha);
+        if (PS) {
+          upv[j] = up;
+          wpv[j] = wp;
+        }
+        bool sp;
+        up = alif_step(up, wp, xv[j], beta, rho, q, theta0, u_r, sp);
+        s1[j] = sp ? 0.0f : 1.0f;
+      }
+    } else if (active) {
       const Buf bi(I + nb0 + row0 * N), bs(S + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
       const Buf bu(U + nb0 + row0 * N), bw(W + nb0 + row0 * N);
       const float up0 = row0 > 0 ? ld_row(U + nb0 + (row0 - 1) * N, lb) : u0n;
@@ -821,6 +862,8 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
           wpv[j] = wp;
         }
       }
+    }
+    if (active) {
       float P = 1.0f, Q = 0.0f;
 #pragma unroll
       for (int j = C - 1; j >= 0; --j) {
@@ -975,10 +1018,11 @@ static void launch_alif_build(const float* I, char* w, const lsh_alif_layout& L,
 template <int D>
 static void launch_alif_fwd(const float* I, const float* su, const float* sw, float* U, float* W,
                             float* S, float* eu, float* ew, int64_t N, int64_t Ls, int64_t M,
-                            float beta, float rho, float q, float theta0, float u_r, hipStream_t st) {
+                            float beta, float rho, float q, float theta0, float u_r, hipStream_t st,
+                            const float* dpar = nullptr) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   hipLaunchKernelGGL(k_alif_fwd<D>, dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, su, sw, U, W, S,
-                     eu, ew, N, Ls, NB, beta, rho, q, theta0, u_r);
+                     eu, ew, N, Ls, NB, beta, rho, q, theta0, u_r, dpar);
 }
 
 }  // namespace lsh
@@ -994,6 +1038,20 @@ extern "C" int lsh_alif_serial_fwd(const float* I, const float* u0, const float*
   if (T == 0 || N == 0) return LSH_OK;
   launch_alif_fwd<16>(I, u0, w0, U, W, S, nullptr, nullptr, N, T, 1, beta, rho, q, theta0, u_r,
                       (hipStream_t)stream);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" int lsh_alif_serial_fwd_dparams(const float* I, const float* u0, const float* w0,
+                                           float* U, float* W, float* S, int64_t T, int64_t N,
+                                           const float* params, float u_r, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(w0) || bad_ptr(U) || bad_ptr(W) || bad_ptr(S) ||
+      bad_ptr(params))
+    return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  launch_alif_fwd<16>(I, u0, w0, U, W, S, nullptr, nullptr, N, T, 1, 0.0f, 0.0f, 0.0f, 0.0f, u_r,
+                      (hipStream_t)stream, params);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }
@@ -1110,37 +1168,41 @@ extern "C" int64_t lsh_alif_bwd_partials(int64_t T, int64_t N, int mode, int C) 
   return (T / C) * NB;
 }
 
-template <int C, int W, bool WLW, bool PS>
+template <int C, int W, bool WLW, bool PS, bool RC>
 static void launch_alif_fused_w(const float* I, const float* u0, const float* w0, const float* U,
                                 const float* W_, const float* S, const float* GS, float* LW,
                                 float* LV, float* DW0, double* partials, int64_t N, int M, int NB,
                                 float beta, float rho, float q, float theta0, float alpha,
-                                hipStream_t st) {
-  hipLaunchKernelGGL((k_alif_bwd_fused<C, W, WLW, PS>), dim3((unsigned)NB), dim3(WAVE * W), 0, st, I,
-                     u0, w0, U, W_, S, GS, LW, LV, DW0, partials, N, M, beta, rho, q, theta0, alpha);
+                                float u_r, hipStream_t st, const float* dpar) {
+  hipLaunchKernelGGL((k_alif_bwd_fused<C, W, WLW, PS, RC>), dim3((unsigned)NB), dim3(WAVE * W), 0, st,
+                     I, u0, w0, U, W_, S, GS, LW, LV, DW0, partials, N, M, beta, rho, q, theta0,
+                     alpha, u_r, dpar);
 }
 
-template <int C, bool WLW, bool PS>
+// RC (recompute the states) keeps the stored-state variant's wave count, so both sum the
+// chunks in the same order.
+template <int C, bool WLW, bool PS, bool RC = false>
 static void launch_alif_fused(const float* I, const float* u0, const float* w0, const float* U,
                               const float* W, const float* S, const float* GS, float* LW, float* LV,
                               float* DW0, double* partials, int64_t N, int M, int NB, float beta,
-                              float rho, float q, float theta0, float alpha, hipStream_t st) {
+                              float rho, float q, float theta0, float alpha, hipStream_t st,
+                              const float* dpar, float u_r = 0.0f) {
   // registers allow 16 waves at C = 16 without the parameter sums, 4 at C = 32 with them, else 8
   constexpr int WMAX = (C == 16 && !PS) ? 16 : ((C == 32 && PS) ? 4 : 8);
   const int nw = fused_waves(NB, WMAX);
   if constexpr (WMAX >= 16) {
     if (nw == 16) {
-      launch_alif_fused_w<C, 16, WLW, PS>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB, beta,
-                                          rho, q, theta0, alpha, st);
+      launch_alif_fused_w<C, 16, WLW, PS, RC>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB,
+                                              beta, rho, q, theta0, alpha, u_r, st, dpar);
       return;
     }
   }
   if (nw == 8)
-    launch_alif_fused_w<C, 8, WLW, PS>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB, beta,
-                                       rho, q, theta0, alpha, st);
+    launch_alif_fused_w<C, 8, WLW, PS, RC>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB,
+                                           beta, rho, q, theta0, alpha, u_r, st, dpar);
   else
-    launch_alif_fused_w<C, 4, WLW, PS>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB, beta,
-                                       rho, q, theta0, alpha, st);
+    launch_alif_fused_w<C, 4, WLW, PS, RC>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB,
+                                           beta, rho, q, theta0, alpha, u_r, st, dpar);
 }
 
 template <bool WLW, bool PS>
@@ -1148,16 +1210,16 @@ static void launch_alif_serial_bwd(const float* I, const float* u0, const float*
                                    const float* W, const float* S, const float* GS, float* LW,
                                    float* LV, float* DW0, double* partials, int64_t N, int64_t T,
                                    int NB, float beta, float rho, float q, float theta0, float alpha,
-                                   hipStream_t st) {
+                                   hipStream_t st, const float* dpar) {
   hipLaunchKernelGGL((k_alif_bwd_serial<8, WLW, PS>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, w0,
-                     U, W, S, GS, LW, LV, DW0, partials, N, T, beta, rho, q, theta0, alpha);
+                     U, W, S, GS, LW, LV, DW0, partials, N, T, beta, rho, q, theta0, alpha, dpar);
 }
 
-extern "C" int lsh_alif_bwd(const float* I, const float* U, const float* W, const float* S,
-                            const float* GS, const float* u0, const float* w0, float* LV,
-                            float* LW, float* DW0, double* partials, int64_t T, int64_t N,
-                            float beta, float rho, float q, float theta0, float alpha, int mode,
-                            int C, void* ws, size_t ws_bytes, void* stream) {
+static int alif_bwd(const float* I, const float* U, const float* W, const float* S,
+                    const float* GS, const float* u0, const float* w0, float* LV, float* LW,
+                    float* DW0, double* partials, int64_t T, int64_t N, float beta, float rho,
+                    float q, float theta0, float alpha, const float* dpar, int mode, int C, void* ws,
+                    size_t ws_bytes, void* stream) {
   if (bad_ptr(I) || bad_ptr(U) || bad_ptr(W) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(u0) ||
       bad_ptr(w0) || bad_ptr(LV))
     return LSH_ERR_ARG;
@@ -1171,16 +1233,16 @@ extern "C" int lsh_alif_bwd(const float* I, const float* U, const float* W, cons
   if (mode == 0) {
     if (wlw && ps)
       launch_alif_serial_bwd<true, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, NB, beta,
-                                         rho, q, theta0, alpha, st);
+                                         rho, q, theta0, alpha, st, dpar);
     else if (wlw)
       launch_alif_serial_bwd<true, false>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, NB,
-                                          beta, rho, q, theta0, alpha, st);
+                                          beta, rho, q, theta0, alpha, st, dpar);
     else if (ps)
       launch_alif_serial_bwd<false, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, NB,
-                                          beta, rho, q, theta0, alpha, st);
+                                          beta, rho, q, theta0, alpha, st, dpar);
     else
       launch_alif_serial_bwd<false, false>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, NB,
-                                           beta, rho, q, theta0, alpha, st);
+                                           beta, rho, q, theta0, alpha, st, dpar);
     LSH_CHECK_LAUNCH();
     return LSH_OK;
   }
@@ -1194,16 +1256,16 @@ extern "C" int lsh_alif_bwd(const float* I, const float* U, const float* W, cons
   do {                                                                                             \
     if (wlw && ps)                                                                                 \
       launch_alif_fused<CC, true, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB,   \
-                                        beta, rho, q, theta0, alpha, st);                          \
+                                        beta, rho, q, theta0, alpha, st, dpar);                    \
     else if (wlw)                                                                                  \
       launch_alif_fused<CC, true, false>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB,  \
-                                         beta, rho, q, theta0, alpha, st);                         \
+                                         beta, rho, q, theta0, alpha, st, dpar);                   \
     else if (ps)                                                                                   \
       launch_alif_fused<CC, false, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB,  \
-                                         beta, rho, q, theta0, alpha, st);                         \
+                                         beta, rho, q, theta0, alpha, st, dpar);                   \
     else                                                                                           \
       launch_alif_fused<CC, false, false>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, NB, \
-                                          beta, rho, q, theta0, alpha, st);                        \
+                                          beta, rho, q, theta0, alpha, st, dpar);                  \
   } while (0)
     if (C == 16)
       LSH_FUSED(16);
@@ -1224,19 +1286,85 @@ extern "C" int lsh_alif_bwd(const float* I, const float* U, const float* W, cons
   float* LE = reinterpret_cast<float*>(w + 2 * mn);
   const dim3 g((unsigned)((int64_t)M * NB)), b(WAVE), gc((unsigned)NB);
   hipLaunchKernelGGL((k_alif_bwd<0, false>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_,
-                     nullptr, nullptr, nullptr, N, C, NB, beta, rho, q, theta0, alpha);
+                     nullptr, nullptr, nullptr, N, C, NB, beta, rho, q, theta0, alpha, dpar);
   hipLaunchKernelGGL(k_rev_carry, gc, b, 0, st, PA_, PB_, LE, N, M);
   hipLaunchKernelGGL((k_alif_bwd<1, false>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_, LE,
-                     DW0, nullptr, N, C, NB, beta, rho, q, theta0, alpha);
+                     DW0, nullptr, N, C, NB, beta, rho, q, theta0, alpha, dpar);
   hipLaunchKernelGGL((k_alif_bwd<2, false>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_,
-                     nullptr, nullptr, nullptr, N, C, NB, beta, rho, q, theta0, alpha);
+                     nullptr, nullptr, nullptr, N, C, NB, beta, rho, q, theta0, alpha, dpar);
   hipLaunchKernelGGL(k_rev_carry, gc, b, 0, st, PA_, PB_, LE, N, M);
   if (ps)
     hipLaunchKernelGGL((k_alif_bwd<3, true>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_,
-                       LE, nullptr, partials, N, C, NB, beta, rho, q, theta0, alpha);
+                       LE, nullptr, partials, N, C, NB, beta, rho, q, theta0, alpha, dpar);
   else
     hipLaunchKernelGGL((k_alif_bwd<3, false>), g, b, 0, st, I, u0, w0, U, W, S, GS, LW, LV, PA_, PB_,
-                       LE, nullptr, nullptr, N, C, NB, beta, rho, q, theta0, alpha);
+                       LE, nullptr, nullptr, N, C, NB, beta, rho, q, theta0, alpha, dpar);
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
+}
+
+extern "C" int lsh_alif_bwd(const float* I, const float* U, const float* W, const float* S,
+                            const float* GS, const float* u0, const float* w0, float* LV,
+                            float* LW, float* DW0, double* partials, int64_t T, int64_t N,
+                            float beta, float rho, float q, float theta0, float alpha, int mode,
+                            int C, void* ws, size_t ws_bytes, void* stream) {
+  return alif_bwd(I, U, W, S, GS, u0, w0, LV, LW, DW0, partials, T, N, beta, rho, q, theta0, alpha,
+                  nullptr, mode, C, ws, ws_bytes, stream);
+}
+
+extern "C" int lsh_alif_bwd_dparams(const float* I, const float* U, const float* W,
+                                    const float* S, const float* GS, const float* u0,
+                                    const float* w0, float* LV, float* LW, float* DW0,
+                                    double* partials, int64_t T, int64_t N, const float* params,
+                                    float alpha, int mode, int C, void* ws, size_t ws_bytes,
+                                    void* stream) {
+  if (bad_ptr(params)) return LSH_ERR_ARG;
+  return alif_bwd(I, U, W, S, GS, u0, w0, LV, LW, DW0, partials, T, N, 0.0f, 0.0f, 0.0f, 0.0f,
+                  alpha, params, mode, C, ws, ws_bytes, stream);
+}
+
+// Single-pass adjoint with the states recomputed from the rows before each chunk (RC above);
+// params (if given) is the device vector [beta, rho, q, theta0] read in place of the floats.
+extern "C" int lsh_alif_bwd_recompute(const float* I, const float* U, const float* W,
+                                      const float* GS, const float* u0, const float* w0, float* LV,
+                                      float* LW, float* DW0, double* partials, int64_t T, int64_t N,
+                                      const float* params, float beta, float rho, float q,
+                                      float theta0, float u_r, float alpha, int C, void* stream) {
+  if (bad_ptr(I) || bad_ptr(U) || bad_ptr(W) || bad_ptr(GS) || bad_ptr(u0) || bad_ptr(w0) ||
+      bad_ptr(LV))
+    return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C != 16 && C != 32) return LSH_ERR_SHAPE;
+  if (T % C != 0) return LSH_ERR_DIVISIBILITY;
+  if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+  if (T == 0 || N == 0) return LSH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  const int M = (int)(T / C);
+  const bool wlw = LW != nullptr, ps = partials != nullptr;
+  const float* S = nullptr;  // not read
+  const float* dpar = params;
+#define LSH_FUSED_RC(CC)                                                                           \
+  do {                                                                                             \
+    if (wlw && ps)                                                                                 \
+      launch_alif_fused<CC, true, true, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, M, \
+                                              NB, beta, rho, q, theta0, alpha, st, dpar, u_r);     \
+    else if (wlw)                                                                                  \
+      launch_alif_fused<CC, true, false, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N,   \
+                                               M, NB, beta, rho, q, theta0, alpha, st, dpar, u_r); \
+    else if (ps)                                                                                   \
+      launch_alif_fused<CC, false, true, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N,   \
+                                               M, NB, beta, rho, q, theta0, alpha, st, dpar, u_r); \
+    else                                                                                           \
+      launch_alif_fused<CC, false, false, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N,  \
+                                                M, NB, beta, rho, q, theta0, alpha, st, dpar,      \
+                                                u_r);                                              \
+  } while (0)
+  if (C == 16)
+    LSH_FUSED_RC(16);
+  else
+    LSH_FUSED_RC(32);
+#undef LSH_FUSED_RC
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }

@@ -20,6 +20,9 @@ from .hip_lif import _f32, _f32s, _input, _vec, _same, chunked_bwd_C
 # single-pass backward (one workgroup per 64 neurons) pays off only with many neuron blocks
 ALIF_FUSED_BWD_MIN_N = 8192
 ALIF_FUSED_BWD_C = 16
+# ALIFFn's single-pass adjoint after the serial forward recomputes u, w, s inside each chunk from
+# the stored row before it (lsh_alif_bwd_recompute) instead of reading U, W, S: same bits
+ALIF_RECOMPUTE_BWD = True
 
 
 def alif_fwd_cfg(N):
@@ -41,6 +44,32 @@ def alif_serial_forward(I, beta, rho, q, theta0, u_r, u0, w0, BN=32, D=0, num_wa
         _n.check(_n.lib().lsh_alif_serial_fwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(U), _n.ptr(W), _n.ptr(S), T, N, _f32(beta),
             _f32(rho), _f32(q), _f32(theta0), _f32(u_r), _n.stream_of(I)), "lsh_alif_serial_fwd")
+    return U, W, S
+
+
+def _dev_params(I, beta, rho, q, theta0):
+    """[beta, rho, q, theta0] as one fp32 vector on I's device when any of them is a device tensor
+    (device ops only: nothing is read back to the host), else None.  Each value is rounded to
+    fp32 as the kernels' float arguments round it."""
+    ps = (beta, rho, q, theta0)
+    if not any(torch.is_tensor(p) and p.device.type != "cpu" for p in ps):
+        return None
+    return torch.stack([p.detach().reshape(()).to(device=I.device, dtype=torch.float32)
+                        if torch.is_tensor(p) else
+                        torch.full((), float(p), device=I.device, dtype=torch.float32) for p in ps])
+
+
+def _alif_serial_forward_dp(I, dp, u_r, u0, w0):
+    """Serial ALIF with the parameters read by the kernel from dp = [beta, rho, q, theta0]."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    w0 = _vec(w0, N, I, "w0")
+    U, W, S = torch.empty_like(I), torch.empty_like(I), torch.empty_like(I)
+    with torch.cuda.device(I.device):
+        _n.check(_n.lib().lsh_alif_serial_fwd_dparams(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(U), _n.ptr(W), _n.ptr(S), T, N, _n.ptr(dp),
+            _f32(u_r), _n.stream_of(I)), "lsh_alif_serial_fwd_dparams")
     return U, W, S
 
 
@@ -189,14 +218,22 @@ def _bwd_mode(mode, T, N, C):
     raise ValueError(f"unknown mode {mode!r}")
 
 
-def _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C, want_lw, want_params):
-    """One lsh_alif_bwd call -> (LV, LW or None, DW0 [N], param sums [4] fp64 or None)."""
+def _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C, want_lw, want_params,
+                   dp=None, recompute_ur=None):
+    """One lsh_alif_bwd call -> (LV, LW or None, DW0 [N], param sums [4] fp64 or None); with dp
+    (device [beta, rho, q, theta0]) the kernels read the parameters from it (lsh_alif_bwd_dparams)
+    and beta, rho, q, theta0 are ignored.  recompute_ur (the reset value u_r) selects, when the
+    mode resolves to the single pass, lsh_alif_bwd_recompute: S is not read and U, W only at
+    chunk boundaries, for U, W, S of one serial trajectory."""
     I = _input(I)
     T, N = I.shape
     u0 = _vec(u0, N, I)
     w0 = _vec(w0, N, I, "w0")
-    U, W, S, GS = (_same(a, I, nm) for a, nm in ((U, "U"), (W, "W"), (S, "S"), (GS, "GS")))
+    U, W, GS = (_same(a, I, nm) for a, nm in ((U, "U"), (W, "W"), (GS, "GS")))
     code, C = _bwd_mode(mode, T, N, C)
+    rc = recompute_ur is not None and code == 2
+    if not rc:
+        S = _same(S, I, "S")
     L = _n.lib()
     LV = torch.empty_like(I)
     LW = torch.empty_like(I) if (want_lw or code == 1) else None
@@ -214,10 +251,23 @@ def _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C,
         nbytes = L.lsh_alif_bwd_workspace(T, N, C)
         ws = _n.workspace(nbytes, I.device)
     with torch.cuda.device(I.device):
-        _n.check(L.lsh_alif_bwd(
-            _n.ptr(I), _n.ptr(U), _n.ptr(W), _n.ptr(S), _n.ptr(GS), _n.ptr(u0), _n.ptr(w0), _n.ptr(LV),
-            _n.ptr(LW), _n.ptr(DW0), _n.ptr(parts), T, N, _f32(beta), _f32(rho), _f32(q), _f32(theta0),
-            _f32(alpha), code, C, _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_alif_bwd")
+        if rc:
+            p = (0.0,) * 4 if dp is not None else (beta, rho, q, theta0)
+            _n.check(L.lsh_alif_bwd_recompute(
+                _n.ptr(I), _n.ptr(U), _n.ptr(W), _n.ptr(GS), _n.ptr(u0), _n.ptr(w0), _n.ptr(LV),
+                _n.ptr(LW), _n.ptr(DW0), _n.ptr(parts), T, N, _n.ptr(dp), *(_f32(v) for v in p),
+                _f32(recompute_ur), _f32(alpha), C, _n.stream_of(I)), "lsh_alif_bwd_recompute")
+        elif dp is not None:
+            _n.check(L.lsh_alif_bwd_dparams(
+                _n.ptr(I), _n.ptr(U), _n.ptr(W), _n.ptr(S), _n.ptr(GS), _n.ptr(u0), _n.ptr(w0),
+                _n.ptr(LV), _n.ptr(LW), _n.ptr(DW0), _n.ptr(parts), T, N, _n.ptr(dp), _f32(alpha), code,
+                C, _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_alif_bwd_dparams")
+        else:
+            _n.check(L.lsh_alif_bwd(
+                _n.ptr(I), _n.ptr(U), _n.ptr(W), _n.ptr(S), _n.ptr(GS), _n.ptr(u0), _n.ptr(w0),
+                _n.ptr(LV), _n.ptr(LW), _n.ptr(DW0), _n.ptr(parts), T, N, _f32(beta), _f32(rho),
+                _f32(q), _f32(theta0), _f32(alpha), code, C, _n.ptr(ws), nbytes, _n.stream_of(I)),
+                "lsh_alif_bwd")
     sums = parts.sum(0) if parts is not None else None
     return LV, (LW if want_lw else None), DW0, sums
 
@@ -238,19 +288,28 @@ class ALIFFn(torch.autograd.Function):
     Forward: serial, or the box scan with prediction Wpred (K1 = K2 = 32, block 4, no repair,
     as the reference); backward: serial or scan.  Gradients for I, u0, w0, beta, rho, q, theta0:
     the adjoint kernels also return dL/dw0 and the four parameter sums (fp64), so LW is never
-    written to memory."""
+    written to memory.  Parameters may be floats or 0-d tensors; with the serial forward, device
+    tensors stay on the device (the kernels read them there, no host synchronization), while the
+    box scan reads them on the host as the reference does (triton_alif.py:530)."""
 
     @staticmethod
     def forward(ctx, I, u0, w0, beta, rho, q, theta0, u_r, alpha, fwd, bwd, Wpred, dw, C, Cb):
-        b, r, qq, th = _f32s(beta, rho, q, theta0)
         ctx.set_materialize_grads(False)  # U and W usually get no gradient: no zero fills
-        if fwd == "serial":
+        dp = _dev_params(I, beta, rho, q, theta0) if fwd == "serial" else None
+        ctx.dp = dp
+        if dp is not None:
+            b = r = qq = th = None
+            U, W, S = _alif_serial_forward_dp(I, dp, u_r, u0, w0)
+        elif fwd == "serial":
+            b, r, qq, th = _f32s(beta, rho, q, theta0)
             U, W, S = alif_serial_forward(I, b, r, qq, th, u_r, u0, w0)
         else:
+            b, r, qq, th = _f32s(beta, rho, q, theta0)
             U, W, S = alif_scan_forward(I, b, r, qq, th, u_r, u0, w0, Wpred, dw, C=C, K1=32, K2=32,
                                         BN=4, BNc=1, D=4)
         ctx.save_for_backward(I, u0, w0, U, W, S)
         ctx.c = (b, r, qq, th, u_r, alpha, bwd, Cb)
+        ctx.serial = fwd == "serial"
         ctx.mark_non_differentiable(U, W)
         return S, U, W
 
@@ -262,22 +321,24 @@ class ALIFFn(torch.autograd.Function):
         b, r, qq, th, u_r, alpha, bwd, Cb = ctx.c
         need = ctx.needs_input_grad
         want_params = any(need[3:7])
+        dp = ctx.dp
         LV, _, DW0, sums = _alif_bwd_call(I, U, W, S, gS.contiguous(), b, r, qq, th, u0, w0, alpha,
                                           "serial_tuned" if bwd == "serial" else bwd, Cb,
-                                          want_lw=False, want_params=want_params)
-        if sums is None:
-            db = dr = dq = dth = None
-        else:
+                                          want_lw=False, want_params=want_params, dp=dp,
+                                          recompute_ur=u_r if ctx.serial and ALIF_RECOMPUTE_BWD else None)
+        db = dr = dq = dth = None
+        if sums is not None:  # a gradient only for the parameters given as tensors
             sums = sums.float()
-            db, dr, dq, dth = sums[0], sums[1], sums[2], -sums[3]
-        return (LV, b * LV[0], DW0.reshape(w0.shape) if w0.dim() else DW0, db, dr, dq, dth,
+            db, dr, dq = (sums[k] if need[3 + k] else None for k in range(3))
+            dth = -sums[3] if need[6] else None
+        du0 = (dp[0] if dp is not None else b) * LV[0]
+        return (LV, du0, DW0.reshape(w0.shape) if w0.dim() else DW0, db, dr, dq, dth,
                 None, None, None, None, None, None, None, None)
 
 
 def alif(I, u0, w0, beta, rho, q, theta0=1.0, u_r=0.0, alpha=4.0, fwd="serial", bwd="scan",
          Wpred=None, dw=None, C=128, Cb=64):
     """Differentiable ALIF layer -> (S, U, W) (triton_alif.py:557-560).  Parameters may be
-    0-d tensors (requires_grad) or floats."""
-    t = lambda v: v if torch.is_tensor(v) else torch.tensor(float(v), device=I.device)
-    return ALIFFn.apply(I, u0, w0, t(beta), t(rho), t(q), t(theta0), u_r, alpha, fwd, bwd, Wpred,
-                        dw, C, Cb)
+    0-d tensors (requires_grad) or floats; floats are passed to the kernels as they are (the
+    reference wraps them in device tensors and reads them back, the same fp32 values)."""
+    return ALIFFn.apply(I, u0, w0, beta, rho, q, theta0, u_r, alpha, fwd, bwd, Wpred, dw, C, Cb)

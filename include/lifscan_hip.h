@@ -193,6 +193,13 @@ int lsh_lif_scan_fused_bwd_starts(const float* I, const float* STARTS, const flo
 int lsh_alif_serial_fwd(const float* I, const float* u0, const float* w0, float* U, float* W,
                         float* S, int64_t T, int64_t N, float beta, float rho, float q,
                         float theta0, float u_r, void* stream);
+/* The same forward with params = device pointer to [beta, rho, q, theta0] (fp32), for callers
+ * whose parameters are device tensors (triton_alif.py:530 reads them with float(), a device-to-
+ * host copy before every launch); U, W, S are bit-identical to lsh_alif_serial_fwd with those
+ * values. */
+int lsh_alif_serial_fwd_dparams(const float* I, const float* u0, const float* w0, float* U,
+                                float* W, float* S, int64_t T, int64_t N, const float* params,
+                                float u_r, void* stream);
 
 /* Predicted chunk-entry adaptation WP[T/C, N]: chunk m simulates chunks max(m-Wn, 0)..m-1 from
  * (u_init, w_init), from (UI, WI)[max(m-Wn,0)] when both are given, or from (u0, w0) when the
@@ -339,6 +346,24 @@ int lsh_alif_bwd(const float* I, const float* U, const float* W, const float* S,
                  double* partials, int64_t T, int64_t N, float beta, float rho, float q,
                  float theta0, float alpha, int mode, int C, void* ws, size_t ws_bytes,
                  void* stream);
+/* lsh_alif_bwd with params = device pointer to [beta, rho, q, theta0] (fp32), the parameters of
+ * ALIFFn.backward (triton_alif.py:543-554) when they stay on the device; outputs bit-identical. */
+int lsh_alif_bwd_dparams(const float* I, const float* U, const float* W, const float* S,
+                         const float* GS, const float* u0, const float* w0, float* LV, float* LW,
+                         float* DW0, double* partials, int64_t T, int64_t N, const float* params,
+                         float alpha, int mode, int C, void* ws, size_t ws_bytes, void* stream);
+/* Single-pass ALIF adjoint (mode 2 above, C in {16, 32}, same outputs bit for bit) that reads
+ * I and GS, and U, W only at the row before each chunk: u_{t-1}, w_{t-1} and s_t inside the chunk
+ * are recomputed with the forward step (reset value u_r).  Valid when U, W (and the S they imply)
+ * are one serial trajectory from (u0, w0), as lsh_alif_serial_fwd writes them; 8.5 bytes read
+ * per neuron-step at C = 16 instead of 20.  params: NULL (use beta, rho, q, theta0) or a device
+ * pointer to [beta, rho, q, theta0].  Replaces the adjoint half of ALIFFn.backward
+ * (triton_alif.py:541-554) for its serial forward (triton_alif.py:531-533). */
+int lsh_alif_bwd_recompute(const float* I, const float* U, const float* W, const float* GS,
+                           const float* u0, const float* w0, float* LV, float* LW, float* DW0,
+                           double* partials, int64_t T, int64_t N, const float* params, float beta,
+                           float rho, float q, float theta0, float u_r, float alpha, int C,
+                           void* stream);
 
 #ifdef __cplusplus
 }

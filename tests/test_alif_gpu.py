@@ -293,3 +293,115 @@ def test_alif_backward_param_sums_and_dw0(AL, dev, mode, C, T, N):
     got = host(sums)
     for k, w in enumerate((want[3], want[4], want[5], -want[6])):
         assert rel(got[k], w) < 1e-3, k
+
+
+@pytest.mark.parametrize("mode,C", [("serial", 64), ("chunked", 64), ("fused", 16), ("fused", 32)])
+def test_alif_device_params_entries_bitexact(AL, dev, mode, C):
+    """lsh_alif_serial_fwd_dparams and lsh_alif_bwd_dparams (parameters read from a device
+    vector) give the bits of the entries that take them as floats: U, W, S, LV, LW, dL/dw0 and
+    the parameter partial sums."""
+    from lifscan import hip_alif
+    beta, rho, q, th = 0.95, 0.995, 0.9, 1.0
+    T, N = 1024, 130
+    x = _inputs(beta, 2.0, T, N, 31)
+    G = normal(T, N, 0.0, 1.0, 32)
+    u0 = gpu(uniform(N, -0.1, 0.3, 33), dev)
+    w0 = gpu(uniform(N, 0.0, 0.2, 34), dev)
+    xg = gpu(x, dev)
+    print(f"alif dparams {mode} C={C}", flush=True)
+    dp = hip_alif._dev_params(xg, torch.tensor(beta, device=dev), rho, q, th)
+    U, W, S = AL.alif_serial_forward(xg, beta, rho, q, th, 0.0, u0, w0)
+    U2, W2, S2 = hip_alif._alif_serial_forward_dp(xg, dp, 0.0, u0, w0)
+    assert torch.equal(U, U2) and torch.equal(W, W2) and torch.equal(S, S2)
+    args = (xg, U, W, S, gpu(G, dev), beta, rho, q, th, u0, w0, 4.0, mode, C)
+    ref = hip_alif._alif_bwd_call(*args, want_lw=True, want_params=True)
+    got = hip_alif._alif_bwd_call(*args[:5], None, None, None, None, *args[9:], want_lw=True,
+                                  want_params=True, dp=dp)
+    for a, b in zip(ref, got):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("fwd", ["serial", "scan"])
+def test_alif_float_and_tensor_params_agree(AL, dev, fwd):
+    """alif() with float parameters (kernel arguments), with device tensors (read on the device
+    by the serial forward and the adjoint) and with a mix: identical S, U, W and input
+    gradients; parameter gradients only for the tensors, equal to the all-tensor call's."""
+    beta, rho, q, T, N, C = 0.95, 0.995, 0.9, 1024, 96, 128
+    x = _inputs(beta, 2.0, T, N, 35)
+    G = gpu(normal(T, N, 0.0, 1.0, 36), dev)
+    u0 = uniform(N, -0.1, 0.3, 37)
+    w0 = uniform(N, 0.0, 0.2, 38)
+    _, W, _ = A.serial_forward(x, beta, rho, q, 1.0, 0.0, u0, w0)
+    Wp = gpu(np.concatenate([w0[None], W[C - 1:-1:C]], 0), dev)
+    print(f"alif float/tensor params fwd={fwd}", flush=True)
+
+    def run(ps):
+        xg = gpu(x, dev).requires_grad_(True)
+        ug = gpu(u0, dev).requires_grad_(True)
+        wg = gpu(w0, dev).requires_grad_(True)
+        out = AL.alif(xg, ug, wg, *ps, fwd=fwd, bwd="scan", Wpred=Wp, dw=0.1 * q, C=C)
+        (out[0] * G).sum().backward()
+        return out, (xg.grad, ug.grad, wg.grad)
+
+    o1, g1 = run([beta, rho, q, 1.0])
+    pt = [torch.tensor(v, device=dev, requires_grad=True) for v in (beta, rho, q, 1.0)]
+    o2, g2 = run(pt)
+    pm = [torch.tensor(beta, device=dev, requires_grad=True), rho,
+          torch.tensor(q, device=dev, requires_grad=True), 1.0]
+    o3, g3 = run(pm)
+    for a, b, c in zip(o1 + g1, o2 + g2, o3 + g3):
+        assert torch.equal(a, b) and torch.equal(a, c)
+    assert torch.equal(pm[0].grad, pt[0].grad) and torch.equal(pm[2].grad, pt[2].grad)
+    assert all(p.grad is not None for p in pt)
+
+
+@pytest.mark.parametrize("C", [16, 32])
+@pytest.mark.parametrize("T,N,u_r", [(1024, 130, 0.0), (512, 33, -0.2), (32, 70, 0.1)])
+def test_alif_recompute_bwd_bitexact(AL, dev, C, T, N, u_r):
+    """lsh_alif_bwd_recompute (S not read, U and W only before each chunk) equals the single pass
+    that reads the stored states, bit for bit, for float and device parameters; and both match
+    the fp64 adjoint."""
+    from lifscan import hip_alif
+    beta, rho, q, th = 0.95, 0.995, 0.9, 1.0
+    x = _inputs(beta, 2.0, T, N, 41)
+    G = normal(T, N, 0.0, 1.0, 42)
+    u0 = uniform(N, -0.1, 0.3, 43)
+    w0 = uniform(N, 0.0, 0.2, 44)
+    U, W, S = A.serial_forward(x, beta, rho, q, th, u_r, u0, w0)
+    args = [gpu(a, dev) for a in (x, U, W, S, G)]
+    ug, wg = gpu(u0, dev), gpu(w0, dev)
+    print(f"alif recompute bwd C={C} T={T} N={N} u_r={u_r}", flush=True)
+    ref = hip_alif._alif_bwd_call(*args, beta, rho, q, th, ug, wg, 4.0, "fused", C, want_lw=True,
+                                  want_params=True)
+    got = hip_alif._alif_bwd_call(*args, beta, rho, q, th, ug, wg, 4.0, "fused", C, want_lw=True,
+                                  want_params=True, recompute_ur=u_r)
+    dp = hip_alif._dev_params(args[0], torch.tensor(beta, device=dev), rho, q, th)
+    got2 = hip_alif._alif_bwd_call(*args[:3], None, args[4], None, None, None, None, ug, wg, 4.0, "fused",
+                                   C, want_lw=True, want_params=True, dp=dp, recompute_ur=u_r)
+    for a, b, c in zip(ref, got, got2):
+        assert torch.equal(a, b) and torch.equal(a, c)
+    LV6, LW6 = A.backward(x, U, W, S, G, beta, rho, q, th, u0, w0, 4.0, dtype=np.float64)
+    assert rel(host(got[0]), LV6) < 1e-4 and rel(host(got[1]), LW6) < 1e-4
+
+
+def test_alif_layer_recompute_equals_stored(AL, dev, monkeypatch):
+    """alif(fwd="serial", bwd="scan") at N >= 8192 takes the recomputing single pass: the
+    gradients for I, u0, w0 and the four parameters equal those of the stored-state pass."""
+    from lifscan import hip_alif
+    beta, rho, q, T, N = 0.95, 0.995, 0.2, 256, 8256
+    x = gpu(_inputs(beta, 2.0, T, N, 45), dev)
+    G = gpu(normal(T, N, 0.0, 1.0, 46), dev)
+    u0 = gpu(uniform(N, -0.1, 0.3, 47), dev)
+    w0 = gpu(uniform(N, 0.0, 0.2, 48), dev)
+    print("alif layer recompute vs stored", flush=True)
+
+    def run(flag):
+        monkeypatch.setattr(hip_alif, "ALIF_RECOMPUTE_BWD", flag)
+        xg, ug, wg = (a.clone().requires_grad_(True) for a in (x, u0, w0))
+        ps = [torch.tensor(v, device=dev, requires_grad=True) for v in (beta, rho, q, 1.0)]
+        S, _, _ = AL.alif(xg, ug, wg, *ps, u_r=-0.1, fwd="serial", bwd="scan")
+        (S * G).sum().backward()
+        return [xg.grad, ug.grad, wg.grad] + [p.grad for p in ps]
+
+    for a, b in zip(run(True), run(False)):
+        assert torch.equal(a, b)

@@ -778,6 +778,259 @@ __global__ __launch_bounds__(64) void k_alif_bwd_serial(
   }
 }
 
+// The fused serial sweep with wave roles (as serial_pipe.hip): one workgroup per 64 neurons,
+// ALIF_PIPE_P producer waves and one consumer wave, tiles of ALIF_PIPE_D rows from the end of
+// time in an LDS double buffer.  Producers load the inputs one tile ahead, write (sg_t, g_t,
+// (1 - s_t)*beta) per row, and store LV (and LW) of the tile the consumer finished one round
+// earlier, adding the parameter sums there with the (u_{t-1}, w_{t-1}, s_t, sg_t) they kept;
+// the consumer runs d = g + q*lw, lv = ((1-s)*beta)*lv + sg*d, lw = rho*lw - sg*d.  Same
+// operations in the same order as k_alif_bwd_serial, so LV, LW and dL/dw0 are bit-identical;
+// the fp64 sums are added in another order.
+constexpr int ALIF_PIPE_D = 32;
+constexpr int ALIF_PIPE_P = 15;
+
+// Serial ALIF forward from (u0, w0) with the same wave roles (triton_alif.py:35-42,
+// :263-273): the consumer runs alif_step through LDS, the producers stage I one tile ahead and
+// store U, W, S of the tile finished one round earlier; bit-identical to k_alif_fwd.
+constexpr int ALIF_FPIPE_D = 64;
+
+__global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
+    float* __restrict__ U, float* __restrict__ W, float* __restrict__ S, int64_t N, int64_t T,
+    float beta, float rho, float q, float theta0, float u_r, const float* __restrict__ dpar) {
+  if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
+  constexpr int D = ALIF_FPIPE_D, P = ALIF_PIPE_P, R = (D + P - 1) / P;
+  __shared__ float sX[2][D][WAVE];
+  __shared__ float4 sUWS[2][D][WAVE];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const unsigned lane = threadIdx.x % WAVE;
+  const int64_t nb0 = (int64_t)blockIdx.x * WAVE;
+  const bool valid = nb0 + lane < N;
+  const unsigned ln = valid ? lane : (unsigned)(N - 1 - nb0);
+  const unsigned lb = ln * 4u, sb = lane * 4u;
+  const int64_t ntiles = (T + D - 1) / D;
+  auto rows = [&](int64_t k) { return (int)(T - k * D > D ? D : T - k * D); };
+
+  if (w == 0) {  // consumer: tile k - 1 in round k
+    __builtin_amdgcn_s_setprio(3);
+    float u = u0[nb0 + ln], ww = w0[nb0 + ln];
+    for (int64_t k = 0; k <= ntiles + 1; ++k) {
+      if (k >= 1 && k <= ntiles) {
+        const int buf = (int)((k - 1) & 1);
+        const int nr = rows(k - 1);
+        auto step = [&](int j, float x) {
+          bool sp;
+          u = alif_step(u, ww, x, beta, rho, q, theta0, u_r, sp);
+          sUWS[buf][j][lane] = make_float4(u, ww, sp ? 1.0f : 0.0f, 0.0f);
+        };
+        if (nr == D) {
+#pragma unroll
+          for (int g = 0; g < D; g += 16) {
+            float x[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) x[i] = sX[buf][g + i][lane];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) step(g + i, x[i]);
+          }
+        } else {
+          for (int j = 0; j < nr; ++j) step(j, sX[buf][j][lane]);
+        }
+      }
+      __syncthreads();
+    }
+    return;
+  }
+
+  const int p = w - 1;
+  float xr[R];
+  auto load = [&](int64_t k) {
+    const int nr = rows(k);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int j = p + r * P;
+      if (j < nr) xr[r] = ld_row(I + (size_t)(k * D + j) * (size_t)N + (size_t)nb0, lb);
+    }
+  };
+  if (ntiles > 0) load(0);
+  for (int64_t k = 0; k <= ntiles + 1; ++k) {
+    if (k < ntiles) {
+      const int buf = (int)(k & 1);
+      const int nr = rows(k);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int j = p + r * P;
+        if (j < nr) sX[buf][j][lane] = xr[r];
+      }
+      if (k + 1 < ntiles) load(k + 1);
+    }
+    if (k >= 2 && valid) {
+      const int buf = (int)(k & 1);
+      const int nr = rows(k - 2);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int j = p + r * P;
+        if (j < nr) {
+          const size_t row = (size_t)((k - 2) * D + j) * (size_t)N + (size_t)nb0;
+          const float4 o = sUWS[buf][j][lane];
+          st_row_nt(U + row, sb, o.x);
+          st_row_nt(W + row, sb, o.y);
+          st_row_nt(S + row, sb, o.z);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <bool WLW, bool PS>
+__global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_bwd_pipe(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
+    const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
+    const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
+    float* __restrict__ DW0, double* __restrict__ partials, int64_t N, int64_t T, float beta,
+    float rho, float q, float theta0, float alpha, const float* __restrict__ dpar) {
+  if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
+  constexpr int D = ALIF_PIPE_D, P = ALIF_PIPE_P, R = (D + P - 1) / P;
+  __shared__ float4 sIn[2][D][WAVE];   // sg, g, (1 - s)*beta
+  __shared__ float4 sOut[2][D][WAVE];  // lv_t, lw_t (before the step), d_t
+  __shared__ double sAcc[P][4];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const unsigned lane = threadIdx.x % WAVE;
+  const int64_t nb0 = (int64_t)blockIdx.x * WAVE;
+  const bool valid = nb0 + lane < N;
+  const unsigned ln = valid ? lane : (unsigned)(N - 1 - nb0);
+  const unsigned lb = ln * 4u, sb = lane * 4u;
+  const int64_t ntiles = (T + D - 1) / D;
+  const int64_t rounds = (ntiles + 3) & ~(int64_t)1;  // >= ntiles + 2, even
+  auto tile_lo = [&](int64_t k) { const int64_t hi = T - k * D; return hi > D ? hi - D : (int64_t)0; };
+  auto tile_rows = [&](int64_t k) { const int64_t hi = T - k * D; return (int)(hi > D ? D : hi); };
+
+  if (w == 0) {  // consumer: tile k - 1 in round k
+    __builtin_amdgcn_s_setprio(3);
+    float lw = 0.0f, lv = 0.0f;
+    for (int64_t k = 0; k < rounds; ++k) {
+      if (k >= 1 && k <= ntiles) {
+        const int buf = (int)((k - 1) & 1);
+        const int nr = tile_rows(k - 1);
+        auto step = [&](int j, const float4 in) {
+          const float d = in.y + q * lw;
+          const float lw_old = lw;
+          lv = in.z * lv + in.x * d;
+          lw = rho * lw - in.x * d;
+          sOut[buf][j][lane] = make_float4(lv, lw_old, d, 0.0f);
+        };
+        if (nr == D) {
+#pragma unroll
+          for (int g = D - 8; g >= 0; g -= 8) {
+            float4 in[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) in[i] = sIn[buf][g + i][lane];
+#pragma unroll
+            for (int i = 7; i >= 0; --i) step(g + i, in[i]);
+          }
+        } else {
+          for (int j = nr - 1; j >= 0; --j) step(j, sIn[buf][j][lane]);
+        }
+      }
+      __syncthreads();
+    }
+    if (DW0 && valid) DW0[nb0 + lane] = lw;
+  } else {  // producers: inputs of tile k, outputs of tile k - 2 in round k
+    const int p = w - 1;
+    const float u0n = u0[nb0 + ln], w0n = w0[nb0 + ln];
+    float xr[R], sr[R], gr[R], ur[R], wr[R];
+    float keep0[4][PS ? R : 1], keep1[4][PS ? R : 1];  // (up, wp, s, sg) of the tiles in flight
+    ParamAcc acc;
+    auto load = [&](int64_t k) {
+      const int64_t lo = tile_lo(k);
+      const int nr = tile_rows(k);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int j = p + r * P;
+        if (j < nr) {
+          const int64_t t = lo + j;
+          const size_t row = (size_t)t * (size_t)N + (size_t)nb0;
+          xr[r] = ld_row(I + row, lb);
+          sr[r] = ld_row(S + row, lb);
+          gr[r] = ld_row(GS + row, lb);
+          ur[r] = t > 0 ? ld_row(U + row - N, lb) : u0n;
+          wr[r] = t > 0 ? ld_row(W + row - N, lb) : w0n;
+        }
+      }
+    };
+    // tile k's kept values land where tile k - 2's were: use those first
+    auto round = [&](int64_t k, float(&keep)[4][PS ? R : 1]) {
+      if (k >= 2 && k - 2 < ntiles && valid) {
+        const int buf = (int)(k & 1);
+        const int64_t lo = tile_lo(k - 2);
+        const int nr = tile_rows(k - 2);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int j = p + r * P;
+          if (j < nr) {
+            const float4 o = sOut[buf][j][lane];
+            const size_t row = (size_t)(lo + j) * (size_t)N + (size_t)nb0;
+            if (WLW) st_row_nt(LW + row, sb, o.y);
+            st_row_nt(LV + row, sb, o.x);
+            if constexpr (PS) acc.add(o.x, keep[0][r], o.y, keep[1][r], keep[2][r], keep[3][r], o.z);
+          }
+        }
+      }
+      if (k < ntiles) {
+        float x[R], sv[R], g[R], up[R], wp[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          x[r] = xr[r];
+          sv[r] = sr[r];
+          g[r] = gr[r];
+          up[r] = ur[r];
+          wp[r] = wr[r];
+        }
+        if (k + 1 < ntiles) load(k + 1);
+        const int buf = (int)(k & 1);
+        const int nr = tile_rows(k);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int j = p + r * P;
+          if (j < nr) {
+            const float sg = alif_sg(up[r], wp[r], x[r], beta, theta0, alpha);
+            sIn[buf][j][lane] = make_float4(sg, g[r], (1.0f - sv[r]) * beta, 0.0f);
+            if constexpr (PS) {
+              keep[0][r] = up[r];
+              keep[1][r] = wp[r];
+              keep[2][r] = sv[r];
+              keep[3][r] = sg;
+            }
+          }
+        }
+      }
+      __syncthreads();
+    };
+    if (ntiles > 0) load(0);
+    for (int64_t k = 0; k < rounds; k += 2) {
+      round(k, keep0);
+      round(k + 1, keep1);
+    }
+    if constexpr (PS) {
+      acc.wave_sum();
+      if (lane == 0) acc.store(sAcc[p]);
+    }
+  }
+  if constexpr (PS) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      ParamAcc tot;
+      for (int v = 0; v < P; ++v) {
+        tot.b += sAcc[v][0];
+        tot.r += sAcc[v][1];
+        tot.q += sAcc[v][2];
+        tot.t += sAcc[v][3];
+      }
+      tot.store(partials + (size_t)blockIdx.x * 4);
+    }
+  }
+}
+
 // Single-pass two-scan adjoint: one workgroup of W waves owns 64 neurons and walks the time
 // axis backwards in rounds of W chunks.  Each wave keeps its chunk's (sg_t, g_t, s_t) in
 // registers, composes the lw recurrence into (P1, Q1), takes lw at its chunk end from the
@@ -1036,8 +1289,14 @@ extern "C" int lsh_alif_serial_fwd(const float* I, const float* u0, const float*
     return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (T == 0 || N == 0) return LSH_OK;
-  launch_alif_fwd<16>(I, u0, w0, U, W, S, nullptr, nullptr, N, T, 1, beta, rho, q, theta0, u_r,
-                      (hipStream_t)stream);
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  if (NB <= serial_pipe_max_blocks())
+    hipLaunchKernelGGL(k_alif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)), 0,
+                       (hipStream_t)stream, I, u0, w0, U, W, S, N, T, beta, rho, q, theta0, u_r,
+                       nullptr);
+  else
+    launch_alif_fwd<16>(I, u0, w0, U, W, S, nullptr, nullptr, N, T, 1, beta, rho, q, theta0, u_r,
+                        (hipStream_t)stream);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }
@@ -1050,8 +1309,14 @@ extern "C" int lsh_alif_serial_fwd_dparams(const float* I, const float* u0, cons
     return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (T == 0 || N == 0) return LSH_OK;
-  launch_alif_fwd<16>(I, u0, w0, U, W, S, nullptr, nullptr, N, T, 1, 0.0f, 0.0f, 0.0f, 0.0f, u_r,
-                      (hipStream_t)stream, params);
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  if (NB <= serial_pipe_max_blocks())
+    hipLaunchKernelGGL(k_alif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)), 0,
+                       (hipStream_t)stream, I, u0, w0, U, W, S, N, T, 0.0f, 0.0f, 0.0f, 0.0f, u_r,
+                       params);
+  else
+    launch_alif_fwd<16>(I, u0, w0, U, W, S, nullptr, nullptr, N, T, 1, 0.0f, 0.0f, 0.0f, 0.0f, u_r,
+                        (hipStream_t)stream, params);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }
@@ -1211,6 +1476,12 @@ static void launch_alif_serial_bwd(const float* I, const float* u0, const float*
                                    float* LV, float* DW0, double* partials, int64_t N, int64_t T,
                                    int NB, float beta, float rho, float q, float theta0, float alpha,
                                    hipStream_t st, const float* dpar) {
+  if (NB <= serial_pipe_max_blocks()) {
+    hipLaunchKernelGGL((k_alif_bwd_pipe<WLW, PS>), dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)),
+                       0, st, I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, beta, rho, q,
+                       theta0, alpha, dpar);
+    return;
+  }
   hipLaunchKernelGGL((k_alif_bwd_serial<8, WLW, PS>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, w0,
                      U, W, S, GS, LW, LV, DW0, partials, N, T, beta, rho, q, theta0, alpha, dpar);
 }

@@ -74,4 +74,14 @@ int lif_param_bwd_lookback(const float* I, const float* u0, const float* U, cons
                            size_t ws_bytes, int64_t T, int64_t N, float beta, float theta,
                            float u_r, float alpha, int ps, hipStream_t st);
 
+// Wave-specialised serial sweeps (serial_pipe.hip): used instead of the one-wave serial kernels
+// up to serial_pipe_max_blocks() blocks of 64 neurons (lsh_serial_pipe_config sets it).
+int serial_pipe_max_blocks();
+void lif_serial_fwd_pipe(const float* I, const float* u0, float* U, float* S, int64_t N, int64_t T,
+                         float beta, float theta, float u_r, hipStream_t st);
+void lif_serial_bwd_pipe(const float* I, const float* u0, const float* U, const float* S,
+                         const float* GS, const float* GU, float* Lam, int64_t N, int64_t T,
+                         float beta, float theta, float u_r, float alpha, bool detach,
+                         hipStream_t st);
+
 }  // namespace lsh

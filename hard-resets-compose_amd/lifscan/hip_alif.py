@@ -15,7 +15,7 @@ import math
 import torch
 
 from . import _native as _n
-from .hip_lif import _f32, _f32s, _input, _vec, _same, chunked_bwd_C
+from .hip_lif import _f32, _f32s, _input, _vec, _same
 
 # single-pass backward (one workgroup per 64 neurons) pays off only with many neuron blocks
 ALIF_FUSED_BWD_MIN_N = 8192
@@ -200,13 +200,29 @@ def alif_scan_forward(I, beta, rho, q, theta0, u_r, u0, w0, Wpred, dw, C=128, K1
     return U, W, S
 
 
+def alif_chunked_C(T, C=64):
+    """Chunk of the chunked (four-pass) adjoint: the power of two in 16..512 dividing T nearest
+    to sqrt(T/4), which balances the passes' per-chunk sweeps against the sequential carry over
+    T/C chunks (swept on MI355X at N = 64..8192: best 32 at T = 4096, 128 at T = 65536, 256-512
+    at T = 262144); the given C when none divides T."""
+    cands = [c for c in (16, 32, 64, 128, 256, 512) if T % c == 0]
+    if not cands:
+        return int(C)
+    target = math.sqrt(max(T, 1) / 4.0)
+    return min(cands, key=lambda c: abs(math.log2(c / target)))
+
+
 def _bwd_mode(mode, T, N, C):
-    """Kernel mode code and chunk for an alif_backward mode name."""
+    """Kernel mode code and chunk for an alif_backward mode name.  "scan": the single pass from
+    ALIF_FUSED_BWD_MIN_N neurons, else the chunked passes at alif_chunked_C (N = 1024,
+    T = 65536: C = 128 1.44 ms, the single pass 2.99 ms).  Below that N the single pass would
+    run 16 waves per workgroup without the parameter sums and 8 with them, so dI would depend
+    in its last bits on whether the parameters need a gradient; the chunked passes do not."""
     C = int(C)
     if mode == "scan":
         fused = N >= ALIF_FUSED_BWD_MIN_N and T % ALIF_FUSED_BWD_C == 0
         mode = "fused" if fused else "chunked"
-        C = ALIF_FUSED_BWD_C if fused else chunked_bwd_C(T, N, C)
+        C = ALIF_FUSED_BWD_C if fused else alif_chunked_C(T, C)
     if mode in ("serial_pf", "serial_tuned", "serial"):
         return 0, C
     if mode == "fused":  # single pass, C in {16, 32}
@@ -277,7 +293,7 @@ def alif_backward(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha=4.0, mode=
     """(LV, LW) with LV[t] = dL/dv_t (= dL/dI_t), LW[t] = dL/dw_t for dL/dS = GS
     (triton_alif.py:490-521).  mode: serial_pf / serial_tuned / serial (fused serial sweep),
     chunked (two-level affine scans over chunks of C), fused (single pass, C in {16, 32}) or
-    scan (fused when N is large, else chunked)."""
+    scan (fused when N is large, else chunked at its own chunk; _bwd_mode)."""
     LV, LW, _, _ = _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C,
                                   want_lw=True, want_params=False)
     return LV, LW

@@ -124,6 +124,13 @@ def serial_forward_auto(I, beta, theta, u_r, u0):
     return serial_forward(I, beta, theta, u_r, u0)
 
 
+def serial_pipe_max_blocks(n=None):
+    """Largest count of 64-neuron blocks whose serial sweeps run as producer and consumer waves
+    (bit-identical to the one-wave kernels, faster with few neurons); n sets it (0 disables).
+    Returns the value in force before the call."""
+    return int(_n.lib().lsh_serial_pipe_config(-1 if n is None else int(n)))
+
+
 def serial_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, BN=BN_DEFAULT):
     """Serial adjoint (triton_lif.py:254-259) -> Lam [T, N] (= dL/dI).  GU may be None (zeros)."""
     I = _input(I)

@@ -56,6 +56,13 @@ int lsh_lif_serial_bwd(const float* I, const float* u0, const float* U, const fl
                        const float* GS, const float* GU, float* Lam, int64_t T, int64_t N,
                        float beta, float theta, float u_r, float alpha, int detach, void* stream);
 
+/* Serial sweeps with few neurons run as one workgroup per 64 neurons of producer waves (loads,
+ * per-step coefficients, stores, through an LDS double buffer) and one consumer wave (the
+ * recurrence), bit-identical to the one-wave kernels.  Sets the largest neuron-block count that
+ * takes them (0: never; negative: unchanged) and returns the previous value (default 128).
+ * No counterpart in the reference: a tuning and testing knob of this library. */
+int lsh_serial_pipe_config(int max_blocks);
+
 /* Two-level exact scan forward (envelope bound + capacity-K chunk maps, sequential carry
  * with overflow-to-serial fallback, replay, Jacobi repair on device).
  * Replaces triton_lif.py:782-817 (scan_forward_v3) and :1228-1232 (scan_forward_auto).

@@ -405,3 +405,59 @@ def test_alif_layer_recompute_equals_stored(AL, dev, monkeypatch):
 
     for a, b in zip(run(True), run(False)):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("T,N", [(1, 1), (31, 64), (32, 100), (33, 7), (1000, 130), (4113, 1029)])
+def test_alif_serial_bwd_pipe_equals_one_wave(AL, dev, T, N):
+    """The producer/consumer serial adjoint gives the one-wave kernel's LV, LW and dL/dw0 bit for
+    bit; its fp64 parameter sums (added in another order) within 1e-12."""
+    from lifscan import hip_alif, hip_lif
+    beta, rho, q = 0.95, 0.995, 0.9
+    x = _inputs(beta, 2.0, T, N, 51)
+    G = normal(T, N, 0.0, 1.0, 52)
+    u0 = uniform(N, -0.1, 0.3, 53)
+    w0 = uniform(N, 0.0, 0.2, 54)
+    U, W, S = A.serial_forward(x, beta, rho, q, 1.0, 0.0, u0, w0)
+    args = [gpu(a, dev) for a in (x, U, W, S, G)]
+    ug, wg = gpu(u0, dev), gpu(w0, dev)
+    print(f"alif serial bwd pipe T={T} N={N}", flush=True)
+    prev = hip_lif.serial_pipe_max_blocks(0)
+    try:
+        ref = hip_alif._alif_bwd_call(*args, beta, rho, q, 1.0, ug, wg, 4.0, "serial", 64, want_lw=True,
+                                      want_params=True)
+        ref2 = AL.alif_backward(*args, beta, rho, q, 1.0, ug, wg, mode="serial")
+        hip_lif.serial_pipe_max_blocks(1 << 20)
+        got = hip_alif._alif_bwd_call(*args, beta, rho, q, 1.0, ug, wg, 4.0, "serial", 64, want_lw=True,
+                                      want_params=True)
+        got2 = AL.alif_backward(*args, beta, rho, q, 1.0, ug, wg, mode="serial")
+    finally:
+        hip_lif.serial_pipe_max_blocks(prev)
+    for a, b in zip(ref[:3] + ref2, got[:3] + got2):
+        assert torch.equal(a, b)
+    s_ref, s_got = host(ref[3]), host(got[3])
+    assert np.all(np.abs(s_got - s_ref) <= 1e-12 * (np.abs(s_ref) + 1.0))
+
+
+@pytest.mark.parametrize("T,N", [(1, 1), (63, 64), (64, 100), (65, 7), (1000, 130), (4113, 1029)])
+def test_alif_serial_fwd_pipe_equals_one_wave(AL, dev, T, N):
+    """The producer/consumer serial forward gives U, W, S of the one-wave kernel and the oracle
+    bit for bit, with float and with device parameters."""
+    from lifscan import hip_alif, hip_lif
+    beta, rho, q = 0.95, 0.995, 0.9
+    x = _inputs(beta, 2.0, T, N, 55)
+    u0 = uniform(N, -0.1, 0.3, 56)
+    w0 = uniform(N, 0.0, 0.2, 57)
+    Ur, Wr, Sr = A.serial_forward(x, beta, rho, q, 1.0, 0.0, u0, w0)
+    xg, ug, wg = gpu(x, dev), gpu(u0, dev), gpu(w0, dev)
+    print(f"alif serial fwd pipe T={T} N={N}", flush=True)
+    prev = hip_lif.serial_pipe_max_blocks(0)
+    try:
+        ref = AL.alif_serial_forward(xg, beta, rho, q, 1.0, 0.0, ug, wg)
+        hip_lif.serial_pipe_max_blocks(1 << 20)
+        got = AL.alif_serial_forward(xg, beta, rho, q, 1.0, 0.0, ug, wg)
+        dp = hip_alif._dev_params(xg, torch.tensor(beta, device=dev), rho, q, 1.0)
+        got2 = hip_alif._alif_serial_forward_dp(xg, dp, 0.0, ug, wg)
+    finally:
+        hip_lif.serial_pipe_max_blocks(prev)
+    for a, b, c, o in zip(ref, got, got2, (Ur, Wr, Sr)):
+        assert torch.equal(a, b) and torch.equal(a, c) and np.array_equal(host(b), o)

@@ -314,3 +314,44 @@ def test_scan_v4_rejects_bad_shapes(L, dev):
         L.scan_forward_v4(I, 0.9, 1.0, 0.0, u0, C=64, G=2)
     with pytest.raises(ValueError):
         L.scan_forward_v4(I, 0.9, 1.0, 0.0, u0, C=64, G=5, K=16, K2=8)
+
+
+@pytest.mark.parametrize("T,N", [(1, 1), (63, 64), (64, 100), (65, 7), (1000, 130), (4113, 1029)])
+@pytest.mark.parametrize("detach,with_gu", [(True, False), (True, True), (False, True)])
+def test_serial_backward_pipe_equals_one_wave(L, dev, T, N, detach, with_gu):
+    """The producer/consumer serial adjoint gives the one-wave kernel's Lam bit for bit (full and
+    partial tiles, ragged neuron blocks, detached or not, with and without GU)."""
+    I = normal(T, N, 0.1, 0.5, 61)
+    u0 = uniform(N, -0.2, 0.6, 62)
+    GS = normal(T, N, 0.0, 1.0, 63)
+    GU = normal(T, N, 0.0, 0.3, 64) if with_gu else None
+    U, S = O.serial_forward(I, 0.93, 1.0, 0.1, u0)
+    args = [gpu(a, dev) for a in (I, u0, U, S, GS)] + [gpu(GU, dev) if with_gu else None]
+    print(f"serial bwd pipe T={T} N={N} detach={detach} gu={with_gu}", flush=True)
+    prev = L.serial_pipe_max_blocks(0)
+    try:
+        ref = L.serial_backward(*args, 0.93, 1.0, 0.1, 4.0, detach)
+        L.serial_pipe_max_blocks(1 << 20)
+        got = L.serial_backward(*args, 0.93, 1.0, 0.1, 4.0, detach)
+    finally:
+        L.serial_pipe_max_blocks(prev)
+    assert torch.equal(got, ref)
+
+
+@pytest.mark.parametrize("T,N", [(1, 1), (63, 64), (64, 100), (65, 7), (1000, 130), (4113, 1029)])
+def test_serial_forward_pipe_equals_one_wave(L, dev, T, N):
+    """The producer/consumer serial forward gives the one-wave kernel's U, S and the oracle's,
+    bit for bit."""
+    I = normal(T, N, 0.15, 0.5, 65)
+    u0 = uniform(N, -0.2, 0.9, 66)
+    Ur, Sr = O.serial_forward(I, 0.93, 1.0, 0.1, u0)
+    print(f"serial fwd pipe T={T} N={N}", flush=True)
+    prev = L.serial_pipe_max_blocks(0)
+    try:
+        U1, S1 = L.serial_forward(gpu(I, dev), 0.93, 1.0, 0.1, gpu(u0, dev))
+        L.serial_pipe_max_blocks(1 << 20)
+        U2, S2 = L.serial_forward(gpu(I, dev), 0.93, 1.0, 0.1, gpu(u0, dev))
+    finally:
+        L.serial_pipe_max_blocks(prev)
+    assert torch.equal(U1, U2) and torch.equal(S1, S2)
+    assert np.array_equal(host(U2), Ur) and np.array_equal(host(S2), Sr)

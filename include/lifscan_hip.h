@@ -59,7 +59,7 @@ int lsh_lif_serial_bwd(const float* I, const float* u0, const float* U, const fl
 /* Serial sweeps with few neurons run as one workgroup per 64 neurons of producer waves (loads,
  * per-step coefficients, stores, through an LDS double buffer) and one consumer wave (the
  * recurrence), bit-identical to the one-wave kernels.  Sets the largest neuron-block count that
- * takes them (0: never; negative: unchanged) and returns the previous value (default 128).
+ * takes them (0: never; negative: unchanged) and returns the previous value (default: all).
  * No counterpart in the reference: a tuning and testing knob of this library. */
 int lsh_serial_pipe_config(int max_blocks);
 

@@ -90,18 +90,21 @@ class LIFParamFn(torch.autograd.Function):
             I, u0, U, S = ctx.saved_tensors
             lam, sums = _param_backward(I, u0, U, S, gS.contiguous(), b, th, ur, alpha, bwd_mode)
         sums = sums.float()
-        return (lam, b * lam[0], sums[0], -sums[1], b * sums[2], None, None, None, None)
+        need = ctx.needs_input_grad  # a gradient only for the parameters given as tensors
+        return (lam, b * lam[0], sums[0] if need[2] else None, -sums[1] if need[3] else None,
+                b * sums[2] if need[4] else None, None, None, None, None)
 
 
 def lif_param(I, u0, beta, theta, u_r, alpha=4.0, mode="auto", K=16):
-    """fit.py:51-57: mode "auto" picks serial / scan per pass from (N, T)."""
+    """fit.py:51-57: mode "auto" picks serial / scan per pass from (N, T).  Parameters may be
+    0-d tensors or floats; floats go to the kernels as they are (the reference wraps them in
+    device tensors and reads them back: the same fp32 values, one synchronizing copy more)."""
     T, N = I.shape
     if mode == "auto":
         fwd, bwd = L.auto_modes(N, T)
     else:
         fwd = bwd = mode
-    t = lambda v: v if torch.is_tensor(v) else torch.tensor(float(v), device=I.device)
-    return LIFParamFn.apply(I, u0, t(beta), t(theta), t(u_r), alpha, fwd, bwd, K)
+    return LIFParamFn.apply(I, u0, beta, theta, u_r, alpha, fwd, bwd, K)
 
 
 class LIFSoftFn(torch.autograd.Function):

@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from oracle import lif_oracle as O
-from tests._inputs import gpu, host, normal
+from tests._inputs import gpu, host, normal, uniform
 
 pytestmark = pytest.mark.gpu
 
@@ -116,3 +116,31 @@ def test_lif_param_auto_recomputing_path(dev):
     assert rel(host(g1), want[0]) < 1e-4
     for k in range(3):
         assert rel(p1[k], want[2 + k]) < 1e-4, k
+
+
+@pytest.mark.parametrize("mode", ["serial", "scan"])
+def test_lif_param_float_and_tensor_params_agree(dev, mode):
+    """lif_param with float parameters, with 0-d tensors and with a mix: the same S and input
+    gradients bit for bit; parameter gradients only for the tensors, equal to the all-tensor
+    call's."""
+    from lifscan.fit import lif_param
+    T, N = 512, 96
+    I = gpu(normal(T, N, 0.12, 0.3, 81), dev)
+    G = gpu(normal(T, N, 0.0, 1.0, 82), dev)
+    u0 = gpu(uniform(N, 0.0, 0.5, 83), dev)
+    print(f"lif_param float/tensor {mode}", flush=True)
+
+    def run(ps):
+        Ig, ug = I.clone().requires_grad_(True), u0.clone().requires_grad_(True)
+        S = lif_param(Ig, ug, *ps, mode=mode)
+        (S * G).sum().backward()
+        return S, Ig.grad, ug.grad
+
+    r1 = run([0.9, 1.0, 0.1])
+    pt = [torch.tensor(v, device=dev, requires_grad=True) for v in (0.9, 1.0, 0.1)]
+    r2 = run(pt)
+    pm = [torch.tensor(0.9, device=dev, requires_grad=True), 1.0, 0.1]
+    r3 = run(pm)
+    for a, b, c in zip(r1, r2, r3):
+        assert torch.equal(a, b) and torch.equal(a, c)
+    assert torch.equal(pm[0].grad, pt[0].grad) and all(p.grad is not None for p in pt)

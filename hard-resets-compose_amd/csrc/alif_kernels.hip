@@ -627,6 +627,13 @@ struct ParamAcc {
     q += (double)lw * (double)s;
     t += (double)sg * (double)d;
   }
+  // one chunk's four sums formed in fp32 (fma per term), added here in fp64
+  __device__ __forceinline__ void add_chunk(float cb, float cr, float cq, float ct) {
+    b += (double)cb;
+    r += (double)cr;
+    q += (double)cq;
+    t += (double)ct;
+  }
   __device__ __forceinline__ void wave_sum() {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
@@ -1036,8 +1043,9 @@ __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_bwd_pipe(
 // registers, composes the lw recurrence into (P1, Q1), takes lw at its chunk end from the
 // later chunks through LDS, replays lw (kept in registers), composes the lv recurrence
 // (which reads lw_t) into (P2, Q2), takes lv at its chunk end the same way and replays lv.
-// WLW: write LW.  PS: also keep u_{t-1}, w_{t-1} and sum the parameter gradients (one
-// partials row per workgroup).  DW0 (if given) receives lw_{-1} from the first chunk.
+// WLW: write LW.  PS: also keep u_{t-1}, w_{t-1} and sum the parameter gradients (each
+// chunk's in fp32, the chunks in fp64; one partials row per workgroup).  DW0 (if given)
+// receives lw_{-1} from the first chunk.
 // RC: S is not read and U, W only at the row before each chunk; the chunk's u_{t-1}, w_{t-1}
 // and s_t are recomputed with the forward's own step (alif_step, reset value u_r) from that
 // entry state, which gives the stored bits when U, W, S come from one serial trajectory.  The
@@ -1156,6 +1164,7 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
       float lam = sLv[lane];
       for (int v = 0; v < w; ++v) lam = sQ[v][lane] + sP[v][lane] * lam;
       const Buf bo(LW + nb0 + row0 * N), bv(LV + nb0 + row0 * N);
+      float cb = 0.0f, cr = 0.0f, cq = 0.0f, ct = 0.0f;  // PS: this chunk's sums
 #pragma unroll
       for (int j = C - 1; j >= 0; --j) {
         const float d = g[j] + q * lwv[j];
@@ -1163,9 +1172,15 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
         if (valid) {
           if (WLW) bo.st_nt(sb, j * rstride, lwv[j]);
           bv.st_nt(sb, j * rstride, lam);
-          if (PS) acc.add(lam, upv[j], lwv[j], wpv[j], 1.0f - s1[j], sg[j], d);
+        }
+        if (PS) {
+          cb = fmaf(lam, upv[j], cb);
+          cr = fmaf(lwv[j], wpv[j], cr);
+          cq += s1[j] == 0.0f ? lwv[j] : 0.0f;
+          ct = fmaf(sg[j], d, ct);
         }
       }
+      if (PS && valid) acc.add_chunk(cb, cr, cq, ct);
       lv_end = lam;
     }
     __syncthreads();

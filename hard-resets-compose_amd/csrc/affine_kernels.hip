@@ -19,13 +19,6 @@
 
 namespace lsh {
 
-__device__ __forceinline__ float aff_step(float u, float x, float beta, float theta, float gamma,
-                                          float delta, bool& s) {
-  const float v = lif_v(u, x, beta);
-  s = v >= theta;
-  return s ? __fadd_rn(__fmul_rn(gamma, v), delta) : v;
-}
-
 // ---------------------------------------------------------------------------------------
 // Serial / replay over segments of Ls steps from su (triton_affine.py:143-162).
 template <int D>
@@ -456,8 +449,11 @@ extern "C" int lsh_aff_serial_fwd(const float* I, const float* u0, float* U, flo
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (T == 0 || N == 0) return LSH_OK;
   const int NB = (int)((N + WAVE - 1) / WAVE);
-  hipLaunchKernelGGL((k_aff_fwd<16>), dim3((unsigned)NB), dim3(WAVE), 0, (hipStream_t)stream, I, u0,
-                     U, S, nullptr, N, T, NB, beta, theta, gamma, delta);
+  if (NB <= serial_pipe_max_blocks())
+    aff_serial_fwd_pipe(I, u0, U, S, N, T, beta, theta, gamma, delta, (hipStream_t)stream);
+  else
+    hipLaunchKernelGGL((k_aff_fwd<16>), dim3((unsigned)NB), dim3(WAVE), 0, (hipStream_t)stream, I,
+                       u0, U, S, nullptr, N, T, NB, beta, theta, gamma, delta);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }

@@ -79,6 +79,8 @@ int lif_param_bwd_lookback(const float* I, const float* u0, const float* U, cons
 int serial_pipe_max_blocks();
 void lif_serial_fwd_pipe(const float* I, const float* u0, float* U, float* S, int64_t N, int64_t T,
                          float beta, float theta, float u_r, hipStream_t st);
+void aff_serial_fwd_pipe(const float* I, const float* u0, float* U, float* S, int64_t N, int64_t T,
+                         float beta, float theta, float gamma, float delta, hipStream_t st);
 void lif_serial_bwd_pipe(const float* I, const float* u0, const float* U, const float* S,
                          const float* GS, const float* GU, float* Lam, int64_t N, int64_t T,
                          float beta, float theta, float u_r, float alpha, bool detach,

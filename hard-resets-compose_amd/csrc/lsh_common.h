@@ -33,6 +33,14 @@ __device__ __forceinline__ float lif_v(float u, float x, float beta) {
   return __fadd_rn(__fmul_rn(beta, u), x);
 }
 
+// One affine-reset step (triton_affine.py:20-24): u' = s ? fl(fl(gamma*v) + delta) : v.
+__device__ __forceinline__ float aff_step(float u, float x, float beta, float theta, float gamma,
+                                          float delta, bool& s) {
+  const float v = __fadd_rn(__fmul_rn(beta, u), x);
+  s = v >= theta;
+  return s ? __fadd_rn(__fmul_rn(gamma, v), delta) : v;
+}
+
 // One hard-reset LIF step; returns the new state and writes the spike.
 __device__ __forceinline__ float lif_step(float u, float x, float beta, float theta, float u_r,
                                           bool& s) {

@@ -152,12 +152,29 @@ __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_lif_bwd_pipe(
   }
 }
 
-// Serial hard-reset LIF forward from u0 (triton_lif.py:30-39 serial_fwd_kernel, :460-466
-// serial_forward_tiled): tiles in time order; the consumer runs lif_step, the producers stage
-// I into LDS one tile ahead and store U, S of the tile finished one round earlier.
-__global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_lif_fwd_pipe(
+// The two serial forwards' steps: hard reset (triton_lif.py:21-25) and affine reset
+// (triton_affine.py:20-24), with the one-wave kernels' arithmetic (lif_step, aff_step).
+struct LifStep {
+  float beta, theta, u_r;
+  __device__ __forceinline__ float operator()(float u, float x, bool& s) const {
+    return lif_step(u, x, beta, theta, u_r, s);
+  }
+};
+struct AffStep {
+  float beta, theta, gamma, delta;
+  __device__ __forceinline__ float operator()(float u, float x, bool& s) const {
+    return aff_step(u, x, beta, theta, gamma, delta, s);
+  }
+};
+
+// Serial forward from u0 (triton_lif.py:30-39 serial_fwd_kernel, :460-466
+// serial_forward_tiled; triton_affine.py:143-162): tiles in time order; the consumer runs the
+// step, the producers stage I into LDS one tile ahead and store U, S of the tile finished one
+// round earlier.
+template <class Step>
+__global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_serial_fwd_pipe(
     const float* __restrict__ I, const float* __restrict__ u0, float* __restrict__ U,
-    float* __restrict__ S, int64_t N, int64_t T, float beta, float theta, float u_r) {
+    float* __restrict__ S, int64_t N, int64_t T, Step step) {
   constexpr int D = PIPE_D, P = PIPE_P, R = PIPE_R;
   __shared__ float sX[2][D][WAVE];
   __shared__ float2 sUS[2][D][WAVE];
@@ -186,14 +203,14 @@ __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_lif_fwd_pipe(
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
               bool sp;
-              u = lif_step(u, x[i], beta, theta, u_r, sp);
+              u = step(u, x[i], sp);
               sUS[buf][g + i][lane] = make_float2(u, sp ? 1.0f : 0.0f);
             }
           }
         } else {
           for (int j = 0; j < nr; ++j) {
             bool sp;
-            u = lif_step(u, sX[buf][j][lane], beta, theta, u_r, sp);
+            u = step(u, sX[buf][j][lane], sp);
             sUS[buf][j][lane] = make_float2(u, sp ? 1.0f : 0.0f);
           }
         }
@@ -247,8 +264,15 @@ __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_lif_fwd_pipe(
 void lif_serial_fwd_pipe(const float* I, const float* u0, float* U, float* S, int64_t N, int64_t T,
                          float beta, float theta, float u_r, hipStream_t st) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
-  hipLaunchKernelGGL(k_lif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (PIPE_P + 1)), 0, st, I, u0, U,
-                     S, N, T, beta, theta, u_r);
+  hipLaunchKernelGGL((k_serial_fwd_pipe<LifStep>), dim3((unsigned)NB), dim3(WAVE * (PIPE_P + 1)), 0,
+                     st, I, u0, U, S, N, T, LifStep{beta, theta, u_r});
+}
+
+void aff_serial_fwd_pipe(const float* I, const float* u0, float* U, float* S, int64_t N, int64_t T,
+                         float beta, float theta, float gamma, float delta, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  hipLaunchKernelGGL((k_serial_fwd_pipe<AffStep>), dim3((unsigned)NB), dim3(WAVE * (PIPE_P + 1)), 0,
+                     st, I, u0, U, S, N, T, AffStep{beta, theta, gamma, delta});
 }
 
 template <bool DETACH, bool HAS_GU>

@@ -15,6 +15,7 @@
 // (slot-contiguous, so the 32 lanes of one neuron store 128 contiguous bytes).
 #include "lsh_abi.h"
 #include "lsh_common.h"
+#include "lsh_lookback.h"
 
 namespace lsh {
 
@@ -1208,6 +1209,197 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
   }
 }
 
+// ALIF adjoint for few neurons: both recurrences of k_alif_bwd_fused in one pass, segments of
+// ALIF_LB_W chunks of ALIF_LB_C steps chained across workgroups by decoupled look-back (as the LIF
+// adjoint in lif_lookback.hip), once for lw and then for lv:
+//   1. every wave loads its chunk once (I, u_{t-1}, w_{t-1}, S, GS) and keeps (sg, g, 1 - s);
+//   2. lw: chunk maps (a = rho - q*sg, b = -sg*g) -> segment map, published (flag 1); wave 0
+//      looks back over the later segments to lw at its segment end, publishes lw at its start
+//      (flag 2); every wave replays lw from its chunk end (kept in registers);
+//   3. lv: the same with a = (1 - s)*beta, b = sg*(g + q*lw), then the replay stores LV (and LW)
+//      and sums the parameter gradients (fp32 per chunk, fp64 per workgroup).
+// Workgroups take (segment, block) tiles latest segment first through a ticket counter and wait
+// only for tiles with smaller tickets, which are running or done: every wait ends (and is
+// bounded; a give-up is counted in the header).  The same waves per workgroup with and without
+// the sums, so dI does not depend on whether the parameters need a gradient.
+constexpr int ALIF_LB_C = 16;
+constexpr int ALIF_LB_W = 8;
+constexpr int ALIF_LB_SEG = ALIF_LB_C * ALIF_LB_W;
+
+template <bool WLW, bool PS>
+__global__ __launch_bounds__(WAVE* ALIF_LB_W) void k_alif_bwd_lookback(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
+    const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
+    const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
+    float* __restrict__ DW0, double* __restrict__ partials, float* __restrict__ agg,
+    int* __restrict__ flags, WsHeader* hdr, int64_t N, int NB, int NSEG, float beta, float rho,
+    float q, float theta0, float alpha, const float* __restrict__ dpar) {
+  if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
+  constexpr int C = ALIF_LB_C, WV = ALIF_LB_W;
+  __shared__ float sP[WV][WAVE], sQ[WV][WAVE];
+  __shared__ float sEnd[WAVE];
+  __shared__ double sAcc[WV][4];
+  __shared__ int sTicket;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
+  const unsigned lane = threadIdx.x % WAVE;
+  if (threadIdx.x == 0) sTicket = (int)atomicAdd(&hdr->ticket, 1u);
+  __syncthreads();
+  const int tk = sTicket;
+  const int nb = tk % NB;
+  const int seg = NSEG - 1 - tk / NB;  // latest segments first
+  const int64_t nb0 = (int64_t)nb * WAVE;
+  const bool valid = nb0 + lane < N;
+  const unsigned ln = valid ? lane : (unsigned)(N - 1 - nb0);
+  const unsigned lb = ln * 4u, sb = lane * 4u;
+  const unsigned rstride = (unsigned)(N * 4);
+  const size_t row0 = ((size_t)seg * WV + (WV - 1 - w)) * C;  // wave 0 holds the latest chunk
+  const size_t sn = (size_t)NSEG * (size_t)N;
+  const size_t so = (size_t)seg * N + nb0 + lane;
+
+  // 1. the chunk's per-step quantities
+  float sg[C], g[C], s1[C], lwv[C];
+  float upv[PS ? C : 1], wpv[PS ? C : 1];
+  {
+    const Buf bi(I + nb0 + row0 * N), bs(S + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
+    const Buf bu(U + nb0 + row0 * N), bw(W + nb0 + row0 * N);
+    const float up0 = row0 > 0 ? ld_row(U + nb0 + (row0 - 1) * N, lb) : u0[nb0 + ln];
+    const float wp0 = row0 > 0 ? ld_row(W + nb0 + (row0 - 1) * N, lb) : w0[nb0 + ln];
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      const unsigned o = j * rstride;
+      const float up = j == 0 ? up0 : bu.ld(lb, o - rstride);
+      const float wp = j == 0 ? wp0 : bw.ld(lb, o - rstride);
+      sg[j] = alif_sg(up, wp, bi.ld(lb, o), beta, theta0, alpha);
+      g[j] = bg.ld(lb, o);
+      s1[j] = 1.0f - bs.ld(lb, o);
+      if (PS) {
+        upv[j] = up;
+        wpv[j] = wp;
+      }
+    }
+  }
+
+  // segment map of the chunk maps in sP/sQ, look-back, the value at this segment's end; the
+  // phase's aggregates are agg[phase][0..2] (P, Q, inclusive), its flags flags[phase]
+  auto look_back = [&](int phase) {
+    float* aP = agg + (size_t)phase * 3 * sn;
+    float* aQ = aP + sn;
+    float* inc = aQ + sn;
+    int* fl = flags + (size_t)phase * NSEG * NB;
+    float Ps = 1.0f, Qs = 0.0f;  // value at segment start = Qs + Ps * value at segment end
+    for (int v = 0; v < WV; ++v) {
+      Qs = sQ[v][lane] + sP[v][lane] * Qs;
+      Ps = sP[v][lane] * Ps;
+    }
+    int* const myflag = fl + (size_t)seg * NB + nb;
+    float end = 0.0f;
+    if (seg < NSEG - 1) {
+      if (valid) {
+        st_coh(aP + so, Ps);
+        st_coh(aQ + so, Qs);
+      }
+      publish_flag(myflag, 1);
+      float Pa = 1.0f, Qa = 0.0f;
+      for (int j = seg + 1; j < NSEG; ++j) {
+        const int f = flag_wait(fl + (size_t)j * NB + nb, &hdr->spin_timeouts);
+        const size_t oj = (size_t)j * N + nb0 + ln;
+        if (f == 2 || f < 0) {
+          const float x = f == 2 ? ld_coh(inc + oj) : 0.0f;
+          end = Qa + Pa * x;
+          break;
+        }
+        const float pj = ld_coh(aP + oj), qj = ld_coh(aQ + oj);
+        Qa = Qa + Pa * qj;
+        Pa = Pa * pj;
+      }
+    }
+    if (valid) st_coh(inc + so, Qs + Ps * end);
+    publish_flag(myflag, 2);
+    sEnd[lane] = end;
+  };
+
+  // 2. lw
+  {
+    float P = 1.0f, Q = 0.0f;
+#pragma unroll
+    for (int j = C - 1; j >= 0; --j) {
+      const float a = rho - q * sg[j];
+      P = a * P;
+      Q = a * Q - sg[j] * g[j];
+    }
+    sP[w][lane] = P;
+    sQ[w][lane] = Q;
+  }
+  __syncthreads();
+  if (w == 0) look_back(0);
+  __syncthreads();
+  {
+    float lam = sEnd[lane];
+    for (int v = 0; v < w; ++v) lam = sQ[v][lane] + sP[v][lane] * lam;
+#pragma unroll
+    for (int j = C - 1; j >= 0; --j) {
+      lwv[j] = lam;
+      lam = (rho - q * sg[j]) * lam - sg[j] * g[j];
+    }
+    if (row0 == 0 && DW0 && valid) DW0[nb0 + lane] = lam;
+  }
+  __syncthreads();
+
+  // 3. lv
+  {
+    float P = 1.0f, Q = 0.0f;
+#pragma unroll
+    for (int j = C - 1; j >= 0; --j) {
+      const float a = s1[j] * beta;
+      P = a * P;
+      Q = a * Q + sg[j] * (g[j] + q * lwv[j]);
+    }
+    sP[w][lane] = P;
+    sQ[w][lane] = Q;
+  }
+  __syncthreads();
+  if (w == 0) look_back(1);
+  __syncthreads();
+  ParamAcc acc;
+  {
+    float lam = sEnd[lane];
+    for (int v = 0; v < w; ++v) lam = sQ[v][lane] + sP[v][lane] * lam;
+    const Buf bo(LW + nb0 + row0 * N), bv(LV + nb0 + row0 * N);
+    float cb = 0.0f, cr = 0.0f, cq = 0.0f, ct = 0.0f;
+#pragma unroll
+    for (int j = C - 1; j >= 0; --j) {
+      const float d = g[j] + q * lwv[j];
+      lam = s1[j] * beta * lam + sg[j] * d;
+      if (valid) {
+        if (WLW) bo.st_nt(sb, j * rstride, lwv[j]);
+        bv.st_nt(sb, j * rstride, lam);
+      }
+      if (PS) {
+        cb = fmaf(lam, upv[j], cb);
+        cr = fmaf(lwv[j], wpv[j], cr);
+        cq += s1[j] == 0.0f ? lwv[j] : 0.0f;
+        ct = fmaf(sg[j], d, ct);
+      }
+    }
+    if (PS && valid) acc.add_chunk(cb, cr, cq, ct);
+  }
+  if constexpr (PS) {
+    acc.wave_sum();
+    if (lane == 0) acc.store(sAcc[w]);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      ParamAcc tot;
+      for (int v = 0; v < WV; ++v) {
+        tot.b += sAcc[v][0];
+        tot.r += sAcc[v][1];
+        tot.q += sAcc[v][2];
+        tot.t += sAcc[v][3];
+      }
+      tot.store(partials + ((size_t)seg * NB + nb) * 4);
+    }
+  }
+}
+
 __global__ __launch_bounds__(64) void k_rev_carry(const float* __restrict__ PA_,
                                                   const float* __restrict__ PB_,
                                                   float* __restrict__ lam_end, int64_t N, int M) {
@@ -1440,9 +1632,17 @@ extern "C" size_t lsh_alif_bwd_workspace(int64_t T, int64_t N, int C) {
   return kWsHeaderBytes + 3 * align_up(mn, 256);
 }
 
+extern "C" size_t lsh_alif_bwd_lookback_workspace(int64_t T, int64_t N) {
+  if (T < 0 || N < 0 || T % ALIF_LB_SEG != 0) return 0;
+  const size_t sn = (size_t)(T / ALIF_LB_SEG) * (size_t)N;
+  const size_t nf = (size_t)(T / ALIF_LB_SEG) * (size_t)((N + WAVE - 1) / WAVE);
+  return kWsHeaderBytes + align_up(6 * sn * 4, 256) + align_up(2 * nf * 4, 256);
+}
+
 extern "C" int64_t lsh_alif_bwd_partials(int64_t T, int64_t N, int mode, int C) {
-  if (T < 0 || N < 0 || mode < 0 || mode > 2) return -1;
+  if (T < 0 || N < 0 || mode < 0 || mode > 3) return -1;
   const int64_t NB = (N + WAVE - 1) / WAVE;
+  if (mode == 3) return T % ALIF_LB_SEG == 0 ? (T / ALIF_LB_SEG) * NB : -1;
   if (mode != 1) return NB;
   if (C < 1 || T % C != 0) return -1;
   return (T / C) * NB;
@@ -1510,12 +1710,45 @@ static int alif_bwd(const float* I, const float* U, const float* W, const float*
       bad_ptr(w0) || bad_ptr(LV))
     return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
-  if (mode < 0 || mode > 2) return LSH_ERR_ARG;
+  if (mode < 0 || mode > 3) return LSH_ERR_ARG;
   if (mode == 1 && bad_ptr(LW)) return LSH_ERR_ARG;  // the chunked scans keep LW in between
+  if (mode == 3) {  // look-back single pass (few neurons)
+    if (T % ALIF_LB_SEG != 0) return LSH_ERR_DIVISIBILITY;
+    if ((uint64_t)N * (uint64_t)ALIF_LB_C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+    if ((T / ALIF_LB_SEG) * ((N + WAVE - 1) / WAVE) > ((int64_t)1 << 31) - 1) return LSH_ERR_SHAPE;
+    if (bad_ptr(ws) || ws_bytes < lsh_alif_bwd_lookback_workspace(T, N) ||
+        (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+      return LSH_ERR_WORKSPACE;
+  }
   if (T == 0 || N == 0) return LSH_OK;
   hipStream_t st = (hipStream_t)stream;
   const int NB = (int)((N + WAVE - 1) / WAVE);
   const bool wlw = LW != nullptr, ps = partials != nullptr;
+  if (mode == 3) {
+    const int NSEG = (int)(T / ALIF_LB_SEG);
+    const size_t sn = (size_t)NSEG * (size_t)N;
+    char* wsb = static_cast<char*>(ws);
+    WsHeader* hdr = reinterpret_cast<WsHeader*>(wsb);
+    float* agg = reinterpret_cast<float*>(wsb + kWsHeaderBytes);
+    int* flags = reinterpret_cast<int*>(wsb + kWsHeaderBytes + align_up(6 * sn * 4, 256));
+    hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, hdr);
+    fill_i32_launch(flags, 2 * (int64_t)NSEG * NB, 0, st);
+#define LSH_LB(WL, P)                                                                              \
+  hipLaunchKernelGGL((k_alif_bwd_lookback<WL, P>), dim3((unsigned)((int64_t)NSEG * NB)),           \
+                     dim3(WAVE * ALIF_LB_W), 0, st, I, u0, w0, U, W, S, GS, LW, LV, DW0, partials,  \
+                     agg, flags, hdr, N, NB, NSEG, beta, rho, q, theta0, alpha, dpar)
+    if (wlw && ps)
+      LSH_LB(true, true);
+    else if (wlw)
+      LSH_LB(true, false);
+    else if (ps)
+      LSH_LB(false, true);
+    else
+      LSH_LB(false, false);
+#undef LSH_LB
+    LSH_CHECK_LAUNCH();
+    return LSH_OK;
+  }
   if (mode == 0) {
     if (wlw && ps)
       launch_alif_serial_bwd<true, true>(I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, NB, beta,

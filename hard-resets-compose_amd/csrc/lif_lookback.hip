@@ -21,6 +21,7 @@
 // they go through coherent vector atomics only (see ld_coh / st_coh / publish_flag).
 #include "lsh_abi.h"
 #include "lsh_common.h"
+#include "lsh_lookback.h"
 
 namespace lsh {
 
@@ -29,32 +30,9 @@ __global__ __launch_bounds__(64) void k_fill_i32(int* __restrict__ p, int64_t n,
   if (i < n) p[i] = v;
 }
 
-// Cross-workgroup values are written and read with agent-scope relaxed atomics (coherent
-// vector loads/stores that bypass the non-coherent L2 of each XCD) instead of release/acquire
-// fences, which would write back or invalidate a whole L2 per hand-off.  Ordering: a producer
-// waits for its value stores to be acknowledged (s_waitcnt) before storing the flag; a consumer
-// issues its value loads only after the flag load has returned non-zero.
-__device__ __forceinline__ float ld_coh(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coh(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void publish_flag(int* f, int v) {
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's value stores are acknowledged
-  if (__lane_id() == 0) __hip_atomic_store(f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// flag of (segment, block) -> value seen by the whole wave
-__device__ __forceinline__ int flag_wait(int* f, unsigned int* timeouts) {
-  for (int it = 0; it < (1 << 22); ++it) {
-    int v = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    v = __builtin_amdgcn_readfirstlane(v);
-    if (v != 0) return v;
-    __builtin_amdgcn_s_sleep(2);
-  }
-  if (__lane_id() == 0) atomicAdd(timeouts, 1u);
-  return -1;
+void fill_i32_launch(int* p, int64_t n, int v, hipStream_t st) {
+  if (n > 0)
+    hipLaunchKernelGGL(k_fill_i32, dim3((unsigned)((n + WAVE - 1) / WAVE)), dim3(WAVE), 0, st, p, n, v);
 }
 
 // PS (detached, no GU): parameter sums in fp64, one partials row per workgroup (tile), as

@@ -74,6 +74,9 @@ int lif_param_bwd_lookback(const float* I, const float* u0, const float* U, cons
                            size_t ws_bytes, int64_t T, int64_t N, float beta, float theta,
                            float u_r, float alpha, int ps, hipStream_t st);
 
+// Fills n ints with v on the stream (lif_lookback.hip; look-back flags).
+void fill_i32_launch(int* p, int64_t n, int v, hipStream_t st);
+
 // Wave-specialised serial sweeps (serial_pipe.hip): used instead of the one-wave serial kernels
 // up to serial_pipe_max_blocks() blocks of 64 neurons (lsh_serial_pipe_config sets it).
 int serial_pipe_max_blocks();

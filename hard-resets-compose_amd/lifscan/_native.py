@@ -111,6 +111,7 @@ SIGNATURES = {
                                 ctypes.POINTER(c_p), c_p]),
     "lsh_alif_bwd_workspace": (c_sz, [c_i64, c_i64, c_i]),
     "lsh_alif_bwd_partials": (c_i64, [c_i64, c_i64, c_i, c_i]),
+    "lsh_alif_bwd_lookback_workspace": (c_sz, [c_i64, c_i64]),
     "lsh_lif_param_partials": (c_i64, [c_i64, c_i64, c_i, c_i]),
     "lsh_lif_scan_lookback_bwd_workspace": (c_sz, [c_i64, c_i64]),
     "lsh_lif_scan_lookback_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,

@@ -20,6 +20,9 @@ from .hip_lif import _f32, _f32s, _input, _vec, _same
 # single-pass backward (one workgroup per 64 neurons) pays off only with many neuron blocks
 ALIF_FUSED_BWD_MIN_N = 8192
 ALIF_FUSED_BWD_C = 16
+# below that, the single pass with look-back across workgroups when T is a multiple of its segment
+ALIF_LOOKBACK_SEG = 128
+ALIF_LOOKBACK = True
 # ALIFFn's single-pass adjoint after the serial forward recomputes u, w, s inside each chunk from
 # the stored row before it (lsh_alif_bwd_recompute) instead of reading U, W, S: same bits
 ALIF_RECOMPUTE_BWD = True
@@ -214,15 +217,21 @@ def alif_chunked_C(T, C=64):
 
 def _bwd_mode(mode, T, N, C):
     """Kernel mode code and chunk for an alif_backward mode name.  "scan": the single pass from
-    ALIF_FUSED_BWD_MIN_N neurons, else the chunked passes at alif_chunked_C (N = 1024,
-    T = 65536: C = 128 1.44 ms, the single pass 2.99 ms).  Below that N the single pass would
-    run 16 waves per workgroup without the parameter sums and 8 with them, so dI would depend
-    in its last bits on whether the parameters need a gradient; the chunked passes do not."""
+    ALIF_FUSED_BWD_MIN_N neurons; below that the look-back single pass when T is a multiple of
+    ALIF_LOOKBACK_SEG, else the chunked passes at alif_chunked_C.  (The workgroup-per-64-neurons
+    single pass is slow there: N = 1024, T = 65536: 2.99 ms against 1.44 ms chunked.)"""
     C = int(C)
     if mode == "scan":
-        fused = N >= ALIF_FUSED_BWD_MIN_N and T % ALIF_FUSED_BWD_C == 0
-        mode = "fused" if fused else "chunked"
-        C = ALIF_FUSED_BWD_C if fused else alif_chunked_C(T, C)
+        if N >= ALIF_FUSED_BWD_MIN_N and T % ALIF_FUSED_BWD_C == 0:
+            mode, C = "fused", ALIF_FUSED_BWD_C
+        elif ALIF_LOOKBACK and T % ALIF_LOOKBACK_SEG == 0:
+            mode = "lookback"
+        else:
+            mode, C = "chunked", alif_chunked_C(T, C)
+    if mode == "lookback":
+        if T % ALIF_LOOKBACK_SEG:
+            raise ValueError(f"T={T} must be divisible by {ALIF_LOOKBACK_SEG} for the look-back pass")
+        return 3, 16
     if mode in ("serial_pf", "serial_tuned", "serial"):
         return 0, C
     if mode == "fused":  # single pass, C in {16, 32}
@@ -266,6 +275,9 @@ def _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C,
     if code == 1:
         nbytes = L.lsh_alif_bwd_workspace(T, N, C)
         ws = _n.workspace(nbytes, I.device)
+    elif code == 3:
+        nbytes = L.lsh_alif_bwd_lookback_workspace(T, N)
+        ws = _n.workspace(nbytes, I.device)
     with torch.cuda.device(I.device):
         if rc:
             p = (0.0,) * 4 if dp is not None else (beta, rho, q, theta0)
@@ -284,16 +296,29 @@ def _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C,
                 _n.ptr(LV), _n.ptr(LW), _n.ptr(DW0), _n.ptr(parts), T, N, _f32(beta), _f32(rho),
                 _f32(q), _f32(theta0), _f32(alpha), code, C, _n.ptr(ws), nbytes, _n.stream_of(I)),
                 "lsh_alif_bwd")
+    global _LAST_BWD_WS
+    _LAST_BWD_WS = ws
     sums = parts.sum(0) if parts is not None else None
     return LV, (LW if want_lw else None), DW0, sums
+
+
+_LAST_BWD_WS = None
+
+
+def last_bwd_spin_timeouts():
+    """Bounded waits that gave up in the last look-back adjoint (0 when its result is valid)."""
+    if _LAST_BWD_WS is None:
+        return 0
+    return int(_n.read_stats(_LAST_BWD_WS, 1).spin_timeouts)
 
 
 def alif_backward(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha=4.0, mode="scan", C=64,
                   BN=32, D=4, nw=1):
     """(LV, LW) with LV[t] = dL/dv_t (= dL/dI_t), LW[t] = dL/dw_t for dL/dS = GS
     (triton_alif.py:490-521).  mode: serial_pf / serial_tuned / serial (fused serial sweep),
-    chunked (two-level affine scans over chunks of C), fused (single pass, C in {16, 32}) or
-    scan (fused when N is large, else chunked at its own chunk; _bwd_mode)."""
+    chunked (two-level affine scans over chunks of C), fused (single pass, C in {16, 32}),
+    lookback (single pass with look-back across workgroups, T % 128 == 0) or scan (fused when N
+    is large, else lookback or chunked; _bwd_mode)."""
     LV, LW, _, _ = _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C,
                                   want_lw=True, want_params=False)
     return LV, LW

@@ -339,14 +339,19 @@ int lsh_reverse_affine_scan(const float* A, const float* B, float* L, int64_t T,
 /* ALIF adjoint: LW[t] = dL/dw_t, LV[t] = dL/dv_t (= dL/dI_t) for dL/dS = GS.
  * mode 0: fused serial sweep (triton_alif.py:444-487); 1: chunked two-level affine scans of
  * chunk C (triton_alif.py:510-521, needs lsh_alif_bwd_workspace(T, N, C) bytes); 2: single
- * pass, internal chunk C in {16, 32} (no workspace).  Replaces triton_alif.py:490-521 and the
- * reductions of ALIFFn.backward (triton_alif.py:541-554):
- *   LW       may be NULL in modes 0 and 2 (not written);
+ * pass, internal chunk C in {16, 32} (no workspace); 3: single pass with look-back across
+ * workgroups (T % 128 == 0, lsh_alif_bwd_lookback_workspace(T, N) bytes, C ignored).  Replaces
+ * triton_alif.py:490-521 and the reductions of ALIFFn.backward (triton_alif.py:541-554):
+ *   LW       may be NULL in modes 0, 2 and 3 (not written);
  *   DW0      NULL or [N]: dL/dw0 = lw_{-1} = rho*LW[0] - sg_0*(g_0 + q*LW[0]);
- *   partials NULL or [lsh_alif_bwd_partials(T, N, mode, C)][4] doubles, one row per block:
+ *   partials NULL or [lsh_alif_bwd_partials(T, N, mode, C)][4] doubles, one row per workgroup:
  *            sum LV*u_{t-1}, sum LW*w_{t-1}, sum LW*S, sum sg*(g + q*LW) (fp64); their column
  *            sums are dbeta, drho, dq and -dtheta0. */
 size_t lsh_alif_bwd_workspace(int64_t T, int64_t N, int C);
+/* mode 3: the single pass for few neurons, segments of 128 steps chained across workgroups by
+ * decoupled look-back (first lw, then lv); requires T % 128 == 0 and this many workspace bytes.
+ * No counterpart in the reference (same recurrences as triton_alif.py:490-521). */
+size_t lsh_alif_bwd_lookback_workspace(int64_t T, int64_t N);
 int64_t lsh_alif_bwd_partials(int64_t T, int64_t N, int mode, int C);
 int lsh_alif_bwd(const float* I, const float* U, const float* W, const float* S, const float* GS,
                  const float* u0, const float* w0, float* LV, float* LW, float* DW0,

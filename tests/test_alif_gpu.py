@@ -202,7 +202,7 @@ def test_alif_scan_phases_and_shapes(AL, dev):
 
 @pytest.mark.parametrize("beta,rho,q", [(0.95, 0.995, 0.9), (0.99, 0.96, 0.2)])
 @pytest.mark.parametrize("mode,C", [("serial", 64), ("chunked", 64), ("chunked", 16), ("fused", 16),
-                                    ("fused", 32)])
+                                    ("fused", 32), ("lookback", 16)])
 def test_alif_backward_modes(AL, dev, beta, rho, q, mode, C):
     T, N = 1024, 130
     x = _inputs(beta, 2.0, T, N, 15)
@@ -265,7 +265,8 @@ def test_alif_layer_gradients(AL, dev, fwd, bwd, beta, rho, q, T, N):
         assert rel(host(a), b) < (1e-4 if k < 3 else 1e-3), k
 
 
-@pytest.mark.parametrize("mode,C", [("serial", 64), ("chunked", 64), ("fused", 16), ("fused", 32)])
+@pytest.mark.parametrize("mode,C", [("serial", 64), ("chunked", 64), ("fused", 16), ("fused", 32),
+                                    ("lookback", 16)])
 @pytest.mark.parametrize("T,N", [(1024, 130), (77 * 16, 33)])
 def test_alif_backward_param_sums_and_dw0(AL, dev, mode, C, T, N):
     """The adjoint kernels' own reductions (dL/dw0 and the four parameter sums, one fp64 row per
@@ -273,6 +274,13 @@ def test_alif_backward_param_sums_and_dw0(AL, dev, mode, C, T, N):
     with and without LW written."""
     from lifscan import hip_alif
     beta, rho, q = 0.95, 0.995, 0.9
+    if mode == "lookback" and T % 128:  # its segments are 128 steps: refused, not mis-computed
+        z = torch.zeros(T, N, device=dev)
+        v = torch.zeros(N, device=dev)
+        with pytest.raises(ValueError):
+            hip_alif._alif_bwd_call(z, z, z, z, z, beta, rho, q, 1.0, v, v, 4.0, mode, C,
+                                    want_lw=False, want_params=True)
+        return
     if mode != "serial" and T % C:
         C = 16
     x = _inputs(beta, 2.0, T, N, 23)
@@ -461,3 +469,37 @@ def test_alif_serial_fwd_pipe_equals_one_wave(AL, dev, T, N):
         hip_lif.serial_pipe_max_blocks(prev)
     for a, b, c, o in zip(ref, got, got2, (Ur, Wr, Sr)):
         assert torch.equal(a, b) and torch.equal(a, c) and np.array_equal(host(b), o)
+
+
+@pytest.mark.parametrize("T,N", [(128, 1), (1280, 64), (4096, 70), (16384, 130)])
+def test_alif_lookback_bwd(AL, dev, T, N):
+    """The look-back single pass (mode 3): LV and LW against the fp32 oracle and the fp64
+    adjoint, dL/dw0 and the four sums against the fp64 assembly, with float and device
+    parameters (same bits), and no bounded wait given up."""
+    from lifscan import hip_alif
+    beta, rho, q = 0.95, 0.995, 0.9
+    x = _inputs(beta, 2.0, T, N, 95)
+    G = normal(T, N, 0.0, 1.0, 96)
+    u0 = uniform(N, -0.1, 0.3, 97)
+    w0 = uniform(N, 0.0, 0.2, 98)
+    U, W, S = A.serial_forward(x, beta, rho, q, 1.0, 0.0, u0, w0)
+    args = [gpu(a, dev) for a in (x, U, W, S, G)]
+    ug, wg = gpu(u0, dev), gpu(w0, dev)
+    print(f"alif lookback T={T} N={N}", flush=True)
+    LV, LW, DW0, sums = hip_alif._alif_bwd_call(*args, beta, rho, q, 1.0, ug, wg, 4.0, "lookback", 16,
+                                                want_lw=True, want_params=True)
+    assert hip_alif.last_bwd_spin_timeouts() == 0
+    dp = hip_alif._dev_params(args[0], torch.tensor(beta, device=dev), rho, q, 1.0)
+    got = hip_alif._alif_bwd_call(*args, None, None, None, None, ug, wg, 4.0, "lookback", 16,
+                                  want_lw=True, want_params=True, dp=dp)
+    for a, b in zip((LV, LW, DW0, sums), got):
+        assert torch.equal(a, b)
+    LVo, LWo = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0)
+    LV6, LW6 = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0, dtype=np.float64)
+    assert rel(host(LV), LVo) < 1e-5 and rel(host(LW), LWo) < 1e-5
+    assert rel(host(LV), LV6) < 1e-4 and rel(host(LW), LW6) < 1e-4
+    want = A.param_grads(x, U, W, S, G, LV6, LW6, beta, rho, q, 1.0, u0, w0, 4.0)
+    assert rel(host(DW0), want[2]) < 1e-4
+    got_s = host(sums)
+    for k, w in enumerate((want[3], want[4], want[5], -want[6])):
+        assert rel(got_s[k], w) < 1e-3, k

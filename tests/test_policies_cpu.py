@@ -23,16 +23,18 @@ def test_chunked_bwd_chunk_choice():
 
 
 def test_alif_scan_adjoint_dispatch():
-    """ALIF adjoint "scan": the single pass from 8192 neurons, else the chunked passes at the
-    power-of-two chunk nearest sqrt(T/4)."""
+    """ALIF adjoint "scan": the single pass from 8192 neurons, else the look-back single pass when
+    T is a multiple of 128, else the chunked passes at the power-of-two chunk nearest sqrt(T/4)."""
     from lifscan import hip_alif as H
     assert H.alif_chunked_C(4096) == 32
     assert H.alif_chunked_C(65536) == 128
     assert H.alif_chunked_C(2 ** 20) == 512
     assert H.alif_chunked_C(1000, C=8) == 8          # no power of two in 16..512 divides T
-    assert H._bwd_mode("scan", 65536, 1024, 64) == (1, 128)
-    assert H._bwd_mode("scan", 16384, 4096, 64) == (1, 64)
+    assert H._bwd_mode("scan", 65536, 1024, 64) == (3, 16)   # look-back single pass
+    assert H._bwd_mode("scan", 16384, 4096, 64) == (3, 16)
     assert H._bwd_mode("scan", 4096, 16384, 64) == (2, 16)
+    assert H._bwd_mode("scan", 4160, 1024, 64) == (1, 32)    # T % 128 != 0: chunked
+    assert H._bwd_mode("chunked", 65536, 1024, 128) == (1, 128)
     assert H._bwd_mode("serial", 4096, 16, 64) == (0, 64)
     with pytest.raises(ValueError):
         H._bwd_mode("chunked", 100, 8, 64)

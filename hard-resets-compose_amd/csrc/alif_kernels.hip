@@ -1221,19 +1221,21 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
 // Workgroups take (segment, block) tiles latest segment first through a ticket counter and wait
 // only for tiles with smaller tickets, which are running or done: every wait ends (and is
 // bounded; a give-up is counted in the header).  The same waves per workgroup with and without
-// the sums, so dI does not depend on whether the parameters need a gradient.
+// the sums, so dI does not depend on whether the parameters need a gradient.  RC: as in
+// k_alif_bwd_fused, S is not read and U, W only at the row before each chunk (the chunk's states
+// recomputed with alif_step from there; the same bits as the stored variant).
 constexpr int ALIF_LB_C = 16;
 constexpr int ALIF_LB_W = 8;
 constexpr int ALIF_LB_SEG = ALIF_LB_C * ALIF_LB_W;
 
-template <bool WLW, bool PS>
+template <bool WLW, bool PS, bool RC = false>
 __global__ __launch_bounds__(WAVE* ALIF_LB_W) void k_alif_bwd_lookback(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
     const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
     float* __restrict__ DW0, double* __restrict__ partials, float* __restrict__ agg,
     int* __restrict__ flags, WsHeader* hdr, int64_t N, int NB, int NSEG, float beta, float rho,
-    float q, float theta0, float alpha, const float* __restrict__ dpar) {
+    float q, float theta0, float alpha, float u_r, const float* __restrict__ dpar) {
   if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
   constexpr int C = ALIF_LB_C, WV = ALIF_LB_W;
   __shared__ float sP[WV][WAVE], sQ[WV][WAVE];
@@ -1259,7 +1261,28 @@ __global__ __launch_bounds__(WAVE* ALIF_LB_W) void k_alif_bwd_lookback(
   // 1. the chunk's per-step quantities
   float sg[C], g[C], s1[C], lwv[C];
   float upv[PS ? C : 1], wpv[PS ? C : 1];
-  {
+  if constexpr (RC) {
+    const Buf bi(I + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
+    float up = row0 > 0 ? ld_row(U + nb0 + (row0 - 1) * N, lb) : u0[nb0 + ln];
+    float wp = row0 > 0 ? ld_row(W + nb0 + (row0 - 1) * N, lb) : w0[nb0 + ln];
+    float xv[C];
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      xv[j] = bi.ld(lb, j * rstride);
+      g[j] = bg.ld(lb, j * rstride);
+    }
+#pragma unroll
+    for (int j = 0; j < C; ++j) {
+      sg[j] = alif_sg(up, wp, xv[j], beta, theta0, alpha);
+      if (PS) {
+        upv[j] = up;
+        wpv[j] = wp;
+      }
+      bool sp;
+      up = alif_step(up, wp, xv[j], beta, rho, q, theta0, u_r, sp);
+      s1[j] = sp ? 0.0f : 1.0f;
+    }
+  } else {
     const Buf bi(I + nb0 + row0 * N), bs(S + nb0 + row0 * N), bg(GS + nb0 + row0 * N);
     const Buf bu(U + nb0 + row0 * N), bw(W + nb0 + row0 * N);
     const float up0 = row0 > 0 ? ld_row(U + nb0 + (row0 - 1) * N, lb) : u0[nb0 + ln];
@@ -1701,6 +1724,39 @@ static void launch_alif_serial_bwd(const float* I, const float* u0, const float*
                      U, W, S, GS, LW, LV, DW0, partials, N, T, beta, rho, q, theta0, alpha, dpar);
 }
 
+// The look-back single pass (mode 3): header reset, flags cleared, one workgroup per (segment,
+// 64-neuron block).  Shapes and the workspace are checked by the caller.
+template <bool RC>
+static void alif_lookback_launch(const float* I, const float* U, const float* W, const float* S,
+                                 const float* GS, const float* u0, const float* w0, float* LV,
+                                 float* LW, float* DW0, double* partials, int64_t T, int64_t N,
+                                 float beta, float rho, float q, float theta0, float u_r, float alpha,
+                                 const float* dpar, void* ws, hipStream_t st) {
+  const int NB = (int)((N + WAVE - 1) / WAVE);
+  const int NSEG = (int)(T / ALIF_LB_SEG);
+  const size_t sn = (size_t)NSEG * (size_t)N;
+  char* wsb = static_cast<char*>(ws);
+  WsHeader* hdr = reinterpret_cast<WsHeader*>(wsb);
+  float* agg = reinterpret_cast<float*>(wsb + kWsHeaderBytes);
+  int* flags = reinterpret_cast<int*>(wsb + kWsHeaderBytes + align_up(6 * sn * 4, 256));
+  hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, hdr);
+  fill_i32_launch(flags, 2 * (int64_t)NSEG * NB, 0, st);
+  const bool wlw = LW != nullptr, ps = partials != nullptr;
+#define LSH_LB(WL, P)                                                                              \
+  hipLaunchKernelGGL((k_alif_bwd_lookback<WL, P, RC>), dim3((unsigned)((int64_t)NSEG * NB)),       \
+                     dim3(WAVE * ALIF_LB_W), 0, st, I, u0, w0, U, W, S, GS, LW, LV, DW0, partials,  \
+                     agg, flags, hdr, N, NB, NSEG, beta, rho, q, theta0, alpha, u_r, dpar)
+  if (wlw && ps)
+    LSH_LB(true, true);
+  else if (wlw)
+    LSH_LB(true, false);
+  else if (ps)
+    LSH_LB(false, true);
+  else
+    LSH_LB(false, false);
+#undef LSH_LB
+}
+
 static int alif_bwd(const float* I, const float* U, const float* W, const float* S,
                     const float* GS, const float* u0, const float* w0, float* LV, float* LW,
                     float* DW0, double* partials, int64_t T, int64_t N, float beta, float rho,
@@ -1725,27 +1781,8 @@ static int alif_bwd(const float* I, const float* U, const float* W, const float*
   const int NB = (int)((N + WAVE - 1) / WAVE);
   const bool wlw = LW != nullptr, ps = partials != nullptr;
   if (mode == 3) {
-    const int NSEG = (int)(T / ALIF_LB_SEG);
-    const size_t sn = (size_t)NSEG * (size_t)N;
-    char* wsb = static_cast<char*>(ws);
-    WsHeader* hdr = reinterpret_cast<WsHeader*>(wsb);
-    float* agg = reinterpret_cast<float*>(wsb + kWsHeaderBytes);
-    int* flags = reinterpret_cast<int*>(wsb + kWsHeaderBytes + align_up(6 * sn * 4, 256));
-    hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, hdr);
-    fill_i32_launch(flags, 2 * (int64_t)NSEG * NB, 0, st);
-#define LSH_LB(WL, P)                                                                              \
-  hipLaunchKernelGGL((k_alif_bwd_lookback<WL, P>), dim3((unsigned)((int64_t)NSEG * NB)),           \
-                     dim3(WAVE * ALIF_LB_W), 0, st, I, u0, w0, U, W, S, GS, LW, LV, DW0, partials,  \
-                     agg, flags, hdr, N, NB, NSEG, beta, rho, q, theta0, alpha, dpar)
-    if (wlw && ps)
-      LSH_LB(true, true);
-    else if (wlw)
-      LSH_LB(true, false);
-    else if (ps)
-      LSH_LB(false, true);
-    else
-      LSH_LB(false, false);
-#undef LSH_LB
+    alif_lookback_launch<false>(I, U, W, S, GS, u0, w0, LV, LW, DW0, partials, T, N, beta, rho, q,
+                                theta0, 0.0f, alpha, dpar, ws, st);
     LSH_CHECK_LAUNCH();
     return LSH_OK;
   }
@@ -1848,11 +1885,26 @@ extern "C" int lsh_alif_bwd_recompute(const float* I, const float* U, const floa
                                       const float* GS, const float* u0, const float* w0, float* LV,
                                       float* LW, float* DW0, double* partials, int64_t T, int64_t N,
                                       const float* params, float beta, float rho, float q,
-                                      float theta0, float u_r, float alpha, int C, void* stream) {
+                                      float theta0, float u_r, float alpha, int mode, int C,
+                                      void* ws, size_t ws_bytes, void* stream) {
   if (bad_ptr(I) || bad_ptr(U) || bad_ptr(W) || bad_ptr(GS) || bad_ptr(u0) || bad_ptr(w0) ||
       bad_ptr(LV))
     return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (mode != 2 && mode != 3) return LSH_ERR_ARG;
+  if (mode == 3) {
+    if (T % ALIF_LB_SEG != 0) return LSH_ERR_DIVISIBILITY;
+    if ((uint64_t)N * (uint64_t)ALIF_LB_C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
+    if ((T / ALIF_LB_SEG) * ((N + WAVE - 1) / WAVE) > ((int64_t)1 << 31) - 1) return LSH_ERR_SHAPE;
+    if (bad_ptr(ws) || ws_bytes < lsh_alif_bwd_lookback_workspace(T, N) ||
+        (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+      return LSH_ERR_WORKSPACE;
+    if (T == 0 || N == 0) return LSH_OK;
+    alif_lookback_launch<true>(I, U, W, nullptr, GS, u0, w0, LV, LW, DW0, partials, T, N, beta, rho,
+                               q, theta0, u_r, alpha, params, ws, (hipStream_t)stream);
+    LSH_CHECK_LAUNCH();
+    return LSH_OK;
+  }
   if (C != 16 && C != 32) return LSH_ERR_SHAPE;
   if (T % C != 0) return LSH_ERR_DIVISIBILITY;
   if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;

@@ -123,7 +123,7 @@ SIGNATURES = {
     "lsh_alif_bwd_dparams": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64,
                                    c_i64, c_p, c_f, c_i, c_i, c_p, c_sz, c_p]),
     "lsh_alif_bwd_recompute": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64,
-                                     c_p, c_f, c_f, c_f, c_f, c_f, c_f, c_i, c_p]),
+                                     c_p, c_f, c_f, c_f, c_f, c_f, c_f, c_i, c_i, c_p, c_sz, c_p]),
     "lsh_aff_serial_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f, c_p]),
     "lsh_aff_scan_workspace": (c_sz, [c_i64, c_i64, c_i, c_i]),
     "lsh_aff_scan_layout": (c_i, [c_i64, c_i64, c_i, c_i, ctypes.POINTER(AffLayout)]),

@@ -248,15 +248,15 @@ def _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C,
     """One lsh_alif_bwd call -> (LV, LW or None, DW0 [N], param sums [4] fp64 or None); with dp
     (device [beta, rho, q, theta0]) the kernels read the parameters from it (lsh_alif_bwd_dparams)
     and beta, rho, q, theta0 are ignored.  recompute_ur (the reset value u_r) selects, when the
-    mode resolves to the single pass, lsh_alif_bwd_recompute: S is not read and U, W only at
-    chunk boundaries, for U, W, S of one serial trajectory."""
+    mode resolves to a single pass (fused or look-back), lsh_alif_bwd_recompute: S is not read
+    and U, W only at chunk boundaries, for U, W, S of one serial trajectory."""
     I = _input(I)
     T, N = I.shape
     u0 = _vec(u0, N, I)
     w0 = _vec(w0, N, I, "w0")
     U, W, GS = (_same(a, I, nm) for a, nm in ((U, "U"), (W, "W"), (GS, "GS")))
     code, C = _bwd_mode(mode, T, N, C)
-    rc = recompute_ur is not None and code == 2
+    rc = recompute_ur is not None and code in (2, 3)
     if not rc:
         S = _same(S, I, "S")
     L = _n.lib()
@@ -284,7 +284,8 @@ def _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C,
             _n.check(L.lsh_alif_bwd_recompute(
                 _n.ptr(I), _n.ptr(U), _n.ptr(W), _n.ptr(GS), _n.ptr(u0), _n.ptr(w0), _n.ptr(LV),
                 _n.ptr(LW), _n.ptr(DW0), _n.ptr(parts), T, N, _n.ptr(dp), *(_f32(v) for v in p),
-                _f32(recompute_ur), _f32(alpha), C, _n.stream_of(I)), "lsh_alif_bwd_recompute")
+                _f32(recompute_ur), _f32(alpha), code, C, _n.ptr(ws), nbytes, _n.stream_of(I)),
+                "lsh_alif_bwd_recompute")
         elif dp is not None:
             _n.check(L.lsh_alif_bwd_dparams(
                 _n.ptr(I), _n.ptr(U), _n.ptr(W), _n.ptr(S), _n.ptr(GS), _n.ptr(u0), _n.ptr(w0),

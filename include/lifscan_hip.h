@@ -364,18 +364,19 @@ int lsh_alif_bwd_dparams(const float* I, const float* U, const float* W, const f
                          const float* GS, const float* u0, const float* w0, float* LV, float* LW,
                          float* DW0, double* partials, int64_t T, int64_t N, const float* params,
                          float alpha, int mode, int C, void* ws, size_t ws_bytes, void* stream);
-/* Single-pass ALIF adjoint (mode 2 above, C in {16, 32}, same outputs bit for bit) that reads
- * I and GS, and U, W only at the row before each chunk: u_{t-1}, w_{t-1} and s_t inside the chunk
- * are recomputed with the forward step (reset value u_r).  Valid when U, W (and the S they imply)
- * are one serial trajectory from (u0, w0), as lsh_alif_serial_fwd writes them; 8.5 bytes read
- * per neuron-step at C = 16 instead of 20.  params: NULL (use beta, rho, q, theta0) or a device
- * pointer to [beta, rho, q, theta0].  Replaces the adjoint half of ALIFFn.backward
- * (triton_alif.py:541-554) for its serial forward (triton_alif.py:531-533). */
+/* The ALIF adjoint of mode 2 (C in {16, 32}) or mode 3 (look-back; ws as for lsh_alif_bwd) above,
+ * same outputs bit for bit, reading I and GS, and U, W only at the row before each chunk: u_{t-1},
+ * w_{t-1} and s_t inside the chunk are recomputed with the forward step (reset value u_r).  Valid
+ * when U, W (and the S they imply) are one serial trajectory from (u0, w0), as
+ * lsh_alif_serial_fwd writes them; 8.5 bytes read per neuron-step at 16-step chunks instead of
+ * 20.  params: NULL (use beta, rho, q, theta0) or a device pointer to [beta, rho, q, theta0].
+ * Replaces the adjoint half of ALIFFn.backward (triton_alif.py:541-554) for its serial forward
+ * (triton_alif.py:531-533). */
 int lsh_alif_bwd_recompute(const float* I, const float* U, const float* W, const float* GS,
                            const float* u0, const float* w0, float* LV, float* LW, float* DW0,
                            double* partials, int64_t T, int64_t N, const float* params, float beta,
-                           float rho, float q, float theta0, float u_r, float alpha, int C,
-                           void* stream);
+                           float rho, float q, float theta0, float u_r, float alpha, int mode,
+                           int C, void* ws, size_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

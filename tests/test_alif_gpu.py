@@ -357,9 +357,13 @@ def test_alif_float_and_tensor_params_agree(AL, dev, fwd):
     pm = [torch.tensor(beta, device=dev, requires_grad=True), rho,
           torch.tensor(q, device=dev, requires_grad=True), 1.0]
     o3, g3 = run(pm)
-    for a, b, c in zip(o1 + g1, o2 + g2, o3 + g3):
+    for a, b, c in zip(o1, o2, o3):
         assert torch.equal(a, b) and torch.equal(a, c)
-    assert torch.equal(pm[0].grad, pt[0].grad) and torch.equal(pm[2].grad, pt[2].grad)
+    # below 8192 neurons the adjoint is the look-back pass, whose last bits depend on timing
+    for a, b, c in zip(g1, g2, g3):
+        assert rel(host(b), host(a)) < 1e-6 and rel(host(c), host(a)) < 1e-6
+    assert rel(host(pm[0].grad), host(pt[0].grad)) < 1e-6
+    assert rel(host(pm[2].grad), host(pt[2].grad)) < 1e-6
     assert all(p.grad is not None for p in pt)
 
 
@@ -492,8 +496,8 @@ def test_alif_lookback_bwd(AL, dev, T, N):
     dp = hip_alif._dev_params(args[0], torch.tensor(beta, device=dev), rho, q, 1.0)
     got = hip_alif._alif_bwd_call(*args, None, None, None, None, ug, wg, 4.0, "lookback", 16,
                                   want_lw=True, want_params=True, dp=dp)
-    for a, b in zip((LV, LW, DW0, sums), got):
-        assert torch.equal(a, b)
+    for a, b in zip((LV, LW, DW0, sums), got):  # timing decides the look-back's last bits
+        assert rel(host(b), host(a)) < 1e-6
     LVo, LWo = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0)
     LV6, LW6 = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0, dtype=np.float64)
     assert rel(host(LV), LVo) < 1e-5 and rel(host(LW), LWo) < 1e-5
@@ -503,3 +507,55 @@ def test_alif_lookback_bwd(AL, dev, T, N):
     got_s = host(sums)
     for k, w in enumerate((want[3], want[4], want[5], -want[6])):
         assert rel(got_s[k], w) < 1e-3, k
+
+
+@pytest.mark.parametrize("T,N,u_r", [(1280, 130, 0.0), (512, 33, -0.2)])
+def test_alif_lookback_recompute(AL, dev, T, N, u_r):
+    """The look-back pass recomputing the chunk states (lsh_alif_bwd_recompute, mode 3) agrees with
+    the look-back pass reading them, for float and device parameters: to 1e-6, since which later
+    segments a workgroup composes before it meets a published value depends on timing (the
+    chunk values themselves are the same bits; the fused pass's bit-exact test covers them)."""
+    from lifscan import hip_alif
+    beta, rho, q, th = 0.95, 0.995, 0.9, 1.0
+    x = _inputs(beta, 2.0, T, N, 101)
+    G = normal(T, N, 0.0, 1.0, 102)
+    u0 = uniform(N, -0.1, 0.3, 103)
+    w0 = uniform(N, 0.0, 0.2, 104)
+    U, W, S = A.serial_forward(x, beta, rho, q, th, u_r, u0, w0)
+    args = [gpu(a, dev) for a in (x, U, W, S, G)]
+    ug, wg = gpu(u0, dev), gpu(w0, dev)
+    print(f"alif lookback recompute T={T} N={N}", flush=True)
+    ref = hip_alif._alif_bwd_call(*args, beta, rho, q, th, ug, wg, 4.0, "lookback", 16, want_lw=True,
+                                  want_params=True)
+    got = hip_alif._alif_bwd_call(*args, beta, rho, q, th, ug, wg, 4.0, "lookback", 16, want_lw=True,
+                                  want_params=True, recompute_ur=u_r)
+    dp = hip_alif._dev_params(args[0], torch.tensor(beta, device=dev), rho, q, th)
+    got2 = hip_alif._alif_bwd_call(*args[:3], None, args[4], None, None, None, None, ug, wg, 4.0,
+                                   "lookback", 16, want_lw=True, want_params=True, dp=dp,
+                                   recompute_ur=u_r)
+    assert hip_alif.last_bwd_spin_timeouts() == 0
+    for a, b, c in zip(ref, got, got2):
+        assert rel(host(b), host(a)) < 1e-6 and rel(host(c), host(a)) < 1e-6
+
+
+def test_alif_layer_small_n_recompute_equals_stored(AL, dev, monkeypatch):
+    """alif(fwd="serial", bwd="scan") below 8192 neurons takes the recomputing look-back pass: the
+    gradients of the look-back pass that reads the stored states, to 1e-6."""
+    from lifscan import hip_alif
+    beta, rho, q, T, N = 0.95, 0.995, 0.2, 1024, 200
+    x = gpu(_inputs(beta, 2.0, T, N, 105), dev)
+    G = gpu(normal(T, N, 0.0, 1.0, 106), dev)
+    u0 = gpu(uniform(N, -0.1, 0.3, 107), dev)
+    w0 = gpu(uniform(N, 0.0, 0.2, 108), dev)
+    print("alif layer small-N recompute vs stored", flush=True)
+
+    def run(flag):
+        monkeypatch.setattr(hip_alif, "ALIF_RECOMPUTE_BWD", flag)
+        xg, ug, wg = (a.clone().requires_grad_(True) for a in (x, u0, w0))
+        ps = [torch.tensor(v, device=dev, requires_grad=True) for v in (beta, rho, q, 1.0)]
+        S, _, _ = AL.alif(xg, ug, wg, *ps, u_r=-0.1, fwd="serial", bwd="scan")
+        (S * G).sum().backward()
+        return [xg.grad, ug.grad, wg.grad] + [p.grad for p in ps]
+
+    for a, b in zip(run(True), run(False)):
+        assert rel(host(a), host(b)) < 1e-6

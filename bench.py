@@ -74,6 +74,30 @@ def ev_time(fn, reps, warm=1, warm_s=0.0):
     return statistics.median(ts)
 
 
+def bb_time(fn, reps, groups=5, warm=2, warm_s=0.0):
+    """Throughput ms per call: fn() called reps times back to back between two HIP events
+    (as the headline's step loop runs), the median over groups.  Unlike ev_time, the host's
+    work before each launch overlaps the previous call's kernels."""
+    import torch
+    for _ in range(warm):
+        fn()
+    t_end = time.perf_counter() + warm_s
+    while time.perf_counter() < t_end:
+        fn()
+    ts = []
+    for _ in range(groups):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) / reps)
+    return statistics.median(ts)
+
+
 def profiled_traffic():
     """HBM bytes per launch of the dominant kernel from the committed counter summary
     (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled on a copy kernel)."""
@@ -158,9 +182,11 @@ def bench_cfg3(torch, dev, reps):
             S = L.lif_tuned(Ig, torch.zeros(I.shape[1], device=dev), beta=0.95, mode="scan", K=16,
                             repair=10 ** 6)
             S.backward(g2)
-    # small kernels (~65 us per layer): the per-call host work is a large share, and the figure
-    # has varied between 0.19 and 0.33 ms from run to run on these boxes
-    out["lif_layers_fwd_bwd_ms"] = ev_time(layers, max(reps, 10), warm=2, warm_s=0.5)
+    # small kernels (~65 us per layer): timed back to back (the host's per-call work overlaps
+    # the previous call's kernels, as in a training loop), and per call (one call between two
+    # synchronizations, the host's launch latency included)
+    out["lif_layers_fwd_bwd_ms"] = bb_time(layers, max(reps, 10), warm=2, warm_s=0.5)
+    out["lif_layers_fwd_bwd_per_call_ms"] = ev_time(layers, max(reps, 10), warm=2)
     for mode in ("scan", "serial", "auto"):
         torch.manual_seed(4)
         netm = Net(mode).to(dev)
@@ -253,7 +279,9 @@ def bench_cfg5(torch, dev, reps):
             Wp = A.alif_warm_predict(I, beta, rho, q, 1.0, 0.0, z, z, C, Wn=4) if fwd == "scan" else None
             S, _, _ = A.alif(Ig, z, z, *ps, fwd=fwd, bwd="scan", Wpred=Wp, dw=0.1 * q, C=C)
             S.backward(gS)
-        out[f"alif_fwd_{fwd}_bwd_scan_ms"] = ev_time(step, reps, warm=2)
+        # back to back as the headline's step loop; per call: one step between two synchronizations
+        out[f"alif_fwd_{fwd}_bwd_scan_ms"] = bb_time(step, reps, warm=2)
+        out[f"alif_fwd_{fwd}_bwd_scan_per_call_ms"] = ev_time(step, reps, warm=1)
     out["serial_fwd_ms"] = ev_time(lambda: A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z), reps)
     U, W, S = A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z)
     # Two predictions of the chunk-entry adaptation (experiments/e25d_alif_fwd.py:44-50): the
@@ -301,7 +329,7 @@ def bench_cfg5(torch, dev, reps):
 
 
 def bench_alif_reference_shape(torch, dev):
-    """The shape the reference publishes for ALIF (BASELINE.md "cfg5 nearest": lsnn beta=0.95,
+    """The shape the reference publishes for ALIF (lsnn beta=0.95,
     rho=0.995, q=0.9, free mean 1.0, N=1024, T=65536; inputs as experiments/e25d_alif_fwd.py:37,
     u0=w0=0): serial forward; box scan with the previous-iterate prediction (1.005x input, C=256,
     dw=0.1q, K1=K2=32; without repair as the reference times it, and with repair, exact); serial

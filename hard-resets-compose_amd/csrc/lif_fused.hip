@@ -197,7 +197,7 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_fwd_fused(const float* __restri
   }
   fixups = wave_sum_u64(fixups);
   unknown = wave_sum_u64(unknown);
-  if (lane == 0) {
+  if (lane == 0 && hdr != nullptr) {  // the starts-only forward may run without counters
     if (fixups) atomicAdd(&hdr->fused_fixups, fixups);
     if (unknown) atomicAdd(&hdr->fused_unknown, unknown);
     if (timeouts) atomicAdd(&hdr->spin_timeouts, timeouts);
@@ -626,16 +626,18 @@ extern "C" int lsh_lif_scan_exact_fwd_starts(const float* I, const float* u0, fl
                                              float* S, int64_t T, int64_t N, float beta,
                                              float theta, float u_r, int C, void* ws,
                                              size_t ws_bytes, void* stream) {
-  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(STARTS) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(STARTS) || bad_ptr(S)) return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (C != 16 && C != 32 && C != 64) return LSH_ERR_SHAPE;
   if (T % C != 0) return LSH_ERR_DIVISIBILITY;
   if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
-  if (ws_bytes < kWsHeaderBytes || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+  // ws NULL: no counters, and no reset launch before the forward
+  if (ws != nullptr &&
+      (ws_bytes < kWsHeaderBytes || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0))
     return LSH_ERR_WORKSPACE;
   hipStream_t st = (hipStream_t)stream;
   WsHeader* h = reinterpret_cast<WsHeader*>(ws);
-  hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, h);
+  if (h != nullptr) hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, h);
   if (T > 0 && N > 0) {
     const int M = (int)(T / C);
     switch (C) {

@@ -4,6 +4,7 @@ torch is imported first so that the HIP runtime it loads (SONAME libamdhip64.so.
 one the library binds to: streams and device pointers handed over by torch are then valid
 in the library.  There is no fallback: if the library is missing, every call raises.
 """
+import contextlib
 import ctypes
 import os
 
@@ -180,7 +181,17 @@ def ptr(t):
 
 
 def stream_of(t):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """torch's current stream on t's device as a raw hipStream_t."""
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(t.device.index))
+
+
+def on_device(t):
+    """Context making t's device the current one; a no-op when it already is (the common
+    case, which then costs no device exchange on the host)."""
+    idx = t.device.index
+    if idx == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(idx)
 
 
 def workspace(nbytes, device):

@@ -47,7 +47,7 @@ def _param_backward(I, u0, U, S, GS, beta, theta, u_r, alpha, mode):
     elif code == 3:
         nbytes = lib.lsh_lif_scan_lookback_bwd_workspace(T, N)
         ws = _n.workspace(nbytes, I.device)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(lib.lsh_lif_param_bwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS), _n.ptr(Lam), _n.ptr(parts), T, N,
             _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), code, C, _n.ptr(ws), nbytes,
@@ -91,7 +91,8 @@ class LIFParamFn(torch.autograd.Function):
             lam, sums = _param_backward(I, u0, U, S, gS.contiguous(), b, th, ur, alpha, bwd_mode)
         sums = sums.float()
         need = ctx.needs_input_grad  # a gradient only for the parameters given as tensors
-        return (lam, b * lam[0], sums[0] if need[2] else None, -sums[1] if need[3] else None,
+        du0 = b * lam[0] if ctx.needs_input_grad[1] else None
+        return (lam, du0, sums[0] if need[2] else None, -sums[1] if need[3] else None,
                 b * sums[2] if need[4] else None, None, None, None, None)
 
 
@@ -127,7 +128,8 @@ class LIFSoftFn(torch.autograd.Function):
         b, th, alpha = ctx.cfg
         need_b = ctx.needs_input_grad[2]
         lam, db = TS._soft_backward(I, u0, U, gS.contiguous(), b, th, alpha, need_b)
-        return lam, b * lam[0], (db.float().reshape(()) if need_b else None), None, None
+        du0 = b * lam[0] if ctx.needs_input_grad[1] else None
+        return lam, du0, (db.float().reshape(()) if need_b else None), None, None
 
 
 def lif_soft(I, u0, beta, theta=1.0, alpha=4.0):
@@ -161,7 +163,8 @@ class LIFSoftScanFn(torch.autograd.Function):
         b, th, alpha = ctx.cfg
         need_b = ctx.needs_input_grad[2]
         lam, db = TS._soft_backward(I, u0, U, gS.contiguous(), b, th, alpha, need_b)
-        return (lam, b * lam[0], (db.float().reshape(()) if need_b else None), None, None, None, None,
+        du0 = b * lam[0] if ctx.needs_input_grad[1] else None
+        return (lam, du0, (db.float().reshape(()) if need_b else None), None, None, None, None,
                 None)
 
 

@@ -32,7 +32,7 @@ def aff_serial_forward(I, beta, theta, gamma, delta, u0, BN=32):
     if I.numel() == 0:
         _gamma(_f32(gamma))
         return U, S
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(_n.lib().lsh_aff_serial_fwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N, _f32(beta), _f32(theta),
             _gamma(_f32(gamma)), _f32(delta), _n.stream_of(I)), "lsh_aff_serial_fwd")
@@ -91,7 +91,7 @@ def aff_scan_forward(I, beta, theta, gamma, delta, u0, C=128, K=32, BN=16, BNc=1
     ws = _n.workspace(nbytes, I.device)
     U, S = torch.empty_like(I), torch.empty_like(I)
     r_theta = g * th + d  # in double from the Python floats, as the reference (:171)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(lib.lsh_aff_scan_fwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N, b, th, g, d, r_theta, C, K,
             int(repair), _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_aff_scan_fwd")
@@ -110,7 +110,7 @@ def reverse_affine_scan(a, b):
     b = _same(b, a, "b")
     T, N = a.shape
     out = torch.empty_like(a)
-    with torch.cuda.device(a.device):
+    with _n.on_device(a):
         _n.check(_n.lib().lsh_reverse_affine_scan(_n.ptr(a), _n.ptr(b), _n.ptr(out), T, N,
                                                   _n.stream_of(a)), "lsh_reverse_affine_scan")
     return out
@@ -156,7 +156,7 @@ def _aff_backward(I, u0, U, S, GS, beta, theta, gamma, alpha, mode="auto", C=Non
     elif code == 3:
         nbytes = lib.lsh_lif_scan_lookback_bwd_workspace(T, N)
         ws = _n.workspace(nbytes, I.device)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(lib.lsh_aff_bwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS), _n.ptr(Lam), _n.ptr(parts), T, N,
             _f32(beta), _f32(theta), _gamma(_f32(gamma)), _f32(alpha), code, C, _n.ptr(ws), nbytes,

@@ -43,7 +43,7 @@ def alif_serial_forward(I, beta, rho, q, theta0, u_r, u0, w0, BN=32, D=0, num_wa
     u0 = _vec(u0, N, I)
     w0 = _vec(w0, N, I, "w0")
     U, W, S = torch.empty_like(I), torch.empty_like(I), torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(_n.lib().lsh_alif_serial_fwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(U), _n.ptr(W), _n.ptr(S), T, N, _f32(beta),
             _f32(rho), _f32(q), _f32(theta0), _f32(u_r), _n.stream_of(I)), "lsh_alif_serial_fwd")
@@ -69,7 +69,7 @@ def _alif_serial_forward_dp(I, dp, u_r, u0, w0):
     u0 = _vec(u0, N, I)
     w0 = _vec(w0, N, I, "w0")
     U, W, S = torch.empty_like(I), torch.empty_like(I), torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(_n.lib().lsh_alif_serial_fwd_dparams(
             _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(U), _n.ptr(W), _n.ptr(S), T, N, _n.ptr(dp),
             _f32(u_r), _n.stream_of(I)), "lsh_alif_serial_fwd_dparams")
@@ -92,7 +92,7 @@ def alif_warm_predict(I, beta, rho, q, theta0, u_r, u0, w0, C, Wn=4, u_init=0.0,
         if UI.shape != (M, N) or WI.shape != (M, N):
             raise ValueError(f"UI, WI must be [{M}, {N}]")
     WP = torch.empty(M, N, device=I.device, dtype=torch.float32)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(_n.lib().lsh_alif_warm_predict(
             _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(UI), _n.ptr(WI), _n.ptr(WP), T, N, int(C),
             int(Wn), float(u_init), float(w_init), _f32(beta), _f32(rho), _f32(q), _f32(theta0),
@@ -182,7 +182,7 @@ def alif_scan_forward(I, beta, rho, q, theta0, u_r, u0, w0, Wpred, dw, C=128, K1
         for e in evs:
             e.record()  # creates the underlying HIP event
         ev_arr = (_n.c_p * 5)(*[e.cuda_event for e in evs])
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(L.lsh_alif_scan_fwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(Wp), _f32(dw), _n.ptr(U), _n.ptr(W), _n.ptr(S),
             T, N, _f32(beta), _f32(rho), _f32(q), _f32(theta0), _f32(u_r), _rho_pow_c(rho, C), C, K1,
@@ -278,7 +278,7 @@ def _alif_bwd_call(I, U, W, S, GS, beta, rho, q, theta0, u0, w0, alpha, mode, C,
     elif code == 3:
         nbytes = L.lsh_alif_bwd_lookback_workspace(T, N)
         ws = _n.workspace(nbytes, I.device)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         if rc:
             p = (0.0,) * 4 if dp is not None else (beta, rho, q, theta0)
             _n.check(L.lsh_alif_bwd_recompute(
@@ -373,7 +373,7 @@ class ALIFFn(torch.autograd.Function):
             sums = sums.float()
             db, dr, dq = (sums[k] if need[3 + k] else None for k in range(3))
             dth = -sums[3] if need[6] else None
-        du0 = (dp[0] if dp is not None else b) * LV[0]
+        du0 = (dp[0] if dp is not None else b) * LV[0] if need[1] else None
         return (LV, du0, DW0.reshape(w0.shape) if w0.dim() else DW0, db, dr, dq, dth,
                 None, None, None, None, None, None, None, None)
 

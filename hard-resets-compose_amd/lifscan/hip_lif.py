@@ -69,6 +69,9 @@ def _input(I):
 def _vec(v, N, like, name="u0"):
     if not torch.is_tensor(v):
         v = torch.full((N,), float(v), device=like.device, dtype=torch.float32)
+    elif (v.dim() == 1 and v.shape[0] == N and v.dtype == torch.float32 and v.device == like.device
+          and v.is_contiguous()):
+        return v  # already the [N] fp32 vector the kernels read (only its pointer is passed)
     v = v.detach()
     if v.numel() != N:
         raise ValueError(f"{name} must have N={N} elements")
@@ -107,7 +110,7 @@ def serial_forward(I, beta, theta, u_r, u0, BN=BN_DEFAULT):
     u0 = _vec(u0, N, I)
     U = torch.empty_like(I)
     S = torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(_n.lib().lsh_lif_serial_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
                                              _f32(beta), _f32(theta), _f32(u_r), _n.stream_of(I)),
                  "lsh_lif_serial_fwd")
@@ -139,7 +142,7 @@ def serial_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=Tru
     U, S, GS = _same(U, I, "U"), _same(S, I, "S"), _same(GS, I, "GS")
     GU = _same(GU, I, "GU")
     Lam = torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(_n.lib().lsh_lif_serial_bwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS), _n.ptr(GU), _n.ptr(Lam), T, N,
             _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), int(bool(detach)), _n.stream_of(I)),
@@ -239,7 +242,7 @@ def _scan2(I, beta, theta, u_r, u0, C, K, repair, stats, lo=None):
     ws = _n.workspace(nbytes, I.device)
     U = torch.empty_like(I)
     S = torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         st = _n.stream_of(I)
         if lo is None:
             rc = L.lsh_lif_scan_v3_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
@@ -395,7 +398,7 @@ def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=
     ws = _n.workspace(nbytes, I.device)
     U = torch.empty_like(I)
     S = torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(L.lsh_lif_scan_v4_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
                                        _f32(beta), _f32(theta), _f32(u_r), C, G, K, K2,
                                        int(repair), _n.ptr(ws), nbytes, _n.stream_of(I)),
@@ -455,7 +458,7 @@ def scan_forward_exact(I, beta, theta, u_r, u0, C=None, K=8, maps="auto"):
     ws = _n.workspace(nbytes, I.device)
     U = torch.empty_like(I)
     S = torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         st = _n.stream_of(I)
         if maps:
             rc = L.lsh_lif_scan_exact_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
@@ -487,7 +490,7 @@ def scan_backward_fused(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach
     if C not in (16, 32, 64) or T % C:
         raise ValueError(f"single-pass backward needs C in (16, 32, 64) dividing T={T}")
     Lam = torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(_n.lib().lsh_lif_scan_fused_bwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS), _n.ptr(GU), _n.ptr(Lam), T, N,
             _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), int(bool(detach)), C, _n.stream_of(I)),
@@ -512,15 +515,12 @@ def scan_forward_exact_starts(I, beta, theta, u_r, u0, C=None):
     C = int(C or FUSED_FWD_C)
     if C not in (16, 32, 64) or T % C:
         raise ValueError(f"the starts-only forward needs C in (16, 32, 64) dividing T={T}")
-    L = _n.lib()
-    nbytes = L.lsh_lif_scan_exact_workspace()
-    ws = _n.workspace(nbytes, I.device)
     S = torch.empty_like(I)
     ST = torch.empty(T // C, N, device=I.device, dtype=torch.float32)
-    with torch.cuda.device(I.device):
-        _n.check(L.lsh_lif_scan_exact_fwd_starts(
+    with _n.on_device(I):  # no workspace: the counters are not read here
+        _n.check(_n.lib().lsh_lif_scan_exact_fwd_starts(
             _n.ptr(I), _n.ptr(u0), _n.ptr(ST), _n.ptr(S), T, N, _f32(beta), _f32(theta), _f32(u_r), C,
-            _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_lif_scan_exact_fwd_starts")
+            None, 0, _n.stream_of(I)), "lsh_lif_scan_exact_fwd_starts")
     return S, ST
 
 
@@ -539,7 +539,7 @@ def scan_backward_fused_starts(I, STARTS, GS, beta, theta, u_r, alpha=4.0, want_
     parts = None
     if want_sums:
         parts = torch.zeros((N + 63) // 64, 3, device=I.device, dtype=torch.float64)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(_n.lib().lsh_lif_scan_fused_bwd_starts(
             _n.ptr(I), _n.ptr(STARTS), _n.ptr(GS), _n.ptr(Lam), _n.ptr(parts), T, N,
             _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), C, _n.stream_of(I)),
@@ -600,7 +600,7 @@ def scan_backward_lookback(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, det
         raise ValueError(f"look-back adjoint needs T % {LOOKBACK_SEG} == 0 (T={T})")
     ws = _n.workspace(nbytes, I.device)
     Lam = torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(L.lsh_lif_scan_lookback_bwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS), _n.ptr(GU), _n.ptr(Lam), T, N,
             _f32(beta), _f32(theta), _f32(u_r), _f32(alpha), int(bool(detach)), int(C), _n.ptr(ws),
@@ -649,7 +649,7 @@ def scan_backward_chunked(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, deta
     nbytes = L.lsh_lif_scan_bwd_workspace(T, N, C)
     ws = _n.workspace(nbytes, I.device)
     Lam = torch.empty_like(I)
-    with torch.cuda.device(I.device):
+    with _n.on_device(I):
         _n.check(L.lsh_lif_scan_bwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), _n.ptr(GS),
                                     _n.ptr(GU), _n.ptr(Lam), T, N, _f32(beta), _f32(theta),
                                     _f32(u_r), _f32(alpha), int(bool(detach)), C, _n.ptr(ws),
@@ -726,7 +726,8 @@ class LIFFunction(torch.autograd.Function):
             Lam = serial_backward(I, u0, U, S, gS, None, b, theta, u_r, alpha)
         else:
             Lam = scan_backward(I, u0, U, S, gS, None, b, theta, u_r, alpha, C=C)
-        return (Lam, b * Lam[0], _beta_grad(Lam, U, u0, ctx.needs_input_grad[2]),
+        du0 = b * Lam[0] if ctx.needs_input_grad[1] else None
+        return (Lam, du0, _beta_grad(Lam, U, u0, ctx.needs_input_grad[2]),
                 None, None, None, None, None, None, None)
 
 
@@ -769,13 +770,15 @@ class LIFTuned(torch.autograd.Function):
             need_b = ctx.needs_input_grad[2]
             Lam, sums = scan_backward_fused_starts(I, ST, gS, b, theta, u_r, alpha, need_b)
             db = sums[0].float().reshape(()) if need_b else None
-            return (Lam, b * Lam[0], db, None, None, None, None, None, None)
+            du0 = b * Lam[0] if ctx.needs_input_grad[1] else None
+            return (Lam, du0, db, None, None, None, None, None, None)
         I, u0, U, S = ctx.saved_tensors
         if mode == "serial":
             Lam = serial_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
         else:
             Lam = scan_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
-        return (Lam, b * Lam[0], _beta_grad(Lam, U, u0, ctx.needs_input_grad[2]),
+        du0 = b * Lam[0] if ctx.needs_input_grad[1] else None
+        return (Lam, du0, _beta_grad(Lam, U, u0, ctx.needs_input_grad[2]),
                 None, None, None, None, None, None)
 
 
@@ -817,13 +820,15 @@ class LIFAuto(torch.autograd.Function):
             need_b = ctx.needs_input_grad[2]
             Lam, sums = scan_backward_fused_starts(I, ST, gS, b, theta, u_r, alpha, need_b)
             db = sums[0].float().reshape(()) if need_b else None
-            return (Lam, b * Lam[0], db, None, None, None, None, None, None, None)
+            du0 = b * Lam[0] if ctx.needs_input_grad[1] else None
+            return (Lam, du0, db, None, None, None, None, None, None, None)
         I, u0, U, S = ctx.saved_tensors
         if bwd_mode == "scan":
             Lam = scan_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
         else:
             Lam = serial_backward_auto(I, u0, U, S, gS, None, b, theta, u_r, alpha)
-        return (Lam, b * Lam[0], _beta_grad(Lam, U, u0, ctx.needs_input_grad[2]),
+        du0 = b * Lam[0] if ctx.needs_input_grad[1] else None
+        return (Lam, du0, _beta_grad(Lam, U, u0, ctx.needs_input_grad[2]),
                 None, None, None, None, None, None, None)
 
 

@@ -80,7 +80,7 @@ def _soft_call(I, u0, U, V, GS, beta, theta, alpha, want_dbeta):
     if want_dbeta:
         parts = torch.zeros(max(lib.lsh_soft_bwd_partials(T, N, C), 1), dtype=torch.float64,
                             device=like.device)
-    with torch.cuda.device(like.device):
+    with _n.on_device(like):
         _n.check(lib.lsh_soft_bwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(V), _n.ptr(GS), _n.ptr(Lam), _n.ptr(parts), T, N,
             float(beta), _f32(theta), _f32(alpha), C, _n.ptr(ws), nbytes, _n.stream_of(like)),

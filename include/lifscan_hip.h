@@ -181,7 +181,8 @@ int lsh_lif_scan_fused_bwd(const float* I, const float* u0, const float* U, cons
  * u_{t-1} and s_t are the forward's bits and Lam is the same as lsh_lif_scan_fused_bwd's with
  * the reset detached and no GU.  HBM traffic: forward 8 B, adjoint 12 B per neuron-step
  * (instead of 12 + 20).  C in {16, 32, 64}, the same C for both, T % C == 0; the forward is the
- * single-pass exact forward without maps (workspace lsh_lif_scan_exact_workspace()).
+ * single-pass exact forward without maps (workspace lsh_lif_scan_exact_workspace(), or NULL
+ * with ws_bytes 0: then its counters are not kept and no reset kernel precedes it).
  * partials: NULL, or [ceil(N/64)] rows of 3 doubles as lsh_lif_param_bwd mode 2 (sum of
  * lam_t*u_{t-1}, gs_t*sg_t, s_t*lam_{t+1}). */
 int lsh_lif_scan_exact_fwd_starts(const float* I, const float* u0, float* STARTS, float* S,

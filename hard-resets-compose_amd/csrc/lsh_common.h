@@ -79,13 +79,20 @@ __device__ __forceinline__ void st_row_nt(float* __restrict__ row, unsigned boff
 // per time row.  The unrolled time loops then need no per-access address registers.
 // Descriptor word 3 (0x00020000) is the gfx9-family raw-buffer format (32-bit data).  The
 // record count is left at its maximum: callers keep every access in bounds themselves.
+// Cache policy of the streaming row loads: 2 = nt (non-temporal, the streaming hint; the rows
+// are read once per pass).  Measured at cfg2: adjoint 0.622 -> 0.606-0.612 ms, forward ~1.5%
+// faster than with the default policy 0, same bits.
+#ifndef LSH_LD_POLICY
+#define LSH_LD_POLICY 2
+#endif
+
 struct Buf {
   __amdgpu_buffer_rsrc_t r;
   __device__ __forceinline__ explicit Buf(const void* base)
       : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)0xffffffff,
                                             0x00020000)) {}
   __device__ __forceinline__ float ld(unsigned voff, unsigned soff) const {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, LSH_LD_POLICY));
   }
   // non-temporal store (cache policy bit 1 = nt on gfx94x/gfx950)
   __device__ __forceinline__ void st_nt(unsigned voff, unsigned soff, float v) const {

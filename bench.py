@@ -234,6 +234,7 @@ def bench_cfg4(torch, dev, reps):
     U3, S3 = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=256, K=16, repair=10 ** 6)
     out["v3_converged_equals_serial"] = exact(U3, S3)
     out["v3_converged_chunk"] = L.last_scan_run().C
+    out["v3_converged_pieces"] = L.last_scan_run().pieces
     del U3, S3
     out["fwd_v3_converged_ms"] = ev_time(lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=256, K=16,
                                                                    repair=10 ** 6), reps)

@@ -5,6 +5,8 @@
 // t*N + n).  One lane owns one neuron; a wave64 covers 64 consecutive neurons,
 // so every time row is one contiguous 256-byte access per wave.  Per-chunk
 // arrays are [M, N] and map slots [M, K, N] (neuron-contiguous, coalesced).
+#include <mutex>
+
 #include "lsh_abi.h"
 #include "lsh_common.h"
 
@@ -777,14 +779,14 @@ static void launch_build(const float* I, const float* u0, char* ws, const lsh_v3
                        F(L.MC), N, C, NB, K, beta, theta, u_r);
 }
 
+// The carry over the M chunk maps from u0 (the envelope seed and the first start).
 template <int KMAX>
-static void launch_build_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
-                               const lsh_v3_layout& L, int64_t N, int M, int C, int K, float beta,
-                               float theta, float u_r, hipStream_t st) {
+static void launch_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
+                         const lsh_v3_layout& L, int64_t N, int M, int C, int K, float beta,
+                         float theta, float u_r, hipStream_t st) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(ws + off); };
-  launch_build<KMAX>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
   if (M >= 4 * CarryStage<KMAX>::R && KMAX <= 32) {
     // long chunk sequences: map reads staged through LDS by three loader waves
     hipLaunchKernelGGL((k_lif_carry_staged<KMAX>), dim3((unsigned)NB), dim3(256), 0, st, I, u0,
@@ -797,6 +799,38 @@ static void launch_build_carry(const float* I, const float* u0, const float* lo_
                      F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX), F(L.MC),
                      lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS),
                      reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r);
+}
+
+template <int KMAX>
+static void launch_build_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
+                               const lsh_v3_layout& L, int64_t N, int M, int C, int K, float beta,
+                               float theta, float u_r, hipStream_t st) {
+  launch_build<KMAX>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
+  launch_carry<KMAX>(I, u0, lo_neuron, ws, L, N, M, C, K, beta, theta, u_r, st);
+}
+
+static void lif_carry_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L,
+                             int64_t N, int M, int C, int K, float beta, float theta, float u_r,
+                             hipStream_t st) {
+  if (K <= 4) launch_carry<4>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
+  else if (K <= 8) launch_carry<8>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
+  else if (K <= 16) launch_carry<16>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
+  else if (K <= 32) launch_carry<32>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
+  else launch_carry<64>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
+}
+
+// One non-blocking side stream per device (default priority), created on first use on the
+// current device and kept until the process ends.
+static hipStream_t side_stream() {
+  static std::mutex mu;
+  static hipStream_t streams[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (streams[dev] == nullptr &&
+      hipStreamCreateWithFlags(&streams[dev], hipStreamNonBlocking) != hipSuccess)
+    streams[dev] = nullptr;
+  return streams[dev];
 }
 
 // Build kernel alone (used by the three-level scan).
@@ -940,6 +974,89 @@ extern "C" int lsh_lif_scan_v3_fwd(const float* I, const float* u0, float* U, fl
                                    int64_t repair, void* ws, size_t ws_bytes, void* stream) {
   return scan2_fwd(I, u0, nullptr, U, S, T, N, beta, theta, u_r, C, K, repair, ws, ws_bytes,
                    stream);
+}
+
+// The converged two-level scan in P pieces of T/P steps (consecutive chunks).  Piece p's maps
+// depend only on its rows of I and on the pruning bound max(u0, theta, u_r), which bounds every
+// state of every piece (after one step a state is below theta or equal to u_r), so they are
+// the maps of the unsplit scan; the builds run back to back on a side stream.  On the caller's
+// stream, piece p waits for its build, then carries, replays and repairs to convergence from
+// the last row of U of piece p-1 (u0 for piece 0): each piece is the serial recurrence from
+// an exact start, so U and S are the serial recurrence.  The memory-bound replays overlap the
+// VALU-bound builds of the later pieces.
+static constexpr int kMaxPieces = 64;
+
+static int pieces_check(int64_t T, int64_t N, int C, int K, int P, lsh_v3_layout* L,
+                        size_t* piece_bytes) {
+  if (P < 1 || P > kMaxPieces || C < 1) return LSH_ERR_SHAPE;
+  if (T % ((int64_t)C * P) != 0) return LSH_ERR_DIVISIBILITY;
+  const int rc = v3_check(T / P, N, C, K);
+  if (rc != LSH_OK) return rc;
+  v3_layout_fill(T / P, N, C, K, L);
+  *piece_bytes = align_up(L->total, 256);
+  return LSH_OK;
+}
+
+extern "C" size_t lsh_lif_scan_v3_pieces_workspace(int64_t T, int64_t N, int C, int K, int P) {
+  lsh_v3_layout L;
+  size_t pb = 0;
+  if (pieces_check(T, N, C, K, P, &L, &pb) != LSH_OK) return 0;
+  return (size_t)P * pb;
+}
+
+extern "C" int lsh_lif_scan_v3_pieces_fwd(const float* I, const float* u0, float* U, float* S,
+                                          int64_t T, int64_t N, float beta, float theta,
+                                          float u_r, int C, int K, int P, void* ws,
+                                          size_t ws_bytes, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
+  lsh_v3_layout L;
+  size_t pb = 0;
+  const int rc = pieces_check(T, N, C, K, P, &L, &pb);
+  if (rc != LSH_OK) return rc;
+  if (ws_bytes < (size_t)P * pb || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0)
+    return LSH_ERR_WORKSPACE;
+  if (T == 0 || N == 0) return LSH_OK;
+  hipStream_t st = (hipStream_t)stream;
+  hipStream_t side = st;  // the caller's stream may be the null stream (handle 0)
+  if (P > 1 && (side = side_stream()) == nullptr) return LSH_ERR_HIP;
+  char* w = static_cast<char*>(ws);
+  const int64_t Tp = T / P;
+  const int Mp = (int)(Tp / C);
+  hipEvent_t ev[kMaxPieces + 1];
+  int made = 0;
+  bool ok = true;
+  for (; made <= P && ok; ++made)
+    ok = hipEventCreateWithFlags(&ev[made], hipEventDisableTiming) == hipSuccess;
+  if (!ok) made -= 1;  // the failed create made no event
+  if (ok) {
+    // fork: the builds start after the work already queued on the caller's stream
+    ok = hipEventRecord(ev[P], st) == hipSuccess && hipStreamWaitEvent(side, ev[P], 0) == hipSuccess;
+    for (int p = 0; ok && p < P; ++p) {
+      char* wp = w + (size_t)p * pb;
+      hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, side,
+                         reinterpret_cast<WsHeader*>(wp));
+      lif_build_launch(I + (size_t)p * Tp * N, u0, wp, L, N, Mp, C, K, beta, theta, u_r, side);
+      ok = hipEventRecord(ev[p], side) == hipSuccess;
+    }
+    for (int p = 0; ok && p < P; ++p) {
+      ok = hipStreamWaitEvent(st, ev[p], 0) == hipSuccess;
+      if (!ok) break;
+      char* wp = w + (size_t)p * pb;
+      const size_t r0 = (size_t)p * Tp * N;
+      const float* up = p == 0 ? u0 : U + r0 - N;
+      lif_carry_launch(I + r0, up, wp, L, N, Mp, C, K, beta, theta, u_r, st);
+      lif_replay_repair_launch(I + r0, up, U + r0, S + r0, reinterpret_cast<float*>(wp + L.STARTS),
+                               reinterpret_cast<float*>(wp + L.ENDS),
+                               reinterpret_cast<int*>(wp + L.LIST0),
+                               reinterpret_cast<int*>(wp + L.LIST1),
+                               reinterpret_cast<WsHeader*>(wp), N, Mp, C, Mp, beta, theta, u_r, st);
+    }
+  }
+  // an event recorded but not yet reached is released once it completes
+  for (int i = 0; i < made; ++i) (void)hipEventDestroy(ev[i]);
+  if (!ok) return LSH_ERR_HIP;
+  LSH_CHECK_LAUNCH();
+  return LSH_OK;
 }
 
 extern "C" int lsh_lif_scan_lo_fwd(const float* I, const float* u0, const float* lo, float* U,

@@ -197,6 +197,8 @@ def state_bounds(I, beta, theta, u_r, u0):
 class _ScanRun:
     """Holds the workspace of one scan call (maps, starts, ends) for stats and tests."""
 
+    pieces = 1  # lsh_lif_scan_v3_pieces_fwd: the arrays are the first piece's (T = its steps)
+
     def __init__(self, ws, T, N, C, K):
         self.ws, self.T, self.N, self.C, self.K = ws, T, N, C, K
 
@@ -275,6 +277,9 @@ def scan_forward_v3(I, beta, theta, u_r, u0, C=64, K=16, BN=32, nw=1, BNc=16, nw
     if int(C) >= 1 and T % int(C) == 0 and _fused_fwd_ok(T, C, K, repair, stats):
         long_c = long_sequence_C(T, N)
         if long_c:  # few neurons, long T: the multi-kernel scan with long chunks is faster
+            C2, P = long_sequence_plan(T, N)
+            if P > 1:
+                return _scan2_pieces(I, beta, theta, u_r, u0, C2, LONG_K, P)
             return _scan2(I, beta, theta, u_r, u0, long_c, LONG_K, T // long_c, None)
         return scan_forward_exact(I, beta, theta, u_r, u0, K=K)
     return _scan2(I, beta, theta, u_r, u0, C, K, repair, stats)
@@ -301,6 +306,51 @@ def long_sequence_C(T, N):
         if T % c == 0 and (T // c) * nb >= 1024:
             return c
     return 0
+
+
+# The long-chunk path in pieces of consecutive chunks (lsh_lif_scan_v3_pieces_fwd): the
+# builds of later pieces run on a side stream while earlier pieces carry and replay.  Each
+# piece costs at least one chunk's serial replay, so it pays only on large work: measured on
+# MI355X, N = 1024, T = 2^20: unsplit (C 4096) 8.15 ms, C 4096 in 2 pieces 7.33, C 2048 in 4
+# pieces 7.13, C 1024 in 8 pieces 8.43; at 2^27-2^28 neuron-steps (N = 256, T = 2^18; N = 512,
+# T = 2^19; N = 1024, T = 2^18) every split was slower than or within 4 % of the unsplit scan.
+LONG_PIECES = 4
+LONG_PIECES_MIN_WORK = 2 ** 30  # neuron-steps
+
+
+def long_sequence_plan(T, N):
+    """(C, P) of the converged long-chunk forward: the chunk and pieces, (long_sequence_C, 1)
+    below LONG_PIECES_MIN_WORK neuron-steps, else half that chunk in LONG_PIECES pieces; C is 0
+    when the single pass is used."""
+    C = long_sequence_C(T, N)
+    if C and T * N >= LONG_PIECES_MIN_WORK and T % (C // 2 * LONG_PIECES) == 0:
+        return C // 2, LONG_PIECES
+    return C, 1
+
+
+def _scan2_pieces(I, beta, theta, u_r, u0, C, K, P):
+    """The converged two-level scan in P pieces -> (U, S), the serial recurrence."""
+    global _LAST_RUN
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    C, K, P = int(C), int(K), int(P)
+    if C < 1 or P < 1 or T % (C * P):
+        raise ValueError(f"T={T} must be divisible by C*P={C * P}")
+    L = _n.lib()
+    nbytes = L.lsh_lif_scan_v3_pieces_workspace(T, N, C, K, P)
+    if nbytes == 0:
+        raise ValueError(f"unsupported scan shape T={T} N={N} C={C} K={K} P={P}")
+    ws = _n.workspace(nbytes, I.device)
+    U = torch.empty_like(I)
+    S = torch.empty_like(I)
+    with _n.on_device(I):
+        _n.check(L.lsh_lif_scan_v3_pieces_fwd(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N, _f32(beta), _f32(theta), _f32(u_r),
+            C, K, P, _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_lif_scan_v3_pieces_fwd")
+    _LAST_RUN = _ScanRun(ws, T // P, N, C, K)  # the first piece's arrays
+    _LAST_RUN.pieces = P
+    return U, S
 
 
 def scan_forward(I, beta, theta, u_r, u0, C=64, K=16, BN=BN_DEFAULT, repair=0, stats=None):

@@ -74,6 +74,21 @@ int lsh_lif_scan_v3_fwd(const float* I, const float* u0, float* U, float* S, int
                         float beta, float theta, float u_r, int C, int K, int64_t repair,
                         void* ws, size_t ws_bytes, void* stream);
 
+/* The converged lsh_lif_scan_v3_fwd (repair to convergence, no statistics) in P pieces of T/P
+ * steps: the chunk maps of every piece are built on a side stream (one non-blocking stream per
+ * device at the default priority, created on first use and kept), while the caller's stream
+ * carries, replays and repairs piece after piece, each from the last row of U of the one before
+ * (u0 for the first).  U and S are the serial recurrence, as lsh_lif_scan_v3_fwd's converged
+ * result; the memory-bound replays overlap the builds of later pieces.  The path of
+ * scan_forward_v3 (triton_lif.py:782-817) for few neurons and long T.  Requires
+ * T % (C*P) == 0, 1 <= P <= 64; workspace: P pieces of the v3 layout of (T/P, N, C, K), each
+ * 256-byte aligned.  Ordering with the caller's stream is by events; concurrent calls from
+ * several host threads on one device share the side stream (correct, serialised builds). */
+size_t lsh_lif_scan_v3_pieces_workspace(int64_t T, int64_t N, int C, int K, int P);
+int lsh_lif_scan_v3_pieces_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
+                               int64_t N, float beta, float theta, float u_r, int C, int K, int P,
+                               void* ws, size_t ws_bytes, void* stream);
+
 /* Two-level scan pruned with one caller-given lower bound per neuron (lo[N], e.g. the loose
  * state_bounds of triton_lif.py:238-243) instead of the per-chunk envelope.  Replaces
  * triton_lif.py:262-295 (scan_forward), :479-509 (scan_forward_tiled) and :609-642

@@ -142,6 +142,43 @@ def test_converged_v3_long_sequence_path(L, dev):
     assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
 
 
+def test_converged_v3_pieces_path_cfg4(L, dev):
+    """At cfg4's size (N = 1024, T = 2^20, beta = 0.99) the converged scan_forward_v3 takes the
+    long-chunk scan in pieces (C = 2048, 4 pieces) and returns the serial forward bit for bit
+    (the serial forward is pinned to the oracle by test_serial_forward_bitexact)."""
+    from lifscan import hip_lif as H
+    T, N, beta = 2 ** 20, 1024, 0.99
+    assert H.long_sequence_plan(T, N) == (2048, 4)
+    g = torch.Generator(device=dev).manual_seed(41)
+    I = torch.randn(T, N, device=dev, generator=g).mul_(0.08).add_(0.012)
+    u0 = torch.rand(N, device=dev, generator=g)
+    print("v3 pieces at cfg4", flush=True)
+    U, S = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=256, K=16, repair=10 ** 6)
+    assert H.last_scan_run().pieces == 4 and H.last_scan_run().C == 2048
+    Us, Ss = H.serial_forward(I, beta, 1.0, 0.0, u0)
+    assert torch.equal(U, Us) and torch.equal(S, Ss)
+    del I, U, S, Us, Ss
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("K", [4, 32])
+@pytest.mark.parametrize("P", [1, 2, 3, 4, 8])
+def test_scan_v3_pieces_equals_serial(L, dev, P, K):
+    """The converged two-level scan in P pieces (maps built on a side stream, each piece
+    carried and repaired from the previous piece's last row of U) is the serial recurrence bit
+    for bit, with overflowing maps (K = 4 at beta = 0.99) and a reset value below zero."""
+    T, N, C, beta, u_r = 24576, 300, 256, 0.99, -0.1
+    I = normal(T, N, 0.012, 0.08, 31)
+    u0 = uniform(N, 0.0, 1.0, 32)
+    from lifscan import hip_lif as H
+    print(f"v3 pieces P={P} K={K}", flush=True)
+    U, S = H._scan2_pieces(gpu(I, dev), beta, 1.0, u_r, gpu(u0, dev), C, K, P)
+    Us, Ss = O.serial_forward(I, beta, 1.0, u_r, u0)
+    assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+    with pytest.raises(ValueError):
+        H._scan2_pieces(gpu(I, dev), beta, 1.0, u_r, gpu(u0, dev), C, K, 7)  # 96 chunks
+
+
 @pytest.mark.parametrize("R", [1, 2, 3])
 def test_scan_v3_finite_repair_rounds(L, dev, R):
     T, N, C = 2048, 300, 64

@@ -38,3 +38,15 @@ def test_alif_scan_adjoint_dispatch():
     assert H._bwd_mode("serial", 4096, 16, 64) == (0, 64)
     with pytest.raises(ValueError):
         H._bwd_mode("chunked", 100, 8, 64)
+
+
+def test_long_sequence_plan():
+    """The converged long-chunk forward: unsplit below 2^30 neuron-steps, else half the long
+    chunk in LONG_PIECES pieces (the measured optimum at N = 1024, T = 2^20)."""
+    from lifscan import hip_lif as L
+    assert L.long_sequence_C(2 ** 20, 1024) == 4096
+    assert L.long_sequence_plan(2 ** 20, 1024) == (2048, L.LONG_PIECES)
+    assert L.long_sequence_plan(2 ** 18, 1024) == (4096, 1)
+    assert L.long_sequence_plan(2 ** 19, 512) == (4096, 1)
+    assert L.long_sequence_plan(65536, 1000) == (1024, 1)
+    assert L.long_sequence_plan(4096, 65536) == (0, 1)             # single pass

@@ -800,7 +800,10 @@ constexpr int ALIF_PIPE_P = 15;
 // Serial ALIF forward from (u0, w0) with the same wave roles (triton_alif.py:35-42,
 // :263-273): the consumer runs alif_step through LDS, the producers stage I one tile ahead and
 // store U, W, S of the tile finished one round earlier; bit-identical to k_alif_fwd.
-constexpr int ALIF_FPIPE_D = 64;
+#ifndef LSH_ALIF_FPIPE_D
+#define LSH_ALIF_FPIPE_D 64  // rows per tile (LDS: 2 x D x 64 x (4 + 16) B)
+#endif
+constexpr int ALIF_FPIPE_D = LSH_ALIF_FPIPE_D;
 
 __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,

@@ -798,10 +798,13 @@ constexpr int ALIF_PIPE_D = 32;
 constexpr int ALIF_PIPE_P = 15;
 
 // Serial ALIF forward from (u0, w0) with the same wave roles (triton_alif.py:35-42,
-// :263-273): the consumer runs alif_step through LDS, the producers stage I one tile ahead and
-// store U, W, S of the tile finished one round earlier; bit-identical to k_alif_fwd.
+// :263-273): the consumer runs alif_step through LDS and writes (u, w) per step and each tile's
+// entry state; the producers stage I one tile ahead and store U, W, S of the tile finished one
+// round earlier, recomputing s_t = (fl(fl(beta*u_{t-1}) + x_t) >= theta0 + w_{t-1}) with the
+// consumer's own operations from the rows they loaded (kept two rounds in registers), so the
+// consumer's chain carries no spike-to-float select; bit-identical to k_alif_fwd.
 #ifndef LSH_ALIF_FPIPE_D
-#define LSH_ALIF_FPIPE_D 64  // rows per tile (LDS: 2 x D x 64 x (4 + 16) B)
+#define LSH_ALIF_FPIPE_D 64  // rows per tile (LDS: 2 x D x 64 x (4 + 8) B)
 #endif
 constexpr int ALIF_FPIPE_D = LSH_ALIF_FPIPE_D;
 
@@ -812,7 +815,8 @@ __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
   if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
   constexpr int D = ALIF_FPIPE_D, P = ALIF_PIPE_P, R = (D + P - 1) / P;
   __shared__ float sX[2][D][WAVE];
-  __shared__ float4 sUWS[2][D][WAVE];
+  __shared__ float2 sUW[2][D][WAVE];
+  __shared__ float2 sEntry[2][WAVE];  // (u, w) before row 0 of the tile in the same buffer
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const unsigned lane = threadIdx.x % WAVE;
   const int64_t nb0 = (int64_t)blockIdx.x * WAVE;
@@ -829,10 +833,11 @@ __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
       if (k >= 1 && k <= ntiles) {
         const int buf = (int)((k - 1) & 1);
         const int nr = rows(k - 1);
+        sEntry[buf][lane] = make_float2(u, ww);
         auto step = [&](int j, float x) {
           bool sp;
           u = alif_step(u, ww, x, beta, rho, q, theta0, u_r, sp);
-          sUWS[buf][j][lane] = make_float4(u, ww, sp ? 1.0f : 0.0f, 0.0f);
+          sUW[buf][j][lane] = make_float2(u, ww);
         };
         if (nr == D) {
 #pragma unroll
@@ -853,7 +858,11 @@ __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
   }
 
   const int p = w - 1;
-  float xr[R];
+  // xr: the rows of the tile being loaded; at the start of round k, x1 and x2 hold this
+  // producer's rows of tiles k - 1 and k - 2
+  float xr[R], x1[R], x2[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) xr[r] = x1[r] = x2[r] = 0.0f;
   auto load = [&](int64_t k) {
     const int nr = rows(k);
 #pragma unroll
@@ -864,6 +873,9 @@ __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
   };
   if (ntiles > 0) load(0);
   for (int64_t k = 0; k <= ntiles + 1; ++k) {
+    float xk[R];  // this producer's rows of tile k
+#pragma unroll
+    for (int r = 0; r < R; ++r) xk[r] = xr[r];
     if (k < ntiles) {
       const int buf = (int)(k & 1);
       const int nr = rows(k);
@@ -882,12 +894,19 @@ __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
         const int j = p + r * P;
         if (j < nr) {
           const size_t row = (size_t)((k - 2) * D + j) * (size_t)N + (size_t)nb0;
-          const float4 o = sUWS[buf][j][lane];
+          const float2 o = sUW[buf][j][lane];
+          const float2 pr = j == 0 ? sEntry[buf][lane] : sUW[buf][j - 1][lane];
+          const bool sp = lif_v(pr.x, x2[r], beta) >= theta0 + pr.y;
           st_row_nt(U + row, sb, o.x);
           st_row_nt(W + row, sb, o.y);
-          st_row_nt(S + row, sb, o.z);
+          st_row_nt(S + row, sb, sp ? 1.0f : 0.0f);
         }
       }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      x2[r] = x1[r];
+      x1[r] = xk[r];
     }
     __syncthreads();
   }

@@ -154,30 +154,37 @@ __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_lif_bwd_pipe(
 
 // The two serial forwards' steps: hard reset (triton_lif.py:21-25) and affine reset
 // (triton_affine.py:20-24), with the one-wave kernels' arithmetic (lif_step, aff_step).
+// spike(u, x): the step's threshold decision from the state before it, with the step's own
+// operations (the producers recompute S with it).
 struct LifStep {
   float beta, theta, u_r;
   __device__ __forceinline__ float operator()(float u, float x, bool& s) const {
     return lif_step(u, x, beta, theta, u_r, s);
   }
+  __device__ __forceinline__ bool spike(float u, float x) const { return lif_v(u, x, beta) >= theta; }
 };
 struct AffStep {
   float beta, theta, gamma, delta;
   __device__ __forceinline__ float operator()(float u, float x, bool& s) const {
     return aff_step(u, x, beta, theta, gamma, delta, s);
   }
+  __device__ __forceinline__ bool spike(float u, float x) const { return lif_v(u, x, beta) >= theta; }
 };
 
 // Serial forward from u0 (triton_lif.py:30-39 serial_fwd_kernel, :460-466
 // serial_forward_tiled; triton_affine.py:143-162): tiles in time order; the consumer runs the
-// step, the producers stage I into LDS one tile ahead and store U, S of the tile finished one
-// round earlier.
+// step and writes u per step (and each tile's entry state), the producers stage I into LDS one
+// tile ahead and store U, S of the tile finished one round earlier, recomputing each spike
+// from the state before it and their own loaded rows (kept two rounds in registers) with the
+// step's operations, so the consumer's chain carries no spike-to-float select.
 template <class Step>
 __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_serial_fwd_pipe(
     const float* __restrict__ I, const float* __restrict__ u0, float* __restrict__ U,
     float* __restrict__ S, int64_t N, int64_t T, Step step) {
   constexpr int D = PIPE_D, P = PIPE_P, R = PIPE_R;
   __shared__ float sX[2][D][WAVE];
-  __shared__ float2 sUS[2][D][WAVE];
+  __shared__ float sU[2][D][WAVE];
+  __shared__ float sEntry[2][WAVE];  // u before row 0 of the tile in the same buffer
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const unsigned lane = threadIdx.x % WAVE;
   const int64_t nb0 = (int64_t)blockIdx.x * WAVE;
@@ -194,6 +201,7 @@ __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_serial_fwd_pipe(
       if (k >= 1 && k <= ntiles) {
         const int buf = (int)((k - 1) & 1);
         const int nr = rows(k - 1);
+        sEntry[buf][lane] = u;
         if (nr == D) {
 #pragma unroll
           for (int g = 0; g < D; g += 16) {
@@ -204,14 +212,14 @@ __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_serial_fwd_pipe(
             for (int i = 0; i < 16; ++i) {
               bool sp;
               u = step(u, x[i], sp);
-              sUS[buf][g + i][lane] = make_float2(u, sp ? 1.0f : 0.0f);
+              sU[buf][g + i][lane] = u;
             }
           }
         } else {
           for (int j = 0; j < nr; ++j) {
             bool sp;
             u = step(u, sX[buf][j][lane], sp);
-            sUS[buf][j][lane] = make_float2(u, sp ? 1.0f : 0.0f);
+            sU[buf][j][lane] = u;
           }
         }
       }
@@ -220,9 +228,13 @@ __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_serial_fwd_pipe(
     return;
   }
 
-  // producers: I of tile k into LDS (loaded one round ahead) and U, S of tile k - 2 in round k
+  // producers: I of tile k into LDS (loaded one round ahead) and U, S of tile k - 2 in round k;
+  // xr: the rows of the tile being loaded; at the start of round k, x1 and x2 hold this
+  // producer's rows of tiles k - 1 and k - 2
   const int p = w - 1;
-  float xr[R];
+  float xr[R], x1[R], x2[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) xr[r] = x1[r] = x2[r] = 0.0f;
   auto load = [&](int64_t k) {
     const int nr = rows(k);
 #pragma unroll
@@ -233,6 +245,9 @@ __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_serial_fwd_pipe(
   };
   if (ntiles > 0) load(0);
   for (int64_t k = 0; k <= ntiles + 1; ++k) {
+    float xk[R];  // this producer's rows of tile k
+#pragma unroll
+    for (int r = 0; r < R; ++r) xk[r] = xr[r];
     if (k < ntiles) {
       const int buf = (int)(k & 1);
       const int nr = rows(k);
@@ -251,11 +266,17 @@ __global__ __launch_bounds__(WAVE*(PIPE_P + 1)) void k_serial_fwd_pipe(
         const int j = p + r * P;
         if (j < nr) {
           const size_t row = (size_t)((k - 2) * D + j) * (size_t)N + (size_t)nb0;
-          const float2 us = sUS[buf][j][lane];
-          st_row_nt(U + row, sb, us.x);
-          st_row_nt(S + row, sb, us.y);
+          const float u = sU[buf][j][lane];
+          const float up = j == 0 ? sEntry[buf][lane] : sU[buf][j - 1][lane];
+          st_row_nt(U + row, sb, u);
+          st_row_nt(S + row, sb, step.spike(up, x2[r]) ? 1.0f : 0.0f);
         }
       }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      x2[r] = x1[r];
+      x1[r] = xk[r];
     }
     __syncthreads();
   }

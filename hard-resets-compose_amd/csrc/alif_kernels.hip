@@ -612,7 +612,7 @@ __global__ __launch_bounds__(256) void k_alif_repair(
 __device__ __forceinline__ float alif_sg(float up, float wp, float x, float beta, float theta0,
                                          float alpha) {
   const float v = lif_v(up, x, beta);
-  const float sig = 1.0f / (1.0f + expf(-(alpha * ((v - theta0) - wp))));
+  const float sig = sigmoid_neg(alpha * ((v - theta0) - wp));
   return alpha * sig * (1.0f - sig);
 }
 

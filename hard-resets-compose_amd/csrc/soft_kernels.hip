@@ -18,7 +18,8 @@
 namespace lsh {
 
 __device__ __forceinline__ float soft_b(float v, float gs, float theta, float alpha) {
-  const float sg = 1.0f / (1.0f + expf(-(alpha * (v - theta))));
+  // the float64 adjoint (soft_adjoint_fft) keeps the library exp and the rounded division
+  const float sg = sigmoid_neg_exact(alpha * (v - theta));
   return gs * alpha * sg * (1.0f - sg);
 }
 

@@ -180,12 +180,14 @@ def check(rc, what):
 
 
 def ptr(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    """Device address of t (NULL for None) for a c_void_p argument: ctypes converts the plain
+    int itself, which costs less per call than building a c_void_p."""
+    return t.data_ptr() if t is not None else None
 
 
 def stream_of(t):
-    """torch's current stream on t's device as a raw hipStream_t."""
-    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(t.device.index))
+    """torch's current stream on t's device as a raw hipStream_t (an int, as ptr)."""
+    return torch._C._cuda_getCurrentRawStream(t.device.index)
 
 
 def on_device(t):

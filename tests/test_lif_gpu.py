@@ -161,6 +161,25 @@ def test_converged_v3_pieces_path_cfg4(L, dev):
     torch.cuda.empty_cache()
 
 
+def test_scan_v3_pieces_on_a_user_stream(L, dev):
+    """The pieces forward on a non-default stream, right after that stream produced I: the side
+    stream's builds wait for the caller's stream (event fork), and the caller's stream waits for
+    every build, so the result is the serial recurrence."""
+    from lifscan import hip_lif as H
+    T, N, C, P, beta = 16384, 1024, 256, 4, 0.99
+    g = torch.Generator(device=dev).manual_seed(43)
+    u0 = torch.rand(N, device=dev, generator=g)
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    print("v3 pieces on a user stream", flush=True)
+    with torch.cuda.stream(s):
+        I = torch.randn(T, N, device=dev, generator=g).mul_(0.08).add_(0.012)
+        U, S = H._scan2_pieces(I, beta, 1.0, 0.0, u0, C, 32, P)
+    s.synchronize()
+    Us, Ss = H.serial_forward(I, beta, 1.0, 0.0, u0)
+    assert torch.equal(U, Us) and torch.equal(S, Ss)
+
+
 @pytest.mark.parametrize("K", [4, 32])
 @pytest.mark.parametrize("P", [1, 2, 3, 4, 8])
 def test_scan_v3_pieces_equals_serial(L, dev, P, K):

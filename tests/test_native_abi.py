@@ -56,6 +56,24 @@ def test_workspace_queries_and_shape_checks():
     assert L.lsh_lif_scan_v3_layout(100, 1000, 64, 16, ctypes.byref(lay)) == -3
 
 
+def test_pieces_workspace_and_checks():
+    """The converged scan in pieces: P pieces of the v3 layout of T/P steps, each 256-byte
+    aligned; T % (C*P) != 0, P < 1 and P > 64 are refused (host-side checks, no GPU)."""
+    from lifscan import _native
+    L = _native.lib()
+    T, N, C, K = 2 ** 20, 1024, 2048, 32
+    for P in (1, 2, 4, 8):
+        piece = L.lsh_lif_scan_v3_workspace(T // P, N, C, K)
+        assert piece > 0
+        assert L.lsh_lif_scan_v3_pieces_workspace(T, N, C, K, P) == P * ((piece + 255) // 256 * 256)
+    assert L.lsh_lif_scan_v3_pieces_workspace(T, N, C, K, 3) == 0    # 512 chunks: 3 does not divide
+    assert L.lsh_lif_scan_v3_pieces_workspace(T, N, C, K, 0) == 0
+    assert L.lsh_lif_scan_v3_pieces_workspace(T, N, C, K, 65) == 0
+    rc = L.lsh_lif_scan_v3_pieces_fwd(None, None, None, None, T, N, 0.9, 1.0, 0.0, C, K, 4, None, 0,
+                                      None)
+    assert rc == -1
+
+
 def test_null_pointer_rejected_before_launch():
     from lifscan import _native
     L = _native.lib()

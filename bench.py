@@ -4,18 +4,20 @@
 Workload ("cfg2"): 65,536 neurons x T = 4,096, fp32, beta = 0.9,
 x ~ N(0.12, 0.25^2) (seeded CPU generator, copied to HBM before timing), u0 = 0, theta = 1,
 u_r = 0, upstream gradient gS ~ N(0, 1).  One step = lif_tuned(mode="scan", K=8, repair on)
-forward + backward through autograd: the exact two-level scan (single pass, bit-identical to
-the serial recurrence) and the single-pass affine-scan adjoint.  lif_tuned keeps U only for its
-backward, so its forward stores S and the exact state at every 32-step chunk entry, and the
-adjoint replays each chunk's forward from that state in registers (same S, same gradients):
-20 bytes of HBM traffic per neuron-step instead of 32.  value = neuron-steps/s of that fwd+bwd
-step; the passes that store U are timed beside it ("stored_U_path").
+forward + backward through autograd.  What runs: the exact single-pass forward with 32-step
+chunks handed on from wave to wave (no chunk maps: K is unused) and the single-pass affine-scan
+adjoint.  lif_tuned keeps U only for its backward, so its forward stores S and the exact state
+at every 32-step chunk entry, and the adjoint replays each chunk's forward from that state in
+registers (same S, same gradients): 20 bytes of HBM traffic per neuron-step instead of 32.
+value = neuron-steps/s of that fwd+bwd step, whose S and dI are checked once (outside the timed
+region) against the serial forward and the stored-U adjoint; the passes that store U are timed
+beside it ("stored_U_path").
 
-The JSON line also carries the forward-only rate, the scan with map speculation forced on,
-the in-house HIP serial baseline, the beta = 0.99 variant, the map statistics of the
-reference's chunking (C = 128, K = 8), the roofline of the dominant kernel (HIP events on the
-stream it runs on) and the CPU baseline (PyTorch-CPU port of the reference's fast.py on a
-bounded sample, timed on this host).
+The JSON line also carries the forward-only rate, the in-house HIP serial baseline, the map
+scan of configs[1] as stated (C = 32/64/128, K = 8, repair on, beta = 0.9 and 0.99:
+"cfg2_mapscan"), the roofline of the dominant kernel (HIP events on the stream it runs on) and
+the CPU baseline (PyTorch-CPU port of the reference's fast.py on a bounded sample, timed on
+this host).
 
 The other BASELINE configurations (cfg3 network step, cfg4 long sequence, cfg5 ALIF) are
 measured after the headline and reported under "other_configs" (--headline-only skips them).
@@ -121,6 +123,25 @@ def inputs(beta, dev):
     return I_cpu, I_cpu.to(dev), gS
 
 
+def cpu_model():
+    """The host CPU's model name (lscpu's "Model name", else /proc/cpuinfo's "model name")."""
+    import subprocess
+    try:
+        txt = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in txt.splitlines():
+            if line.strip().startswith("Model name"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(I_cpu, beta, n_cols):
     """PyTorch-CPU port of fast.py: two-level pruned scan forward (C=64, K=8, repair on) and
     the Hillis-Steele affine-scan backward, plus the serial pair, on the first n_cols neurons
@@ -151,6 +172,58 @@ def cpu_baseline(I_cpu, beta, n_cols):
             fn()
             ts.append(time.perf_counter() - t0)
         out[name] = statistics.median(ts)
+    return out
+
+
+def check_step(L, step, I, gS, u0, beta):
+    """One timed-step call checked outside the timed region: its S equals the serial forward's
+    and its dI the stored-U single-pass adjoint's (same chunk and wave count), bit for bit; no
+    chunk hand-off of the starts-only forward gave up.  Raises on a mismatch: a wrong step gets
+    no throughput line."""
+    import torch
+    S, dI = step()
+    Us, Ss = L.serial_forward(I, beta, 1.0, 0.0, u0)
+    Lam = L.scan_backward_fused(I, u0, Us, Ss, gS, None, beta, 1.0, 0.0, 4.0)
+    out = {"S_equals_serial_forward": bool(torch.equal(S, Ss)),
+           "dI_equals_stored_U_adjoint": bool(torch.equal(dI, Lam)),
+           "spin_timeouts": L.starts_forward_timeouts(I.device)}
+    if not (out["S_equals_serial_forward"] and out["dI_equals_stored_U_adjoint"]
+            and out["spin_timeouts"] == 0):
+        raise RuntimeError(f"the timed step's result is wrong: {out}")
+    return out
+
+
+def bench_cfg2_mapscan(torch, L, dev, u0, reps):
+    """BASELINE configs[1] as stated: the two-level map-scan forward (scan_forward_v3's own
+    pipeline: envelope + capacity-K chunk maps, carry with overflow fallback, replay, device
+    repair to convergence) at C in {32, 64, 128}, K = 8, for beta = 0.9 and 0.99, against the
+    serial forward; % of the 12 B/neuron-step roofline, overflow fraction and repair rounds.
+    Also the single pass with map speculation (C = 16, K = 8)."""
+    T, N = T_CFG, N_CFG
+    out = {}
+    for beta in (0.9, 0.99):
+        _, I, _ = inputs(beta, dev)
+        Us, Ss = L.serial_forward(I, beta, 1.0, 0.0, u0)
+        r = {"serial_fwd_ms": round(ev_time(lambda: L.serial_forward(I, beta, 1.0, 0.0, u0), reps), 4)}
+        for C in (32, 64, 128):
+            st = {}
+            U, S = L.scan_forward_mapscan(I, beta, 1.0, 0.0, u0, C=C, K=8, repair=10 ** 6, stats=st)
+            ok = bool(torch.equal(U, Us) and torch.equal(S, Ss))
+            del U, S
+            t = ev_time(lambda: L.scan_forward_mapscan(I, beta, 1.0, 0.0, u0, C=C, K=8, repair=10 ** 6),
+                        reps)
+            r[f"C{C}_K8"] = {"ms": round(t, 4),
+                             "pct_roofline_12B": round(100 * B_FWD * N * T / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2),
+                             "equals_serial": ok, "overflow_frac": round(st["overflow_frac"], 6),
+                             "repair_iters": st["repair_iters"], "mean_pieces": round(st["mean_pieces"], 4),
+                             "max_pieces": st["max_pieces"]}
+        t = ev_time(lambda: L.scan_forward_exact(I, beta, 1.0, 0.0, u0, C=16, K=8, maps=True), reps)
+        U, S = L.scan_forward_exact(I, beta, 1.0, 0.0, u0, C=16, K=8, maps=True)
+        r["single_pass_maps_C16_K8"] = {"ms": round(t, 4), "equals_serial": bool(torch.equal(U, Us) and torch.equal(S, Ss)),
+                                        **L.last_fused_counters()}
+        out[f"beta{beta}"] = r
+        del I, Us, Ss, U, S
+        torch.cuda.empty_cache()
     return out
 
 
@@ -510,12 +583,14 @@ def main():
         Ig = I.detach().requires_grad_(True)
         S = TL.lif_tuned(Ig, u0, beta, 1.0, 0.0, 4.0, mode="scan", K=K, repair=10 ** 6)
         S.backward(gS)
-        return Ig.grad
+        return S, Ig.grad
 
     log(f"warmup {args.warmup}")
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    check = check_step(L, step, I, gS, u0, beta)
+    log(f"timed step checked: {json.dumps(check)}")
     log(f"timing {args.steps} steps")
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -526,22 +601,17 @@ def main():
     log(f"fwd+bwd {ms_step:.3f} ms/step  {value / 1e9:.1f} G neuron-steps/s")
 
     # components (HIP events, median of 10)
-    C = L._pick_C(T, D=16)
     reps = 10
-    U, S = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6)
     ms = {}
-    ms["scan_fwd"] = ev_time(lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6), reps)
+    U, S = L.serial_forward(I, beta, 1.0, 0.0, u0)
+    ms["exact_fwd_stored_U"] = ev_time(lambda: L.scan_forward_exact(I, beta, 1.0, 0.0, u0, maps=False), reps)
     ms["scan_fwd_maps_forced_C16"] = ev_time(
         lambda: L.scan_forward_exact(I, beta, 1.0, 0.0, u0, C=16, K=K, maps=True), reps)
     L.scan_forward_exact(I, beta, 1.0, 0.0, u0, C=16, K=K, maps=True)
     maps_ctr = L.last_fused_counters()
-    ms["scan_bwd"] = ev_time(lambda: L.scan_backward_tiled(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0, C=C), reps)
-    ms["multikernel_scan_fwd_C128"] = ev_time(
-        lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6, stats={}), 3)
+    ms["adjoint_stored_U"] = ev_time(lambda: L.scan_backward_fused(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), reps)
     ms["serial_fwd"] = ev_time(lambda: L.serial_forward(I, beta, 1.0, 0.0, u0), reps)
     ms["serial_bwd"] = ev_time(lambda: L.serial_backward(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), reps)
-    st = {}
-    L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6, stats=st)
     del U, S
     # the recomputing pair lif_tuned runs here: S + chunk entry states, adjoint from them
     S_rc, ST = L.scan_forward_exact_starts(I, beta, 1.0, 0.0, u0)
@@ -551,17 +621,8 @@ def main():
     ms["rc_bwd"] = t_dom
     log("ms " + json.dumps({k: round(v, 4) for k, v in ms.items()}) + f" dominant {t_dom:.4f}")
     del S_rc, ST
-
-    # beta = 0.99 variant of cfg2
-    _, I99, _ = inputs(0.99, dev)
-    U99, S99 = L.scan_forward_v3(I99, 0.99, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6)
-    ms["scan_fwd_beta0.99"] = ev_time(lambda: L.scan_forward_v3(I99, 0.99, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6), reps)
-    ms["scan_bwd_beta0.99"] = ev_time(lambda: L.scan_backward_tiled(I99, u0, U99, S99, gS, None, 0.99, 1.0, 0.0, 4.0, C=C), reps)
-    ms["scan_fwd_maps_forced_C16_beta0.99"] = ev_time(
-        lambda: L.scan_forward_exact(I99, 0.99, 1.0, 0.0, u0, C=16, K=K, maps=True), reps)
-    st99 = {}
-    L.scan_forward_v3(I99, 0.99, 1.0, 0.0, u0, C=C, K=K, repair=10 ** 6, stats=st99)
-    del U99, S99, I99
+    mapscan = bench_cfg2_mapscan(torch, L, dev, u0, reps=5)
+    log("cfg2 map scan " + json.dumps(mapscan))
 
     achieved = B_BWD_RC * N * T / (t_dom / 1000.0) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -593,7 +654,7 @@ def main():
                "sample": f"fast.py two-level pruned scan fwd (C=64,K=8,repair on) + Hillis-Steele "
                          f"affine-scan bwd on {args.cpu_cols} of {N} neurons x T={T}, median of 3",
                "serial_fwd_bwd_value": round(nsteps / r["serial"], 1),
-               "os_cpu_count": os.cpu_count()}
+               "os_cpu_count": os.cpu_count(), "cpu_model": cpu_model()}
 
     pct = lambda b, t: round(100 * b * N * T / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
     out = {
@@ -609,22 +670,34 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded CPU generator: x~N(0.12,0.25^2), gS~N(0,1))",
-        "config": {"workload": "cfg2: lif_tuned(mode=scan, K=8, repair on) fwd+bwd, N=65536 "
-                               "(256x256), T=4096, beta=0.9, theta=1, u_r=0, u0=0",
-                   "N": N, "T": T, "beta": beta, "C": C, "K": K},
+        "config": {"workload": "cfg2: lif_tuned(I, u0, beta, mode='scan', K=8, repair=1e6) forward + "
+                               "backward through autograd at N=65536 (256x256), T=4096, beta=0.9, "
+                               "theta=1, u_r=0, u0=0.  Kernels that run: forward "
+                               "k_lif_fwd_fused<1,32,4,SPEC=false,SO=true> (exact single pass: 32-step "
+                               "chunks handed on wave to wave, no chunk maps, K unused; writes S and "
+                               "the chunk entry states), adjoint k_lif_bwd_fused<32,4,...,RC=true> "
+                               "(single-pass affine-scan adjoint replaying each chunk from its entry "
+                               "state).  The map scan (C=32..128, K=8) is measured in cfg2_mapscan.",
+                   "N": N, "T": T, "beta": beta, "internal_chunk": L.FUSED_FWD_C, "maps": False},
         "bytes_per_neuron_step": B_FWD_RC + B_BWD_RC,
+        "roofline_basis": "20 B per neuron-step, the bytes the recomputing pair moves (fwd: read I, "
+                          "write S and 1/32 row of entry states; bwd: read I, gS, write dI).  SURVEY "
+                          "8(d)'s 32 B counts U written and re-read, which lif_tuned never exposes: "
+                          "on that basis this step would be above the HBM peak; the stored-U passes "
+                          "are reported on it in stored_U_path",
         "pct_roofline_fwd_bwd": pct(B_FWD_RC + B_BWD_RC, ms_step),
         "fwd_value": round(N * T / (ms["rc_fwd"] / 1000.0), 1),
         "pct_roofline_fwd": pct(B_FWD_RC, ms["rc_fwd"]),
         "pct_roofline_bwd": pct(B_BWD_RC, ms["rc_bwd"]),
-        "stored_U_path": {"fwd_bwd_ms": round(ms["scan_fwd"] + ms["scan_bwd"], 4),
-                          "pct_roofline_fwd": pct(B_FWD, ms["scan_fwd"]),
-                          "pct_roofline_bwd": pct(B_BWD, ms["scan_bwd"]),
+        "timed_step_check": check,
+        "stored_U_path": {"fwd_bwd_ms": round(ms["exact_fwd_stored_U"] + ms["adjoint_stored_U"], 4),
+                          "pct_roofline_fwd": pct(B_FWD, ms["exact_fwd_stored_U"]),
+                          "pct_roofline_bwd": pct(B_BWD, ms["adjoint_stored_U"]),
                           "bytes_per_neuron_step": B_FWD + B_BWD},
         "ms": {k: round(v, 4) for k, v in ms.items()},
         "serial_hip_fwd_bwd_value": round(N * T / ((ms["serial_fwd"] + ms["serial_bwd"]) / 1000.0), 1),
         "maps_forced_counters": maps_ctr,
-        "stats_C128_K8": {"beta0.9": st, "beta0.99": st99},
+        "cfg2_mapscan": mapscan,
         "roofline": roofline,
         "cpu_baseline": cpu,
         "other_configs": others,

@@ -448,12 +448,7 @@ extern "C" int lsh_aff_serial_fwd(const float* I, const float* u0, float* U, flo
   if (!(gamma >= 0.0f && gamma <= 1.0f)) return LSH_ERR_ARG;
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (T == 0 || N == 0) return LSH_OK;
-  const int NB = (int)((N + WAVE - 1) / WAVE);
-  if (NB <= serial_pipe_max_blocks())
-    aff_serial_fwd_pipe(I, u0, U, S, N, T, beta, theta, gamma, delta, (hipStream_t)stream);
-  else
-    hipLaunchKernelGGL((k_aff_fwd<16>), dim3((unsigned)NB), dim3(WAVE), 0, (hipStream_t)stream, I,
-                       u0, U, S, nullptr, N, T, NB, beta, theta, gamma, delta);
+  aff_serial_fwd_pipe(I, u0, U, S, N, T, beta, theta, gamma, delta, (hipStream_t)stream);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }

@@ -712,88 +712,16 @@ __global__ __launch_bounds__(64) void k_alif_bwd(
   }
 }
 
-// Fused serial sweep of both recurrences (triton_alif.py:444-487), one lane per neuron,
-// reverse tiles of D steps with the next tile's loads issued before the current tile's steps:
-//   d = g + q*lw;  lv = (1-s)*beta*lv + sg*d;  LW[t] = lw;  LV[t] = lv;  lw <- rho*lw - sg*d.
-// DW0 (if given) receives lw_{-1}; with PS, partials[blockIdx.x] the block's parameter sums.
-template <int D, bool WLW, bool PS>
-__global__ __launch_bounds__(64) void k_alif_bwd_serial(
-    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
-    const float* __restrict__ U, const float* __restrict__ W, const float* __restrict__ S,
-    const float* __restrict__ GS, float* __restrict__ LW, float* __restrict__ LV,
-    float* __restrict__ DW0, double* __restrict__ partials, int64_t N, int64_t T, float beta,
-    float rho, float q, float theta0, float alpha, const float* __restrict__ dpar) {
-  if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
-  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
-  ParamAcc acc;
-  if (n < N) {
-    const float u0n = u0[n], w0n = w0[n];
-    float lw = 0.0f, lv = 0.0f;
-    auto load = [&](int64_t t, float& x, float& s, float& g, float& up, float& wp) {
-      const size_t o = (size_t)t * N + n;
-      x = I[o];
-      s = S[o];
-      g = GS[o];
-      up = t > 0 ? U[o - N] : u0n;
-      wp = t > 0 ? W[o - N] : w0n;
-    };
-    auto step = [&](int64_t t, float x, float s, float g, float up, float wp) {
-      const size_t o = (size_t)t * N + n;
-      const float sg = alif_sg(up, wp, x, beta, theta0, alpha);
-      const float d = g + q * lw;
-      lv = (1.0f - s) * beta * lv + sg * d;
-      if (WLW) st_nt(LW + o, lw);
-      st_nt(LV + o, lv);
-      if (PS) acc.add(lv, up, lw, wp, s, sg, d);
-      lw = rho * lw - sg * d;
-    };
-    const int64_t nt = T / D;  // full tiles, from the end; the T % D first steps follow
-    float xa[D], sa[D], ga[D], ua[D], wa[D];
-    if (nt > 0) {
-#pragma unroll
-      for (int j = 0; j < D; ++j) load(T - 1 - j, xa[j], sa[j], ga[j], ua[j], wa[j]);
-    }
-    for (int64_t b = 0; b < nt; ++b) {
-      float xb[D], sb[D], gb[D], ub[D], wb[D];
-      const bool more = b + 1 < nt;
-      if (more) {
-#pragma unroll
-        for (int j = 0; j < D; ++j) load(T - 1 - (b + 1) * D - j, xb[j], sb[j], gb[j], ub[j], wb[j]);
-      }
-#pragma unroll
-      for (int j = 0; j < D; ++j) step(T - 1 - b * D - j, xa[j], sa[j], ga[j], ua[j], wa[j]);
-      if (more) {
-#pragma unroll
-        for (int j = 0; j < D; ++j) {
-          xa[j] = xb[j];
-          sa[j] = sb[j];
-          ga[j] = gb[j];
-          ua[j] = ub[j];
-          wa[j] = wb[j];
-        }
-      }
-    }
-    for (int64_t t = T - nt * D - 1; t >= 0; --t) {
-      float x, s, g, up, wp;
-      load(t, x, s, g, up, wp);
-      step(t, x, s, g, up, wp);
-    }
-    if (DW0) DW0[n] = lw;
-  }
-  if (PS) {
-    acc.wave_sum();
-    if (threadIdx.x == 0) acc.store(partials + (size_t)blockIdx.x * 4);
-  }
-}
-
-// The fused serial sweep with wave roles (as serial_pipe.hip): one workgroup per 64 neurons,
+// The fused serial sweep of both recurrences (triton_alif.py:444-487:
+//   d = g + q*lw;  lv = (1-s)*beta*lv + sg*d;  LW[t] = lw;  LV[t] = lv;  lw <- rho*lw - sg*d,
+// DW0 = lw_{-1}, partials = the block's parameter sums) with wave roles (as serial_pipe.hip):
+// one workgroup per 64 neurons,
 // ALIF_PIPE_P producer waves and one consumer wave, tiles of ALIF_PIPE_D rows from the end of
 // time in an LDS double buffer.  Producers load the inputs one tile ahead, write (sg_t, g_t,
 // (1 - s_t)*beta) per row, and store LV (and LW) of the tile the consumer finished one round
 // earlier, adding the parameter sums there with the (u_{t-1}, w_{t-1}, s_t, sg_t) they kept;
-// the consumer runs d = g + q*lw, lv = ((1-s)*beta)*lv + sg*d, lw = rho*lw - sg*d.  Same
-// operations in the same order as k_alif_bwd_serial, so LV, LW and dL/dw0 are bit-identical;
-// the fp64 sums are added in another order.
+// the consumer runs d = g + q*lw, lv = ((1-s)*beta)*lv + sg*d, lw = rho*lw - sg*d, one step
+// after another in the reference's order.
 constexpr int ALIF_PIPE_D = 32;
 constexpr int ALIF_PIPE_P = 15;
 
@@ -1235,9 +1163,11 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
 // ALIF_LB_W chunks of ALIF_LB_C steps chained across workgroups by decoupled look-back (as the LIF
 // adjoint in lif_lookback.hip), once for lw and then for lv:
 //   1. every wave loads its chunk once (I, u_{t-1}, w_{t-1}, S, GS) and keeps (sg, g, 1 - s);
-//   2. lw: chunk maps (a = rho - q*sg, b = -sg*g) -> segment map, published (flag 1); wave 0
-//      looks back over the later segments to lw at its segment end, publishes lw at its start
-//      (flag 2); every wave replays lw from its chunk end (kept in registers);
+//   2. lw: chunk maps (a = rho - q*sg, b = -sg*g) -> segment map; wave 0 takes lw at its segment
+//      end from the later segments' published maps and an anchor's inclusive value in an order
+//      fixed by the segment index (lb_value_at_end, lsh_lookback.h: the same bits on every run;
+//      non-anchors publish their map first, anchors their value at the start afterwards); every
+//      wave replays lw from its chunk end (kept in registers);
 //   3. lv: the same with a = (1 - s)*beta, b = sg*(g + q*lw), then the replay stores LV (and LW)
 //      and sums the parameter gradients (fp32 per chunk, fp64 per workgroup).
 // Workgroups take (segment, block) tiles latest segment first through a ticket counter and wait
@@ -1262,6 +1192,7 @@ __global__ __launch_bounds__(WAVE* ALIF_LB_W) void k_alif_bwd_lookback(
   constexpr int C = ALIF_LB_C, WV = ALIF_LB_W;
   __shared__ float sP[WV][WAVE], sQ[WV][WAVE];
   __shared__ float sEnd[WAVE];
+  __shared__ float sLbP[LB_GROUP][WAVE], sLbQ[LB_GROUP][WAVE];
   __shared__ double sAcc[WV][4];
   __shared__ int sTicket;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -1324,43 +1255,46 @@ __global__ __launch_bounds__(WAVE* ALIF_LB_W) void k_alif_bwd_lookback(
     }
   }
 
-  // segment map of the chunk maps in sP/sQ, look-back, the value at this segment's end; the
-  // phase's aggregates are agg[phase][0..2] (P, Q, inclusive), its flags flags[phase]
+  // The look-back of one phase (its aggregates agg[phase][0..2] = P, Q, inclusive; its flags
+  // flags[phase]) over the chunk maps in sP/sQ: wave 0 composes the segment map and, outside
+  // an anchor, publishes it; every wave fetches look-back operands; wave 0 composes them in a
+  // fixed order (lsh_lookback.h) to the value at this segment's end (sEnd) and, at an anchor,
+  // publishes the value at its start.
+  const bool anchor = lb_is_anchor(seg);
+  int* const myflag0 = flags + (size_t)seg * NB + nb;
+  float Ps = 1.0f, Qs = 0.0f;  // value at segment start = Qs + Ps * value at segment end
   auto look_back = [&](int phase) {
     float* aP = agg + (size_t)phase * 3 * sn;
     float* aQ = aP + sn;
     float* inc = aQ + sn;
     int* fl = flags + (size_t)phase * NSEG * NB;
-    float Ps = 1.0f, Qs = 0.0f;  // value at segment start = Qs + Ps * value at segment end
-    for (int v = 0; v < WV; ++v) {
-      Qs = sQ[v][lane] + sP[v][lane] * Qs;
-      Ps = sP[v][lane] * Ps;
-    }
-    int* const myflag = fl + (size_t)seg * NB + nb;
-    float end = 0.0f;
-    if (seg < NSEG - 1) {
-      if (valid) {
-        st_coh(aP + so, Ps);
-        st_coh(aQ + so, Qs);
+    int* const myflag = myflag0 + (size_t)phase * NSEG * NB;
+    if (w == 0) {
+      Ps = 1.0f;
+      Qs = 0.0f;
+      for (int v = 0; v < WV; ++v) {
+        Qs = sQ[v][lane] + sP[v][lane] * Qs;
+        Ps = sP[v][lane] * Ps;
       }
-      publish_flag(myflag, 1);
-      float Pa = 1.0f, Qa = 0.0f;
-      for (int j = seg + 1; j < NSEG; ++j) {
-        const int f = flag_wait(fl + (size_t)j * NB + nb, &hdr->spin_timeouts);
-        const size_t oj = (size_t)j * N + nb0 + ln;
-        if (f == 2 || f < 0) {
-          const float x = f == 2 ? ld_coh(inc + oj) : 0.0f;
-          end = Qa + Pa * x;
-          break;
+      if (!anchor) {
+        if (valid) {
+          st_coh(aP + so, Ps);
+          st_coh(aQ + so, Qs);
         }
-        const float pj = ld_coh(aP + oj), qj = ld_coh(aQ + oj);
-        Qa = Qa + Pa * qj;
-        Pa = Pa * pj;
+        publish_flag(myflag, 1);
       }
     }
-    if (valid) st_coh(inc + so, Qs + Ps * end);
-    publish_flag(myflag, 2);
-    sEnd[lane] = end;
+    lb_fetch(seg, NSEG, NB, nb, N, nb0 + ln, w, WV, aP, aQ, inc, fl, sLbP, sLbQ,
+             &hdr->spin_timeouts);
+    __syncthreads();
+    if (w == 0) {
+      const float end = lb_compose(seg, NSEG, sLbP, sLbQ);
+      if (anchor) {
+        if (valid) st_coh(inc + so, Qs + Ps * end);
+        publish_flag(myflag, 2);
+      }
+      sEnd[lane] = end;
+    }
   };
 
   // 2. lw
@@ -1376,7 +1310,7 @@ __global__ __launch_bounds__(WAVE* ALIF_LB_W) void k_alif_bwd_lookback(
     sQ[w][lane] = Q;
   }
   __syncthreads();
-  if (w == 0) look_back(0);
+  look_back(0);
   __syncthreads();
   {
     float lam = sEnd[lane];
@@ -1403,7 +1337,7 @@ __global__ __launch_bounds__(WAVE* ALIF_LB_W) void k_alif_bwd_lookback(
     sQ[w][lane] = Q;
   }
   __syncthreads();
-  if (w == 0) look_back(1);
+  look_back(1);
   __syncthreads();
   ParamAcc acc;
   {
@@ -1542,13 +1476,9 @@ extern "C" int lsh_alif_serial_fwd(const float* I, const float* u0, const float*
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (T == 0 || N == 0) return LSH_OK;
   const int NB = (int)((N + WAVE - 1) / WAVE);
-  if (NB <= serial_pipe_max_blocks())
-    hipLaunchKernelGGL(k_alif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)), 0,
-                       (hipStream_t)stream, I, u0, w0, U, W, S, N, T, beta, rho, q, theta0, u_r,
-                       nullptr);
-  else
-    launch_alif_fwd<16>(I, u0, w0, U, W, S, nullptr, nullptr, N, T, 1, beta, rho, q, theta0, u_r,
-                        (hipStream_t)stream);
+  hipLaunchKernelGGL(k_alif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)), 0,
+                     (hipStream_t)stream, I, u0, w0, U, W, S, N, T, beta, rho, q, theta0, u_r,
+                     nullptr);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }
@@ -1562,13 +1492,9 @@ extern "C" int lsh_alif_serial_fwd_dparams(const float* I, const float* u0, cons
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (T == 0 || N == 0) return LSH_OK;
   const int NB = (int)((N + WAVE - 1) / WAVE);
-  if (NB <= serial_pipe_max_blocks())
-    hipLaunchKernelGGL(k_alif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)), 0,
-                       (hipStream_t)stream, I, u0, w0, U, W, S, N, T, 0.0f, 0.0f, 0.0f, 0.0f, u_r,
-                       params);
-  else
-    launch_alif_fwd<16>(I, u0, w0, U, W, S, nullptr, nullptr, N, T, 1, 0.0f, 0.0f, 0.0f, 0.0f, u_r,
-                        (hipStream_t)stream, params);
+  hipLaunchKernelGGL(k_alif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)), 0,
+                     (hipStream_t)stream, I, u0, w0, U, W, S, N, T, 0.0f, 0.0f, 0.0f, 0.0f, u_r,
+                     params);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }
@@ -1736,14 +1662,9 @@ static void launch_alif_serial_bwd(const float* I, const float* u0, const float*
                                    float* LV, float* DW0, double* partials, int64_t N, int64_t T,
                                    int NB, float beta, float rho, float q, float theta0, float alpha,
                                    hipStream_t st, const float* dpar) {
-  if (NB <= serial_pipe_max_blocks()) {
-    hipLaunchKernelGGL((k_alif_bwd_pipe<WLW, PS>), dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)),
-                       0, st, I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, beta, rho, q,
-                       theta0, alpha, dpar);
-    return;
-  }
-  hipLaunchKernelGGL((k_alif_bwd_serial<8, WLW, PS>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, w0,
-                     U, W, S, GS, LW, LV, DW0, partials, N, T, beta, rho, q, theta0, alpha, dpar);
+  hipLaunchKernelGGL((k_alif_bwd_pipe<WLW, PS>), dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)),
+                     0, st, I, u0, w0, U, W, S, GS, LW, LV, DW0, partials, N, T, beta, rho, q,
+                     theta0, alpha, dpar);
 }
 
 // The look-back single pass (mode 3): header reset, flags cleared, one workgroup per (segment,

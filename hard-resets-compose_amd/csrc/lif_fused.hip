@@ -631,13 +631,14 @@ extern "C" int lsh_lif_scan_exact_fwd_starts(const float* I, const float* u0, fl
   if (C != 16 && C != 32 && C != 64) return LSH_ERR_SHAPE;
   if (T % C != 0) return LSH_ERR_DIVISIBILITY;
   if ((uint64_t)N * (uint64_t)C * 4u >= ((uint64_t)1 << 32)) return LSH_ERR_SHAPE;
-  // ws NULL: no counters, and no reset launch before the forward
+  // ws NULL: no counters.  Otherwise the kernel adds its counters (spin_timeouts) to the
+  // header without clearing it first: no reset launch precedes the forward, and a header the
+  // caller cleared once accumulates over many calls.
   if (ws != nullptr &&
       (ws_bytes < kWsHeaderBytes || (reinterpret_cast<uintptr_t>(ws) & 255u) != 0))
     return LSH_ERR_WORKSPACE;
   hipStream_t st = (hipStream_t)stream;
   WsHeader* h = reinterpret_cast<WsHeader*>(ws);
-  if (h != nullptr) hipLaunchKernelGGL(k_ws_header_reset, dim3(1), dim3(64), 0, st, h);
   if (T > 0 && N > 0) {
     const int M = (int)(T / C);
     switch (C) {

@@ -697,7 +697,7 @@ static void launch_bwd3(const float* I, const float* u0, const float* U, const f
                         float* PB, int64_t N, int64_t Ls, int64_t M, float beta, float theta,
                         float u_r, float alpha, hipStream_t st, double* partials = nullptr) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
-  if (M == 1 && !COMPOSE && PS == 0 && !lam_end && NB <= serial_pipe_max_blocks()) {
+  if (M == 1 && !COMPOSE && PS == 0 && !lam_end) {
     // the serial adjoint with few neurons: producer and consumer waves (serial_pipe.hip)
     lif_serial_bwd_pipe(I, u0, U, S, GS, GU, Lam, N, Ls, beta, theta, u_r, alpha, DETACH, st);
     return;
@@ -886,12 +886,7 @@ extern "C" int lsh_lif_serial_fwd(const float* I, const float* u0, float* U, flo
   if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
   if (T == 0 || N == 0) return LSH_OK;
   hipStream_t st = (hipStream_t)stream;
-  if ((N + WAVE - 1) / WAVE <= serial_pipe_max_blocks())
-    lif_serial_fwd_pipe(I, u0, U, S, N, T, beta, theta, u_r, st);
-  else if (T >= 32)
-    launch_fwd<32>(I, u0, U, S, nullptr, N, T, 1, beta, theta, u_r, st);
-  else
-    launch_fwd<4>(I, u0, U, S, nullptr, N, T, 1, beta, theta, u_r, st);
+  lif_serial_fwd_pipe(I, u0, U, S, N, T, beta, theta, u_r, st);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }

@@ -9,10 +9,11 @@
 // workgroups take segments latest-first through a ticket counter:
 //   1. every wave loads its chunk once (I, U_{t-1}, S, GS[, GU]) into registers and composes
 //      its affine map (P, Q);
-//   2. wave 0 composes the segment map and publishes it (flag 1);
-//   3. wave 0 looks back over the later segments, composing published segment maps until it
-//      meets a published inclusive value (flag 2), which gives lam at its segment end; it then
-//      publishes its own inclusive value (lam at the segment start, flag 2);
+//   2. wave 0 composes the segment map;
+//   3. wave 0 takes lam at its segment end from the later segments' published maps and an
+//      anchor's inclusive value, in an order fixed by the segment index (lb_value_at_end: the
+//      same bits on every run); an anchor then publishes its inclusive value (lam at the
+//      segment start, flag 2), every other segment has published its map (flag 1) before;
 //   4. every wave takes lam at its chunk end from the later chunks of the segment and replays,
 //      storing dI.
 // A workgroup only waits for segments whose tickets are smaller than its own, i.e. for
@@ -49,6 +50,7 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
   constexpr bool AFF = PS == 2;
   __shared__ float sP[W][WAVE], sQ[W][WAVE];
   __shared__ float sLamEnd[WAVE];
+  __shared__ float sLbP[LB_GROUP][WAVE], sLbQ[LB_GROUP][WAVE];
   __shared__ double sAcc[PS ? W : 1][3];
   __shared__ int sTicket;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
@@ -114,40 +116,35 @@ __global__ __launch_bounds__(WAVE* W) void k_lif_bwd_lookback(
   sQ[w][lane] = Q;
   __syncthreads();
 
-  // 2.-3. segment map, look-back, inclusive value (wave 0)
+  // 2. segment map (wave 0); a segment that is not an anchor publishes it now
+  const bool anchor = lb_is_anchor(seg);
+  const size_t so = (size_t)seg * N + nb0 + lane;
+  int* const myflag = flags + (size_t)seg * NB + nb;
+  float Ps = 1.0f, Qs = 0.0f;  // lam_start(seg) = Qs + Ps * lam_end(seg)
   if (w == 0) {
-    float Ps = 1.0f, Qs = 0.0f;  // lam_start(seg) = Qs + Ps * lam_end(seg)
     for (int v = 0; v < W; ++v) {
       Qs = sQ[v][lane] + sP[v][lane] * Qs;
       Ps = sP[v][lane] * Ps;
     }
-    const size_t so = (size_t)seg * N + nb0 + lane;
-    int* const myflag = flags + (size_t)seg * NB + nb;
-    float lam_end = 0.0f;
-    if (seg < NSEG - 1) {
+    if (!anchor) {
       if (valid) {
         st_coh(aggP + so, Ps);
         st_coh(aggQ + so, Qs);
       }
       publish_flag(myflag, 1);
-      // lam_end(seg) = F(lam_start(j)) with F the composition of segments seg+1 .. j-1
-      float Pa = 1.0f, Qa = 0.0f;
-      for (int j = seg + 1; j < NSEG; ++j) {
-        const int f = flag_wait(flags + (size_t)j * NB + nb, &hdr->spin_timeouts);
-        const size_t oj = (size_t)j * N + nb0 + ln;
-        if (f == 2 || f < 0) {
-          const float x = f == 2 ? ld_coh(incl + oj) : 0.0f;
-          lam_end = Qa + Pa * x;
-          break;
-        }
-        const float pj = ld_coh(aggP + oj), qj = ld_coh(aggQ + oj);
-        Qa = Qa + Pa * qj;
-        Pa = Pa * pj;
-      }
     }
-    const float lam_start = Qs + Ps * lam_end;
-    if (valid) st_coh(incl + so, lam_start);
-    publish_flag(myflag, 2);
+  }
+  // 3. look-back: every wave fetches operands, wave 0 composes them in a fixed order; an anchor
+  //    publishes its inclusive value
+  lb_fetch(seg, NSEG, NB, nb, N, nb0 + ln, w, W, aggP, aggQ, incl, flags, sLbP, sLbQ,
+           &hdr->spin_timeouts);
+  __syncthreads();
+  if (w == 0) {
+    const float lam_end = lb_compose(seg, NSEG, sLbP, sLbQ);
+    if (anchor) {
+      if (valid) st_coh(incl + so, Qs + Ps * lam_end);
+      publish_flag(myflag, 2);
+    }
     sLamEnd[lane] = lam_end;
   }
   __syncthreads();

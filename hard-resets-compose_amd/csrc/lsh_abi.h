@@ -77,9 +77,8 @@ int lif_param_bwd_lookback(const float* I, const float* u0, const float* U, cons
 // Fills n ints with v on the stream (lif_lookback.hip; look-back flags).
 void fill_i32_launch(int* p, int64_t n, int v, hipStream_t st);
 
-// Wave-specialised serial sweeps (serial_pipe.hip): used instead of the one-wave serial kernels
-// up to serial_pipe_max_blocks() blocks of 64 neurons (lsh_serial_pipe_config sets it).
-int serial_pipe_max_blocks();
+// Wave-specialised serial sweeps (serial_pipe.hip): the serial entry points' kernels at every
+// neuron count; the one-wave serial kernels remain for scan replays and the parameter sums.
 void lif_serial_fwd_pipe(const float* I, const float* u0, float* U, float* S, int64_t N, int64_t T,
                          float beta, float theta, float u_r, hipStream_t st);
 void aff_serial_fwd_pipe(const float* I, const float* u0, float* U, float* S, int64_t N, int64_t T,

@@ -16,11 +16,9 @@
 
 namespace lsh {
 
-// Largest neuron-block count that takes these kernels (lsh_serial_pipe_config).  Measured on
-// MI355X (LIF adjoint, one wave -> pipe): N = 1024, T = 2^20: 172 -> 36.6 ms; N = 16384,
-// T = 4096: 0.71 -> 0.26 ms; N = 65536, T = 4096: 1.13 -> 1.06 ms; so by default every size.
-static int g_pipe_max_blocks = 1 << 30;
-int serial_pipe_max_blocks() { return g_pipe_max_blocks; }
+// Every serial sweep of the library's serial entry points runs here, at every neuron count.
+// Measured on MI355X (LIF adjoint, one wave -> pipe): N = 1024, T = 2^20: 172 -> 36.6 ms;
+// N = 16384, T = 4096: 0.71 -> 0.26 ms; N = 65536, T = 4096: 1.13 -> 1.06 ms.
 
 #ifndef LSH_PIPE_D
 #define LSH_PIPE_D 64
@@ -334,9 +332,3 @@ void lif_serial_bwd_pipe(const float* I, const float* u0, const float* U, const 
 }
 
 }  // namespace lsh
-
-extern "C" int lsh_serial_pipe_config(int max_blocks) {
-  const int prev = lsh::g_pipe_max_blocks;
-  if (max_blocks >= 0) lsh::g_pipe_max_blocks = max_blocks;
-  return prev;
-}

@@ -75,7 +75,6 @@ SIGNATURES = {
     "lsh_arch": (ctypes.c_char_p, []),
     "lsh_status_string": (ctypes.c_char_p, [c_i]),
     "lsh_lif_serial_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_p]),
-    "lsh_serial_pipe_config": (c_i, [c_i]),
     "lsh_lif_serial_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,
                                  c_f, c_i, c_p]),
     "lsh_lif_scan_v3_workspace": (c_sz, [c_i64, c_i64, c_i, c_i]),

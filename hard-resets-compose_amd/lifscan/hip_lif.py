@@ -15,6 +15,7 @@ serial kernel, the scan's replay and its fallbacks agree bit for bit, and after 
 scan equals the serial recurrence exactly.
 """
 import math
+import os
 
 import torch
 
@@ -125,13 +126,6 @@ def serial_forward_tiled(I, beta, theta, u_r, u0, BN=32, D=4, num_warps=1):
 def serial_forward_auto(I, beta, theta, u_r, u0):
     """Tuned serial forward (triton_lif.py:1221-1225)."""
     return serial_forward(I, beta, theta, u_r, u0)
-
-
-def serial_pipe_max_blocks(n=None):
-    """Largest count of 64-neuron blocks whose serial sweeps run as producer and consumer waves
-    (bit-identical to the one-wave kernels, faster with few neurons); n sets it (0 disables).
-    Returns the value in force before the call."""
-    return int(_n.lib().lsh_serial_pipe_config(-1 if n is None else int(n)))
 
 
 def serial_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=True, BN=BN_DEFAULT):
@@ -353,6 +347,13 @@ def _scan2_pieces(I, beta, theta, u_r, u0, C, K, P):
     return U, S
 
 
+def scan_forward_mapscan(I, beta, theta, u_r, u0, C=64, K=16, repair=0, stats=None):
+    """The two-level map scan of scan_forward_v3 itself (envelope + capacity-K chunk maps, carry
+    with overflow fallback, replay, device repair) -> (U, S), also where scan_forward_v3 would
+    compute its converged result by a faster exact path.  For measuring the map scan."""
+    return _scan2(I, beta, theta, u_r, u0, C, K, repair, stats)
+
+
 def scan_forward(I, beta, theta, u_r, u0, C=64, K=16, BN=BN_DEFAULT, repair=0, stats=None):
     """Two-level scan pruned with the loose global state_bounds (triton_lif.py:262-295)."""
     I = _input(I)
@@ -556,6 +557,31 @@ def scan_backward_fused(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach
 RECOMPUTE_BWD = True
 
 
+# The starts-only forward adds the count of chunk hand-offs whose bounded wait gave up to a
+# per-device counter header that is cleared once and never by the calls themselves (no reset
+# launch per call).  It must stay 0: starts_forward_timeouts() reads it (synchronizing), and
+# with CHECK_WAITS (environment LIFSCAN_CHECK_WAITS=1) every call reads it and raises.
+CHECK_WAITS = os.environ.get("LIFSCAN_CHECK_WAITS", "0") not in ("", "0")
+_WAIT_HEADERS = {}
+
+
+def _wait_header(device):
+    h = _WAIT_HEADERS.get(device)
+    if h is None:
+        h = torch.zeros(max(int(_n.lib().lsh_lif_scan_exact_workspace()), 256), dtype=torch.uint8,
+                        device=device)
+        _WAIT_HEADERS[device] = h
+    return h
+
+
+def starts_forward_timeouts(device=None):
+    """Hand-offs of the starts-only forward on `device` (default: the current one) that gave
+    up since the process started (must be 0).  Synchronizes."""
+    device = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    h = _WAIT_HEADERS.get(device)
+    return 0 if h is None else int(_n.read_stats(h, 1).spin_timeouts)
+
+
 def scan_forward_exact_starts(I, beta, theta, u_r, u0, C=None):
     """Single-pass exact forward -> (S, STARTS [T//C, N]): S as scan_forward_exact, and the
     state before every C-step chunk (STARTS[0] = u0) in place of U."""
@@ -567,10 +593,14 @@ def scan_forward_exact_starts(I, beta, theta, u_r, u0, C=None):
         raise ValueError(f"the starts-only forward needs C in (16, 32, 64) dividing T={T}")
     S = torch.empty_like(I)
     ST = torch.empty(T // C, N, device=I.device, dtype=torch.float32)
-    with _n.on_device(I):  # no workspace: the counters are not read here
+    hdr = _wait_header(I.device)
+    with _n.on_device(I):
         _n.check(_n.lib().lsh_lif_scan_exact_fwd_starts(
             _n.ptr(I), _n.ptr(u0), _n.ptr(ST), _n.ptr(S), T, N, _f32(beta), _f32(theta), _f32(u_r), C,
-            None, 0, _n.stream_of(I)), "lsh_lif_scan_exact_fwd_starts")
+            _n.ptr(hdr), hdr.numel(), _n.stream_of(I)), "lsh_lif_scan_exact_fwd_starts")
+    if CHECK_WAITS and int(_n.read_stats(hdr, 1).spin_timeouts) != 0:
+        raise RuntimeError("lsh_lif_scan_exact_fwd_starts: a chunk hand-off wait gave up; "
+                           "S and the chunk entry states are not valid")
     return S, ST
 
 
@@ -600,10 +630,13 @@ def scan_backward_fused_starts(I, STARTS, GS, beta, theta, u_r, alpha=4.0, want_
 def _recompute_ok(T, N, K, repair):
     """True when scan_forward_auto and scan_backward_auto would both take the single-pass
     kernels (converged forward without maps, fused adjoint): then the recomputing pair gives
-    the same S and Lam."""
+    the same S and Lam.  False (never an error) for lengths the chunk policy rejects."""
     if not RECOMPUTE_BWD or FUSED_FWD_C != FUSED_BWD_C or T == 0 or N == 0:
         return False
-    if T % _pick_C(T, D=16) or not _fused_fwd_ok(T, _pick_C(T, D=16), K, repair, None):
+    if T % FUSED_FWD_C:
+        return False
+    C = _chunk_or_none(T, 16)
+    if C is None or not _fused_fwd_ok(T, C, K, repair, None):
         return False
     if long_sequence_C(T, N) or N <= FUSED_MAPS_MAX_N:
         return False
@@ -722,6 +755,14 @@ def _pick_C(T, D=8):
     raise ValueError(f"T={T} needs a chunk length divisible by {D}")
 
 
+def _chunk_or_none(T, D):
+    """_pick_C(T, D), or None where that policy raises."""
+    try:
+        return _pick_C(T, D=D)
+    except ValueError:
+        return None
+
+
 def scan_forward_auto(I, beta, theta, u_r, u0, K=16, repair=0):
     """Two-level exact forward with the reference's default chunking (triton_lif.py:1228-1232)."""
     T = I.shape[0]
@@ -737,9 +778,16 @@ def scan_backward_auto(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0):
 
 
 def auto_modes(N, T):
-    """Serial or scan per pass from (N, T) (triton_lif.py:997-1000)."""
+    """Serial or scan per pass from (N, T) (triton_lif.py:997-1000).  A pass whose chunk policy
+    has no chunk for T (scan_forward_auto: _pick_C(T, D=16); scan_backward_auto: D=2) stays
+    serial, so lif_auto runs for every T (e.g. T = 1000 or 1002), as the reference's does at
+    its thresholds."""
     fwd = "scan" if (N <= AUTO_FWD_MAX_N and T >= AUTO_FWD_MIN_T) else "serial"
     bwd = "scan" if (N <= AUTO_BWD_MAX_N and T >= AUTO_BWD_MIN_T) else "serial"
+    if fwd == "scan" and _chunk_or_none(T, 16) is None:
+        fwd = "serial"
+    if bwd == "scan" and _chunk_or_none(T, 2) is None:
+        bwd = "serial"
     return fwd, bwd
 
 

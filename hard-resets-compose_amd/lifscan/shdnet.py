@@ -1,75 +1,68 @@
-"""Feed-forward hard-reset LIF network of the reference's ``lifscan/shdnet.py`` (LIFLayer, Net)
-on the HIP kernels: Linear(din -> H) -> lif_tuned / lif_auto per layer, two layers, linear
-readout averaged over time (x10).  Input is time-major [T, B, 700].
+"""The spiking classifier the reference trains on SHD (its ``lifscan/shdnet.py``): two hard-reset
+LIF layers of H neurons fed by linear maps, and a linear readout of the second layer's spikes.
 
-SHD/SSC loading needs h5py, imported only by `load` (it is not installed in every environment);
-`batch_dense` builds the dense raster on the device from (time bin, unit) event lists.  The
-spikingjelly baseline mode of the reference is not provided.
+What a caller of the reference can rely on, kept here (shdnet.py:30-66):
+  * ``Net(mode, beta=0.95, H=256, n_out=20)`` with children ``l1``, ``l2`` (``LIFLayer``) and
+    ``out`` (``nn.Linear``), so parameter names and state dicts are the reference's;
+  * ``LIFLayer(din, dout, beta, mode, K=16, repair=10**6)`` with attributes ``fc``, ``beta``,
+    ``mode``, ``K``, ``repair`` (experiments set ``repair`` on a built net);
+  * the LIF weight init U(-1.5/sqrt(din), +1.5/sqrt(din)) drawn after nn.Linear's own init, so
+    a seeded construction draws the same numbers; the readout's default nn.Linear init;
+  * ``forward(x)`` with x time-major [T, B, din] -> (logits [B, n_out], (s1, s2)), logits = 10 x
+    the time average of the readout; ``set_mode(mode)``.
+Modes: "serial" and "scan" run ``lif_tuned`` (repair as given), "auto" runs ``lif_auto`` without
+repair.  The reference's SpikingJelly mode and its SHD/SSC h5 loader are not part of this
+package (the benchmark input is a synthetic raster built by the caller).
+
+The readout is applied to the time-averaged spikes, out(mean_t s2), rather than averaging the
+readout of every step: the same function (out is affine), one [B, H] x [H, n_out] product
+instead of a [T*B, H] one, and no [T, B, n_out] intermediate.
 """
-import os
-
-import numpy as np
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import hip_lif as L
 
-DATA = os.environ.get("SHD_DATA", "data/shd")  # directory with {shd,ssc}_{train,test}.h5
+THETA = 1.0       # firing threshold of every LIF neuron of the network
+RESET = 0.0       # hard-reset value
+SURROGATE = 4.0   # slope alpha of the sigmoid surrogate gradient
+READOUT_GAIN = 10.0
+_LAYER_MODES = ("serial", "scan", "auto")
 
 
-def load(split, T, dataset="shd"):
-    """(events, labels) of one split (shdnet.py:12-19): events[i] = int64 [n, 2] (time bin in
-    [0, T), unit) from a 1 s window."""
-    try:
-        import h5py
-    except ImportError as e:  # pragma: no cover - depends on the environment
-        raise ImportError("shdnet.load needs h5py to read the SHD/SSC files") from e
-    with h5py.File(f"{DATA}/{dataset}_{split}.h5", "r") as f:
-        y = torch.tensor(f["labels"][:].astype(np.int64))
-        ev = []
-        for tt, uu in zip(f["spikes"]["times"][:], f["spikes"]["units"][:]):
-            b = np.minimum((tt * T).astype(np.int64), T - 1)
-            ev.append(torch.tensor(np.stack([b, uu.astype(np.int64)], 1)))
-    return ev, y
-
-
-def batch_dense(ev, idx, T, dev="cuda"):
-    """Dense 0/1 raster [T, len(idx), 700] of the chosen samples (shdnet.py:22-27)."""
-    x = torch.zeros(T, len(idx), 700, device=dev)
-    for j, i in enumerate(idx):
-        e = ev[i].to(dev, non_blocking=True)
-        x[e[:, 0], j, e[:, 1]] = 1.0
-    return x
+def spike_train(I, beta, mode, K, repair):
+    """Spikes [T, N] of LIF neurons that start at rest, driven by the currents I [T, N]."""
+    if mode not in _LAYER_MODES:
+        raise ValueError(f"mode {mode!r}: one of {_LAYER_MODES}")
+    rest = I.new_zeros(I.shape[1])
+    if mode == "auto":
+        return L.lif_auto(I, rest, beta, THETA, RESET, SURROGATE, K=K, repair=0)
+    return L.lif_tuned(I, rest, beta, THETA, RESET, SURROGATE, mode=mode, K=K, repair=repair)
 
 
 class LIFLayer(nn.Module):
-    """Linear(din -> dout) with weights U(+-1.5/sqrt(din)), then the LIF layer over time
-    (shdnet.py:30-50).  mode: serial / scan (lif_tuned, repair as given) or auto (lif_auto,
-    no repair)."""
+    """x [T, B, din] -> spikes [T, B, dout]: currents fc(x) for all B*dout neurons, one exact
+    LIF scan over time (B and dout flattened into the neuron axis)."""
 
     def __init__(self, din, dout, beta, mode, K=16, repair=10 ** 6):
         super().__init__()
         self.fc = nn.Linear(din, dout)
-        nn.init.uniform_(self.fc.weight, -1.5 / din ** 0.5, 1.5 / din ** 0.5)
+        bound = 1.5 / din ** 0.5
+        with torch.no_grad():
+            self.fc.weight.uniform_(-bound, bound)
         self.beta, self.mode, self.K, self.repair = beta, mode, K, repair
 
     def forward(self, x):
-        Tn, B, _ = x.shape
-        I = self.fc(x).reshape(Tn, -1).contiguous()
-        u0 = torch.zeros(I.shape[1], device=I.device)
-        if self.mode == "auto":
-            s = L.lif_auto(I, u0, beta=self.beta, theta=1.0, u_r=0.0, alpha=4.0, K=self.K, repair=0)
-        elif self.mode in ("serial", "scan"):
-            s = L.lif_tuned(I, u0, beta=self.beta, theta=1.0, u_r=0.0, alpha=4.0, mode=self.mode,
-                            K=self.K, repair=self.repair)
-        else:
-            raise ValueError(f"mode {self.mode!r}: only serial, scan and auto are provided")
-        return s.reshape(Tn, B, -1)
+        steps, batch, din = x.shape
+        currents = F.linear(x.reshape(steps * batch, din), self.fc.weight, self.fc.bias)
+        s = spike_train(currents.view(steps, -1), self.beta, self.mode, self.K, self.repair)
+        return s.view(steps, batch, -1)
 
 
 class Net(nn.Module):
-    """700 -> H -> H LIF layers and a linear readout; logits = mean over time x 10
-    (shdnet.py:53-66)."""
+    """din=700 -> H -> H spiking layers, linear readout of the time-averaged second-layer
+    spikes (x READOUT_GAIN)."""
 
     def __init__(self, mode, beta=0.95, H=256, n_out=20):
         super().__init__()
@@ -78,9 +71,10 @@ class Net(nn.Module):
         self.out = nn.Linear(H, n_out)
 
     def set_mode(self, mode):
-        self.l1.mode = self.l2.mode = mode
+        for layer in (self.l1, self.l2):
+            layer.mode = mode
 
     def forward(self, x):
         s1 = self.l1(x)
         s2 = self.l2(s1)
-        return self.out(s2).mean(0) * 10, (s1, s2)
+        return READOUT_GAIN * self.out(s2.mean(0)), (s1, s2)

@@ -41,7 +41,13 @@ int lsh_abi_version(void);
 const char* lsh_arch(void);                /* "gfx950" */
 const char* lsh_status_string(int status); /* static string for a status code */
 
-/* Serial hard-reset LIF forward, one lane per neuron, time-tiled with register prefetch.
+/* The serial sweeps (lsh_lif_serial_fwd/_bwd, lsh_alif_serial_fwd*, lsh_alif_bwd mode 0,
+ * lsh_aff_serial_fwd) run one workgroup per 64 neurons: producer waves load a tile of rows one
+ * tile ahead, compute every per-step quantity that does not depend on the recurrence into an
+ * LDS double buffer and store the outputs, while one consumer wave runs the recurrence itself,
+ * with the serial step's operations in the reference's order. */
+
+/* Serial hard-reset LIF forward.
  * Replaces triton_lif.py:460-466 (serial_forward_tiled), :246-251 (serial_forward) and
  * :1221-1225 (serial_forward_auto).  U, S: [T, N] outputs. */
 int lsh_lif_serial_fwd(const float* I, const float* u0, float* U, float* S, int64_t T, int64_t N,
@@ -55,13 +61,6 @@ int lsh_lif_serial_fwd(const float* I, const float* u0, float* U, float* S, int6
 int lsh_lif_serial_bwd(const float* I, const float* u0, const float* U, const float* S,
                        const float* GS, const float* GU, float* Lam, int64_t T, int64_t N,
                        float beta, float theta, float u_r, float alpha, int detach, void* stream);
-
-/* Serial sweeps with few neurons run as one workgroup per 64 neurons of producer waves (loads,
- * per-step coefficients, stores, through an LDS double buffer) and one consumer wave (the
- * recurrence), bit-identical to the one-wave kernels.  Sets the largest neuron-block count that
- * takes them (0: never; negative: unchanged) and returns the previous value (default: all).
- * No counterpart in the reference: a tuning and testing knob of this library. */
-int lsh_serial_pipe_config(int max_blocks);
 
 /* Two-level exact scan forward (envelope bound + capacity-K chunk maps, sequential carry
  * with overflow-to-serial fallback, replay, Jacobi repair on device).
@@ -196,8 +195,11 @@ int lsh_lif_scan_fused_bwd(const float* I, const float* u0, const float* U, cons
  * u_{t-1} and s_t are the forward's bits and Lam is the same as lsh_lif_scan_fused_bwd's with
  * the reset detached and no GU.  HBM traffic: forward 8 B, adjoint 12 B per neuron-step
  * (instead of 12 + 20).  C in {16, 32, 64}, the same C for both, T % C == 0; the forward is the
- * single-pass exact forward without maps (workspace lsh_lif_scan_exact_workspace(), or NULL
- * with ws_bytes 0: then its counters are not kept and no reset kernel precedes it).
+ * single-pass exact forward without maps.  Its ws is NULL (ws_bytes 0: no counters) or a
+ * 256-byte aligned header of lsh_lif_scan_exact_workspace() bytes to which the kernel ADDS its
+ * counters without clearing it first (no reset launch precedes the forward): clear it once
+ * (any fill kernel) and read it with lsh_scan_stats_read whenever convenient; a non-zero
+ * spin_timeouts means a chunk hand-off gave up and the S/STARTS of that call are not valid.
  * partials: NULL, or [ceil(N/64)] rows of 3 doubles as lsh_lif_param_bwd mode 2 (sum of
  * lam_t*u_{t-1}, gs_t*sg_t, s_t*lam_{t+1}). */
 int lsh_lif_scan_exact_fwd_starts(const float* I, const float* u0, float* STARTS, float* S,

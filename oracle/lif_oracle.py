@@ -83,6 +83,41 @@ def serial_backward(I, u0, U, S, GS, GU, beta, theta, u_r, alpha=4.0, detach=Tru
     return Lam
 
 
+def serial_backward_long(I, u0, U, S, GS, beta, theta, u_r, alpha=4.0, block=1024):
+    """The fp64 adjoint of serial_backward (detached reset, no GU) for long sequences, where a
+    Python loop over every step is slow: the same recurrence lam_t = b_t + a_t*lam_{t+1} (fp64
+    coefficients of triton_lif.py:43-50) evaluated blockwise, i.e. each block of `block` steps
+    composed to lam_start = P*lam_end + Q, the block ends carried from the last block, then each
+    block replayed (the structure of triton_lif.py:512-526, in fp64).  Agrees with
+    serial_backward(dtype=float64) to reassociation (~1e-13 relative; pinned in
+    tests/test_oracle_lif.py).  T % block == 0."""
+    dt = np.float64
+    T, N = I.shape
+    if T % block:
+        raise ValueError("T must be a multiple of block")
+    M = T // block
+    Uprev = np.concatenate([np.asarray(u0, dtype=f32).reshape(1, N), U[:-1]], 0)
+    a, b = coef(Uprev, I, S, GS, None, beta, theta, u_r, alpha, True, dt)
+    a = a.reshape(M, block, N)
+    b = b.reshape(M, block, N)
+    P = np.ones((M, N), dt)
+    Q = np.zeros((M, N), dt)
+    for j in range(block - 1, -1, -1):
+        Q = b[:, j] + a[:, j] * Q
+        P = a[:, j] * P
+    lam_end = np.zeros((M, N), dt)
+    lam = np.zeros(N, dt)
+    for m in range(M - 1, -1, -1):
+        lam_end[m] = lam
+        lam = Q[m] + P[m] * lam
+    Lam = np.empty((M, block, N), dt)
+    lam = lam_end
+    for j in range(block - 1, -1, -1):
+        lam = b[:, j] + a[:, j] * lam
+        Lam[:, j] = lam
+    return Lam.reshape(T, N)
+
+
 def param_grads(I, u0, U, S, GS, Lam, beta, theta, u_r, alpha=4.0):
     """LIFParamFn.backward assembly (fit.py:36-48), fp64, detached reset:
     (dI, du0, dbeta, dtheta, du_r) = (Lam, beta*Lam[0], sum Lam_t u_{t-1},

@@ -359,11 +359,10 @@ def test_alif_float_and_tensor_params_agree(AL, dev, fwd):
     o3, g3 = run(pm)
     for a, b, c in zip(o1, o2, o3):
         assert torch.equal(a, b) and torch.equal(a, c)
-    # below 8192 neurons the adjoint is the look-back pass, whose last bits depend on timing
+    # below 8192 neurons the adjoint is the look-back pass (deterministic: the same bits)
     for a, b, c in zip(g1, g2, g3):
-        assert rel(host(b), host(a)) < 1e-6 and rel(host(c), host(a)) < 1e-6
-    assert rel(host(pm[0].grad), host(pt[0].grad)) < 1e-6
-    assert rel(host(pm[2].grad), host(pt[2].grad)) < 1e-6
+        assert torch.equal(a, b) and torch.equal(a, c)
+    assert torch.equal(pm[0].grad, pt[0].grad) and torch.equal(pm[2].grad, pt[2].grad)
     assert all(p.grad is not None for p in pt)
 
 
@@ -419,11 +418,13 @@ def test_alif_layer_recompute_equals_stored(AL, dev, monkeypatch):
         assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("T,N", [(1, 1), (31, 64), (32, 100), (33, 7), (1000, 130), (4113, 1029)])
-def test_alif_serial_bwd_pipe_equals_one_wave(AL, dev, T, N):
-    """The producer/consumer serial adjoint gives the one-wave kernel's LV, LW and dL/dw0 bit for
-    bit; its fp64 parameter sums (added in another order) within 1e-12."""
-    from lifscan import hip_alif, hip_lif
+@pytest.mark.parametrize("T,N", [(1, 1), (63, 64), (64, 100), (65, 7), (1000, 130), (4113, 1029)])
+def test_alif_serial_bwd_pipe(AL, dev, T, N):
+    """The producer/consumer serial adjoint (mode 0; full and partial tiles, ragged neuron blocks):
+    LV, LW and dL/dw0 within 1e-5 of the fp32 oracle and 1e-4 of the fp64 adjoint, the parameter
+    sums within 1e-3 of their fp64 assembly (the reference's bar for these cancelling sums,
+    tests/test_alif_grad.py:34); alif_backward(mode="serial") gives the same bits."""
+    from lifscan import hip_alif
     beta, rho, q = 0.95, 0.995, 0.9
     x = _inputs(beta, 2.0, T, N, 51)
     G = normal(T, N, 0.0, 1.0, 52)
@@ -433,28 +434,26 @@ def test_alif_serial_bwd_pipe_equals_one_wave(AL, dev, T, N):
     args = [gpu(a, dev) for a in (x, U, W, S, G)]
     ug, wg = gpu(u0, dev), gpu(w0, dev)
     print(f"alif serial bwd pipe T={T} N={N}", flush=True)
-    prev = hip_lif.serial_pipe_max_blocks(0)
-    try:
-        ref = hip_alif._alif_bwd_call(*args, beta, rho, q, 1.0, ug, wg, 4.0, "serial", 64, want_lw=True,
-                                      want_params=True)
-        ref2 = AL.alif_backward(*args, beta, rho, q, 1.0, ug, wg, mode="serial")
-        hip_lif.serial_pipe_max_blocks(1 << 20)
-        got = hip_alif._alif_bwd_call(*args, beta, rho, q, 1.0, ug, wg, 4.0, "serial", 64, want_lw=True,
-                                      want_params=True)
-        got2 = AL.alif_backward(*args, beta, rho, q, 1.0, ug, wg, mode="serial")
-    finally:
-        hip_lif.serial_pipe_max_blocks(prev)
-    for a, b in zip(ref[:3] + ref2, got[:3] + got2):
-        assert torch.equal(a, b)
-    s_ref, s_got = host(ref[3]), host(got[3])
-    assert np.all(np.abs(s_got - s_ref) <= 1e-12 * (np.abs(s_ref) + 1.0))
+    LV, LW, DW0, sums = hip_alif._alif_bwd_call(*args, beta, rho, q, 1.0, ug, wg, 4.0, "serial", 64,
+                                                want_lw=True, want_params=True)
+    LV2, LW2 = AL.alif_backward(*args, beta, rho, q, 1.0, ug, wg, mode="serial")
+    assert torch.equal(LV, LV2) and torch.equal(LW, LW2)
+    LVo, LWo = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0)
+    LV6, LW6 = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0, dtype=np.float64)
+    assert rel(host(LV), LVo) < 1e-5 and rel(host(LW), LWo) < 1e-5
+    assert rel(host(LV), LV6) < 1e-4 and rel(host(LW), LW6) < 1e-4
+    want = A.param_grads(x, U, W, S, G, LV6, LW6, beta, rho, q, 1.0, u0, w0, 4.0)
+    assert rel(host(DW0), want[2]) < 1e-4
+    got = host(sums)
+    for k, w in enumerate((want[3], want[4], want[5], -want[6])):
+        assert rel(got[k], w) < 1e-3, k
 
 
 @pytest.mark.parametrize("T,N", [(1, 1), (63, 64), (64, 100), (65, 7), (1000, 130), (4113, 1029)])
-def test_alif_serial_fwd_pipe_equals_one_wave(AL, dev, T, N):
-    """The producer/consumer serial forward gives U, W, S of the one-wave kernel and the oracle
-    bit for bit, with float and with device parameters."""
-    from lifscan import hip_alif, hip_lif
+def test_alif_serial_fwd_pipe(AL, dev, T, N):
+    """The producer/consumer serial forward gives U, W, S of the oracle bit for bit, with float
+    and with device parameters."""
+    from lifscan import hip_alif
     beta, rho, q = 0.95, 0.995, 0.9
     x = _inputs(beta, 2.0, T, N, 55)
     u0 = uniform(N, -0.1, 0.3, 56)
@@ -462,24 +461,19 @@ def test_alif_serial_fwd_pipe_equals_one_wave(AL, dev, T, N):
     Ur, Wr, Sr = A.serial_forward(x, beta, rho, q, 1.0, 0.0, u0, w0)
     xg, ug, wg = gpu(x, dev), gpu(u0, dev), gpu(w0, dev)
     print(f"alif serial fwd pipe T={T} N={N}", flush=True)
-    prev = hip_lif.serial_pipe_max_blocks(0)
-    try:
-        ref = AL.alif_serial_forward(xg, beta, rho, q, 1.0, 0.0, ug, wg)
-        hip_lif.serial_pipe_max_blocks(1 << 20)
-        got = AL.alif_serial_forward(xg, beta, rho, q, 1.0, 0.0, ug, wg)
-        dp = hip_alif._dev_params(xg, torch.tensor(beta, device=dev), rho, q, 1.0)
-        got2 = hip_alif._alif_serial_forward_dp(xg, dp, 0.0, ug, wg)
-    finally:
-        hip_lif.serial_pipe_max_blocks(prev)
-    for a, b, c, o in zip(ref, got, got2, (Ur, Wr, Sr)):
-        assert torch.equal(a, b) and torch.equal(a, c) and np.array_equal(host(b), o)
+    got = AL.alif_serial_forward(xg, beta, rho, q, 1.0, 0.0, ug, wg)
+    dp = hip_alif._dev_params(xg, torch.tensor(beta, device=dev), rho, q, 1.0)
+    got2 = hip_alif._alif_serial_forward_dp(xg, dp, 0.0, ug, wg)
+    for b, c, o in zip(got, got2, (Ur, Wr, Sr)):
+        assert torch.equal(b, c) and np.array_equal(host(b), o)
 
 
 @pytest.mark.parametrize("T,N", [(128, 1), (1280, 64), (4096, 70), (16384, 130)])
 def test_alif_lookback_bwd(AL, dev, T, N):
     """The look-back single pass (mode 3): LV and LW against the fp32 oracle and the fp64
     adjoint, dL/dw0 and the four sums against the fp64 assembly, with float and device
-    parameters (same bits), and no bounded wait given up."""
+    parameters (the same bits: the look-back's association order is fixed), and no bounded wait
+    given up."""
     from lifscan import hip_alif
     beta, rho, q = 0.95, 0.995, 0.9
     x = _inputs(beta, 2.0, T, N, 95)
@@ -496,8 +490,8 @@ def test_alif_lookback_bwd(AL, dev, T, N):
     dp = hip_alif._dev_params(args[0], torch.tensor(beta, device=dev), rho, q, 1.0)
     got = hip_alif._alif_bwd_call(*args, None, None, None, None, ug, wg, 4.0, "lookback", 16,
                                   want_lw=True, want_params=True, dp=dp)
-    for a, b in zip((LV, LW, DW0, sums), got):  # timing decides the look-back's last bits
-        assert rel(host(b), host(a)) < 1e-6
+    for a, b in zip((LV, LW, DW0, sums), got):  # deterministic look-back: the same bits
+        assert torch.equal(a, b)
     LVo, LWo = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0)
     LV6, LW6 = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0, dtype=np.float64)
     assert rel(host(LV), LVo) < 1e-5 and rel(host(LW), LWo) < 1e-5
@@ -512,9 +506,8 @@ def test_alif_lookback_bwd(AL, dev, T, N):
 @pytest.mark.parametrize("T,N,u_r", [(1280, 130, 0.0), (512, 33, -0.2)])
 def test_alif_lookback_recompute(AL, dev, T, N, u_r):
     """The look-back pass recomputing the chunk states (lsh_alif_bwd_recompute, mode 3) agrees with
-    the look-back pass reading them, for float and device parameters: to 1e-6, since which later
-    segments a workgroup composes before it meets a published value depends on timing (the
-    chunk values themselves are the same bits; the fused pass's bit-exact test covers them)."""
+    the look-back pass reading them, for float and device parameters, bit for bit (the recomputed
+    chunk states are the stored bits, and the look-back's association order is fixed)."""
     from lifscan import hip_alif
     beta, rho, q, th = 0.95, 0.995, 0.9, 1.0
     x = _inputs(beta, 2.0, T, N, 101)
@@ -535,12 +528,12 @@ def test_alif_lookback_recompute(AL, dev, T, N, u_r):
                                    recompute_ur=u_r)
     assert hip_alif.last_bwd_spin_timeouts() == 0
     for a, b, c in zip(ref, got, got2):
-        assert rel(host(b), host(a)) < 1e-6 and rel(host(c), host(a)) < 1e-6
+        assert torch.equal(a, b) and torch.equal(a, c)
 
 
 def test_alif_layer_small_n_recompute_equals_stored(AL, dev, monkeypatch):
     """alif(fwd="serial", bwd="scan") below 8192 neurons takes the recomputing look-back pass: the
-    gradients of the look-back pass that reads the stored states, to 1e-6."""
+    gradients of the look-back pass that reads the stored states, bit for bit."""
     from lifscan import hip_alif
     beta, rho, q, T, N = 0.95, 0.995, 0.2, 1024, 200
     x = gpu(_inputs(beta, 2.0, T, N, 105), dev)
@@ -558,4 +551,4 @@ def test_alif_layer_small_n_recompute_equals_stored(AL, dev, monkeypatch):
         return [xg.grad, ug.grad, wg.grad] + [p.grad for p in ps]
 
     for a, b in zip(run(True), run(False)):
-        assert rel(host(a), host(b)) < 1e-6
+        assert torch.equal(a, b)

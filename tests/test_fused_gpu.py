@@ -138,8 +138,9 @@ def test_fused_cfg2_full_size(L, dev):
                                                   (8192, 130, False, True, 16), (256, 7, True, False, 32),
                                                   (65536, 256, True, False, 16)])
 def test_lookback_backward(dev, T, N, detach, with_gu, C):
-    """Decoupled look-back adjoint vs the fp32 serial oracle (1e-5) and fp64 (1e-4); every
-    bounded wait ended on its flag (no give-ups)."""
+    """Decoupled look-back adjoint vs the fp32 serial oracle (1e-5) and fp64 (1e-4); the same
+    bits on a second run (fixed association order); every bounded wait ended on its flag (no
+    give-ups).  (256, 7): one segment; (65536, 256): 256 segments, 16 anchor runs."""
     from lifscan import hip_lif as L
     beta = 0.95
     I = normal(T, N, 0.06, 0.2, 31)
@@ -148,9 +149,10 @@ def test_lookback_backward(dev, T, N, detach, with_gu, C):
     GU = normal(T, N, 0.0, 1.0, 34) if with_gu else None
     U, S = O.serial_forward(I, beta, 1.0, -0.1, u0)
     print(f"lookback bwd T={T} N={N} detach={detach} gu={with_gu} C={C}", flush=True)
-    Lam = L.scan_backward_lookback(gpu(I, dev), gpu(u0, dev), gpu(U, dev), gpu(S, dev), gpu(GS, dev),
-                                   gpu(GU, dev) if with_gu else None, beta, 1.0, -0.1, 4.0, detach, C=C)
+    args = [gpu(a, dev) for a in (I, u0, U, S, GS)] + [gpu(GU, dev) if with_gu else None]
+    Lam = L.scan_backward_lookback(*args, beta, 1.0, -0.1, 4.0, detach, C=C)
     assert L.last_lookback_timeouts() == 0
+    assert torch.equal(L.scan_backward_lookback(*args, beta, 1.0, -0.1, 4.0, detach, C=C), Lam)
     Lo = O.serial_backward(I, u0, U, S, GS, GU, beta, 1.0, -0.1, 4.0, detach)
     L6 = O.serial_backward(I, u0, U, S, GS, GU, beta, 1.0, -0.1, 4.0, detach, dtype=np.float64)
     assert rel(host(Lam), Lo) < 1e-5 and rel(host(Lam), L6) < 1e-4

@@ -303,6 +303,30 @@ def test_lif_auto_matches_serial(L, dev):
     assert np.array_equal(host(S), So)
 
 
+@pytest.mark.parametrize("T", [1000, 1032])
+def test_lif_auto_and_lif_param_lengths_without_a_chunk(L, dev, T):
+    """T with no chunk divisible by 16 (the scan forward's policy): lif_auto and
+    lif_param(mode="auto") run (serial forward, chunked scan adjoint at C = 8), spikes equal the
+    serial recurrence and the gradients the fp64 adjoint."""
+    from lifscan.fit import lif_param
+    N = 4096
+    I = normal(T, N, 0.12, 0.25, 40)
+    W = normal(T, N, 0.0, 1.0, 41)
+    u0 = np.zeros(N, np.float32)
+    Uo, So = O.serial_forward(I, 0.9, 1.0, 0.0, u0)
+    Lam = O.serial_backward(I, u0, Uo, So, W, None, 0.9, 1.0, 0.0, 4.0, dtype=np.float64)
+    print(f"lif_auto / lif_param T={T}", flush=True)
+    for fn in ("auto", "param"):
+        Ig = gpu(I, dev).requires_grad_(True)
+        if fn == "auto":
+            S = L.lif_auto(Ig, torch.zeros(N, device=dev), 0.9, 1.0, 0.0, 4.0)
+        else:
+            S = lif_param(Ig, torch.zeros(N, device=dev), 0.9, 1.0, 0.0, 4.0, mode="auto")
+        (gpu(W, dev) * S).sum().backward()
+        assert np.array_equal(host(S), So), fn
+        assert rel(host(Ig.grad), Lam) < REL_FP64, fn
+
+
 def test_cfg2_scan_equals_serial_full_size(L, dev):
     """BASELINE cfg2 at full size (65,536 x 4,096, beta in {0.9, 0.99}, K=8, repair on):
     spikes and potentials of the scan equal the serial kernel's everywhere, and 512 columns
@@ -374,9 +398,11 @@ def test_scan_v4_rejects_bad_shapes(L, dev):
 
 @pytest.mark.parametrize("T,N", [(1, 1), (63, 64), (64, 100), (65, 7), (1000, 130), (4113, 1029)])
 @pytest.mark.parametrize("detach,with_gu", [(True, False), (True, True), (False, True)])
-def test_serial_backward_pipe_equals_one_wave(L, dev, T, N, detach, with_gu):
-    """The producer/consumer serial adjoint gives the one-wave kernel's Lam bit for bit (full and
-    partial tiles, ragged neuron blocks, detached or not, with and without GU)."""
+def test_serial_backward_pipe(L, dev, T, N, detach, with_gu):
+    """The producer/consumer serial adjoint (full and partial tiles, ragged neuron blocks,
+    detached or not, with and without GU) against the fp32 oracle; detached without GU it gives
+    the one-wave kernel's Lam (lif_param's serial adjoint) bit for bit."""
+    from lifscan.fit import _param_backward
     I = normal(T, N, 0.1, 0.5, 61)
     u0 = uniform(N, -0.2, 0.6, 62)
     GS = normal(T, N, 0.0, 1.0, 63)
@@ -384,30 +410,23 @@ def test_serial_backward_pipe_equals_one_wave(L, dev, T, N, detach, with_gu):
     U, S = O.serial_forward(I, 0.93, 1.0, 0.1, u0)
     args = [gpu(a, dev) for a in (I, u0, U, S, GS)] + [gpu(GU, dev) if with_gu else None]
     print(f"serial bwd pipe T={T} N={N} detach={detach} gu={with_gu}", flush=True)
-    prev = L.serial_pipe_max_blocks(0)
-    try:
-        ref = L.serial_backward(*args, 0.93, 1.0, 0.1, 4.0, detach)
-        L.serial_pipe_max_blocks(1 << 20)
-        got = L.serial_backward(*args, 0.93, 1.0, 0.1, 4.0, detach)
-    finally:
-        L.serial_pipe_max_blocks(prev)
-    assert torch.equal(got, ref)
+    got = L.serial_backward(*args, 0.93, 1.0, 0.1, 4.0, detach)
+    ref = O.serial_backward(I, u0, U, S, GS, GU, 0.93, 1.0, 0.1, 4.0, detach)
+    assert rel(host(got), ref) < REL_FP32
+    if detach and not with_gu:
+        one_wave, _ = _param_backward(*args[:5], 0.93, 1.0, 0.1, 4.0, "serial")
+        assert torch.equal(got, one_wave)
 
 
 @pytest.mark.parametrize("T,N", [(1, 1), (63, 64), (64, 100), (65, 7), (1000, 130), (4113, 1029)])
 def test_serial_forward_pipe_equals_one_wave(L, dev, T, N):
-    """The producer/consumer serial forward gives the one-wave kernel's U, S and the oracle's,
-    bit for bit."""
+    """The producer/consumer serial forward gives the oracle's U, S bit for bit, and the one-wave
+    replay kernel's (the two-level scan with one chunk of T steps and no repair replays from u0)."""
     I = normal(T, N, 0.15, 0.5, 65)
     u0 = uniform(N, -0.2, 0.9, 66)
     Ur, Sr = O.serial_forward(I, 0.93, 1.0, 0.1, u0)
     print(f"serial fwd pipe T={T} N={N}", flush=True)
-    prev = L.serial_pipe_max_blocks(0)
-    try:
-        U1, S1 = L.serial_forward(gpu(I, dev), 0.93, 1.0, 0.1, gpu(u0, dev))
-        L.serial_pipe_max_blocks(1 << 20)
-        U2, S2 = L.serial_forward(gpu(I, dev), 0.93, 1.0, 0.1, gpu(u0, dev))
-    finally:
-        L.serial_pipe_max_blocks(prev)
-    assert torch.equal(U1, U2) and torch.equal(S1, S2)
-    assert np.array_equal(host(U2), Ur) and np.array_equal(host(S2), Sr)
+    U, S = L.serial_forward(gpu(I, dev), 0.93, 1.0, 0.1, gpu(u0, dev))
+    U1, S1 = L.scan_forward_v3(gpu(I, dev), 0.93, 1.0, 0.1, gpu(u0, dev), C=T, K=1, repair=0)
+    assert np.array_equal(host(U), Ur) and np.array_equal(host(S), Sr)
+    assert torch.equal(U, U1) and torch.equal(S, S1)

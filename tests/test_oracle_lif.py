@@ -220,6 +220,58 @@ def test_envelope_is_below_the_trajectory(beta, mu, sd):
     assert (Lo <= starts).all()
 
 
+@pytest.mark.parametrize("beta,mu,sd", [(0.9, 0.12, 0.25), (0.99, 0.012, 0.08), (0.5, -0.1, 0.6),
+                                        (1.0, 0.05, 0.3)])
+def test_envelope_bound_equals_stepwise_brute_force(beta, mu, sd):
+    """Lo at every chunk start against the stepwise envelope l_t = min(u_r, beta*l_{t-1} + x_t),
+    l_0 = u0, run in fp64 over all T steps, minus the margin 1e-5(|l| + 1): two-sided, to 3e-6
+    (|l| + 1) (the fp32 chunk sums of 64 steps round to ~1e-6 at beta = 1), so a wrong margin, a
+    dropped min or a wrong composition fails (a bound that is merely below the trajectory would
+    pass test_envelope_is_below_the_trajectory)."""
+    T, N, C, u_r = 1024, 256, 64, -0.1
+    I = normal(T, N, mu, sd, 10)
+    u0 = uniform(N, -0.3, 0.9, 11)
+    EC, EA, EB = O.envelope_chunks(I, beta, u_r, C)
+    Lo = O.envelope_carry(u0, EC, EA, EB)
+    l = u0.astype(np.float64)
+    b = np.float64(np.float32(beta))
+    want = np.empty((T // C, N))
+    for t in range(T):
+        if t % C == 0:
+            want[t // C] = l - 1e-5 * (np.abs(l) + 1.0)
+        l = np.minimum(np.float64(np.float32(u_r)), b * l + I[t].astype(np.float64))
+    assert np.all(np.abs(Lo - want) <= 3e-6 * (np.abs(want) + 1.0))
+
+
+def test_envelope_chunk_map_is_the_closed_form_composition():
+    """On dyadic inputs (beta = 1/2, x on a 1/64 grid, 8-step chunks: every fp32 operation is
+    exact) the chunk map l -> min(c, a*l + b) equals the 8-step min-affine recurrence from
+    every entry l exactly, with a = beta^8 (the composition lemma of paper/main.tex:266-272)."""
+    C, N = 8, 64
+    g = np.random.default_rng(3)
+    I = (g.integers(-32, 48, size=(4 * C, N)) / 64.0).astype(np.float32)
+    EC, EA, EB = O.envelope_chunks(I, 0.5, 0.0, C)
+    assert np.all(EA == np.float32(0.5 ** C))
+    for l0 in (np.float32(-3.0), np.float32(-0.25), np.float32(0.0), np.float32(0.75)):
+        for m in range(I.shape[0] // C):
+            l = np.full(N, l0, np.float32)
+            for t in range(m * C, (m + 1) * C):
+                l = np.minimum(np.float32(0.0), np.float32(0.5) * l + I[t])
+            got = np.minimum(EC[m], EA[m] * l0 + EB[m])
+            assert np.array_equal(got, l), (l0, m)
+
+
+def test_long_sequence_fp64_adjoint_equals_the_serial_one():
+    T, N = 4096, 32
+    I = normal(T, N, 0.012, 0.08, 51)
+    u0 = uniform(N, 0.0, 1.0, 52)
+    GS = normal(T, N, 0.0, 1.0, 53)
+    U, S = O.serial_forward(I, 0.99, 1.0, 0.0, u0)
+    ref = O.serial_backward(I, u0, U, S, GS, None, 0.99, 1.0, 0.0, 4.0, dtype=np.float64)
+    got = O.serial_backward_long(I, u0, U, S, GS, 0.99, 1.0, 0.0, 4.0, block=256)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 1e-12
+
+
 REGIMES = [(b, mu, sd) for b in (0.5, 0.9, 0.99, 1.0) for (mu, sd) in ((0.15, 0.4), (-0.1, 0.6), (0.4, 0.2))]
 
 

@@ -50,3 +50,19 @@ def test_long_sequence_plan():
     assert L.long_sequence_plan(2 ** 19, 512) == (4096, 1)
     assert L.long_sequence_plan(65536, 1000) == (1024, 1)
     assert L.long_sequence_plan(4096, 65536) == (0, 1)             # single pass
+
+
+def test_auto_policies_accept_lengths_the_chunk_policy_rejects():
+    """lif_auto / lif_param(mode="auto") run for every T: a pass whose chunk policy has no
+    chunk for T stays serial, and the recomputing-pair test answers False instead of raising
+    (T = 1000 and 1032 have no chunk divisible by 16; T = 1002 none divisible by 2 either)."""
+    from lifscan import hip_lif as L
+    for T in (1000, 1032, 257, 1002):
+        assert L._recompute_ok(T, 65536, 16, 10 ** 6) is False
+        assert L._recompute_ok(T, 4096, 16, T) is False
+    assert L.auto_modes(4096, 1000) == ("serial", "scan")
+    assert L.auto_modes(4096, 1032) == ("serial", "scan")
+    assert L.auto_modes(4096, 1002) == ("serial", "serial")
+    assert L.auto_modes(1024, 16386) == ("serial", "serial")   # 16386 = 2 * 8193
+    assert L.auto_modes(1024, 16392) == ("serial", "scan")     # chunk 8 for the adjoint only
+    assert L._recompute_ok(4096, 65536, 16, 10 ** 6) is True

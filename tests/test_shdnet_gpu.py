@@ -23,9 +23,11 @@ def _raster(T, B, seed):
     return (torch.rand(T, B, 700, generator=g) < 0.015).float()
 
 
-def test_net_scan_equals_serial_and_oracle(dev):
+@pytest.mark.parametrize("T,B", [(256, 8), (1024, 64)])  # (1024, 64): BASELINE cfg3
+def test_net_scan_equals_serial_and_oracle(dev, T, B):
+    """experiments/e7c_timing.py's step (cross-entropy on the logits, backward) in scan and
+    serial mode, on a Bernoulli(0.015) raster."""
     from lifscan.shdnet import Net
-    T, B = 256, 8
     x = _raster(T, B, 3).to(dev)
     y = torch.randint(0, 20, (B,), generator=torch.Generator().manual_seed(5)).to(dev)
     nets, out = {}, {}
@@ -39,15 +41,16 @@ def test_net_scan_equals_serial_and_oracle(dev):
         loss.backward()
         nets[mode] = net
         out[mode] = (logits.detach(), s1, s2)
-        print(f"shdnet {mode} loss {loss.item():.6f}", flush=True)
+        print(f"shdnet T={T} B={B} {mode} loss {loss.item():.6f}", flush=True)
     assert torch.equal(out["scan"][0], out["serial"][0])
     assert torch.equal(out["scan"][1], out["serial"][1]) and torch.equal(out["scan"][2], out["serial"][2])
     for (n1, p1), (n2, p2) in zip(nets["scan"].named_parameters(), nets["serial"].named_parameters()):
         assert rel(host(p1.grad), host(p2.grad)) < 1e-5, n1
     # layer 1 against the oracle: current = fc(x), spikes and dL/dI
     net = nets["scan"]
-    with torch.no_grad():
-        I1 = net.l1.fc(x).reshape(T, -1).contiguous()
+    with torch.no_grad():  # the layer's own current computation (one GEMM over T*B rows)
+        I1 = torch.nn.functional.linear(x.reshape(T * B, -1), net.l1.fc.weight,
+                                        net.l1.fc.bias).reshape(T, -1).contiguous()
     I1h = host(I1)
     N1 = I1h.shape[1]
     u0 = np.zeros(N1, np.float32)

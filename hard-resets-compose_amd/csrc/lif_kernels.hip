@@ -876,6 +876,7 @@ extern "C" const char* lsh_status_string(int status) {
     case LSH_ERR_DIVISIBILITY: return "T must be divisible by the chunk length (and M by G)";
     case LSH_ERR_WORKSPACE: return "workspace too small or not 256-byte aligned";
     case LSH_ERR_HIP: return "HIP launch/runtime error";
+    case LSH_ERR_SCRATCH: return "problem larger than the static scratch array of the _noalloc entry";
     default: return "unknown status";
   }
 }

@@ -20,6 +20,8 @@
 // workgroups already running, so the waits end; each is bounded all the same (a give-up is
 // counted in the header and the result is then not valid).  Flags and aggregates cross XCDs;
 // they go through coherent vector atomics only (see ld_coh / st_coh / publish_flag).
+#include <mutex>
+
 #include "lsh_abi.h"
 #include "lsh_common.h"
 #include "lsh_lookback.h"
@@ -286,6 +288,49 @@ extern "C" int lsh_lif_scan_lookback_bwd(const float* I, const float* u0, const 
                        detach != 0, st);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// The look-back adjoint without a workspace argument (lsh_lif_scan_lookback_bwd_noalloc), for
+// callers that cannot allocate: its workspace (header, segment aggregates, flags) is `scratch`,
+// a static device array that every device the library runs on holds until the process ends.
+// The array's name is a host-side stand-in in host code: its device address is taken once per
+// device with hipGetSymbolAddress (with that device current) and kept in g_scratch_ptr, and only
+// that address reaches kernels.  The header and the flags are cleared by kernels at every call
+// (no memset node), so the array needs no initial contents.
+static __device__ __align__(256) unsigned char scratch[LSH_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64];  // per device; set on the first call on that device
+
+static void* scratch_address() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess) return nullptr;
+    g_scratch_ptr[dev] = p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+extern "C" int lsh_lif_scan_lookback_bwd_noalloc(const float* I, const float* u0, const float* U,
+                                                 const float* S, const float* GS, const float* GU,
+                                                 float* Lam, int64_t T, int64_t N, float beta,
+                                                 float theta, float u_r, float alpha, int detach,
+                                                 int C, void* stream) {
+  if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(GS) || bad_ptr(Lam))
+    return LSH_ERR_ARG;
+  if (T < 0 || N < 0 || N > (int64_t)1 << 31) return LSH_ERR_SHAPE;
+  if (C != 16 && C != 32) return LSH_ERR_SHAPE;
+  if (T % kLookbackSeg != 0) return LSH_ERR_DIVISIBILITY;
+  if (lsh_lif_scan_lookback_bwd_workspace(T, N) > (size_t)LSH_NOALLOC_SCRATCH_BYTES)
+    return LSH_ERR_SCRATCH;
+  void* ws = scratch_address();
+  if (ws == nullptr) return LSH_ERR_HIP;
+  return lsh_lif_scan_lookback_bwd(I, u0, U, S, GS, GU, Lam, T, N, beta, theta, u_r, alpha, detach,
+                                   C, ws, (size_t)LSH_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int lsh::lif_param_bwd_lookback(const float* I, const float* u0, const float* U, const float* S,

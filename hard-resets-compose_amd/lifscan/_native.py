@@ -20,6 +20,7 @@ LSH_ERR_SHAPE = -2
 LSH_ERR_DIVISIBILITY = -3
 LSH_ERR_WORKSPACE = -4
 LSH_ERR_HIP = -5
+LSH_ERR_SCRATCH = -6
 
 c_p = ctypes.c_void_p
 c_i64 = ctypes.c_int64
@@ -119,6 +120,8 @@ SIGNATURES = {
     "lsh_lif_scan_lookback_bwd_workspace": (c_sz, [c_i64, c_i64]),
     "lsh_lif_scan_lookback_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f,
                                         c_f, c_i, c_i, c_p, c_sz, c_p]),
+    "lsh_lif_scan_lookback_bwd_noalloc": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f,
+                                                c_f, c_f, c_f, c_i, c_i, c_p]),
     "lsh_lif_param_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f,
                                 c_i, c_i, c_p, c_sz, c_p]),
     "lsh_alif_bwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f,
@@ -173,7 +176,7 @@ def check(rc, what):
     if rc == LSH_OK:
         return
     msg = f"{what}: {lib().lsh_status_string(rc).decode()} (status {rc})"
-    if rc in (LSH_ERR_ARG, LSH_ERR_SHAPE, LSH_ERR_DIVISIBILITY):
+    if rc in (LSH_ERR_ARG, LSH_ERR_SHAPE, LSH_ERR_DIVISIBILITY, LSH_ERR_SCRATCH):
         raise ValueError(msg)
     raise RuntimeError(msg)
 

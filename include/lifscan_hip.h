@@ -35,6 +35,7 @@ extern "C" {
 #define LSH_ERR_DIVISIBILITY (-3) /* T % C != 0 (or M % G != 0) */
 #define LSH_ERR_WORKSPACE (-4)    /* workspace too small or misaligned */
 #define LSH_ERR_HIP (-5)          /* HIP launch / runtime error */
+#define LSH_ERR_SCRATCH (-6)      /* problem larger than the static scratch array (_noalloc) */
 
 /* Library identity. */
 int lsh_abi_version(void);
@@ -272,6 +273,22 @@ int lsh_lif_scan_lookback_bwd(const float* I, const float* u0, const float* U, c
                               const float* GS, const float* GU, float* Lam, int64_t T, int64_t N,
                               float beta, float theta, float u_r, float alpha, int detach, int C,
                               void* ws, size_t ws_bytes, void* stream);
+
+/* lsh_lif_scan_lookback_bwd with no workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Its workspace is a static device array of
+ * LSH_NOALLOC_SCRATCH_BYTES (64 MiB) that every device the library runs on holds until the process
+ * ends; its address is looked up once per device (with that device current) on the first call.
+ * Returns LSH_ERR_SCRATCH, launching nothing, when lsh_lif_scan_lookback_bwd_workspace(T, N)
+ * exceeds it (about T * N <= 1.4e9 neuron-steps: N = 1024, T = 2^20 fits).  Calls no allocating
+ * routine.  Every call on one device shares its array (the call clears what must start at zero):
+ * calls that overlap on one device, from several streams or threads, race.  Same outputs as
+ * lsh_lif_scan_lookback_bwd, bit for bit. */
+#define LSH_NOALLOC_SCRATCH_BYTES (64u << 20)
+int lsh_lif_scan_lookback_bwd_noalloc(const float* I, const float* u0, const float* U,
+                                      const float* S, const float* GS, const float* GU, float* Lam,
+                                      int64_t T, int64_t N, float beta, float theta, float u_r,
+                                      float alpha, int detach, int C, void* stream);
 
 /* LIF adjoint with the neuron-parameter gradients of fit.py LIFParamFn.backward
  * (fit.py:30-48): Lam as lsh_lif_*_bwd with the reset detached and no GU, plus per block

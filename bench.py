@@ -25,6 +25,7 @@ measured after the headline and reported under "other_configs" (--headline-only 
   python bench.py [--steps K] [--warmup W] [--no-cpu] [--headline-only]
   python bench.py --only cfg4        # one other configuration (profiling runs)
   python bench.py --dominant-only    # short run for rocprofv3 --pmc passes (copy + kernel)
+  python bench.py --counters-workload  # the non-HBM-bound kernels once each (counter passes)
 """
 import argparse
 import json
@@ -542,6 +543,51 @@ def dominant_only(L, torch, dev):
                       "kernel": "k_lif_bwd_fused<32, 4, true, false, 0, true>", "launches": 3}))
 
 
+def counters_workload(torch, dev):
+    """Short program for counter passes (rocprofv3 --pmc) over the kernels that are not HBM-bound
+    by design, each launched once or twice at its configuration: a 256 MiB copy (FETCH/WRITE
+    calibration); cfg5's box scan with repair (k_alif_build<4,4>, k_alif_carry, k_alif_repair);
+    cfg2's map scan at C = 128, K = 8 (k_lif_build<8,8>, k_lif_carry<8>); cfg4's converged v3 in
+    pieces (k_lif_build<32,8>, k_lif_carry_staged<32>), its v4 at C 2048 / G 4 / K 32 / K2 64 and at
+    the reference default (k_lif_compose, k_map_carry) and its look-back adjoint
+    (k_lif_bwd_lookback<16,16,...>)."""
+    from lifscan import hip_lif as L
+    from lifscan import triton_alif as A
+    x = torch.empty(64 * 2 ** 20, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    del x, y
+    torch.cuda.synchronize()
+    log("counters: cfg5 box scan")
+    T, N, b, r, q, C = 4096, 16384, 0.95, 0.995, 0.2, 128
+    I = (0.15 + 0.3 * torch.randn(T, N, generator=torch.Generator().manual_seed(0))).to(dev)
+    z = torch.zeros(N, device=dev)
+    WP = A.alif_warm_predict(I, b, r, q, 1.0, 0.0, z, z, C, Wn=4)
+    A.alif_scan_forward(I, b, r, q, 1.0, 0.0, z, z, WP, 0.1 * q, C=C, K1=32, K2=32, BN=4, repair=10 ** 6)
+    torch.cuda.synchronize()
+    del I, WP
+    log("counters: cfg2 map scan")
+    _, I, _ = inputs(0.9, dev)
+    u0 = torch.zeros(N_CFG, device=dev)
+    L.scan_forward_mapscan(I, 0.9, 1.0, 0.0, u0, C=128, K=8, repair=10 ** 6)
+    torch.cuda.synchronize()
+    del I
+    torch.cuda.empty_cache()
+    log("counters: cfg4")
+    T, N = 2 ** 20, 1024
+    I = (0.012 + 0.08 * torch.randn(T, N, generator=torch.Generator().manual_seed(0))).to(dev)
+    u0 = torch.rand(N, generator=torch.Generator().manual_seed(2)).to(dev)
+    U, S = L.scan_forward_v3(I, 0.99, 1.0, 0.0, u0, C=256, K=16, repair=10 ** 6)
+    for C, G, K, K2 in ((2048, 4, 32, 64), (64, 16, 16, 32)):
+        L.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
+        torch.cuda.synchronize()
+    gS = torch.randn(T, N, generator=torch.Generator().manual_seed(1)).to(dev)
+    L.scan_backward_tiled(I, u0, U, S, gS, None, 0.99, 1.0, 0.0, 4.0)
+    torch.cuda.synchronize()
+    print(json.dumps({"counters_workload": True}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -550,6 +596,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-cols", type=int, default=8192)
     ap.add_argument("--dominant-only", action="store_true")
+    ap.add_argument("--counters-workload", action="store_true",
+                    help="run each non-HBM-bound kernel once at its configuration (counter passes)")
     ap.add_argument("--headline-only", action="store_true",
                     help="skip the cfg3 / cfg4 / cfg5 / affine-reset measurements")
     ap.add_argument("--only", choices=("cfg3", "cfg4", "cfg5", "affine"),
@@ -569,6 +617,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.dominant_only:
         dominant_only(L, torch, dev)
+        return
+    if args.counters_workload:
+        counters_workload(torch, dev)
         return
     if args.only:
         fn = {"cfg3": bench_cfg3, "cfg4": bench_cfg4, "cfg5": bench_cfg5,

@@ -236,10 +236,13 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
   constexpr int GW = BLK > 2 ? BLK / 2 : 1;       // waves per split-decision block
   static_assert(BLK <= 2 || GW == NW, "a split-decision block is one workgroup");
   constexpr int TS = kAlifTS;
-  __shared__ float sX[kAlifNPW][TS], sS[kAlifNPW][TS], sC[kAlifNPW][TS], sHi[kAlifNPW][TS],
-      sLo[kAlifNPW][TS], sR[TS];
+  // one padding column per row: the neurons of a wave read the same step of different rows
+  // (and phases (a), (c) walk rows in step), which a 64-float row stride would put on one bank
+  constexpr int TSP = TS + 1;
+  __shared__ float sX[kAlifNPW][TSP], sS[kAlifNPW][TSP], sC[kAlifNPW][TSP], sHi[kAlifNPW][TSP],
+      sLo[kAlifNPW][TSP], sR[TS];
   __shared__ float sA[kAlifNPW], sB[kAlifNPW], sLU[kAlifNPW], sHU[kAlifNPW], sHW[kAlifNPW];
-  __shared__ int s_cut[NW];
+  __shared__ int s_cut[2][NW];  // per-step split flags, double-buffered by step parity
   __shared__ int s_slot[NW][WAVE];
   const int64_t m = blockIdx.x / NBLK;
   const int blk = (int)(blockIdx.x - m * NBLK);
@@ -272,14 +275,22 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
   int npc = 0;
   int ovf = 0;
   const unsigned long long hmask = 0xffffffffull << hb;
-  const float* __restrict__ Ipn = I + (size_t)m * C * N + pnn;
+  const int64_t n0 = (int64_t)blk * kAlifNPW;
+  const float* __restrict__ Iblk = I + (size_t)m * C * N;
+  int kstep = 0;  // steps done in this chunk (parity of the split flags)
   for (int j0 = 0; j0 < C; j0 += TS) {
     const int ts = min(TS, C - j0);
-    // (a) sequential recurrences, inputs staged
+    // (a0) the tile's inputs, staged by every thread of the workgroup (neuron-contiguous runs)
+    for (int e = tid; e < kAlifNPW * ts; e += NW * WAVE) {
+      const int k = e / kAlifNPW, nu = e - k * kAlifNPW;
+      const int64_t nq = n0 + nu < N ? n0 + nu : N - 1;
+      sX[nu][k] = Iblk[(size_t)(j0 + k) * N + nq];
+    }
+    __syncthreads();
+    // (a) sequential recurrences
     if (tid < kAlifNPW) {
       for (int k = 0; k < ts; ++k) {
-        const float x = Ipn[(size_t)(j0 + k) * N];
-        sX[tid][k] = x;
+        const float x = sX[tid][k];
         pA = beta * pA;
         pB = lif_v(pB, x, beta);
         sS[tid][k] = pA;  // A_j, replaced by sj in (b)
@@ -327,14 +338,17 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
       } else if (BLK == 2) {
         cut = cb != 0ull;
       } else {
-        if (lane == 0) s_cut[wv] = cb != 0ull ? 1 : 0;
+        // one barrier per step: the flags of step k + 2 reuse this step's buffer only after the
+        // barrier of step k + 1, which every wave passes after reading this step's flags
+        const int par = kstep & 1;
+        if (lane == 0) s_cut[par][wv] = cb != 0ull ? 1 : 0;
         __syncthreads();
         int any = 0;
 #pragma unroll
-        for (int kk = 0; kk < GW; ++kk) any |= s_cut[kk];
-        __syncthreads();
+        for (int kk = 0; kk < GW; ++kk) any |= s_cut[par][kk];
         cut = any != 0;
       }
+      ++kstep;
       if (cut) {
         const float z = rr / pa;
         const int nout = (es ? 1 : 0) + (en ? 1 : 0);
@@ -603,6 +617,65 @@ __global__ __launch_bounds__(256) void k_alif_repair(
     __syncthreads();
   }
   if (tid == 0) atomicMax(&hdr->repair_iters, (unsigned int)rounds);
+}
+
+// Repair to convergence in one ordered pass over each neuron's chunks (lsh_alif_scan_fwd with
+// repair = -1; the result of Jacobi rounds run until nothing changes, which is the serial
+// recurrence): chunk m's exact entry is chunk m-1's exact exit; a chunk whose carried start
+// (u, w) differs from it in any bit is replayed from it, which writes its U, W, S and gives its
+// exact exit; a chunk whose start agrees keeps its replay and its exit.  Every chunk is replayed
+// at most once more, where the Jacobi rounds advance the exact prefix by one chunk per round
+// when the carried w agrees with the exact one only to rounding (20 rounds at cfg5).  One lane
+// per neuron; the wave runs a chunk's replay when any of its lanes needs it (lanes that do not
+// store nothing), with the chunk's inputs streamed 16 rows ahead and the next chunk's starts
+// and exits loaded during the current one.
+__global__ __launch_bounds__(64) void k_alif_chain(
+    const float* __restrict__ I, float* __restrict__ U, float* __restrict__ W, float* __restrict__ S,
+    const float* __restrict__ su, const float* __restrict__ sw, const float* __restrict__ eu,
+    const float* __restrict__ ew, int64_t N, int M, int C, float beta, float rho, float q,
+    float theta0, float u_r) {
+  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
+  const bool valid = n < N;
+  const int64_t nn = valid ? n : N - 1;
+  float xu = eu[nn], xw = ew[nn];  // exact exit of chunk 0 (its start, (u0, w0), is exact)
+  float nsu = 0.0f, nsw = 0.0f, neu = 0.0f, new_ = 0.0f;
+  if (M > 1) {
+    const size_t o1 = (size_t)N + nn;
+    nsu = su[o1];
+    nsw = sw[o1];
+    neu = eu[o1];
+    new_ = ew[o1];
+  }
+  for (int m = 1; m < M; ++m) {
+    const float csu = nsu, csw = nsw, ceu = neu, cew = new_;
+    if (m + 1 < M) {  // the next chunk's starts and exits, loaded while this one runs
+      const size_t on = (size_t)(m + 1) * N + nn;
+      nsu = su[on];
+      nsw = sw[on];
+      neu = eu[on];
+      new_ = ew[on];
+    }
+    const bool redo = valid && !(same_bits(xu, csu) && same_bits(xw, csw));
+    if (__ballot(redo) != 0ull) {
+      float u = xu, w = xw;
+      const size_t base = (size_t)m * C * N + nn;
+      stream_rows<16>(I + base, (size_t)N, C, [&](int64_t j, float x) {
+        bool s;
+        u = alif_step(u, w, x, beta, rho, q, theta0, u_r, s);
+        if (redo) {
+          const size_t o = base + (size_t)j * N;
+          st_nt(U + o, u);
+          st_nt(W + o, w);
+          st_nt(S + o, s ? 1.0f : 0.0f);
+        }
+      });
+      xu = redo ? u : ceu;
+      xw = redo ? w : cew;
+    } else {
+      xu = ceu;
+      xw = cew;
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1541,7 +1614,7 @@ extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w
   if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(w0) || bad_ptr(Wpred) || bad_ptr(U) || bad_ptr(W) ||
       bad_ptr(S) || bad_ptr(ws))
     return LSH_ERR_ARG;
-  if (repair < 0) return LSH_ERR_ARG;
+  if (repair < -1) return LSH_ERR_ARG;
   const int rc = alif_scan_check(T, N, C, K1, K2, block);
   if (rc != LSH_OK) return rc;
   lsh_alif_layout L;
@@ -1587,7 +1660,10 @@ extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w
   launch_alif_fwd<16>(I, F(L.SU), F(L.SW), U, W, S, F(L.EU), F(L.EW), N, C, M, beta, rho, q, theta0,
                       u_r, st);
   mark(4);
-  if (repair > 0 && M > 1) {
+  if (repair == -1 && M > 1) {
+    hipLaunchKernelGGL(k_alif_chain, dim3((unsigned)NB), dim3(WAVE), 0, st, I, U, W, S, F(L.SU),
+                       F(L.SW), F(L.EU), F(L.EW), N, M, C, beta, rho, q, theta0, u_r);
+  } else if (repair > 0 && M > 1) {
     const int64_t rounds = repair < (int64_t)M ? repair : (int64_t)M;
     hipLaunchKernelGGL(k_alif_repair, dim3((unsigned)NB), dim3(256), 0, st, I, U, W, S, F(L.SU),
                        F(L.SW), F(L.EU), F(L.EW), Iq(L.LIST0), Iq(L.LIST1), h, N, M, C, rounds, beta,

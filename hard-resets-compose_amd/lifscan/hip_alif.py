@@ -152,12 +152,25 @@ def _rho_pow_c(rho, C):
     return float(torch.tensor(_f32(rho), dtype=torch.float32) ** C)
 
 
+def _repair_arg(repair, M, stats):
+    """The C entry's repair argument: -1 (ordered chain to convergence) for a converged repair
+    whose round count nobody reads, else the Jacobi round budget."""
+    repair = int(repair)
+    if repair < 0:
+        raise ValueError("repair must be >= 0")
+    return -1 if (stats is None and repair >= M and M > 1) else repair
+
+
 def alif_scan_forward(I, beta, rho, q, theta0, u_r, u0, w0, Wpred, dw, C=128, K1=16, K2=32, BN=16,
                       nw=1, BNc=1, BNr=32, D=4, repair=0, stats=None, phases=None):
     """Exact ALIF scan with a predicted adaptation box (triton_alif.py:301-358) -> (U, W, S).
     Wpred: [T//C, N] predicted entry adaptation (row 0 is replaced by w0); dw: box half-width.
     stats: repair_iters, miss_frac, overflow_frac, mean_lines, mean_pieces, max_pieces.
-    phases: per-phase GPU times in ms (envelope, build, carry, replay)."""
+    phases: per-phase GPU times in ms (envelope, build, carry, replay).
+    With repair >= T//C (converged) and no stats, the repair is one ordered pass over each
+    neuron's chunks (replaying a chunk once from its predecessor's exact exit where its carried
+    start differs) instead of Jacobi rounds: the same result, the serial recurrence, without the
+    round count that stats would report."""
     global _LAST_ALIF
     I = _input(I)
     T, N = I.shape
@@ -186,7 +199,8 @@ def alif_scan_forward(I, beta, rho, q, theta0, u_r, u0, w0, Wpred, dw, C=128, K1
         _n.check(L.lsh_alif_scan_fwd(
             _n.ptr(I), _n.ptr(u0), _n.ptr(w0), _n.ptr(Wp), _f32(dw), _n.ptr(U), _n.ptr(W), _n.ptr(S),
             T, N, _f32(beta), _f32(rho), _f32(q), _f32(theta0), _f32(u_r), _rho_pow_c(rho, C), C, K1,
-            K2, BN, int(repair), _n.ptr(ws), nbytes, ev_arr, _n.stream_of(I)), "lsh_alif_scan_fwd")
+            K2, BN, _repair_arg(repair, M, stats), _n.ptr(ws), nbytes, ev_arr, _n.stream_of(I)),
+            "lsh_alif_scan_fwd")
     _LAST_ALIF = _ALIFRun(ws, T, N, C, K1, K2)
     if phases is not None:
         torch.cuda.synchronize(I.device)

@@ -241,7 +241,11 @@ int lsh_alif_warm_predict(const float* I, const float* u0, const float* w0, cons
  * device.  `block` neurons share the per-step decision to split pieces (the reference's
  * Triton BN; 1, 2, 4, 8 or 16).  rhoC = rho^C as fp32 (computed by the caller).  Replaces
  * triton_alif.py:301-358 (alif_scan_forward), :96-186 (build), :214-252 (carry).
- * K1 <= 32, K2 <= 32 and a power of two, T % C == 0. */
+ * K1 <= 32, K2 <= 32 and a power of two, T % C == 0.  repair: the maximum number of Jacobi
+ * rounds (0 = none; T/C or more converges, stats' repair_iters counts them), or -1: repair to
+ * convergence by one ordered pass over every neuron's chunks (each chunk whose carried start
+ * differs from the previous chunk's exact exit is replayed once from it): the same U, W, S as
+ * converged Jacobi rounds, the serial recurrence; repair_iters is then not counted (0). */
 typedef struct lsh_alif_layout {
   size_t EC, EA, EB, LU, HU, LW, HW; /* envelope maps, box [M, N] */
   size_t MA, MB, NL, NP, OVF;        /* per-chunk scalars [M, N] (NL, NP, OVF int32) */

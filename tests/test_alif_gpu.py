@@ -142,7 +142,8 @@ def test_alif_box_scan_matches_oracle(AL, dev, name, beta, rho, q, block):
 @pytest.mark.parametrize("mfree", [0.5, 2.0])
 def test_alif_box_scan_with_repair_equals_serial(AL, dev, name, beta, rho, q, mfree):
     """The reference's contract (tests/test_alif.py:10-39): with repair the box scan equals the
-    serial recurrence for any prediction, good or bad."""
+    serial recurrence for any prediction, good or bad; with the Jacobi rounds (stats requested)
+    and with the ordered chain pass (no stats)."""
     T, N, C = 4096, 200, 128
     I = _inputs(beta, mfree, T, N, 11)
     u0 = np.zeros(N, np.float32)
@@ -157,6 +158,11 @@ def test_alif_box_scan_with_repair_equals_serial(AL, dev, name, beta, rho, q, mf
                                            C=C, K1=16, K2=32, BN=block, repair=10 ** 6, stats=st)
             assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), (tag, block)
             assert np.array_equal(host(S), Sr), (tag, block)
+            # without stats the converged repair is the ordered chain pass: the same result
+            U, W, S = AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, gpu(Wp, dev), 0.1 * q,
+                                           C=C, K1=16, K2=32, BN=block, repair=10 ** 6)
+            assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), (tag, block, "chain")
+            assert np.array_equal(host(S), Sr), (tag, block, "chain")
             if T * N <= 4096 * 200 and block == 4 and tag in ("oracle", "bad"):
                 A.scan_forward(I, beta, rho, q, 1.0, 0.0, u0, w0, Wp, 0.1 * q, C=C, K1=16, K2=32,
                                block=block, repair=10 ** 6, stats=sto)

@@ -169,7 +169,8 @@ def test_cfg5_box_scan_with_repair_equals_serial(dev):
     """cfg5's box scan (C = 128, K1 = K2 = 32, block 4) with repair equals the serial forward bit
     for bit for both chunk-entry predictions of the reference's protocol (the warm-up predictor
     with Wn = 4, and the previous iterate emulated by a 1.005x input,
-    experiments/e25d_alif_fwd.py:44-50) at dw = 0.1q and 0.3q."""
+    experiments/e25d_alif_fwd.py:44-50) at dw = 0.1q and 0.3q, with the Jacobi rounds (stats
+    requested) and with the ordered chain pass (no stats)."""
     from lifscan import triton_alif as AL
     c = CFG5
     I, z = _cfg5_inputs(dev)
@@ -187,6 +188,9 @@ def test_cfg5_box_scan_with_repair_equals_serial(dev):
                                               BN=4, repair=10 ** 6, stats=st)
             assert torch.equal(U2, U) and torch.equal(W2, W) and torch.equal(S2, S), (name, dwq, st)
             print(f"  stats {st}", flush=True)
+            U2, W2, S2 = AL.alif_scan_forward(I, b, r, q, 1.0, 0.0, z, z, WP, dwq * q, C=C, K1=32, K2=32,
+                                              BN=4, repair=10 ** 6)  # no stats: the ordered chain
+            assert torch.equal(U2, U) and torch.equal(W2, W) and torch.equal(S2, S), (name, dwq, "chain")
             del U2, W2, S2
     del I, U, W, S
     torch.cuda.empty_cache()

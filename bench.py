@@ -283,8 +283,10 @@ def bench_cfg4(torch, dev, reps):
     """cfg4: N=1024, T=2^20, beta=0.99, x~N(0.012,0.08^2), u0~U[0,1).
     Forward: the three-level scan_forward_v4 (repair on) on a small grid of (C, G, K, K2) with
     overflow statistics, as the reference's e9d grid does (the reference default first); the
-    converged two-level scan_forward_v3 (which takes the long-chunk path here); the single-pass
-    exact forward; the serial forward.  Backward: the affine-scan adjoint and the serial one.
+    converged two-level scan_forward_v3 (which takes the warm-started chunks here), the warm
+    forward at other chunk / warm-up lengths and the long-chunk map scan in pieces it replaced;
+    the single-pass exact forward; the serial forward.  Backward: the affine-scan adjoint and the
+    serial one.
     fwd+bwd = the fastest exact forward + the scan adjoint."""
     from lifscan import hip_lif as L
     T, N, beta = 2 ** 20, 1024, 0.99
@@ -307,11 +309,34 @@ def bench_cfg4(torch, dev, reps):
     out["v4"] = v4
     U3, S3 = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=256, K=16, repair=10 ** 6)
     out["v3_converged_equals_serial"] = exact(U3, S3)
-    out["v3_converged_chunk"] = L.last_scan_run().C
-    out["v3_converged_pieces"] = L.last_scan_run().pieces
+    run = L.last_scan_run()
+    out["v3_converged_path"] = ("warm-started chunks" if getattr(run, "warm", False) else
+                                f"long-chunk map scan in {run.pieces} piece(s)")
+    out["v3_converged_chunk"] = run.C
+    if getattr(run, "warm", False):
+        out["v3_converged_warmup"] = run.W
+    else:
+        out["v3_converged_pieces"] = run.pieces
     del U3, S3
     out["fwd_v3_converged_ms"] = ev_time(lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=256, K=16,
                                                                    repair=10 ** 6), reps)
+    warm = {}
+    for C, W in ((16384, 2560), (16384, 4096), (8192, 2048), (4096, 2048)):
+        st = {}
+        Uw, Sw = L.scan_forward_warm(I, beta, 1.0, 0.0, u0, C=C, W=W, stats=st)
+        ok = exact(Uw, Sw)
+        del Uw, Sw
+        ms = ev_time(lambda: L.scan_forward_warm(I, beta, 1.0, 0.0, u0, C=C, W=W), reps)
+        warm[f"C{C}_W{W}"] = {"ms": round(ms, 4), "equals_serial": ok,
+                              "missed_frac": round(st["missed_frac"], 6),
+                              "repair_iters": st["repair_iters"]}
+    out["warm"] = warm
+    C2, P = L.long_sequence_plan(T, N)
+    U2, S2 = L._scan2_pieces(I, beta, 1.0, 0.0, u0, C2, L.LONG_K, P)
+    out["longchunk_pieces_equals_serial"] = exact(U2, S2)
+    del U2, S2
+    out["fwd_longchunk_pieces_ms"] = ev_time(
+        lambda: L._scan2_pieces(I, beta, 1.0, 0.0, u0, C2, L.LONG_K, P), reps)
     U2, S2 = L.scan_forward_exact(I, beta, 1.0, 0.0, u0, K=8, maps=False)
     out["single_pass_equals_serial"] = exact(U2, S2)
     del U2, S2
@@ -320,7 +345,8 @@ def bench_cfg4(torch, dev, reps):
     out["bwd_scan_ms"] = ev_time(lambda: L.scan_backward_tiled(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), reps)
     out["bwd_serial_ms"] = ev_time(lambda: L.serial_backward(I, u0, U, S, gS, None, beta, 1.0, 0.0, 4.0), 2)
     ns = T * N
-    t_fwd = min(out["fwd_v3_converged_ms"], out["fwd_single_pass_ms"], min(r["ms"] for r in v4.values()))
+    t_fwd = min(out["fwd_v3_converged_ms"], out["fwd_single_pass_ms"], min(r["ms"] for r in v4.values()),
+                min(r["ms"] for r in warm.values() if r["equals_serial"]))
     t_fb = t_fwd + out["bwd_scan_ms"]
     out["fwd_bwd_ms"] = t_fb
     out["fwd_bwd_value"] = round(ns / (t_fb / 1000.0), 1)

@@ -644,14 +644,20 @@ __global__ __launch_bounds__(256) void k_lif_repair(const float* __restrict__ I,
       const int64_t n = (int64_t)nb * WAVE + (e % WAVE);
       float u = starts[(size_t)m * N + n];
       const size_t base = (size_t)m * C * N + n;
-      stream_rows<16>(I + base, (size_t)N, C, [&](int64_t j, float x) {
-        bool s;
-        u = lif_step(u, x, beta, theta, u_r, s);
-        U[base + (size_t)j * N] = u;
-        S[base + (size_t)j * N] = s ? 1.0f : 0.0f;
-      });
+      // U holds this chunk's replay from its previous start.  Once the new trajectory has
+      // the same state bits at some step, every later step is the same too (the step is a
+      // function of the state and the input), so the replay stops there and the chunk's end
+      // is unchanged: exact, and the round gives the same states as a full re-replay.
+      const bool met = stream_rows_until<16>(
+          I + base, U + base, (size_t)N, C, [&](int64_t j, float x, float u_old) {
+            bool s;
+            u = lif_step(u, x, beta, theta, u_r, s);
+            U[base + (size_t)j * N] = u;
+            S[base + (size_t)j * N] = s ? 1.0f : 0.0f;
+            return same_bits(u, u_old);
+          });
       const size_t oe = (size_t)m * N + n;
-      if (u != ends[oe]) {
+      if (!met && u != ends[oe]) {
         ends[oe] = u;
         if (m + 1 < M) cl[atomicAdd(&s_nc, 1)] = e + WAVE;
       }
@@ -850,6 +856,14 @@ void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* 
                               int C, int64_t repair, float beta, float theta, float u_r,
                               hipStream_t st) {
   launch_fwd_auto(I, starts, U, S, ends, N, C, M, beta, theta, u_r, st);
+  lif_repair_launch(I, U, S, starts, ends, list0, list1, hdr, N, M, C, repair, beta, theta, u_r,
+                    st);
+}
+
+// The device repair rounds alone, after a replay that wrote U, S and ends from starts.
+void lif_repair_launch(const float* I, float* U, float* S, float* starts, float* ends, int* list0,
+                       int* list1, WsHeader* hdr, int64_t N, int M, int C, int64_t repair,
+                       float beta, float theta, float u_r, hipStream_t st) {
   if (repair > 0 && M > 1) {
     // Round r makes the starts of chunks 0..r exact, so M rounds always converge; the cap
     // only bounds the work when NaN inputs make the comparison fail forever.

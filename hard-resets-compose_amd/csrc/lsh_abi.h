@@ -74,6 +74,13 @@ int lif_param_bwd_lookback(const float* I, const float* u0, const float* U, cons
                            size_t ws_bytes, int64_t T, int64_t N, float beta, float theta,
                            float u_r, float alpha, int ps, hipStream_t st);
 
+// Device repair rounds of the two-level scan (lif_kernels.hip, k_lif_repair) after a replay that
+// wrote U, S and ends from starts: at most min(repair, M) rounds; list0/list1 hold
+// ceil(N/64)*M*64 ints each.
+void lif_repair_launch(const float* I, float* U, float* S, float* starts, float* ends, int* list0,
+                       int* list1, WsHeader* hdr, int64_t N, int M, int C, int64_t repair,
+                       float beta, float theta, float u_r, hipStream_t st);
+
 // Fills n ints with v on the stream (lif_lookback.hip; look-back flags).
 void fill_i32_launch(int* p, int64_t n, int v, hipStream_t st);
 

@@ -147,6 +147,50 @@ __device__ __forceinline__ void stream_rows(const float* __restrict__ p, size_t 
   for (int64_t j = nt * D; j < n; ++j) f(j, p[(size_t)j * stride]);
 }
 
+// f(j, p[j*stride], q[j*stride]) for j = 0, 1, ... in order until f returns true or j = n;
+// returns whether f stopped the walk.  Rows of p and q are loaded in tiles of D with the next
+// tile's loads in flight, as stream_rows.  f may store to q's row j (it has been read).
+template <int D, class F>
+__device__ __forceinline__ bool stream_rows_until(const float* __restrict__ p,
+                                                  const float* q, size_t stride,
+                                                  int64_t n, F&& f) {
+  const int64_t nt = n / D;
+  float a[D], c[D];
+  if (nt > 0) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      a[k] = p[(size_t)k * stride];
+      c[k] = q[(size_t)k * stride];
+    }
+  }
+  for (int64_t t = 0; t < nt; ++t) {
+    float b[D], d[D];
+    const bool more = t + 1 < nt;
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        b[k] = p[(size_t)((t + 1) * D + k) * stride];
+        d[k] = q[(size_t)((t + 1) * D + k) * stride];
+      }
+    }
+    bool stop = false;
+#pragma unroll
+    for (int k = 0; k < D; ++k)
+      if (!stop) stop = f(t * D + k, a[k], c[k]);
+    if (stop) return true;
+    if (more) {
+#pragma unroll
+      for (int k = 0; k < D; ++k) {
+        a[k] = b[k];
+        c[k] = d[k];
+      }
+    }
+  }
+  for (int64_t j = nt * D; j < n; ++j)
+    if (f(j, p[(size_t)j * stride], q[(size_t)j * stride])) return true;
+  return false;
+}
+
 __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, WAVE));

@@ -192,6 +192,7 @@ class _ScanRun:
     """Holds the workspace of one scan call (maps, starts, ends) for stats and tests."""
 
     pieces = 1  # lsh_lif_scan_v3_pieces_fwd: the arrays are the first piece's (T = its steps)
+    warm = False
 
     def __init__(self, ws, T, N, C, K):
         self.ws, self.T, self.N, self.C, self.K = ws, T, N, C, K
@@ -264,10 +265,16 @@ def scan_forward_v3(I, beta, theta, u_r, u0, C=64, K=16, BN=32, nw=1, BNc=16, nw
     uninitialised).  stats receives repair_iters, overflow_frac, mean_pieces, max_pieces with
     the reference's definitions (mean/max of kept breakpoints + 1).  With the repair budget at
     least T/C (converged) and no stats requested, the result is the serial recurrence and the
-    fastest exact path computes it: the single-pass kernel, or for few neurons and long T
-    the same two-level scan with long chunks (long_sequence_C)."""
+    fastest exact path computes it: for up to 8192 neurons and long T the warm-started chunks
+    (warm_plan), else the single-pass kernel, or for few neurons and long T the same two-level
+    scan with long chunks (long_sequence_C)."""
     I = _input(I)
     T, N = I.shape
+    if (stats is None and int(C) >= 1 and T % int(C) == 0 and int(repair) >= T // int(C)
+            and T > 0 and N > 0):
+        plan = warm_plan(T, N, beta)
+        if plan is not None:
+            return _scan_warm_run(I, beta, theta, u_r, u0, *plan)
     if int(C) >= 1 and T % int(C) == 0 and _fused_fwd_ok(T, C, K, repair, stats):
         long_c = long_sequence_C(T, N)
         if long_c:  # few neurons, long T: the multi-kernel scan with long chunks is faster
@@ -344,6 +351,95 @@ def _scan2_pieces(I, beta, theta, u_r, u0, C, K, P):
             C, K, P, _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_lif_scan_v3_pieces_fwd")
     _LAST_RUN = _ScanRun(ws, T // P, N, C, K)  # the first piece's arrays
     _LAST_RUN.pieces = P
+    return U, S
+
+
+# Warm-started converged forward (lsh_lif_scan_warm_fwd): the warm-up must run long enough for
+# the true trajectory and the one from u_r to spike together; the time to forget a start grows
+# like 1/(1 - beta), so W = 24/(1 - |beta|) steps rounded up to 256 (256 to 8192).  Chunks of at
+# least 3W keep the re-read of the warm-up rows <= 1/3 of a pass; the longest chunk (a power of
+# two dividing T) that still gives >= WARM_WAVES (chunk, 64-neuron block) waves, else the
+# shortest, with >= 4 chunks.  Measured on MI355X (converged scan_forward_v3 before -> warm):
+# N = 1024, T = 2^20: 7.2 -> 3.1 ms (beta .99), 6.8 -> 2.7 ms (.9); N = 256, T = 2^18: 1.7 ->
+# 0.57 / 1.4 -> 0.19; N = 64, T = 2^20: 3.5 -> 0.56 / 3.3 -> 0.23; N = 1024, T = 65536: 1.14 ->
+# 0.54 / 0.92 -> 0.16; N = 4096, T = 65536: 1.62 -> 0.93 / 1.62 -> 0.69; N = 8192, T = 65536:
+# 1.89 -> 1.71 / 1.89 -> 1.41.  With only 2 chunks (N = 4096 or 1024, T = 16384, beta .99) the
+# single pass stays faster, and from 16384 neurons it is as fast or faster.
+WARM_MAX_N = 8192
+WARM_MIN_CHUNKS = 4
+WARM_WAVES = 1024
+WARM_K = 24.0
+
+
+def warm_plan(T, N, beta):
+    """(C, W) of the warm-started converged forward for [T, N] inputs and decay beta, or None
+    when the single pass or the long-chunk scan is used."""
+    if N > WARM_MAX_N or N < 1 or T < 1:
+        return None
+    b = abs(_f32(beta))
+    W = 8192 if b >= 1.0 else int(min(8192, max(256, 256 * math.ceil(WARM_K / (1.0 - b) / 256.0))))
+    nb = (N + 63) // 64
+    best = None
+    c = 1 << 16
+    while c >= 3 * W:
+        if T % c == 0 and T // c >= WARM_MIN_CHUNKS:
+            best = c
+            if (T // c) * nb >= WARM_WAVES:
+                break
+        c //= 2
+    return (best, W) if best else None
+
+
+def _scan_warm_run(I, beta, theta, u_r, u0, C, W):
+    global _LAST_RUN
+    U, S = scan_forward_warm(I, beta, theta, u_r, u0, C=C, W=W)
+    _LAST_RUN = _WarmRun(C, W)
+    return U, S
+
+
+class _WarmRun:
+    """The most recent converged forward took the warm-started chunks (chunk C, warm-up W)."""
+
+    pieces = 1
+    warm = True
+
+    def __init__(self, C, W):
+        self.C, self.W = C, W
+
+
+def scan_forward_warm(I, beta, theta, u_r, u0, C=2048, W=None, stats=None):
+    """Converged exact forward by warm-started chunks (lsh_lif_scan_warm_fwd) -> (U, S), the
+    serial recurrence: chunk m's entry is predicted by W steps of the recurrence from u_r over
+    the rows before it (W defaults to C), every chunk is replayed from its prediction, and the
+    device repair replays the chunks whose prediction missed.  stats receives repair_iters
+    (rounds) and missed_frac (the fraction of chunk entries m >= 1 whose prediction differed
+    from the exit of chunk m-1 replayed from its own prediction, before the repair)."""
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    C = int(C)
+    W = C if W is None else int(W)
+    if C < 1 or T % C or W < 0:
+        raise ValueError(f"the warm-started forward needs C >= 1 dividing T={T} and W >= 0")
+    if T == 0 or N == 0:  # nothing to compute (an empty tensor has no device address)
+        if stats is not None:
+            stats["repair_iters"], stats["missed_frac"] = 0, 0.0
+        return torch.empty_like(I), torch.empty_like(I)
+    L = _n.lib()
+    nbytes = L.lsh_lif_scan_warm_workspace(T, N, C)
+    if nbytes == 0:
+        raise ValueError(f"unsupported scan shape T={T} N={N} C={C}")
+    ws = _n.workspace(nbytes, I.device)
+    U = torch.empty_like(I)
+    S = torch.empty_like(I)
+    with _n.on_device(I):
+        _n.check(L.lsh_lif_scan_warm_fwd(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N, _f32(beta), _f32(theta), _f32(u_r),
+            C, W, _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_lif_scan_warm_fwd")
+    if stats is not None:
+        st = _n.read_stats(ws, max((T // C - 1) * N, 1))
+        stats["repair_iters"] = int(st.repair_iters)
+        stats["missed_frac"] = float(st.fused_fixups) / max((T // C - 1) * N, 1)
     return U, S
 
 

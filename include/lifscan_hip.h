@@ -89,6 +89,22 @@ int lsh_lif_scan_v3_pieces_fwd(const float* I, const float* u0, float* U, float*
                                int64_t N, float beta, float theta, float u_r, int C, int K, int P,
                                void* ws, size_t ws_bytes, void* stream);
 
+/* The converged lsh_lif_scan_v3_fwd (repair to convergence, no statistics) by warm-started
+ * chunks, for few neurons and long T: the entry state of chunk m >= 1 is predicted by W steps
+ * of the recurrence over the W rows before the chunk, started from u_r (from u0 when those rows
+ * reach row 0: then it is exact), every chunk is replayed from its prediction, and the device
+ * repair of the two-level scan replays each chunk whose prediction differs from its
+ * predecessor's replayed exit, stopping where the new trajectory meets the stored one, until
+ * nothing changes.  U and S are the serial recurrence bit for bit.  The path of scan_forward_v3
+ * (triton_lif.py:782-817, repair >= T/C) for few neurons and long T; the prediction is the
+ * hard-reset analogue of the reference's ALIF warm predictor (triton_alif.py:75-92, :276-285).
+ * Requires T % C == 0, C >= 1, W >= 0.  Workspace lsh_lif_scan_warm_workspace(T, N, C) bytes,
+ * 256-byte aligned; its header's fused_fixups counts the predictions that missed. */
+size_t lsh_lif_scan_warm_workspace(int64_t T, int64_t N, int C);
+int lsh_lif_scan_warm_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
+                          int64_t N, float beta, float theta, float u_r, int C, int W, void* ws,
+                          size_t ws_bytes, void* stream);
+
 /* Two-level scan pruned with one caller-given lower bound per neuron (lo[N], e.g. the loose
  * state_bounds of triton_lif.py:238-243) instead of the per-chunk envelope.  Replaces
  * triton_lif.py:262-295 (scan_forward), :479-509 (scan_forward_tiled) and :609-642

@@ -129,33 +129,45 @@ def test_scan_v3_long_sequence_staged_carry(L, dev, K):
 
 
 def test_converged_v3_long_sequence_path(L, dev):
-    """Few neurons, long T, converged repair: scan_forward_v3 runs the two-level scan with
-    long chunks (C = 1024, K = 32) and returns the serial recurrence bit for bit."""
+    """Few neurons, long T, converged repair: the two-level scan with long chunks (C = 1024,
+    K = 32) returns the serial recurrence bit for bit; scan_forward_v3 itself takes the
+    warm-started chunks there (warm_plan) and returns the same bits."""
+    from lifscan import hip_lif as H
     T, N, beta = 65536, 1000, 0.99
     assert L.long_sequence_C(T, N) == 1024
     I = normal(T, N, 0.012, 0.08, 23)
     u0 = uniform(N, 0.0, 1.0, 24)
     print("v3 long-sequence path", flush=True)
-    U, S = L.scan_forward_v3(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=256, K=16, repair=10 ** 6)
-    assert L.last_scan_run().C == 1024
+    Ig, u0g = gpu(I, dev), gpu(u0, dev)
+    U, S = H._scan2(Ig, beta, 1.0, 0.0, u0g, 1024, H.LONG_K, T // 1024, None)
     Us, Ss = O.serial_forward(I, beta, 1.0, 0.0, u0)
+    assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+    U, S = L.scan_forward_v3(Ig, beta, 1.0, 0.0, u0g, C=256, K=16, repair=10 ** 6)
+    assert H.last_scan_run().warm and (H.last_scan_run().C, H.last_scan_run().W) == H.warm_plan(T, N, beta)
     assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
 
 
 def test_converged_v3_pieces_path_cfg4(L, dev):
-    """At cfg4's size (N = 1024, T = 2^20, beta = 0.99) the converged scan_forward_v3 takes the
-    long-chunk scan in pieces (C = 2048, 4 pieces) and returns the serial forward bit for bit
-    (the serial forward is pinned to the oracle by test_serial_forward_bitexact)."""
+    """At cfg4's size (N = 1024, T = 2^20, beta = 0.99) the long-chunk scan in pieces (C = 2048,
+    4 pieces) and the converged scan_forward_v3 (warm-started chunks, C = 16384) return the
+    serial forward bit for bit (the serial forward is pinned to the oracle by
+    test_serial_forward_bitexact)."""
     from lifscan import hip_lif as H
     T, N, beta = 2 ** 20, 1024, 0.99
     assert H.long_sequence_plan(T, N) == (2048, 4)
+    assert H.warm_plan(T, N, beta)[0] == 16384
     g = torch.Generator(device=dev).manual_seed(41)
     I = torch.randn(T, N, device=dev, generator=g).mul_(0.08).add_(0.012)
     u0 = torch.rand(N, device=dev, generator=g)
     print("v3 pieces at cfg4", flush=True)
-    U, S = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=256, K=16, repair=10 ** 6)
-    assert H.last_scan_run().pieces == 4 and H.last_scan_run().C == 2048
     Us, Ss = H.serial_forward(I, beta, 1.0, 0.0, u0)
+    U, S = H._scan2_pieces(I, beta, 1.0, 0.0, u0, 2048, H.LONG_K, 4)
+    assert H.last_scan_run().pieces == 4 and H.last_scan_run().C == 2048
+    assert torch.equal(U, Us) and torch.equal(S, Ss)
+    del U, S
+    print("v3 converged (warm) at cfg4", flush=True)
+    U, S = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=256, K=16, repair=10 ** 6)
+    assert H.last_scan_run().warm and H.last_scan_run().C == 16384
     assert torch.equal(U, Us) and torch.equal(S, Ss)
     del I, U, S, Us, Ss
     torch.cuda.empty_cache()

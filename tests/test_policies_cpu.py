@@ -66,3 +66,20 @@ def test_auto_policies_accept_lengths_the_chunk_policy_rejects():
     assert L.auto_modes(1024, 16386) == ("serial", "serial")   # 16386 = 2 * 8193
     assert L.auto_modes(1024, 16392) == ("serial", "scan")     # chunk 8 for the adjoint only
     assert L._recompute_ok(4096, 65536, 16, 10 ** 6) is True
+
+
+def test_warm_plan():
+    """The warm-started converged forward: W = 24/(1 - |beta|) rounded up to 256 (256..8192),
+    the longest power-of-two chunk >= 3W dividing T with >= 1024 (chunk, block) waves, else the
+    shortest, at least 4 chunks; none above 8192 neurons."""
+    from lifscan import hip_lif as L
+    assert L.warm_plan(2 ** 20, 1024, 0.99) == (16384, 2560)   # cfg4
+    assert L.warm_plan(2 ** 20, 1024, 0.9) == (16384, 256)
+    assert L.warm_plan(2 ** 18, 256, 0.99) == (8192, 2560)     # 32 chunks x 4 blocks
+    assert L.warm_plan(65536, 4096, 0.99) == (8192, 2560)
+    assert L.warm_plan(16384, 1024, 0.99) is None              # 2 chunks only
+    assert L.warm_plan(16384, 4096, 0.9) == (1024, 256)
+    assert L.warm_plan(4096, 65536, 0.9) is None               # N > 8192: single pass
+    assert L.warm_plan(1000, 64, 0.9) is None                  # no power-of-two chunk
+    assert L.warm_plan(2 ** 20, 64, 1.0)[1] == 8192
+    assert L.warm_plan(0, 64, 0.9) is None and L.warm_plan(4096, 0, 0.9) is None

@@ -331,6 +331,22 @@ def bench_cfg4(torch, dev, reps):
                               "missed_frac": round(st["missed_frac"], 6),
                               "repair_iters": st["repair_iters"]}
     out["warm"] = warm
+    # the two-level map scan at long chunks with its two carries: the associative one (chunk
+    # maps composed by a parallel prefix, DPP in the wave and LDS across waves) and the
+    # sequential one (one map after another per neuron), both run to convergence
+    maps = {}
+    for carry, fn in (("assoc", L.scan_forward_assoc), ("sequential", L.scan_forward_mapscan)):
+        for C, K in ((2048, 32), (4096, 32)):
+            st = {}
+            kw = {} if carry == "assoc" else {"repair": 10 ** 6}
+            Um, Sm = fn(I, beta, 1.0, 0.0, u0, C=C, K=K, stats=st, **kw)
+            ok = exact(Um, Sm)
+            del Um, Sm
+            ms = ev_time(lambda: fn(I, beta, 1.0, 0.0, u0, C=C, K=K, **kw), 3)
+            maps[f"{carry}_C{C}_K{K}"] = {"ms": round(ms, 4), "equals_serial": ok,
+                                          **{k: (round(v, 6) if isinstance(v, float) else v)
+                                             for k, v in st.items()}}
+    out["mapscan_converged"] = maps
     C2, P = L.long_sequence_plan(T, N)
     U2, S2 = L._scan2_pieces(I, beta, 1.0, 0.0, u0, C2, L.LONG_K, P)
     out["longchunk_pieces_equals_serial"] = exact(U2, S2)

@@ -84,6 +84,9 @@ SIGNATURES = {
     "lsh_lif_scan_v3_pieces_workspace": (c_sz, [c_i64, c_i64, c_i, c_i, c_i]),
     "lsh_lif_scan_v3_pieces_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i,
                                          c_i, c_p, c_sz, c_p]),
+    "lsh_lif_scan_v3_assoc_workspace": (c_sz, [c_i64, c_i64, c_i, c_i]),
+    "lsh_lif_scan_v3_assoc_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i,
+                                        c_i64, c_p, c_sz, c_p]),
     "lsh_lif_scan_warm_workspace": (c_sz, [c_i64, c_i64, c_i]),
     "lsh_lif_scan_warm_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i, c_p,
                                     c_sz, c_p]),

@@ -443,6 +443,44 @@ def scan_forward_warm(I, beta, theta, u_r, u0, C=2048, W=None, stats=None):
     return U, S
 
 
+def scan_forward_assoc(I, beta, theta, u_r, u0, C=2048, K=32, repair=None, stats=None):
+    """The two-level map scan with the associative carry (lsh_lif_scan_v3_assoc_fwd) -> (U, S):
+    the single-read chunk-map build, then the chunk maps of each neuron composed by a parallel
+    prefix (DPP inside each wave, the wave totals in LDS; overflowed chunks run serially), the
+    replay, and repair rounds (default: to convergence, T/C rounds: the serial recurrence bit
+    for bit).  With repair = 0 the chunk starts are the scan's own predictions.  stats:
+    repair_iters, overflow_frac, mean_pieces, max_pieces (the truncation's, as scan_forward_v3).
+    beta >= 0 (the envelope maps compose only then), 1 <= K <= 32, T % C == 0."""
+    global _LAST_RUN
+    I = _input(I)
+    T, N = I.shape
+    u0 = _vec(u0, N, I)
+    C, K = int(C), int(K)
+    if C < 1 or T % C or not 1 <= K <= 32 or _f32(beta) < 0:
+        raise ValueError(f"the associative map scan needs C >= 1 dividing T={T}, 1 <= K <= 32, "
+                         f"beta >= 0")
+    R = T // C if repair is None else int(repair)
+    if T == 0 or N == 0:
+        if stats is not None:
+            stats.update(repair_iters=0, overflow_frac=0.0, mean_pieces=1.0, max_pieces=1)
+        return torch.empty_like(I), torch.empty_like(I)
+    L = _n.lib()
+    nbytes = L.lsh_lif_scan_v3_assoc_workspace(T, N, C, K)
+    if nbytes == 0:
+        raise ValueError(f"unsupported scan shape T={T} N={N} C={C} K={K}")
+    ws = _n.workspace(nbytes, I.device)
+    U = torch.empty_like(I)
+    S = torch.empty_like(I)
+    with _n.on_device(I):
+        _n.check(L.lsh_lif_scan_v3_assoc_fwd(
+            _n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N, _f32(beta), _f32(theta), _f32(u_r),
+            C, K, R, _n.ptr(ws), nbytes, _n.stream_of(I)), "lsh_lif_scan_v3_assoc_fwd")
+    _LAST_RUN = _ScanRun(ws, T, N, C, K)
+    if stats is not None:
+        _fill_stats(stats, _n.read_stats(ws, (T // C) * N))
+    return U, S
+
+
 def scan_forward_mapscan(I, beta, theta, u_r, u0, C=64, K=16, repair=0, stats=None):
     """The two-level map scan of scan_forward_v3 itself (envelope + capacity-K chunk maps, carry
     with overflow fallback, replay, device repair) -> (U, S), also where scan_forward_v3 would

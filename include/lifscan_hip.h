@@ -89,6 +89,24 @@ int lsh_lif_scan_v3_pieces_fwd(const float* I, const float* u0, float* U, float*
                                int64_t N, float beta, float theta, float u_r, int C, int K, int P,
                                void* ws, size_t ws_bytes, void* stream);
 
+/* The two-level map scan of lsh_lif_scan_v3_fwd with an associative carry: after the chunk-map
+ * build, the chunk maps of each neuron are composed by a parallel prefix instead of being
+ * evaluated one after another: one workgroup per neuron, one chunk per lane, an inclusive scan
+ * inside each wave by DPP moves (row_shr 1/2/4/8, row_bcast 15/31) and the wave totals composed
+ * in LDS, segmented at capacity-overflowed chunks, which run serially; the envelope bounds of
+ * the chunk entries by the same scan over the min-affine envelope maps.  Then the replay and
+ * `repair` Jacobi repair rounds (repair >= T/C: U and S are the serial recurrence).  Replaces
+ * the sequential carry of triton_lif.py:782-817 (scan_forward_v3: env_carry_kernel :723-733,
+ * carry2_kernel :579-606) by the composition monoid of :864-892 (compose_group_kernel).
+ * The starts before repair are predictions whose rounding differs from the sequential carry's,
+ * so repair_iters is not the reference's; overflow_frac / mean_pieces / max_pieces are the
+ * truncation's, as lsh_lif_scan_v3_fwd's.  Requires beta >= 0, T % C == 0, 1 <= K <= 32.
+ * Workspace lsh_lif_scan_v3_assoc_workspace(T, N, C, K) bytes (the v3 layout). */
+size_t lsh_lif_scan_v3_assoc_workspace(int64_t T, int64_t N, int C, int K);
+int lsh_lif_scan_v3_assoc_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
+                              int64_t N, float beta, float theta, float u_r, int C, int K,
+                              int64_t repair, void* ws, size_t ws_bytes, void* stream);
+
 /* The converged lsh_lif_scan_v3_fwd (repair to convergence, no statistics) by warm-started
  * chunks, for few neurons and long T: the entry state of chunk m >= 1 is predicted by W steps
  * of the recurrence over the W rows before the chunk, started from u_r (from u0 when those rows

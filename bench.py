@@ -588,11 +588,13 @@ def dominant_only(L, torch, dev):
 def counters_workload(torch, dev):
     """Short program for counter passes (rocprofv3 --pmc) over the kernels that are not HBM-bound
     by design, each launched once or twice at its configuration: a 256 MiB copy (FETCH/WRITE
-    calibration); cfg5's box scan with repair (k_alif_build<4,4>, k_alif_carry, k_alif_repair);
-    cfg2's map scan at C = 128, K = 8 (k_lif_build<8,8>, k_lif_carry<8>); cfg4's converged v3 in
-    pieces (k_lif_build<32,8>, k_lif_carry_staged<32>), its v4 at C 2048 / G 4 / K 32 / K2 64 and at
-    the reference default (k_lif_compose, k_map_carry) and its look-back adjoint
-    (k_lif_bwd_lookback<16,16,...>)."""
+    calibration); cfg5's box scan with repair, converged (k_alif_build<4,4>, k_alif_carry,
+    k_alif_chain) and with the statistics (k_alif_repair); cfg2's map scan at C = 128, K = 8
+    (k_lif_build<8,8>, k_lif_carry<8>); at cfg4: the converged forward (k_lif_fwd_warm,
+    k_lif_repair_wide), the long-chunk map scan in pieces (k_lif_build<32,8>,
+    k_lif_carry_staged<32>) and with the associative carry (k_map_scan), v4 at C 2048 / G 4 /
+    K 32 / K2 64 and at the reference default (k_lif_compose, k_map_carry) and the look-back
+    adjoint (k_lif_bwd_lookback<16,16,...>)."""
     from lifscan import hip_lif as L
     from lifscan import triton_alif as A
     x = torch.empty(64 * 2 ** 20, device=dev)
@@ -607,6 +609,8 @@ def counters_workload(torch, dev):
     z = torch.zeros(N, device=dev)
     WP = A.alif_warm_predict(I, b, r, q, 1.0, 0.0, z, z, C, Wn=4)
     A.alif_scan_forward(I, b, r, q, 1.0, 0.0, z, z, WP, 0.1 * q, C=C, K1=32, K2=32, BN=4, repair=10 ** 6)
+    A.alif_scan_forward(I, b, r, q, 1.0, 0.0, z, z, WP, 0.1 * q, C=C, K1=32, K2=32, BN=4, repair=10 ** 6,
+                        stats={})
     torch.cuda.synchronize()
     del I, WP
     log("counters: cfg2 map scan")
@@ -620,7 +624,10 @@ def counters_workload(torch, dev):
     T, N = 2 ** 20, 1024
     I = (0.012 + 0.08 * torch.randn(T, N, generator=torch.Generator().manual_seed(0))).to(dev)
     u0 = torch.rand(N, generator=torch.Generator().manual_seed(2)).to(dev)
-    U, S = L.scan_forward_v3(I, 0.99, 1.0, 0.0, u0, C=256, K=16, repair=10 ** 6)
+    U, S = L.scan_forward_v3(I, 0.99, 1.0, 0.0, u0, C=256, K=16, repair=10 ** 6)  # warm-started
+    C2, P = L.long_sequence_plan(T, N)
+    L._scan2_pieces(I, 0.99, 1.0, 0.0, u0, C2, L.LONG_K, P)
+    L.scan_forward_assoc(I, 0.99, 1.0, 0.0, u0, C=2048, K=32)
     for C, G, K, K2 in ((2048, 4, 32, 64), (64, 16, 16, 32)):
         L.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
         torch.cuda.synchronize()

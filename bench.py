@@ -261,6 +261,19 @@ def bench_cfg3(torch, dev, reps):
     # synchronizations, the host's launch latency included)
     out["lif_layers_fwd_bwd_ms"] = bb_time(layers, max(reps, 10), warm=2, warm_s=0.5)
     out["lif_layers_fwd_bwd_per_call_ms"] = ev_time(layers, max(reps, 10), warm=2)
+    # lif_tuned runs its recomputing pair from the C++ autograd function (lifscan/_ops.cpp);
+    # the same kernels through the Python autograd function, for the host cost it removes
+    out["lif_tuned_host_path"] = "c++" if L._rc_path(I1, torch.zeros(I1.shape[1], device=dev), 0.95,
+                                                     "scan", 16, 10 ** 6) is not None else "python"
+
+    def layers_py():
+        for I in (I1, I2):
+            Ig = I.detach().requires_grad_(True)
+            S = L.LIFTuned.apply(Ig, torch.zeros(I.shape[1], device=dev), 0.95, 1.0, 0.0, 4.0, "scan",
+                                 16, 10 ** 6)
+            S.backward(g2)
+    out["lif_layers_fwd_bwd_python_autograd_ms"] = bb_time(layers_py, max(reps, 10), warm=2, warm_s=0.5)
+    out["lif_layers_fwd_bwd_python_autograd_per_call_ms"] = ev_time(layers_py, max(reps, 10), warm=2)
     for mode in ("scan", "serial", "auto"):
         torch.manual_seed(4)
         netm = Net(mode).to(dev)

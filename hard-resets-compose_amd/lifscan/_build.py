@@ -100,5 +100,27 @@ def build_library(verbose=False, extra_flags=(), out=None, jobs=None, incrementa
     return out
 
 
+OPS_NAME = "lifscan_ops"
+OPS_DIR = os.path.join(LIB_DIR, "_ops")
+OPS_PATH = os.path.join(OPS_DIR, OPS_NAME + ".so")
+
+
+def build_ops(verbose=False):
+    """Compile lifscan/_ops.cpp (the C++ autograd function of lif_tuned's recomputing pair) into
+    the in-tree lifscan/_lib/_ops/lifscan_ops.so with torch's extension builder (host compiler,
+    torch and HIP headers; it calls the HIP library through addresses handed over at load)."""
+    import torch  # noqa: F401  (the builder needs torch's headers and libraries)
+    from torch.utils import cpp_extension
+    os.makedirs(OPS_DIR, exist_ok=True)
+    torch_lib = os.path.join(os.path.dirname(torch.__file__), "lib")
+    cpp_extension.load(
+        name=OPS_NAME, sources=[os.path.join(PKG_DIR, "_ops.cpp")], build_directory=OPS_DIR,
+        extra_cflags=["-O2", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1"],
+        extra_include_paths=["/opt/rocm/include"],
+        extra_ldflags=[f"-L{torch_lib}", "-lc10_hip", f"-Wl,-rpath,{torch_lib}"],
+        with_cuda=False, is_python_module=True, verbose=verbose)
+    return OPS_PATH
+
+
 if __name__ == "__main__":
     print(build_library(verbose="-v" in sys.argv, incremental="-i" in sys.argv))

@@ -178,6 +178,29 @@ def lib():
     return _LIB
 
 
+_OPS = None
+
+
+def ops():
+    """The C++ autograd module of lif_tuned's recomputing pair (lifscan/_ops.cpp, built in-tree
+    by build()) with the library's entry points handed over, or None when it is not built (the
+    layer then runs the same kernels through its Python autograd function)."""
+    global _OPS
+    if _OPS is None:
+        if not os.path.exists(_build.OPS_PATH):
+            return None
+        import importlib.util
+        spec = importlib.util.spec_from_file_location(_build.OPS_NAME, _build.OPS_PATH)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        L = lib()
+        addr = lambda f: ctypes.cast(f, ctypes.c_void_p).value
+        mod.set_entry_points(addr(L.lsh_lif_scan_exact_fwd_starts),
+                             addr(L.lsh_lif_scan_fused_bwd_starts), addr(L.lsh_status_string))
+        _OPS = mod
+    return _OPS
+
+
 def check(rc, what):
     if rc == LSH_OK:
         return

@@ -1014,7 +1014,41 @@ class LIFTuned(torch.autograd.Function):
                 None, None, None, None, None, None)
 
 
+_RC_OK = {}
+
+
+def _rc_path(I, u0, beta, mode, K, repair):
+    """u0 as the [N] vector of the C++ recomputing pair (lifscan/_ops.cpp) when lif_tuned can take
+    it: the recomputing pair applies, beta needs no gradient, u0 is already the layer's [N] fp32
+    vector (or needs none) and the module is built; else None."""
+    if mode == "serial" or CHECK_WAITS or not torch.is_tensor(I) or I.dim() != 2:
+        return None
+    if not I.is_cuda or I.dtype != torch.float32:
+        return None
+    if torch.is_tensor(beta) and beta.requires_grad:
+        return None
+    T, N = I.shape
+    key = (T, N, int(K), int(repair))
+    ok = _RC_OK.get(key)
+    if ok is None:
+        ok = _RC_OK[key] = _recompute_ok(T, N, K, repair)
+    if not ok:
+        return None
+    if (torch.is_tensor(u0) and u0.dim() == 1 and u0.shape[0] == N and u0.dtype == torch.float32
+            and u0.device == I.device and u0.is_contiguous()):
+        u0v = u0
+    elif torch.is_tensor(u0) and u0.requires_grad:
+        return None
+    else:
+        u0v = _vec(u0, N, I)
+    return u0v if _n.ops() is not None else None
+
+
 def lif_tuned(I, u0, beta=0.9, theta=1.0, u_r=0.0, alpha=4.0, mode="scan", K=16, repair=0):
+    u0v = _rc_path(I, u0, beta, mode, K, repair)
+    if u0v is not None:  # the same kernels and bits as LIFTuned's recomputing pair, from C++
+        return _n.ops().lif_tuned_rc(I, u0v, _f32(beta), float(theta), float(u_r), float(alpha),
+                                     _wait_header(I.device), FUSED_FWD_C)
     return LIFTuned.apply(I, u0, beta, theta, u_r, alpha, mode, K, repair)
 
 

@@ -198,97 +198,110 @@ __global__ __launch_bounds__(64) void k_alif_box(const float* __restrict__ Wpred
 }
 
 // ---------------------------------------------------------------------------------------
-// Box-scan chunk map (triton_alif.py:96-186).  A workgroup owns 16 neurons (BLK neurons when
-// BLK >= 4: see AlifBuildShape); in the
-// piece loop 32 lanes serve one neuron (two neurons per wave): lane i holds first-spike line
-// slot i (< K1) and post-spike piece slot i (< K2).  Steps go in tiles of TS:
+// Box-scan chunk map (triton_alif.py:96-186).  One neuron per 16-lane row of a wave (four
+// neurons a wave, a DPP row each): slot s of the neuron's first-spike lines (< K1) and of its
+// post-spike pieces (< K2) sits in lane s & 15 of its row, register s >> 4, so a neuron's 32
+// slots take two registers per lane and the second is touched only while some neuron of the
+// wave holds more than 16 pieces (or lines).  Steps go in tiles of TS:
 //  0. the per-neuron line quantities of the tile, which do not depend on the pieces, are
-//     computed once per neuron instead of on 32 lanes, into LDS: (a) one thread per neuron runs
-//     the sequential recurrences A_j = beta*A, B_j = fl(fl(beta*B) + x_j) and R_j = rho^j;
-//     (b) all threads divide, sj = R_j/A_j, cj = (theta0 - B_j)/A_j, whi_j = min(hw, (hu - cj)/sj),
+//     computed once per neuron into LDS: (a) one thread per neuron runs the sequential
+//     recurrences A_j = beta*A, B_j = fl(fl(beta*B) + x_j) and R_j = rho^j; (b) all threads
+//     divide, sj = R_j/A_j, cj = (theta0 - B_j)/A_j, whi_j = min(hw, (hu - cj)/sj),
 //     (lu - cj)/sj; (c) one thread per neuron runs the running max wlo_j.  Same operations as
 //     the serial formulation, so the same bits.
 //  1. per step every piece is advanced; pieces cut by the threshold are split and the list
-//     compacted (exclusive prefix sum of the output counts, binary search of every output
-//     slot's source, gathers: all as shuffles within the neuron's 32 lanes).  The split runs
+//     compacted: exclusive prefix sum of the output counts over the neuron's slots (DPP row
+//     shifts within its row, register 0's total added to register 1's), every output slot's
+//     source through an LDS scatter, the sources' fields read back from LDS.  The split runs
 //     for all neurons of a block of BLK neurons when any of them has a cut (the reference's
-//     Triton block); blocks wider than one wave agree through LDS.
+//     Triton block): a wave decides for blocks of up to 4 neurons with one ballot; blocks of 8
+//     or 16 (a workgroup of 2 or 4 waves) agree through LDS.
 //  2. the step's first-spike line u0 >= sj*w0 + cj is added unless an existing line dominates
 //     it on [wlo, whi]; its post-spike piece x in [cx*wlo + q, cx*whi + q] (widened) is added.
-// Neurons per workgroup: 16 (8 waves) without a cross-wave split decision; a block of BLK >= 4
-// neurons is one workgroup of BLK/2 waves, so the per-step decision syncs only those waves.
+// Neurons per workgroup: 16 (4 waves) for blocks of up to 4, else one block.
 template <int BLK>
 struct AlifBuildShape {
-  static constexpr int NPW = BLK >= 4 ? BLK : 16;
+  static constexpr int NPW = BLK >= 8 ? BLK : 16;  // neurons per workgroup
+  static constexpr int NW = NPW / 4;               // waves per workgroup
 };
-constexpr int kAlifTS = 64;   // steps per tile
+constexpr int kAlifTS = 32;   // steps per tile (LDS: 5 x 16 neurons x 33 floats)
 
-template <int BLK, int kAlifNPW = AlifBuildShape<BLK>::NPW>
-__global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
+// Waves per SIMD the build is compiled for (registers <= 512 / WPE per lane).  Measured at cfg5
+// (N 16384, T 4096, BN 4, dw 0.1q / 0.3q): 5 (90 VGPRs) 3.01 / 3.53 ms, 6: 2.73 / 3.21, 7: 2.64 /
+// 3.16, 8 (64 VGPRs, 36 spilled) 3.56 / 4.14 ms; the steps are VALU-bound (~90 VALU per step of
+// a wave's 4 neurons) once 7 waves hide the per-step LDS and ballot latencies.
+#ifndef LSH_ALIF_BUILD_WPE
+#define LSH_ALIF_BUILD_WPE 7
+#endif
+template <int BLK>
+__global__ __launch_bounds__(WAVE * AlifBuildShape<BLK>::NW)
+__attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
     const float* __restrict__ I, const float* __restrict__ LU, const float* __restrict__ HU,
     const float* __restrict__ LWb, const float* __restrict__ HWb, float* __restrict__ MA,
     float* __restrict__ MB, int* __restrict__ NL, int* __restrict__ NP, int* __restrict__ OVF,
     float* __restrict__ LS, float* __restrict__ LC, float* __restrict__ LX, int* __restrict__ POWN,
     float* __restrict__ PXL, float* __restrict__ PXR, float* __restrict__ PU, float* __restrict__ PA,
-    float* __restrict__ POF, int64_t N, int NBLK, int C, int K1, int K2, int logk2, float beta,
-    float rho, float q, float theta0, float u_r) {
-  constexpr int NW = kAlifNPW / 2;                // waves per workgroup
-  constexpr int GW = BLK > 2 ? BLK / 2 : 1;       // waves per split-decision block
-  static_assert(BLK <= 2 || GW == NW, "a split-decision block is one workgroup");
+    float* __restrict__ POF, int64_t N, int NBLK, int C, int K1, int K2, float beta, float rho,
+    float q, float theta0, float u_r) {
+  constexpr int NPW = AlifBuildShape<BLK>::NPW;
+  constexpr int NW = AlifBuildShape<BLK>::NW;
+  constexpr int GW = BLK > 4 ? BLK / 4 : 1;  // waves per split-decision block (> 1: all of them)
+  static_assert(GW == 1 || GW == NW, "a split-decision block wider than a wave is one workgroup");
   constexpr int TS = kAlifTS;
   // one padding column per row: the neurons of a wave read the same step of different rows
   // (and phases (a), (c) walk rows in step), which a 64-float row stride would put on one bank
   constexpr int TSP = TS + 1;
-  __shared__ float sX[kAlifNPW][TSP], sS[kAlifNPW][TSP], sC[kAlifNPW][TSP], sHi[kAlifNPW][TSP],
-      sLo[kAlifNPW][TSP], sR[TS];
-  __shared__ float sA[kAlifNPW], sB[kAlifNPW], sLU[kAlifNPW], sHU[kAlifNPW], sHW[kAlifNPW];
-  __shared__ int s_cut[2][NW];  // per-step split flags, double-buffered by step parity
-  __shared__ int s_slot[NW][WAVE];
+  __shared__ float sX[NPW][TSP], sS[NPW][TSP], sC[NPW][TSP], sHi[NPW][TSP], sLo[NPW][TSP], sR[TS];
+  __shared__ float sA[NPW], sB[NPW], sLU[NPW], sHU[NPW], sHW[NPW];
+  __shared__ int s_cut[2][NW];               // per-step split flags (blocks wider than a wave)
+  __shared__ int sD[NW][4][32];              // output slot -> (source slot << 1) | spiking part
   const int64_t m = blockIdx.x / NBLK;
   const int blk = (int)(blockIdx.x - m * NBLK);
   const int tid = threadIdx.x;
   const int wv = tid / WAVE;
   const int lane = tid % WAVE;
-  const int half = lane >> 5;
-  const int i = lane & 31;  // slot
-  const int hb = half << 5;
-  const int ln = wv * 2 + half;  // neuron of this lane within the workgroup
-  const int64_t n = (int64_t)blk * kAlifNPW + ln;
+  const int g = lane >> 4;         // neuron of this lane within the wave (its DPP row)
+  const int i = lane & 15;         // slot i (register 0) and 16 + i (register 1)
+  const int rowb = lane & 48;      // the row's first lane
+  const int ln = wv * 4 + g;       // neuron of this lane within the workgroup
+  const int64_t n = (int64_t)blk * NPW + ln;
   const bool valid_n = n < N;
   const int64_t nn = valid_n ? n : N - 1;
   const size_t o = (size_t)m * N + nn;
-  // per-neuron sequential state for phases (a) and (c): thread t < 16 serves neuron t
-  const int64_t pn = (int64_t)blk * kAlifNPW + (tid < kAlifNPW ? tid : 0);
+  const unsigned long long gmask = 0xffffull << (16 * g);
+  const unsigned long long bmask = BLK == 1 ? gmask : BLK == 2 ? (0xffffffffull << (32 * (g >> 1))) : ~0ull;
+  // per-neuron sequential state for phases (a) and (c): thread t < NPW serves neuron t
+  const int64_t pn = (int64_t)blk * NPW + (tid < NPW ? tid : 0);
   const int64_t pnn = pn < N ? pn : N - 1;
   const size_t po = (size_t)m * N + pnn;
   float pA = 1.0f, pB = 0.0f, pR = 1.0f, pW = 0.0f;
-  if (tid < kAlifNPW) {
+  if (tid < NPW) {
     pW = LWb[po];
     sLU[tid] = LU[po];
     sHU[tid] = HU[po];
     sHW[tid] = HWb[po];
   }
-  float ls = 0.0f, lc = INFINITY, lx = 0.0f;
-  int nl = 0;
-  int pown = -1;
-  float pxl = INFINITY, pxr = INFINITY, pu = 0.0f, pa = 1.0f, pof = 0.0f;
-  int npc = 0;
+  // lines and pieces: index [r] is slot 16 r + i
+  float ls[2] = {0.0f, 0.0f}, lc[2] = {INFINITY, INFINITY}, lx[2] = {0.0f, 0.0f};
+  int pown[2] = {-1, -1};
+  float pxl[2] = {INFINITY, INFINITY}, pxr[2] = {INFINITY, INFINITY}, pu[2] = {0.0f, 0.0f};
+  float pa[2] = {1.0f, 1.0f}, pof[2] = {0.0f, 0.0f};
+  int nl = 0, npc = 0;
   int ovf = 0;
-  const unsigned long long hmask = 0xffffffffull << hb;
-  const int64_t n0 = (int64_t)blk * kAlifNPW;
+  const int64_t n0 = (int64_t)blk * NPW;
   const float* __restrict__ Iblk = I + (size_t)m * C * N;
   int kstep = 0;  // steps done in this chunk (parity of the split flags)
   for (int j0 = 0; j0 < C; j0 += TS) {
     const int ts = min(TS, C - j0);
     // (a0) the tile's inputs, staged by every thread of the workgroup (neuron-contiguous runs)
-    for (int e = tid; e < kAlifNPW * ts; e += NW * WAVE) {
-      const int k = e / kAlifNPW, nu = e - k * kAlifNPW;
+    for (int e = tid; e < NPW * ts; e += NW * WAVE) {
+      const int k = e / NPW, nu = e - k * NPW;
       const int64_t nq = n0 + nu < N ? n0 + nu : N - 1;
       sX[nu][k] = Iblk[(size_t)(j0 + k) * N + nq];
     }
     __syncthreads();
     // (a) sequential recurrences
-    if (tid < kAlifNPW) {
+    if (tid < NPW) {
       for (int k = 0; k < ts; ++k) {
         const float x = sX[tid][k];
         pA = beta * pA;
@@ -303,7 +316,7 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
     }
     __syncthreads();
     // (b) divisions, every (neuron, step) pair of the tile in parallel
-    for (int e = tid; e < kAlifNPW * ts; e += NW * WAVE) {
+    for (int e = tid; e < NPW * ts; e += NW * WAVE) {
       const int nu = e / ts, k = e - nu * ts;
       const float Aj = sS[nu][k], Bj = sC[nu][k];
       const float sj = sR[k] / Aj;
@@ -315,7 +328,7 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
     }
     __syncthreads();
     // (c) running max of the lower w bound: sLo[k] becomes wlo before step k
-    if (tid < kAlifNPW) {
+    if (tid < NPW) {
       for (int k = 0; k < ts; ++k) {
         const float cand = sLo[tid][k];
         sLo[tid][k] = pW;
@@ -324,19 +337,33 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
     }
     __syncthreads();
     for (int k = 0; k < ts; ++k) {
+      // the step's input and line quantities, read before the piece stage so that their LDS
+      // latency overlaps it
       const float x = sX[ln][k];
+      const float sj = sS[ln][k], cj = sC[ln][k], whi = sHi[ln][k], wlo = sLo[ln][k];
+      const float cx = sR[k] * rho;
+      // does any neuron of the wave hold pieces in register 1 (slots 16..31)?
+      const bool hi_p = __ballot(npc > 16) != 0ull;
       // 1. advance the post-spike pieces; a piece spikes for x <= (v - theta0 - pof)/pa
-      const bool valid = i < npc;
-      const float v = lif_v(pu, x, beta);
-      const float rr = (v - theta0) - pof;
-      const bool es = valid && rr > pa * pxl;
-      const bool en = valid && rr < pa * pxr;
-      const unsigned long long cb = __ballot(es && en);
+      bool es[2], en[2];
+      float v[2], rr[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        if (r == 1 && !hi_p) {
+          es[1] = en[1] = false;
+          v[1] = rr[1] = 0.0f;
+          continue;
+        }
+        const bool valid = 16 * r + i < npc;
+        v[r] = lif_v(pu[r], x, beta);
+        rr[r] = (v[r] - theta0) - pof[r];
+        es[r] = valid && rr[r] > pa[r] * pxl[r];
+        en[r] = valid && rr[r] < pa[r] * pxr[r];
+      }
+      const unsigned long long cb = __ballot((es[0] && en[0]) || (es[1] && en[1]));
       bool cut;
-      if (BLK == 1) {
-        cut = (cb & hmask) != 0ull;
-      } else if (BLK == 2) {
-        cut = cb != 0ull;
+      if (GW == 1) {
+        cut = (cb & bmask) != 0ull;
       } else {
         // one barrier per step: the flags of step k + 2 reuse this step's buffer only after the
         // barrier of step k + 1, which every wave passes after reading this step's flags
@@ -349,70 +376,150 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
         cut = any != 0;
       }
       ++kstep;
-      if (cut) {
-        const float z = rr / pa;
-        const int nout = (es ? 1 : 0) + (en ? 1 : 0);
-        // inclusive prefix sum of the output counts over the neuron's 32 slots: row shifts
-        // within 16-lane rows, then the last lane of rows 0 / 2 added to rows 1 / 3 (DPP)
-        int incl = nout;
-        incl += __builtin_amdgcn_update_dpp(0, incl, 0x111, 0xF, 0xF, true);  // row_shr:1
-        incl += __builtin_amdgcn_update_dpp(0, incl, 0x112, 0xF, 0xF, true);  // row_shr:2
-        incl += __builtin_amdgcn_update_dpp(0, incl, 0x114, 0xF, 0xF, true);  // row_shr:4
-        incl += __builtin_amdgcn_update_dpp(0, incl, 0x118, 0xF, 0xF, true);  // row_shr:8
-        incl += __builtin_amdgcn_update_dpp(0, incl, 0x142, 0xA, 0xF, false);  // row_bcast:15
-        const int p = incl - nout;
-        const int ntot = __shfl(incl, 31, 32);
-        if (ntot > K2) ovf = 1;
-        // every output slot learns its source piece (and whether it is the spiking part)
-        // from a scatter through this wave's LDS row (same-wave LDS accesses stay in order)
-        int* slot = s_slot[wv] + hb;
-        if (nout >= 1 && p < K2) slot[p] = (i << 1) | (es ? 1 : 0);
-        if (nout == 2 && p + 1 < K2) slot[p + 1] = i << 1;
-        const int src = slot[i];
-        const int idx = (src >> 1) & 31;
-        const bool is_s = (src & 1) != 0;
-        // every shuffle runs on all lanes of the neuron: a bpermute reads 0 from a lane that
-        // is switched off, so none may sit behind a per-lane condition
-        const float g_xl = __shfl(pxl, idx, 32), g_xr = __shfl(pxr, idx, 32);
-        const float g_z = __shfl(z, idx, 32), g_v = __shfl(v, idx, 32);
-        const float g_pa = __shfl(pa, idx, 32), g_po = __shfl(pof, idx, 32);
-        const int g_own = __shfl(pown, idx, 32);
+      if (__ballot(cut) != 0ull) {
+        // split and compaction for the neurons whose block has a cut (the others' lanes run
+        // along and keep their own update below)
+        float z[2];
+        int nout[2], incl[2], tot[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          z[r] = (r == 1 && !hi_p) ? 0.0f : rr[r] / pa[r];
+          nout[r] = (es[r] ? 1 : 0) + (en[r] ? 1 : 0);
+          // inclusive prefix sum over the row's 16 lanes (DPP row shifts), the row's total
+          int c = nout[r];
+          c += __builtin_amdgcn_update_dpp(0, c, 0x111, 0xF, 0xF, true);  // row_shr:1
+          c += __builtin_amdgcn_update_dpp(0, c, 0x112, 0xF, 0xF, true);  // row_shr:2
+          c += __builtin_amdgcn_update_dpp(0, c, 0x114, 0xF, 0xF, true);  // row_shr:4
+          c += __builtin_amdgcn_update_dpp(0, c, 0x118, 0xF, 0xF, true);  // row_shr:8
+          incl[r] = c;
+          tot[r] = __shfl(c, rowb + 15, WAVE);
+        }
+        const int p0 = incl[0] - nout[0];
+        const int p1 = tot[0] + incl[1] - nout[1];
+        const int ntot = tot[0] + tot[1];
         const int n_new = min(ntot, K2);
-        const bool keep = i < n_new;
-        pxl = keep ? (is_s ? g_xl : nmax(g_xl, g_z)) : INFINITY;
-        pxr = keep ? (is_s ? nmin(g_xr, g_z) : g_xr) : INFINITY;
-        pu = keep ? (is_s ? u_r : g_v) : 0.0f;
-        pa = keep ? rho * g_pa : 1.0f;
-        pof = keep ? (is_s ? rho * g_po + q : rho * g_po) : 0.0f;
-        pown = keep ? g_own : -1;
-        npc = n_new;
-      } else if (valid) {
-        pu = es ? u_r : v;
-        pof = es ? rho * pof + q : rho * pof;
-        pa = rho * pa;
+        // every output slot learns its source through an LDS scatter (same-wave LDS accesses
+        // complete in order, so the reads below see these writes); the sources' fields come
+        // from their lanes of the same row by cross-lane reads
+        int* dsc = sD[wv][g];
+        if (cut) {
+          if (nout[0] >= 1 && p0 < K2) dsc[p0] = (i << 1) | (es[0] ? 1 : 0);
+          if (nout[0] == 2 && p0 + 1 < K2) dsc[p0 + 1] = i << 1;
+          if (nout[1] >= 1 && p1 < K2) dsc[p1] = ((16 + i) << 1) | (es[1] ? 1 : 0);
+          if (nout[1] == 2 && p1 + 1 < K2) dsc[p1 + 1] = (16 + i) << 1;
+          if (ntot > K2) ovf = 1;
+        }
+        __builtin_amdgcn_wave_barrier();
+        const bool hi_o = __ballot(cut && n_new > 16) != 0ull;
+        // new fields of both registers first (the gathers read the sources' current fields),
+        // then all at once
+        float nxl[2], nxr[2], nu_[2], na[2], nof[2];
+        int now[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          nxl[r] = pxl[r];
+          nxr[r] = pxr[r];
+          nu_[r] = pu[r];
+          na[r] = pa[r];
+          nof[r] = pof[r];
+          now[r] = pown[r];
+          if (r == 1 && !hi_o && !hi_p) continue;
+          const int slot = 16 * r + i;
+          const bool keep = cut && slot < n_new;
+          const int src = keep ? dsc[slot] : 0;
+          const int idx = (src >> 1) & 31;
+          const bool is_s = (src & 1) != 0;
+          // the source's fields: both registers of its lane (a bpermute reads 0 from a lane that
+          // is switched off, so these run on every lane of the wave)
+          const int sl = rowb + (idx & 15);
+          const bool s1 = idx >= 16;
+          auto gather = [&](const float* f) {
+            const float a0 = __shfl(f[0], sl, WAVE);
+            const float a1 = hi_p ? __shfl(f[1], sl, WAVE) : 0.0f;
+            return s1 ? a1 : a0;
+          };
+          const float g_xl = gather(pxl), g_xr = gather(pxr), g_z = gather(z), g_v = gather(v);
+          const float g_pa = gather(pa), g_po = gather(pof);
+          const int o0 = __shfl(pown[0], sl, WAVE);
+          const int o1 = hi_p ? __shfl(pown[1], sl, WAVE) : 0;
+          const int g_own = s1 ? o1 : o0;
+          if (cut) {
+            nxl[r] = keep ? (is_s ? g_xl : nmax(g_xl, g_z)) : INFINITY;
+            nxr[r] = keep ? (is_s ? nmin(g_xr, g_z) : g_xr) : INFINITY;
+            nu_[r] = keep ? (is_s ? u_r : g_v) : 0.0f;
+            na[r] = keep ? rho * g_pa : 1.0f;
+            nof[r] = keep ? (is_s ? rho * g_po + q : rho * g_po) : 0.0f;
+            now[r] = keep ? g_own : -1;
+          } else if (slot < npc) {
+            nu_[r] = es[r] ? u_r : v[r];
+            nof[r] = es[r] ? rho * pof[r] + q : rho * pof[r];
+            na[r] = rho * pa[r];
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          pxl[r] = nxl[r];
+          pxr[r] = nxr[r];
+          pu[r] = nu_[r];
+          pa[r] = na[r];
+          pof[r] = nof[r];
+          pown[r] = now[r];
+        }
+        // reads of this step's sources and slots precede the next step's writes to them
+        __builtin_amdgcn_wave_barrier();
+        if (cut) npc = n_new;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          if (r == 1 && !hi_p) continue;
+          if (16 * r + i < npc) {
+            pu[r] = es[r] ? u_r : v[r];
+            pof[r] = es[r] ? rho * pof[r] + q : rho * pof[r];
+            pa[r] = rho * pa[r];
+          }
+        }
       }
       // 2. first-spike line of this step
-      const float sj = sS[ln][k], cj = sC[ln][k], whi = sHi[ln][k], wlo = sLo[ln][k];
-      const bool dl = i < nl && (ls * wlo + lc <= sj * wlo + cj) && (ls * whi + lc <= sj * whi + cj);
-      const bool dom = (__ballot(dl) & hmask) != 0ull;
+      const bool hi_l = __ballot(nl > 16) != 0ull;
+      bool dl = i < nl && (ls[0] * wlo + lc[0] <= sj * wlo + cj) &&
+                (ls[0] * whi + lc[0] <= sj * whi + cj);
+      if (hi_l)
+        dl = dl || (16 + i < nl && (ls[1] * wlo + lc[1] <= sj * wlo + cj) &&
+                    (ls[1] * whi + lc[1] <= sj * whi + cj));
+      const bool dom = (__ballot(dl) & gmask) != 0ull;
       const bool newc = (wlo < whi) && !dom && valid_n;
-      const float cx = sR[k] * rho;
-      if (newc && i == nl && nl < K1) {
-        ls = sj;
-        lc = cj;
-        lx = cx;
+      if (newc && nl < K1 && i == (nl & 15)) {
+        if (nl < 16) {
+          ls[0] = sj;
+          lc[0] = cj;
+          lx[0] = cx;
+        } else {
+          ls[1] = sj;
+          lc[1] = cj;
+          lx[1] = cx;
+        }
       }
       if (newc && nl >= K1) ovf = 1;
       const float xlo = cx * wlo + q;
       const float xhi = cx * whi + q;
       const float pd = 4e-7f * (fabsf(xhi) + 1.0f);
-      if (newc && i == npc && npc < K2) {
-        pxl = xlo - pd;
-        pxr = xhi + pd;
-        pu = u_r;
-        pa = 1.0f;
-        pof = 0.0f;
-        pown = nl;
+      if (newc && npc < K2 && i == (npc & 15)) {
+        const int r = npc >> 4;
+        if (r == 0) {
+          pxl[0] = xlo - pd;
+          pxr[0] = xhi + pd;
+          pu[0] = u_r;
+          pa[0] = 1.0f;
+          pof[0] = 0.0f;
+          pown[0] = nl;
+        } else {
+          pxl[1] = xlo - pd;
+          pxr[1] = xhi + pd;
+          pu[1] = u_r;
+          pa[1] = 1.0f;
+          pof[1] = 0.0f;
+          pown[1] = nl;
+        }
       }
       if (newc && npc >= K2) ovf = 1;
       if (newc) {
@@ -431,20 +538,24 @@ __global__ __launch_bounds__(WAVE * kAlifNPW / 2) void k_alif_build(
     NP[o] = npc;
     OVF[o] = ovf;
   }
-  if (i < K1) {
-    const size_t os = o * K1 + i;
-    LS[os] = ls;
-    LC[os] = lc;
-    LX[os] = lx;
-  }
-  if (i < K2) {
-    const size_t os = o * K2 + i;
-    POWN[os] = pown;
-    PXL[os] = pxl;
-    PXR[os] = pxr;
-    PU[os] = pu;
-    PA[os] = pa;
-    POF[os] = pof;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const int slot = 16 * r + i;
+    if (slot < K1) {
+      const size_t os = o * K1 + slot;
+      LS[os] = ls[r];
+      LC[os] = lc[r];
+      LX[os] = lx[r];
+    }
+    if (slot < K2) {
+      const size_t os = o * K2 + slot;
+      POWN[os] = pown[r];
+      PXL[os] = pxl[r];
+      PXR[os] = pxr[r];
+      PU[os] = pu[r];
+      PA[os] = pa[r];
+      POF[os] = pof[r];
+    }
   }
 }
 
@@ -1514,17 +1625,15 @@ template <int BLK>
 static void launch_alif_build(const float* I, char* w, const lsh_alif_layout& L, int64_t N, int M,
                               int C, int K1, int K2, float beta, float rho, float q, float theta0,
                               float u_r, hipStream_t st) {
-  constexpr int kAlifNPW = AlifBuildShape<BLK>::NPW;
-  const int NBLK = (int)((N + kAlifNPW - 1) / kAlifNPW);
-  int logk2 = 0;
-  while ((1 << logk2) < K2) ++logk2;
+  constexpr int NPW = AlifBuildShape<BLK>::NPW;
+  const int NBLK = (int)((N + NPW - 1) / NPW);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
-  hipLaunchKernelGGL((k_alif_build<BLK>), dim3((unsigned)((int64_t)M * NBLK)), dim3(WAVE * kAlifNPW / 2),
-                     0, st,
+  hipLaunchKernelGGL((k_alif_build<BLK>), dim3((unsigned)((int64_t)M * NBLK)),
+                     dim3(WAVE * AlifBuildShape<BLK>::NW), 0, st,
                      I, F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
                      Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),
-                     F(L.PA), F(L.POF), N, NBLK, C, K1, K2, logk2, beta, rho, q, theta0, u_r);
+                     F(L.PA), F(L.POF), N, NBLK, C, K1, K2, beta, rho, q, theta0, u_r);
 }
 
 template <int D>

@@ -98,7 +98,7 @@ def test_alif_prev_wpred(AL, dev):
 
 
 @pytest.mark.parametrize("name,beta,rho,q", NEURONS)
-@pytest.mark.parametrize("block", [1, 4])
+@pytest.mark.parametrize("block", [1, 2, 4, 8, 16])
 def test_alif_box_scan_matches_oracle(AL, dev, name, beta, rho, q, block):
     """repair = 0: every intermediate of the box scan and the replayed outputs equal the
     oracle's (same block of the split decision)."""

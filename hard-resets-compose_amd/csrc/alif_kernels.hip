@@ -562,6 +562,9 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
 // Verified carry (triton_alif.py:214-252): the first line that fires gives the first spike
 // step and x = lx*w + q; the unique piece of that line containing x gives (u, w) at the
 // chunk end.  Out of box, overflow or not exactly one piece: the chunk runs serially.
+// One neuron per 16-lane row (four a wave): slot s of the lines and pieces in lane s & 15,
+// register s >> 4, as the build keeps them; a serial fallback runs for the lanes of the
+// neurons that need it, once per chunk for the wave.
 __global__ __launch_bounds__(64) void k_alif_carry(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     const float* __restrict__ LU, const float* __restrict__ HU, const float* __restrict__ LWb,
@@ -574,16 +577,23 @@ __global__ __launch_bounds__(64) void k_alif_carry(
     int64_t N, int M, int C, int K1, int K2, float beta, float rho, float q, float theta0,
     float u_r, float rhoC) {
   const int lane = threadIdx.x;
-  const int half = lane >> 5;
-  const int i = lane & 31;
-  const int hb = half << 5;
-  const int64_t n = (int64_t)blockIdx.x * 2 + half;
+  const int g = lane >> 4;
+  const int i = lane & 15;
+  const int rowb = lane & 48;
+  const int64_t n = (int64_t)blockIdx.x * 4 + g;
   const bool valid_n = n < N;
   const int64_t nn = valid_n ? n : N - 1;
-  const unsigned long long hmask = 0xffffffffull << hb;
   float u = u0[nn], w = w0[nn];
   unsigned long long miss_acc = 0, ovf_acc = 0, lines_acc = 0, pcs_acc = 0;
   int pmax = 0;
+  // the first set bit of this row's part of a wave ballot, or -1
+  auto row_first = [&](unsigned long long b) {
+    const unsigned int r = (unsigned int)(b >> rowb) & 0xffffu;
+    return r ? __builtin_ctz(r) : -1;
+  };
+  auto row_count = [&](unsigned long long b) {
+    return __builtin_popcount((unsigned int)(b >> rowb) & 0xffffu);
+  };
   for (int m = 0; m < M; ++m) {
     const size_t o = (size_t)m * N + nn;
     if (valid_n && i == 0) {
@@ -591,30 +601,44 @@ __global__ __launch_bounds__(64) void k_alif_carry(
       SW[o] = w;
     }
     const int nl = NL[o], npc = NP[o], ovf = OVF[o];
-    const float ls = i < K1 ? LS[o * K1 + i] : 0.0f;
-    const float lc = i < K1 ? LC[o * K1 + i] : INFINITY;
-    const float lx = i < K1 ? LX[o * K1 + i] : 0.0f;
-    const bool fire = i < nl && u >= ls * w + lc;
-    const unsigned long long fm = (__ballot(fire) & hmask) >> hb;
-    const int first = fm ? __builtin_ctzll(fm) : K1;
+    float ls[2], lc[2], lx[2], pl[2], pr[2], pu_[2], pa_[2], po_[2];
+    int pw[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int slot = 16 * r + i;
+      ls[r] = slot < K1 ? LS[o * K1 + slot] : 0.0f;
+      lc[r] = slot < K1 ? LC[o * K1 + slot] : INFINITY;
+      lx[r] = slot < K1 ? LX[o * K1 + slot] : 0.0f;
+      pw[r] = slot < K2 ? POWN[o * K2 + slot] : -1;
+      pl[r] = slot < K2 ? PXL[o * K2 + slot] : INFINITY;
+      pr[r] = slot < K2 ? PXR[o * K2 + slot] : INFINITY;
+      pu_[r] = slot < K2 ? PU[o * K2 + slot] : 0.0f;
+      pa_[r] = slot < K2 ? PA[o * K2 + slot] : 0.0f;
+      po_[r] = slot < K2 ? POF[o * K2 + slot] : 0.0f;
+    }
+    // the first line that fires
+    const unsigned long long f0 = __ballot(i < nl && u >= ls[0] * w + lc[0]);
+    const unsigned long long f1 = __ballot(16 + i < nl && u >= ls[1] * w + lc[1]);
+    const int a0 = row_first(f0), a1 = row_first(f1);
+    const int first = a0 >= 0 ? a0 : (a1 >= 0 ? 16 + a1 : K1);
     const bool none_ = first == K1;
-    const float lx_first = __shfl(lx, first < K1 ? first : 0, 32);  // all lanes shuffle
-    const float lxf = none_ ? 0.0f : lx_first;
+    const int fl = rowb + (first & 15);
+    const float lx0 = __shfl(lx[0], fl, WAVE), lx1 = __shfl(lx[1], fl, WAVE);  // all lanes
+    const float lxf = none_ ? 0.0f : (first >= 16 ? lx1 : lx0);
     const float xq = lxf * w + q;
-    const int pw = i < K2 ? POWN[o * K2 + i] : -1;
-    const float pl = i < K2 ? PXL[o * K2 + i] : INFINITY;
-    const float pr = i < K2 ? PXR[o * K2 + i] : INFINITY;
-    const bool hit = i < npc && pw == first && pl <= xq && xq < pr;
-    const unsigned long long hm = (__ballot(hit) & hmask) >> hb;
-    const int nh = __builtin_popcountll(hm);
-    const int hl = hm ? __builtin_ctzll(hm) : 0;
-    const float pu_i = i < K2 ? PU[o * K2 + i] : 0.0f;
-    const float pa_i = i < K2 ? PA[o * K2 + i] : 0.0f;
-    const float po_i = i < K2 ? POF[o * K2 + i] : 0.0f;
-    const float pu_hit = __shfl(pu_i, hl, 32);
-    const float pw_hit = __shfl(pa_i * xq + po_i, hl, 32);
-    const float mu = nh ? pu_hit : 0.0f;
-    const float mw = nh ? pw_hit : 0.0f;
+    // the pieces of that line containing x
+    const bool h0 = i < npc && pw[0] == first && pl[0] <= xq && xq < pr[0];
+    const bool h1 = 16 + i < npc && pw[1] == first && pl[1] <= xq && xq < pr[1];
+    const unsigned long long hm0 = __ballot(h0), hm1 = __ballot(h1);
+    const int nh = row_count(hm0) + row_count(hm1);
+    const int b0 = row_first(hm0), b1 = row_first(hm1);
+    const int hs = b0 >= 0 ? b0 : (b1 >= 0 ? 16 + b1 : 0);  // the first hit slot
+    const int hl = rowb + (hs & 15);
+    const float pu0 = __shfl(pu_[0], hl, WAVE), pu1 = __shfl(pu_[1], hl, WAVE);
+    const float pw0 = __shfl(pa_[0] * xq + po_[0], hl, WAVE);
+    const float pw1 = __shfl(pa_[1] * xq + po_[1], hl, WAVE);
+    const float mu = nh ? (hs >= 16 ? pu1 : pu0) : 0.0f;
+    const float mw = nh ? (hs >= 16 ? pw1 : pw0) : 0.0f;
     float nu = none_ ? __fadd_rn(__fmul_rn(MA[o], u), MB[o]) : mu;
     float nw = none_ ? rhoC * w : mw;
     const bool inbox = (u >= LU[o]) && (u < HU[o]) && (w >= LWb[o]) && (w <= HWb[o]);
@@ -1760,7 +1784,7 @@ extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w
     default: launch_alif_build<16>(I, w, L, N, M, C, K1, K2, beta, rho, q, theta0, u_r, st); break;
   }
   mark(2);
-  hipLaunchKernelGGL(k_alif_carry, dim3((unsigned)((N + 1) / 2)), dim3(WAVE), 0, st, I, u0, w0,
+  hipLaunchKernelGGL(k_alif_carry, dim3((unsigned)((N + 3) / 4)), dim3(WAVE), 0, st, I, u0, w0,
                      F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
                      Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),
                      F(L.PA), F(L.POF), F(L.SU), F(L.SW), Iq(L.MISS), h, N, M, C, K1, K2, beta, rho,

@@ -488,43 +488,40 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
                     (ls[1] * whi + lc[1] <= sj * whi + cj));
       const bool dom = (__ballot(dl) & gmask) != 0ull;
       const bool newc = (wlo < whi) && !dom && valid_n;
-      if (newc && nl < K1 && i == (nl & 15)) {
-        if (nl < 16) {
-          ls[0] = sj;
-          lc[0] = cj;
-          lx[0] = cx;
-        } else {
-          ls[1] = sj;
-          lc[1] = cj;
-          lx[1] = cx;
+      if (__ballot(newc) != 0ull) {
+        // the new line goes to slot nl and its piece to slot npc, written by selects on both
+        // registers so the slots stay in registers; the whole block is skipped on the (most)
+        // steps where no row of the wave adds a line
+        const bool putl = newc && nl < K1 && i == (nl & 15);
+        const bool l1 = nl >= 16;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const bool pl = putl && (r == 1) == l1;
+          ls[r] = pl ? sj : ls[r];
+          lc[r] = pl ? cj : lc[r];
+          lx[r] = pl ? cx : lx[r];
         }
-      }
-      if (newc && nl >= K1) ovf = 1;
-      const float xlo = cx * wlo + q;
-      const float xhi = cx * whi + q;
-      const float pd = 4e-7f * (fabsf(xhi) + 1.0f);
-      if (newc && npc < K2 && i == (npc & 15)) {
-        const int r = npc >> 4;
-        if (r == 0) {
-          pxl[0] = xlo - pd;
-          pxr[0] = xhi + pd;
-          pu[0] = u_r;
-          pa[0] = 1.0f;
-          pof[0] = 0.0f;
-          pown[0] = nl;
-        } else {
-          pxl[1] = xlo - pd;
-          pxr[1] = xhi + pd;
-          pu[1] = u_r;
-          pa[1] = 1.0f;
-          pof[1] = 0.0f;
-          pown[1] = nl;
+        if (newc && nl >= K1) ovf = 1;
+        const float xlo = cx * wlo + q;
+        const float xhi = cx * whi + q;
+        const float pd = 4e-7f * (fabsf(xhi) + 1.0f);
+        const bool putp = newc && npc < K2 && i == (npc & 15);
+        const bool p1 = npc >= 16;
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const bool pp = putp && (r == 1) == p1;
+          pxl[r] = pp ? xlo - pd : pxl[r];
+          pxr[r] = pp ? xhi + pd : pxr[r];
+          pu[r] = pp ? u_r : pu[r];
+          pa[r] = pp ? 1.0f : pa[r];
+          pof[r] = pp ? 0.0f : pof[r];
+          pown[r] = pp ? nl : pown[r];
         }
-      }
-      if (newc && npc >= K2) ovf = 1;
-      if (newc) {
-        nl = min(nl + 1, K1);
-        npc = min(npc + 1, K2);
+        if (newc && npc >= K2) ovf = 1;
+        if (newc) {
+          nl = min(nl + 1, K1);
+          npc = min(npc + 1, K2);
+        }
       }
     }
     __syncthreads();  // the tile's LDS rows are rewritten next

@@ -224,6 +224,34 @@ struct AlifBuildShape {
   static constexpr int NPW = BLK >= 8 ? BLK : 16;  // neurons per workgroup
   static constexpr int NW = NPW / 4;               // waves per workgroup
 };
+// Inclusive prefix sum of c over each 16-lane row (DPP row shifts; lanes shifted in from outside
+// the row read 0).
+__device__ __forceinline__ int row_prefix16(int c) {
+  c += __builtin_amdgcn_update_dpp(0, c, 0x111, 0xF, 0xF, true);  // row_shr:1
+  c += __builtin_amdgcn_update_dpp(0, c, 0x112, 0xF, 0xF, true);  // row_shr:2
+  c += __builtin_amdgcn_update_dpp(0, c, 0x114, 0xF, 0xF, true);  // row_shr:4
+  c += __builtin_amdgcn_update_dpp(0, c, 0x118, 0xF, 0xF, true);  // row_shr:8
+  return c;
+}
+
+// The lanes (a wave-wide mask) of the blocks of BLK neurons, one neuron a 16-lane row, in which
+// the ballot b has a lane set.  Wave-uniform arithmetic on the ballot, turned back into a
+// per-lane flag by the caller with inverse_ballot.
+template <int BLK>
+__device__ __forceinline__ unsigned long long block_lanes(unsigned long long b) {
+  if (BLK >= 4) return b != 0ull ? ~0ull : 0ull;
+  const unsigned lo = (unsigned)b, hi = (unsigned)(b >> 32);
+  unsigned mlo, mhi;
+  if (BLK == 2) {
+    mlo = lo != 0u ? 0xffffffffu : 0u;
+    mhi = hi != 0u ? 0xffffffffu : 0u;
+  } else {
+    mlo = ((lo & 0xffffu) != 0u ? 0xffffu : 0u) | ((lo >> 16) != 0u ? 0xffff0000u : 0u);
+    mhi = ((hi & 0xffffu) != 0u ? 0xffffu : 0u) | ((hi >> 16) != 0u ? 0xffff0000u : 0u);
+  }
+  return ((unsigned long long)mhi << 32) | mlo;
+}
+
 constexpr int kAlifTS = 32;   // steps per tile (LDS: 5 x 16 neurons x 33 floats)
 
 // Waves per SIMD the build is compiled for (registers <= 512 / WPE per lane).  Measured at cfg5
@@ -252,6 +280,7 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
   // (and phases (a), (c) walk rows in step), which a 64-float row stride would put on one bank
   constexpr int TSP = TS + 1;
   __shared__ float sX[NPW][TSP], sS[NPW][TSP], sC[NPW][TSP], sHi[NPW][TSP], sLo[NPW][TSP], sR[TS];
+  __shared__ float sLwl[NPW][TSP], sLwh[NPW][TSP];  // sj*wlo + cj, sj*whi + cj
   __shared__ float sA[NPW], sB[NPW], sLU[NPW], sHU[NPW], sHW[NPW];
   __shared__ int s_cut[2][NW];               // per-step split flags (blocks wider than a wave)
   __shared__ int sD[NW][4][32];              // output slot -> (source slot << 1) | spiking part
@@ -268,8 +297,7 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
   const bool valid_n = n < N;
   const int64_t nn = valid_n ? n : N - 1;
   const size_t o = (size_t)m * N + nn;
-  const unsigned long long gmask = 0xffffull << (16 * g);
-  const unsigned long long bmask = BLK == 1 ? gmask : BLK == 2 ? (0xffffffffull << (32 * (g >> 1))) : ~0ull;
+  const unsigned long long vmask = __ballot(valid_n);  // lanes of neurons < N
   // per-neuron sequential state for phases (a) and (c): thread t < NPW serves neuron t
   const int64_t pn = (int64_t)blk * NPW + (tid < NPW ? tid : 0);
   const int64_t pnn = pn < N ? pn : N - 1;
@@ -331,6 +359,9 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
     if (tid < NPW) {
       for (int k = 0; k < ts; ++k) {
         const float cand = sLo[tid][k];
+        const float sjk = sS[tid][k], cjk = sC[tid][k];
+        sLwl[tid][k] = sjk * pW + cjk;  // the step's line at both ends of its w range
+        sLwh[tid][k] = sjk * sHi[tid][k] + cjk;
         sLo[tid][k] = pW;
         pW = nmax(pW, cand);
       }
@@ -340,30 +371,44 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
       // the step's input and line quantities, read before the piece stage so that their LDS
       // latency overlaps it
       const float x = sX[ln][k];
-      const float sj = sS[ln][k], cj = sC[ln][k], whi = sHi[ln][k], wlo = sLo[ln][k];
-      const float cx = sR[k] * rho;
+      const float wlo = sLo[ln][k], whi = sHi[ln][k];
+      const float lwl = sLwl[ln][k], lwh = sLwh[ln][k];
       // does any neuron of the wave hold pieces in register 1 (slots 16..31)?
       const bool hi_p = __ballot(npc > 16) != 0ull;
-      // 1. advance the post-spike pieces; a piece spikes for x <= (v - theta0 - pof)/pa
-      bool es[2], en[2];
-      float v[2], rr[2];
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        if (r == 1 && !hi_p) {
-          es[1] = en[1] = false;
-          v[1] = rr[1] = 0.0f;
-          continue;
-        }
-        const bool valid = 16 * r + i < npc;
-        v[r] = lif_v(pu[r], x, beta);
-        rr[r] = (v[r] - theta0) - pof[r];
-        es[r] = valid && rr[r] > pa[r] * pxl[r];
-        en[r] = valid && rr[r] < pa[r] * pxr[r];
+      // 1. advance the post-spike pieces; a piece spikes for x <= (v - theta0 - pof)/pa.  Every
+      // piece first takes the update of an uncut piece, in place; a split below rebuilds the
+      // fields of the cut neurons from these updated fields and from v, rho*pof and z.  Slots
+      // from npc on hold no piece: their tests are false, and their (u, a, of), advanced with
+      // the others, are never read (a slot that receives a piece gets every field written).
+      const bool va0 = i < npc;
+      const float v0 = lif_v(pu[0], x, beta);
+      const float rr0 = (v0 - theta0) - pof[0];
+      const float pa0 = pa[0];
+      const bool es0 = va0 & (rr0 > pa0 * pxl[0]);
+      const bool en0 = va0 & (rr0 < pa0 * pxr[0]);
+      const float ro0 = rho * pof[0];
+      pu[0] = es0 ? u_r : v0;
+      pof[0] = es0 ? ro0 + q : ro0;
+      pa[0] = rho * pa0;
+      unsigned long long cb = __ballot(es0 & en0);
+      bool es1 = false, en1 = false;
+      float v1 = 0.0f, rr1 = 0.0f, pa1 = 1.0f, ro1 = 0.0f;
+      if (hi_p) {
+        const bool va1 = 16 + i < npc;
+        v1 = lif_v(pu[1], x, beta);
+        rr1 = (v1 - theta0) - pof[1];
+        pa1 = pa[1];
+        es1 = va1 & (rr1 > pa1 * pxl[1]);
+        en1 = va1 & (rr1 < pa1 * pxr[1]);
+        ro1 = rho * pof[1];
+        pu[1] = es1 ? u_r : v1;
+        pof[1] = es1 ? ro1 + q : ro1;
+        pa[1] = rho * pa1;
+        cb |= __ballot(es1 & en1);
       }
-      const unsigned long long cb = __ballot((es[0] && en[0]) || (es[1] && en[1]));
-      bool cut;
+      unsigned long long cutm;  // lanes of the neurons whose block has a cut
       if (GW == 1) {
-        cut = (cb & bmask) != 0ull;
+        cutm = block_lanes<BLK>(cb);
       } else {
         // one barrier per step: the flags of step k + 2 reuse this step's buffer only after the
         // barrier of step k + 1, which every wave passes after reading this step's flags
@@ -373,125 +418,114 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
         int any = 0;
 #pragma unroll
         for (int kk = 0; kk < GW; ++kk) any |= s_cut[par][kk];
-        cut = any != 0;
+        cutm = any != 0 ? ~0ull : 0ull;
       }
       ++kstep;
-      if (__ballot(cut) != 0ull) {
-        // split and compaction for the neurons whose block has a cut (the others' lanes run
-        // along and keep their own update below)
-        float z[2];
-        int nout[2], incl[2], tot[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          z[r] = (r == 1 && !hi_p) ? 0.0f : rr[r] / pa[r];
-          nout[r] = (es[r] ? 1 : 0) + (en[r] ? 1 : 0);
-          // inclusive prefix sum over the row's 16 lanes (DPP row shifts), the row's total
-          int c = nout[r];
-          c += __builtin_amdgcn_update_dpp(0, c, 0x111, 0xF, 0xF, true);  // row_shr:1
-          c += __builtin_amdgcn_update_dpp(0, c, 0x112, 0xF, 0xF, true);  // row_shr:2
-          c += __builtin_amdgcn_update_dpp(0, c, 0x114, 0xF, 0xF, true);  // row_shr:4
-          c += __builtin_amdgcn_update_dpp(0, c, 0x118, 0xF, 0xF, true);  // row_shr:8
-          incl[r] = c;
-          tot[r] = __shfl(c, rowb + 15, WAVE);
+      if (cutm != 0ull) {
+        // split and compaction for the neurons whose block has a cut
+        const bool cut = __builtin_amdgcn_inverse_ballot_w64(cutm);
+        const float z0 = rr0 / pa0;
+        const float z1 = hi_p ? rr1 / pa1 : 0.0f;
+        const int nout0 = (es0 ? 1 : 0) + (en0 ? 1 : 0);
+        const int nout1 = (es1 ? 1 : 0) + (en1 ? 1 : 0);
+        // inclusive prefix sums over the row's 16 lanes (DPP row shifts), the row's totals
+        const int incl0 = row_prefix16(nout0);
+        const int tot0 = __shfl(incl0, rowb + 15, WAVE);
+        int incl1 = 0, tot1 = 0;
+        if (hi_p) {
+          incl1 = row_prefix16(nout1);
+          tot1 = __shfl(incl1, rowb + 15, WAVE);
         }
-        const int p0 = incl[0] - nout[0];
-        const int p1 = tot[0] + incl[1] - nout[1];
-        const int ntot = tot[0] + tot[1];
+        const int p0 = incl0 - nout0;
+        const int p1 = tot0 + incl1 - nout1;
+        const int ntot = tot0 + tot1;
         const int n_new = min(ntot, K2);
         // every output slot learns its source through an LDS scatter (same-wave LDS accesses
         // complete in order, so the reads below see these writes); the sources' fields come
         // from their lanes of the same row by cross-lane reads
         int* dsc = sD[wv][g];
         if (cut) {
-          if (nout[0] >= 1 && p0 < K2) dsc[p0] = (i << 1) | (es[0] ? 1 : 0);
-          if (nout[0] == 2 && p0 + 1 < K2) dsc[p0 + 1] = i << 1;
-          if (nout[1] >= 1 && p1 < K2) dsc[p1] = ((16 + i) << 1) | (es[1] ? 1 : 0);
-          if (nout[1] == 2 && p1 + 1 < K2) dsc[p1 + 1] = (16 + i) << 1;
+          if (nout0 >= 1 && p0 < K2) dsc[p0] = (i << 1) | (es0 ? 1 : 0);
+          if (nout0 == 2 && p0 + 1 < K2) dsc[p0 + 1] = i << 1;
+          if (nout1 >= 1 && p1 < K2) dsc[p1] = ((16 + i) << 1) | (es1 ? 1 : 0);
+          if (nout1 == 2 && p1 + 1 < K2) dsc[p1 + 1] = (16 + i) << 1;
           if (ntot > K2) ovf = 1;
         }
         __builtin_amdgcn_wave_barrier();
         const bool hi_o = __ballot(cut && n_new > 16) != 0ull;
-        // new fields of both registers first (the gathers read the sources' current fields),
-        // then all at once
-        float nxl[2], nxr[2], nu_[2], na[2], nof[2];
-        int now[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          nxl[r] = pxl[r];
-          nxr[r] = pxr[r];
-          nu_[r] = pu[r];
-          na[r] = pa[r];
-          nof[r] = pof[r];
-          now[r] = pown[r];
-          if (r == 1 && !hi_o && !hi_p) continue;
-          const int slot = 16 * r + i;
-          const bool keep = cut && slot < n_new;
-          const int src = keep ? dsc[slot] : 0;
-          const int idx = (src >> 1) & 31;
-          const bool is_s = (src & 1) != 0;
-          // the source's fields: both registers of its lane (a bpermute reads 0 from a lane that
-          // is switched off, so these run on every lane of the wave)
-          const int sl = rowb + (idx & 15);
-          const bool s1 = idx >= 16;
-          auto gather = [&](const float* f) {
-            const float a0 = __shfl(f[0], sl, WAVE);
-            const float a1 = hi_p ? __shfl(f[1], sl, WAVE) : 0.0f;
-            return s1 ? a1 : a0;
-          };
-          const float g_xl = gather(pxl), g_xr = gather(pxr), g_z = gather(z), g_v = gather(v);
-          const float g_pa = gather(pa), g_po = gather(pof);
-          const int o0 = __shfl(pown[0], sl, WAVE);
-          const int o1 = hi_p ? __shfl(pown[1], sl, WAVE) : 0;
-          const int g_own = s1 ? o1 : o0;
-          if (cut) {
-            nxl[r] = keep ? (is_s ? g_xl : nmax(g_xl, g_z)) : INFINITY;
-            nxr[r] = keep ? (is_s ? nmin(g_xr, g_z) : g_xr) : INFINITY;
-            nu_[r] = keep ? (is_s ? u_r : g_v) : 0.0f;
-            na[r] = keep ? rho * g_pa : 1.0f;
-            nof[r] = keep ? (is_s ? rho * g_po + q : rho * g_po) : 0.0f;
-            now[r] = keep ? g_own : -1;
-          } else if (slot < npc) {
-            nu_[r] = es[r] ? u_r : v[r];
-            nof[r] = es[r] ? rho * pof[r] + q : rho * pof[r];
-            na[r] = rho * pa[r];
-          }
+        // every gather first, then each field replaced once: a kept part of source piece s has
+        // bounds from s's and z, u = u_r (spiking part) or v_s, a = rho*a_s (s's updated a),
+        // of = rho*of_s (+ q for the spiking part)
+        auto gather = [&](float f0, float f1, int sl, bool s1) {
+          const float a0 = __shfl(f0, sl, WAVE);
+          const float a1 = hi_p ? __shfl(f1, sl, WAVE) : 0.0f;
+          return s1 ? a1 : a0;
+        };
+        auto gather_i = [&](int f0, int f1, int sl, bool s1) {
+          const int a0 = __shfl(f0, sl, WAVE);
+          const int a1 = hi_p ? __shfl(f1, sl, WAVE) : 0;
+          return s1 ? a1 : a0;
+        };
+        const bool keep0 = cut && i < n_new;
+        const int src0 = keep0 ? dsc[i] : 0;
+        const int idx0 = (src0 >> 1) & 31;
+        const bool iss0 = (src0 & 1) != 0;
+        const int sl0 = rowb + (idx0 & 15);
+        const bool s10 = idx0 >= 16;
+        const float g0xl = gather(pxl[0], pxl[1], sl0, s10), g0xr = gather(pxr[0], pxr[1], sl0, s10);
+        const float g0z = gather(z0, z1, sl0, s10), g0v = gather(v0, v1, sl0, s10);
+        const float g0a = gather(pa[0], pa[1], sl0, s10), g0r = gather(ro0, ro1, sl0, s10);
+        const int g0w = gather_i(pown[0], pown[1], sl0, s10);
+        bool keep1 = false, iss1 = false;
+        float g1xl = 0.0f, g1xr = 0.0f, g1z = 0.0f, g1v = 0.0f, g1a = 0.0f, g1r = 0.0f;
+        int g1w = 0;
+        if (hi_o) {
+          keep1 = cut && 16 + i < n_new;
+          const int src1 = keep1 ? dsc[16 + i] : 0;
+          const int idx1 = (src1 >> 1) & 31;
+          iss1 = (src1 & 1) != 0;
+          const int sl1 = rowb + (idx1 & 15);
+          const bool s11 = idx1 >= 16;
+          g1xl = gather(pxl[0], pxl[1], sl1, s11);
+          g1xr = gather(pxr[0], pxr[1], sl1, s11);
+          g1z = gather(z0, z1, sl1, s11);
+          g1v = gather(v0, v1, sl1, s11);
+          g1a = gather(pa[0], pa[1], sl1, s11);
+          g1r = gather(ro0, ro1, sl1, s11);
+          g1w = gather_i(pown[0], pown[1], sl1, s11);
         }
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          pxl[r] = nxl[r];
-          pxr[r] = nxr[r];
-          pu[r] = nu_[r];
-          pa[r] = na[r];
-          pof[r] = nof[r];
-          pown[r] = now[r];
+        pxl[0] = cut ? (keep0 ? (iss0 ? g0xl : nmax(g0xl, g0z)) : INFINITY) : pxl[0];
+        pxr[0] = cut ? (keep0 ? (iss0 ? nmin(g0xr, g0z) : g0xr) : INFINITY) : pxr[0];
+        pu[0] = cut ? (keep0 ? (iss0 ? u_r : g0v) : 0.0f) : pu[0];
+        pa[0] = cut ? (keep0 ? g0a : 1.0f) : pa[0];
+        pof[0] = cut ? (keep0 ? (iss0 ? g0r + q : g0r) : 0.0f) : pof[0];
+        pown[0] = cut ? (keep0 ? g0w : -1) : pown[0];
+        if (hi_o || hi_p) {
+          pxl[1] = cut ? (keep1 ? (iss1 ? g1xl : nmax(g1xl, g1z)) : INFINITY) : pxl[1];
+          pxr[1] = cut ? (keep1 ? (iss1 ? nmin(g1xr, g1z) : g1xr) : INFINITY) : pxr[1];
+          pu[1] = cut ? (keep1 ? (iss1 ? u_r : g1v) : 0.0f) : pu[1];
+          pa[1] = cut ? (keep1 ? g1a : 1.0f) : pa[1];
+          pof[1] = cut ? (keep1 ? (iss1 ? g1r + q : g1r) : 0.0f) : pof[1];
+          pown[1] = cut ? (keep1 ? g1w : -1) : pown[1];
         }
         // reads of this step's sources and slots precede the next step's writes to them
         __builtin_amdgcn_wave_barrier();
-        if (cut) npc = n_new;
-      } else {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          if (r == 1 && !hi_p) continue;
-          if (16 * r + i < npc) {
-            pu[r] = es[r] ? u_r : v[r];
-            pof[r] = es[r] ? rho * pof[r] + q : rho * pof[r];
-            pa[r] = rho * pa[r];
-          }
-        }
+        npc = cut ? n_new : npc;
       }
-      // 2. first-spike line of this step
+      // 2. first-spike line of this step: added unless a line dominates it on [wlo, whi]
       const bool hi_l = __ballot(nl > 16) != 0ull;
-      bool dl = i < nl && (ls[0] * wlo + lc[0] <= sj * wlo + cj) &&
-                (ls[0] * whi + lc[0] <= sj * whi + cj);
+      unsigned long long bl =
+          __ballot((i < nl) & (ls[0] * wlo + lc[0] <= lwl) & (ls[0] * whi + lc[0] <= lwh));
       if (hi_l)
-        dl = dl || (16 + i < nl && (ls[1] * wlo + lc[1] <= sj * wlo + cj) &&
-                    (ls[1] * whi + lc[1] <= sj * whi + cj));
-      const bool dom = (__ballot(dl) & gmask) != 0ull;
-      const bool newc = (wlo < whi) && !dom && valid_n;
-      if (__ballot(newc) != 0ull) {
+        bl |= __ballot((16 + i < nl) & (ls[1] * wlo + lc[1] <= lwl) & (ls[1] * whi + lc[1] <= lwh));
+      const unsigned long long newm = __ballot(wlo < whi) & ~block_lanes<1>(bl) & vmask;
+      if (newm != 0ull) {
         // the new line goes to slot nl and its piece to slot npc, written by selects on both
         // registers so the slots stay in registers; the whole block is skipped on the (most)
         // steps where no row of the wave adds a line
+        const bool newc = __builtin_amdgcn_inverse_ballot_w64(newm);
+        const float sj = sS[ln][k], cj = sC[ln][k];
+        const float cx = sR[k] * rho;
         const bool putl = newc && nl < K1 && i == (nl & 15);
         const bool l1 = nl >= 16;
 #pragma unroll
@@ -518,10 +552,8 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
           pown[r] = pp ? nl : pown[r];
         }
         if (newc && npc >= K2) ovf = 1;
-        if (newc) {
-          nl = min(nl + 1, K1);
-          npc = min(npc + 1, K2);
-        }
+        nl = newc ? min(nl + 1, K1) : nl;
+        npc = newc ? min(npc + 1, K2) : npc;
       }
     }
     __syncthreads();  // the tile's LDS rows are rewritten next
@@ -549,9 +581,10 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
       POWN[os] = pown[r];
       PXL[os] = pxl[r];
       PXR[os] = pxr[r];
-      PU[os] = pu[r];
-      PA[os] = pa[r];
-      POF[os] = pof[r];
+      const bool vs = slot < npc;  // the fields of an empty slot: (u, a, of) = (0, 1, 0)
+      PU[os] = vs ? pu[r] : 0.0f;
+      PA[os] = vs ? pa[r] : 1.0f;
+      POF[os] = vs ? pof[r] : 0.0f;
     }
   }
 }

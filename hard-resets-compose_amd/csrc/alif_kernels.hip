@@ -204,15 +204,19 @@ __global__ __launch_bounds__(64) void k_alif_box(const float* __restrict__ Wpred
 // slots take two registers per lane and the second is touched only while some neuron of the
 // wave holds more than 16 pieces (or lines).  Steps go in tiles of TS:
 //  0. the per-neuron line quantities of the tile, which do not depend on the pieces, are
-//     computed once per neuron into LDS: (a) one thread per neuron runs the sequential
-//     recurrences A_j = beta*A, B_j = fl(fl(beta*B) + x_j) and R_j = rho^j; (b) all threads
-//     divide, sj = R_j/A_j, cj = (theta0 - B_j)/A_j, whi_j = min(hw, (hu - cj)/sj),
-//     (lu - cj)/sj; (c) one thread per neuron runs the running max wlo_j.  Same operations as
-//     the serial formulation, so the same bits.
+//     computed once per neuron into the wave's own LDS rows (no workgroup barrier): (a) the
+//     row's lane 0 runs the sequential recurrences A_j = beta*A, B_j = fl(fl(beta*B) + x_j)
+//     and R_j = rho^j; (b) lane i of the row divides for steps 2i and 2i + 1, sj = R_j/A_j,
+//     cj = (theta0 - B_j)/A_j, whi_j = min(hw, (hu - cj)/sj), (lu - cj)/sj; (c) the running
+//     max wlo_j is a prefix over the row (DPP), and the line's values at wlo_j and whi_j are
+//     kept for the dominance test.  Same operations as the serial formulation, so the same
+//     bits.  The next tile's inputs are loaded while a tile is processed.
 //  1. per step every piece is advanced; pieces cut by the threshold are split and the list
 //     compacted: exclusive prefix sum of the output counts over the neuron's slots (DPP row
 //     shifts within its row, register 0's total added to register 1's), every output slot's
-//     source through an LDS scatter, the sources' fields read back from LDS.  The split runs
+//     source through an LDS scatter, the sources' fields read from their lanes of the row
+//     (every piece first takes the uncut update in place; a split rebuilds the cut neurons'
+//     fields from the updated ones, v, rho*of and the cut point z).  The split runs
 //     for all neurons of a block of BLK neurons when any of them has a cut (the reference's
 //     Triton block): a wave decides for blocks of up to 4 neurons with one ballot; blocks of 8
 //     or 16 (a workgroup of 2 or 4 waves) agree through LDS.
@@ -252,14 +256,37 @@ __device__ __forceinline__ unsigned long long block_lanes(unsigned long long b) 
   return ((unsigned long long)mhi << 32) | mlo;
 }
 
+// Broadcast of lane L of each 16-lane row to the row (DPP row_newbcast).
+template <int L>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + L, 0xF, 0xF, false));
+}
+
+// x of the lane before in the row (DPP row_shr:1); fill for the row's first lane.
+__device__ __forceinline__ float row_shr1_fill(float x, float fill) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(fill), __float_as_int(x), 0x111, 0xF, 0xF, false));
+}
+
+// Inclusive prefix of nmax over each 16-lane row in lane order (DPP row shifts; lanes shifted
+// in from outside the row contribute -inf), the earlier operand first.
+__device__ __forceinline__ float row_prefix_nmax16(float x) {
+  const int fill = __float_as_int(-INFINITY);
+  x = nmax(__int_as_float(__builtin_amdgcn_update_dpp(fill, __float_as_int(x), 0x111, 0xF, 0xF, false)), x);
+  x = nmax(__int_as_float(__builtin_amdgcn_update_dpp(fill, __float_as_int(x), 0x112, 0xF, 0xF, false)), x);
+  x = nmax(__int_as_float(__builtin_amdgcn_update_dpp(fill, __float_as_int(x), 0x114, 0xF, 0xF, false)), x);
+  x = nmax(__int_as_float(__builtin_amdgcn_update_dpp(fill, __float_as_int(x), 0x118, 0xF, 0xF, false)), x);
+  return x;
+}
+
 constexpr int kAlifTS = 32;   // steps per tile (LDS: 5 x 16 neurons x 33 floats)
 
 // Waves per SIMD the build is compiled for (registers <= 512 / WPE per lane).  Measured at cfg5
-// (N 16384, T 4096, BN 4, dw 0.1q / 0.3q): 5 (90 VGPRs) 3.01 / 3.53 ms, 6: 2.73 / 3.21, 7: 2.64 /
-// 3.16, 8 (64 VGPRs, 36 spilled) 3.56 / 4.14 ms; the steps are VALU-bound (~90 VALU per step of
-// a wave's 4 neurons) once 7 waves hide the per-step LDS and ballot latencies.
+// (N 16384, T 4096, BN 4, dw 0.1q / 0.3q) with the per-wave tile phases: 6 (80 VGPRs) 1.68 /
+// 2.13 ms, 7 (72 VGPRs, more spilled) 1.88 / 2.32 ms.  The steps are latency-bound (about a
+// third of the SIMD's VALU issue used), so fewer spills count for more than a seventh wave.
 #ifndef LSH_ALIF_BUILD_WPE
-#define LSH_ALIF_BUILD_WPE 7
+#define LSH_ALIF_BUILD_WPE 6
 #endif
 template <int BLK>
 __global__ __launch_bounds__(WAVE * AlifBuildShape<BLK>::NW)
@@ -276,12 +303,16 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
   constexpr int GW = BLK > 4 ? BLK / 4 : 1;  // waves per split-decision block (> 1: all of them)
   static_assert(GW == 1 || GW == NW, "a split-decision block wider than a wave is one workgroup");
   constexpr int TS = kAlifTS;
+  static_assert(TS == 32, "phase (b, c) gives each lane of a row two steps of the tile");
   // one padding column per row: the neurons of a wave read the same step of different rows
-  // (and phases (a), (c) walk rows in step), which a 64-float row stride would put on one bank
+  // (and the row leaders of phase (a) walk rows in step), which a 32-float row stride would
+  // put on one bank
   constexpr int TSP = TS + 1;
-  __shared__ float sX[NPW][TSP], sS[NPW][TSP], sC[NPW][TSP], sHi[NPW][TSP], sLo[NPW][TSP], sR[TS];
+  // a wave's tile rows: its four neurons (rows 4 wv .. 4 wv + 3), written and read by that wave
+  // only, so the tile phases need no workgroup barrier
+  __shared__ float sX[NPW][TSP], sS[NPW][TSP], sC[NPW][TSP], sHi[NPW][TSP], sLo[NPW][TSP];
+  __shared__ float sR[NPW][TSP];                     // rho^j
   __shared__ float sLwl[NPW][TSP], sLwh[NPW][TSP];  // sj*wlo + cj, sj*whi + cj
-  __shared__ float sA[NPW], sB[NPW], sLU[NPW], sHU[NPW], sHW[NPW];
   __shared__ int s_cut[2][NW];               // per-step split flags (blocks wider than a wave)
   __shared__ int sD[NW][4][32];              // output slot -> (source slot << 1) | spiking part
   const int64_t m = blockIdx.x / NBLK;
@@ -298,17 +329,10 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
   const int64_t nn = valid_n ? n : N - 1;
   const size_t o = (size_t)m * N + nn;
   const unsigned long long vmask = __ballot(valid_n);  // lanes of neurons < N
-  // per-neuron sequential state for phases (a) and (c): thread t < NPW serves neuron t
-  const int64_t pn = (int64_t)blk * NPW + (tid < NPW ? tid : 0);
-  const int64_t pnn = pn < N ? pn : N - 1;
-  const size_t po = (size_t)m * N + pnn;
-  float pA = 1.0f, pB = 0.0f, pR = 1.0f, pW = 0.0f;
-  if (tid < NPW) {
-    pW = LWb[po];
-    sLU[tid] = LU[po];
-    sHU[tid] = HU[po];
-    sHW[tid] = HWb[po];
-  }
+  // the neuron's entry box, in every lane of its row; pW: the running max of the lower w bound
+  const float lu_n = LU[o], hu_n = HU[o], hw_n = HWb[o];
+  float pW = LWb[o];
+  float pA = 1.0f, pB = 0.0f, pR = 1.0f;  // the chunk's recurrences, in the row's lane 0
   // lines and pieces: index [r] is slot 16 r + i
   float ls[2] = {0.0f, 0.0f}, lc[2] = {INFINITY, INFINITY}, lx[2] = {0.0f, 0.0f};
   int pown[2] = {-1, -1};
@@ -316,57 +340,86 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
   float pa[2] = {1.0f, 1.0f}, pof[2] = {0.0f, 0.0f};
   int nl = 0, npc = 0;
   int ovf = 0;
-  const int64_t n0 = (int64_t)blk * NPW;
-  const float* __restrict__ Iblk = I + (size_t)m * C * N;
+  // inputs of the row's neuron: lane i holds steps 2i and 2i + 1 of a tile, the next tile's
+  // loaded while a tile is processed
+  const float* __restrict__ Icol = I + (size_t)m * C * N + nn;
+  const int k0 = 2 * i, k1 = 2 * i + 1;
+  float xq0 = 0.0f, xq1 = 0.0f;
+  {
+    const int ts = min(TS, C);
+    if (k0 < ts) xq0 = Icol[(size_t)k0 * N];
+    if (k1 < ts) xq1 = Icol[(size_t)k1 * N];
+  }
   int kstep = 0;  // steps done in this chunk (parity of the split flags)
   for (int j0 = 0; j0 < C; j0 += TS) {
     const int ts = min(TS, C - j0);
-    // (a0) the tile's inputs, staged by every thread of the workgroup (neuron-contiguous runs)
-    for (int e = tid; e < NPW * ts; e += NW * WAVE) {
-      const int k = e / NPW, nu = e - k * NPW;
-      const int64_t nq = n0 + nu < N ? n0 + nu : N - 1;
-      sX[nu][k] = Iblk[(size_t)(j0 + k) * N + nq];
+    // (a0) the tile's inputs to the wave's rows; the next tile's loads issued
+    if (k0 < ts) sX[ln][k0] = xq0;
+    if (k1 < ts) sX[ln][k1] = xq1;
+    if (j0 + TS < C) {
+      const int tn = min(TS, C - j0 - TS);
+      if (k0 < tn) xq0 = Icol[(size_t)(j0 + TS + k0) * N];
+      if (k1 < tn) xq1 = Icol[(size_t)(j0 + TS + k1) * N];
     }
-    __syncthreads();
-    // (a) sequential recurrences
-    if (tid < NPW) {
+    __builtin_amdgcn_wave_barrier();
+    // (a) the sequential recurrences A_j = beta*A, B_j = fl(fl(beta*B) + x_j), R_j = rho^j, by
+    // the row's lane 0 (same operations as the serial formulation, so the same bits)
+    if (i == 0) {
       for (int k = 0; k < ts; ++k) {
-        const float x = sX[tid][k];
+        const float x = sX[ln][k];
         pA = beta * pA;
         pB = lif_v(pB, x, beta);
-        sS[tid][k] = pA;  // A_j, replaced by sj in (b)
-        sC[tid][k] = pB;  // B_j, replaced by cj in (b)
-        if (tid == 0) sR[k] = pR;
+        sS[ln][k] = pA;  // A_j, replaced by sj in (b)
+        sC[ln][k] = pB;  // B_j, replaced by cj in (b)
+        sR[ln][k] = pR;
         pR = rho * pR;
       }
-      sA[tid] = pA;
-      sB[tid] = pB;
     }
-    __syncthreads();
-    // (b) divisions, every (neuron, step) pair of the tile in parallel
-    for (int e = tid; e < NPW * ts; e += NW * WAVE) {
-      const int nu = e / ts, k = e - nu * ts;
-      const float Aj = sS[nu][k], Bj = sC[nu][k];
-      const float sj = sR[k] / Aj;
-      const float cj = (theta0 - Bj) / Aj;
-      sS[nu][k] = sj;
-      sC[nu][k] = cj;
-      sHi[nu][k] = nmin(sHW[nu], (sHU[nu] - cj) / sj);
-      sLo[nu][k] = (sLU[nu] - cj) / sj;  // candidate of the running max
+    __builtin_amdgcn_wave_barrier();
+    // (b) divisions, lane i of a row for steps 2i and 2i + 1: sj = R_j/A_j, cj = (theta0 -
+    // B_j)/A_j, whi_j = min(hw, (hu - cj)/sj), and the candidate (lu - cj)/sj of the running max
+    float sj0 = 0.0f, cj0 = 0.0f, hi0 = 0.0f, cd0 = -INFINITY;
+    float sj1 = 0.0f, cj1 = 0.0f, hi1 = 0.0f, cd1 = -INFINITY;
+    if (k0 < ts) {
+      const float Aj = sS[ln][k0];
+      sj0 = sR[ln][k0] / Aj;
+      cj0 = (theta0 - sC[ln][k0]) / Aj;
+      hi0 = nmin(hw_n, (hu_n - cj0) / sj0);
+      cd0 = (lu_n - cj0) / sj0;
     }
-    __syncthreads();
-    // (c) running max of the lower w bound: sLo[k] becomes wlo before step k
-    if (tid < NPW) {
-      for (int k = 0; k < ts; ++k) {
-        const float cand = sLo[tid][k];
-        const float sjk = sS[tid][k], cjk = sC[tid][k];
-        sLwl[tid][k] = sjk * pW + cjk;  // the step's line at both ends of its w range
-        sLwh[tid][k] = sjk * sHi[tid][k] + cjk;
-        sLo[tid][k] = pW;
-        pW = nmax(pW, cand);
-      }
+    if (k1 < ts) {
+      const float Aj = sS[ln][k1];
+      sj1 = sR[ln][k1] / Aj;
+      cj1 = (theta0 - sC[ln][k1]) / Aj;
+      hi1 = nmin(hw_n, (hu_n - cj1) / sj1);
+      cd1 = (lu_n - cj1) / sj1;
     }
-    __syncthreads();
+    // (c) the running max wlo before each step, pW folded with the candidates of the steps
+    // before it: a prefix over the row in step order (DPP row shifts, earlier operand first).
+    // nmax returns its later operand on ties and its earliest NaN, so any grouping gives the
+    // sequential fold's bits.
+    const float incl = row_prefix_nmax16(nmax(cd0, cd1));
+    const float excl = row_shr1_fill(incl, -INFINITY);  // the candidates of steps < 2i
+    const float wlo0 = nmax(pW, excl);
+    const float wlo1 = nmax(pW, nmax(excl, cd0));
+    if (k0 < ts) {
+      sS[ln][k0] = sj0;
+      sC[ln][k0] = cj0;
+      sHi[ln][k0] = hi0;
+      sLo[ln][k0] = wlo0;
+      sLwl[ln][k0] = sj0 * wlo0 + cj0;  // the step's line at both ends of its w range
+      sLwh[ln][k0] = sj0 * hi0 + cj0;
+    }
+    if (k1 < ts) {
+      sS[ln][k1] = sj1;
+      sC[ln][k1] = cj1;
+      sHi[ln][k1] = hi1;
+      sLo[ln][k1] = wlo1;
+      sLwl[ln][k1] = sj1 * wlo1 + cj1;
+      sLwh[ln][k1] = sj1 * hi1 + cj1;
+    }
+    pW = nmax(pW, row_bcast<15>(incl));
+    __builtin_amdgcn_wave_barrier();
     for (int k = 0; k < ts; ++k) {
       // the step's input and line quantities, read before the piece stage so that their LDS
       // latency overlaps it
@@ -525,7 +578,7 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
         // steps where no row of the wave adds a line
         const bool newc = __builtin_amdgcn_inverse_ballot_w64(newm);
         const float sj = sS[ln][k], cj = sC[ln][k];
-        const float cx = sR[k] * rho;
+        const float cx = sR[ln][k] * rho;
         const bool putl = newc && nl < K1 && i == (nl & 15);
         const bool l1 = nl >= 16;
 #pragma unroll
@@ -556,13 +609,12 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
         npc = newc ? min(npc + 1, K2) : npc;
       }
     }
-    __syncthreads();  // the tile's LDS rows are rewritten next
+    __builtin_amdgcn_wave_barrier();  // the tile's rows are rewritten next
   }
-  const float A = sA[ln], B = sB[ln];
   if (!valid_n) return;
   if (i == 0) {
-    MA[o] = A;
-    MB[o] = B;
+    MA[o] = pA;
+    MB[o] = pB;
     NL[o] = nl;
     NP[o] = npc;
     OVF[o] = ovf;
@@ -589,12 +641,39 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
   }
 }
 
+// 16 serial ALIF steps of a row's neuron: lane i of the 16-lane row holds the input of step i
+// in xb, and each step takes its input from that lane by a row broadcast (no load per step).
+template <int L = 0>
+__device__ __forceinline__ void alif_row_block16(float xb, float& u, float& w, float beta,
+                                                 float rho, float q, float theta0, float u_r) {
+  if constexpr (L < 16) {
+    bool s;
+    u = alif_step(u, w, row_bcast<L>(xb), beta, rho, q, theta0, u_r, s);
+    alif_row_block16<L + 1>(xb, u, w, beta, rho, q, theta0, u_r);
+  }
+}
+
+// One chunk's map as the carry reads it (one neuron per 16-lane row, slot s in lane s & 15,
+// register s >> 4), and the inputs of its first 128 steps for the serial fallback (lane i of a
+// row: step 16 b + i in xb[b]).
+constexpr int kCarryXB = 8;
+struct AlifCarryChunk {
+  float ma, mb, lu, hu, lw, hw;
+  int nl, npc, ovf;
+  float ls[2], lc[2], lx[2], pl[2], pr[2], pu[2], pa[2], po[2];
+  int pw[2];
+  float xb[kCarryXB];
+};
+
 // Verified carry (triton_alif.py:214-252): the first line that fires gives the first spike
 // step and x = lx*w + q; the unique piece of that line containing x gives (u, w) at the
 // chunk end.  Out of box, overflow or not exactly one piece: the chunk runs serially.
 // One neuron per 16-lane row (four a wave): slot s of the lines and pieces in lane s & 15,
 // register s >> 4, as the build keeps them; a serial fallback runs for the lanes of the
-// neurons that need it, once per chunk for the wave.
+// neurons that need it, once per chunk for the wave.  The next chunk's map and inputs are
+// loaded while a chunk is evaluated and replayed; with C a multiple of 16 the fallback takes
+// its inputs from registers by row broadcasts (the inputs of the steps past the first 128
+// loaded one group of 128 ahead), else it streams them row by row.
 __global__ __launch_bounds__(64) void k_alif_carry(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     const float* __restrict__ LU, const float* __restrict__ HU, const float* __restrict__ LWb,
@@ -613,6 +692,8 @@ __global__ __launch_bounds__(64) void k_alif_carry(
   const int64_t n = (int64_t)blockIdx.x * 4 + g;
   const bool valid_n = n < N;
   const int64_t nn = valid_n ? n : N - 1;
+  const bool xdpp = (C & 15) == 0;  // the fallback's inputs in registers
+  const int nb = C >> 4;            // blocks of 16 steps a chunk (xdpp)
   float u = u0[nn], w = w0[nn];
   unsigned long long miss_acc = 0, ovf_acc = 0, lines_acc = 0, pcs_acc = 0;
   int pmax = 0;
@@ -624,64 +705,109 @@ __global__ __launch_bounds__(64) void k_alif_carry(
   auto row_count = [&](unsigned long long b) {
     return __builtin_popcount((unsigned int)(b >> rowb) & 0xffffu);
   };
+  auto load = [&](int m, AlifCarryChunk& d) {
+    const size_t o = (size_t)m * N + nn;
+    if (xdpp) {
+      const float* xp = I + ((size_t)m * C + i) * N + nn;
+#pragma unroll
+      for (int b = 0; b < kCarryXB; ++b) d.xb[b] = b < nb ? xp[(size_t)(16 * b) * N] : 0.0f;
+    }
+    d.ma = MA[o];
+    d.mb = MB[o];
+    d.lu = LU[o];
+    d.hu = HU[o];
+    d.lw = LWb[o];
+    d.hw = HWb[o];
+    d.nl = NL[o];
+    d.npc = NP[o];
+    d.ovf = OVF[o];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int slot = 16 * r + i;
+      d.ls[r] = slot < K1 ? LS[o * K1 + slot] : 0.0f;
+      d.lc[r] = slot < K1 ? LC[o * K1 + slot] : INFINITY;
+      d.lx[r] = slot < K1 ? LX[o * K1 + slot] : 0.0f;
+      d.pw[r] = slot < K2 ? POWN[o * K2 + slot] : -1;
+      d.pl[r] = slot < K2 ? PXL[o * K2 + slot] : INFINITY;
+      d.pr[r] = slot < K2 ? PXR[o * K2 + slot] : INFINITY;
+      d.pu[r] = slot < K2 ? PU[o * K2 + slot] : 0.0f;
+      d.pa[r] = slot < K2 ? PA[o * K2 + slot] : 0.0f;
+      d.po[r] = slot < K2 ? POF[o * K2 + slot] : 0.0f;
+    }
+  };
+  AlifCarryChunk cur, nxt;
+  load(0, cur);
   for (int m = 0; m < M; ++m) {
+    if (m + 1 < M) load(m + 1, nxt);
     const size_t o = (size_t)m * N + nn;
     if (valid_n && i == 0) {
       SU[o] = u;
       SW[o] = w;
     }
-    const int nl = NL[o], npc = NP[o], ovf = OVF[o];
-    float ls[2], lc[2], lx[2], pl[2], pr[2], pu_[2], pa_[2], po_[2];
-    int pw[2];
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int slot = 16 * r + i;
-      ls[r] = slot < K1 ? LS[o * K1 + slot] : 0.0f;
-      lc[r] = slot < K1 ? LC[o * K1 + slot] : INFINITY;
-      lx[r] = slot < K1 ? LX[o * K1 + slot] : 0.0f;
-      pw[r] = slot < K2 ? POWN[o * K2 + slot] : -1;
-      pl[r] = slot < K2 ? PXL[o * K2 + slot] : INFINITY;
-      pr[r] = slot < K2 ? PXR[o * K2 + slot] : INFINITY;
-      pu_[r] = slot < K2 ? PU[o * K2 + slot] : 0.0f;
-      pa_[r] = slot < K2 ? PA[o * K2 + slot] : 0.0f;
-      po_[r] = slot < K2 ? POF[o * K2 + slot] : 0.0f;
-    }
+    const int nl = cur.nl, npc = cur.npc, ovf = cur.ovf;
     // the first line that fires
-    const unsigned long long f0 = __ballot(i < nl && u >= ls[0] * w + lc[0]);
-    const unsigned long long f1 = __ballot(16 + i < nl && u >= ls[1] * w + lc[1]);
+    const unsigned long long f0 = __ballot(i < nl && u >= cur.ls[0] * w + cur.lc[0]);
+    const unsigned long long f1 = __ballot(16 + i < nl && u >= cur.ls[1] * w + cur.lc[1]);
     const int a0 = row_first(f0), a1 = row_first(f1);
     const int first = a0 >= 0 ? a0 : (a1 >= 0 ? 16 + a1 : K1);
     const bool none_ = first == K1;
     const int fl = rowb + (first & 15);
-    const float lx0 = __shfl(lx[0], fl, WAVE), lx1 = __shfl(lx[1], fl, WAVE);  // all lanes
+    const float lx0 = __shfl(cur.lx[0], fl, WAVE), lx1 = __shfl(cur.lx[1], fl, WAVE);  // all lanes
     const float lxf = none_ ? 0.0f : (first >= 16 ? lx1 : lx0);
     const float xq = lxf * w + q;
     // the pieces of that line containing x
-    const bool h0 = i < npc && pw[0] == first && pl[0] <= xq && xq < pr[0];
-    const bool h1 = 16 + i < npc && pw[1] == first && pl[1] <= xq && xq < pr[1];
+    const bool h0 = i < npc && cur.pw[0] == first && cur.pl[0] <= xq && xq < cur.pr[0];
+    const bool h1 = 16 + i < npc && cur.pw[1] == first && cur.pl[1] <= xq && xq < cur.pr[1];
     const unsigned long long hm0 = __ballot(h0), hm1 = __ballot(h1);
     const int nh = row_count(hm0) + row_count(hm1);
     const int b0 = row_first(hm0), b1 = row_first(hm1);
     const int hs = b0 >= 0 ? b0 : (b1 >= 0 ? 16 + b1 : 0);  // the first hit slot
     const int hl = rowb + (hs & 15);
-    const float pu0 = __shfl(pu_[0], hl, WAVE), pu1 = __shfl(pu_[1], hl, WAVE);
-    const float pw0 = __shfl(pa_[0] * xq + po_[0], hl, WAVE);
-    const float pw1 = __shfl(pa_[1] * xq + po_[1], hl, WAVE);
+    const float pu0 = __shfl(cur.pu[0], hl, WAVE), pu1 = __shfl(cur.pu[1], hl, WAVE);
+    const float pw0 = __shfl(cur.pa[0] * xq + cur.po[0], hl, WAVE);
+    const float pw1 = __shfl(cur.pa[1] * xq + cur.po[1], hl, WAVE);
     const float mu = nh ? (hs >= 16 ? pu1 : pu0) : 0.0f;
     const float mw = nh ? (hs >= 16 ? pw1 : pw0) : 0.0f;
-    float nu = none_ ? __fadd_rn(__fmul_rn(MA[o], u), MB[o]) : mu;
+    float nu = none_ ? __fadd_rn(__fmul_rn(cur.ma, u), cur.mb) : mu;
     float nw = none_ ? rhoC * w : mw;
-    const bool inbox = (u >= LU[o]) && (u < HU[o]) && (w >= LWb[o]) && (w <= HWb[o]);
+    const bool inbox = (u >= cur.lu) && (u < cur.hu) && (w >= cur.lw) && (w <= cur.hw);
     const bool bad = !inbox || ovf != 0 || (!none_ && nh != 1);
     if (valid_n && i == 0) MISS[o] = bad ? 1 : 0;
-    if (bad) {
+    if (__ballot(bad) != 0ull) {
       float uu = u, ww = w;
-      stream_rows<16>(I + (size_t)m * C * N + nn, (size_t)N, C, [&](int64_t, float x) {
-        bool s;
-        uu = alif_step(uu, ww, x, beta, rho, q, theta0, u_r, s);
-      });
-      nu = uu;
-      nw = ww;
+      if (xdpp) {
+        // groups of 128 steps; the next group's inputs loaded while one is replayed (every
+        // lane runs the steps: the row broadcasts read lanes of rows that may not need them)
+        float xa[kCarryXB];
+#pragma unroll
+        for (int b = 0; b < kCarryXB; ++b) xa[b] = cur.xb[b];
+        for (int g0 = 0; g0 < nb; g0 += kCarryXB) {
+          float xn[kCarryXB];
+          const bool more = g0 + kCarryXB < nb;
+          if (more) {
+            const float* xp = I + ((size_t)m * C + 16 * (g0 + kCarryXB) + i) * N + nn;
+#pragma unroll
+            for (int b = 0; b < kCarryXB; ++b)
+              xn[b] = g0 + kCarryXB + b < nb ? xp[(size_t)(16 * b) * N] : 0.0f;
+          }
+#pragma unroll
+          for (int b = 0; b < kCarryXB; ++b)
+            if (g0 + b < nb) alif_row_block16(xa[b], uu, ww, beta, rho, q, theta0, u_r);
+          if (more) {
+#pragma unroll
+            for (int b = 0; b < kCarryXB; ++b) xa[b] = xn[b];
+          }
+        }
+      } else if (bad) {
+        stream_rows<4>(I + (size_t)m * C * N + nn, (size_t)N, C, [&](int64_t, float x) {
+          bool s;
+          uu = alif_step(uu, ww, x, beta, rho, q, theta0, u_r, s);
+        });
+      }
+      if (bad) {
+        nu = uu;
+        nw = ww;
+      }
     }
     u = nu;
     w = nw;
@@ -692,6 +818,7 @@ __global__ __launch_bounds__(64) void k_alif_carry(
       pcs_acc += (unsigned long long)npc;
       pmax = max(pmax, npc);
     }
+    cur = nxt;
   }
   miss_acc = wave_sum_u64(miss_acc);
   ovf_acc = wave_sum_u64(ovf_acc);

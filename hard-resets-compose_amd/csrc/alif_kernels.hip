@@ -654,12 +654,17 @@ __device__ __forceinline__ void alif_row_block16(float xb, float& u, float& w, f
 }
 
 // One chunk's map as the carry reads it (one neuron per 16-lane row, slot s in lane s & 15,
-// register s >> 4), and the inputs of its first 128 steps for the serial fallback (lane i of a
-// row: step 16 b + i in xb[b]).
+// register s >> 4): the per-neuron header, loaded two chunks ahead, and the slots below the
+// line and piece counts (loads of empty slots masked off) with the inputs of the chunk's
+// first 128 steps for the serial fallback (lane i of a row: step 16 b + i in xb[b]), loaded
+// one chunk ahead.
 constexpr int kCarryXB = 8;
-struct AlifCarryChunk {
+constexpr int kCarryWaves = 4;  // waves (of four neurons) per workgroup
+struct AlifCarryHdr {
   float ma, mb, lu, hu, lw, hw;
   int nl, npc, ovf;
+};
+struct AlifCarrySlots {
   float ls[2], lc[2], lx[2], pl[2], pr[2], pu[2], pa[2], po[2];
   int pw[2];
   float xb[kCarryXB];
@@ -668,13 +673,15 @@ struct AlifCarryChunk {
 // Verified carry (triton_alif.py:214-252): the first line that fires gives the first spike
 // step and x = lx*w + q; the unique piece of that line containing x gives (u, w) at the
 // chunk end.  Out of box, overflow or not exactly one piece: the chunk runs serially.
-// One neuron per 16-lane row (four a wave): slot s of the lines and pieces in lane s & 15,
-// register s >> 4, as the build keeps them; a serial fallback runs for the lanes of the
-// neurons that need it, once per chunk for the wave.  The next chunk's map and inputs are
-// loaded while a chunk is evaluated and replayed; with C a multiple of 16 the fallback takes
-// its inputs from registers by row broadcasts (the inputs of the steps past the first 128
-// loaded one group of 128 ahead), else it streams them row by row.
-__global__ __launch_bounds__(64) void k_alif_carry(
+// One neuron per 16-lane row (four a wave, sixteen a workgroup): slot s of the lines and
+// pieces in lane s & 15, register s >> 4, as the build keeps them; a serial fallback runs for
+// the lanes of the neurons that need it, once per chunk for the wave.  The maps are read
+// ahead of the chunk that uses them, and with C a multiple of 16 the fallback takes its inputs
+// from registers by row broadcasts (the inputs past the first 128 steps loaded one group of
+// 128 ahead), else it streams them row by row.  Workgroups of neighbouring neurons go to one
+// XCD (blockIdx b -> group (b % 8) * per + b / 8), so they share its L2 for the inputs and the
+// per-neuron arrays.  The statistics are summed per workgroup before the atomics.
+__global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     const float* __restrict__ LU, const float* __restrict__ HU, const float* __restrict__ LWb,
     const float* __restrict__ HWb, const float* __restrict__ MA, const float* __restrict__ MB,
@@ -685,11 +692,18 @@ __global__ __launch_bounds__(64) void k_alif_carry(
     float* __restrict__ SU, float* __restrict__ SW, int* __restrict__ MISS, WsHeader* hdr,
     int64_t N, int M, int C, int K1, int K2, float beta, float rho, float q, float theta0,
     float u_r, float rhoC) {
-  const int lane = threadIdx.x;
+  __shared__ unsigned long long s_acc[kCarryWaves][4];
+  __shared__ int s_max[kCarryWaves];
+  const int64_t ngroups = (N + 4 * kCarryWaves - 1) / (4 * kCarryWaves);
+  const int64_t per = gridDim.x / 8;
+  const int64_t grp = (int64_t)(blockIdx.x % 8) * per + blockIdx.x / 8;
+  if (grp >= ngroups) return;  // the whole workgroup (the grid is rounded up to 8 per XCD)
+  const int wv = threadIdx.x / WAVE;
+  const int lane = threadIdx.x % WAVE;
   const int g = lane >> 4;
   const int i = lane & 15;
   const int rowb = lane & 48;
-  const int64_t n = (int64_t)blockIdx.x * 4 + g;
+  const int64_t n = grp * (4 * kCarryWaves) + wv * 4 + g;
   const bool valid_n = n < N;
   const int64_t nn = valid_n ? n : N - 1;
   const bool xdpp = (C & 15) == 0;  // the fallback's inputs in registers
@@ -705,72 +719,80 @@ __global__ __launch_bounds__(64) void k_alif_carry(
   auto row_count = [&](unsigned long long b) {
     return __builtin_popcount((unsigned int)(b >> rowb) & 0xffffu);
   };
-  auto load = [&](int m, AlifCarryChunk& d) {
+  auto load_hdr = [&](int m, AlifCarryHdr& h) {
+    const size_t o = (size_t)m * N + nn;
+    h.ma = MA[o];
+    h.mb = MB[o];
+    h.lu = LU[o];
+    h.hu = HU[o];
+    h.lw = LWb[o];
+    h.hw = HWb[o];
+    h.nl = NL[o];
+    h.npc = NP[o];
+    h.ovf = OVF[o];
+  };
+  auto load_slots = [&](int m, const AlifCarryHdr& h, AlifCarrySlots& d) {
     const size_t o = (size_t)m * N + nn;
     if (xdpp) {
       const float* xp = I + ((size_t)m * C + i) * N + nn;
 #pragma unroll
       for (int b = 0; b < kCarryXB; ++b) d.xb[b] = b < nb ? xp[(size_t)(16 * b) * N] : 0.0f;
     }
-    d.ma = MA[o];
-    d.mb = MB[o];
-    d.lu = LU[o];
-    d.hu = HU[o];
-    d.lw = LWb[o];
-    d.hw = HWb[o];
-    d.nl = NL[o];
-    d.npc = NP[o];
-    d.ovf = OVF[o];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int slot = 16 * r + i;
-      d.ls[r] = slot < K1 ? LS[o * K1 + slot] : 0.0f;
-      d.lc[r] = slot < K1 ? LC[o * K1 + slot] : INFINITY;
-      d.lx[r] = slot < K1 ? LX[o * K1 + slot] : 0.0f;
-      d.pw[r] = slot < K2 ? POWN[o * K2 + slot] : -1;
-      d.pl[r] = slot < K2 ? PXL[o * K2 + slot] : INFINITY;
-      d.pr[r] = slot < K2 ? PXR[o * K2 + slot] : INFINITY;
-      d.pu[r] = slot < K2 ? PU[o * K2 + slot] : 0.0f;
-      d.pa[r] = slot < K2 ? PA[o * K2 + slot] : 0.0f;
-      d.po[r] = slot < K2 ? POF[o * K2 + slot] : 0.0f;
+      const bool vl = slot < h.nl, vp = slot < h.npc;  // nl <= K1, npc <= K2
+      d.ls[r] = vl ? LS[o * K1 + slot] : 0.0f;
+      d.lc[r] = vl ? LC[o * K1 + slot] : INFINITY;
+      d.lx[r] = vl ? LX[o * K1 + slot] : 0.0f;
+      d.pw[r] = vp ? POWN[o * K2 + slot] : -1;
+      d.pl[r] = vp ? PXL[o * K2 + slot] : INFINITY;
+      d.pr[r] = vp ? PXR[o * K2 + slot] : INFINITY;
+      d.pu[r] = vp ? PU[o * K2 + slot] : 0.0f;
+      d.pa[r] = vp ? PA[o * K2 + slot] : 0.0f;
+      d.po[r] = vp ? POF[o * K2 + slot] : 0.0f;
     }
   };
-  AlifCarryChunk cur, nxt;
-  load(0, cur);
+  AlifCarryHdr hc, hn, hn2;
+  AlifCarrySlots sc, sn;
+  load_hdr(0, hc);
+  load_slots(0, hc, sc);
+  if (M > 1) load_hdr(1, hn);
   for (int m = 0; m < M; ++m) {
-    if (m + 1 < M) load(m + 1, nxt);
+    if (m + 1 < M) load_slots(m + 1, hn, sn);
+    if (m + 2 < M) load_hdr(m + 2, hn2);
     const size_t o = (size_t)m * N + nn;
     if (valid_n && i == 0) {
       SU[o] = u;
       SW[o] = w;
     }
-    const int nl = cur.nl, npc = cur.npc, ovf = cur.ovf;
+    const int nl = hc.nl, npc = hc.npc, ovf = hc.ovf;
     // the first line that fires
-    const unsigned long long f0 = __ballot(i < nl && u >= cur.ls[0] * w + cur.lc[0]);
-    const unsigned long long f1 = __ballot(16 + i < nl && u >= cur.ls[1] * w + cur.lc[1]);
+    const unsigned long long f0 = __ballot(i < nl && u >= sc.ls[0] * w + sc.lc[0]);
+    const unsigned long long f1 = __ballot(16 + i < nl && u >= sc.ls[1] * w + sc.lc[1]);
     const int a0 = row_first(f0), a1 = row_first(f1);
     const int first = a0 >= 0 ? a0 : (a1 >= 0 ? 16 + a1 : K1);
     const bool none_ = first == K1;
     const int fl = rowb + (first & 15);
-    const float lx0 = __shfl(cur.lx[0], fl, WAVE), lx1 = __shfl(cur.lx[1], fl, WAVE);  // all lanes
+    const float lx0 = __shfl(sc.lx[0], fl, WAVE), lx1 = __shfl(sc.lx[1], fl, WAVE);  // all lanes
     const float lxf = none_ ? 0.0f : (first >= 16 ? lx1 : lx0);
     const float xq = lxf * w + q;
     // the pieces of that line containing x
-    const bool h0 = i < npc && cur.pw[0] == first && cur.pl[0] <= xq && xq < cur.pr[0];
-    const bool h1 = 16 + i < npc && cur.pw[1] == first && cur.pl[1] <= xq && xq < cur.pr[1];
+    const bool h0 = i < npc && sc.pw[0] == first && sc.pl[0] <= xq && xq < sc.pr[0];
+    const bool h1 = 16 + i < npc && sc.pw[1] == first && sc.pl[1] <= xq && xq < sc.pr[1];
     const unsigned long long hm0 = __ballot(h0), hm1 = __ballot(h1);
     const int nh = row_count(hm0) + row_count(hm1);
     const int b0 = row_first(hm0), b1 = row_first(hm1);
     const int hs = b0 >= 0 ? b0 : (b1 >= 0 ? 16 + b1 : 0);  // the first hit slot
     const int hl = rowb + (hs & 15);
-    const float pu0 = __shfl(cur.pu[0], hl, WAVE), pu1 = __shfl(cur.pu[1], hl, WAVE);
-    const float pw0 = __shfl(cur.pa[0] * xq + cur.po[0], hl, WAVE);
-    const float pw1 = __shfl(cur.pa[1] * xq + cur.po[1], hl, WAVE);
+    const float pu0 = __shfl(sc.pu[0], hl, WAVE), pu1 = __shfl(sc.pu[1], hl, WAVE);
+    const float pw0 = __shfl(sc.pa[0] * xq + sc.po[0], hl, WAVE);
+    const float pw1 = __shfl(sc.pa[1] * xq + sc.po[1], hl, WAVE);
     const float mu = nh ? (hs >= 16 ? pu1 : pu0) : 0.0f;
     const float mw = nh ? (hs >= 16 ? pw1 : pw0) : 0.0f;
-    float nu = none_ ? __fadd_rn(__fmul_rn(cur.ma, u), cur.mb) : mu;
+    float nu = none_ ? __fadd_rn(__fmul_rn(hc.ma, u), hc.mb) : mu;
     float nw = none_ ? rhoC * w : mw;
-    const bool inbox = (u >= cur.lu) && (u < cur.hu) && (w >= cur.lw) && (w <= cur.hw);
+    const bool inbox = (u >= hc.lu) && (u < hc.hu) && (w >= hc.lw) && (w <= hc.hw);
     const bool bad = !inbox || ovf != 0 || (!none_ && nh != 1);
     if (valid_n && i == 0) MISS[o] = bad ? 1 : 0;
     if (__ballot(bad) != 0ull) {
@@ -780,7 +802,7 @@ __global__ __launch_bounds__(64) void k_alif_carry(
         // lane runs the steps: the row broadcasts read lanes of rows that may not need them)
         float xa[kCarryXB];
 #pragma unroll
-        for (int b = 0; b < kCarryXB; ++b) xa[b] = cur.xb[b];
+        for (int b = 0; b < kCarryXB; ++b) xa[b] = sc.xb[b];
         for (int g0 = 0; g0 < nb; g0 += kCarryXB) {
           float xn[kCarryXB];
           const bool more = g0 + kCarryXB < nb;
@@ -818,7 +840,9 @@ __global__ __launch_bounds__(64) void k_alif_carry(
       pcs_acc += (unsigned long long)npc;
       pmax = max(pmax, npc);
     }
-    cur = nxt;
+    hc = hn;
+    sc = sn;
+    hn = hn2;
   }
   miss_acc = wave_sum_u64(miss_acc);
   ovf_acc = wave_sum_u64(ovf_acc);
@@ -826,6 +850,21 @@ __global__ __launch_bounds__(64) void k_alif_carry(
   pcs_acc = wave_sum_u64(pcs_acc);
   pmax = wave_max_i(pmax);
   if (lane == 0) {
+    s_acc[wv][0] = miss_acc;
+    s_acc[wv][1] = ovf_acc;
+    s_acc[wv][2] = lines_acc;
+    s_acc[wv][3] = pcs_acc;
+    s_max[wv] = pmax;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < kCarryWaves; ++k) {
+      miss_acc += s_acc[k][0];
+      ovf_acc += s_acc[k][1];
+      lines_acc += s_acc[k][2];
+      pcs_acc += s_acc[k][3];
+      pmax = max(pmax, s_max[k]);
+    }
     const unsigned long long old_lo =
         atomicAdd(&hdr->miss_count_lo, (unsigned int)(miss_acc & 0xffffffffull));
     const unsigned int carry = (old_lo + (miss_acc & 0xffffffffull)) > 0xffffffffull ? 1u : 0u;
@@ -1941,7 +1980,10 @@ extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w
     default: launch_alif_build<16>(I, w, L, N, M, C, K1, K2, beta, rho, q, theta0, u_r, st); break;
   }
   mark(2);
-  hipLaunchKernelGGL(k_alif_carry, dim3((unsigned)((N + 3) / 4)), dim3(WAVE), 0, st, I, u0, w0,
+  // workgroups of 16 neurons, the grid rounded up to a multiple of 8 (one share per XCD)
+  const int64_t carry_groups = (N + 4 * kCarryWaves - 1) / (4 * kCarryWaves);
+  hipLaunchKernelGGL(k_alif_carry, dim3((unsigned)(8 * ((carry_groups + 7) / 8))),
+                     dim3(WAVE * kCarryWaves), 0, st, I, u0, w0,
                      F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
                      Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),
                      F(L.PA), F(L.POF), F(L.SU), F(L.SW), Iq(L.MISS), h, N, M, C, K1, K2, beta, rho,

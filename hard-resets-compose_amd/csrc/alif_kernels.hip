@@ -56,12 +56,14 @@ __global__ __launch_bounds__(64) void k_alif_fwd(const float* __restrict__ I,
                                                  float* __restrict__ eu, float* __restrict__ ew,
                                                  int64_t N, int64_t Ls, int NB, float beta, float rho,
                                                  float q, float theta0, float u_r,
-                                                 const float* __restrict__ dpar) {
+                                                 const float* __restrict__ dpar,
+                                                 const int* __restrict__ mstar) {
   if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
   const int64_t m = blockIdx.x / NB;
   const int nb = (int)(blockIdx.x - m * NB);
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
   if (n >= N) return;
+  if (mstar && m >= mstar[n]) return;  // a start that a later serial pass replaces
   float u = su[m * N + n], w = sw[m * N + n];
   const size_t base = (size_t)m * (size_t)Ls * (size_t)N + (size_t)n;
   const float* __restrict__ Ip = I + base;
@@ -689,9 +691,9 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     const float* __restrict__ LS, const float* __restrict__ LC, const float* __restrict__ LX,
     const int* __restrict__ POWN, const float* __restrict__ PXL, const float* __restrict__ PXR,
     const float* __restrict__ PU, const float* __restrict__ PA, const float* __restrict__ POF,
-    float* __restrict__ SU, float* __restrict__ SW, int* __restrict__ MISS, WsHeader* hdr,
-    int64_t N, int M, int C, int K1, int K2, float beta, float rho, float q, float theta0,
-    float u_r, float rhoC) {
+    float* __restrict__ SU, float* __restrict__ SW, int* __restrict__ MISS,
+    int* __restrict__ MSTAR, WsHeader* hdr, int64_t N, int M, int C, int K1, int K2, float beta,
+    float rho, float q, float theta0, float u_r, float rhoC) {
   __shared__ unsigned long long s_acc[kCarryWaves][4];
   __shared__ int s_max[kCarryWaves];
   const int64_t ngroups = (N + 4 * kCarryWaves - 1) / (4 * kCarryWaves);
@@ -709,6 +711,10 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
   const bool xdpp = (C & 15) == 0;  // the fallback's inputs in registers
   const int nb = C >> 4;            // blocks of 16 steps a chunk (xdpp)
   float u = u0[nn], w = w0[nn];
+  // mstar: the first chunk whose start came through a map (so it agrees with the serial
+  // recurrence only to rounding); the starts before it came from (u0, w0) through serial
+  // replays only, so they are the serial recurrence's states
+  int mstar = M;
   unsigned long long miss_acc = 0, ovf_acc = 0, lines_acc = 0, pcs_acc = 0;
   int pmax = 0;
   // the first set bit of this row's part of a wave ballot, or -1
@@ -833,6 +839,7 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     }
     u = nu;
     w = nw;
+    if (!bad && mstar == M) mstar = m + 1;
     if (valid_n && i == 0) {
       miss_acc += bad ? 1ull : 0ull;
       ovf_acc += ovf ? 1ull : 0ull;
@@ -844,6 +851,7 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     sc = sn;
     hn = hn2;
   }
+  if (valid_n && i == 0) MSTAR[nn] = mstar;
   miss_acc = wave_sum_u64(miss_acc);
   ovf_acc = wave_sum_u64(ovf_acc);
   lines_acc = wave_sum_u64(lines_acc);
@@ -948,65 +956,6 @@ __global__ __launch_bounds__(256) void k_alif_repair(
     __syncthreads();
   }
   if (tid == 0) atomicMax(&hdr->repair_iters, (unsigned int)rounds);
-}
-
-// Repair to convergence in one ordered pass over each neuron's chunks (lsh_alif_scan_fwd with
-// repair = -1; the result of Jacobi rounds run until nothing changes, which is the serial
-// recurrence): chunk m's exact entry is chunk m-1's exact exit; a chunk whose carried start
-// (u, w) differs from it in any bit is replayed from it, which writes its U, W, S and gives its
-// exact exit; a chunk whose start agrees keeps its replay and its exit.  Every chunk is replayed
-// at most once more, where the Jacobi rounds advance the exact prefix by one chunk per round
-// when the carried w agrees with the exact one only to rounding (20 rounds at cfg5).  One lane
-// per neuron; the wave runs a chunk's replay when any of its lanes needs it (lanes that do not
-// store nothing), with the chunk's inputs streamed 16 rows ahead and the next chunk's starts
-// and exits loaded during the current one.
-__global__ __launch_bounds__(64) void k_alif_chain(
-    const float* __restrict__ I, float* __restrict__ U, float* __restrict__ W, float* __restrict__ S,
-    const float* __restrict__ su, const float* __restrict__ sw, const float* __restrict__ eu,
-    const float* __restrict__ ew, int64_t N, int M, int C, float beta, float rho, float q,
-    float theta0, float u_r) {
-  const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
-  const bool valid = n < N;
-  const int64_t nn = valid ? n : N - 1;
-  float xu = eu[nn], xw = ew[nn];  // exact exit of chunk 0 (its start, (u0, w0), is exact)
-  float nsu = 0.0f, nsw = 0.0f, neu = 0.0f, new_ = 0.0f;
-  if (M > 1) {
-    const size_t o1 = (size_t)N + nn;
-    nsu = su[o1];
-    nsw = sw[o1];
-    neu = eu[o1];
-    new_ = ew[o1];
-  }
-  for (int m = 1; m < M; ++m) {
-    const float csu = nsu, csw = nsw, ceu = neu, cew = new_;
-    if (m + 1 < M) {  // the next chunk's starts and exits, loaded while this one runs
-      const size_t on = (size_t)(m + 1) * N + nn;
-      nsu = su[on];
-      nsw = sw[on];
-      neu = eu[on];
-      new_ = ew[on];
-    }
-    const bool redo = valid && !(same_bits(xu, csu) && same_bits(xw, csw));
-    if (__ballot(redo) != 0ull) {
-      float u = xu, w = xw;
-      const size_t base = (size_t)m * C * N + nn;
-      stream_rows<16>(I + base, (size_t)N, C, [&](int64_t j, float x) {
-        bool s;
-        u = alif_step(u, w, x, beta, rho, q, theta0, u_r, s);
-        if (redo) {
-          const size_t o = base + (size_t)j * N;
-          st_nt(U + o, u);
-          st_nt(W + o, w);
-          st_nt(S + o, s ? 1.0f : 0.0f);
-        }
-      });
-      xu = redo ? u : ceu;
-      xw = redo ? w : cew;
-    } else {
-      xu = ceu;
-      xw = cew;
-    }
-  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1140,10 +1089,16 @@ constexpr int ALIF_PIPE_P = 15;
 #endif
 constexpr int ALIF_FPIPE_D = LSH_ALIF_FPIPE_D;
 
+//
+// With mstar (the box scan's repair to convergence): the rows from chunk c0 on, c0 the least
+// mstar of the block's neurons, from the exact exits (eu, ew) of chunk c0 - 1 (which the replay
+// of the chunks below mstar wrote); rows before c0 C are left as they are.
 __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     float* __restrict__ U, float* __restrict__ W, float* __restrict__ S, int64_t N, int64_t T,
-    float beta, float rho, float q, float theta0, float u_r, const float* __restrict__ dpar) {
+    float beta, float rho, float q, float theta0, float u_r, const float* __restrict__ dpar,
+    const int* __restrict__ mstar, const float* __restrict__ eu, const float* __restrict__ ew,
+    int C) {
   if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
   constexpr int D = ALIF_FPIPE_D, P = ALIF_PIPE_P, R = (D + P - 1) / P;
   __shared__ float sX[2][D][WAVE];
@@ -1155,12 +1110,19 @@ __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
   const bool valid = nb0 + lane < N;
   const unsigned ln = valid ? lane : (unsigned)(N - 1 - nb0);
   const unsigned lb = ln * 4u, sb = lane * 4u;
-  const int64_t ntiles = (T + D - 1) / D;
-  auto rows = [&](int64_t k) { return (int)(T - k * D > D ? D : T - k * D); };
+  // first chunk of the block's pass (the same in every wave of the block)
+  int c0 = 0;
+  if (mstar) c0 = -wave_max_i(-(valid ? mstar[nb0 + lane] : 0x7fffffff));
+  const int64_t row0 = (int64_t)c0 * C;
+  const int64_t Tr = T > row0 ? T - row0 : 0;
+  const int64_t ntiles = (Tr + D - 1) / D;
+  auto rows = [&](int64_t k) { return (int)(Tr - k * D > D ? D : Tr - k * D); };
 
   if (w == 0) {  // consumer: tile k - 1 in round k
     __builtin_amdgcn_s_setprio(3);
-    float u = u0[nb0 + ln], ww = w0[nb0 + ln];
+    const bool from_exit = c0 > 0 && ntiles > 0;
+    const size_t oe = from_exit ? (size_t)(c0 - 1) * (size_t)N + (size_t)(nb0 + ln) : 0;
+    float u = from_exit ? eu[oe] : u0[nb0 + ln], ww = from_exit ? ew[oe] : w0[nb0 + ln];
     for (int64_t k = 0; k <= ntiles + 1; ++k) {
       if (k >= 1 && k <= ntiles) {
         const int buf = (int)((k - 1) & 1);
@@ -1200,7 +1162,7 @@ __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int j = p + r * P;
-      if (j < nr) xr[r] = ld_row(I + (size_t)(k * D + j) * (size_t)N + (size_t)nb0, lb);
+      if (j < nr) xr[r] = ld_row(I + (size_t)(row0 + k * D + j) * (size_t)N + (size_t)nb0, lb);
     }
   };
   if (ntiles > 0) load(0);
@@ -1225,7 +1187,7 @@ __global__ __launch_bounds__(WAVE*(ALIF_PIPE_P + 1)) void k_alif_fwd_pipe(
       for (int r = 0; r < R; ++r) {
         const int j = p + r * P;
         if (j < nr) {
-          const size_t row = (size_t)((k - 2) * D + j) * (size_t)N + (size_t)nb0;
+          const size_t row = (size_t)(row0 + (k - 2) * D + j) * (size_t)N + (size_t)nb0;
           const float2 o = sUW[buf][j][lane];
           const float2 pr = j == 0 ? sEntry[buf][lane] : sUW[buf][j - 1][lane];
           const bool sp = lif_v(pr.x, x2[r], beta) >= theta0 + pr.y;
@@ -1827,6 +1789,7 @@ static void alif_scan_layout(int64_t T, int64_t N, int C, int K1, int K2, lsh_al
   L->EU = c.take(mn);
   L->EW = c.take(mn);
   L->MISS = c.take(mn);
+  L->MSTAR = c.take((size_t)N * 4);
   L->LIST0 = c.take(nb * (size_t)M * WAVE * 4);
   L->LIST1 = c.take(nb * (size_t)M * WAVE * 4);
   L->total = c.off;
@@ -1860,10 +1823,10 @@ template <int D>
 static void launch_alif_fwd(const float* I, const float* su, const float* sw, float* U, float* W,
                             float* S, float* eu, float* ew, int64_t N, int64_t Ls, int64_t M,
                             float beta, float rho, float q, float theta0, float u_r, hipStream_t st,
-                            const float* dpar = nullptr) {
+                            const float* dpar = nullptr, const int* mstar = nullptr) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   hipLaunchKernelGGL(k_alif_fwd<D>, dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, su, sw, U, W, S,
-                     eu, ew, N, Ls, NB, beta, rho, q, theta0, u_r, dpar);
+                     eu, ew, N, Ls, NB, beta, rho, q, theta0, u_r, dpar, mstar);
 }
 
 }  // namespace lsh
@@ -1880,7 +1843,7 @@ extern "C" int lsh_alif_serial_fwd(const float* I, const float* u0, const float*
   const int NB = (int)((N + WAVE - 1) / WAVE);
   hipLaunchKernelGGL(k_alif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)), 0,
                      (hipStream_t)stream, I, u0, w0, U, W, S, N, T, beta, rho, q, theta0, u_r,
-                     nullptr);
+                     nullptr, nullptr, nullptr, nullptr, 1);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }
@@ -1896,7 +1859,7 @@ extern "C" int lsh_alif_serial_fwd_dparams(const float* I, const float* u0, cons
   const int NB = (int)((N + WAVE - 1) / WAVE);
   hipLaunchKernelGGL(k_alif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)), 0,
                      (hipStream_t)stream, I, u0, w0, U, W, S, N, T, 0.0f, 0.0f, 0.0f, 0.0f, u_r,
-                     params);
+                     params, nullptr, nullptr, nullptr, 1);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }
@@ -1986,15 +1949,20 @@ extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w
                      dim3(WAVE * kCarryWaves), 0, st, I, u0, w0,
                      F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
                      Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),
-                     F(L.PA), F(L.POF), F(L.SU), F(L.SW), Iq(L.MISS), h, N, M, C, K1, K2, beta, rho,
-                     q, theta0, u_r, rhoC);
+                     F(L.PA), F(L.POF), F(L.SU), F(L.SW), Iq(L.MISS), Iq(L.MSTAR), h, N, M, C, K1,
+                     K2, beta, rho, q, theta0, u_r, rhoC);
   mark(3);
+  // repair to convergence: the replay covers the chunks whose starts are the serial states
+  // (below mstar), and one serial pass per block of 64 neurons runs from the block's least
+  // mstar on, from the exact exit before it (the converged Jacobi rounds' result)
+  const bool chain = repair == -1 && M > 1;
   launch_alif_fwd<16>(I, F(L.SU), F(L.SW), U, W, S, F(L.EU), F(L.EW), N, C, M, beta, rho, q, theta0,
-                      u_r, st);
+                      u_r, st, nullptr, chain ? Iq(L.MSTAR) : nullptr);
   mark(4);
-  if (repair == -1 && M > 1) {
-    hipLaunchKernelGGL(k_alif_chain, dim3((unsigned)NB), dim3(WAVE), 0, st, I, U, W, S, F(L.SU),
-                       F(L.SW), F(L.EU), F(L.EW), N, M, C, beta, rho, q, theta0, u_r);
+  if (chain) {
+    hipLaunchKernelGGL(k_alif_fwd_pipe, dim3((unsigned)NB), dim3(WAVE * (ALIF_PIPE_P + 1)), 0, st,
+                       I, u0, w0, U, W, S, N, T, beta, rho, q, theta0, u_r, nullptr, Iq(L.MSTAR),
+                       F(L.EU), F(L.EW), C);
   } else if (repair > 0 && M > 1) {
     const int64_t rounds = repair < (int64_t)M ? repair : (int64_t)M;
     hipLaunchKernelGGL(k_alif_repair, dim3((unsigned)NB), dim3(256), 0, st, I, U, W, S, F(L.SU),

@@ -66,8 +66,8 @@ class AffLayout(ctypes.Structure):
 class ALIFLayout(ctypes.Structure):
     _fields_ = [(n, ctypes.c_size_t) for n in (
         "EC", "EA", "EB", "LU", "HU", "LW", "HW", "MA", "MB", "NL", "NP", "OVF", "LS", "LC", "LX",
-        "POWN", "PXL", "PXR", "PU", "PA", "POF", "SU", "SW", "EU", "EW", "MISS", "LIST0", "LIST1",
-        "total")]
+        "POWN", "PXL", "PXR", "PU", "PA", "POF", "SU", "SW", "EU", "EW", "MISS", "MSTAR", "LIST0",
+        "LIST1", "total")]
 
 
 # name -> (restype, argtypes); mirrors include/lifscan_hip.h

@@ -126,11 +126,13 @@ class _ALIFRun:
         return L
 
     def view(self, name, dtype=torch.float32):
-        """[M, N] arrays; LS/LC/LX as [M, K1, N] and piece arrays as [M, K2, N] (the reference's
-        layout; the workspace stores them slot-contiguous, [M, N, K])."""
+        """[M, N] arrays; MSTAR as [N]; LS/LC/LX as [M, K1, N] and piece arrays as [M, K2, N]
+        (the reference's layout; the workspace stores them slot-contiguous, [M, N, K])."""
         L = self.layout()
         M = self.T // self.C
         off = getattr(L, name)
+        if name == "MSTAR":
+            return self.ws[off:off + 4 * self.N].view(dtype)
         if name in ("LS", "LC", "LX"):
             K = self.K1
         elif name in ("POWN", "PXL", "PXR", "PU", "PA", "POF"):

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define LSH_ABI_VERSION 1
+#define LSH_ABI_VERSION 2
 
 #define LSH_OK 0
 #define LSH_ERR_ARG (-1)          /* null pointer or bad scalar argument */
@@ -277,15 +277,17 @@ int lsh_alif_warm_predict(const float* I, const float* u0, const float* w0, cons
  * triton_alif.py:301-358 (alif_scan_forward), :96-186 (build), :214-252 (carry).
  * K1 <= 32, K2 <= 32 and a power of two, T % C == 0.  repair: the maximum number of Jacobi
  * rounds (0 = none; T/C or more converges, stats' repair_iters counts them), or -1: repair to
- * convergence by one ordered pass over every neuron's chunks (each chunk whose carried start
- * differs from the previous chunk's exact exit is replayed once from it): the same U, W, S as
- * converged Jacobi rounds, the serial recurrence; repair_iters is then not counted (0). */
+ * convergence: the chunks whose carried starts are the serial states (those before MSTAR, the
+ * first chunk whose start the carry took through a map) are replayed in parallel, and one
+ * serial pass per 64 neurons runs from the least MSTAR on: the same U, W, S as converged
+ * Jacobi rounds, the serial recurrence; repair_iters is then not counted (0). */
 typedef struct lsh_alif_layout {
   size_t EC, EA, EB, LU, HU, LW, HW; /* envelope maps, box [M, N] */
   size_t MA, MB, NL, NP, OVF;        /* per-chunk scalars [M, N] (NL, NP, OVF int32) */
   size_t LS, LC, LX;                 /* first-spike lines [M, N, K1] */
   size_t POWN, PXL, PXR, PU, PA, POF; /* post-spike pieces [M, N, K2] (POWN int32) */
   size_t SU, SW, EU, EW, MISS;       /* chunk entry / exit states, carry misses [M, N] */
+  size_t MSTAR;                      /* [N] int32: first chunk whose start came through a map */
   size_t LIST0, LIST1;               /* repair work lists */
   size_t total;
 } lsh_alif_layout;

@@ -132,10 +132,47 @@ def test_alif_box_scan_matches_oracle(AL, dev, name, beta, rho, q, block):
         for g in ("SU", "SW"):
             assert np.array_equal(host(run.view(g)), keep[g]), (tag, g)
         assert np.array_equal(host(run.view("MISS", torch.int32)), keep["MISS"]), tag
+        # the first chunk whose start the carry took through a map: chunk m's start is the
+        # serial state while every chunk before it was replayed serially (a miss)
+        miss = keep["MISS"]
+        used_map = np.nonzero(miss == 0)
+        mstar = np.full(N, T // C, np.int32)
+        for m_, n_ in zip(*used_map):
+            mstar[n_] = min(mstar[n_], m_ + 1)
+        assert np.array_equal(host(run.view("MSTAR", torch.int32)), mstar), tag
         assert np.array_equal(host(U), Uo) and np.array_equal(host(W), Wo) and np.array_equal(host(S), So)
         for k in ("miss_frac", "overflow_frac", "mean_lines", "mean_pieces"):
             assert st[k] == pytest.approx(sto[k], abs=1e-12), (tag, k)
         assert st["max_pieces"] == sto["max_pieces"] and st["repair_iters"] == 0
+
+
+def test_alif_box_scan_chunk_not_multiple_of_16(AL, dev):
+    """C = 40: the carry's fallback streams its inputs row by row (the register path needs C a
+    multiple of 16) and the converged pass starts inside a 64-row tile; intermediates equal the
+    oracle's, the converged scan the serial recurrence."""
+    beta, rho, q = 0.95, 0.995, 0.9
+    T, N, C = 2000, 70, 40
+    I = _inputs(beta, 2.0, T, N, 15)
+    u0 = np.zeros(N, np.float32)
+    w0 = uniform(N, 0.0, 0.1, 16)
+    (Ur, Wr, Sr), preds = _preds(I, beta, rho, q, u0, w0, C)
+    for tag in ("oracle", "warm4"):
+        Wp = preds[tag]
+        print(f"alif box C=40 pred={tag}", flush=True)
+        st, sto, keep = {}, {}, {}
+        U, W, S = AL.alif_scan_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev),
+                                       gpu(Wp, dev), 0.1 * q, C=C, K1=16, K2=32, BN=4, repair=0, stats=st)
+        run = AL.last_alif_run()
+        Uo, Wo, So = A.scan_forward(I, beta, rho, q, 1.0, 0.0, u0, w0, Wp, 0.1 * q, C=C, K1=16, K2=32,
+                                    block=4, repair=0, stats=sto, keep=keep)
+        for g in ("SU", "SW"):
+            assert np.array_equal(host(run.view(g)), keep[g]), (tag, g)
+        assert np.array_equal(host(run.view("MISS", torch.int32)), keep["MISS"]), tag
+        assert np.array_equal(host(U), Uo) and np.array_equal(host(W), Wo) and np.array_equal(host(S), So)
+        U, W, S = AL.alif_scan_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev),
+                                       gpu(Wp, dev), 0.1 * q, C=C, K1=16, K2=32, BN=4, repair=10 ** 6)
+        assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), tag
+        assert np.array_equal(host(S), Sr), tag
 
 
 @pytest.mark.parametrize("name,beta,rho,q", NEURONS)

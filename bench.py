@@ -601,8 +601,9 @@ def dominant_only(L, torch, dev):
 def counters_workload(torch, dev):
     """Short program for counter passes (rocprofv3 --pmc) over the kernels that are not HBM-bound
     by design, each launched once or twice at its configuration: a 256 MiB copy (FETCH/WRITE
-    calibration); cfg5's box scan with repair, converged (k_alif_build<4,4>, k_alif_carry,
-    k_alif_chain) and with the statistics (k_alif_repair); cfg2's map scan at C = 128, K = 8
+    calibration); cfg5's box scan with repair, converged (k_alif_build<4>, k_alif_carry, the
+    replay k_alif_fwd<16> below MSTAR and the serial pass k_alif_fwd_pipe from it) and with the
+    statistics (k_alif_repair); cfg2's map scan at C = 128, K = 8
     (k_lif_build<8,8>, k_lif_carry<8>); at cfg4: the converged forward (k_lif_fwd_warm,
     k_lif_repair_wide), the long-chunk map scan in pieces (k_lif_build<32,8>,
     k_lif_carry_staged<32>) and with the associative carry (k_map_scan), v4 at C 2048 / G 4 /

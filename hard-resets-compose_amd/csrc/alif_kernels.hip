@@ -1375,8 +1375,11 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
     float* __restrict__ DW0, double* __restrict__ partials, int64_t N, int M, float beta,
     float rho, float q, float theta0, float alpha, float u_r, const float* __restrict__ dpar) {
   if (dpar) alif_params_from(dpar, beta, rho, q, theta0);
-  __shared__ float sP[WV][WAVE], sQ[WV][WAVE];
-  __shared__ float sLw[WAVE], sLv[WAVE];
+  // the two recurrences' chunk aggregates in separate arrays and the lv carry double-buffered
+  // by round parity, so a round needs two barriers: round r + 1 writes nothing that a wave
+  // still in round r reads (every reader passes one of the two barriers first)
+  __shared__ float sP1[WV][WAVE], sQ1[WV][WAVE], sP2[WV][WAVE], sQ2[WV][WAVE];
+  __shared__ float sLw[WAVE], sLv[2][WAVE];
   __shared__ double sAcc[WV][4];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE);
   const unsigned lane = threadIdx.x % WAVE;
@@ -1389,11 +1392,12 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
   ParamAcc acc;
   if (w == 0) {
     sLw[lane] = 0.0f;
-    sLv[lane] = 0.0f;
+    sLv[0][lane] = 0.0f;
   }
   __syncthreads();
   const int rounds = (M + WV - 1) / WV;
   for (int r = 0; r < rounds; ++r) {
+    const int par = r & 1;
     const int m = M - 1 - (r * WV + w);
     const bool active = m >= 0;
     const size_t row0 = (size_t)(active ? m : 0) * C;
@@ -1449,13 +1453,13 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
         P = a * P;
         Q = a * Q - sg[j] * g[j];
       }
-      sP[w][lane] = P;
-      sQ[w][lane] = Q;
+      sP1[w][lane] = P;
+      sQ1[w][lane] = Q;
     }
     __syncthreads();
     if (active) {
       float lam = sLw[lane];
-      for (int v = 0; v < w; ++v) lam = sQ[v][lane] + sP[v][lane] * lam;
+      for (int v = 0; v < w; ++v) lam = sQ1[v][lane] + sP1[v][lane] * lam;
 #pragma unroll
       for (int j = C - 1; j >= 0; --j) {
         lwv[j] = lam;
@@ -1464,7 +1468,6 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
       lw_end = lam;
       if (m == 0 && DW0 && valid) DW0[nb0 + lane] = lam;
     }
-    __syncthreads();
     if (active) {
       float P = 1.0f, Q = 0.0f;
 #pragma unroll
@@ -1473,13 +1476,13 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
         P = a * P;
         Q = a * Q + sg[j] * (g[j] + q * lwv[j]);
       }
-      sP[w][lane] = P;
-      sQ[w][lane] = Q;
+      sP2[w][lane] = P;
+      sQ2[w][lane] = Q;
     }
     __syncthreads();
     if (active) {
-      float lam = sLv[lane];
-      for (int v = 0; v < w; ++v) lam = sQ[v][lane] + sP[v][lane] * lam;
+      float lam = sLv[par][lane];
+      for (int v = 0; v < w; ++v) lam = sQ2[v][lane] + sP2[v][lane] * lam;
       const Buf bo(LW + nb0 + row0 * N), bv(LV + nb0 + row0 * N);
       float cb = 0.0f, cr = 0.0f, cq = 0.0f, ct = 0.0f;  // PS: this chunk's sums
 #pragma unroll
@@ -1500,13 +1503,12 @@ __global__ __launch_bounds__(WAVE* WV) void k_alif_bwd_fused(
       if (PS && valid) acc.add_chunk(cb, cr, cq, ct);
       lv_end = lam;
     }
-    __syncthreads();
+    // the carries into the next round (its readers are past the next round's first barrier)
     const int last = min(WV, M - r * WV) - 1;
     if (w == last) {
       sLw[lane] = lw_end;
-      sLv[lane] = lv_end;
+      sLv[par ^ 1][lane] = lv_end;
     }
-    __syncthreads();
   }
   if (PS) {
     acc.wave_sum();

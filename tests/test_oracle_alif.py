@@ -6,7 +6,9 @@
   and deliberately bad boxes, for two block sizes of the split decision (the reference's own
   contract, tests/test_alif.py:10-39);
 * states the carry predicts without falling back land on the serial end state (u exactly,
-  w to rounding);
+  w to rounding), and exactly, u and w bit for bit, on dyadic inputs with beta = rho = 1/2,
+  where every operation of the build and the carry is exact (first-spike lines, post-spike
+  pieces and the no-spike map pinned, not only to rounding);
 * the warm predictor equals its definition; the adjoint equals fp64 autograd through the
   recurrence (tests/test_alif_grad.py:8-36 restated).
 """
@@ -95,6 +97,41 @@ def test_carry_predictions_land_on_the_serial_state():
         exact += int((ok & (SU[m + 1] == su)).sum())
         checked += int(ok.sum())
     assert checked > 100 and exact > 0.8 * checked
+
+
+def test_carry_is_exact_on_dyadic_inputs():
+    """beta = rho = 1/2 and q, theta0, u_r, the entries, the box and the inputs on dyadic grids:
+    every operation of the build and of the carry is then exact in fp32 (products by powers of
+    two, short dyadic sums; 16-step chunks keep every state within 24 bits), so a chunk the carry
+    takes through its map (no miss) lands exactly on the serial chunk end, u and w bit for bit.
+    This pins the first-spike lines (which line fires first), the post-spike pieces (their u,
+    their w affine in x = lx*w + q, the piece that holds x) and the no-spike map exactly, where
+    test_carry_predictions_land_on_the_serial_state pins w to rounding only."""
+    beta, rho, q, theta0, u_r = 0.5, 0.5, 0.25, 1.0, -0.25
+    C, N = 16, 512
+    rng = np.random.default_rng(21)
+    # half the columns driven hard (they spike), half kept below threshold (the no-spike map)
+    hi_cols = rng.integers(-32, 96, (2 * C, N // 2))
+    lo_cols = rng.integers(-32, 16, (2 * C, N - N // 2))
+    I = (np.concatenate([hi_cols, lo_cols], 1) / 64.0).astype(np.float32)
+    u0 = (rng.integers(-48, 64, N) / 64.0).astype(np.float32)
+    w0 = (rng.integers(0, 33, N) / 64.0).astype(np.float32)
+    Lu = np.full((2, N), -1.0, np.float32)
+    Hu = np.full((2, N), 3.0, np.float32)
+    Lw = np.zeros((2, N), np.float32)
+    Hw = np.full((2, N), 0.5, np.float32)
+    su, sw = A.serial_segment(I[:C], beta, rho, q, theta0, u_r, u0, w0)
+    for block in (1, 4):
+        mp = A.build_maps(I, Lu, Hu, Lw, Hw, beta, rho, q, theta0, u_r, C, 32, 32, block)
+        SU, SW, MISS = A.carry(I, u0, w0, Lu, Hu, Lw, Hw, mp, beta, rho, q, theta0, u_r, C)
+        took = MISS[0] == 0
+        assert took.sum() > N // 2, (block, int(took.sum()))
+        assert np.array_equal(SU[1][took], su[took]), block
+        assert np.array_equal(SW[1][took], sw[took]), block
+        # the lines and pieces were exercised: chunks that spiked and chunks that did not
+        spiked = np.array([A.serial_forward(I[:C, [n]], beta, rho, q, theta0, u_r, u0[[n]], w0[[n]])[2].any()
+                           for n in range(N)])
+        assert (took & spiked).sum() > 100 and (took & ~spiked).sum() > 5, block
 
 
 def test_warm_predict_definition():

@@ -693,7 +693,7 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     const float* __restrict__ PU, const float* __restrict__ PA, const float* __restrict__ POF,
     float* __restrict__ SU, float* __restrict__ SW, int* __restrict__ MISS,
     int* __restrict__ MSTAR, WsHeader* hdr, int64_t N, int M, int C, int K1, int K2, float beta,
-    float rho, float q, float theta0, float u_r, float rhoC) {
+    float rho, float q, float theta0, float u_r, float rhoC, int stop_at_mstar) {
   __shared__ unsigned long long s_acc[kCarryWaves][4];
   __shared__ int s_max[kCarryWaves];
   const int64_t ngroups = (N + 4 * kCarryWaves - 1) / (4 * kCarryWaves);
@@ -847,6 +847,9 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
       pcs_acc += (unsigned long long)npc;
       pmax = max(pmax, npc);
     }
+    // repair to convergence: past every neuron's MSTAR the starts are replaced by the serial
+    // pass, so the wave stops (the statistics then cover the chunks it walked)
+    if (stop_at_mstar && __ballot(valid_n && mstar == M) == 0ull) break;
     hc = hn;
     sc = sn;
     hn = hn2;
@@ -1952,7 +1955,7 @@ extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w
                      F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
                      Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),
                      F(L.PA), F(L.POF), F(L.SU), F(L.SW), Iq(L.MISS), Iq(L.MSTAR), h, N, M, C, K1,
-                     K2, beta, rho, q, theta0, u_r, rhoC);
+                     K2, beta, rho, q, theta0, u_r, rhoC, repair == -1 && M > 1 ? 1 : 0);
   mark(3);
   // repair to convergence: the replay covers the chunks whose starts are the serial states
   // (below mstar), and one serial pass per block of 64 neurons runs from the block's least

@@ -280,7 +280,9 @@ int lsh_alif_warm_predict(const float* I, const float* u0, const float* w0, cons
  * convergence: the chunks whose carried starts are the serial states (those before MSTAR, the
  * first chunk whose start the carry took through a map) are replayed in parallel, and one
  * serial pass per 64 neurons runs from the least MSTAR on: the same U, W, S as converged
- * Jacobi rounds, the serial recurrence; repair_iters is then not counted (0). */
+ * Jacobi rounds, the serial recurrence; the carry stops once every neuron of a wave is past its
+ * MSTAR, so repair_iters is not counted (0) and the other statistics cover the chunks it walked
+ * (request statistics with a finite repair budget, as the Python layer does). */
 typedef struct lsh_alif_layout {
   size_t EC, EA, EB, LU, HU, LW, HW; /* envelope maps, box [M, N] */
   size_t MA, MB, NL, NP, OVF;        /* per-chunk scalars [M, N] (NL, NP, OVF int32) */

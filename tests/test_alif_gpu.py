@@ -146,6 +146,26 @@ def test_alif_box_scan_matches_oracle(AL, dev, name, beta, rho, q, block):
         assert st["max_pieces"] == sto["max_pieces"] and st["repair_iters"] == 0
 
 
+@pytest.mark.parametrize("M", [1, 2, 3])
+def test_alif_box_scan_converged_few_chunks(AL, dev, M):
+    """Repair to convergence with one to three chunks: M = 1 runs the replay only (no serial
+    pass), M = 2, 3 the replay below MSTAR and the serial pass from the least MSTAR; the result
+    is the serial recurrence for a good and a bad prediction."""
+    beta, rho, q = 0.95, 0.995, 0.9
+    C, N = 128, 100
+    T = M * C
+    I = _inputs(beta, 2.0, T, N, 17)
+    u0 = np.zeros(N, np.float32)
+    w0 = uniform(N, 0.0, 0.1, 18)
+    (Ur, Wr, Sr), preds = _preds(I, beta, rho, q, u0, w0, C)
+    for tag in ("oracle", "bad"):
+        print(f"alif converged M={M} pred={tag}", flush=True)
+        U, W, S = AL.alif_scan_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev),
+                                       gpu(preds[tag], dev), 0.1 * q, C=C, K1=32, K2=32, BN=4, repair=10 ** 6)
+        assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), tag
+        assert np.array_equal(host(S), Sr), tag
+
+
 def test_alif_box_scan_chunk_not_multiple_of_16(AL, dev):
     """C = 40: the carry's fallback streams its inputs row by row (the register path needs C a
     multiple of 16) and the converged pass starts inside a 64-row tile; intermediates equal the

@@ -23,7 +23,8 @@ The other BASELINE configurations (cfg3 network step, cfg4 long sequence, cfg5 A
 measured after the headline and reported under "other_configs" (--headline-only skips them).
 
   python bench.py [--steps K] [--warmup W] [--no-cpu] [--headline-only]
-  python bench.py --only cfg4        # one other configuration (profiling runs)
+  python bench.py --only cfg4        # one other configuration (profiling runs; also
+                                     # cfg2_mapscan, cfg3, cfg5, affine)
   python bench.py --dominant-only    # short run for rocprofv3 --pmc passes (copy + kernel)
   python bench.py --counters-workload  # the non-HBM-bound kernels once each (counter passes)
 """
@@ -199,7 +200,13 @@ def bench_cfg2_mapscan(torch, L, dev, u0, reps):
     pipeline: envelope + capacity-K chunk maps, carry with overflow fallback, replay, device
     repair to convergence) at C in {32, 64, 128}, K = 8, for beta = 0.9 and 0.99, against the
     serial forward; % of the 12 B/neuron-step roofline, overflow fraction and repair rounds.
-    Also the single pass with map speculation (C = 16, K = 8)."""
+    The timed calls request no statistics, so their repair is the ordered pass (one walk over
+    each neuron's chunks) where the launcher picks it; repair_iters is the Jacobi round count
+    of a separate call with statistics (the reference's definition).  Also the single pass
+    with map speculation (C = 16, K = 8), and reference_inputs: the reference's published cfg2
+    cells (results/logs/node5/e6d_0.9.log:15, e6d_0.99.log:15: x ~ N(0.15, 0.4^2), u0 = 0,
+    scan_forward_v3 at its best cell C = 256, K = 8, timed there without repair) on the same
+    inputs, without and with repair."""
     T, N = T_CFG, N_CFG
     out = {}
     for beta in (0.9, 0.99):
@@ -225,6 +232,38 @@ def bench_cfg2_mapscan(torch, L, dev, u0, reps):
         out[f"beta{beta}"] = r
         del I, Us, Ss, U, S
         torch.cuda.empty_cache()
+    # results/e6d_full_beta0.9.json / _beta0.99.json, the N = 65536, T = 4096 rows: the best
+    # scan cell's time, overflow fraction and mean pieces (its inputs are drawn on the device, so
+    # these are the same distribution, not the same values), and the tuned serial forward
+    published = {0.9: {"scan_fwd_ms": 4.156, "serial_fwd_ms": 2.226, "overflow_frac": 0.000177,
+                       "mean_pieces": 4.0647, "spike_flips": 0},
+                 0.99: {"scan_fwd_ms": 4.560, "serial_fwd_ms": 2.238, "overflow_frac": 0.027790,
+                        "mean_pieces": 5.2204, "spike_flips": 0}}
+    ref = {}
+    for beta in (0.9, 0.99):
+        g = torch.Generator().manual_seed(0)
+        I = (0.15 + 0.4 * torch.randn(T, N, generator=g)).to(dev)
+        Us, Ss = L.serial_forward(I, beta, 1.0, 0.0, u0)
+        st = {}
+        U, S = L.scan_forward_mapscan(I, beta, 1.0, 0.0, u0, C=256, K=8, repair=0, stats=st)
+        flips = int((S != Ss).sum().item())
+        t0 = ev_time(lambda: L.scan_forward_mapscan(I, beta, 1.0, 0.0, u0, C=256, K=8, repair=0), reps)
+        U, S = L.scan_forward_mapscan(I, beta, 1.0, 0.0, u0, C=256, K=8, repair=10 ** 6)
+        ok = bool(torch.equal(U, Us) and torch.equal(S, Ss))
+        t1 = ev_time(lambda: L.scan_forward_mapscan(I, beta, 1.0, 0.0, u0, C=256, K=8, repair=10 ** 6), reps)
+        ts = ev_time(lambda: L.serial_forward(I, beta, 1.0, 0.0, u0), reps)
+        pub = published[beta]
+        ref[f"beta{beta}"] = {
+            "scan_no_repair_ms": round(t0, 4), "scan_no_repair_spike_flips": flips,
+            "overflow_frac": round(st["overflow_frac"], 6), "mean_pieces": round(st["mean_pieces"], 4),
+            "scan_repair_ms": round(t1, 4),
+            "scan_repair_equals_serial": ok, "serial_fwd_ms": round(ts, 4),
+            "reference_rtx5090_ms": pub,
+            "speedup_vs_reference": {"scan_fwd": round(pub["scan_fwd_ms"] / t0, 3),
+                                     "serial_fwd": round(pub["serial_fwd_ms"] / ts, 3)}}
+        del I, Us, Ss, U, S
+        torch.cuda.empty_cache()
+    out["reference_inputs"] = ref
     return out
 
 
@@ -663,7 +702,7 @@ def main():
                     help="run each non-HBM-bound kernel once at its configuration (counter passes)")
     ap.add_argument("--headline-only", action="store_true",
                     help="skip the cfg3 / cfg4 / cfg5 / affine-reset measurements")
-    ap.add_argument("--only", choices=("cfg3", "cfg4", "cfg5", "affine"),
+    ap.add_argument("--only", choices=("cfg2_mapscan", "cfg3", "cfg4", "cfg5", "affine"),
                     help="measure one of the other configurations only (for profiling runs); "
                          "prints its JSON, not the headline line")
     args = ap.parse_args()
@@ -685,7 +724,9 @@ def main():
         counters_workload(torch, dev)
         return
     if args.only:
-        fn = {"cfg3": bench_cfg3, "cfg4": bench_cfg4, "cfg5": bench_cfg5,
+        fn = {"cfg2_mapscan": lambda torch, dev, reps: bench_cfg2_mapscan(
+                  torch, L, dev, torch.zeros(N_CFG, device=dev), reps),
+              "cfg3": bench_cfg3, "cfg4": bench_cfg4, "cfg5": bench_cfg5,
               "affine": bench_affine}[args.only]
         print(json.dumps({args.only: fn(torch, dev, 5)}))
         return

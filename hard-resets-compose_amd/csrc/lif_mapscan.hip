@@ -406,7 +406,7 @@ extern "C" int lsh_lif_scan_v3_assoc_fwd(const float* I, const float* u0, float*
                                          int C, int K, int64_t repair, void* ws, size_t ws_bytes,
                                          void* stream) {
   if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
-  if (repair < 0) return LSH_ERR_ARG;
+  if (repair < -1) return LSH_ERR_ARG;
   const int rc = assoc_check(T, N, C, K, beta);
   if (rc != LSH_OK) return rc;
   lsh_v3_layout L;

@@ -459,7 +459,7 @@ extern "C" int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, fl
                                    int K, int K2, int64_t repair, void* ws, size_t ws_bytes,
                                    void* stream) {
   if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
-  if (repair < 0) return LSH_ERR_ARG;
+  if (repair < -1) return LSH_ERR_ARG;
   const int rc = v4_check(T, N, C, G, K, K2);
   if (rc != LSH_OK) return rc;
   lsh_v4_layout L;

@@ -76,7 +76,8 @@ int lif_param_bwd_lookback(const float* I, const float* u0, const float* U, cons
 
 // Device repair rounds of the two-level scan (lif_kernels.hip, k_lif_repair) after a replay that
 // wrote U, S and ends from starts: at most min(repair, M) rounds; list0/list1 hold
-// ceil(N/64)*M*64 ints each.
+// ceil(N/64)*M*64 ints each.  repair = -1: to convergence without the round count (the ordered
+// pass k_lif_repair_ordered where it is faster, else M rounds).
 void lif_repair_launch(const float* I, float* U, float* S, float* starts, float* ends, int* list0,
                        int* list1, WsHeader* hdr, int64_t N, int M, int C, int64_t repair,
                        float beta, float theta, float u_r, hipStream_t st);

@@ -221,6 +221,16 @@ def last_scan_run():
     return _LAST_RUN
 
 
+def _repair_arg(repair, M, stats):
+    """The C entry's repair argument: -1 (to convergence without the round count, the ordered
+    pass where it is faster) for a converged repair whose round count nobody reads, else the
+    Jacobi round budget."""
+    repair = int(repair)
+    if repair < 0:
+        raise ValueError("repair must be >= 0")
+    return -1 if (stats is None and repair >= M and M > 1) else repair
+
+
 def _scan2(I, beta, theta, u_r, u0, C, K, repair, stats, lo=None):
     global _LAST_RUN
     I = _input(I)
@@ -231,7 +241,7 @@ def _scan2(I, beta, theta, u_r, u0, C, K, repair, stats, lo=None):
         raise ValueError(f"T={T} must be divisible by the chunk length C={C}")
     if not 1 <= K <= 64:
         raise ValueError("map capacity K must be in [1, 64]")
-    repair = int(repair)
+    repair = _repair_arg(repair, T // C, stats)
     L = _n.lib()
     nbytes = L.lsh_lif_scan_v3_workspace(T, N, C, K)
     if nbytes == 0:
@@ -459,7 +469,7 @@ def scan_forward_assoc(I, beta, theta, u_r, u0, C=2048, K=32, repair=None, stats
     if C < 1 or T % C or not 1 <= K <= 32 or _f32(beta) < 0:
         raise ValueError(f"the associative map scan needs C >= 1 dividing T={T}, 1 <= K <= 32, "
                          f"beta >= 0")
-    R = T // C if repair is None else int(repair)
+    R = _repair_arg(T // C if repair is None else repair, T // C, stats)
     if T == 0 or N == 0:
         if stats is not None:
             stats.update(repair_iters=0, overflow_frac=0.0, mean_pieces=1.0, max_pieces=1)
@@ -586,7 +596,8 @@ def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=
     with _n.on_device(I):
         _n.check(L.lsh_lif_scan_v4_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
                                        _f32(beta), _f32(theta), _f32(u_r), C, G, K, K2,
-                                       int(repair), _n.ptr(ws), nbytes, _n.stream_of(I)),
+                                       _repair_arg(repair, T // C, stats), _n.ptr(ws), nbytes,
+                                       _n.stream_of(I)),
                  "lsh_lif_scan_v4_fwd")
     _LAST_RUN = _ScanRunV4(ws, T, N, C, G, K, K2)
     if stats is not None:

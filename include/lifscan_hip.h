@@ -67,8 +67,11 @@ int lsh_lif_serial_bwd(const float* I, const float* u0, const float* U, const fl
  * with overflow-to-serial fallback, replay, Jacobi repair on device).
  * Replaces triton_lif.py:782-817 (scan_forward_v3) and :1228-1232 (scan_forward_auto).
  * repair: maximum number of repair rounds (0 = none; the result is bit-identical to the
- * serial recurrence once the rounds converge, at most T/C rounds).  Requires T % C == 0,
- * 1 <= K <= 64, C >= 1. */
+ * serial recurrence once the rounds converge, at most T/C rounds), or -1: repair to
+ * convergence without counting rounds (the same U and S; where N and T/C are large, one
+ * ordered pass per 64 neurons replays each chunk whose start differs from its predecessor's
+ * exact exit, until it meets the stored trajectory; repair_iters is then not the reference's,
+ * so request statistics with a finite budget).  Requires T % C == 0, 1 <= K <= 64, C >= 1. */
 size_t lsh_lif_scan_v3_workspace(int64_t T, int64_t N, int C, int K);
 int lsh_lif_scan_v3_fwd(const float* I, const float* u0, float* U, float* S, int64_t T, int64_t N,
                         float beta, float theta, float u_r, int C, int K, int64_t repair,
@@ -95,7 +98,8 @@ int lsh_lif_scan_v3_pieces_fwd(const float* I, const float* u0, float* U, float*
  * inside each wave by DPP moves (row_shr 1/2/4/8, row_bcast 15/31) and the wave totals composed
  * in LDS, segmented at capacity-overflowed chunks, which run serially; the envelope bounds of
  * the chunk entries by the same scan over the min-affine envelope maps.  Then the replay and
- * `repair` Jacobi repair rounds (repair >= T/C: U and S are the serial recurrence).  Replaces
+ * `repair` Jacobi repair rounds (repair >= T/C: U and S are the serial recurrence; -1 as for
+ * lsh_lif_scan_v3_fwd).  Replaces
  * the sequential carry of triton_lif.py:782-817 (scan_forward_v3: env_carry_kernel :723-733,
  * carry2_kernel :579-606) by the composition monoid of :864-892 (compose_group_kernel).
  * The starts before repair are predictions whose rounding differs from the sequential carry's,
@@ -126,7 +130,7 @@ int lsh_lif_scan_warm_fwd(const float* I, const float* u0, float* U, float* S, i
 /* Two-level scan pruned with one caller-given lower bound per neuron (lo[N], e.g. the loose
  * state_bounds of triton_lif.py:238-243) instead of the per-chunk envelope.  Replaces
  * triton_lif.py:262-295 (scan_forward), :479-509 (scan_forward_tiled) and :609-642
- * (scan_forward_v2).  Same workspace as lsh_lif_scan_v3_fwd. */
+ * (scan_forward_v2).  Same workspace and `repair` as lsh_lif_scan_v3_fwd. */
 int lsh_lif_scan_lo_fwd(const float* I, const float* u0, const float* lo, float* U, float* S,
                         int64_t T, int64_t N, float beta, float theta, float u_r, int C, int K,
                         int64_t repair, void* ws, size_t ws_bytes, void* stream);
@@ -188,7 +192,8 @@ int lsh_lif_scan_v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3_layout* ou
 
 /* Three-level exact scan for long sequences: capacity-K chunk maps composed in groups of G
  * into capacity-K2 super maps, carry over the super maps, carry inside every super map in
- * parallel, replay, Jacobi repair on device.  Replaces triton_lif.py:935-983
+ * parallel, replay, Jacobi repair on device (`repair` as for lsh_lif_scan_v3_fwd, -1
+ * included).  Replaces triton_lif.py:935-983
  * (scan_forward_v4), :829-899 (compose_group_kernel), :903-932 (carry_inner_kernel).
  * Requires T % C == 0, (T / C) % G == 0, 1 <= K <= K2, K <= 32, K2 <= 64. */
 typedef struct lsh_v4_layout {

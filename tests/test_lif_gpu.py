@@ -355,6 +355,9 @@ def test_cfg2_scan_equals_serial_full_size(L, dev):
             U, S = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=8, repair=10 ** 6, stats=st)
             assert torch.equal(U, Us) and torch.equal(S, Ss)
             print(f"  C={C} stats={st}", flush=True)
+            # without statistics the map scan repairs by the ordered pass
+            U, S = L.scan_forward_mapscan(I, beta, 1.0, 0.0, u0, C=C, K=8, repair=10 ** 6)
+            assert torch.equal(U, Us) and torch.equal(S, Ss)
         cols = np.arange(0, N, N // 512)
         Uo, So = O.serial_forward(host(I[:, cols]), beta, 1.0, 0.0, np.zeros(len(cols), np.float32))
         assert np.array_equal(host(Us[:, cols]), Uo) and np.array_equal(host(Ss[:, cols]), So)

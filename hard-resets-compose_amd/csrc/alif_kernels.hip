@@ -656,17 +656,15 @@ __device__ __forceinline__ void alif_row_block16(float xb, float& u, float& w, f
 }
 
 // One chunk's map as the carry reads it (one neuron per 16-lane row, slot s in lane s & 15,
-// register s >> 4): the per-neuron header, loaded two chunks ahead, and the slots below the
-// line and piece counts (loads of empty slots masked off) with the inputs of the chunk's
-// first 128 steps for the serial fallback (lane i of a row: step 16 b + i in xb[b]), loaded
-// one chunk ahead.
+// register s >> 4): the per-neuron header, every slot below K1 / K2 (the slots past the line
+// and piece counts hold no map; each use is masked by the counts, so their loads need not
+// wait for the header) and the inputs of the chunk's first 128 steps for the serial fallback
+// (lane i of a row: step 16 b + i in xb[b]).
 constexpr int kCarryXB = 8;
 constexpr int kCarryWaves = 4;  // waves (of four neurons) per workgroup
-struct AlifCarryHdr {
+struct AlifCarryMap {
   float ma, mb, lu, hu, lw, hw;
   int nl, npc, ovf;
-};
-struct AlifCarrySlots {
   float ls[2], lc[2], lx[2], pl[2], pr[2], pu[2], pa[2], po[2];
   int pw[2];
   float xb[kCarryXB];
@@ -678,11 +676,16 @@ struct AlifCarrySlots {
 // One neuron per 16-lane row (four a wave, sixteen a workgroup): slot s of the lines and
 // pieces in lane s & 15, register s >> 4, as the build keeps them; a serial fallback runs for
 // the lanes of the neurons that need it, once per chunk for the wave.  The maps are read
-// ahead of the chunk that uses them, and with C a multiple of 16 the fallback takes its inputs
+// PD chunks ahead of the chunk that uses them into a ring of PD + 1 register sets, the chunk
+// loop unrolled by the ring's length so that no set is copied (a copy would wait for the loads
+// into it).  PD = 1 is what runs: on MI355X 2 and 3 were no faster with 1024 neurons (256
+// waves) and slower with 16384 (the extra registers cost waves).  With C a
+// multiple of 16 the fallback takes its inputs
 // from registers by row broadcasts (the inputs past the first 128 steps loaded one group of
 // 128 ahead), else it streams them row by row.  Workgroups of neighbouring neurons go to one
 // XCD (blockIdx b -> group (b % 8) * per + b / 8), so they share its L2 for the inputs and the
 // per-neuron arrays.  The statistics are summed per workgroup before the atomics.
+template <int PD>
 __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     const float* __restrict__ LU, const float* __restrict__ HU, const float* __restrict__ LWb,
@@ -725,48 +728,55 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
   auto row_count = [&](unsigned long long b) {
     return __builtin_popcount((unsigned int)(b >> rowb) & 0xffffu);
   };
-  auto load_hdr = [&](int m, AlifCarryHdr& h) {
-    const size_t o = (size_t)m * N + nn;
-    h.ma = MA[o];
-    h.mb = MB[o];
-    h.lu = LU[o];
-    h.hu = HU[o];
-    h.lw = LWb[o];
-    h.hw = HWb[o];
-    h.nl = NL[o];
-    h.npc = NP[o];
-    h.ovf = OVF[o];
-  };
-  auto load_slots = [&](int m, const AlifCarryHdr& h, AlifCarrySlots& d) {
-    const size_t o = (size_t)m * N + nn;
-    if (xdpp) {
-      const float* xp = I + ((size_t)m * C + i) * N + nn;
+  // Every load is issued unconditionally, its index clamped into the arrays (chunk <= M - 1,
+  // slot <= K - 1, row <= C - 1; the extra values are never used), so that the compiler knows
+  // how many loads were issued after each one and waits for the ring set in use only.
+  auto load_map = [&](int m, AlifCarryMap& d) {
+    const size_t o = (size_t)min(m, M - 1) * N + nn;
+    d.ma = MA[o];
+    d.mb = MB[o];
+    d.lu = LU[o];
+    d.hu = HU[o];
+    d.lw = LWb[o];
+    d.hw = HWb[o];
+    d.nl = NL[o];
+    d.npc = NP[o];
+    d.ovf = OVF[o];
+    {
+      const float* xp = I + (size_t)min(m, M - 1) * C * N + nn;
 #pragma unroll
-      for (int b = 0; b < kCarryXB; ++b) d.xb[b] = b < nb ? xp[(size_t)(16 * b) * N] : 0.0f;
+      for (int b = 0; b < kCarryXB; ++b) d.xb[b] = xp[(size_t)min(16 * b + i, C - 1) * N];
     }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
-      const int slot = 16 * r + i;
-      const bool vl = slot < h.nl, vp = slot < h.npc;  // nl <= K1, npc <= K2
-      d.ls[r] = vl ? LS[o * K1 + slot] : 0.0f;
-      d.lc[r] = vl ? LC[o * K1 + slot] : INFINITY;
-      d.lx[r] = vl ? LX[o * K1 + slot] : 0.0f;
-      d.pw[r] = vp ? POWN[o * K2 + slot] : -1;
-      d.pl[r] = vp ? PXL[o * K2 + slot] : INFINITY;
-      d.pr[r] = vp ? PXR[o * K2 + slot] : INFINITY;
-      d.pu[r] = vp ? PU[o * K2 + slot] : 0.0f;
-      d.pa[r] = vp ? PA[o * K2 + slot] : 0.0f;
-      d.po[r] = vp ? POF[o * K2 + slot] : 0.0f;
+      const int sl = min(16 * r + i, K1 - 1), sp = min(16 * r + i, K2 - 1);
+      d.ls[r] = LS[o * K1 + sl];
+      d.lc[r] = LC[o * K1 + sl];
+      d.lx[r] = LX[o * K1 + sl];
+      d.pw[r] = POWN[o * K2 + sp];
+      d.pl[r] = PXL[o * K2 + sp];
+      d.pr[r] = PXR[o * K2 + sp];
+      d.pu[r] = PU[o * K2 + sp];
+      d.pa[r] = PA[o * K2 + sp];
+      d.po[r] = POF[o * K2 + sp];
     }
   };
-  AlifCarryHdr hc, hn, hn2;
-  AlifCarrySlots sc, sn;
-  load_hdr(0, hc);
-  load_slots(0, hc, sc);
-  if (M > 1) load_hdr(1, hn);
-  for (int m = 0; m < M; ++m) {
-    if (m + 1 < M) load_slots(m + 1, hn, sn);
-    if (m + 2 < M) load_hdr(m + 2, hn2);
+  // a ring of PD + 1 maps: chunk m in mr[m % (PD + 1)]
+  AlifCarryMap mr[PD + 1];
+#pragma unroll
+  for (int k = 0; k < PD; ++k) load_map(k, mr[k]);
+  bool done = false;
+  for (int m0 = 0; m0 < M && !done; m0 += PD + 1) {
+#pragma unroll
+  for (int ph = 0; ph <= PD; ++ph) {
+    const int m = m0 + ph;
+    if (m >= M) {
+      done = true;
+      break;
+    }
+    load_map(m + PD, mr[(ph + PD) % (PD + 1)]);  // the set of chunk m - 1
+    const AlifCarryMap& hc = mr[ph];
+    const AlifCarryMap& sc = mr[ph];
     const size_t o = (size_t)m * N + nn;
     if (valid_n && i == 0) {
       SU[o] = u;
@@ -849,10 +859,11 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     }
     // repair to convergence: past every neuron's MSTAR the starts are replaced by the serial
     // pass, so the wave stops (the statistics then cover the chunks it walked)
-    if (stop_at_mstar && __ballot(valid_n && mstar == M) == 0ull) break;
-    hc = hn;
-    sc = sn;
-    hn = hn2;
+    if (stop_at_mstar && __ballot(valid_n && mstar == M) == 0ull) {
+      done = true;
+      break;
+    }
+  }
   }
   if (valid_n && i == 0) MSTAR[nn] = mstar;
   miss_acc = wave_sum_u64(miss_acc);
@@ -1950,7 +1961,7 @@ extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w
   mark(2);
   // workgroups of 16 neurons, the grid rounded up to a multiple of 8 (one share per XCD)
   const int64_t carry_groups = (N + 4 * kCarryWaves - 1) / (4 * kCarryWaves);
-  hipLaunchKernelGGL(k_alif_carry, dim3((unsigned)(8 * ((carry_groups + 7) / 8))),
+  hipLaunchKernelGGL(k_alif_carry<1>, dim3((unsigned)(8 * ((carry_groups + 7) / 8))),
                      dim3(WAVE * kCarryWaves), 0, st, I, u0, w0,
                      F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
                      Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),

@@ -120,7 +120,10 @@ struct Buf {
 // Wave-level reductions (wave64).
 // f(j, p[j*stride]) for j = 0..n-1 in order, loading the rows in tiles of D with the next
 // tile's loads issued before the current tile is consumed (serial fallbacks and repairs run
-// one dependent chain per lane; without this every step waits for its own load).
+// one dependent chain per lane; without this every step waits for its own load).  The next
+// tile's loads are issued on every tile (the last tile reloads itself): behind a branch the
+// compiler could not tell whether they were issued, and its wait for the current tile would
+// then cover them too.
 template <int D, class F>
 __device__ __forceinline__ void stream_rows(const float* __restrict__ p, size_t stride, int64_t n,
                                             F&& f) {
@@ -132,17 +135,13 @@ __device__ __forceinline__ void stream_rows(const float* __restrict__ p, size_t 
   }
   for (int64_t t = 0; t < nt; ++t) {
     float b[D];
-    const bool more = t + 1 < nt;
-    if (more) {
+    const int64_t tn = t + 1 < nt ? t + 1 : t;
 #pragma unroll
-      for (int k = 0; k < D; ++k) b[k] = p[(size_t)((t + 1) * D + k) * stride];
-    }
+    for (int k = 0; k < D; ++k) b[k] = p[(size_t)(tn * D + k) * stride];
 #pragma unroll
     for (int k = 0; k < D; ++k) f(t * D + k, a[k]);
-    if (more) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) a[k] = b[k];
-    }
+    for (int k = 0; k < D; ++k) a[k] = b[k];
   }
   for (int64_t j = nt * D; j < n; ++j) f(j, p[(size_t)j * stride]);
 }
@@ -165,25 +164,21 @@ __device__ __forceinline__ bool stream_rows_until(const float* __restrict__ p,
   }
   for (int64_t t = 0; t < nt; ++t) {
     float b[D], d[D];
-    const bool more = t + 1 < nt;
-    if (more) {
+    const int64_t tn = t + 1 < nt ? t + 1 : t;  // issued on every tile, as in stream_rows
 #pragma unroll
-      for (int k = 0; k < D; ++k) {
-        b[k] = p[(size_t)((t + 1) * D + k) * stride];
-        d[k] = q[(size_t)((t + 1) * D + k) * stride];
-      }
+    for (int k = 0; k < D; ++k) {
+      b[k] = p[(size_t)(tn * D + k) * stride];
+      d[k] = q[(size_t)(tn * D + k) * stride];
     }
     bool stop = false;
 #pragma unroll
     for (int k = 0; k < D; ++k)
       if (!stop) stop = f(t * D + k, a[k], c[k]);
     if (stop) return true;
-    if (more) {
 #pragma unroll
-      for (int k = 0; k < D; ++k) {
-        a[k] = b[k];
-        c[k] = d[k];
-      }
+    for (int k = 0; k < D; ++k) {
+      a[k] = b[k];
+      c[k] = d[k];
     }
   }
   for (int64_t j = nt * D; j < n; ++j)

@@ -503,7 +503,8 @@ def bench_alif_reference_shape(torch, dev):
     u0=w0=0): serial forward; box scan with the previous-iterate prediction (1.005x input, C=256,
     dw=0.1q, K1=K2=32; without repair as the reference times it, and with repair, exact); serial
     and scan adjoints.  RTX 5090 figures (results/e25d_alif_fwd.json, e25e_alif_fb.json): 2.94 /
-    9.42 ms forward, 8.82 / 3.90 ms adjoint."""
+    9.42 ms forward, 8.82 / 3.90 ms adjoint.  few_neurons: the same at N = 16 and 128, where the
+    box scan beats the serial forward (0.677 / 1.385 ms there against 2.14 / 2.78 serial)."""
     import math
     from lifscan import triton_alif as A
     beta, rho, q, m, N, T, C = 0.95, 0.995, 0.9, 1.0, 1024, 65536, 256
@@ -532,8 +533,37 @@ def bench_alif_reference_shape(torch, dev):
            "bwd_scan_ms": 3.90}
     out["reference_rtx5090_ms"] = ref
     out["speedup_vs_reference"] = {k: round(v / out[k], 3) for k, v in ref.items()}
-    out["config"] = "ALIF lsnn N=1024, T=65536, free mean 1.0 (experiments/e25d_alif_fwd.py inputs)"
     del I, gS, U, W, S, WP
+    # the box scan's own regime, few neurons (results/e25d_alif_fwd.json, lsnn m = 1.0, T = 65536,
+    # the previous-iterate prediction; the reference's best cell of its grid): the best of
+    # C in {256, 512} x dw in {0.1q, 0.3q}, without repair as timed there, against its times
+    small = {}
+    for Ns, ref_serial, ref_box in ((16, 2.143, 0.677), (128, 2.783, 1.385)):
+        g = torch.Generator().manual_seed(0)
+        I = ((1 - beta) * m + 0.5 * math.sqrt(1 - beta * beta) * torch.randn(T, Ns, generator=g)).to(dev)
+        z = torch.zeros(Ns, device=dev)
+        _, _, S = A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z)
+        ts = ev_time(lambda: A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z), 5)
+        _, Wprev, _ = A.alif_serial_forward((1.005 * I).contiguous(), beta, rho, q, 1.0, 0.0, z, z)
+        best = None
+        for Cs in (256, 512):
+            WPs = A.alif_prev_wpred(Wprev, z, Cs)
+            for dwq in (0.1, 0.3):
+                t = ev_time(lambda: A.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, WPs, dwq * q, C=Cs,
+                                                        K1=32, K2=32, BN=4, repair=0), 5)
+                if best is None or t < best[0]:
+                    best = (t, Cs, dwq, WPs)
+        t, Cs, dwq, WPs = best
+        _, _, S2 = A.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, WPs, dwq * q, C=Cs, K1=32, K2=32, BN=4,
+                                       repair=0)
+        small[f"N{Ns}"] = {"fwd_serial_ms": round(ts, 4), "fwd_box_scan_no_repair_ms": round(t, 4), "C": Cs,
+                           "dw_over_q": dwq, "spike_flips": int((S2 != S).sum().item()),
+                           "reference_rtx5090_ms": {"fwd_serial_ms": ref_serial, "fwd_box_scan_no_repair_ms": ref_box},
+                           "speedup_vs_reference": {"fwd_serial_ms": round(ref_serial / ts, 3),
+                                                    "fwd_box_scan_no_repair_ms": round(ref_box / t, 3)}}
+        del I, S, S2, Wprev, WPs
+    out["few_neurons"] = small
+    out["config"] = "ALIF lsnn N=1024, T=65536, free mean 1.0 (experiments/e25d_alif_fwd.py inputs)"
     torch.cuda.empty_cache()
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out.items()}
 

@@ -661,7 +661,19 @@ __device__ __forceinline__ void alif_row_block16(float xb, float& u, float& w, f
 // wait for the header) and the inputs of the chunk's first 128 steps for the serial fallback
 // (lane i of a row: step 16 b + i in xb[b]).
 constexpr int kCarryXB = 8;
-constexpr int kCarryWaves = 4;  // waves (of four neurons) per workgroup
+constexpr int kCarryWaves = 4;  // waves per workgroup
+// Neurons per wave: a wave runs the serial fallback when any of its neurons misses, so with
+// few neurons (an idle chip) one neuron a wave (its four rows replicating it) cuts the
+// fallbacks; with many, four a wave keep the instruction count per neuron low.  Measured on
+// MI355X (lsnn, free mean 1.0, previous-iterate prediction, dw 0.1q, no repair; carry / box
+// scan): N 16 0.41 / 0.64 ms against 0.66 / 0.89 with four a wave, N 128 0.33 / 0.77 against
+// 0.63 / 1.08, N 512 0.59 / 1.65 against 0.86 / 1.93, N 1024 0.61 / 2.52 against 0.84 / 2.79;
+// N 2048 0.54 / 2.44 against 0.48 / 2.37, N 4096 0.54 / 2.39 against 0.32 / 2.19, cfg5 (walking
+// every chunk) 1.06 against 0.36 ms carry.  Two a wave was between the two at every size.
+#ifndef LSH_ALIF_CARRY_NPW1_MAX_N
+#define LSH_ALIF_CARRY_NPW1_MAX_N 1024
+#endif
+constexpr int64_t kCarryNpw1MaxN = LSH_ALIF_CARRY_NPW1_MAX_N;
 struct AlifCarryMap {
   float ma, mb, lu, hu, lw, hw;
   int nl, npc, ovf;
@@ -685,7 +697,7 @@ struct AlifCarryMap {
 // 128 ahead), else it streams them row by row.  Workgroups of neighbouring neurons go to one
 // XCD (blockIdx b -> group (b % 8) * per + b / 8), so they share its L2 for the inputs and the
 // per-neuron arrays.  The statistics are summed per workgroup before the atomics.
-template <int PD>
+template <int PD, int NPW>
 __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
     const float* __restrict__ LU, const float* __restrict__ HU, const float* __restrict__ LWb,
@@ -699,7 +711,8 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     float rho, float q, float theta0, float u_r, float rhoC, int stop_at_mstar) {
   __shared__ unsigned long long s_acc[kCarryWaves][4];
   __shared__ int s_max[kCarryWaves];
-  const int64_t ngroups = (N + 4 * kCarryWaves - 1) / (4 * kCarryWaves);
+  static_assert(NPW == 1 || NPW == 4, "neurons per wave");
+  const int64_t ngroups = (N + NPW * kCarryWaves - 1) / (NPW * kCarryWaves);
   const int64_t per = gridDim.x / 8;
   const int64_t grp = (int64_t)(blockIdx.x % 8) * per + blockIdx.x / 8;
   if (grp >= ngroups) return;  // the whole workgroup (the grid is rounded up to 8 per XCD)
@@ -708,7 +721,10 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
   const int g = lane >> 4;
   const int i = lane & 15;
   const int rowb = lane & 48;
-  const int64_t n = grp * (4 * kCarryWaves) + wv * 4 + g;
+  // NPW neurons a wave: with one, the four rows hold the same neuron (same loads, same steps,
+  // so the same results) and row 0 stores and counts
+  const int64_t n = grp * (NPW * kCarryWaves) + wv * NPW + (g % NPW);
+  const bool lead = g < NPW;
   const bool valid_n = n < N;
   const int64_t nn = valid_n ? n : N - 1;
   const bool xdpp = (C & 15) == 0;  // the fallback's inputs in registers
@@ -778,7 +794,7 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     const AlifCarryMap& hc = mr[ph];
     const AlifCarryMap& sc = mr[ph];
     const size_t o = (size_t)m * N + nn;
-    if (valid_n && i == 0) {
+    if (valid_n && lead && i == 0) {
       SU[o] = u;
       SW[o] = w;
     }
@@ -810,7 +826,7 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     float nw = none_ ? rhoC * w : mw;
     const bool inbox = (u >= hc.lu) && (u < hc.hu) && (w >= hc.lw) && (w <= hc.hw);
     const bool bad = !inbox || ovf != 0 || (!none_ && nh != 1);
-    if (valid_n && i == 0) MISS[o] = bad ? 1 : 0;
+    if (valid_n && lead && i == 0) MISS[o] = bad ? 1 : 0;
     if (__ballot(bad) != 0ull) {
       float uu = u, ww = w;
       if (xdpp) {
@@ -820,21 +836,18 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
 #pragma unroll
         for (int b = 0; b < kCarryXB; ++b) xa[b] = sc.xb[b];
         for (int g0 = 0; g0 < nb; g0 += kCarryXB) {
+          // issued for every group (rows clamped into the chunk, the extra values unused), so
+          // the wait for this group's inputs does not cover them
           float xn[kCarryXB];
-          const bool more = g0 + kCarryXB < nb;
-          if (more) {
-            const float* xp = I + ((size_t)m * C + 16 * (g0 + kCarryXB) + i) * N + nn;
+          const float* xp = I + (size_t)m * C * N + nn;
 #pragma unroll
-            for (int b = 0; b < kCarryXB; ++b)
-              xn[b] = g0 + kCarryXB + b < nb ? xp[(size_t)(16 * b) * N] : 0.0f;
-          }
+          for (int b = 0; b < kCarryXB; ++b)
+            xn[b] = xp[(size_t)min(16 * (g0 + kCarryXB + b) + i, C - 1) * N];
 #pragma unroll
           for (int b = 0; b < kCarryXB; ++b)
             if (g0 + b < nb) alif_row_block16(xa[b], uu, ww, beta, rho, q, theta0, u_r);
-          if (more) {
 #pragma unroll
-            for (int b = 0; b < kCarryXB; ++b) xa[b] = xn[b];
-          }
+          for (int b = 0; b < kCarryXB; ++b) xa[b] = xn[b];
         }
       } else if (bad) {
         stream_rows<4>(I + (size_t)m * C * N + nn, (size_t)N, C, [&](int64_t, float x) {
@@ -850,7 +863,7 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     u = nu;
     w = nw;
     if (!bad && mstar == M) mstar = m + 1;
-    if (valid_n && i == 0) {
+    if (valid_n && lead && i == 0) {
       miss_acc += bad ? 1ull : 0ull;
       ovf_acc += ovf ? 1ull : 0ull;
       lines_acc += (unsigned long long)nl;
@@ -865,7 +878,7 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     }
   }
   }
-  if (valid_n && i == 0) MSTAR[nn] = mstar;
+  if (valid_n && lead && i == 0) MSTAR[nn] = mstar;
   miss_acc = wave_sum_u64(miss_acc);
   ovf_acc = wave_sum_u64(ovf_acc);
   lines_acc = wave_sum_u64(lines_acc);
@@ -1960,8 +1973,10 @@ extern "C" int lsh_alif_scan_fwd(const float* I, const float* u0, const float* w
   }
   mark(2);
   // workgroups of 16 neurons, the grid rounded up to a multiple of 8 (one share per XCD)
-  const int64_t carry_groups = (N + 4 * kCarryWaves - 1) / (4 * kCarryWaves);
-  hipLaunchKernelGGL(k_alif_carry<1>, dim3((unsigned)(8 * ((carry_groups + 7) / 8))),
+  const int npw = N <= kCarryNpw1MaxN ? 1 : 4;
+  const int64_t carry_groups = (N + npw * kCarryWaves - 1) / (npw * kCarryWaves);
+  auto carry = npw == 1 ? k_alif_carry<1, 1> : k_alif_carry<1, 4>;
+  hipLaunchKernelGGL(carry, dim3((unsigned)(8 * ((carry_groups + 7) / 8))),
                      dim3(WAVE * kCarryWaves), 0, st, I, u0, w0,
                      F(L.LU), F(L.HU), F(L.LW), F(L.HW), F(L.MA), F(L.MB), Iq(L.NL), Iq(L.NP),
                      Iq(L.OVF), F(L.LS), F(L.LC), F(L.LX), Iq(L.POWN), F(L.PXL), F(L.PXR), F(L.PU),

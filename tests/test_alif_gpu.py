@@ -97,53 +97,73 @@ def test_alif_prev_wpred(AL, dev):
         AL.alif_prev_wpred(gpu(W[:1000], dev), gpu(w0, dev), C)
 
 
+def _check_box_scan(AL, dev, I, u0, w0, Wp, dw, beta, rho, q, C, K1, K2, block, tag):
+    """repair = 0: every intermediate of the box scan and the replayed outputs equal the
+    oracle's (same block of the split decision), in pipeline order."""
+    T, N = I.shape
+    st, sto, keep = {}, {}, {}
+    U, W, S = AL.alif_scan_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev),
+                                   gpu(Wp, dev), dw, C=C, K1=K1, K2=K2, BN=block, repair=0, stats=st)
+    run = AL.last_alif_run()
+    Uo, Wo, So = A.scan_forward(I, beta, rho, q, 1.0, 0.0, u0, w0, Wp, dw, C=C, K1=K1, K2=K2,
+                                block=block, repair=0, stats=sto, keep=keep)
+    # in pipeline order, so a failure names the first stage that differs
+    for g, o in (("LU", "Lu"), ("HU", "Hu"), ("LW", "Lw"), ("HW", "Hw"), ("MA", "A"), ("MB", "B")):
+        assert np.array_equal(host(run.view(g)), keep[o]), (tag, g)
+    for g, o in (("NL", "nl"), ("NP", "npc"), ("OVF", "ovf")):
+        assert np.array_equal(host(run.view(g, torch.int32)), keep[o]), (tag, g)
+    nl, npc = keep["nl"], keep["npc"]
+    lmask = np.arange(K1)[None, :, None] < nl[:, None]
+    pmask = np.arange(K2)[None, :, None] < npc[:, None]
+    for g, o in (("LS", "ls"), ("LC", "lc"), ("LX", "lx")):
+        assert np.array_equal(host(run.view(g))[lmask], keep[o][lmask]), (tag, g)
+    for g, o in (("PXL", "pxl"), ("PXR", "pxr"), ("PU", "pu"), ("PA", "pa"), ("POF", "pof")):
+        assert np.array_equal(host(run.view(g))[pmask], keep[o][pmask]), (tag, g)
+    assert np.array_equal(host(run.view("POWN", torch.int32))[pmask], keep["pown"][pmask])
+    for g in ("SU", "SW"):
+        assert np.array_equal(host(run.view(g)), keep[g]), (tag, g)
+    assert np.array_equal(host(run.view("MISS", torch.int32)), keep["MISS"]), tag
+    # the first chunk whose start the carry took through a map: chunk m's start is the
+    # serial state while every chunk before it was replayed serially (a miss)
+    miss = keep["MISS"]
+    used_map = np.nonzero(miss == 0)
+    mstar = np.full(N, T // C, np.int32)
+    for m_, n_ in zip(*used_map):
+        mstar[n_] = min(mstar[n_], m_ + 1)
+    assert np.array_equal(host(run.view("MSTAR", torch.int32)), mstar), tag
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(W), Wo) and np.array_equal(host(S), So)
+    for k in ("miss_frac", "overflow_frac", "mean_lines", "mean_pieces"):
+        assert st[k] == pytest.approx(sto[k], abs=1e-12), (tag, k)
+    assert st["max_pieces"] == sto["max_pieces"] and st["repair_iters"] == 0
+
+
 @pytest.mark.parametrize("name,beta,rho,q", NEURONS)
 @pytest.mark.parametrize("block", [1, 2, 4, 8, 16])
 def test_alif_box_scan_matches_oracle(AL, dev, name, beta, rho, q, block):
     """repair = 0: every intermediate of the box scan and the replayed outputs equal the
-    oracle's (same block of the split decision)."""
+    oracle's (same block of the split decision); N = 72, so the carry runs one neuron a wave."""
     T, N, C, K1, K2 = 2048, 72, 128, 16, 32
     I = _inputs(beta, 2.0, T, N, 9)
     u0 = np.zeros(N, np.float32)
     w0 = uniform(N, 0.0, 0.1, 10)
     _, preds = _preds(I, beta, rho, q, u0, w0, C)
     for tag in ("oracle", "warm4", "bad"):
-        Wp, dw = preds[tag], 0.1 * q
         print(f"alif box {name} block={block} pred={tag}", flush=True)
-        st, sto, keep = {}, {}, {}
-        U, W, S = AL.alif_scan_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev),
-                                       gpu(Wp, dev), dw, C=C, K1=K1, K2=K2, BN=block, repair=0, stats=st)
-        run = AL.last_alif_run()
-        Uo, Wo, So = A.scan_forward(I, beta, rho, q, 1.0, 0.0, u0, w0, Wp, dw, C=C, K1=K1, K2=K2,
-                                    block=block, repair=0, stats=sto, keep=keep)
-        # in pipeline order, so a failure names the first stage that differs
-        for g, o in (("LU", "Lu"), ("HU", "Hu"), ("LW", "Lw"), ("HW", "Hw"), ("MA", "A"), ("MB", "B")):
-            assert np.array_equal(host(run.view(g)), keep[o]), (tag, g)
-        for g, o in (("NL", "nl"), ("NP", "npc"), ("OVF", "ovf")):
-            assert np.array_equal(host(run.view(g, torch.int32)), keep[o]), (tag, g)
-        nl, npc = keep["nl"], keep["npc"]
-        lmask = np.arange(K1)[None, :, None] < nl[:, None]
-        pmask = np.arange(K2)[None, :, None] < npc[:, None]
-        for g, o in (("LS", "ls"), ("LC", "lc"), ("LX", "lx")):
-            assert np.array_equal(host(run.view(g))[lmask], keep[o][lmask]), (tag, g)
-        for g, o in (("PXL", "pxl"), ("PXR", "pxr"), ("PU", "pu"), ("PA", "pa"), ("POF", "pof")):
-            assert np.array_equal(host(run.view(g))[pmask], keep[o][pmask]), (tag, g)
-        assert np.array_equal(host(run.view("POWN", torch.int32))[pmask], keep["pown"][pmask])
-        for g in ("SU", "SW"):
-            assert np.array_equal(host(run.view(g)), keep[g]), (tag, g)
-        assert np.array_equal(host(run.view("MISS", torch.int32)), keep["MISS"]), tag
-        # the first chunk whose start the carry took through a map: chunk m's start is the
-        # serial state while every chunk before it was replayed serially (a miss)
-        miss = keep["MISS"]
-        used_map = np.nonzero(miss == 0)
-        mstar = np.full(N, T // C, np.int32)
-        for m_, n_ in zip(*used_map):
-            mstar[n_] = min(mstar[n_], m_ + 1)
-        assert np.array_equal(host(run.view("MSTAR", torch.int32)), mstar), tag
-        assert np.array_equal(host(U), Uo) and np.array_equal(host(W), Wo) and np.array_equal(host(S), So)
-        for k in ("miss_frac", "overflow_frac", "mean_lines", "mean_pieces"):
-            assert st[k] == pytest.approx(sto[k], abs=1e-12), (tag, k)
-        assert st["max_pieces"] == sto["max_pieces"] and st["repair_iters"] == 0
+        _check_box_scan(AL, dev, I, u0, w0, preds[tag], 0.1 * q, beta, rho, q, C, K1, K2, block, tag)
+
+
+def test_alif_box_scan_matches_oracle_four_neurons_a_wave(AL, dev):
+    """The same intermediates above the carry's one-neuron-a-wave range (N = 1030 > 1024: four
+    neurons a wave, the last workgroup partial), for a good and a bad prediction."""
+    beta, rho, q = 0.95, 0.995, 0.9
+    T, N, C, K1, K2 = 512, 1030, 128, 16, 32
+    I = _inputs(beta, 2.0, T, N, 9)
+    u0 = np.zeros(N, np.float32)
+    w0 = uniform(N, 0.0, 0.1, 10)
+    _, preds = _preds(I, beta, rho, q, u0, w0, C)
+    for tag in ("oracle", "bad"):
+        print(f"alif box N={N} pred={tag}", flush=True)
+        _check_box_scan(AL, dev, I, u0, w0, preds[tag], 0.1 * q, beta, rho, q, C, K1, K2, 4, tag)
 
 
 @pytest.mark.parametrize("M", [1, 2, 3])

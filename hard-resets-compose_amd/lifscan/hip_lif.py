@@ -366,10 +366,12 @@ def _scan2_pieces(I, beta, theta, u_r, u0, C, K, P):
 
 # Warm-started converged forward (lsh_lif_scan_warm_fwd): the warm-up must run long enough for
 # the true trajectory and the one from u_r to spike together; the time to forget a start grows
-# like 1/(1 - beta), so W = 24/(1 - |beta|) steps rounded up to 256 (256 to 8192).  Chunks of at
-# least 3W keep the re-read of the warm-up rows <= 1/3 of a pass; the longest chunk (a power of
-# two dividing T) that still gives >= WARM_WAVES (chunk, 64-neuron block) waves, else the
-# shortest, with >= 4 chunks.  Measured on MI355X (converged scan_forward_v3 before -> warm):
+# like 1/(1 - beta), so W = 24/(1 - |beta|) steps rounded up to 256 (256 to 8192).  Above
+# WARM_FEW_MAX_N neurons, chunks of at least 3W keep the re-read of the warm-up rows <= 1/3 of a
+# pass; the longest chunk (a power of two dividing T) that still gives >= WARM_WAVES (chunk,
+# 64-neuron block) waves, else the shortest, with >= 4 chunks.  Up to WARM_FEW_MAX_N neurons the
+# chunk gives the waves the pass needs instead (below).  Measured on MI355X with the 3W rule
+# (converged scan_forward_v3 before -> warm):
 # N = 1024, T = 2^20: 7.2 -> 3.1 ms (beta .99), 6.8 -> 2.7 ms (.9); N = 256, T = 2^18: 1.7 ->
 # 0.57 / 1.4 -> 0.19; N = 64, T = 2^20: 3.5 -> 0.56 / 3.3 -> 0.23; N = 1024, T = 65536: 1.14 ->
 # 0.54 / 0.92 -> 0.16; N = 4096, T = 65536: 1.62 -> 0.93 / 1.62 -> 0.69; N = 8192, T = 65536:
@@ -379,6 +381,20 @@ WARM_MAX_N = 8192
 WARM_MIN_CHUNKS = 4
 WARM_WAVES = 1024
 WARM_K = 24.0
+# Up to WARM_FEW_MAX_N neurons the chip has waves to spare, so the chunks are made short enough
+# for about WARM_TARGET_WAVES waves (WARM_TARGET_WAVES_LARGE from WARM_LARGE_WORK neuron-steps,
+# where the pass is bandwidth-bound) instead of 3W long: a wave's time is its W + C dependent
+# steps.  Measured on MI355X (beta 0.99, W 2560, x ~ N(0.012, 0.08^2) / N(0.15, 0.4^2); this
+# rule's chunk against the 3W rule's, or the single pass where that had none): N 128, T 16384
+# 0.15 / 0.10 ms against 0.37 / 0.39 (single pass); N 128, T 65536 0.28 / 0.13 against 0.40 /
+# 0.39; N 1024, T 65536 0.34 / 0.21 against 0.47 / 0.40; N 256, T 2^18 0.40 / 0.23 against 0.46
+# / 0.40; N 4096, T 16384 0.32 / 0.20 against 0.41 / 0.42; N 4096, T 65536 and cfg4 (N 1024,
+# T 2^20) keep their chunk (8192, 16384).  From 8192 neurons the single pass is as fast.
+WARM_FEW_MAX_N = 4096
+WARM_MIN_C = 256
+WARM_TARGET_WAVES = 512
+WARM_TARGET_WAVES_LARGE = 1024
+WARM_LARGE_WORK = 2 ** 29
 
 
 def warm_plan(T, N, beta):
@@ -389,6 +405,20 @@ def warm_plan(T, N, beta):
     b = abs(_f32(beta))
     W = 8192 if b >= 1.0 else int(min(8192, max(256, 256 * math.ceil(WARM_K / (1.0 - b) / 256.0))))
     nb = (N + 63) // 64
+    if N <= WARM_FEW_MAX_N:
+        # warm-ups that reach back to row 0 for most chunks make the pass a serial sweep
+        if T < WARM_MIN_CHUNKS * W:
+            return None
+        target = WARM_TARGET_WAVES_LARGE if T * N >= WARM_LARGE_WORK else WARM_TARGET_WAVES
+        best = None
+        c = 1 << 16
+        while c >= WARM_MIN_C:
+            if T % c == 0 and T // c >= WARM_MIN_CHUNKS:
+                miss = abs(math.log2((T // c) * nb / target))
+                if best is None or miss < best[0]:  # ties keep the longer chunk
+                    best = (miss, c)
+            c //= 2
+        return (best[1], W) if best else None
     best = None
     c = 1 << 16
     while c >= 3 * W:

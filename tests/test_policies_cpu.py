@@ -69,16 +69,22 @@ def test_auto_policies_accept_lengths_the_chunk_policy_rejects():
 
 
 def test_warm_plan():
-    """The warm-started converged forward: W = 24/(1 - |beta|) rounded up to 256 (256..8192),
-    the longest power-of-two chunk >= 3W dividing T with >= 1024 (chunk, block) waves, else the
-    shortest, at least 4 chunks; none above 8192 neurons."""
+    """The warm-started converged forward: W = 24/(1 - |beta|) rounded up to 256 (256..8192).
+    Up to 4096 neurons and from T = 4W: the power-of-two chunk (>= 256, >= 4 chunks) whose
+    (chunk, block) waves come nearest 512 (1024 from 2^29 neuron-steps), the longer on a tie.
+    Above: the longest chunk >= 3W dividing T with >= 1024 waves, else the shortest; none above
+    8192 neurons."""
     from lifscan import hip_lif as L
-    assert L.warm_plan(2 ** 20, 1024, 0.99) == (16384, 2560)   # cfg4
+    assert L.warm_plan(2 ** 20, 1024, 0.99) == (16384, 2560)   # cfg4: 16 blocks x 64 chunks
     assert L.warm_plan(2 ** 20, 1024, 0.9) == (16384, 256)
-    assert L.warm_plan(2 ** 18, 256, 0.99) == (8192, 2560)     # 32 chunks x 4 blocks
-    assert L.warm_plan(65536, 4096, 0.99) == (8192, 2560)
-    assert L.warm_plan(16384, 1024, 0.99) is None              # 2 chunks only
-    assert L.warm_plan(16384, 4096, 0.9) == (1024, 256)
+    assert L.warm_plan(2 ** 18, 256, 0.99) == (2048, 2560)     # 4 blocks x 128 chunks
+    assert L.warm_plan(65536, 4096, 0.99) == (8192, 2560)      # 64 blocks x 8 chunks
+    assert L.warm_plan(16384, 1024, 0.99) == (512, 2560)       # 16 blocks x 32 chunks
+    assert L.warm_plan(16384, 128, 0.99) == (256, 2560)        # as many waves as chunks of 256 give
+    assert L.warm_plan(8192, 128, 0.99) is None                # T < 4W: a serial sweep
+    assert L.warm_plan(16384, 4096, 0.9) == (2048, 256)
+    assert L.warm_plan(65536, 8192, 0.99) == (8192, 2560)      # above 4096 neurons: the 3W rule
+    assert L.warm_plan(16384, 8192, 0.99) is None
     assert L.warm_plan(4096, 65536, 0.9) is None               # N > 8192: single pass
     assert L.warm_plan(1000, 64, 0.9) is None                  # no power-of-two chunk
     assert L.warm_plan(2 ** 20, 64, 1.0)[1] == 8192

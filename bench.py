@@ -206,7 +206,8 @@ def bench_cfg2_mapscan(torch, L, dev, u0, reps):
     with map speculation (C = 16, K = 8), and reference_inputs: the reference's published cfg2
     cells (results/logs/node5/e6d_0.9.log:15, e6d_0.99.log:15: x ~ N(0.15, 0.4^2), u0 = 0,
     scan_forward_v3 at its best cell C = 256, K = 8, timed there without repair) on the same
-    inputs, without and with repair."""
+    inputs, without and with repair, and its few-neuron, long-sequence cells (N = 128 / 1024,
+    T = 16384 / 65536) against this build's exact forward and scan adjoint."""
     T, N = T_CFG, N_CFG
     out = {}
     for beta in (0.9, 0.99):
@@ -264,6 +265,36 @@ def bench_cfg2_mapscan(torch, L, dev, u0, reps):
         del I, Us, Ss, U, S
         torch.cuda.empty_cache()
     out["reference_inputs"] = ref
+    # the reference's few-neuron, long-sequence cells (the same e6d logs, rows N = 128 / 1024,
+    # T = 16384 / 65536): its tuned serial sweeps and its best scan cell (forward without repair,
+    # the chunked affine-scan adjoint) against this build's serial sweeps, its converged exact
+    # forward (scan_forward_v3 with repair to convergence: the serial recurrence) and
+    # scan_backward_auto, on the reference's inputs
+    pub = {(0.9, 128, 16384): (0.341, 1.310, 0.137, 0.072), (0.9, 128, 65536): (1.495, 7.765, 0.265, 0.314),
+           (0.9, 1024, 16384): (0.411, 1.980, 0.334, 0.487), (0.9, 1024, 65536): (1.600, 7.793, 1.326, 1.957),
+           (0.99, 128, 16384): (0.342, 1.318, 0.149, 0.073), (0.99, 128, 65536): (1.499, 7.758, 0.287, 0.313),
+           (0.99, 1024, 16384): (0.412, 1.969, 0.403, 0.489), (0.99, 1024, 65536): (1.604, 7.808, 1.601, 1.965)}
+    few = {}
+    for (beta, Nf, Tf), (rsf, rsb, rcf, rcb) in pub.items():
+        g = torch.Generator().manual_seed(0)
+        I = (0.15 + 0.4 * torch.randn(Tf, Nf, generator=g)).to(dev)
+        GS = torch.randn(Tf, Nf, generator=torch.Generator().manual_seed(1)).to(dev)
+        z = torch.zeros(Nf, device=dev)
+        U, S = L.serial_forward(I, beta, 1.0, 0.0, z)
+        U2, S2 = L.scan_forward_v3(I, beta, 1.0, 0.0, z, C=64, K=16, repair=10 ** 6)
+        ok = bool(torch.equal(U2, U) and torch.equal(S2, S))
+        mine = (ev_time(lambda: L.serial_forward(I, beta, 1.0, 0.0, z), reps),
+                ev_time(lambda: L.serial_backward(I, z, U, S, GS, None, beta, 1.0, 0.0), reps),
+                ev_time(lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, z, C=64, K=16, repair=10 ** 6), reps),
+                ev_time(lambda: L.scan_backward_auto(I, z, U, S, GS, None, beta, 1.0, 0.0), reps))
+        keys = ("serial_fwd_ms", "serial_bwd_ms", "scan_fwd_ms", "scan_bwd_ms")
+        few[f"beta{beta}_N{Nf}_T{Tf}"] = {
+            **{k: round(v, 4) for k, v in zip(keys, mine)}, "scan_fwd_equals_serial": ok,
+            "reference_rtx5090_ms": dict(zip(keys, (rsf, rsb, rcf, rcb))),
+            "speedup_vs_reference": {k: round(r / v, 3) for k, v, r in zip(keys, mine, (rsf, rsb, rcf, rcb))}}
+        del I, GS, U, S, U2, S2
+    out["reference_inputs"]["few_neurons"] = few
+    torch.cuda.empty_cache()
     return out
 
 

@@ -260,8 +260,18 @@ __global__ __launch_bounds__(64) void k_lif_compose(
   }
 }
 
-// Sequential carry over pre-pruned maps (n and ovf final) with the next map's loads issued
-// before the current evaluation; overflowed maps fall back to L serial steps.
+template <int KMAX>
+struct SuperMap {
+  float xd[KMAX], cd[KMAX], a, b;
+  int cnt, ovf;
+};
+
+// Sequential carry over pre-pruned maps (n and ovf final); overflowed maps fall back to L
+// serial steps.  The maps are read one ahead into a ring of two register sets (the loop unrolled by two, so no
+// set is copied), every load unconditional with its index clamped into the arrays (map <= M -
+// 1, slot <= K - 1; eval_slots masks the slots past the count): the compiler's wait for the map
+// in use then leaves the next map's loads in flight.  Lanes past N repeat neuron N - 1 and store
+// nothing.
 template <int KMAX>
 __global__ __launch_bounds__(64) void k_map_carry(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ MA,
@@ -269,40 +279,38 @@ __global__ __launch_bounds__(64) void k_map_carry(
     const float* __restrict__ MX, const float* __restrict__ MC, float* __restrict__ starts,
     int64_t N, int M, int K, int64_t L, float beta, float theta, float u_r) {
   const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
-  if (n >= N) return;
-  float u = u0[n];
-  float xd[KMAX], cd[KMAX], A, B;
-  int cnt, ovf;
-  auto load = [&](int m, float* x, float* c, float& a, float& b, int& k, int& f) {
-    const size_t o = (size_t)m * N + n;
-    a = MA[o];
-    b = MB[o];
-    k = MN[o];
-    f = OVF[o];
+  const bool valid = n < N;
+  const int64_t nn = valid ? n : N - 1;
+  if (M <= 0) return;
+  float u = u0[nn];
+  auto load = [&](int m, SuperMap<KMAX>& d) {
+    const size_t mc = (size_t)min(m, M - 1);
+    const size_t o = mc * N + nn;
+    d.a = MA[o];
+    d.b = MB[o];
+    d.cnt = MN[o];
+    d.ovf = OVF[o];
 #pragma unroll
     for (int i = 0; i < KMAX; ++i) {
-      x[i] = i < K ? MX[((size_t)m * K + i) * N + n] : INFINITY;
-      c[i] = i < K ? MC[((size_t)m * K + i) * N + n] : 0.0f;
+      const size_t os = (mc * K + min(i, K - 1)) * N + nn;
+      d.xd[i] = MX[os];
+      d.cd[i] = MC[os];
     }
   };
-  if (M > 0) load(0, xd, cd, A, B, cnt, ovf);
-  for (int m = 0; m < M; ++m) {
-    float xd2[KMAX], cd2[KMAX], A2 = 1.0f, B2 = 0.0f;
-    int cnt2 = 0, ovf2 = 0;
-    if (m + 1 < M) load(m + 1, xd2, cd2, A2, B2, cnt2, ovf2);
-    starts[(size_t)m * N + n] = u;
-    float nu = eval_slots<KMAX>(xd, cd, cnt, A, B, u);
-    if (ovf) nu = serial_rows(I, N, n, (int64_t)m * L, L, u, beta, theta, u_r);
-    u = nu;
+  SuperMap<KMAX> mr[2];
+  load(0, mr[0]);
+  for (int m0 = 0; m0 < M; m0 += 2) {
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-      xd[i] = xd2[i];
-      cd[i] = cd2[i];
+    for (int ph = 0; ph < 2; ++ph) {
+      const int m = m0 + ph;
+      if (m >= M) break;
+      load(m + 1, mr[ph ^ 1]);
+      const SuperMap<KMAX>& d = mr[ph];
+      if (valid) starts[(size_t)m * N + nn] = u;
+      float nu = eval_slots<KMAX>(d.xd, d.cd, d.cnt, d.a, d.b, u);
+      if (d.ovf) nu = serial_rows(I, N, nn, (int64_t)m * L, L, u, beta, theta, u_r);
+      u = nu;
     }
-    A = A2;
-    B = B2;
-    cnt = cnt2;
-    ovf = ovf2;
   }
 }
 

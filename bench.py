@@ -370,7 +370,8 @@ def bench_cfg4(torch, dev, reps):
     forward at other chunk / warm-up lengths and the long-chunk map scan in pieces it replaced;
     the single-pass exact forward; the serial forward.  Backward: the affine-scan adjoint and the
     serial one.
-    fwd+bwd = the fastest exact forward + the scan adjoint."""
+    fwd+bwd = the fastest exact forward + the scan adjoint.  reference_cells: the reference's
+    published e9d cells (N = 128 / 1024, T = 2^18, its inputs) against this build's passes."""
     from lifscan import hip_lif as L
     T, N, beta = 2 ** 20, 1024, 0.99
     I = (0.012 + 0.08 * torch.randn(T, N, generator=torch.Generator().manual_seed(0))).to(dev)
@@ -453,6 +454,33 @@ def bench_cfg4(torch, dev, reps):
     out["config"] = "N=1024, T=1048576, beta=0.99, x~N(0.012,0.08^2), u0~U[0,1)"
     del I, U, S, gS
     torch.cuda.empty_cache()
+    # the reference's nearest published cells (results/logs/node5/e9d_0.99.log: N = 128 / 1024,
+    # T = 2^18, x ~ N(0.15, 0.4^2), u0 = 0): its tuned serial sweeps, its best v3 and v4 cells
+    # (no repair; v4 at C 128, G 8, K 16) and its scan adjoint, against this build's serial sweeps,
+    # converged exact forward, v4 at the same cell without repair and scan_backward_auto
+    e9d = {}
+    for Nr, pub in ((128, (6.021, 1.280, 1.565, 30.981, 1.255)), (1024, (6.459, 6.297, 8.279, 31.040, 8.071))):
+        Tr = 2 ** 18
+        g = torch.Generator().manual_seed(0)
+        Ir = (0.15 + 0.4 * torch.randn(Tr, Nr, generator=g)).to(dev)
+        GSr = torch.randn(Tr, Nr, generator=torch.Generator().manual_seed(1)).to(dev)
+        z = torch.zeros(Nr, device=dev)
+        Ur, Sr = L.serial_forward(Ir, beta, 1.0, 0.0, z)
+        U2, S2 = L.scan_forward_v3(Ir, beta, 1.0, 0.0, z, C=256, K=16, repair=10 ** 6)
+        ok = bool(torch.equal(U2, Ur) and torch.equal(S2, Sr))
+        del U2, S2
+        mine = (ev_time(lambda: L.serial_forward(Ir, beta, 1.0, 0.0, z), 3),
+                ev_time(lambda: L.scan_forward_v3(Ir, beta, 1.0, 0.0, z, C=256, K=16, repair=10 ** 6), 3),
+                ev_time(lambda: L.scan_forward_v4(Ir, beta, 1.0, 0.0, z, C=128, G=8, K=16, K2=32, repair=0), 3),
+                ev_time(lambda: L.serial_backward(Ir, z, Ur, Sr, GSr, None, beta, 1.0, 0.0), 3),
+                ev_time(lambda: L.scan_backward_auto(Ir, z, Ur, Sr, GSr, None, beta, 1.0, 0.0), 3))
+        keys = ("serial_fwd_ms", "v3_fwd_ms", "v4_fwd_ms", "serial_bwd_ms", "scan_bwd_ms")
+        e9d[f"N{Nr}_T{Tr}"] = {**{k: round(v, 4) for k, v in zip(keys, mine)}, "v3_equals_serial": ok,
+                               "reference_rtx5090_ms": dict(zip(keys, pub)),
+                               "speedup_vs_reference": {k: round(r / v, 3) for k, v, r in zip(keys, mine, pub)}}
+        del Ir, GSr, Ur, Sr
+        torch.cuda.empty_cache()
+    out["reference_cells"] = e9d
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out.items()}
 
 

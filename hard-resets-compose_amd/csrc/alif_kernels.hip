@@ -163,19 +163,46 @@ __global__ __launch_bounds__(64) void k_env_chunks(const float* __restrict__ I,
   EB[m * N + n] = b;
 }
 
+// The chunk maps are read in tiles of kEnvD chunks, the next tile's loads (indices clamped to
+// M - 1, so every load is issued) in flight while a tile is folded: with few neurons one wave
+// walks all M chunks, and a load per chunk would cost a memory latency each.
+constexpr int kEnvD = 16;
 __global__ __launch_bounds__(64) void k_env_carry(const float* __restrict__ u0,
                                                   const float* __restrict__ EC,
                                                   const float* __restrict__ EA,
                                                   const float* __restrict__ EB,
                                                   float* __restrict__ LO, int64_t N, int M) {
   const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
-  if (n >= N) return;
+  if (n >= N || M <= 0) return;
   const float margin = 1e-5f;
   float l = u0[n];
-  for (int m = 0; m < M; ++m) {
-    const size_t o = (size_t)m * N + n;
-    LO[o] = l - margin * (fabsf(l) + 1.0f);
-    l = fminf(EC[o], __fadd_rn(__fmul_rn(EA[o], l), EB[o]));
+  float ec[kEnvD], ea[kEnvD], eb[kEnvD];
+  auto load = [&](int m0, float* c, float* a, float* b) {
+#pragma unroll
+    for (int k = 0; k < kEnvD; ++k) {
+      const size_t o = (size_t)min(m0 + k, M - 1) * N + n;
+      c[k] = EC[o];
+      a[k] = EA[o];
+      b[k] = EB[o];
+    }
+  };
+  load(0, ec, ea, eb);
+  for (int m0 = 0; m0 < M; m0 += kEnvD) {
+    float nc[kEnvD], na[kEnvD], nbb[kEnvD];
+    load(m0 + kEnvD, nc, na, nbb);
+#pragma unroll
+    for (int k = 0; k < kEnvD; ++k) {
+      if (m0 + k < M) {
+        LO[(size_t)(m0 + k) * N + n] = l - margin * (fabsf(l) + 1.0f);
+        l = fminf(ec[k], __fadd_rn(__fmul_rn(ea[k], l), eb[k]));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kEnvD; ++k) {
+      ec[k] = nc[k];
+      ea[k] = na[k];
+      eb[k] = nbb[k];
+    }
   }
 }
 

@@ -480,38 +480,42 @@ __global__ __launch_bounds__(256) void k_lif_carry_staged(
   const bool valid = n < N;
   const int64_t nn = valid ? n : N - 1;
   const int stages = (M + R - 1) / R;
-  // stage s into buffer s & 1 by the loader waves 1-3, one whole chunk per wave at a time:
-  // every row index is a compile-time constant, all loads issued before the LDS writes
+  // stage s into buffer s & 1 by the loader waves 1-3, chunks w - 1, w + 2, ... of the stage:
+  // every load of all of a wave's chunks is issued before the first LDS write (indices clamped
+  // into the arrays, so none sits behind a branch), so a stage costs one memory latency; the
+  // rows past the map's count are never read
+  constexpr int CPL = (R + 2) / 3;  // chunks per loader wave
   auto load_stage = [&](int s) {
     const int m0 = s * R;
     const int nch = min(R, M - m0);
-    for (int c = w - 1; c < nch; c += 3) {
-      const size_t o = (size_t)(m0 + c) * N + nn;
-      const size_t os = (size_t)(m0 + c) * K * N + nn;
-      float v[ROWS];
-      v[0] = EC[o];
-      v[1] = EA[o];
-      v[2] = EB[o];
-      v[3] = MA[o];
-      v[4] = MB[o];
-      v[5] = __int_as_float(CNT[o]);
-      v[6] = __int_as_float(OVFRAW[o]);
+    float v[CPL][ROWS];
+#pragma unroll
+    for (int t = 0; t < CPL; ++t) {
+      const int c = w - 1 + 3 * t;
+      const size_t mc = (size_t)min(m0 + c, M - 1);
+      const size_t o = mc * N + nn;
+      const size_t os = mc * K * N + nn;
+      v[t][0] = EC[o];
+      v[t][1] = EA[o];
+      v[t][2] = EB[o];
+      v[t][3] = MA[o];
+      v[t][4] = MB[o];
+      v[t][5] = __int_as_float(CNT[o]);
+      v[t][6] = __int_as_float(OVFRAW[o]);
 #pragma unroll
       for (int i = 0; i < KMAX; ++i) {
-        if (i < K) {
-          v[7 + i] = MX[os + (size_t)i * N];
-          v[7 + KMAX + i] = MC[os + (size_t)i * N];
-        }
+        const size_t oi = os + (size_t)min(i, K - 1) * N;
+        v[t][7 + i] = MX[oi];
+        v[t][7 + KMAX + i] = MC[oi];
       }
-      float* dst = &sbuf[s & 1][c * ROWS][0];
+    }
 #pragma unroll
-      for (int r = 0; r < 7; ++r) dst[r * WAVE + lane] = v[r];
+    for (int t = 0; t < CPL; ++t) {
+      const int c = w - 1 + 3 * t;
+      if (c < nch) {
+        float* dst = &sbuf[s & 1][c * ROWS][0];
 #pragma unroll
-      for (int i = 0; i < KMAX; ++i) {
-        if (i < K) {
-          dst[(7 + i) * WAVE + lane] = v[7 + i];
-          dst[(7 + KMAX + i) * WAVE + lane] = v[7 + KMAX + i];
-        }
+        for (int r = 0; r < ROWS; ++r) dst[r * WAVE + lane] = v[t][r];
       }
     }
   };
@@ -521,6 +525,7 @@ __global__ __launch_bounds__(256) void k_lif_carry_staged(
   unsigned long long ovf_acc = 0, pcs_acc = 0;
   int pmax = 0;
   const float margin = 1e-5f;
+  const float lo_n = lo_neuron ? lo_neuron[nn] : 0.0f;
   float l = u0[nn];
   float u = l;
   for (int s = 0; s < stages; ++s) {
@@ -534,7 +539,7 @@ __global__ __launch_bounds__(256) void k_lif_carry_staged(
         const float* row = &sbuf[s & 1][c * ROWS][0];
         auto rd = [&](int r) { return row[r * WAVE + lane]; };
         const size_t o = (size_t)m * N + nn;
-        const float lo = lo_neuron ? lo_neuron[nn] : l - margin * (fabsf(l) + 1.0f);
+        const float lo = lo_neuron ? lo_n : l - margin * (fabsf(l) + 1.0f);
         l = fminf(rd(0), __fadd_rn(__fmul_rn(rd(1), l), rd(2)));
         const int cnt = __float_as_int(rd(5));
         const bool ovfr = __float_as_int(rd(6)) != 0;

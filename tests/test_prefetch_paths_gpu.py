@@ -1,0 +1,68 @@
+"""GPU parity of the walks that read their data ahead of use, at shapes that exercise the ends of
+their read-ahead (odd counts, partial tiles), and of the warm-start plan for few neurons.
+
+  * v4's super-map carry (maps one ahead in a ring of two): an odd number of super maps; every
+    intermediate equals the oracle's bit for bit and repair gives the serial recurrence;
+  * the ALIF envelope carry (chunk maps in tiles of 16): 40 chunks, two tiles and a partial one;
+    the entry bounds LU and every later intermediate equal the oracle's;
+  * the converged scan_forward_v3 with few neurons takes warm-started chunks shorter than 3W
+    (the chunk length that gives the pass its waves) and returns the serial recurrence.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import lif_oracle as O
+from tests._inputs import gpu, host, normal, uniform
+from tests.test_alif_gpu import _check_box_scan, _inputs, _preds
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("K,K2", [(16, 32), (4, 8)])
+def test_v4_odd_super_map_count(dev, K, K2):
+    from lifscan import hip_lif as L
+    T, N, C, G, beta = 1344, 130, 64, 3, 0.99  # 21 chunks, 7 super maps
+    I = normal(T, N, 0.012, 0.08, 51)
+    u0 = uniform(N, 0.0, 1.0, 52)
+    Ig, u0g = gpu(I, dev), gpu(u0, dev)
+    print(f"v4 odd super maps K={K} K2={K2}", flush=True)
+    st, sto, keep = {}, {}, {}
+    U, S = L.scan_forward_v4(Ig, beta, 1.0, 0.0, u0g, C=C, G=G, K=K, K2=K2, stats=st)
+    run = L.last_scan_run()
+    Uo, So = O.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, stats=sto, keep=keep)
+    assert np.array_equal(host(run.view("SSTARTS")), keep["sstarts"])
+    assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+    Us, Ss = O.serial_forward(I, beta, 1.0, 0.0, u0)
+    U, S = L.scan_forward_v4(Ig, beta, 1.0, 0.0, u0g, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
+    assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+
+
+def test_alif_envelope_tiles(dev):
+    from lifscan import triton_alif as AL
+    beta, rho, q = 0.95, 0.995, 0.9
+    T, N, C, K1, K2 = 1280, 20, 32, 16, 32  # 40 chunks: envelope tiles of 16, 16 and 8
+    I = _inputs(beta, 2.0, T, N, 53)
+    u0 = np.zeros(N, np.float32)
+    w0 = uniform(N, 0.0, 0.1, 54)
+    _, preds = _preds(I, beta, rho, q, u0, w0, C)
+    for tag in ("oracle", "bad"):
+        print(f"alif envelope tiles pred={tag}", flush=True)
+        _check_box_scan(AL, dev, I, u0, w0, preds[tag], 0.1 * q, beta, rho, q, C, K1, K2, 4, tag)
+
+
+@pytest.mark.parametrize("beta", [0.99, 0.9])
+def test_converged_v3_few_neurons_short_warm_chunks(dev, beta):
+    from lifscan import hip_lif as L
+    T, N = 16384, 130
+    C, W = L.warm_plan(T, N, beta)
+    assert C < 3 * W or beta == 0.9  # the few-neuron rule, not the 3W one, at beta 0.99
+    I = normal(T, N, 0.012, 0.08, 55)
+    u0 = uniform(N, 0.0, 1.0, 56)
+    print(f"converged v3, few neurons, beta={beta}: warm C={C} W={W}", flush=True)
+    U, S = L.scan_forward_v3(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=64, K=16, repair=10 ** 6)
+    run = L.last_scan_run()
+    assert run.warm and (run.C, run.W) == (C, W)
+    Us, Ss = O.serial_forward(I, beta, 1.0, 0.0, u0)
+    assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)

@@ -451,6 +451,129 @@ __global__ __launch_bounds__(64) void k_lif_carry(
   }
 }
 
+// The same carry with one wave per neuron, for few neurons (where one lane per neuron leaves
+// one or two waves on the chip to walk every chunk with a memory latency each).  The chunks go
+// in windows of 64: lane j holds the scalars (envelope map, A, B, count, raw overflow) of the
+// window's chunk j, and VGPR g holds the maps of its chunks 4g..4g+3, lane 16r + s the
+// breakpoint and constant of slot s of chunk 4g + r (K <= 16).  The next window's loads are
+// issued, unconditionally with clamped indices, before the current one is walked, so the walk
+// waits on memory once per 64 chunks.  Per chunk, the counts #{xd > lo} and #{xd > u} are
+// ballots over the chunk's 16-lane row, the constant is read from lane 16r + k, and the four
+// per-chunk outputs collect in lane c, stored once per window.  The overflow fallback reads
+// 64 steps at a time, one per lane, and walks them with lane reads.  Results are the same as
+// k_lif_carry's: the same operations on the same values, only distributed over lanes.
+__device__ __forceinline__ float lane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+struct LifCarryWindow {
+  float ec, ea, eb, ma, mb;  // lane j: chunk j of the window
+  int cnt, ovfr;
+  float xd[16], cd[16];  // VGPR g, lane 16r + s: slot s of chunk 4g + r
+};
+
+__global__ __launch_bounds__(64) void k_lif_carry_wave(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ EC,
+    const float* __restrict__ EA, const float* __restrict__ EB, const float* __restrict__ MA,
+    const float* __restrict__ MB, const int* __restrict__ CNT, const int* __restrict__ OVFRAW,
+    const float* __restrict__ MX, const float* __restrict__ MC,
+    const float* __restrict__ lo_neuron, float* __restrict__ LO, int* __restrict__ MN,
+    int* __restrict__ OVF, float* __restrict__ starts, WsHeader* hdr, int64_t N, int M, int C,
+    int K, float beta, float theta, float u_r) {
+  const int64_t n = blockIdx.x;
+  const int lane = threadIdx.x;
+  const int row = lane >> 4, slot = lane & 15;
+  const int sl = min(slot, K - 1);
+  auto load = [&](int w, LifCarryWindow& d) {
+    const size_t o = (size_t)min(w * 64 + lane, M - 1) * N + n;
+    d.ec = EC[o];
+    d.ea = EA[o];
+    d.eb = EB[o];
+    d.ma = MA[o];
+    d.mb = MB[o];
+    d.cnt = CNT[o];
+    d.ovfr = OVFRAW[o];
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      const size_t os = ((size_t)min(w * 64 + 4 * g + row, M - 1) * K + sl) * N + n;
+      d.xd[g] = MX[os];
+      d.cd[g] = MC[os];
+    }
+  };
+  const float margin = 1e-5f;
+  const float lo_n = lo_neuron ? lo_neuron[n] : 0.0f;
+  float l = u0[n];
+  float u = l;
+  unsigned long long ovf_acc = 0, pcs_acc = 0;
+  int pmax = 0;
+  const int NW = (M + 63) / 64;
+  LifCarryWindow cur, nxt;
+  load(0, cur);
+  for (int w = 0; w < NW; ++w) {
+    load(min(w + 1, NW - 1), nxt);
+    const int nc = min(64, M - w * 64);
+    float lo_o = 0.0f, st_o = 0.0f;
+    int mn_o = 0, ovf_o = 0;
+#pragma unroll
+    for (int g = 0; g < 16; ++g) {
+      for (int r = 0; r < 4; ++r) {
+        const int c = 4 * g + r;
+        if (c >= nc) break;
+        const float ec = lane_f(cur.ec, c), ea = lane_f(cur.ea, c), eb = lane_f(cur.eb, c);
+        const int cnt = __builtin_amdgcn_readlane(cur.cnt, c);
+        const bool ovfr = __builtin_amdgcn_readlane(cur.ovfr, c) != 0;
+        const float lo = lo_neuron ? lo_n : l - margin * (fabsf(l) + 1.0f);
+        l = fminf(ec, __fadd_rn(__fmul_rn(ea, l), eb));
+        const bool in_row = row == r;
+        const int gt = __popcll(__ballot(in_row && slot < cnt && cur.xd[g] > lo));
+        const int ne = min(cnt, gt + 1);
+        const bool ovf = ovfr && gt == cnt;
+        const int k = __popcll(__ballot(in_row && slot < ne && cur.xd[g] > u));
+        const float cval = lane_f(cur.cd[g], 16 * r + min(k, 15));
+        float nu = (k == ne)
+                       ? __fadd_rn(__fmul_rn(lane_f(cur.ma, c), u), lane_f(cur.mb, c))
+                       : cval;
+        if (lane == c) {
+          lo_o = lo;
+          st_o = u;
+          mn_o = ne;
+          ovf_o = ovf ? 1 : 0;
+        }
+        if (ovf) {  // rare: serial fallback through this chunk
+          const float* Ip = I + (size_t)(w * 64 + c) * C * N + n;
+          float wv = u;
+          for (int t0 = 0; t0 < C; t0 += 64) {
+            const float xv = Ip[(size_t)min(t0 + lane, C - 1) * N];
+            const int nt = min(64, C - t0);
+            for (int j = 0; j < nt; ++j) {
+              bool sp;
+              wv = lif_step(wv, lane_f(xv, j), beta, theta, u_r, sp);
+            }
+          }
+          nu = wv;
+        }
+        u = nu;
+        ovf_acc += ovf ? 1ull : 0ull;
+        pcs_acc += (unsigned long long)ne;
+        pmax = max(pmax, ne);
+      }
+    }
+    if (lane < nc) {
+      const size_t o = (size_t)(w * 64 + lane) * N + n;
+      LO[o] = lo_o;
+      starts[o] = st_o;
+      MN[o] = mn_o;
+      OVF[o] = ovf_o;
+    }
+    cur = nxt;
+  }
+  if (lane == 0) {
+    atomicAdd(&hdr->ovf_count, ovf_acc);
+    atomicAdd(&hdr->pieces_sum, pcs_acc);
+    atomicMax(&hdr->pieces_max, (unsigned int)pmax);
+  }
+}
+
 // The same carry with its map reads staged through LDS, for long chunk sequences (many M, few
 // neurons), where the one-wave carry above waits a full memory latency per chunk.  A workgroup
 // of 4 waves owns 64 neurons: waves 1-3 load the next R chunks' maps (7 + 2K rows of 64 lanes
@@ -861,6 +984,21 @@ static void launch_carry(const float* I, const float* u0, const float* lo_neuron
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(ws + off); };
+// Most neurons for the one-wave-per-neuron carry.  Measured on MI355X, the map scan (build,
+// carry, replay; x ~ N(0.15, 0.4^2), beta 0.99, C 256, K 16) against the staged carry: N = 128,
+// T = 65536 0.47 -> 0.22 ms; N = 1024, T = 65536 0.70 -> 0.54 ms; N = 4096, T = 65536 1.69 ->
+// 2.01 ms (K 8, with 3 % overflowed chunks: 3.68 -> 1.95 ms); N = 16384, T = 16384 1.48 -> 2.29.
+#ifndef LSH_LIF_CARRY_WAVE_MAX_N
+#define LSH_LIF_CARRY_WAVE_MAX_N 2048
+#endif
+  if (KMAX <= 16 && N <= LSH_LIF_CARRY_WAVE_MAX_N) {
+    // few neurons: one wave per neuron
+    hipLaunchKernelGGL(k_lif_carry_wave, dim3((unsigned)N), dim3(WAVE), 0, st, I, u0, F(L.EC),
+                       F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
+                       F(L.MC), lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS),
+                       reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r);
+    return;
+  }
   if (M >= 4 * CarryStage<KMAX>::R && KMAX <= 32) {
     // long chunk sequences: map reads staged through LDS by three loader waves
     hipLaunchKernelGGL((k_lif_carry_staged<KMAX>), dim3((unsigned)NB), dim3(256), 0, st, I, u0,

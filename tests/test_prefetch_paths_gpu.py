@@ -66,3 +66,32 @@ def test_converged_v3_few_neurons_short_warm_chunks(dev, beta):
     assert run.warm and (run.C, run.W) == (C, W)
     Us, Ss = O.serial_forward(I, beta, 1.0, 0.0, u0)
     assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
+
+
+@pytest.mark.parametrize("N,K", [(70, 1), (70, 4), (70, 16), (2113, 8), (2113, 16)])
+def test_v3_carry_windows_and_fallback(dev, N, K):
+    """The carry at few neurons (one wave per neuron, chunks in windows of 64) and just above
+    them (one lane per neuron, maps staged through LDS): M = 150 chunks (two windows and a
+    partial one), C = 100 (the overflow fallback reads 64 rows, then 36), overflowed chunks at
+    small K.  LO, starts, kept counts, overflow flags, U, S and the stats equal the oracle's
+    bit for bit."""
+    from lifscan import hip_lif as L
+    C, M, beta = 100, 150, 0.99
+    T = C * M
+    I = normal(T, N, 0.012, 0.08, 57)
+    u0 = uniform(N, 0.0, 1.0, 58)
+    print(f"v3 carry windows N={N} K={K}", flush=True)
+    st, sto, keep = {}, {}, {}
+    U, S = L.scan_forward_v3(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=C, K=K, stats=st)
+    run = L.last_scan_run()
+    Uo, So = O.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, stats=sto, keep=keep)
+    assert np.array_equal(host(run.view("LO")), keep["Lo"])
+    assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+    assert np.array_equal(host(run.view("MN", torch.int32)), keep["n"])
+    assert np.array_equal(host(run.view("OVF", torch.int32)), keep["ovf"])
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+    assert st["overflow_frac"] == pytest.approx(sto["overflow_frac"], abs=0)
+    assert st["mean_pieces"] == pytest.approx(sto["mean_pieces"], rel=1e-12)
+    assert st["max_pieces"] == sto["max_pieces"]
+    if K <= 4:
+        assert sto["overflow_frac"] > 0.01

@@ -288,11 +288,18 @@ def bench_cfg2_mapscan(torch, L, dev, u0, reps):
                 ev_time(lambda: L.scan_forward_v3(I, beta, 1.0, 0.0, z, C=64, K=16, repair=10 ** 6), reps),
                 ev_time(lambda: L.scan_backward_auto(I, z, U, S, GS, None, beta, 1.0, 0.0), reps))
         keys = ("serial_fwd_ms", "serial_bwd_ms", "scan_fwd_ms", "scan_bwd_ms")
+        # the map scan itself without repair, as the reference's scan cell (best of C 128 / 256, K 16)
+        ms = min((ev_time(lambda: L.scan_forward_mapscan(I, beta, 1.0, 0.0, z, C=C, K=16, repair=0), reps), C)
+                 for C in (128, 256))
+        _, S3 = L.scan_forward_mapscan(I, beta, 1.0, 0.0, z, C=ms[1], K=16, repair=0)
         few[f"beta{beta}_N{Nf}_T{Tf}"] = {
             **{k: round(v, 4) for k, v in zip(keys, mine)}, "scan_fwd_equals_serial": ok,
+            "map_scan_no_repair_ms": round(ms[0], 4), "map_scan_C": ms[1],
+            "map_scan_spike_flips": int((S3 != S).sum().item()),
             "reference_rtx5090_ms": dict(zip(keys, (rsf, rsb, rcf, rcb))),
-            "speedup_vs_reference": {k: round(r / v, 3) for k, v, r in zip(keys, mine, (rsf, rsb, rcf, rcb))}}
-        del I, GS, U, S, U2, S2
+            "speedup_vs_reference": {**{k: round(r / v, 3) for k, v, r in zip(keys, mine, (rsf, rsb, rcf, rcb))},
+                                     "map_scan_no_repair": round(rcf / ms[0], 3)}}
+        del I, GS, U, S, U2, S2, S3
     out["reference_inputs"]["few_neurons"] = few
     torch.cuda.empty_cache()
     return out

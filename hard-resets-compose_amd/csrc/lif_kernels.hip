@@ -480,7 +480,11 @@ __global__ __launch_bounds__(64) void k_lif_carry_wave(
     const float* __restrict__ lo_neuron, float* __restrict__ LO, int* __restrict__ MN,
     int* __restrict__ OVF, float* __restrict__ starts, WsHeader* hdr, int64_t N, int M, int C,
     int K, float beta, float theta, float u_r) {
-  const int64_t n = blockIdx.x;
+  // Neurons in eight contiguous ranges, range x on the blocks b with b % 8 == x: consecutive
+  // workgroups go to the eight XCDs in turn, so each XCD's L2 holds the map lines (32 neurons
+  // a line) of its own neurons.
+  const int64_t b = blockIdx.x, q = N / 8, rem = N % 8, x = b % 8;
+  const int64_t n = x * q + (x < rem ? x : rem) + b / 8;
   const int lane = threadIdx.x;
   const int row = lane >> 4, slot = lane & 15;
   const int sl = min(slot, K - 1);
@@ -986,8 +990,9 @@ static void launch_carry(const float* I, const float* u0, const float* lo_neuron
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(ws + off); };
 // Most neurons for the one-wave-per-neuron carry.  Measured on MI355X, the map scan (build,
 // carry, replay; x ~ N(0.15, 0.4^2), beta 0.99, C 256, K 16) against the staged carry: N = 128,
-// T = 65536 0.47 -> 0.22 ms; N = 1024, T = 65536 0.70 -> 0.54 ms; N = 4096, T = 65536 1.69 ->
-// 2.01 ms (K 8, with 3 % overflowed chunks: 3.68 -> 1.95 ms); N = 16384, T = 16384 1.48 -> 2.29.
+// T = 65536 0.47 -> 0.22 ms; N = 1024, T = 65536 0.70 -> 0.50 ms; N = 2048, T = 65536 1.04 ->
+// 0.90 ms (T = 16384: 0.29 -> 0.32); N = 4096, T = 65536 1.69 -> 2.01 ms (K 8, with 3 %
+// overflowed chunks: 3.68 -> 1.95 ms); N = 16384, T = 16384 1.48 -> 2.29.
 #ifndef LSH_LIF_CARRY_WAVE_MAX_N
 #define LSH_LIF_CARRY_WAVE_MAX_N 2048
 #endif

@@ -462,10 +462,6 @@ __global__ __launch_bounds__(64) void k_lif_carry(
 // per-chunk outputs collect in lane c, stored once per window.  The overflow fallback reads
 // 64 steps at a time, one per lane, and walks them with lane reads.  Results are the same as
 // k_lif_carry's: the same operations on the same values, only distributed over lanes.
-__device__ __forceinline__ float lane_f(float v, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
-}
-
 struct LifCarryWindow {
   float ec, ea, eb, ma, mb;  // lane j: chunk j of the window
   int cnt, ovfr;
@@ -480,11 +476,7 @@ __global__ __launch_bounds__(64) void k_lif_carry_wave(
     const float* __restrict__ lo_neuron, float* __restrict__ LO, int* __restrict__ MN,
     int* __restrict__ OVF, float* __restrict__ starts, WsHeader* hdr, int64_t N, int M, int C,
     int K, float beta, float theta, float u_r) {
-  // Neurons in eight contiguous ranges, range x on the blocks b with b % 8 == x: consecutive
-  // workgroups go to the eight XCDs in turn, so each XCD's L2 holds the map lines (32 neurons
-  // a line) of its own neurons.
-  const int64_t b = blockIdx.x, q = N / 8, rem = N % 8, x = b % 8;
-  const int64_t n = x * q + (x < rem ? x : rem) + b / 8;
+  const int64_t n = xcd_neuron(blockIdx.x, N);
   const int lane = threadIdx.x;
   const int row = lane >> 4, slot = lane & 15;
   const int sl = min(slot, K - 1);

@@ -314,6 +314,120 @@ __global__ __launch_bounds__(64) void k_map_carry(
   }
 }
 
+// The two sequential walks above with one wave per neuron, for few neurons: one lane per
+// neuron leaves one or two waves on the chip, each waiting on memory for every chunk or super
+// map.  The maps go in windows of 64: lane j holds the scalars of the window's map j, the next
+// window's loads are issued (indices clamped, so every load is issued) before the current one
+// is walked, and the per-map outputs collect in lane c, stored once per window.  The
+// operations and values are those of k_lif_env_lo and k_map_carry, so the bits are the same.
+//
+// Envelope bounds: l walks the window's envelope maps read from their lanes.
+__global__ __launch_bounds__(64) void k_lif_env_lo_wave(const float* __restrict__ u0,
+                                                        const float* __restrict__ EC,
+                                                        const float* __restrict__ EA,
+                                                        const float* __restrict__ EB,
+                                                        float* __restrict__ LO, int64_t N, int M) {
+  if (M <= 0) return;
+  const int64_t n = xcd_neuron(blockIdx.x, N);
+  const int lane = threadIdx.x;
+  const float margin = 1e-5f;
+  float l = u0[n];
+  auto load = [&](int w, float& c, float& a, float& b) {
+    const size_t o = (size_t)min(w * 64 + lane, M - 1) * N + n;
+    c = EC[o];
+    a = EA[o];
+    b = EB[o];
+  };
+  const int NW = (M + 63) / 64;
+  float c0, a0, b0;
+  load(0, c0, a0, b0);
+  for (int w = 0; w < NW; ++w) {
+    float c1, a1, b1;
+    load(min(w + 1, NW - 1), c1, a1, b1);
+    const int nc = min(64, M - w * 64);
+    float lo_o = 0.0f;
+    for (int c = 0; c < nc; ++c) {
+      if (lane == c) lo_o = l - margin * (fabsf(l) + 1.0f);
+      l = fminf(lane_f(c0, c), __fadd_rn(__fmul_rn(lane_f(a0, c), l), lane_f(b0, c)));
+    }
+    if (lane < nc) LO[(size_t)(w * 64 + lane) * N + n] = lo_o;
+    c0 = c1;
+    a0 = a1;
+    b0 = b1;
+  }
+}
+
+// Super-map carry (K2 <= 32): VGPR g holds super maps 2g and 2g + 1 of the window, lane 32h + s
+// slot s of map 2g + h; k = #{s < n : xd[s] > u} is a ballot over the map's half-wave and the
+// constant a lane read.  An overflowed map reads its L rows 64 at a time, one per lane.
+struct SuperWindow {
+  float a, b;  // lane j: map j of the window
+  int cnt, ovf;
+  float xd[32], cd[32];  // VGPR g, lane 32h + s: slot s of map 2g + h
+};
+
+__global__ __launch_bounds__(64) void k_map_carry_wave(
+    const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ MA,
+    const float* __restrict__ MB, const int* __restrict__ MN, const int* __restrict__ OVF,
+    const float* __restrict__ MX, const float* __restrict__ MC, float* __restrict__ starts,
+    int64_t N, int M, int K, int64_t L, float beta, float theta, float u_r) {
+  if (M <= 0) return;
+  const int64_t n = xcd_neuron(blockIdx.x, N);
+  const int lane = threadIdx.x;
+  const int half = lane >> 5, slot = lane & 31;
+  const int sl = min(slot, K - 1);
+  auto load = [&](int w, SuperWindow& d) {
+    const size_t o = (size_t)min(w * 64 + lane, M - 1) * N + n;
+    d.a = MA[o];
+    d.b = MB[o];
+    d.cnt = MN[o];
+    d.ovf = OVF[o];
+#pragma unroll
+    for (int g = 0; g < 32; ++g) {
+      const size_t os = ((size_t)min(w * 64 + 2 * g + half, M - 1) * K + sl) * N + n;
+      d.xd[g] = MX[os];
+      d.cd[g] = MC[os];
+    }
+  };
+  float u = u0[n];
+  const int NW = (M + 63) / 64;
+  SuperWindow cur, nxt;
+  load(0, cur);
+  for (int w = 0; w < NW; ++w) {
+    load(min(w + 1, NW - 1), nxt);
+    const int nc = min(64, M - w * 64);
+    float st_o = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 32; ++g) {
+      for (int h = 0; h < 2; ++h) {
+        const int c = 2 * g + h;
+        if (c >= nc) break;
+        const int cnt = __builtin_amdgcn_readlane(cur.cnt, c);
+        const int k = __popcll(__ballot(half == h && slot < cnt && cur.xd[g] > u));
+        float nu = k == cnt ? __fadd_rn(__fmul_rn(lane_f(cur.a, c), u), lane_f(cur.b, c))
+                            : lane_f(cur.cd[g], 32 * h + min(k, 31));
+        if (lane == c) st_o = u;
+        if (__builtin_amdgcn_readlane(cur.ovf, c) != 0) {  // serial fallback through the map
+          const float* Ip = I + (size_t)(w * 64 + c) * L * N + n;
+          float wv = u;
+          for (int64_t t0 = 0; t0 < L; t0 += 64) {
+            const float xv = Ip[(size_t)min<int64_t>(t0 + lane, L - 1) * N];
+            const int nt = (int)min<int64_t>(64, L - t0);
+            for (int j = 0; j < nt; ++j) {
+              bool sp;
+              wv = lif_step(wv, lane_f(xv, j), beta, theta, u_r, sp);
+            }
+          }
+          nu = wv;
+        }
+        u = nu;
+      }
+    }
+    if (lane < nc) starts[(size_t)(w * 64 + lane) * N + n] = st_o;
+    cur = nxt;
+  }
+}
+
 template <int KMAX>
 __global__ __launch_bounds__(64) void k_lif_carry_inner(
     const float* __restrict__ I, const float* __restrict__ sstarts, const float* __restrict__ MA,
@@ -350,6 +464,11 @@ void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* 
                               int C, int64_t repair, float beta, float theta, float u_r,
                               hipStream_t st);
 
+// Most neurons for the one-wave-per-neuron envelope and super-map walks.
+#ifndef LSH_V4_WAVE_MAX_N
+#define LSH_V4_WAVE_MAX_N 2048
+#endif
+
 static int kcap(int k) { return k <= 4 ? 4 : k <= 8 ? 8 : k <= 16 ? 16 : k <= 32 ? 32 : 64; }
 
 template <int KMAX, int K2MAX>
@@ -384,8 +503,12 @@ static void launch_chunk_kernels(const float* I, const float* u0, char* w, const
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
-  hipLaunchKernelGGL((k_lif_env_lo<16>), dim3((unsigned)NB), dim3(WAVE), 0, st, u0, F(L.v3.EC),
-                     F(L.v3.EA), F(L.v3.EB), F(L.v3.LO), N, M);
+  if (N <= LSH_V4_WAVE_MAX_N)
+    hipLaunchKernelGGL(k_lif_env_lo_wave, dim3((unsigned)N), dim3(WAVE), 0, st, u0, F(L.v3.EC),
+                       F(L.v3.EA), F(L.v3.EB), F(L.v3.LO), N, M);
+  else
+    hipLaunchKernelGGL((k_lif_env_lo<16>), dim3((unsigned)NB), dim3(WAVE), 0, st, u0, F(L.v3.EC),
+                       F(L.v3.EA), F(L.v3.EB), F(L.v3.LO), N, M);
   // ~8192 blocks in all: enough to fill the chip, few header atomics
   const int MB = (int)std::max<int64_t>(1, std::min<int64_t>(M, 8192 / NB));
   hipLaunchKernelGGL((k_lif_trunc<KMAX>), dim3((unsigned)((int64_t)MB * NB)), dim3(WAVE), 0, st,
@@ -411,6 +534,12 @@ static void launch_super_carry(const float* I, const float* u0, char* w, const l
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  if (K2MAX <= 32 && N <= LSH_V4_WAVE_MAX_N) {
+    hipLaunchKernelGGL(k_map_carry_wave, dim3((unsigned)N), dim3(WAVE), 0, st, I, u0, F(L.SA),
+                       F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC), F(L.SSTARTS), N, M2, K2,
+                       Lsteps, beta, theta, u_r);
+    return;
+  }
   hipLaunchKernelGGL((k_map_carry<K2MAX>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, F(L.SA),
                      F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC), F(L.SSTARTS), N, M2, K2,
                      Lsteps, beta, theta, u_r);

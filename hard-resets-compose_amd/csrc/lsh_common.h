@@ -49,6 +49,19 @@ __device__ __forceinline__ float lif_step(float u, float x, float beta, float th
   return s ? u_r : v;
 }
 
+// The value of v in lane `lane` (wave-uniform), for walks with one wave per neuron.
+__device__ __forceinline__ float lane_f(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Neuron of workgroup b for kernels with one wave per neuron: eight contiguous ranges, range x
+// on the workgroups b with b % 8 == x.  Consecutive workgroups go to the eight XCDs in turn,
+// so each XCD's L2 then holds the cache lines (32 neurons a line) of its own neurons.
+__device__ __forceinline__ int64_t xcd_neuron(int64_t b, int64_t N) {
+  const int64_t q = N / 8, rem = N % 8, x = b % 8;
+  return x * q + (x < rem ? x : rem) + b / 8;
+}
+
 // 1 / (1 + exp(-z)), the logistic sigmoid of every surrogate.  LSH_FAST_SURROGATE (default)
 // takes the hardware exponential and reciprocal (a few ulp; the reference's Triton path also
 // uses approximate exp and division) instead of the library expf and a correctly rounded

@@ -95,3 +95,30 @@ def test_v3_carry_windows_and_fallback(dev, N, K):
     assert st["max_pieces"] == sto["max_pieces"]
     if K <= 4:
         assert sto["overflow_frac"] > 0.01
+
+
+@pytest.mark.parametrize("N,K,K2", [(70, 4, 8), (70, 16, 32), (2113, 4, 8)])
+def test_v4_walks_windows_and_fallback(dev, N, K, K2):
+    """v4's envelope walk and super-map carry at few neurons (one wave per neuron, maps in
+    windows of 64) and just above them (one lane per neuron): 150 super maps of G = 5 chunks of
+    C = 20 steps (an overflowed super map's fallback reads 64 rows, then 36), overflowed super
+    maps at small K2.  LO, super starts, chunk starts, U, S and the stats equal the oracle's
+    bit for bit."""
+    from lifscan import hip_lif as L
+    C, G, M2, beta = 20, 5, 150, 0.99
+    T = C * G * M2
+    I = normal(T, N, 0.012, 0.08, 59)
+    u0 = uniform(N, 0.0, 1.0, 60)
+    print(f"v4 walks windows N={N} K={K} K2={K2}", flush=True)
+    st, sto, keep = {}, {}, {}
+    U, S = L.scan_forward_v4(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=C, G=G, K=K, K2=K2, stats=st)
+    run = L.last_scan_run()
+    Uo, So = O.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, stats=sto, keep=keep)
+    assert np.array_equal(host(run.view("LO")), keep["Lo"])
+    assert np.array_equal(host(run.view("SSTARTS")), keep["sstarts"])
+    assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+    for k in sto:
+        assert st[k] == pytest.approx(sto[k], rel=1e-12), k
+    if K2 == 8:
+        assert keep["SOVF"].mean() > 0.01

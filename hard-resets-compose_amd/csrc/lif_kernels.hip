@@ -535,19 +535,8 @@ __global__ __launch_bounds__(64) void k_lif_carry_wave(
           mn_o = ne;
           ovf_o = ovf ? 1 : 0;
         }
-        if (ovf) {  // rare: serial fallback through this chunk
-          const float* Ip = I + (size_t)(w * 64 + c) * C * N + n;
-          float wv = u;
-          for (int t0 = 0; t0 < C; t0 += 64) {
-            const float xv = Ip[(size_t)min(t0 + lane, C - 1) * N];
-            const int nt = min(64, C - t0);
-            for (int j = 0; j < nt; ++j) {
-              bool sp;
-              wv = lif_step(wv, lane_f(xv, j), beta, theta, u_r, sp);
-            }
-          }
-          nu = wv;
-        }
+        if (ovf)  // rare: serial fallback through this chunk
+          nu = wave_serial_rows(I, N, n, (int64_t)(w * 64 + c) * C, C, u, beta, theta, u_r);
         u = nu;
         ovf_acc += ovf ? 1ull : 0ull;
         pcs_acc += (unsigned long long)ne;

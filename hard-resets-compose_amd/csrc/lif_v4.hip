@@ -260,6 +260,112 @@ __global__ __launch_bounds__(64) void k_lif_compose(
   }
 }
 
+// The same composition with one wave per neuron, for few neurons (one lane per neuron gives
+// M/G * N/64 waves, 128 at N = 128 and M/G = 64, each composing its slots one after another).
+// A wave takes SPW consecutive super maps of one neuron; lane i holds slot i of the composed
+// map (K2 <= 64) and of the chunk map being composed.  (1) pushes every kept constant through
+// the right map at once (its count over the right map's breakpoints, read from their lanes, then
+// a lane shuffle for the constant); (2) walks the right map's breakpoints in order, as wave-
+// uniform values, appending the accepted ones in lane nH; the next chunk map's loads (indices
+// clamped into the group) are issued before the current one is composed.  The same operations
+// on the same values as k_lif_compose, so the same bits; the statistics take one atomic per
+// wave.
+__global__ __launch_bounds__(64) void k_lif_compose_wave(
+    const float* __restrict__ MA, const float* __restrict__ MB, const int* __restrict__ MN,
+    const int* __restrict__ OVF, const float* __restrict__ MX, const float* __restrict__ MC,
+    const float* __restrict__ LO, const float* __restrict__ u0, float* __restrict__ SA,
+    float* __restrict__ SB, int* __restrict__ SN, int* __restrict__ SOVF, float* __restrict__ SX,
+    float* __restrict__ SC, WsHeader* hdr, int64_t N, int M2, int SPW, int G, int K, int K2,
+    float theta, float u_r) {
+  const int64_t b = blockIdx.x;
+  const int64_t n = xcd_neuron(b % N, N);
+  const int s0 = (int)(b / N) * SPW;
+  const int lane = threadIdx.x;
+  const int sl = min(lane, K - 1);
+  const float hi = fmaxf(u0[n], fmaxf(theta, u_r));
+  unsigned long long so = 0, sp = 0;
+  int smax = 0;
+  struct Chunk {
+    float a, b, yd, dd;
+    int cnt, ovf;
+  };
+  auto load = [&](int64_t m, Chunk& d) {
+    const size_t o = (size_t)m * N + n;
+    d.a = MA[o];
+    d.b = MB[o];
+    d.cnt = MN[o];
+    d.ovf = OVF[o];
+    const size_t os = ((size_t)m * K + sl) * N + n;
+    d.yd = MX[os];
+    d.dd = MC[os];
+  };
+  const int s1 = min(s0 + SPW, M2);
+  for (int s = s0; s < s1; ++s) {
+    const int64_t m0 = (int64_t)s * G;
+    const float lo = LO[(size_t)m0 * N + n];
+    Chunk h, nx;
+    load(m0, h);
+    load(m0 + min(1, G - 1), nx);
+    float A = h.a, B = h.b;
+    int nH = h.cnt;
+    int ov = h.ovf;
+    float X = lane < K ? h.yd : INFINITY;
+    float Cc = lane < K ? h.dd : 0.0f;
+    float xmin = INFINITY;
+    for (int i = 0; i < nH; ++i) xmin = fminf(xmin, lane_f(X, i));
+    for (int jj = 1; jj < G; ++jj) {
+      const Chunk g = nx;
+      load(m0 + min(jj + 1, G - 1), nx);
+      const int ng = g.cnt;
+      ov |= g.ovf;
+      // (1) the left map's constants pushed through the right map
+      int c = 0;
+      for (int j = 0; j < ng; ++j) c += lane_f(g.yd, j) > Cc ? 1 : 0;
+      const float gc = __shfl(g.dd, min(c, 63));
+      if (lane < nH) Cc = (c == ng) ? __fadd_rn(__fmul_rn(g.a, Cc), g.b) : gc;
+      // (2) the right map's breakpoints pulled back through the left map's affine part
+      for (int j = 0; j < ng; ++j) {
+        const float dj = lane_f(g.dd, j);
+        const float num = lane_f(g.yd, j) - B;
+        const float z = A == 0.0f ? (num > 0.0f ? INFINITY : -INFINITY) : num / A;
+        bool nw = (z < xmin) && (z <= hi) && (xmin > lo);
+        if (nw && nH >= K2) ov = 1;
+        nw = nw && (nH < K2);
+        if (nw) {
+          if (lane == nH) {
+            X = z;
+            Cc = dj;
+          }
+          ++nH;
+          xmin = z;
+        }
+      }
+      // (3) affine parts
+      B = __fadd_rn(__fmul_rn(g.a, B), g.b);
+      A = g.a * A;
+    }
+    const size_t o = (size_t)s * N + n;
+    if (lane == 0) {
+      SA[o] = A;
+      SB[o] = B;
+      SN[o] = nH;
+      SOVF[o] = ov;
+    }
+    if (lane < K2) {
+      SX[((size_t)s * K2 + lane) * N + n] = X;
+      SC[((size_t)s * K2 + lane) * N + n] = Cc;
+    }
+    so += ov ? 1ull : 0ull;
+    sp += (unsigned long long)nH;
+    smax = max(smax, nH);
+  }
+  if (lane == 0) {
+    atomicAdd(&hdr->super_ovf_count, so);
+    atomicAdd(&hdr->super_pieces_sum, sp);
+    atomicMax(&hdr->super_pieces_max, (unsigned int)smax);
+  }
+}
+
 template <int KMAX>
 struct SuperMap {
   float xd[KMAX], cd[KMAX], a, b;
@@ -407,19 +513,8 @@ __global__ __launch_bounds__(64) void k_map_carry_wave(
         float nu = k == cnt ? __fadd_rn(__fmul_rn(lane_f(cur.a, c), u), lane_f(cur.b, c))
                             : lane_f(cur.cd[g], 32 * h + min(k, 31));
         if (lane == c) st_o = u;
-        if (__builtin_amdgcn_readlane(cur.ovf, c) != 0) {  // serial fallback through the map
-          const float* Ip = I + (size_t)(w * 64 + c) * L * N + n;
-          float wv = u;
-          for (int64_t t0 = 0; t0 < L; t0 += 64) {
-            const float xv = Ip[(size_t)min<int64_t>(t0 + lane, L - 1) * N];
-            const int nt = (int)min<int64_t>(64, L - t0);
-            for (int j = 0; j < nt; ++j) {
-              bool sp;
-              wv = lif_step(wv, lane_f(xv, j), beta, theta, u_r, sp);
-            }
-          }
-          nu = wv;
-        }
+        if (__builtin_amdgcn_readlane(cur.ovf, c) != 0)  // serial fallback through the map
+          nu = wave_serial_rows(I, N, n, (int64_t)(w * 64 + c) * L, L, u, beta, theta, u_r);
         u = nu;
       }
     }
@@ -464,12 +559,12 @@ void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* 
                               int C, int64_t repair, float beta, float theta, float u_r,
                               hipStream_t st);
 
-// Most neurons for the one-wave-per-neuron envelope and super-map walks.
+static int kcap(int k) { return k <= 4 ? 4 : k <= 8 ? 8 : k <= 16 ? 16 : k <= 32 ? 32 : 64; }
+
+// Most neurons for the one-wave-per-neuron envelope walk, composition and super-map carry.
 #ifndef LSH_V4_WAVE_MAX_N
 #define LSH_V4_WAVE_MAX_N 2048
 #endif
-
-static int kcap(int k) { return k <= 4 ? 4 : k <= 8 ? 8 : k <= 16 ? 16 : k <= 32 ? 32 : 64; }
 
 template <int KMAX, int K2MAX>
 static void launch_compose(char* w, const lsh_v4_layout& L, const float* u0, int64_t N, int M2,
@@ -477,6 +572,17 @@ static void launch_compose(char* w, const lsh_v4_layout& L, const float* u0, int
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  if (N <= LSH_V4_WAVE_MAX_N && K2 <= 64 && (int64_t)M2 * NB <= 256) {
+    // few neurons and few super maps (the lane kernel would leave three quarters of the SIMDs
+    // idle): one wave per neuron and SPW super maps, about 2048 waves in all
+    const int SPW = (int)std::max<int64_t>(1, ((int64_t)M2 * N + 2047) / 2048);
+    const int64_t nblk = N * (((int64_t)M2 + SPW - 1) / SPW);
+    hipLaunchKernelGGL(k_lif_compose_wave, dim3((unsigned)nblk), dim3(WAVE), 0, st, F(L.v3.MA),
+                       F(L.v3.MB), Iq(L.v3.MN), Iq(L.v3.OVF), F(L.v3.MX), F(L.v3.MC), F(L.v3.LO),
+                       u0, F(L.SA), F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC),
+                       reinterpret_cast<WsHeader*>(w), N, M2, SPW, G, K, K2, theta, u_r);
+    return;
+  }
   hipLaunchKernelGGL((k_lif_compose<KMAX, K2MAX>), dim3((unsigned)((int64_t)M2 * NB)), dim3(WAVE), 0,
                      st, F(L.v3.MA), F(L.v3.MB), Iq(L.v3.MN), Iq(L.v3.OVF), F(L.v3.MX), F(L.v3.MC),
                      F(L.v3.LO), u0, F(L.SA), F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC),

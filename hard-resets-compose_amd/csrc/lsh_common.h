@@ -54,6 +54,29 @@ __device__ __forceinline__ float lane_f(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// L serial LIF steps of column n from row r0, for a walk with one wave per neuron (every lane
+// holds the same state u): the rows are read 64 at a time, one per lane, the next 64 (index
+// clamped to the last row) while a block is walked, and each step takes its input from its lane.
+// The same step arithmetic as the replay.
+__device__ __forceinline__ float wave_serial_rows(const float* __restrict__ I, int64_t N,
+                                                  int64_t n, int64_t r0, int64_t L, float u,
+                                                  float beta, float theta, float u_r) {
+  const int lane = threadIdx.x & 63;
+  const float* Ip = I + (size_t)r0 * N + n;
+  float xv = Ip[(size_t)min<int64_t>(lane, L - 1) * N];
+  for (int64_t t0 = 0; t0 < L; t0 += 64) {
+    const float xn = Ip[(size_t)min<int64_t>(t0 + 64 + lane, L - 1) * N];
+    const int nt = (int)min<int64_t>(64, L - t0);
+#pragma unroll 8
+    for (int j = 0; j < nt; ++j) {
+      bool s;
+      u = lif_step(u, lane_f(xv, j), beta, theta, u_r, s);
+    }
+    xv = xn;
+  }
+  return u;
+}
+
 // Neuron of workgroup b for kernels with one wave per neuron: eight contiguous ranges, range x
 // on the workgroups b with b % 8 == x.  Consecutive workgroups go to the eight XCDs in turn,
 // so each XCD's L2 then holds the cache lines (32 neurons a line) of its own neurons.

@@ -685,8 +685,8 @@ __device__ __forceinline__ void alif_row_block16(float xb, float& u, float& w, f
 // One chunk's map as the carry reads it (one neuron per 16-lane row, slot s in lane s & 15,
 // register s >> 4): the per-neuron header, every slot below K1 / K2 (the slots past the line
 // and piece counts hold no map; each use is masked by the counts, so their loads need not
-// wait for the header) and the inputs of the chunk's first 128 steps for the serial fallback
-// (lane i of a row: step 16 b + i in xb[b]).
+// wait for the header).  The serial fallback reads its inputs in groups of kCarryXB * 16 steps
+// (lane i of a row: step 16 b + i in register b).
 constexpr int kCarryXB = 8;
 constexpr int kCarryWaves = 4;  // waves per workgroup
 // Neurons per wave: a wave runs the serial fallback when any of its neurons misses, so with
@@ -706,7 +706,6 @@ struct AlifCarryMap {
   int nl, npc, ovf;
   float ls[2], lc[2], lx[2], pl[2], pr[2], pu[2], pa[2], po[2];
   int pw[2];
-  float xb[kCarryXB];
 };
 
 // Verified carry (triton_alif.py:214-252): the first line that fires gives the first spike
@@ -719,11 +718,13 @@ struct AlifCarryMap {
 // loop unrolled by the ring's length so that no set is copied (a copy would wait for the loads
 // into it).  PD = 1 is what runs: on MI355X 2 and 3 were no faster with 1024 neurons (256
 // waves) and slower with 16384 (the extra registers cost waves).  With C a
-// multiple of 16 the fallback takes its inputs
-// from registers by row broadcasts (the inputs past the first 128 steps loaded one group of
-// 128 ahead), else it streams them row by row.  Workgroups of neighbouring neurons go to one
-// XCD (blockIdx b -> group (b % 8) * per + b / 8), so they share its L2 for the inputs and the
-// per-neuron arrays.  The statistics are summed per workgroup before the atomics.
+// multiple of 16 the fallback takes its inputs from registers by row broadcasts (loaded when
+// a fallback starts, each later group of 128 steps while the one before is replayed), else it
+// streams them row by row.  The fallback's first inputs are not part of the ring: loading them
+// with every map cost 8 % to 11 % at 16 to 1024 neurons (N = 16, T = 65536: 0.578 -> 0.516
+// ms) for the 4 % to 30 % of chunks that fall back.  Workgroups of neighbouring neurons go to
+// one XCD (blockIdx b -> group (b % 8) * per + b / 8), so they share its L2 for the inputs and
+// the per-neuron arrays.  The statistics are summed per workgroup before the atomics.
 template <int PD, int NPW>
 __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ w0,
@@ -785,11 +786,6 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
     d.nl = NL[o];
     d.npc = NP[o];
     d.ovf = OVF[o];
-    {
-      const float* xp = I + (size_t)min(m, M - 1) * C * N + nn;
-#pragma unroll
-      for (int b = 0; b < kCarryXB; ++b) d.xb[b] = xp[(size_t)min(16 * b + i, C - 1) * N];
-    }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
       const int sl = min(16 * r + i, K1 - 1), sp = min(16 * r + i, K2 - 1);
@@ -859,14 +855,14 @@ __global__ __launch_bounds__(WAVE * kCarryWaves) void k_alif_carry(
       if (xdpp) {
         // groups of 128 steps; the next group's inputs loaded while one is replayed (every
         // lane runs the steps: the row broadcasts read lanes of rows that may not need them)
+        const float* xp = I + (size_t)m * C * N + nn;
         float xa[kCarryXB];
 #pragma unroll
-        for (int b = 0; b < kCarryXB; ++b) xa[b] = sc.xb[b];
+        for (int b = 0; b < kCarryXB; ++b) xa[b] = xp[(size_t)min(16 * b + i, C - 1) * N];
         for (int g0 = 0; g0 < nb; g0 += kCarryXB) {
           // issued for every group (rows clamped into the chunk, the extra values unused), so
           // the wait for this group's inputs does not cover them
           float xn[kCarryXB];
-          const float* xp = I + (size_t)m * C * N + nn;
 #pragma unroll
           for (int b = 0; b < kCarryXB; ++b)
             xn[b] = xp[(size_t)min(16 * (g0 + kCarryXB + b) + i, C - 1) * N];

@@ -66,11 +66,17 @@ __device__ __forceinline__ float wave_serial_rows(const float* __restrict__ I, i
   float xv = Ip[(size_t)min<int64_t>(lane, L - 1) * N];
   for (int64_t t0 = 0; t0 < L; t0 += 64) {
     const float xn = Ip[(size_t)min<int64_t>(t0 + 64 + lane, L - 1) * N];
-    const int nt = (int)min<int64_t>(64, L - t0);
-#pragma unroll 8
-    for (int j = 0; j < nt; ++j) {
-      bool s;
-      u = lif_step(u, lane_f(xv, j), beta, theta, u_r, s);
+    if (L - t0 >= 64) {
+#pragma unroll 16
+      for (int j = 0; j < 64; ++j) {
+        bool s;
+        u = lif_step(u, lane_f(xv, j), beta, theta, u_r, s);
+      }
+    } else {
+      for (int j = 0; j < (int)(L - t0); ++j) {
+        bool s;
+        u = lif_step(u, lane_f(xv, j), beta, theta, u_r, s);
+      }
     }
     xv = xn;
   }

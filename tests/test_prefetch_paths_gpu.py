@@ -122,3 +122,36 @@ def test_v4_walks_windows_and_fallback(dev, N, K, K2):
         assert st[k] == pytest.approx(sto[k], rel=1e-12), k
     if K2 == 8:
         assert keep["SOVF"].mean() > 0.01
+
+
+@pytest.mark.parametrize("N", [1, 5, 2048])
+def test_wave_walks_neuron_order_edges(dev, N):
+    """The one-wave-per-neuron walks place neurons in eight contiguous ranges (one per XCD);
+    fewer neurons than ranges (1, 5) and the largest count they take (2048) give the oracle's
+    v3 and v4 intermediates and outputs bit for bit."""
+    from lifscan import hip_lif as L
+    C, G, M2, beta = 16, 4, 35, 0.99
+    T = C * G * M2
+    I = normal(T, N, 0.012, 0.08, 61)
+    u0 = uniform(N, 0.0, 1.0, 62)
+    Ig, u0g = gpu(I, dev), gpu(u0, dev)
+    print(f"wave walks neuron order N={N}", flush=True)
+    st, sto, keep = {}, {}, {}
+    U, S = L.scan_forward_v3(Ig, beta, 1.0, 0.0, u0g, C=C, K=8, stats=st)
+    run = L.last_scan_run()
+    Uo, So = O.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=8, stats=sto, keep=keep)
+    assert np.array_equal(host(run.view("LO")), keep["Lo"])
+    assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+    assert np.array_equal(host(run.view("MN", torch.int32)), keep["n"])
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+    assert st["max_pieces"] == sto["max_pieces"]
+    st, sto, keep = {}, {}, {}
+    U, S = L.scan_forward_v4(Ig, beta, 1.0, 0.0, u0g, C=C, G=G, K=8, K2=16, stats=st)
+    run = L.last_scan_run()
+    Uo, So = O.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=C, G=G, K=8, K2=16, stats=sto, keep=keep)
+    assert np.array_equal(host(run.view("SSTARTS")), keep["sstarts"])
+    assert np.array_equal(host(run.view("SN", torch.int32)), keep["SN"])
+    assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+    for k in sto:
+        assert st[k] == pytest.approx(sto[k], rel=1e-12), k

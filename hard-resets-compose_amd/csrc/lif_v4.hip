@@ -452,9 +452,15 @@ __global__ __launch_bounds__(64) void k_lif_env_lo_wave(const float* __restrict_
     load(min(w + 1, NW - 1), c1, a1, b1);
     const int nc = min(64, M - w * 64);
     float lo_o = 0.0f;
-    for (int c = 0; c < nc; ++c) {
+    auto step = [&](int c) {
       if (lane == c) lo_o = l - margin * (fabsf(l) + 1.0f);
       l = fminf(lane_f(c0, c), __fadd_rn(__fmul_rn(lane_f(a0, c), l), lane_f(b0, c)));
+    };
+    if (nc == 64) {  // a full window, unrolled so that the lane reads run ahead of the chain
+#pragma unroll 16
+      for (int c = 0; c < 64; ++c) step(c);
+    } else {
+      for (int c = 0; c < nc; ++c) step(c);
     }
     if (lane < nc) LO[(size_t)(w * 64 + lane) * N + n] = lo_o;
     c0 = c1;

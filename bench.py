@@ -742,8 +742,10 @@ def counters_workload(torch, dev):
     (k_lif_build<8,8>, k_lif_carry<8>); at cfg4: the converged forward (k_lif_fwd_warm,
     k_lif_repair_wide), the long-chunk map scan in pieces (k_lif_build<32,8>,
     k_lif_carry_staged<32>) and with the associative carry (k_map_scan), v4 at C 2048 / G 4 /
-    K 32 / K2 64 and at the reference default (k_lif_compose, k_map_carry) and the look-back
-    adjoint (k_lif_bwd_lookback<16,16,...>)."""
+    K 32 / K2 64 and at the reference default (k_lif_compose, k_map_carry; with 1024 neurons the
+    one-wave-per-neuron walks k_lif_env_lo_wave, k_map_carry_wave) and the look-back adjoint
+    (k_lif_bwd_lookback<16,16,...>); with few neurons (N = 128, T = 65536): the map scan at C 256,
+    K 16 (k_lif_carry_wave) and v4 at C 128, G 8 (k_lif_compose_wave)."""
     from lifscan import hip_lif as L
     from lifscan import triton_alif as A
     x = torch.empty(64 * 2 ** 20, device=dev)
@@ -782,6 +784,15 @@ def counters_workload(torch, dev):
         torch.cuda.synchronize()
     gS = torch.randn(T, N, generator=torch.Generator().manual_seed(1)).to(dev)
     L.scan_backward_tiled(I, u0, U, S, gS, None, 0.99, 1.0, 0.0, 4.0)
+    torch.cuda.synchronize()
+    del I, U, S, gS
+    torch.cuda.empty_cache()
+    log("counters: few neurons")
+    T, N = 65536, 128
+    I = (0.15 + 0.4 * torch.randn(T, N, generator=torch.Generator().manual_seed(0))).to(dev)
+    u0 = torch.zeros(N, device=dev)
+    L.scan_forward_mapscan(I, 0.99, 1.0, 0.0, u0, C=256, K=16, repair=0)
+    L.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=128, G=8, K=16, K2=32, repair=0)
     torch.cuda.synchronize()
     print(json.dumps({"counters_workload": True}))
 

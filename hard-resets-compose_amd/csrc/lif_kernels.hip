@@ -972,12 +972,13 @@ static void launch_carry(const float* I, const float* u0, const float* lo_neuron
 // Most neurons for the one-wave-per-neuron carry.  Measured on MI355X, the map scan (build,
 // carry, replay; x ~ N(0.15, 0.4^2), beta 0.99, C 256, K 16) against the staged carry: N = 128,
 // T = 65536 0.47 -> 0.22 ms; N = 1024, T = 65536 0.70 -> 0.50 ms; N = 2048, T = 65536 1.04 ->
-// 0.90 ms (T = 16384: 0.29 -> 0.32); N = 4096, T = 65536 1.69 -> 2.01 ms (K 8, with 3 %
-// overflowed chunks: 3.68 -> 1.95 ms); N = 16384, T = 16384 1.48 -> 2.29.
+// 0.90 ms; N = 2048, T = 16384 0.29 -> 0.32 ms at C 256 (64 chunks) but 0.36 -> 0.33 ms at C 128
+// (128 chunks), so above 1024 neurons it takes 128 chunks or more; N = 4096, T = 65536 1.69 ->
+// 2.01 ms (K 8, with 3 % overflowed chunks: 3.68 -> 1.95 ms); N = 16384, T = 16384 1.48 -> 2.29.
 #ifndef LSH_LIF_CARRY_WAVE_MAX_N
 #define LSH_LIF_CARRY_WAVE_MAX_N 2048
 #endif
-  if (KMAX <= 16 && N <= LSH_LIF_CARRY_WAVE_MAX_N) {
+  if (KMAX <= 16 && N <= LSH_LIF_CARRY_WAVE_MAX_N && (N <= 1024 || M >= 128)) {
     // few neurons: one wave per neuron
     hipLaunchKernelGGL(k_lif_carry_wave, dim3((unsigned)N), dim3(WAVE), 0, st, I, u0, F(L.EC),
                        F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),

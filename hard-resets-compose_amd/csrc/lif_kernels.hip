@@ -454,20 +454,23 @@ __global__ __launch_bounds__(64) void k_lif_carry(
 // The same carry with one wave per neuron, for few neurons (where one lane per neuron leaves
 // one or two waves on the chip to walk every chunk with a memory latency each).  The chunks go
 // in windows of 64: lane j holds the scalars (envelope map, A, B, count, raw overflow) of the
-// window's chunk j, and VGPR g holds the maps of its chunks 4g..4g+3, lane 16r + s the
-// breakpoint and constant of slot s of chunk 4g + r (K <= 16).  The next window's loads are
-// issued, unconditionally with clamped indices, before the current one is walked, so the walk
-// waits on memory once per 64 chunks.  Per chunk, the counts #{xd > lo} and #{xd > u} are
-// ballots over the chunk's 16-lane row, the constant is read from lane 16r + k, and the four
+// window's chunk j, and a map takes a row of RW lanes (RW = 16 for K <= 16, 32 for K <= 32):
+// VGPR g holds chunks (64/RW)g + r, lane RW*r + s the breakpoint and constant of slot s of
+// chunk (64/RW)g + r.  The next window's loads are issued, unconditionally with clamped
+// indices, before the current one is walked, so the walk waits on memory once per 64 chunks.
+// Per chunk, the counts #{xd > lo} and #{xd > u} are ballots over the chunk's row, the
+// constant is read from lane RW*r + k, and the four
 // per-chunk outputs collect in lane c, stored once per window.  The overflow fallback reads
 // 64 steps at a time, one per lane, and walks them with lane reads.  Results are the same as
 // k_lif_carry's: the same operations on the same values, only distributed over lanes.
+template <int RW>
 struct LifCarryWindow {
   float ec, ea, eb, ma, mb;  // lane j: chunk j of the window
   int cnt, ovfr;
-  float xd[16], cd[16];  // VGPR g, lane 16r + s: slot s of chunk 4g + r
+  float xd[RW], cd[RW];  // VGPR g, lane RW*r + s: slot s of chunk (64/RW)*g + r
 };
 
+template <int RW>
 __global__ __launch_bounds__(64) void k_lif_carry_wave(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ EC,
     const float* __restrict__ EA, const float* __restrict__ EB, const float* __restrict__ MA,
@@ -478,9 +481,10 @@ __global__ __launch_bounds__(64) void k_lif_carry_wave(
     int K, float beta, float theta, float u_r) {
   const int64_t n = xcd_neuron(blockIdx.x, N);
   const int lane = threadIdx.x;
-  const int row = lane >> 4, slot = lane & 15;
+  constexpr int CPV = 64 / RW;  // chunks per VGPR
+  const int row = lane / RW, slot = lane % RW;
   const int sl = min(slot, K - 1);
-  auto load = [&](int w, LifCarryWindow& d) {
+  auto load = [&](int w, LifCarryWindow<RW>& d) {
     const size_t o = (size_t)min(w * 64 + lane, M - 1) * N + n;
     d.ec = EC[o];
     d.ea = EA[o];
@@ -490,8 +494,8 @@ __global__ __launch_bounds__(64) void k_lif_carry_wave(
     d.cnt = CNT[o];
     d.ovfr = OVFRAW[o];
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      const size_t os = ((size_t)min(w * 64 + 4 * g + row, M - 1) * K + sl) * N + n;
+    for (int g = 0; g < RW; ++g) {
+      const size_t os = ((size_t)min(w * 64 + CPV * g + row, M - 1) * K + sl) * N + n;
       d.xd[g] = MX[os];
       d.cd[g] = MC[os];
     }
@@ -503,7 +507,7 @@ __global__ __launch_bounds__(64) void k_lif_carry_wave(
   unsigned long long ovf_acc = 0, pcs_acc = 0;
   int pmax = 0;
   const int NW = (M + 63) / 64;
-  LifCarryWindow cur, nxt;
+  LifCarryWindow<RW> cur, nxt;
   load(0, cur);
   for (int w = 0; w < NW; ++w) {
     load(min(w + 1, NW - 1), nxt);
@@ -511,9 +515,9 @@ __global__ __launch_bounds__(64) void k_lif_carry_wave(
     float lo_o = 0.0f, st_o = 0.0f;
     int mn_o = 0, ovf_o = 0;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) {
-      for (int r = 0; r < 4; ++r) {
-        const int c = 4 * g + r;
+    for (int g = 0; g < RW; ++g) {
+      for (int r = 0; r < CPV; ++r) {
+        const int c = CPV * g + r;
         if (c >= nc) break;
         const float ec = lane_f(cur.ec, c), ea = lane_f(cur.ea, c), eb = lane_f(cur.eb, c);
         const int cnt = __builtin_amdgcn_readlane(cur.cnt, c);
@@ -525,7 +529,7 @@ __global__ __launch_bounds__(64) void k_lif_carry_wave(
         const int ne = min(cnt, gt + 1);
         const bool ovf = ovfr && gt == cnt;
         const int k = __popcll(__ballot(in_row && slot < ne && cur.xd[g] > u));
-        const float cval = lane_f(cur.cd[g], 16 * r + min(k, 15));
+        const float cval = lane_f(cur.cd[g], RW * r + min(k, RW - 1));
         float nu = (k == ne)
                        ? __fadd_rn(__fmul_rn(lane_f(cur.ma, c), u), lane_f(cur.mb, c))
                        : cval;
@@ -978,9 +982,9 @@ static void launch_carry(const float* I, const float* u0, const float* lo_neuron
 #ifndef LSH_LIF_CARRY_WAVE_MAX_N
 #define LSH_LIF_CARRY_WAVE_MAX_N 2048
 #endif
-  if (KMAX <= 16 && N <= LSH_LIF_CARRY_WAVE_MAX_N && (N <= 1024 || M >= 128)) {
-    // few neurons: one wave per neuron
-    hipLaunchKernelGGL(k_lif_carry_wave, dim3((unsigned)N), dim3(WAVE), 0, st, I, u0, F(L.EC),
+  if (KMAX <= 32 && N <= LSH_LIF_CARRY_WAVE_MAX_N && (N <= 1024 || M >= 128)) {
+    // few neurons: one wave per neuron, a chunk map on a row of 16 lanes (K <= 16) or 32
+    hipLaunchKernelGGL((k_lif_carry_wave<KMAX <= 16 ? 16 : 32>), dim3((unsigned)N), dim3(WAVE), 0, st, I, u0, F(L.EC),
                        F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
                        F(L.MC), lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS),
                        reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r);

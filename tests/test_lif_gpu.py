@@ -106,9 +106,11 @@ def test_scan_v3_matches_oracle(L, dev, beta, mu, sd):
 
 @pytest.mark.parametrize("K", [4, 8, 16, 32])
 def test_scan_v3_long_sequence_staged_carry(L, dev, K):
-    """Many chunks per neuron (M = 1024): the carry stages its map reads through LDS
-    (k_lif_carry_staged); LO, starts, kept pieces, overflow flags and outputs equal the
-    oracle's bit for bit, including overflowed chunks (K = 4 at beta = 0.99)."""
+    """Many chunks per neuron (M = 1024) with few neurons (N = 130: the carry takes one wave per
+    neuron, a chunk map on a row of 16 or 32 lanes); LO, starts, kept pieces, overflow flags and
+    outputs equal the oracle's bit for bit, including overflowed chunks (K = 4 at beta = 0.99).
+    The staged carry (maps through LDS, above 2048 neurons) is pinned by
+    test_v3_carry_windows_and_fallback."""
     T, N, C, beta = 16384, 130, 16, 0.99
     I = normal(T, N, 0.012, 0.08, 21)
     u0 = uniform(N, 0.0, 1.0, 22)

@@ -68,7 +68,7 @@ def test_converged_v3_few_neurons_short_warm_chunks(dev, beta):
     assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
 
 
-@pytest.mark.parametrize("N,K", [(70, 1), (70, 4), (70, 16), (2113, 8), (2113, 16)])
+@pytest.mark.parametrize("N,K", [(70, 1), (70, 4), (70, 16), (70, 32), (2113, 8), (2113, 16), (2113, 32)])
 def test_v3_carry_windows_and_fallback(dev, N, K):
     """The carry at few neurons (one wave per neuron, chunks in windows of 64) and just above
     them (one lane per neuron, maps staged through LDS): M = 150 chunks (two windows and a

@@ -4,7 +4,9 @@ the C ABI.
 Bars: U, W, S bit-exact for serial, replay and the repaired box scan; every intermediate of the
 box scan (entry box, chunk maps, carried chunk states, miss flags) bit-exact at the same block
 size of the split decision; the adjoint within 1e-5 relative of the fp32 oracle and 1e-4 of the
-fp64 adjoint; parameter gradients within 1e-4 of the fp64 assembly.
+fp64 adjoint; the four parameter gradients (dbeta, drho, dq, dtheta0) within 1e-4 of the fp64
+assembly, or within 4x the error that the same fp64 assembly makes from the fp32 oracle's adjoint
+where that floor is above 2.5e-5 (param_bars).
 """
 import math
 
@@ -24,6 +26,29 @@ def rel(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def param_bars(x, U, W, S, G, beta, rho, q, u0, w0, want, theta0=1.0):
+    """Bars for the four parameter gradients (dbeta, drho, dq, dtheta0) against their fp64 assembly
+    `want[3:7]`: 1e-4 relative (the north star's gradient bar), raised to 4x the fp32 floor where
+    that is higher.  The floor is the error of the same fp64 assembly applied to the fp32 oracle's
+    adjoint: dtheta0 = -sum sg (gS + q LW) cancels to about 1e-3 of its terms at some shapes
+    (5e-4 of fp64 at T 1024, N 96), which no fp32 adjoint can beat.  Prints both."""
+    LV, LW = A.backward(x, U, W, S, G, beta, rho, q, theta0, u0, w0, 4.0)
+    f32 = A.param_grads(x, U, W, S, G, LV.astype(np.float64), LW.astype(np.float64), beta, rho, q,
+                        theta0, u0, w0, 4.0)
+    floors = [rel(f32[k], want[k]) for k in range(3, 7)]
+    return [max(1e-4, 4 * f) for f in floors], floors
+
+
+def check_params(got, want, bars, floors, label=""):
+    """got: (dbeta, drho, dq, dtheta0) as arrays or scalars; want[3:7] their fp64 assembly."""
+    errs = [rel(g, want[3 + k]) for k, g in enumerate(got)]
+    print(f"  {label} parameter grads rel err " + ", ".join(
+        f"{n}={e:.2e} (fp32 floor {f:.2e})" for n, e, f in zip(("dbeta", "drho", "dq", "dtheta0"), errs, floors)),
+        flush=True)
+    for k, (e, b) in enumerate(zip(errs, bars)):
+        assert e < b, (k, e, b)
 
 
 def _inputs(beta, mfree, T, N, seed):
@@ -319,7 +344,7 @@ def test_alif_backward_rejects(AL, dev):
 def test_alif_layer_gradients(AL, dev, fwd, bwd, beta, rho, q, T, N):
     """alif() gradients for I, u0, w0 and the four parameters against the fp64 adjoint and
     ALIFFn's assembly (triton_alif.py:541-554); the second case is the reference's own
-    (tests/test_alif_grad.py:8-36, bar 1e-3 there, 1e-4 here)."""
+    (tests/test_alif_grad.py:8-36, bar 1e-3 there; param_bars here)."""
     C = 128
     x = _inputs(beta, 2.0, T, N, 19)
     G = normal(T, N, 0.0, 1.0, 20)
@@ -341,11 +366,10 @@ def test_alif_layer_gradients(AL, dev, fwd, bwd, beta, rho, q, T, N):
     LV6, LW6 = A.backward(x, U, W, S, G, beta, rho, q, 1.0, u0, w0, 4.0, dtype=np.float64)
     want = A.param_grads(x, U, W, S, G, LV6, LW6, beta, rho, q, 1.0, u0, w0, 4.0)
     got = (xg.grad, ug.grad, wg.grad, *(p.grad for p in ps))
-    for k, (a, b) in enumerate(zip(got, want)):
-        # tensors at the north-star 1e-4; the four parameter gradients are sums over T*N terms
-        # that cancel to a few 1e-3 of their magnitude (dtheta0 most), so they get the
-        # reference's own bar, 1e-3 (tests/test_alif_grad.py:34)
-        assert rel(host(a), b) < (1e-4 if k < 3 else 1e-3), k
+    for k, (a, b) in enumerate(zip(got[:3], want[:3])):
+        assert rel(host(a), b) < 1e-4, k
+    bars, floors = param_bars(x, U, W, S, G, beta, rho, q, u0, w0, want)
+    check_params([host(p) for p in got[3:]], want, bars, floors, f"layer {fwd}/{bwd}")
 
 
 @pytest.mark.parametrize("mode,C", [("serial", 64), ("chunked", 64), ("fused", 16), ("fused", 32),
@@ -382,8 +406,8 @@ def test_alif_backward_param_sums_and_dw0(AL, dev, mode, C, T, N):
     want = A.param_grads(x, U, W, S, G, LV6, LW6, beta, rho, q, 1.0, u0, w0, 4.0)
     assert rel(host(DW0), want[2]) < 1e-4
     got = host(sums)
-    for k, w in enumerate((want[3], want[4], want[5], -want[6])):
-        assert rel(got[k], w) < 1e-3, k
+    bars, floors = param_bars(x, U, W, S, G, beta, rho, q, u0, w0, want)
+    check_params([got[0], got[1], got[2], -got[3]], want, bars, floors, f"sums T={T} N={N}")
 
 
 @pytest.mark.parametrize("mode,C", [("serial", 64), ("chunked", 64), ("fused", 16), ("fused", 32)])
@@ -505,8 +529,8 @@ def test_alif_layer_recompute_equals_stored(AL, dev, monkeypatch):
 def test_alif_serial_bwd_pipe(AL, dev, T, N):
     """The producer/consumer serial adjoint (mode 0; full and partial tiles, ragged neuron blocks):
     LV, LW and dL/dw0 within 1e-5 of the fp32 oracle and 1e-4 of the fp64 adjoint, the parameter
-    sums within 1e-3 of their fp64 assembly (the reference's bar for these cancelling sums,
-    tests/test_alif_grad.py:34); alif_backward(mode="serial") gives the same bits."""
+    sums within param_bars of their fp64 assembly; alif_backward(mode="serial") gives the same
+    bits."""
     from lifscan import hip_alif
     beta, rho, q = 0.95, 0.995, 0.9
     x = _inputs(beta, 2.0, T, N, 51)
@@ -528,8 +552,8 @@ def test_alif_serial_bwd_pipe(AL, dev, T, N):
     want = A.param_grads(x, U, W, S, G, LV6, LW6, beta, rho, q, 1.0, u0, w0, 4.0)
     assert rel(host(DW0), want[2]) < 1e-4
     got = host(sums)
-    for k, w in enumerate((want[3], want[4], want[5], -want[6])):
-        assert rel(got[k], w) < 1e-3, k
+    bars, floors = param_bars(x, U, W, S, G, beta, rho, q, u0, w0, want)
+    check_params([got[0], got[1], got[2], -got[3]], want, bars, floors, f"sums T={T} N={N}")
 
 
 @pytest.mark.parametrize("T,N", [(1, 1), (63, 64), (64, 100), (65, 7), (1000, 130), (4113, 1029)])
@@ -582,8 +606,8 @@ def test_alif_lookback_bwd(AL, dev, T, N):
     want = A.param_grads(x, U, W, S, G, LV6, LW6, beta, rho, q, 1.0, u0, w0, 4.0)
     assert rel(host(DW0), want[2]) < 1e-4
     got_s = host(sums)
-    for k, w in enumerate((want[3], want[4], want[5], -want[6])):
-        assert rel(got_s[k], w) < 1e-3, k
+    bars, floors = param_bars(x, U, W, S, G, beta, rho, q, u0, w0, want)
+    check_params([got_s[0], got_s[1], got_s[2], -got_s[3]], want, bars, floors, f"lookback T={T} N={N}")
 
 
 @pytest.mark.parametrize("T,N,u_r", [(1280, 130, 0.0), (512, 33, -0.2)])

@@ -5,8 +5,8 @@ The serial kernels these are compared with are pinned to the oracle bit for bit 
 test_lif_gpu.py / test_alif_gpu.py; here every config is also checked against the oracle
 itself where it finishes in seconds (a column subset for cfg4's 2^20 steps, all of cfg5).
 Bars: spikes and potentials bit-exact; gradients 1e-5 of the fp32 oracle and 1e-4 of fp64;
-ALIF's four parameter gradients 1e-3 (sums that cancel; the reference's bar,
-tests/test_alif_grad.py:34).
+ALIF's four parameter gradients 1e-4 of their fp64 assembly (the north star's bar; the fp32
+arithmetic floor at cfg5 is about 2e-6).
 """
 import numpy as np
 import pytest
@@ -139,7 +139,7 @@ def test_cfg5_alif_layer_gradients(dev):
     """cfg5 (ALIF, N = 16,384, T = 4,096, beta .95, rho .995, q .2, x ~ N(0.15, 0.3^2), u0 = w0 = 0):
     alif() with the serial forward and the scan adjoint (its default), parameters as 0-d tensors;
     U, W, S equal the oracle, gradients for I, u0, w0 against the fp64 adjoint (1e-4) and for
-    beta, rho, q, theta0 against ALIFFn's fp64 assembly (1e-3)."""
+    beta, rho, q, theta0 against ALIFFn's fp64 assembly (1e-4)."""
     from lifscan import triton_alif as AL
     c = CFG5
     I, z = _cfg5_inputs(dev)
@@ -159,8 +159,11 @@ def test_cfg5_alif_layer_gradients(dev):
                           dtype=np.float64)
     want = A.param_grads(x, Uo, Wo, So, Gh, LV6, LW6, c["beta"], c["rho"], c["q"], 1.0, zh, zh, 4.0)
     got = (xg.grad, ug.grad, wg.grad, *(p.grad for p in ps))
-    for k, (a, b) in enumerate(zip(got, want)):
-        assert rel(host(a), b) < (1e-4 if k < 3 else 1e-3), k
+    errs = [rel(host(a), b) for a, b in zip(got, want)]
+    print("  cfg5 gradient rel errs dI, du0, dw0, dbeta, drho, dq, dtheta0: "
+          + ", ".join(f"{e:.2e}" for e in errs), flush=True)
+    for k, e in enumerate(errs):
+        assert e < 1e-4, k
     del I, G, xg, S, U, W
     torch.cuda.empty_cache()
 

@@ -105,16 +105,16 @@ def test_scan_v3_matches_oracle(L, dev, beta, mu, sd):
 
 
 @pytest.mark.parametrize("K", [4, 8, 16, 32])
-def test_scan_v3_long_sequence_staged_carry(L, dev, K):
+def test_scan_v3_long_sequence_wave_carry(L, dev, K):
     """Many chunks per neuron (M = 1024) with few neurons (N = 130: the carry takes one wave per
     neuron, a chunk map on a row of 16 or 32 lanes); LO, starts, kept pieces, overflow flags and
     outputs equal the oracle's bit for bit, including overflowed chunks (K = 4 at beta = 0.99).
     The staged carry (maps through LDS, above 2048 neurons) is pinned by
-    test_v3_carry_windows_and_fallback."""
+    test_v3_carry_windows_and_fallback at N = 2113, K 1 to 32."""
     T, N, C, beta = 16384, 130, 16, 0.99
     I = normal(T, N, 0.012, 0.08, 21)
     u0 = uniform(N, 0.0, 1.0, 22)
-    print(f"v3 staged carry K={K}", flush=True)
+    print(f"v3 long-sequence wave carry K={K}", flush=True)
     st, sto, keep = {}, {}, {}
     U, S = L.scan_forward_v3(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=C, K=K, stats=st)
     run = L.last_scan_run()
@@ -352,7 +352,7 @@ def test_cfg2_scan_equals_serial_full_size(L, dev):
         I = (mu + sd * torch.randn(T, N, generator=g)).to(dev)
         u0 = torch.zeros(N, device=dev)
         Us, Ss = L.serial_forward(I, beta, 1.0, 0.0, u0)
-        for C in (32, 128):
+        for C in (32, 64, 128):
             st = {}
             U, S = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=8, repair=10 ** 6, stats=st)
             assert torch.equal(U, Us) and torch.equal(S, Ss)

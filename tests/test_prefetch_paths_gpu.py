@@ -68,7 +68,8 @@ def test_converged_v3_few_neurons_short_warm_chunks(dev, beta):
     assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
 
 
-@pytest.mark.parametrize("N,K", [(70, 1), (70, 4), (70, 16), (70, 32), (2113, 8), (2113, 16), (2113, 32)])
+@pytest.mark.parametrize("N,K", [(70, 1), (70, 4), (70, 16), (70, 32), (2113, 1), (2113, 4), (2113, 8),
+                                 (2113, 16), (2113, 32)])
 def test_v3_carry_windows_and_fallback(dev, N, K):
     """The carry at few neurons (one wave per neuron, chunks in windows of 64) and just above
     them (one lane per neuron, maps staged through LDS): M = 150 chunks (two windows and a
@@ -95,6 +96,35 @@ def test_v3_carry_windows_and_fallback(dev, N, K):
     assert st["max_pieces"] == sto["max_pieces"]
     if K <= 4:
         assert sto["overflow_frac"] > 0.01
+
+
+@pytest.mark.parametrize("C,K", [(512, 32), (256, 32), (512, 16)])
+def test_v3_wave_carry_full_rows_and_overflow(dev, C, K):
+    """The one-wave-per-neuron carry on long chunks whose maps fill their row: x ~ N(0.012, 0.02^2)
+    at beta 0.99 keeps 28 pieces a chunk on average at K 32 and overflows 28% of the chunks, so
+    full 32-lane rows (33 pieces), the min(k, row width - 1) clamp and the overflow fallback over
+    C rows all run.  LO, starts, kept counts, overflow flags, U, S and the stats equal the
+    oracle's bit for bit."""
+    from lifscan import hip_lif as L
+    N, beta = 70, 0.99
+    T = 8192
+    I = normal(T, N, 0.012, 0.02, 61)
+    u0 = uniform(N, 0.0, 1.0, 62)
+    print(f"v3 wave carry full rows C={C} K={K}", flush=True)
+    st, sto, keep = {}, {}, {}
+    U, S = L.scan_forward_v3(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=C, K=K, stats=st)
+    run = L.last_scan_run()
+    Uo, So = O.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, stats=sto, keep=keep)
+    assert np.array_equal(host(run.view("LO")), keep["Lo"])
+    assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+    assert np.array_equal(host(run.view("MN", torch.int32)), keep["n"])
+    assert np.array_equal(host(run.view("OVF", torch.int32)), keep["ovf"])
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+    assert st["overflow_frac"] == pytest.approx(sto["overflow_frac"], abs=0)
+    assert st["mean_pieces"] == pytest.approx(sto["mean_pieces"], rel=1e-12)
+    assert st["max_pieces"] == sto["max_pieces"] == K + 1
+    assert sto["overflow_frac"] > 0.05
+    print(f"  stats {st}", flush=True)
 
 
 @pytest.mark.parametrize("N,K,K2", [(70, 4, 8), (70, 16, 32), (2113, 4, 8)])

@@ -90,3 +90,42 @@ def test_noalloc_near_the_limit(dev):
         assert torch.equal(got, ref), (T, N)
         del I, GS, U, S, got, ref, args
         torch.cuda.empty_cache()
+
+
+def test_noalloc_lookback_graph_replays(dev):
+    """The entry point that allocates nothing, captured in a HIP graph (torch.cuda.CUDAGraph) and
+    replayed three times with eager calls and synchronizations between the replays: every replay
+    gives the workspace entry point's Lam bit for bit.  The capture holds only kernel nodes: the
+    flags and the header of the static array are cleared by a kernel at every call, and the
+    array's address was taken by an eager call before the capture."""
+    from lifscan import _native as nat
+    lib = nat.lib()
+    T, N, C, beta = 8192, 300, 16, 0.95
+    h, args = _case(T, N, 91, False, dev)
+    ref = _call("workspace", args, T, N, beta, True, C)
+    I, u0, U, S, GS, GU = args
+    Lam = torch.empty_like(I)
+    p = [nat.ptr(t) for t in (I, u0, U, S, GS, GU, Lam)]
+    print(f"noalloc lookback graph capture T={T} N={N}", flush=True)
+
+    def launch():
+        nat.check(lib.lsh_lif_scan_lookback_bwd_noalloc(*p, T, N, beta, 1.0, -0.1, 4.0, 1, C,
+                                                        nat.stream_of(I)), "noalloc")
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert torch.equal(Lam, ref)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch()
+    for r in range(3):
+        Lam.fill_(-1.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(Lam, ref), r
+        eager = _call("noalloc", args, T, N, beta, True, C)
+        assert torch.equal(eager, ref), r

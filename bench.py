@@ -102,6 +102,104 @@ def bb_time(fn, reps, groups=5, warm=2, warm_s=0.0):
     return statistics.median(ts)
 
 
+_SCRUB = []
+
+
+def scrub():
+    """Read and write 1 GiB (four times MI355X's 256 MB Infinity Cache), so that the next call
+    finds none of its operands in that cache: its reads come from HBM."""
+    import torch
+    if not _SCRUB:
+        _SCRUB.append(torch.zeros(256 * 2 ** 20, device="cuda"))
+    _SCRUB[0].add_(1.0)
+
+
+def ev_time_cold(fn, reps, warm=1):
+    """Median ms of fn() over reps with HIP events, each call after scrub() (outside the events):
+    the cache-cold time, as a call on operands last touched long ago would see."""
+    import torch
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        scrub()
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b))
+    return statistics.median(ts)
+
+
+def hbm_ceilings(torch, dev):
+    """This box's own HBM ceilings on 1 GiB arrays (cache-cold, HIP events, median of 5): a copy
+    (read 1 GiB, write 1 GiB) and a fill (write 1 GiB), in GB/s.  No kernel of this build is
+    credited above them."""
+    x = torch.empty(256 * 2 ** 20, device=dev)
+    y = torch.empty_like(x)
+    nb = 4 * x.numel()
+    t_copy = ev_time_cold(lambda: y.copy_(x), 5)
+    t_fill = ev_time_cold(lambda: y.fill_(1.0), 5)
+    del x, y
+    torch.cuda.empty_cache()
+    return {"copy_GBps": round(2 * nb / (t_copy / 1000.0) / 1e9, 1),
+            "fill_GBps": round(nb / (t_fill / 1000.0) / 1e9, 1), "bytes": nb}
+
+
+def bench_auto_grid(torch, dev, reps=15):
+    """The reference's lif_auto grid (experiments/e11_auto.py:16-41; results/e11_auto.json): one
+    LIF layer's forward + backward through autograd with library defaults at N in {128, 1024,
+    8192, 32768, 131072} x T in {1024, 4096, 16384, 65536}, N*T <= 2^28, x ~ N(0.15, 0.4^2),
+    beta 0.9, u0 = 0, G ~ N(0, 1): lif_tuned(mode="serial"), lif_tuned(mode="scan", repair=0)
+    and lif_auto, HIP events, median.  Per cell: the three times, auto's modes, whether the
+    spikes of all three are equal and auto's gradient against serial's; auto_vs_best = auto's
+    time over the faster of the two modes."""
+    from lifscan import hip_lif as L
+    rows = []
+    for N in (128, 1024, 8192, 32768, 131072):
+        for T in (1024, 4096, 16384, 65536):
+            if N * T > 2 ** 28:
+                continue
+            g = torch.Generator().manual_seed(0)
+            I0 = (0.15 + 0.4 * torch.randn(T, N, generator=g)).to(dev)
+            G = torch.randn(T, N, generator=torch.Generator().manual_seed(1)).to(dev)
+            u0 = torch.zeros(N, device=dev)
+            fns = {"serial": lambda I: L.lif_tuned(I, u0, beta=0.9, mode="serial"),
+                   "scan": lambda I: L.lif_tuned(I, u0, beta=0.9, mode="scan", repair=0),
+                   "auto": lambda I: L.lif_auto(I, u0, beta=0.9)}
+            res = {}
+            for name, f in fns.items():
+                I = I0.clone().requires_grad_(True)
+
+                def step():
+                    I.grad = None
+                    f(I).backward(G)
+                t = ev_time(step, reps, warm=2)
+                I.grad = None
+                s = f(I)
+                s.backward(G)
+                res[name] = (t, s.detach(), I.grad.clone())
+                del I
+            gs = res["serial"][2]
+            best = min(res["serial"][0], res["scan"][0])
+            rows.append({"N": N, "T": T, "modes": list(L.auto_modes(N, T)),
+                         **{k: round(res[k][0], 4) for k in fns},
+                         "spikes_equal": all(torch.equal(res[k][1], res["serial"][1]) for k in ("scan", "auto")),
+                         "grad_rel_auto": float((res["auto"][2] - gs).norm() / gs.norm()),
+                         "auto_vs_best": round(res["auto"][0] / best, 3),
+                         "x_auto_vs_serial": round(res["serial"][0] / res["auto"][0], 3)})
+            del I0, G, res, gs
+            torch.cuda.empty_cache()
+    worst = max(r["auto_vs_best"] for r in rows)
+    return {"cells": rows, "worst_auto_vs_best": worst,
+            "cells_within_5pct": sum(r["auto_vs_best"] <= 1.05 for r in rows), "n_cells": len(rows),
+            "all_spikes_equal": all(r["spikes_equal"] for r in rows),
+            "max_grad_rel_auto": max(r["grad_rel_auto"] for r in rows)}
+
+
 def profiled_traffic():
     """HBM bytes per launch of the dominant kernel from the committed counter summary
     (two rocprofv3 --pmc passes, FETCH_SIZE and WRITE_SIZE, scaled on a copy kernel)."""
@@ -338,6 +436,9 @@ def bench_cfg3(torch, dev, reps):
     # synchronizations, the host's launch latency included)
     out["lif_layers_fwd_bwd_ms"] = bb_time(layers, max(reps, 10), warm=2, warm_s=0.5)
     out["lif_layers_fwd_bwd_per_call_ms"] = ev_time(layers, max(reps, 10), warm=2)
+    # cache-cold: each layer's arrays are 64 MiB, within the 256 MB Infinity Cache when called
+    # back to back; after a 1 GiB scrub the operands come from HBM
+    out["lif_layers_fwd_bwd_cold_ms"] = ev_time_cold(layers, max(reps, 10), warm=2)
     # lif_tuned runs its recomputing pair from the C++ autograd function (lifscan/_ops.cpp);
     # the same kernels through the Python autograd function, for the host cost it removes
     out["lif_tuned_host_path"] = "c++" if L._rc_path(I1, torch.zeros(I1.shape[1], device=dev), 0.95,
@@ -365,6 +466,8 @@ def bench_cfg3(torch, dev, reps):
     out["lif_layers_bytes_per_neuron_step"] = nbytes
     out["lif_layers_pct_roofline"] = round(
         100 * nbytes * nsteps / (out["lif_layers_fwd_bwd_ms"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
+    out["lif_layers_pct_roofline_cold"] = round(
+        100 * nbytes * nsteps / (out["lif_layers_fwd_bwd_cold_ms"] / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
     out["config"] = "700-256-256-20, B=64, T=1024, beta=0.95, lif_tuned(scan, K=16, repair on)"
     return {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out.items()}
 
@@ -517,7 +620,12 @@ def bench_cfg5(torch, dev, reps):
         # back to back as the headline's step loop; per call: one step between two synchronizations
         out[f"alif_fwd_{fwd}_bwd_scan_ms"] = bb_time(step, reps, warm=2)
         out[f"alif_fwd_{fwd}_bwd_scan_per_call_ms"] = ev_time(step, reps, warm=1)
+        # cache-cold: cfg5's arrays are 256 MiB each, so back-to-back calls find part of their
+        # operands in the 256 MB Infinity Cache; after a 1 GiB scrub they read HBM
+        out[f"alif_fwd_{fwd}_bwd_scan_cold_ms"] = ev_time_cold(step, reps)
     out["serial_fwd_ms"] = ev_time(lambda: A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z), reps)
+    out["serial_fwd_cold_ms"] = ev_time_cold(lambda: A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z),
+                                             reps)
     U, W, S = A.alif_serial_forward(I, beta, rho, q, 1.0, 0.0, z, z)
     # Two predictions of the chunk-entry adaptation (experiments/e25d_alif_fwd.py:44-50): the
     # warm-up predictor, and the previous fitting iterate emulated by a 1.005x input.
@@ -530,10 +638,11 @@ def bench_cfg5(torch, dev, reps):
             st, ph = {}, {}
             U2, W2, S2 = A.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, WP, dwq * q, C=C, K1=32, K2=32,
                                              BN=4, repair=10 ** 6, stats=st, phases=ph)
-            ms = ev_time(lambda: A.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, WP, dwq * q, C=C, K1=32,
-                                                     K2=32, BN=4, repair=10 ** 6), 3)
+            box_fn = lambda: A.alif_scan_forward(I, beta, rho, q, 1.0, 0.0, z, z, WP, dwq * q, C=C, K1=32,
+                                                 K2=32, BN=4, repair=10 ** 6)
+            ms = ev_time(box_fn, 3)
             box[f"{pname}_dw{dwq}q"] = {
-                "ms": round(ms, 4),
+                "ms": round(ms, 4), "ms_cold": round(ev_time_cold(box_fn, 3), 4),
                 "equals_serial": bool(torch.equal(U2, U) and torch.equal(W2, W) and torch.equal(S2, S)),
                 "stats": st, "phases_ms": {k: round(v, 4) for k, v in ph.items()}}
             del U2, W2, S2
@@ -556,6 +665,10 @@ def bench_cfg5(torch, dev, reps):
     bps = 16 + (12.5 if H.ALIF_RECOMPUTE_BWD else 24)
     out["bytes_per_neuron_step"] = bps
     out["pct_roofline_fwd_bwd"] = round(100 * bps * ns / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
+    tc = out["alif_fwd_serial_bwd_scan_cold_ms"]
+    out["fwd_bwd_value_cold"] = round(ns / (tc / 1000.0), 1)
+    out["pct_roofline_fwd_bwd_cold"] = round(100 * bps * ns / (tc / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
+    out["serial_fwd_cold_GBps"] = round(16 * ns / (out["serial_fwd_cold_ms"] / 1000.0) / 1e9, 1)
     out["config"] = "ALIF N=16384, T=4096, beta=0.95, rho=0.995, q=0.2, x~N(0.15,0.3^2)"
     del I, gS, U, W, S, Ig
     torch.cuda.empty_cache()
@@ -809,7 +922,8 @@ def main():
                     help="run each non-HBM-bound kernel once at its configuration (counter passes)")
     ap.add_argument("--headline-only", action="store_true",
                     help="skip the cfg3 / cfg4 / cfg5 / affine-reset measurements")
-    ap.add_argument("--only", choices=("cfg2_mapscan", "cfg3", "cfg4", "cfg5", "affine"),
+    ap.add_argument("--only", choices=("cfg2_mapscan", "cfg3", "cfg4", "cfg5", "affine", "auto_grid",
+                                       "ceilings"),
                     help="measure one of the other configurations only (for profiling runs); "
                          "prints its JSON, not the headline line")
     args = ap.parse_args()
@@ -834,7 +948,8 @@ def main():
         fn = {"cfg2_mapscan": lambda torch, dev, reps: bench_cfg2_mapscan(
                   torch, L, dev, torch.zeros(N_CFG, device=dev), reps),
               "cfg3": bench_cfg3, "cfg4": bench_cfg4, "cfg5": bench_cfg5,
-              "affine": bench_affine}[args.only]
+              "affine": bench_affine, "auto_grid": lambda torch, dev, reps: bench_auto_grid(torch, dev),
+              "ceilings": lambda torch, dev, reps: hbm_ceilings(torch, dev)}[args.only]
         print(json.dumps({args.only: fn(torch, dev, 5)}))
         return
     T, N, beta, K = T_CFG, N_CFG, 0.9, 8
@@ -901,10 +1016,13 @@ def main():
         torch.cuda.empty_cache()
         others = {}
         for name, fn in (("cfg3", bench_cfg3), ("cfg5", bench_cfg5), ("cfg4", bench_cfg4),
-                         ("affine", bench_affine)):
+                         ("affine", bench_affine),
+                         ("auto_grid", lambda torch, dev, reps: bench_auto_grid(torch, dev))):
             log(f"{name}")
             others[name] = fn(torch, dev, 5)
             log(f"{name} " + json.dumps(others[name]))
+    ceilings = hbm_ceilings(torch, dev)
+    log("hbm ceilings " + json.dumps(ceilings))
 
     cpu = None
     if not args.no_cpu:
@@ -919,6 +1037,13 @@ def main():
                "os_cpu_count": os.cpu_count(), "cpu_model": cpu_model()}
 
     pct = lambda b, t: round(100 * b * N * T / (t / 1000.0) / 1e9 / HBM_PEAK_GBS, 2)
+    stored_u = {"fwd_bwd_ms": round(ms["exact_fwd_stored_U"] + ms["adjoint_stored_U"], 4),
+                "pct_roofline_fwd_bwd": pct(B_FWD + B_BWD, ms["exact_fwd_stored_U"] + ms["adjoint_stored_U"]),
+                "pct_roofline_fwd": pct(B_FWD, ms["exact_fwd_stored_U"]),
+                "pct_roofline_bwd": pct(B_BWD, ms["adjoint_stored_U"]),
+                "bytes_per_neuron_step": B_FWD + B_BWD}
+    summary = compact_summary(value, ms_step, pct(B_FWD_RC + B_BWD_RC, ms_step), stored_u, mapscan,
+                              others, ceilings)
     out = {
         "metric": "neuron-steps/s fwd and fwd+bwd (LIF, 65536xT4096 fp32); % of HBM roofline",
         "value": round(value, 1),
@@ -952,10 +1077,9 @@ def main():
         "pct_roofline_fwd": pct(B_FWD_RC, ms["rc_fwd"]),
         "pct_roofline_bwd": pct(B_BWD_RC, ms["rc_bwd"]),
         "timed_step_check": check,
-        "stored_U_path": {"fwd_bwd_ms": round(ms["exact_fwd_stored_U"] + ms["adjoint_stored_U"], 4),
-                          "pct_roofline_fwd": pct(B_FWD, ms["exact_fwd_stored_U"]),
-                          "pct_roofline_bwd": pct(B_BWD, ms["adjoint_stored_U"]),
-                          "bytes_per_neuron_step": B_FWD + B_BWD},
+        "summary": summary,
+        "stored_U_path": stored_u,
+        "hbm_ceilings": ceilings,
         "ms": {k: round(v, 4) for k, v in ms.items()},
         "serial_hip_fwd_bwd_value": round(N * T / ((ms["serial_fwd"] + ms["serial_bwd"]) / 1000.0), 1),
         "maps_forced_counters": maps_ctr,
@@ -965,6 +1089,43 @@ def main():
         "other_configs": others,
     }
     print(json.dumps(out))
+    sys.stdout.flush()
+    log("summary " + json.dumps(summary, separators=(",", ":")))
+
+
+def compact_summary(value, ms_step, pct_step, stored_u, mapscan, others, ceilings):
+    """The figures a reader of the run's tail needs, in one short object: the headline, the
+    stored-U pair on the 32 B basis, the six configs[1] map-scan cells (ms, % of the 12 B
+    roofline, overflow fraction, equal to serial), cfg3 / cfg4 / cfg5's headline figures (cfg3 and
+    cfg5 back to back and cache-cold), the auto grid and the HBM ceilings."""
+    sm = {"headline": {"value": round(value, 1), "ms": round(ms_step, 4), "pct_20B": pct_step},
+          "stored_U": {"ms": stored_u["fwd_bwd_ms"], "pct_32B": stored_u["pct_roofline_fwd_bwd"]},
+          "cfg2_mapscan": {f"b{b}_C{C}": [c["ms"], c["pct_roofline_12B"], c["overflow_frac"],
+                                          c["equals_serial"]]
+                           for b in (0.9, 0.99) for C in (32, 64, 128)
+                           for c in (mapscan[f"beta{b}"][f"C{C}_K8"],)},
+          "ceilings_GBps": [ceilings["copy_GBps"], ceilings["fill_GBps"]]}
+    if others:
+        c3, c4, c5, ag = others["cfg3"], others["cfg4"], others["cfg5"], others["auto_grid"]
+        v4 = c4["v4"]
+        sm["cfg3"] = {"layers_ms": c3["lif_layers_fwd_bwd_ms"], "layers_cold_ms": c3["lif_layers_fwd_bwd_cold_ms"],
+                      "pct_cold": c3["lif_layers_pct_roofline_cold"], "step_ms_scan": c3["step_ms_scan"]}
+        sm["cfg4"] = {"fwd_bwd_ms": c4["fwd_bwd_ms"], "pct": c4["pct_roofline_fwd_bwd"],
+                      "v4_ms": {k: [r["ms"], r["equals_serial"]] for k, r in v4.items()},
+                      "assoc_vs_seq_ms": {k: r["ms"] for k, r in c4["mapscan_converged"].items()}}
+        box = c5["box_scan_repair"]
+        sm["cfg5"] = {"fwd_bwd_ms": c5["alif_fwd_serial_bwd_scan_ms"],
+                      "fwd_bwd_cold_ms": c5["alif_fwd_serial_bwd_scan_cold_ms"],
+                      "pct_cold": c5["pct_roofline_fwd_bwd_cold"],
+                      "serial_fwd_cold_GBps": c5["serial_fwd_cold_GBps"],
+                      "box_scan_ms": {k: [r["ms"], r["ms_cold"], r["equals_serial"]] for k, r in box.items()},
+                      "ref_shape_box_repair_ms": c5["reference_shape"]["fwd_box_scan_repair_ms"],
+                      "ref_shape_serial_ms": c5["reference_shape"]["fwd_serial_ms"],
+                      "N16_box_ms": c5["reference_shape"]["few_neurons"]["N16"]["fwd_box_scan_no_repair_ms"]}
+        sm["auto_grid"] = {"worst_auto_vs_best": ag["worst_auto_vs_best"],
+                           "within_5pct": f'{ag["cells_within_5pct"]}/{ag["n_cells"]}',
+                           "spikes_equal": ag["all_spikes_equal"]}
+    return sm
 
 
 if __name__ == "__main__":

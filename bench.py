@@ -474,8 +474,10 @@ def bench_cfg3(torch, dev, reps):
 
 def bench_cfg4(torch, dev, reps):
     """cfg4: N=1024, T=2^20, beta=0.99, x~N(0.012,0.08^2), u0~U[0,1).
-    Forward: the three-level scan_forward_v4 (repair on) on a small grid of (C, G, K, K2) with
-    overflow statistics, as the reference's e9d grid does (the reference default first); the
+    Forward: the three-level pipeline (scan_forward_v4_maps, repair on; an overflowed super map
+    walks its chunk maps, and at the reference default also the reference's serial fallback) on a
+    small grid of (C, G, K, K2) with overflow statistics, as the reference's e9d grid does (the
+    reference default first), and scan_forward_v4's converged dispatch; the
     converged two-level scan_forward_v3 (which takes the warm-started chunks here), the warm
     forward at other chunk / warm-up lengths and the long-chunk map scan in pieces it replaced;
     the single-pass exact forward; the serial forward.  Backward: the affine-scan adjoint and the
@@ -491,16 +493,30 @@ def bench_cfg4(torch, dev, reps):
     U, S = L.serial_forward(I, beta, 1.0, 0.0, u0)
     exact = lambda A, B: bool(torch.equal(A, U) and torch.equal(B, S))
     v4 = {}
-    for C, G, K, K2 in ((64, 16, 16, 32), (1024, 4, 32, 64), (2048, 4, 32, 64)):
+    for C, G, K, K2, fb in ((64, 16, 16, 32, "chunks"), (64, 16, 16, 32, "serial"), (1024, 4, 32, 64, "chunks"),
+                            (2048, 4, 32, 64, "chunks")):
         st = {}
-        U4, S4 = L.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6, stats=st)
+        U4, S4 = L.scan_forward_v4_maps(I, beta, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6, stats=st,
+                                        super_fallback=fb)
         ok = exact(U4, S4)
         del U4, S4
-        ms = ev_time(lambda: L.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2,
-                                               repair=10 ** 6), 2, warm=0)
-        v4[f"C{C}_G{G}_K{K}_K2{K2}"] = {"ms": round(ms, 4), "equals_serial": ok,
-                                        **{k: (round(v, 6) if isinstance(v, float) else v) for k, v in st.items()}}
+        U4, S4 = L.scan_forward_v4_maps(I, beta, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6,
+                                        super_fallback=fb)
+        ok = ok and exact(U4, S4)
+        del U4, S4
+        ms = ev_time(lambda: L.scan_forward_v4_maps(I, beta, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2,
+                                                    repair=10 ** 6, super_fallback=fb), 2, warm=1)
+        key = f"C{C}_G{G}_K{K}_K2{K2}" + ("" if fb == "chunks" else "_serial_fallback")
+        v4[key] = {"ms": round(ms, 4), "equals_serial": ok,
+                   **{k: (round(v, 6) if isinstance(v, float) else v) for k, v in st.items()}}
     out["v4"] = v4
+    # scan_forward_v4 itself at the reference default: converged without statistics it takes the
+    # fastest exact path, as scan_forward_v3 does
+    U4, S4 = L.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=64, G=16, K=16, K2=32, repair=10 ** 6)
+    out["v4_converged_dispatch_equals_serial"] = exact(U4, S4)
+    del U4, S4
+    out["v4_converged_dispatch_ms"] = ev_time(lambda: L.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=64, G=16, K=16,
+                                                                        K2=32, repair=10 ** 6), reps)
     U3, S3 = L.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=256, K=16, repair=10 ** 6)
     out["v3_converged_equals_serial"] = exact(U3, S3)
     run = L.last_scan_run()
@@ -893,7 +909,7 @@ def counters_workload(torch, dev):
     L._scan2_pieces(I, 0.99, 1.0, 0.0, u0, C2, L.LONG_K, P)
     L.scan_forward_assoc(I, 0.99, 1.0, 0.0, u0, C=2048, K=32)
     for C, G, K, K2 in ((2048, 4, 32, 64), (64, 16, 16, 32)):
-        L.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
+        L.scan_forward_v4_maps(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
         torch.cuda.synchronize()
     gS = torch.randn(T, N, generator=torch.Generator().manual_seed(1)).to(dev)
     L.scan_backward_tiled(I, u0, U, S, gS, None, 0.99, 1.0, 0.0, 4.0)

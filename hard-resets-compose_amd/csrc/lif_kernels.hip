@@ -5,6 +5,7 @@
 // t*N + n).  One lane owns one neuron; a wave64 covers 64 consecutive neurons,
 // so every time row is one contiguous 256-byte access per wave.  Per-chunk
 // arrays are [M, N] and map slots [M, K, N] (neuron-contiguous, coalesced).
+#include <cstdlib>
 #include <mutex>
 
 #include "lsh_abi.h"
@@ -857,6 +858,95 @@ __global__ __launch_bounds__(64) void k_lif_repair_ordered(const float* __restri
   }
 }
 
+// The same ordered walk over segments of R chunks at once, for few neurons: one wave per 64
+// neurons walking all M chunks leaves a few waves on the chip, and the Jacobi rounds run one
+// workgroup per 64 neurons.  Launch r is one round over every (segment, 64 neurons): segment g
+// covers chunks m0 = 1 + g R .. m1 - 1 and starts from the stored end of chunk m0 - 1; a
+// chunk whose start differs from the carried exit gets that exit as its start and is
+// replayed (lanes masked) until it meets its stored trajectory, and its end is rewritten when
+// the replay ran to the chunk's end.  After round r every segment is consistent with the end
+// it read before it, and segments 0 .. r - 1 are exact (segment r - 1 read the exact end of
+// segment r - 2, which round r did not change), so S rounds give the serial recurrence; a
+// round in which no segment rewrote its last chunk's end leaves every boundary as the next
+// segment read it, so later rounds find nothing to do: flags[r] records whether round r
+// rewrote one, and round r + 1 returns at once when it did not.  A segment may read its
+// boundary before or after the segment before it rewrites it in the same round; either way it
+// walks a consistent trajectory from the value it read, and the next round compares again.
+// flags[0 .. S] are zero before round 0.
+template <int PF>
+__global__ __launch_bounds__(64) void k_lif_repair_seg(const float* __restrict__ I,
+                                                       float* __restrict__ U, float* __restrict__ S,
+                                                       float* __restrict__ starts,
+                                                       float* __restrict__ ends, int* flags,
+                                                       int64_t N, int M, int C, int R, int NB,
+                                                       int round, float beta, float theta,
+                                                       float u_r) {
+  if (round > 0 && __builtin_nontemporal_load(flags + round - 1) == 0) return;
+  const int g = (int)(blockIdx.x / NB);
+  const int nb = (int)(blockIdx.x - (int64_t)g * NB);
+  const int m0 = 1 + g * R;
+  const int m1 = min(M, m0 + R);
+  if (m0 >= M) return;
+  const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
+  const bool valid = n < N;
+  const int64_t nc = valid ? n : N - 1;  // tail lanes read a valid column and never replay
+  float ue = ends[(size_t)(m0 - 1) * N + nc];
+  if (round > 0 && __ballot(valid && !same_bits(ue, starts[(size_t)m0 * N + nc])) == 0ull)
+    return;  // consistent with its boundary since the last round
+  float st[PF], en[PF];
+#pragma unroll
+  for (int k = 0; k < PF; ++k) {
+    const size_t o = (size_t)min(m0 + k, m1 - 1) * N + nc;
+    st[k] = starts[o];
+    en[k] = ends[o];
+  }
+  bool last_changed = false;
+  for (int m = m0; m < m1; ++m) {
+    const float s0 = st[0], e0 = en[0];
+#pragma unroll
+    for (int k = 0; k + 1 < PF; ++k) {
+      st[k] = st[k + 1];
+      en[k] = en[k + 1];
+    }
+    {
+      const size_t o = (size_t)min(m + PF, m1 - 1) * N + nc;
+      st[PF - 1] = starts[o];
+      en[PF - 1] = ends[o];
+    }
+    const bool dirty = valid && !same_bits(ue, s0);
+    if (__ballot(dirty) == 0ull) {
+      ue = e0;
+      continue;
+    }
+    if (dirty) {
+      const size_t oc = (size_t)m * N + n;
+      starts[oc] = ue;
+      float u = ue;
+      const size_t base = (size_t)m * C * N + n;
+      const bool met = stream_rows_until<16>(
+          I + base, U + base, (size_t)N, C, [&](int64_t j, float x, float u_old) {
+            bool s;
+            u = lif_step(u, x, beta, theta, u_r, s);
+            U[base + (size_t)j * N] = u;
+            S[base + (size_t)j * N] = s ? 1.0f : 0.0f;
+            return same_bits(u, u_old);
+          });
+      if (met) {
+        ue = e0;
+      } else {
+        ue = u;
+        if (!same_bits(u, e0)) {
+          ends[oc] = u;
+          if (m == m1 - 1) last_changed = true;
+        }
+      }
+    } else {
+      ue = e0;
+    }
+  }
+  if (m1 < M && __ballot(last_changed) != 0ull && threadIdx.x == 0) atomicOr(flags + round, 1);
+}
+
 // ---------------------------------------------------------------------------------------
 // host-side launch helpers
 template <int D>
@@ -1057,6 +1147,31 @@ void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* 
                     st);
 }
 
+// The segmented ordered repair (k_lif_repair_seg): from this many chunks, with fewer neurons
+// than the ordered pass needs; segments of at least kRepairSegMinR chunks, at most
+// kRepairSegMax of them (one launch each at worst), about kRepairSegWaves waves a round.
+// LSH_REPAIR_SEG=0 in the environment turns it off (the Jacobi rounds run instead), for
+// measurements.
+constexpr int kRepairSegMinM = 64;
+constexpr int kRepairSegMinR = 16;
+constexpr int kRepairSegMax = 64;
+constexpr int kRepairSegWaves = 2048;
+
+static bool repair_seg_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("LSH_REPAIR_SEG");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
+static int repair_seg_count(int NB, int M) {
+  int sg = kRepairSegWaves / NB;
+  sg = min(sg, (M - 1) / kRepairSegMinR);
+  sg = min(sg, kRepairSegMax);
+  return max(sg, 1);
+}
+
 // The device repair rounds alone, after a replay that wrote U, S and ends from starts.
 void lif_repair_launch(const float* I, float* U, float* S, float* starts, float* ends, int* list0,
                        int* list1, WsHeader* hdr, int64_t N, int M, int C, int64_t repair,
@@ -1069,10 +1184,20 @@ void lif_repair_launch(const float* I, float* U, float* S, float* starts, float*
     // T = 4096: C = 32 8.78 -> 3.52 ms, C = 64 5.02 -> 3.31, C = 128 2.59 -> 2.32, C = 256
     // 1.58 vs 1.65 (Jacobi); N = 8192: C = 32 1.15 -> 0.85, C = 128 0.47 vs 0.75 (Jacobi);
     // N = 1024, T = 65536, C = 256: 3.63 vs 5.77 (Jacobi, 16 waves).
+    const int NB = (int)((N + WAVE - 1) / WAVE);
     if ((N >= 4096 && M >= 64) || (N >= 32768 && M >= 32)) {
-      const int NB = (int)((N + WAVE - 1) / WAVE);
       hipLaunchKernelGGL(k_lif_repair_ordered<8>, dim3((unsigned)NB), dim3(WAVE), 0, st, I, U,
                          S, starts, ends, N, M, C, beta, theta, u_r);
+      return;
+    }
+    if (M >= kRepairSegMinM && repair_seg_enabled()) {
+      // few neurons, many chunks: the ordered walk over segments, one round per launch
+      const int SG = repair_seg_count(NB, M);
+      const int R = (M - 1 + SG - 1) / SG;
+      fill_i32_launch(list0, SG, 0, st);
+      for (int r = 0; r < SG; ++r)
+        hipLaunchKernelGGL(k_lif_repair_seg<8>, dim3((unsigned)((int64_t)SG * NB)), dim3(WAVE), 0,
+                           st, I, U, S, starts, ends, list0, N, M, C, R, NB, r, beta, theta, u_r);
       return;
     }
     repair = M;

@@ -366,24 +366,59 @@ __global__ __launch_bounds__(64) void k_lif_compose_wave(
   }
 }
 
+// The chunk maps behind the super maps (truncated counts and overflow flags, as the inner
+// carry reads them), for the fallback of an overflowed super map; walk = 0: serial steps.
+struct ChunkMaps {
+  const float* MA;
+  const float* MB;
+  const int* MN;
+  const int* OVF;
+  const float* MX;
+  const float* MC;
+  int K, G, C, walk;
+};
+
 template <int KMAX>
 struct SuperMap {
   float xd[KMAX], cd[KMAX], a, b;
   int cnt, ovf;
 };
 
-// Sequential carry over pre-pruned maps (n and ovf final); overflowed maps fall back to L
-// serial steps.  The maps are read one ahead into a ring of two register sets (the loop unrolled by two, so no
+// The G chunk maps of super map s evaluated in turn from u, as k_lif_carry_inner evaluates
+// them (an overflowed chunk map runs its C steps serially): the fallback of an overflowed super
+// map that costs G map evaluations instead of C*G steps.
+template <int KW>
+__device__ __forceinline__ float walk_chunk_maps(const float* __restrict__ I, const ChunkMaps& cm,
+                                                 int64_t N, int64_t n, int64_t s, float u,
+                                                 float beta, float theta, float u_r) {
+  for (int jj = 0; jj < cm.G; ++jj) {
+    const int64_t m = s * cm.G + jj;
+    const size_t o = (size_t)m * N + n;
+    float xd[KW], cd[KW];
+#pragma unroll
+    for (int i = 0; i < KW; ++i) {
+      xd[i] = i < cm.K ? cm.MX[((size_t)m * cm.K + i) * N + n] : INFINITY;
+      cd[i] = i < cm.K ? cm.MC[((size_t)m * cm.K + i) * N + n] : 0.0f;
+    }
+    float nu = eval_slots<KW>(xd, cd, cm.MN[o], cm.MA[o], cm.MB[o], u);
+    if (cm.OVF[o]) nu = serial_rows(I, N, n, m * cm.C, cm.C, u, beta, theta, u_r);
+    u = nu;
+  }
+  return u;
+}
+
+// Sequential carry over pre-pruned maps (n and ovf final); an overflowed map falls back to its
+// L serial steps, or, with chunk maps given (cm.walk), to the walk over its G chunk maps.  The maps are read one ahead into a ring of two register sets (the loop unrolled by two, so no
 // set is copied), every load unconditional with its index clamped into the arrays (map <= M -
 // 1, slot <= K - 1; eval_slots masks the slots past the count): the compiler's wait for the map
 // in use then leaves the next map's loads in flight.  Lanes past N repeat neuron N - 1 and store
 // nothing.
-template <int KMAX>
+template <int KMAX, int KW>
 __global__ __launch_bounds__(64) void k_map_carry(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ MA,
     const float* __restrict__ MB, const int* __restrict__ MN, const int* __restrict__ OVF,
     const float* __restrict__ MX, const float* __restrict__ MC, float* __restrict__ starts,
-    int64_t N, int M, int K, int64_t L, float beta, float theta, float u_r) {
+    int64_t N, int M, int K, int64_t L, float beta, float theta, float u_r, ChunkMaps cm) {
   const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
   const bool valid = n < N;
   const int64_t nn = valid ? n : N - 1;
@@ -414,7 +449,9 @@ __global__ __launch_bounds__(64) void k_map_carry(
       const SuperMap<KMAX>& d = mr[ph];
       if (valid) starts[(size_t)m * N + nn] = u;
       float nu = eval_slots<KMAX>(d.xd, d.cd, d.cnt, d.a, d.b, u);
-      if (d.ovf) nu = serial_rows(I, N, nn, (int64_t)m * L, L, u, beta, theta, u_r);
+      if (d.ovf)
+        nu = cm.walk ? walk_chunk_maps<KW>(I, cm, N, nn, m, u, beta, theta, u_r)
+                     : serial_rows(I, N, nn, (int64_t)m * L, L, u, beta, theta, u_r);
       u = nu;
     }
   }
@@ -478,11 +515,55 @@ struct SuperWindow {
   float xd[32], cd[32];  // VGPR g, lane 32h + s: slot s of map 2g + h
 };
 
+// The G chunk maps of super map s from u, with one wave per neuron (walk_chunk_maps's values):
+// batches of 16 chunk maps, VGPR v of a batch holding chunks v*CPV .. v*CPV + CPV - 1 on rows of
+// RW lanes (slot i of chunk b in lane (b % CPV) RW + i) and the chunk scalars on lanes 0-15;
+// every load of a batch is issued before its first evaluation.
+template <int RW>
+__device__ __forceinline__ float wave_walk_chunk_maps(const float* __restrict__ I, const ChunkMaps& cm,
+                                                      int64_t N, int64_t n, int64_t s, float u,
+                                                      float beta, float theta, float u_r) {
+  constexpr int CPV = 64 / RW;  // chunks per VGPR
+  constexpr int NV = 16 / CPV;  // VGPRs per batch of 16 chunks
+  const int lane = threadIdx.x & 63;
+  const int row = lane / RW, slot = lane % RW;
+  const int sl = min(slot, cm.K - 1);
+  const int64_t c0 = s * cm.G;  // first chunk of the super map
+  for (int j0 = 0; j0 < cm.G; j0 += 16) {
+    const int nb = min(16, cm.G - j0);
+    float xv[NV], cv[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      const size_t m = (size_t)(c0 + j0 + min(v * CPV + row, nb - 1));
+      xv[v] = cm.MX[(m * cm.K + sl) * N + n];
+      cv[v] = cm.MC[(m * cm.K + sl) * N + n];
+    }
+    const size_t ms = (size_t)(c0 + j0 + min(lane, nb - 1)) * N + n;
+    const float av = cm.MA[ms], bv = cm.MB[ms];
+    const int cntv = cm.MN[ms], ovfv = cm.OVF[ms];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      for (int h = 0; h < CPV; ++h) {
+        const int b = v * CPV + h;
+        if (b >= nb) break;
+        const int cnt = __builtin_amdgcn_readlane(cntv, b);
+        const int k = __popcll(__ballot(row == h && slot < cnt && xv[v] > u));
+        float nu = k == cnt ? __fadd_rn(__fmul_rn(lane_f(av, b), u), lane_f(bv, b))
+                            : lane_f(cv[v], h * RW + min(k, RW - 1));
+        if (__builtin_amdgcn_readlane(ovfv, b) != 0)
+          nu = wave_serial_rows(I, N, n, (c0 + j0 + b) * cm.C, cm.C, u, beta, theta, u_r);
+        u = nu;
+      }
+    }
+  }
+  return u;
+}
+
 __global__ __launch_bounds__(64) void k_map_carry_wave(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ MA,
     const float* __restrict__ MB, const int* __restrict__ MN, const int* __restrict__ OVF,
     const float* __restrict__ MX, const float* __restrict__ MC, float* __restrict__ starts,
-    int64_t N, int M, int K, int64_t L, float beta, float theta, float u_r) {
+    int64_t N, int M, int K, int64_t L, float beta, float theta, float u_r, ChunkMaps cm) {
   if (M <= 0) return;
   const int64_t n = xcd_neuron(blockIdx.x, N);
   const int lane = threadIdx.x;
@@ -519,8 +600,15 @@ __global__ __launch_bounds__(64) void k_map_carry_wave(
         float nu = k == cnt ? __fadd_rn(__fmul_rn(lane_f(cur.a, c), u), lane_f(cur.b, c))
                             : lane_f(cur.cd[g], 32 * h + min(k, 31));
         if (lane == c) st_o = u;
-        if (__builtin_amdgcn_readlane(cur.ovf, c) != 0)  // serial fallback through the map
-          nu = wave_serial_rows(I, N, n, (int64_t)(w * 64 + c) * L, L, u, beta, theta, u_r);
+        if (__builtin_amdgcn_readlane(cur.ovf, c) != 0) {  // fallback through the map
+          const int64_t sm = (int64_t)w * 64 + c;
+          if (!cm.walk)
+            nu = wave_serial_rows(I, N, n, sm * L, L, u, beta, theta, u_r);
+          else if (cm.K <= 16)
+            nu = wave_walk_chunk_maps<16>(I, cm, N, n, sm, u, beta, theta, u_r);
+          else
+            nu = wave_walk_chunk_maps<32>(I, cm, N, n, sm, u, beta, theta, u_r);
+        }
         u = nu;
       }
     }
@@ -639,22 +727,47 @@ static void launch_inner(const float* I, char* w, const lsh_v4_layout& L, int64_
                      F(L.v3.MC), F(L.v3.STARTS), N, NB, G, C, K, beta, theta, u_r);
 }
 
-template <int K2MAX>
-static void launch_super_carry(const float* I, const float* u0, char* w, const lsh_v4_layout& L,
-                               int64_t N, int M2, int K2, int64_t Lsteps, float beta, float theta,
-                               float u_r, hipStream_t st) {
+template <int K2MAX, int KW>
+static void launch_super_carry_lanes(const float* I, const float* u0, char* w, const lsh_v4_layout& L,
+                                     int64_t N, int M2, int K2, int64_t Lsteps, float beta,
+                                     float theta, float u_r, const ChunkMaps& cm, hipStream_t st) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  hipLaunchKernelGGL((k_map_carry<K2MAX, KW>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, F(L.SA),
+                     F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC), F(L.SSTARTS), N, M2, K2,
+                     Lsteps, beta, theta, u_r, cm);
+}
+
+// walk != 0: an overflowed super map walks its G chunk maps; else its C*G steps run serially
+// (the reference's rule, triton_lif.py:958-963).
+template <int K2MAX>
+static void launch_super_carry(const float* I, const float* u0, char* w, const lsh_v4_layout& L,
+                               int64_t N, int M2, int K2, int G, int C, int K, int walk,
+                               float beta, float theta, float u_r, hipStream_t st) {
+  auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
+  auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  const ChunkMaps cm{F(L.v3.MA), F(L.v3.MB), Iq(L.v3.MN), Iq(L.v3.OVF), F(L.v3.MX), F(L.v3.MC),
+                     K, G, C, walk};
+  const int64_t Lsteps = (int64_t)C * G;
   if (K2MAX <= 32 && N <= LSH_V4_WAVE_MAX_N) {
     hipLaunchKernelGGL(k_map_carry_wave, dim3((unsigned)N), dim3(WAVE), 0, st, I, u0, F(L.SA),
                        F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC), F(L.SSTARTS), N, M2, K2,
-                       Lsteps, beta, theta, u_r);
+                       Lsteps, beta, theta, u_r, cm);
     return;
   }
-  hipLaunchKernelGGL((k_map_carry<K2MAX>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, F(L.SA),
-                     F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC), F(L.SSTARTS), N, M2, K2,
-                     Lsteps, beta, theta, u_r);
+  // the chunk maps' slot capacity (K <= K2)
+  if (K <= 4)
+    launch_super_carry_lanes<K2MAX, 4>(I, u0, w, L, N, M2, K2, Lsteps, beta, theta, u_r, cm, st);
+  else if (K <= 8 || K2MAX <= 4)
+    launch_super_carry_lanes<K2MAX, (K2MAX < 8 ? K2MAX : 8)>(I, u0, w, L, N, M2, K2, Lsteps, beta,
+                                                             theta, u_r, cm, st);
+  else if (K <= 16 || K2MAX <= 8)
+    launch_super_carry_lanes<K2MAX, (K2MAX < 16 ? K2MAX : 16)>(I, u0, w, L, N, M2, K2, Lsteps, beta,
+                                                               theta, u_r, cm, st);
+  else
+    launch_super_carry_lanes<K2MAX, (K2MAX < 32 ? K2MAX : 32)>(I, u0, w, L, N, M2, K2, Lsteps, beta,
+                                                               theta, u_r, cm, st);
 }
 
 void v3_layout_fill(int64_t T, int64_t N, int C, int K, lsh_v3_layout* L);
@@ -705,10 +818,11 @@ extern "C" size_t lsh_lif_scan_v4_workspace(int64_t T, int64_t N, int C, int G, 
 
 extern "C" int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, float* S, int64_t T,
                                    int64_t N, float beta, float theta, float u_r, int C, int G,
-                                   int K, int K2, int64_t repair, void* ws, size_t ws_bytes,
-                                   void* stream) {
+                                   int K, int K2, int super_walk, int64_t repair, void* ws,
+                                   size_t ws_bytes, void* stream) {
   if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
-  if (repair < -1) return LSH_ERR_ARG;
+  if (repair < -1 || (super_walk != 0 && super_walk != 1)) return LSH_ERR_ARG;
+  const int walk = super_walk;
   const int rc = v4_check(T, N, C, G, K, K2);
   if (rc != LSH_OK) return rc;
   lsh_v4_layout L;
@@ -746,11 +860,11 @@ extern "C" int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, fl
   }
   if (r != LSH_OK) return r;
   switch (kcap(K2)) {
-    case 4: launch_super_carry<4>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
-    case 8: launch_super_carry<8>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
-    case 16: launch_super_carry<16>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
-    case 32: launch_super_carry<32>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
-    default: launch_super_carry<64>(I, u0, w, L, N, M2, K2, (int64_t)C * G, beta, theta, u_r, st); break;
+    case 4: launch_super_carry<4>(I, u0, w, L, N, M2, K2, G, C, K, walk, beta, theta, u_r, st); break;
+    case 8: launch_super_carry<8>(I, u0, w, L, N, M2, K2, G, C, K, walk, beta, theta, u_r, st); break;
+    case 16: launch_super_carry<16>(I, u0, w, L, N, M2, K2, G, C, K, walk, beta, theta, u_r, st); break;
+    case 32: launch_super_carry<32>(I, u0, w, L, N, M2, K2, G, C, K, walk, beta, theta, u_r, st); break;
+    default: launch_super_carry<64>(I, u0, w, L, N, M2, K2, G, C, K, walk, beta, theta, u_r, st); break;
   }
   switch (kcap(K)) {
     case 4: launch_inner<4>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st); break;

@@ -14,6 +14,9 @@ from . import _build
 
 _LIB = None
 
+# LSH_ABI_VERSION of include/lifscan_hip.h that these signatures bind
+ABI_VERSION = 3
+
 LSH_OK = 0
 LSH_ERR_ARG = -1
 LSH_ERR_SHAPE = -2
@@ -108,7 +111,7 @@ SIGNATURES = {
     "lsh_lif_scan_v4_workspace": (c_sz, [c_i64, c_i64, c_i, c_i, c_i, c_i]),
     "lsh_lif_scan_v4_layout": (c_i, [c_i64, c_i64, c_i, c_i, c_i, c_i, ctypes.POINTER(V4Layout)]),
     "lsh_lif_scan_v4_fwd": (c_i, [c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_i, c_i, c_i, c_i,
-                                  c_i64, c_p, c_sz, c_p]),
+                                  c_i, c_i64, c_p, c_sz, c_p]),
     "lsh_alif_serial_fwd": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_f, c_f, c_f, c_f, c_f,
                                   c_p]),
     "lsh_alif_serial_fwd_dparams": (c_i, [c_p, c_p, c_p, c_p, c_p, c_p, c_i64, c_i64, c_p, c_f, c_p]),
@@ -170,6 +173,10 @@ def lib():
                 f"HIP extension not built ({path} missing): run `python -c \"import "
                 f"__graft_entry__ as g; g.build()\"` or `python {_build.__file__}`")
         L = ctypes.CDLL(path)
+        L.lsh_abi_version.restype = c_i
+        if L.lsh_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{path} has C ABI version {L.lsh_abi_version()}, this binding "
+                               f"needs {ABI_VERSION}: rebuild the library")
         for name, (res, args) in SIGNATURES.items():
             f = getattr(L, name)
             f.restype = res

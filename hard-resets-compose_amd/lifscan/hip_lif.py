@@ -26,12 +26,19 @@ BN_DEFAULT = 128
 # auto dispatch thresholds (serial vs scan per pass), measured on MI355X (beta = 0.95, N from
 # 256 to 65536, T from 1024 to 65536): the scan forward of lif_auto (scan_forward_auto, no
 # repair) beats the serial kernel only with <= 1024 neurons and T >= 16384 (e.g. N = 1024,
-# T = 65536: 1.03 vs 1.87 ms; N = 4096, T = 65536: 2.45 vs 2.06 ms); the scan adjoint never
-# loses (N = 65536, T = 1024: 0.275 vs 0.286 ms; N = 1024, T = 65536: 0.49 vs 10.8 ms).
+# T = 65536: 1.03 vs 1.87 ms; N = 4096, T = 65536: 2.45 vs 2.06 ms).  The scan adjoint, one
+# layer's fwd + bwd through autograd (beta 0.9, x ~ N(0.15, 0.4^2)), serial fwd + serial bwd
+# against serial fwd + scan bwd: below 16384 neurons the serial adjoint wins up to T = 1024
+# (N = 1024, T = 1024: 0.108 vs 0.126 ms; N = 8192: 0.117 vs 0.127) and they tie at T = 2048
+# (N = 1024: 0.128 vs 0.125; N = 8192: 0.156 vs 0.154), after which the scan wins (N = 1024,
+# T = 4096: 0.226 vs 0.131); from 16384 neurons the scan (the single pass) wins from T = 256
+# (N = 16384, T = 1024: 0.128 vs 0.110; N = 32768, T = 512: 0.129 vs 0.108).
 AUTO_FWD_MAX_N = 1024
 AUTO_FWD_MIN_T = 16384
 AUTO_BWD_MAX_N = 1 << 31
-AUTO_BWD_MIN_T = 256
+AUTO_BWD_MIN_T = 2048
+AUTO_BWD_WIDE_N = 16384     # from this many neurons the scan adjoint from AUTO_BWD_WIDE_MIN_T
+AUTO_BWD_WIDE_MIN_T = 256
 
 
 # ----------------------------------------------------------------------------- helpers
@@ -279,13 +286,25 @@ def scan_forward_v3(I, beta, theta, u_r, u0, C=64, K=16, BN=32, nw=1, BNc=16, nw
     (warm_plan), else the single-pass kernel, or for few neurons and long T the same two-level
     scan with long chunks (long_sequence_C)."""
     I = _input(I)
+    out = _converged_fast(I, beta, theta, u_r, u0, C, min(int(K), 16), repair, stats)
+    if out is not None:
+        return out
+    return _scan2(I, beta, theta, u_r, u0, C, K, repair, stats)
+
+
+def _converged_fast(I, beta, theta, u_r, u0, C, K, repair, stats):
+    """(U, S) by the fastest exact path when the call asks for the converged result (repair
+    budget >= T/C) and no statistics: the warm-started chunks (warm_plan), else for few neurons
+    and long T the two-level scan with long chunks, else the single pass; None when the call
+    needs the maps' own pipeline (a finite repair budget, statistics, or K > 16)."""
     T, N = I.shape
-    if (stats is None and int(C) >= 1 and T % int(C) == 0 and int(repair) >= T // int(C)
-            and T > 0 and N > 0):
+    if not (int(C) >= 1 and T % int(C) == 0):
+        return None
+    if stats is None and int(repair) >= T // int(C) and T > 0 and N > 0:
         plan = warm_plan(T, N, beta)
         if plan is not None:
             return _scan_warm_run(I, beta, theta, u_r, u0, *plan)
-    if int(C) >= 1 and T % int(C) == 0 and _fused_fwd_ok(T, C, K, repair, stats):
+    if _fused_fwd_ok(T, C, K, repair, stats):
         long_c = long_sequence_C(T, N)
         if long_c:  # few neurons, long T: the multi-kernel scan with long chunks is faster
             C2, P = long_sequence_plan(T, N)
@@ -293,7 +312,7 @@ def scan_forward_v3(I, beta, theta, u_r, u0, C=64, K=16, BN=32, nw=1, BNc=16, nw
                 return _scan2_pieces(I, beta, theta, u_r, u0, C2, LONG_K, P)
             return _scan2(I, beta, theta, u_r, u0, long_c, LONG_K, T // long_c, None)
         return scan_forward_exact(I, beta, theta, u_r, u0, K=K)
-    return _scan2(I, beta, theta, u_r, u0, C, K, repair, stats)
+    return None
 
 
 # Converged exact forward for few neurons and long sequences: the single-pass kernel's hand-off
@@ -603,11 +622,35 @@ class _ScanRunV4(_ScanRun):
 
 
 def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=1, BNg=16, nwg=1,
-                    BNc=16, nwc=1, BNr=32, D=8, nwr=1, repair=0, stats=None):
+                    BNc=16, nwc=1, BNr=32, D=8, nwr=1, repair=0, stats=None, super_fallback="chunks"):
     """Three-level exact scan (triton_lif.py:935-983) -> (U, S).  T must be divisible by C*G
     (ValueError, the reference asserts).  stats receives repair_iters, overflow_frac,
-    super_overflow_frac, mean_pieces, super_mean_pieces, super_max_pieces (:976-982)."""
+    super_overflow_frac, mean_pieces, super_mean_pieces, super_max_pieces (:976-982).
+    super_fallback: how the super-map carry passes an overflowed super map: "chunks" walks its
+    G chunk maps (as the inner carry does; an overflowed chunk map runs its C steps serially),
+    "serial" runs its C*G steps serially (the reference's carry, triton_lif.py:958-963).  With
+    the repair budget at least T/C and no stats requested, the result is the serial recurrence
+    and the fastest exact path computes it, as in scan_forward_v3 (scan_forward_v4_maps runs
+    the three-level pipeline itself)."""
+    I = _input(I)
+    T = I.shape[0]
+    if int(C) >= 1 and int(G) >= 1 and T % int(C) == 0 and (T // int(C)) % int(G) == 0:
+        out = _converged_fast(I, beta, theta, u_r, u0, C, min(int(K), 16), repair, stats)
+        if out is not None:
+            return out
+    return scan_forward_v4_maps(I, beta, theta, u_r, u0, C=C, G=G, K=K, K2=K2, repair=repair,
+                                stats=stats, super_fallback=super_fallback)
+
+
+def scan_forward_v4_maps(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, repair=0, stats=None,
+                         super_fallback="chunks"):
+    """The three-level pipeline of scan_forward_v4 itself (envelope, chunk maps, group
+    composition, super-map carry, inner carry, replay, device repair) -> (U, S), also where
+    scan_forward_v4 would compute its converged result by a faster exact path.  For measuring
+    the three-level scan."""
     global _LAST_RUN
+    if super_fallback not in ("chunks", "serial"):
+        raise ValueError('super_fallback must be "chunks" or "serial"')
     I = _input(I)
     T, N = I.shape
     u0 = _vec(u0, N, I)
@@ -626,6 +669,7 @@ def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=
     with _n.on_device(I):
         _n.check(L.lsh_lif_scan_v4_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
                                        _f32(beta), _f32(theta), _f32(u_r), C, G, K, K2,
+                                       1 if super_fallback == "chunks" else 0,
                                        _repair_arg(repair, T // C, stats), _n.ptr(ws), nbytes,
                                        _n.stream_of(I)),
                  "lsh_lif_scan_v4_fwd")
@@ -958,7 +1002,8 @@ def auto_modes(N, T):
     serial, so lif_auto runs for every T (e.g. T = 1000 or 1002), as the reference's does at
     its thresholds."""
     fwd = "scan" if (N <= AUTO_FWD_MAX_N and T >= AUTO_FWD_MIN_T) else "serial"
-    bwd = "scan" if (N <= AUTO_BWD_MAX_N and T >= AUTO_BWD_MIN_T) else "serial"
+    bwd = "scan" if (N <= AUTO_BWD_MAX_N and (T >= AUTO_BWD_MIN_T or (
+        N >= AUTO_BWD_WIDE_N and T >= AUTO_BWD_WIDE_MIN_T))) else "serial"
     if fwd == "scan" and _chunk_or_none(T, 16) is None:
         fwd = "serial"
     if bwd == "scan" and _chunk_or_none(T, 2) is None:

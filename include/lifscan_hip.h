@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define LSH_ABI_VERSION 2
+#define LSH_ABI_VERSION 3
 
 #define LSH_OK 0
 #define LSH_ERR_ARG (-1)          /* null pointer or bad scalar argument */
@@ -195,6 +195,9 @@ int lsh_lif_scan_v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3_layout* ou
  * parallel, replay, Jacobi repair on device (`repair` as for lsh_lif_scan_v3_fwd, -1
  * included).  Replaces triton_lif.py:935-983
  * (scan_forward_v4), :829-899 (compose_group_kernel), :903-932 (carry_inner_kernel).
+ * super_walk = 0: an overflowed super map runs its C*G steps serially (the reference's carry,
+ * triton_lif.py:958-963); 1: it walks its G chunk maps as the inner carry does (an overflowed
+ * chunk map runs its C steps serially).  Either way the repair gives the serial recurrence.
  * Requires T % C == 0, (T / C) % G == 0, 1 <= K <= K2, K <= 32, K2 <= 64. */
 typedef struct lsh_v4_layout {
   lsh_v3_layout v3;     /* chunk-level arrays, as for lsh_lif_scan_v3_fwd */
@@ -208,7 +211,7 @@ int lsh_lif_scan_v4_layout(int64_t T, int64_t N, int C, int G, int K, int K2,
                            lsh_v4_layout* out);
 int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, float* S, int64_t T, int64_t N,
                         float beta, float theta, float u_r, int C, int G, int K, int K2,
-                        int64_t repair, void* ws, size_t ws_bytes, void* stream);
+                        int super_walk, int64_t repair, void* ws, size_t ws_bytes, void* stream);
 
 /* Affine-scan backward: chunk composition of lam_t = a_t*lam_{t+1} + b_t, reverse carry,
  * reverse replay.  Replaces triton_lif.py:512-526 (scan_backward_tiled), :298-312

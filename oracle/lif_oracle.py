@@ -386,10 +386,41 @@ def carry_inner(I, sstarts, A, B, xd, cd, n, ovf, beta, theta, u_r, C, G):
     return starts
 
 
+def carry_super(I, u0, SA, SB, SX, SC, SN, SOVF, A, B, xd, cd, n, ovf, beta, theta, u_r, C, G,
+                fallback="chunks"):
+    """Sequential carry over the super maps (triton_lif.py:958-963, carry2_kernel with fallback
+    length C*G).  An overflowed super map is passed with fallback "serial" by its C*G serial steps
+    (the reference), with "chunks" by evaluating its G chunk maps in turn from the super's start
+    exactly as carry_inner does (an overflowed chunk map by its C serial steps), so that the
+    next super's start is the value the inner carry reaches at the end of this one."""
+    if fallback == "serial":
+        return carry(I, u0, SA, SB, SX, SC, SN, SOVF, beta, theta, u_r, C * G)
+    M2, N = SA.shape
+    u = np.array(u0, dtype=f32).reshape(N).copy()
+    sstarts = np.empty((M2, N), dtype=f32)
+    for s_ in range(M2):
+        sstarts[s_] = u
+        nu = eval_map(SA[s_], SB[s_], SX[s_], SC[s_], SN[s_], u)
+        bad = SOVF[s_] > 0
+        if bad.any():
+            w = u.copy()
+            for jj in range(G):
+                m = s_ * G + jj
+                v = eval_map(A[m], B[m], xd[m], cd[m], n[m], w)
+                if ovf[m].any():
+                    v = np.where(ovf[m] > 0, serial_segment(I[m * C:(m + 1) * C], beta, theta, u_r, w),
+                                 v).astype(f32)
+                w = v
+            nu = np.where(bad, w, nu).astype(f32)
+        u = nu
+    return sstarts
+
+
 def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, repair=0, stats=None,
-                    keep=None):
+                    keep=None, super_fallback="chunks"):
     """Three-level scan (triton_lif.py:935-983): envelope -> chunk maps -> group composition
-    -> carry over super maps -> inner carry -> replay -> repair; stats as :976-982."""
+    -> carry over super maps (an overflowed one passed as carry_super's `fallback`) -> inner
+    carry -> replay -> repair; stats as :976-982."""
     I = np.ascontiguousarray(I, dtype=f32)
     T, N = I.shape
     M = T // C
@@ -400,7 +431,8 @@ def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, repair=0, 
     Lo = envelope_carry(u0, EC, EA, EB)
     A, B, xd, cd, n, ovf = build_maps(I, beta, theta, u_r, Lo, hi, C, K)
     SA, SB, SX, SC, SN, SOVF = compose_groups(A, B, xd, cd, n, ovf, Lo, u0, theta, u_r, G, K2)
-    sstarts = carry(I, u0, SA, SB, SX, SC, SN, SOVF, beta, theta, u_r, C * G)
+    sstarts = carry_super(I, u0, SA, SB, SX, SC, SN, SOVF, A, B, xd, cd, n, ovf, beta, theta, u_r,
+                          C, G, super_fallback)
     starts = carry_inner(I, sstarts, A, B, xd, cd, n, ovf, beta, theta, u_r, C, G)
     U, S, ends = replay(I, starts, beta, theta, u_r, C)
     it = 0

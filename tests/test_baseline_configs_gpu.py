@@ -80,19 +80,28 @@ def _cfg4_inputs(dev):
 def test_cfg4_scan_v4_equals_serial(dev):
     """cfg4 (N = 1024, T = 2^20, beta = 0.99, x ~ N(0.012, 0.08^2), u0 ~ U[0, 1)): the three-level
     scan_forward_v4 with repair at the reference default (C 64, G 16, K 16, K2 32; most super maps
-    overflow and fall back) and at C 2048, G 4, K 32, K2 64 returns the serial forward bit for
-    bit; 64 columns of the serial forward equal the oracle's."""
+    overflow, passed by walking their chunk maps or by their serial steps) and at C 2048, G 4,
+    K 32, K2 64 returns the serial forward bit for bit, with statistics (the Jacobi rounds) and
+    without (the segmented ordered repair); 64 columns of the serial forward equal the oracle's."""
     from lifscan import hip_lif as L
     T, N, I, u0 = _cfg4_inputs(dev)
     Us, Ss = L.serial_forward(I, 0.99, 1.0, 0.0, u0)
-    for C, G, K, K2 in ((64, 16, 16, 32), (2048, 4, 32, 64)):
-        print(f"cfg4 v4 C={C} G={G} K={K} K2={K2}", flush=True)
+    for C, G, K, K2, fb in ((64, 16, 16, 32, "chunks"), (64, 16, 16, 32, "serial"), (2048, 4, 32, 64, "chunks")):
+        print(f"cfg4 v4 C={C} G={G} K={K} K2={K2} fallback={fb}", flush=True)
         st = {}
-        U, S = L.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6, stats=st)
+        U, S = L.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6, stats=st,
+                                 super_fallback=fb)
         assert torch.equal(U, Us) and torch.equal(S, Ss), st
         print(f"  stats {st}", flush=True)
+        # without statistics: the pipeline's converged repair (the segmented ordered walk here)
+        U, S = L.scan_forward_v4_maps(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6,
+                                      super_fallback=fb)
+        assert torch.equal(U, Us) and torch.equal(S, Ss)
         del U, S
         torch.cuda.empty_cache()
+    U, S = L.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=64, G=16, K=16, K2=32, repair=10 ** 6)
+    assert torch.equal(U, Us) and torch.equal(S, Ss)  # the converged dispatch
+    del U, S
     cols = np.arange(0, N, N // 64)
     Uo, So = O.serial_forward(host(I[:, cols]), 0.99, 1.0, 0.0, host(u0[cols]))
     assert np.array_equal(host(Us[:, cols]), Uo) and np.array_equal(host(Ss[:, cols]), So)

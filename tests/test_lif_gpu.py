@@ -320,10 +320,12 @@ def test_lif_auto_matches_serial(L, dev):
 @pytest.mark.parametrize("T", [1000, 1032])
 def test_lif_auto_and_lif_param_lengths_without_a_chunk(L, dev, T):
     """T with no chunk divisible by 16 (the scan forward's policy): lif_auto and
-    lif_param(mode="auto") run (serial forward, chunked scan adjoint at C = 8), spikes equal the
-    serial recurrence and the gradients the fp64 adjoint."""
+    lif_param(mode="auto") run (serial forward, chunked scan adjoint at C = 8: from 16384 neurons
+    auto takes the scan adjoint from T = 256), spikes equal the serial recurrence and the
+    gradients the fp64 adjoint."""
     from lifscan.fit import lif_param
-    N = 4096
+    N = 16384
+    assert L.auto_modes(N, T) == ("serial", "scan")
     I = normal(T, N, 0.12, 0.25, 40)
     W = normal(T, N, 0.0, 1.0, 41)
     u0 = np.zeros(N, np.float32)
@@ -367,23 +369,27 @@ def test_cfg2_scan_equals_serial_full_size(L, dev):
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("fallback", ["chunks", "serial"])
 @pytest.mark.parametrize("beta,mu,sd", [(0.5, 0.15, 0.4), (0.9, 0.15, 0.4), (0.99, 0.012, 0.08),
                                         (1.0, -0.1, 0.6), (0.9, 0.4, 0.2)])
-def test_scan_v4_matches_oracle(L, dev, beta, mu, sd):
+def test_scan_v4_matches_oracle(L, dev, beta, mu, sd, fallback):
     """Three-level scan (experiments/test_v4.py shapes: N=777): chunk and super maps, starts,
-    U, S and stats equal the oracle bit for bit at repair=0; repair on gives the serial
-    recurrence."""
+    U, S and stats equal the oracle bit for bit at repair=0, with either pass of an overflowed
+    super map; repair on gives the serial recurrence (the three-level pipeline itself,
+    scan_forward_v4_maps, and scan_forward_v4's converged dispatch)."""
     T, N, C, G = 2048, 777, 64, 8
     I = normal(T, N, mu, sd, 25)
     u0 = uniform(N, -0.3, 0.3, 26)
     Ig, u0g = gpu(I, dev), gpu(u0, dev)
     Us, Ss = O.serial_forward(I, beta, 1.0, -0.1, u0)
     for K, K2 in ((16, 32), (8, 16), (4, 4)):
-        print(f"v4 beta={beta} mu={mu} K={K} K2={K2}", flush=True)
+        print(f"v4 beta={beta} mu={mu} K={K} K2={K2} fallback={fallback}", flush=True)
         st, sto, keep = {}, {}, {}
-        U, S = L.scan_forward_v4(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, stats=st)
+        U, S = L.scan_forward_v4(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, stats=st,
+                                 super_fallback=fallback)
         run = L.last_scan_run()
-        Uo, So = O.scan_forward_v4(I, beta, 1.0, -0.1, u0, C=C, G=G, K=K, K2=K2, stats=sto, keep=keep)
+        Uo, So = O.scan_forward_v4(I, beta, 1.0, -0.1, u0, C=C, G=G, K=K, K2=K2, stats=sto, keep=keep,
+                                   super_fallback=fallback)
         assert np.array_equal(host(run.view("LO")), keep["Lo"])
         assert np.array_equal(host(run.view("MN", torch.int32)), keep["n"])
         assert np.array_equal(host(run.view("OVF", torch.int32)), keep["ovf"])
@@ -400,6 +406,9 @@ def test_scan_v4_matches_oracle(L, dev, beta, mu, sd):
         assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
         for k in sto:
             assert st[k] == pytest.approx(sto[k], rel=1e-12), k
+        U2, S2 = L.scan_forward_v4_maps(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, repair=10 ** 6,
+                                        super_fallback=fallback)
+        assert np.array_equal(host(U2), Us) and np.array_equal(host(S2), Ss)
         U2, S2 = L.scan_forward_v4(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
         assert np.array_equal(host(U2), Us) and np.array_equal(host(S2), Ss)
 

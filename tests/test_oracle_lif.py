@@ -437,3 +437,53 @@ def test_scan_v4_super_starts_match_serial_where_maps_are_exact():
     exact = np.concatenate([u0[None], Us[C * G - 1:-1:C * G]], 0)
     frac = (keep["sstarts"] == exact).mean()
     assert frac > 0.99
+
+
+@pytest.mark.parametrize("fallback", ["chunks", "serial"])
+def test_carry_super_fallbacks_exact_on_dyadic_inputs(fallback):
+    """beta = 1/2 and inputs on a 1/4 grid, with spikes often enough that every fp32 state is
+    exact (checked against the rational recurrence first): every map evaluation is then exact,
+    so the super starts equal the serial states at every super boundary, for both ways of
+    passing an overflowed super map (capacity 1 for chunk and super maps: 74% of the super maps
+    and 26% of the chunk maps overflow, so the walk evaluates chunk maps and runs chunks
+    serially)."""
+    rng = np.random.default_rng(31)
+    C, G, M2, N = 4, 4, 16, 64
+    T = C * G * M2
+    cols = [_dyadic_case(rng, T, -4, 9, den=4) for _ in range(N)]
+    I = np.array([[float(c[t]) for c in cols] for t in range(T)], dtype=np.float32)
+    u0 = np.zeros(N, np.float32)
+    Us, _ = O.serial_forward(I, 0.5, 1.0, 0.0, u0)
+    for j in range(N):  # precondition: the fp32 recurrence is the exact one
+        us, _ = _serial_exact(cols[j], Fr(1, 2), Fr(1), Fr(0), Fr(0))
+        assert [Fr(float(v)) for v in Us[:, j]] == us
+    keep = {}
+    O.scan_forward_v4(I, 0.5, 1.0, 0.0, u0, C=C, G=G, K=1, K2=1, keep=keep, super_fallback=fallback)
+    assert keep["SOVF"].mean() > 0.5 and keep["ovf"].mean() > 0.1
+    exact = np.concatenate([u0[None], Us[C * G - 1:-1:C * G]], 0)
+    assert np.array_equal(keep["sstarts"], exact)
+
+
+def test_carry_super_chunks_continues_the_inner_carry():
+    """With the "chunks" fallback the start of the super map after an overflowed one is the
+    state the inner carry reaches at the end of the overflowed one (its last chunk start
+    carried through its last chunk map, or that chunk's serial steps where it overflowed); with
+    "serial" it is the serial state instead."""
+    T, N, C, G = 4096, 96, 64, 8
+    I = normal(T, N, 0.012, 0.08, 33)
+    u0 = uniform(N, 0.0, 1.0, 34)
+    for fallback in ("chunks", "serial"):
+        keep = {}
+        O.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=8, K2=8, keep=keep, super_fallback=fallback)
+        assert keep["SOVF"].mean() > 0.2
+        starts, ss = keep["starts"], keep["sstarts"]
+        M2 = ss.shape[0]
+        for s_ in range(M2 - 1):
+            m = s_ * G + G - 1
+            end = O.eval_map(keep["A"][m], keep["B"][m], keep["xd"][m], keep["cd"][m], keep["n"][m], starts[m])
+            ser = O.serial_segment(I[m * C:(m + 1) * C], 0.99, 1.0, 0.0, starts[m])
+            end = np.where(keep["ovf"][m] > 0, ser, end)
+            full = O.serial_segment(I[s_ * C * G:(s_ + 1) * C * G], 0.99, 1.0, 0.0, ss[s_])
+            bad = keep["SOVF"][s_] > 0
+            want = end if fallback == "chunks" else full
+            assert np.array_equal(ss[s_ + 1][bad], want[bad]), (fallback, s_)

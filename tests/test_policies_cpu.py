@@ -10,6 +10,13 @@ def test_auto_modes_follow_mi355x_measurements():
     assert L.auto_modes(65536, 4096) == ("serial", "scan")
     assert L.auto_modes(1024, 4096) == ("serial", "scan")
     assert L.auto_modes(65536, 128) == ("serial", "serial")
+    # the grid of the reference's experiments/e11_auto.py: the serial adjoint below 16384
+    # neurons up to T = 1024, the scan from T = 2048, and from 16384 neurons from T = 256
+    assert L.auto_modes(1024, 1024) == ("serial", "serial")
+    assert L.auto_modes(8192, 1024) == ("serial", "serial")
+    assert L.auto_modes(8192, 2048) == ("serial", "scan")
+    assert L.auto_modes(32768, 1024) == ("serial", "scan")
+    assert L.auto_modes(16384, 256) == ("serial", "scan")
 
 
 def test_chunked_bwd_chunk_choice():
@@ -60,9 +67,9 @@ def test_auto_policies_accept_lengths_the_chunk_policy_rejects():
     for T in (1000, 1032, 257, 1002):
         assert L._recompute_ok(T, 65536, 16, 10 ** 6) is False
         assert L._recompute_ok(T, 4096, 16, T) is False
-    assert L.auto_modes(4096, 1000) == ("serial", "scan")
-    assert L.auto_modes(4096, 1032) == ("serial", "scan")
-    assert L.auto_modes(4096, 1002) == ("serial", "serial")
+    assert L.auto_modes(16384, 1000) == ("serial", "scan")
+    assert L.auto_modes(16384, 1032) == ("serial", "scan")
+    assert L.auto_modes(16384, 1002) == ("serial", "serial")
     assert L.auto_modes(1024, 16386) == ("serial", "serial")   # 16386 = 2 * 8193
     assert L.auto_modes(1024, 16392) == ("serial", "scan")     # chunk 8 for the adjoint only
     assert L._recompute_ok(4096, 65536, 16, 10 ** 6) is True

@@ -35,7 +35,7 @@ def test_v4_odd_super_map_count(dev, K, K2):
     assert np.array_equal(host(run.view("STARTS")), keep["starts"])
     assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
     Us, Ss = O.serial_forward(I, beta, 1.0, 0.0, u0)
-    U, S = L.scan_forward_v4(Ig, beta, 1.0, 0.0, u0g, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
+    U, S = L.scan_forward_v4_maps(Ig, beta, 1.0, 0.0, u0g, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
     assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
 
 
@@ -127,31 +127,38 @@ def test_v3_wave_carry_full_rows_and_overflow(dev, C, K):
     print(f"  stats {st}", flush=True)
 
 
-@pytest.mark.parametrize("N,K,K2", [(70, 4, 8), (70, 16, 32), (2113, 4, 8)])
-def test_v4_walks_windows_and_fallback(dev, N, K, K2):
+@pytest.mark.parametrize("fallback", ["chunks", "serial"])
+@pytest.mark.parametrize("N,K,K2", [(70, 4, 8), (70, 16, 32), (70, 32, 32), (2113, 4, 8), (2113, 16, 16)])
+def test_v4_walks_windows_and_fallback(dev, N, K, K2, fallback):
     """v4's envelope walk and super-map carry at few neurons (one wave per neuron, maps in
     windows of 64) and just above them (one lane per neuron): 150 super maps of G = 5 chunks of
-    C = 20 steps (an overflowed super map's fallback reads 64 rows, then 36), overflowed super
-    maps at small K2.  LO, super starts, chunk starts, U, S and the stats equal the oracle's
-    bit for bit."""
+    C = 20 steps, overflowed super maps at small K2, passed by their serial steps (the fallback
+    reads 64 rows, then 36) or by walking their chunk maps (rows of 16 or 32 lanes on the wave
+    path, overflowed chunk maps among them at K 4).  LO, super starts, chunk starts, U, S and
+    the stats equal the oracle's bit for bit."""
     from lifscan import hip_lif as L
     C, G, M2, beta = 20, 5, 150, 0.99
     T = C * G * M2
     I = normal(T, N, 0.012, 0.08, 59)
     u0 = uniform(N, 0.0, 1.0, 60)
-    print(f"v4 walks windows N={N} K={K} K2={K2}", flush=True)
+    print(f"v4 walks windows N={N} K={K} K2={K2} fallback={fallback}", flush=True)
     st, sto, keep = {}, {}, {}
-    U, S = L.scan_forward_v4(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=C, G=G, K=K, K2=K2, stats=st)
+    U, S = L.scan_forward_v4(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=C, G=G, K=K, K2=K2, stats=st,
+                             super_fallback=fallback)
     run = L.last_scan_run()
-    Uo, So = O.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, stats=sto, keep=keep)
+    Uo, So = O.scan_forward_v4(I, beta, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, stats=sto, keep=keep,
+                               super_fallback=fallback)
     assert np.array_equal(host(run.view("LO")), keep["Lo"])
     assert np.array_equal(host(run.view("SSTARTS")), keep["sstarts"])
     assert np.array_equal(host(run.view("STARTS")), keep["starts"])
     assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
     for k in sto:
         assert st[k] == pytest.approx(sto[k], rel=1e-12), k
-    if K2 == 8:
+    if K2 <= 16:
         assert keep["SOVF"].mean() > 0.01
+    if K == 4:
+        assert keep["ovf"].mean() > 0.01
+    print(f"  super overflow {keep['SOVF'].mean():.3f}, chunk overflow {keep['ovf'].mean():.3f}", flush=True)
 
 
 @pytest.mark.parametrize("N", [1, 5, 2048])

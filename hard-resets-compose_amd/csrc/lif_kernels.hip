@@ -804,6 +804,8 @@ __global__ __launch_bounds__(256) void k_lif_repair(const float* __restrict__ I,
 // are the serial recurrence, as after the Jacobi rounds, but a run of d consecutive wrong
 // starts costs one pass over them instead of d rounds.  Starts and ends are read PF chunks
 // ahead; they are not written (the converged result is U and S).
+// gate: when not null, the pass runs only if *gate != 0 (the segmented repair's last round
+// still rewrote a segment's last end, so its rounds may not have converged).
 template <int PF>
 __global__ __launch_bounds__(64) void k_lif_repair_ordered(const float* __restrict__ I,
                                                            float* __restrict__ U,
@@ -811,7 +813,9 @@ __global__ __launch_bounds__(64) void k_lif_repair_ordered(const float* __restri
                                                            const float* __restrict__ starts,
                                                            const float* __restrict__ ends,
                                                            int64_t N, int M, int C, float beta,
-                                                           float theta, float u_r) {
+                                                           float theta, float u_r,
+                                                           const int* gate = nullptr) {
+  if (gate != nullptr && __builtin_nontemporal_load(gate) == 0) return;
   const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
   const bool valid = n < N;
   const int64_t nc = valid ? n : N - 1;  // tail lanes read a valid column and never replay
@@ -869,7 +873,8 @@ __global__ __launch_bounds__(64) void k_lif_repair_ordered(const float* __restri
 // segment r - 2, which round r did not change), so S rounds give the serial recurrence; a
 // round in which no segment rewrote its last chunk's end leaves every boundary as the next
 // segment read it, so later rounds find nothing to do: flags[r] records whether round r
-// rewrote one, and round r + 1 returns at once when it did not.  A segment may read its
+// rewrote one, and round r + 1 returns at once when it did not.  The launcher runs at most
+// kRepairSegRounds rounds and then the whole ordered walk, gated on the last round's flag.  A segment may read its
 // boundary before or after the segment before it rewrites it in the same round; either way it
 // walks a consistent trajectory from the value it read, and the next round compares again.
 // flags[0 .. S] are zero before round 0.
@@ -1148,28 +1153,36 @@ void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* 
 }
 
 // The segmented ordered repair (k_lif_repair_seg): from this many chunks, with fewer neurons
-// than the ordered pass needs; segments of at least kRepairSegMinR chunks, at most
-// kRepairSegMax of them (one launch each at worst), about kRepairSegWaves waves a round.
-// LSH_REPAIR_SEG=0 in the environment turns it off (the Jacobi rounds run instead), for
-// measurements.
-constexpr int kRepairSegMinM = 64;
-constexpr int kRepairSegMinR = 16;
-constexpr int kRepairSegMax = 64;
-constexpr int kRepairSegWaves = 2048;
+// than the ordered pass needs; at most kRepairSegRounds rounds, then the ordered walk over all
+// chunks if the last round still changed a boundary (a run of wrong starts across more
+// segment boundaries than that).  LSH_REPAIR_SEG=0 in the environment turns it off (the
+// Jacobi rounds run instead), for measurements.
+constexpr int kRepairSegMinM = 1024;
+constexpr int kRepairSegMinR = 64;
+constexpr int kRepairSegRounds = 32;
+
+static int env_int(const char* name, int dflt) {
+  const char* e = getenv(name);
+  return e && e[0] ? atoi(e) : dflt;
+}
 
 static bool repair_seg_enabled() {
-  static const bool on = [] {
-    const char* e = getenv("LSH_REPAIR_SEG");
-    return !(e && e[0] == '0');
-  }();
+  static const bool on = env_int("LSH_REPAIR_SEG", 1) != 0;
   return on;
 }
 
+// Segments of kRepairSegMinR chunks (LSH_REPAIR_SEG_R overrides it, for measurements).
+// Measured on MI355X (beta 0.99, x ~ N(0.012, 0.08^2), N 1024, T 2^20; the v4 pipeline at the
+// reference default / the map scan at C 64): segments of 4, 8, 16, 64 chunks 26.9 / 23.7,
+// 26.1 / 22.8, 25.4 / 22.4, 24.9 / 22.0 ms against 85.9 / 82.6 with the Jacobi rounds: the
+// first round replays about as much as the replay itself (43 % of the starts are wrong, and a
+// wave walks a chunk until its last lane meets the stored trajectory), whatever the segment.
+// With 256 chunks (N 128 / 1024, T 65536, C 256) the Jacobi rounds were 2-4 % faster, so the
+// segments start at kRepairSegMinM chunks.
 static int repair_seg_count(int NB, int M) {
-  int sg = kRepairSegWaves / NB;
-  sg = min(sg, (M - 1) / kRepairSegMinR);
-  sg = min(sg, kRepairSegMax);
-  return max(sg, 1);
+  static const int r = max(1, env_int("LSH_REPAIR_SEG_R", kRepairSegMinR));
+  (void)NB;
+  return max((M - 1) / r, 1);
 }
 
 // The device repair rounds alone, after a replay that wrote U, S and ends from starts.
@@ -1187,17 +1200,22 @@ void lif_repair_launch(const float* I, float* U, float* S, float* starts, float*
     const int NB = (int)((N + WAVE - 1) / WAVE);
     if ((N >= 4096 && M >= 64) || (N >= 32768 && M >= 32)) {
       hipLaunchKernelGGL(k_lif_repair_ordered<8>, dim3((unsigned)NB), dim3(WAVE), 0, st, I, U,
-                         S, starts, ends, N, M, C, beta, theta, u_r);
+                         S, starts, ends, N, M, C, beta, theta, u_r, (const int*)nullptr);
       return;
     }
     if (M >= kRepairSegMinM && repair_seg_enabled()) {
       // few neurons, many chunks: the ordered walk over segments, one round per launch
       const int SG = repair_seg_count(NB, M);
       const int R = (M - 1 + SG - 1) / SG;
-      fill_i32_launch(list0, SG, 0, st);
-      for (int r = 0; r < SG; ++r)
+      const int rounds = min(SG, kRepairSegRounds);
+      fill_i32_launch(list0, rounds, 0, st);
+      for (int r = 0; r < rounds; ++r)
         hipLaunchKernelGGL(k_lif_repair_seg<8>, dim3((unsigned)((int64_t)SG * NB)), dim3(WAVE), 0,
                            st, I, U, S, starts, ends, list0, N, M, C, R, NB, r, beta, theta, u_r);
+      if (rounds < SG)
+        hipLaunchKernelGGL(k_lif_repair_ordered<8>, dim3((unsigned)NB), dim3(WAVE), 0, st, I, U,
+                           S, starts, ends, N, M, C, beta, theta, u_r,
+                           (const int*)(list0 + rounds - 1));
       return;
     }
     repair = M;

@@ -1,6 +1,6 @@
 """GPU parity of the repair run to convergence without its round count (repair = -1 at the C
-ABI: k_lif_repair_ordered where the launcher picks it, with fewer neurons and at least 64 chunks
-the segmented ordered walk k_lif_repair_seg, else Jacobi rounds to convergence).
+ABI: k_lif_repair_ordered where the launcher picks it, with fewer neurons and at least 1024
+chunks the segmented ordered walk k_lif_repair_seg, else Jacobi rounds to convergence).
 
 Bar: U and S equal the serial recurrence (oracle/lif_oracle.serial_forward) bit for bit, for
 the two-level scan, the scan with a caller-given bound, the associative carry and the
@@ -18,7 +18,7 @@ from tests._inputs import gpu, host, normal, uniform
 pytestmark = pytest.mark.gpu
 
 # (T, N, C): the first two take the ordered pass (N >= 4096 and T/C >= 64), the last the
-# segmented walk (few neurons, 128 chunks)
+# Jacobi rounds (few neurons, 128 chunks)
 SHAPES = [(4096, 4160, 32), (4096, 4100, 64), (8192, 130, 64)]
 
 
@@ -90,25 +90,28 @@ def test_python_rejects_negative_repair(dev):
             fn()
 
 
-@pytest.mark.parametrize("N", [5, 70, 200])
-def test_segmented_repair_long_dirty_runs(dev, N):
+@pytest.mark.parametrize("T,N,beta,mu,sd", [(16384, 5, 0.999, 2e-4, 0.01), (16384, 70, 0.999, 2e-4, 0.01),
+                                             (16384, 200, 0.999, 2e-4, 0.01), (65536, 5, 0.9999, 1e-4, 1e-3)])
+def test_segmented_repair_long_dirty_runs(dev, T, N, beta, mu, sd):
     """The segmented ordered walk when the carried starts are wrong for hundreds of chunks in a
-    row: beta = 0.999 and x ~ N(2e-4, 0.01^2) leave the neurons below threshold for most of the
-    sequence, so the chunk maps' affine pieces give starts that differ from the stepwise states
-    in their last bits across whole runs of segment boundaries (1023 chunks in 63 segments of
-    17): the rounds must carry the exact state from segment to segment.  U and S equal the
+    row: beta near 1 and inputs far below threshold leave the neurons subthreshold for most of
+    the sequence, so the chunk maps' affine pieces give starts that differ from the stepwise
+    states in their last bits across whole runs of segment boundaries (C = 16: 1023 chunks in
+    15 segments of 69; the Jacobi rounds need about 500).  The last case (4095 chunks in 63
+    segments of 65, 7 spikes in all: runs of about 2600 chunks) needs more than the 32 rounds
+    the launcher runs, so the gated ordered walk over all chunks finishes it.  U and S equal the
     serial recurrence and the Jacobi rounds' result (with statistics)."""
     from lifscan import hip_lif as L
-    T, C, beta = 16384, 16, 0.999
-    I = normal(T, N, 2e-4, 0.01, 47)
+    C = 16
+    I = normal(T, N, mu, sd, 47)
     u0 = uniform(N, 0.0, 0.5, 48)
     Us, Ss = O.serial_forward(I, beta, 1.0, 0.0, u0)
     Ig, u0g = gpu(I, dev), gpu(u0, dev)
-    print(f"segmented repair N={N}", flush=True)
+    print(f"segmented repair T={T} N={N} beta={beta}", flush=True)
     U, S = L.scan_forward_mapscan(Ig, beta, 1.0, 0.0, u0g, C=C, K=8, repair=10 ** 6)
     assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss)
     st = {}
     Uj, Sj = L.scan_forward_mapscan(Ig, beta, 1.0, 0.0, u0g, C=C, K=8, repair=10 ** 6, stats=st)
     assert torch.equal(U, Uj) and torch.equal(S, Sj)
     print(f"  Jacobi rounds {st['repair_iters']}", flush=True)
-    assert st["repair_iters"] > 17  # dirty runs longer than a segment
+    assert st["repair_iters"] > 69  # dirty runs longer than a segment

@@ -1197,6 +1197,9 @@ void lif_repair_launch(const float* I, float* U, float* S, float* starts, float*
     // T = 4096: C = 32 8.78 -> 3.52 ms, C = 64 5.02 -> 3.31, C = 128 2.59 -> 2.32, C = 256
     // 1.58 vs 1.65 (Jacobi); N = 8192: C = 32 1.15 -> 0.85, C = 128 0.47 vs 0.75 (Jacobi);
     // N = 1024, T = 65536, C = 256: 3.63 vs 5.77 (Jacobi, 16 waves).
+    // (segments of the ordered walk did not pay with many neurons: N = 65536, T = 4096,
+    // beta 0.99, C 32, 1024 waves walking 128 chunks each 3.39 ms, 4096 to 16384 waves in
+    // segments of 8 or 16 chunks 3.84-4.34 ms; the walk is bound by the replays, not by waves)
     const int NB = (int)((N + WAVE - 1) / WAVE);
     if ((N >= 4096 && M >= 64) || (N >= 32768 && M >= 32)) {
       hipLaunchKernelGGL(k_lif_repair_ordered<8>, dim3((unsigned)NB), dim3(WAVE), 0, st, I, U,

@@ -21,9 +21,12 @@
 //   3. the same DPP scan composes the truncated maps, segmented at overflowed chunks (an
 //      overflowed chunk starts a segment whose map is applied to that chunk's exit); wave 0
 //      composes the wave totals the same way.  A map's breakpoint/constant slots live in LDS
-//      (one region per lane, two buffers), so DPP moves only a map's scalars and the address
-//      of its slots, and a composition reads the other map's slots from LDS with binary
-//      searches over the descending breakpoints;
+//      (one region per lane, two buffers; breakpoints and constants in separate arrays, so a
+//      wave's access to one slot of 64 regions is 64 consecutive 4-byte words, one per bank:
+//      the float2 slots of an earlier layout stalled 47 % of the LDS cycles on bank
+//      conflicts, this one 1 %), so DPP moves only a map's scalars and the address of its
+//      slots, and a composition reads the other map's slots from LDS with binary searches
+//      over the descending breakpoints;
 //   4. chunk starts: without overflowed chunks in the tile, every lane evaluates its prefix map
 //      at the tile's entry state at once; otherwise the overflowed chunks are run serially in
 //      order (C steps of the recurrence from their start) and each segment is evaluated after
@@ -42,7 +45,7 @@ constexpr int MS_WG = 4;   // most waves per workgroup (chunks per tile = 64 * W
                            // buffers take 2 x WG x 64 lanes x KS x 8 B = 128 KB of LDS
 
 // A scanned element: a map over a run of chunks and the domain's lower bound; its slots
-// (breakpoint, constant) are pool[base + i*stride], i < n, breakpoints descending.
+// (breakpoint, constant) are (px, pc)[base + i*stride], i < n, breakpoints descending.
 //   HEAD: the run contains an overflowed chunk; the map takes the exit state of the last one.
 //   BAD : a composition in the run exceeded MS_KS breakpoints (the map is incomplete).
 constexpr int MS_HEAD = 1, MS_BAD = 2;
@@ -52,51 +55,57 @@ struct SMap {
   int n, flags, base, stride;
 };
 
-// #{i < n : pool[base + i*stride].x > u} for descending breakpoints (binary search)
-__device__ __forceinline__ int ms_count_gt(const float2* pool, int base, int stride, int n,
+// #{i < n : px[base + i*stride] > u} for descending breakpoints (binary search).  The
+// breakpoints and the constants are separate arrays, so the searches read 4 bytes a lane.
+__device__ __forceinline__ int ms_count_gt(const float* px, int base, int stride, int n,
                                            float u) {
   int lo = 0, hi = n;
   while (lo < hi) {
     const int mid = (lo + hi) >> 1;
-    if (pool[base + mid * stride].x > u) lo = mid + 1;
+    if (px[base + mid * stride] > u) lo = mid + 1;
     else hi = mid;
   }
   return lo;
 }
 
 // Map evaluation (triton_lif.py:592-599): k = #{xd > u}; k == n -> A*u + B, else cd[k].
-__device__ __forceinline__ float ms_eval(const float2* pool, const SMap& f, float u) {
-  const int k = ms_count_gt(pool, f.base, f.stride, f.n, u);
-  return k == f.n ? __fadd_rn(__fmul_rn(f.A, u), f.B) : pool[f.base + k * f.stride].y;
+__device__ __forceinline__ float ms_eval(const float* px, const float* pc, const SMap& f, float u) {
+  const int k = ms_count_gt(px, f.base, f.stride, f.n, u);
+  return k == f.n ? __fadd_rn(__fmul_rn(f.A, u), f.B) : pc[f.base + k * f.stride];
 }
 
 // g <- g after H (H first), the result's slots written at (ob, os), unless g already starts
-// at an overflowed chunk (then g is kept).  Returns whether it composed.
-__device__ __forceinline__ bool ms_compose(float2* pool, const SMap& H, SMap& g, int ob, int os,
-                                           float hi) {
+// at an overflowed chunk (then g is kept).  Returns whether it composed.  Counting g's
+// breakpoints with compares over registers instead of the binary searches was slower on
+// MI355X (cfg4, C 2048: 1.21 against 0.87 ms): the searches' LDS waits are not what the kernel
+// waits on.
+__device__ __forceinline__ bool ms_compose(float* px, float* pc, const SMap& H, SMap& g, int ob,
+                                           int os, float hi) {
   if (g.flags & MS_HEAD) return false;
   // (1) H's breakpoints, with H's constants pushed through g
   float xmin = INFINITY;
   for (int i = 0; i < H.n; ++i) {
-    const float2 hs = pool[H.base + i * H.stride];
-    const int c = ms_count_gt(pool, g.base, g.stride, g.n, hs.y);
-    const float v = c == g.n ? __fadd_rn(__fmul_rn(g.A, hs.y), g.B) : pool[g.base + c * g.stride].y;
-    pool[ob + i * os] = make_float2(hs.x, v);
-    xmin = hs.x;
+    const float hx = px[H.base + i * H.stride], hc = pc[H.base + i * H.stride];
+    const int c = ms_count_gt(px, g.base, g.stride, g.n, hc);
+    const float v = c == g.n ? __fadd_rn(__fmul_rn(g.A, hc), g.B) : pc[g.base + c * g.stride];
+    px[ob + i * os] = hx;
+    pc[ob + i * os] = v;
+    xmin = hx;
   }
   // (2) g's breakpoints pulled back through H's affine part (kept below H's smallest
   // breakpoint, <= hi, while that one is above the domain's lower bound)
   int rn = H.n;
   int flags = H.flags | (g.flags & MS_BAD);
   for (int j = 0; j < g.n; ++j) {
-    const float2 gs = pool[g.base + j * g.stride];
-    const float num = __fsub_rn(gs.x, H.B);
+    const float gx = px[g.base + j * g.stride];
+    const float num = __fsub_rn(gx, H.B);
     const float z = H.A == 0.0f ? (num > 0.0f ? INFINITY : -INFINITY) : num / H.A;
     if ((z < xmin) && (z <= hi) && (xmin > H.lo)) {
       if (rn >= MS_KS) {
         flags |= MS_BAD;
       } else {
-        pool[ob + rn * os] = make_float2(z, gs.y);
+        px[ob + rn * os] = z;
+        pc[ob + rn * os] = pc[g.base + j * g.stride];
         ++rn;
         xmin = z;
       }
@@ -112,8 +121,8 @@ __device__ __forceinline__ bool ms_compose(float2* pool, const SMap& H, SMap& g,
 // before this lane's.  (ob0, ob1) are this lane's two slot regions (stride os); `cur` tells
 // which one holds its element.
 template <int CTRL, int RM>
-__device__ __forceinline__ void ms_level(float2* pool, SMap& f, bool active, int& cur, int ob0,
-                                         int ob1, int os, float hi) {
+__device__ __forceinline__ void ms_level(float* px, float* pc, SMap& f, bool active, int& cur,
+                                         int ob0, int ob1, int os, float hi) {
   auto mvf = [](float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, RM, 0xF, false));
   };
@@ -121,21 +130,21 @@ __device__ __forceinline__ void ms_level(float2* pool, SMap& f, bool active, int
   const SMap H{mvf(f.A), mvf(f.B), mvf(f.lo), mvi(f.n), mvi(f.flags), mvi(f.base), mvi(f.stride)};
   const int got = mvi(1);
   const int ob = cur == 0 ? ob1 : ob0;
-  if (got && active && ms_compose(pool, H, f, ob, os, hi)) cur ^= 1;
+  if (got && active && ms_compose(px, pc, H, f, ob, os, hi)) cur ^= 1;
   // the next level reads what this one wrote (one wave: LDS accesses complete in order)
   __builtin_amdgcn_wave_barrier();
 }
 
 // Inclusive scan of a wave's elements in lane order, segmented at heads.
-__device__ __forceinline__ void ms_wave_scan(float2* pool, SMap& f, bool active, int& cur, int ob0,
-                                             int ob1, int os, float hi) {
+__device__ __forceinline__ void ms_wave_scan(float* px, float* pc, SMap& f, bool active, int& cur,
+                                             int ob0, int ob1, int os, float hi) {
   __builtin_amdgcn_wave_barrier();
-  ms_level<0x111, 0xF>(pool, f, active, cur, ob0, ob1, os, hi);  // row_shr:1
-  ms_level<0x112, 0xF>(pool, f, active, cur, ob0, ob1, os, hi);  // row_shr:2
-  ms_level<0x114, 0xF>(pool, f, active, cur, ob0, ob1, os, hi);  // row_shr:4
-  ms_level<0x118, 0xF>(pool, f, active, cur, ob0, ob1, os, hi);  // row_shr:8
-  ms_level<0x142, 0xA>(pool, f, active, cur, ob0, ob1, os, hi);  // row_bcast:15 -> rows 1, 3
-  ms_level<0x143, 0xC>(pool, f, active, cur, ob0, ob1, os, hi);  // row_bcast:31 -> rows 2, 3
+  ms_level<0x111, 0xF>(px, pc, f, active, cur, ob0, ob1, os, hi);  // row_shr:1
+  ms_level<0x112, 0xF>(px, pc, f, active, cur, ob0, ob1, os, hi);  // row_shr:2
+  ms_level<0x114, 0xF>(px, pc, f, active, cur, ob0, ob1, os, hi);  // row_shr:4
+  ms_level<0x118, 0xF>(px, pc, f, active, cur, ob0, ob1, os, hi);  // row_shr:8
+  ms_level<0x142, 0xA>(px, pc, f, active, cur, ob0, ob1, os, hi);  // row_bcast:15 -> rows 1, 3
+  ms_level<0x143, 0xC>(px, pc, f, active, cur, ob0, ob1, os, hi);  // row_bcast:31 -> rows 2, 3
 }
 
 // Envelope maps l -> min(c, a*l + b): (c, a, b) after (c1, a1, b1).
@@ -181,8 +190,9 @@ __device__ __forceinline__ int wave_or_flags(int f) {
   return (__ballot(f & MS_HEAD) ? MS_HEAD : 0) | (__ballot(f & MS_BAD) ? MS_BAD : 0);
 }
 
-// LDS layout (float2 units): the in-wave slot regions [buf][wave][slot][lane], then the
-// totals scan's regions [buf][slot][lane] for lanes 0..MS_WG-2 of wave 0.
+// LDS layout (one float per slot, breakpoints in px and constants in pc at the same index):
+// the in-wave slot regions [buf][wave][slot][lane], then the totals scan's regions
+// [buf][slot][lane] for lanes 0..MS_WG-2 of wave 0.
 constexpr int MS_POOL_WAVE = 2 * MS_WG * MS_KS * WAVE;
 constexpr int MS_POOL = MS_POOL_WAVE + 2 * MS_KS * MS_WG;
 
@@ -193,7 +203,7 @@ __global__ __launch_bounds__(WAVE* MS_WG) void k_map_scan(
     const float* __restrict__ MX, const float* __restrict__ MC, float* __restrict__ LO,
     int* __restrict__ MN, int* __restrict__ OVF, float* __restrict__ starts, WsHeader* hdr,
     int64_t N, int M, int C, int K, float beta, float theta, float u_r) {
-  __shared__ float2 pool[MS_POOL];
+  __shared__ float px[MS_POOL], pc[MS_POOL];
   __shared__ SMap sTot[MS_WG];  // wave totals, then the exclusive prefixes of the waves
   __shared__ Env sEnv[MS_WG];
   __shared__ float sLo[MS_WG * WAVE];
@@ -249,13 +259,26 @@ __global__ __launch_bounds__(WAVE* MS_WG) void k_map_scan(
     int cur = 0;
     if (valid) {
       const int cnt = CNT[o];
-      const size_t os = (size_t)m * K * N + n;
+      const size_t os = (size_t)(valid ? m : 0) * K * N + n;
+      // every slot's loads issued before the first is used (K is the same on every lane; the
+      // slots past the count are loaded too, so no load waits for it), then the count's prefix
+      // goes to LDS
+      float xs[MS_KS], cs[MS_KS];
+#pragma unroll
+      for (int i = 0; i < MS_KS; ++i) {
+        if (i < K) {
+          xs[i] = MX[os + (size_t)i * N];
+          cs[i] = MC[os + (size_t)i * N];
+        }
+      }
       int gt = 0;
-      for (int i = 0; i < cnt && i < K; ++i) {
-        const float x = MX[os + (size_t)i * N];
-        const float c = MC[os + (size_t)i * N];
-        pool[ob0 + i * WAVE] = make_float2(x, c);
-        gt += x > lo ? 1 : 0;
+#pragma unroll
+      for (int i = 0; i < MS_KS; ++i) {
+        if (i < K && i < cnt) {
+          px[ob0 + i * WAVE] = xs[i];
+          pc[ob0 + i * WAVE] = cs[i];
+          gt += xs[i] > lo ? 1 : 0;
+        }
       }
       ne = min(cnt, gt + 1);
       ovf = OVFRAW[o] != 0 && gt == cnt;
@@ -275,7 +298,7 @@ __global__ __launch_bounds__(WAVE* MS_WG) void k_map_scan(
       pmax = max(pmax, ne);
     }
     // 3. inclusive segmented scan inside the wave; wave totals to LDS
-    ms_wave_scan(pool, f, true, cur, ob0, ob1, WAVE, hi);
+    ms_wave_scan(px, pc, f, true, cur, ob0, ob1, WAVE, hi);
     if (lane == WAVE - 1) sTot[w] = f;
     const int fl = wave_or_flags(f.flags);
     if (lane == 0 && fl) atomicOr(&sFlags, fl);
@@ -288,7 +311,7 @@ __global__ __launch_bounds__(WAVE* MS_WG) void k_map_scan(
       int tcur = 1;  // the first composition writes region 0
       const int tb0 = MS_POOL_WAVE + lane;
       const int tb1 = MS_POOL_WAVE + MS_KS * MS_WG + lane;
-      ms_wave_scan(pool, t, act, tcur, tb0, tb1, MS_WG, hi);
+      ms_wave_scan(px, pc, t, act, tcur, tb0, tb1, MS_WG, hi);
       const int tf = wave_or_flags(act ? t.flags : 0);
       if (lane == 0 && tf) atomicOr(&sFlags, tf);
       if (act) sTot[lane + 1] = t;  // all reads of sTot above came first (one wave, in order)
@@ -296,10 +319,12 @@ __global__ __launch_bounds__(WAVE* MS_WG) void k_map_scan(
     __syncthreads();
     const int tflags = sFlags;
     const float s_in = sState;
+    if (threadIdx.x == 0 && tflags != 0)  // tiles that leave the parallel evaluation (statistics)
+      atomicAdd((tflags & MS_BAD) ? &hdr->fused_unknown : &hdr->fused_fixups, 1ull);
     if (tflags == 0) {
       // 4a. no overflowed chunk, every composition complete: all chunks at once
-      const float s_w = (w == 0) ? s_in : ms_eval(pool, sTot[w], s_in);
-      sAfter[threadIdx.x] = valid ? ms_eval(pool, f, s_w) : 0.0f;
+      const float s_w = (w == 0) ? s_in : ms_eval(px, pc, sTot[w], s_in);
+      sAfter[threadIdx.x] = valid ? ms_eval(px, pc, f, s_w) : 0.0f;
     } else if ((tflags & MS_BAD) == 0) {
       // 4b. overflowed chunks (heads): waves in order, the heads of each wave in order; a head
       // runs its chunk serially from the exit of the chunk before it
@@ -307,7 +332,7 @@ __global__ __launch_bounds__(WAVE* MS_WG) void k_map_scan(
         if (w == v) {
           const float s_w = (v == 0) ? s_in : sAfter[v * WAVE - 1];
           unsigned long long hm = __ballot(valid && ovf);
-          float after = (f.flags & MS_HEAD) ? 0.0f : ms_eval(pool, f, s_w);
+          float after = (f.flags & MS_HEAD) ? 0.0f : ms_eval(px, pc, f, s_w);
           while (hm) {
             const int h = __builtin_ctzll(hm);
             hm &= hm - 1;
@@ -316,7 +341,7 @@ __global__ __launch_bounds__(WAVE* MS_WG) void k_map_scan(
             if (lane == h) xh = ms_serial(I, N, n, m, C, sh, beta, theta, u_r);
             xh = __shfl(xh, h, WAVE);
             const int h2 = hm ? __builtin_ctzll(hm) : WAVE;
-            if (lane >= h && lane < h2) after = ms_eval(pool, f, xh);
+            if (lane >= h && lane < h2) after = ms_eval(px, pc, f, xh);
           }
           sAfter[threadIdx.x] = valid ? after : 0.0f;
         }

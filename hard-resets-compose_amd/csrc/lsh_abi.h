@@ -35,8 +35,10 @@ struct WsHeader {
   unsigned long long alif_pieces_sum;  // ALIF: post-spike x-pieces kept
   unsigned int alif_pieces_max;
   unsigned int pad0;
-  unsigned long long fused_fixups;     // fused scan: speculative chunk entries that missed
-  unsigned long long fused_unknown;    // fused scan: entries the maps could not predict
+  unsigned long long fused_fixups;     // fused scan: speculative chunk entries that missed;
+                                       // map scan: tiles with overflowed chunks (run in order)
+  unsigned long long fused_unknown;    // fused scan: entries the maps could not predict;
+                                       // map scan: tiles whose composition exceeded capacity
   unsigned int spin_timeouts;          // bounded waits that gave up (must stay 0)
   unsigned int epoch;                  // advanced once per call
   unsigned int ticket;                 // look-back scans: next tile in launch order

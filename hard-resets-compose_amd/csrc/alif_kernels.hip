@@ -12,7 +12,8 @@
 // solved serially, as chunked two-level scans, or in one fused pass.
 //
 // Map layout (workspace): per-chunk scalars [M, N]; line and piece slots [M, N, K]
-// (slot-contiguous, so the 32 lanes of one neuron store 128 contiguous bytes).
+// (slot-contiguous, so the 32 lanes of one neuron store 128 contiguous bytes).  Only the slots
+// below the line and piece counts are written; the others keep whatever the workspace held.
 #include "lsh_abi.h"
 #include "lsh_common.h"
 #include "lsh_lookback.h"
@@ -648,24 +649,25 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
     NP[o] = npc;
     OVF[o] = ovf;
   }
+  // only the populated slots are stored (the carry reads every slot but uses only those below
+  // the counts): with 7 lines and 10 pieces a neuron on average, a third of the map bytes
 #pragma unroll
   for (int r = 0; r < 2; ++r) {
     const int slot = 16 * r + i;
-    if (slot < K1) {
+    if (slot < K1 && slot < nl) {
       const size_t os = o * K1 + slot;
       LS[os] = ls[r];
       LC[os] = lc[r];
       LX[os] = lx[r];
     }
-    if (slot < K2) {
+    if (slot < K2 && slot < npc) {
       const size_t os = o * K2 + slot;
       POWN[os] = pown[r];
       PXL[os] = pxl[r];
       PXR[os] = pxr[r];
-      const bool vs = slot < npc;  // the fields of an empty slot: (u, a, of) = (0, 1, 0)
-      PU[os] = vs ? pu[r] : 0.0f;
-      PA[os] = vs ? pa[r] : 1.0f;
-      POF[os] = vs ? pof[r] : 0.0f;
+      PU[os] = pu[r];
+      PA[os] = pa[r];
+      POF[os] = pof[r];
     }
   }
 }

@@ -294,8 +294,9 @@ int lsh_alif_warm_predict(const float* I, const float* u0, const float* w0, cons
 typedef struct lsh_alif_layout {
   size_t EC, EA, EB, LU, HU, LW, HW; /* envelope maps, box [M, N] */
   size_t MA, MB, NL, NP, OVF;        /* per-chunk scalars [M, N] (NL, NP, OVF int32) */
-  size_t LS, LC, LX;                 /* first-spike lines [M, N, K1] */
-  size_t POWN, PXL, PXR, PU, PA, POF; /* post-spike pieces [M, N, K2] (POWN int32) */
+  size_t LS, LC, LX;                 /* first-spike lines [M, N, K1], slots < NL written */
+  size_t POWN, PXL, PXR, PU, PA, POF; /* post-spike pieces [M, N, K2] (POWN int32), slots < NP
+                                         written */
   size_t SU, SW, EU, EW, MISS;       /* chunk entry / exit states, carry misses [M, N] */
   size_t MSTAR;                      /* [N] int32: first chunk whose start came through a map */
   size_t LIST0, LIST1;               /* repair work lists */

@@ -1355,6 +1355,30 @@ extern "C" int lsh_lif_scan_v3_fwd(const float* I, const float* u0, float* U, fl
 // VALU-bound builds of the later pieces.
 static constexpr int kMaxPieces = 64;
 
+// The fork/join events of the pieces path, per device, created on the first call that needs
+// them and kept until the process ends (no create/destroy per call).  A call holds its device's
+// lock while it records and waits on them, so calls from several host threads do not mix their
+// records (a wait takes the event's most recent record at the time it is enqueued).
+struct PiecesEvents {
+  std::mutex mu;
+  hipEvent_t ev[kMaxPieces + 1] = {};
+  int made = 0;
+};
+
+static PiecesEvents* pieces_events(int P) {
+  static PiecesEvents per_dev[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  PiecesEvents* pe = &per_dev[dev];
+  std::lock_guard<std::mutex> lock(pe->mu);
+  while (pe->made <= P) {
+    if (hipEventCreateWithFlags(&pe->ev[pe->made], hipEventDisableTiming) != hipSuccess)
+      return nullptr;
+    ++pe->made;
+  }
+  return pe;
+}
+
 static int pieces_check(int64_t T, int64_t N, int C, int K, int P, lsh_v3_layout* L,
                         size_t* piece_bytes) {
   if (P < 1 || P > kMaxPieces || C < 1) return LSH_ERR_SHAPE;
@@ -1391,13 +1415,12 @@ extern "C" int lsh_lif_scan_v3_pieces_fwd(const float* I, const float* u0, float
   char* w = static_cast<char*>(ws);
   const int64_t Tp = T / P;
   const int Mp = (int)(Tp / C);
-  hipEvent_t ev[kMaxPieces + 1];
-  int made = 0;
+  PiecesEvents* pe = pieces_events(P);
+  if (pe == nullptr) return LSH_ERR_HIP;
   bool ok = true;
-  for (; made <= P && ok; ++made)
-    ok = hipEventCreateWithFlags(&ev[made], hipEventDisableTiming) == hipSuccess;
-  if (!ok) made -= 1;  // the failed create made no event
-  if (ok) {
+  {
+    std::lock_guard<std::mutex> lock(pe->mu);
+    hipEvent_t* ev = pe->ev;
     // fork: the builds start after the work already queued on the caller's stream
     ok = hipEventRecord(ev[P], st) == hipSuccess && hipStreamWaitEvent(side, ev[P], 0) == hipSuccess;
     for (int p = 0; ok && p < P; ++p) {
@@ -1421,8 +1444,6 @@ extern "C" int lsh_lif_scan_v3_pieces_fwd(const float* I, const float* u0, float
                                reinterpret_cast<WsHeader*>(wp), N, Mp, C, Mp, beta, theta, u_r, st);
     }
   }
-  // an event recorded but not yet reached is released once it completes
-  for (int i = 0; i < made; ++i) (void)hipEventDestroy(ev[i]);
   if (!ok) return LSH_ERR_HIP;
   LSH_CHECK_LAUNCH();
   return LSH_OK;

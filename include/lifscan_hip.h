@@ -328,14 +328,18 @@ int lsh_lif_scan_lookback_bwd(const float* I, const float* u0, const float* U, c
 /* lsh_lif_scan_lookback_bwd with no workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  Its workspace is a static device array of
- * LSH_NOALLOC_SCRATCH_BYTES (64 MiB) that every device the library runs on holds until the process
- * ends; its address is looked up once per device (with that device current) on the first call.
+ * LSH_NOALLOC_SCRATCH_BYTES (64 MiB unless the library is built with another value) that every
+ * device the library's code object is loaded on holds until the process ends, whether or not the
+ * entry point is called; its address is looked up once per device (with that device current) on
+ * the first call.
  * Returns LSH_ERR_SCRATCH, launching nothing, when lsh_lif_scan_lookback_bwd_workspace(T, N)
  * exceeds it (about T * N <= 1.4e9 neuron-steps: N = 1024, T = 2^20 fits).  Calls no allocating
  * routine.  Every call on one device shares its array (the call clears what must start at zero):
  * calls that overlap on one device, from several streams or threads, race.  Same outputs as
  * lsh_lif_scan_lookback_bwd, bit for bit. */
+#ifndef LSH_NOALLOC_SCRATCH_BYTES
 #define LSH_NOALLOC_SCRATCH_BYTES (64u << 20)
+#endif
 int lsh_lif_scan_lookback_bwd_noalloc(const float* I, const float* u0, const float* U,
                                       const float* S, const float* GS, const float* GU, float* Lam,
                                       int64_t T, int64_t N, float beta, float theta, float u_r,

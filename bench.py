@@ -154,9 +154,12 @@ def bench_auto_grid(torch, dev, reps=15):
     LIF layer's forward + backward through autograd with library defaults at N in {128, 1024,
     8192, 32768, 131072} x T in {1024, 4096, 16384, 65536}, N*T <= 2^28, x ~ N(0.15, 0.4^2),
     beta 0.9, u0 = 0, G ~ N(0, 1): lif_tuned(mode="serial"), lif_tuned(mode="scan", repair=0)
-    and lif_auto, HIP events, median.  Per cell: the three times, auto's modes, whether the
-    spikes of all three are equal and auto's gradient against serial's; auto_vs_best = auto's
-    time over the faster of the two modes."""
+    and lif_auto.  Each time is ms per call of calls run back to back between two HIP events (as
+    a training loop runs them; at the smallest cells a call is ~10 us of GPU work and one call
+    between two synchronizations measures the host's latency instead), groups of the three modes
+    interleaved so that clock drift favours none, median of 7 groups.  Per cell: the three times,
+    auto's modes, whether the spikes of all three are equal and auto's gradient against serial's;
+    auto_vs_best = auto's time over the faster of the two modes."""
     from lifscan import hip_lif as L
     rows = []
     for N in (128, 1024, 8192, 32768, 131072):
@@ -171,18 +174,36 @@ def bench_auto_grid(torch, dev, reps=15):
                    "scan": lambda I: L.lif_tuned(I, u0, beta=0.9, mode="scan", repair=0),
                    "auto": lambda I: L.lif_auto(I, u0, beta=0.9)}
             res = {}
+            steps = {}
             for name, f in fns.items():
                 I = I0.clone().requires_grad_(True)
 
-                def step():
+                def step(f=f, I=I):
                     I.grad = None
                     f(I).backward(G)
-                t = ev_time(step, reps, warm=2)
+                for _ in range(3):
+                    step()
+                steps[name] = step
                 I.grad = None
                 s = f(I)
                 s.backward(G)
-                res[name] = (t, s.detach(), I.grad.clone())
-                del I
+                res[name] = [None, s.detach(), I.grad.clone()]
+            times = {name: [] for name in fns}
+            calls = 20 if N * T <= 2 ** 24 else 5
+            for _ in range(7):
+                for name, step in steps.items():
+                    torch.cuda.synchronize()
+                    a = torch.cuda.Event(enable_timing=True)
+                    b = torch.cuda.Event(enable_timing=True)
+                    a.record()
+                    for _ in range(calls):
+                        step()
+                    b.record()
+                    torch.cuda.synchronize()
+                    times[name].append(a.elapsed_time(b) / calls)
+            for name in fns:
+                res[name][0] = statistics.median(times[name])
+            del steps
             gs = res["serial"][2]
             best = min(res["serial"][0], res["scan"][0])
             rows.append({"N": N, "T": T, "modes": list(L.auto_modes(N, T)),
@@ -1084,8 +1105,9 @@ def main():
                    "N": N, "T": T, "beta": beta, "internal_chunk": L.FUSED_FWD_C, "maps": False},
         "bytes_per_neuron_step": B_FWD_RC + B_BWD_RC,
         "roofline_basis": "20 B per neuron-step, the bytes the recomputing pair moves (fwd: read I, "
-                          "write S and 1/32 row of entry states; bwd: read I, gS, write dI).  SURVEY "
-                          "8(d)'s 32 B counts U written and re-read, which lif_tuned never exposes: "
+                          "write S and 1/32 row of entry states; bwd: read I, gS, write dI).  The "
+                          "32 B basis of the stored path counts U written and re-read, which "
+                          "lif_tuned never exposes: "
                           "on that basis this step would be above the HBM peak; the stored-U passes "
                           "are reported on it in stored_U_path",
         "pct_roofline_fwd_bwd": pct(B_FWD_RC + B_BWD_RC, ms_step),

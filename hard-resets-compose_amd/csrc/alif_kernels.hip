@@ -313,8 +313,9 @@ constexpr int kAlifTS = 32;   // steps per tile (LDS: 5 x 16 neurons x 33 floats
 
 // Waves per SIMD the build is compiled for (registers <= 512 / WPE per lane).  Measured at cfg5
 // (N 16384, T 4096, BN 4, dw 0.1q / 0.3q) with the per-wave tile phases: 6 (80 VGPRs) 1.68 /
-// 2.13 ms, 7 (72 VGPRs, more spilled) 1.88 / 2.32 ms.  The steps are latency-bound (about a
-// third of the SIMD's VALU issue used), so fewer spills count for more than a seventh wave.
+// 2.13 ms, 7 (72 VGPRs, more spilled) 1.88 / 2.32 ms.  The kernel is VALU-bound (at cfg5 its
+// 8566 VALU instructions per wave, at 4 cycles each, fill the SIMDs' issue cycles over the
+// launch), so a seventh wave hides nothing and its extra spills cost instructions.
 #ifndef LSH_ALIF_BUILD_WPE
 #define LSH_ALIF_BUILD_WPE 6
 #endif

@@ -29,12 +29,22 @@ __global__ void k_ws_header_reset(WsHeader* h) {
 //   serial forward: one segment (M = 1, Ls = T, starts = u0);
 //   scan replay   : M = T / C segments of Ls = C steps, starts = carried chunk entries.
 // Follows triton_lif.py:354-379 (fwd_tiled_kernel) and :152-165 (replay_kernel).
+// Rows per tile of the carries' exact fallbacks (converged calls).  Measured at cfg2, beta 0.99,
+// the whole map scan at C 32 / 64 / 128: 16 rows 2.44 / 2.04 / 1.20 ms, 32 rows 2.36 / 1.84 /
+// 1.21 ms (64 rows: more than a 32-step chunk, which then loads row by row).  Loading the next
+// chunk's first rows while a chunk's last ones are walked (overflows come in runs) was slower,
+// 2.78 / 2.28 ms: the rows kept across chunks cost the carries their registers.
+constexpr int kFbRows = 32;
+// done (or null): one flag per (chunk, 64-neuron block), set where the carry has already
+// replayed the block's chunk from its start (U, S and the end written); those blocks return.
 template <int D>
 __global__ __launch_bounds__(64) void k_lif_fwd(const float* __restrict__ I,
                                                 const float* __restrict__ starts,
                                                 float* __restrict__ U, float* __restrict__ S,
                                                 float* __restrict__ ends, int64_t N, int64_t Ls,
-                                                int NB, float beta, float theta, float u_r) {
+                                                int NB, float beta, float theta, float u_r,
+                                                const int* __restrict__ done = nullptr) {
+  if (done && done[blockIdx.x] != 0) return;
   const int64_t m = blockIdx.x / NB;
   const int nb = (int)(blockIdx.x - m * NB);
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
@@ -385,7 +395,8 @@ __global__ __launch_bounds__(64) void k_lif_carry(
     const float* __restrict__ MX, const float* __restrict__ MC,
     const float* __restrict__ lo_neuron, float* __restrict__ LO, int* __restrict__ MN,
     int* __restrict__ OVF, float* __restrict__ starts, WsHeader* hdr, int64_t N, int M, int C,
-    int K, float beta, float theta, float u_r) {
+    int K, float beta, float theta, float u_r, float* __restrict__ U, float* __restrict__ S,
+    float* __restrict__ ends, int* __restrict__ done) {
   const int64_t n = (int64_t)blockIdx.x * WAVE + threadIdx.x;
   const bool valid = n < N;
   unsigned long long ovf_acc = 0, pcs_acc = 0;
@@ -428,7 +439,25 @@ __global__ __launch_bounds__(64) void k_lif_carry(
 #pragma unroll
       for (int i = 0; i < KMAX; ++i) cval = (i == k) ? cd[i] : cval;
       float nu = (k == ne) ? __fadd_rn(__fmul_rn(MA[o], u), MB[o]) : cval;
-      if (ovf) {  // rare: serial fallback through this chunk
+      if (done) {
+        // converged result only (done given): when any lane overflows, every lane of the wave
+        // replays the chunk from its start and carries that exact exit; U, S and the end are
+        // written here and the replay skips the block
+        const bool fb = __ballot(ovf) != 0ull;
+        if (fb) {
+          float w = u;
+          const size_t base = (size_t)m * C * N + n;
+          stream_rows<kFbRows>(I + base, (size_t)N, C, [&](int64_t j, float x) {
+            bool s;
+            w = lif_step(w, x, beta, theta, u_r, s);
+            st_nt(U + base + (size_t)j * N, w);
+            st_nt(S + base + (size_t)j * N, s ? 1.0f : 0.0f);
+          });
+          ends[o] = w;
+          nu = w;
+        }
+        if (threadIdx.x == 0) done[(size_t)m * gridDim.x + blockIdx.x] = fb ? 1 : 0;
+      } else if (ovf) {  // rare: serial fallback through this chunk
         float w = u;
         stream_rows<16>(I + (size_t)m * C * N + n, (size_t)N, C, [&](int64_t, float x) {
           bool s;
@@ -583,7 +612,8 @@ __global__ __launch_bounds__(256) void k_lif_carry_staged(
     const float* __restrict__ MX, const float* __restrict__ MC,
     const float* __restrict__ lo_neuron, float* __restrict__ LO, int* __restrict__ MN,
     int* __restrict__ OVF, float* __restrict__ starts, WsHeader* hdr, int64_t N, int M, int C,
-    int K, float beta, float theta, float u_r) {
+    int K, float beta, float theta, float u_r, float* __restrict__ U, float* __restrict__ S,
+    float* __restrict__ ends, int* __restrict__ done) {
   using CS = CarryStage<KMAX>;
   constexpr int ROWS = CS::ROWS, R = CS::R;
   __shared__ float sbuf[2][R * ROWS][WAVE];
@@ -680,7 +710,24 @@ __global__ __launch_bounds__(256) void k_lif_carry_staged(
           MN[o] = ne;
           OVF[o] = ovf ? 1 : 0;
         }
-        if (ovf) {  // rare: serial fallback through this chunk
+        if (done) {  // as in k_lif_carry: the whole wave replays, the replay skips the block
+          const bool fb = __ballot(ovf) != 0ull;
+          if (fb) {
+            float wv = u;
+            const size_t base = (size_t)m * C * N + nn;
+            stream_rows<kFbRows>(I + base, (size_t)N, C, [&](int64_t j, float x) {
+              bool sp;
+              wv = lif_step(wv, x, beta, theta, u_r, sp);
+              if (valid) {
+                st_nt(U + base + (size_t)j * N, wv);
+                st_nt(S + base + (size_t)j * N, sp ? 1.0f : 0.0f);
+              }
+            });
+            if (valid) ends[o] = wv;
+            nu = wv;
+          }
+          if (lane == 0) done[(size_t)m * gridDim.x + blockIdx.x] = fb ? 1 : 0;
+        } else if (ovf) {  // rare: serial fallback through this chunk
           float wv = u;
           stream_rows<16>(I + (size_t)m * C * N + nn, (size_t)N, C, [&](int64_t, float x) {
             bool sp;
@@ -957,19 +1004,19 @@ __global__ __launch_bounds__(64) void k_lif_repair_seg(const float* __restrict__
 template <int D>
 static void launch_fwd(const float* I, const float* starts, float* U, float* S, float* ends,
                        int64_t N, int64_t Ls, int64_t M, float beta, float theta, float u_r,
-                       hipStream_t st) {
+                       hipStream_t st, const int* done = nullptr) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   hipLaunchKernelGGL(k_lif_fwd<D>, dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, starts, U, S,
-                     ends, N, Ls, NB, beta, theta, u_r);
+                     ends, N, Ls, NB, beta, theta, u_r, done);
 }
 
 static void launch_fwd_auto(const float* I, const float* starts, float* U, float* S, float* ends,
                             int64_t N, int64_t Ls, int64_t M, float beta, float theta, float u_r,
-                            hipStream_t st) {
+                            hipStream_t st, const int* done = nullptr) {
   if (Ls >= 32)
-    launch_fwd<16>(I, starts, U, S, ends, N, Ls, M, beta, theta, u_r, st);
+    launch_fwd<16>(I, starts, U, S, ends, N, Ls, M, beta, theta, u_r, st, done);
   else
-    launch_fwd<4>(I, starts, U, S, ends, N, Ls, M, beta, theta, u_r, st);
+    launch_fwd<4>(I, starts, U, S, ends, N, Ls, M, beta, theta, u_r, st, done);
 }
 
 template <bool COMPOSE, bool DETACH, bool HAS_GU, int PS = 0>
@@ -1061,10 +1108,27 @@ static void launch_build(const float* I, const float* u0, char* ws, const lsh_v3
 }
 
 // The carry over the M chunk maps from u0 (the envelope seed and the first start).
+// Exact fallbacks (RP given: only where the result is the converged one, the serial
+// recurrence): a lane carry whose wave runs the serial fallback for an overflowed lane runs it
+// for all its lanes, which then carry the exact exit instead of the map's, and writes U, S and
+// the end of that chunk as the replay would; one flag per (chunk, 64-neuron block) in
+// RP->done, which the replay reads, tells it which blocks are done.  The same steps cost nothing
+// more in the other lanes; at cfg2, beta 0.99 (28-73 % of the chunks overflow at K 8), most
+// blocks are then replayed once, inside the carry, and their starts are exact, so the repair
+// finds little left.  Returns whether the flags were written (the one-wave-per-neuron carry
+// for few neurons keeps the plain fallback).
+struct ReplayInto {
+  float *U, *S, *ends;
+  int* done;
+};
 template <int KMAX>
-static void launch_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
+static bool launch_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
                          const lsh_v3_layout& L, int64_t N, int M, int C, int K, float beta,
-                         float theta, float u_r, hipStream_t st) {
+                         float theta, float u_r, hipStream_t st, const ReplayInto* RP) {
+  float* rU = RP ? RP->U : nullptr;
+  float* rS = RP ? RP->S : nullptr;
+  float* rE = RP ? RP->ends : nullptr;
+  int* rD = RP ? RP->done : nullptr;
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(ws + off); };
@@ -1083,38 +1147,40 @@ static void launch_carry(const float* I, const float* u0, const float* lo_neuron
                        F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
                        F(L.MC), lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS),
                        reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r);
-    return;
+    return false;
   }
   if (M >= 4 * CarryStage<KMAX>::R && KMAX <= 32) {
     // long chunk sequences: map reads staged through LDS by three loader waves
     hipLaunchKernelGGL((k_lif_carry_staged<KMAX>), dim3((unsigned)NB), dim3(256), 0, st, I, u0,
                        F(L.EC), F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
                        F(L.MC), lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS),
-                       reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r);
-    return;
+                       reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r, rU, rS, rE,
+                       rD);
+    return rD != nullptr;
   }
   hipLaunchKernelGGL((k_lif_carry<KMAX>), dim3((unsigned)NB), dim3(WAVE), 0, st, I, u0, F(L.EC),
                      F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX), F(L.MC),
                      lo_neuron, F(L.LO), Iq(L.MN), Iq(L.OVF), F(L.STARTS),
-                     reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r);
+                     reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r, rU, rS, rE, rD);
+  return rD != nullptr;
 }
 
 template <int KMAX>
-static void launch_build_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
+static bool launch_build_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
                                const lsh_v3_layout& L, int64_t N, int M, int C, int K, float beta,
-                               float theta, float u_r, hipStream_t st) {
+                               float theta, float u_r, hipStream_t st, const ReplayInto* RP) {
   launch_build<KMAX>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
-  launch_carry<KMAX>(I, u0, lo_neuron, ws, L, N, M, C, K, beta, theta, u_r, st);
+  return launch_carry<KMAX>(I, u0, lo_neuron, ws, L, N, M, C, K, beta, theta, u_r, st, RP);
 }
 
-static void lif_carry_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L,
+static bool lif_carry_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L,
                              int64_t N, int M, int C, int K, float beta, float theta, float u_r,
-                             hipStream_t st) {
-  if (K <= 4) launch_carry<4>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
-  else if (K <= 8) launch_carry<8>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
-  else if (K <= 16) launch_carry<16>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
-  else if (K <= 32) launch_carry<32>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
-  else launch_carry<64>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st);
+                             hipStream_t st, const ReplayInto* RP) {
+  if (K <= 4) return launch_carry<4>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st, RP);
+  if (K <= 8) return launch_carry<8>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st, RP);
+  if (K <= 16) return launch_carry<16>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st, RP);
+  if (K <= 32) return launch_carry<32>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st, RP);
+  return launch_carry<64>(I, u0, nullptr, ws, L, N, M, C, K, beta, theta, u_r, st, RP);
 }
 
 // One non-blocking side stream per device (default priority), created on first use on the
@@ -1142,14 +1208,23 @@ int lif_build_launch(const float* I, const float* u0, char* ws, const lsh_v3_lay
   return LSH_OK;
 }
 
-// Replay of every chunk from its carried start, then the device repair rounds.
+// Replay of every chunk from its carried start (but the blocks flagged in done, which the
+// carry replayed), then the device repair rounds.
+static void replay_repair(const float* I, float* U, float* S, float* starts, float* ends,
+                          int* list0, int* list1, WsHeader* hdr, int64_t N, int M, int C,
+                          int64_t repair, float beta, float theta, float u_r, hipStream_t st,
+                          const int* done) {
+  launch_fwd_auto(I, starts, U, S, ends, N, C, M, beta, theta, u_r, st, done);
+  lif_repair_launch(I, U, S, starts, ends, list0, list1, hdr, N, M, C, repair, beta, theta, u_r,
+                    st);
+}
+
 void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* S, float* starts,
                               float* ends, int* list0, int* list1, WsHeader* hdr, int64_t N, int M,
                               int C, int64_t repair, float beta, float theta, float u_r,
                               hipStream_t st) {
-  launch_fwd_auto(I, starts, U, S, ends, N, C, M, beta, theta, u_r, st);
-  lif_repair_launch(I, U, S, starts, ends, list0, list1, hdr, N, M, C, repair, beta, theta, u_r,
-                    st);
+  replay_repair(I, U, S, starts, ends, list0, list1, hdr, N, M, C, repair, beta, theta, u_r, st,
+                nullptr);
 }
 
 // The segmented ordered repair (k_lif_repair_seg): from this many chunks, with fewer neurons
@@ -1320,20 +1395,25 @@ static int scan2_fwd(const float* I, const float* u0, const float* lo_neuron, fl
     return LSH_OK;
   }
   const int M = (int)(T / C);
+  // converged without statistics (repair -1): exact fallbacks replayed inside the carry, the
+  // block flags in the second repair list (the Jacobi rounds refill their lists from scratch)
+  const ReplayInto rp{U, S, reinterpret_cast<float*>(w + L.ENDS), reinterpret_cast<int*>(w + L.LIST1)};
+  const ReplayInto* RP = repair < 0 ? &rp : nullptr;
+  bool done = false;
   if (K <= 4)
-    launch_build_carry<4>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
+    done = launch_build_carry<4>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st, RP);
   else if (K <= 8)
-    launch_build_carry<8>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
+    done = launch_build_carry<8>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st, RP);
   else if (K <= 16)
-    launch_build_carry<16>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
+    done = launch_build_carry<16>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st, RP);
   else if (K <= 32)
-    launch_build_carry<32>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
+    done = launch_build_carry<32>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st, RP);
   else
-    launch_build_carry<64>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st);
-  lif_replay_repair_launch(I, u0, U, S, reinterpret_cast<float*>(w + L.STARTS),
-                           reinterpret_cast<float*>(w + L.ENDS), reinterpret_cast<int*>(w + L.LIST0),
-                           reinterpret_cast<int*>(w + L.LIST1), reinterpret_cast<WsHeader*>(w), N,
-                           M, C, repair, beta, theta, u_r, st);
+    done = launch_build_carry<64>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st, RP);
+  replay_repair(I, U, S, reinterpret_cast<float*>(w + L.STARTS),
+                reinterpret_cast<float*>(w + L.ENDS), reinterpret_cast<int*>(w + L.LIST0),
+                reinterpret_cast<int*>(w + L.LIST1), reinterpret_cast<WsHeader*>(w), N, M, C, repair,
+                beta, theta, u_r, st, done ? reinterpret_cast<const int*>(w + L.LIST1) : nullptr);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }
@@ -1436,12 +1516,14 @@ extern "C" int lsh_lif_scan_v3_pieces_fwd(const float* I, const float* u0, float
       char* wp = w + (size_t)p * pb;
       const size_t r0 = (size_t)p * Tp * N;
       const float* up = p == 0 ? u0 : U + r0 - N;
-      lif_carry_launch(I + r0, up, wp, L, N, Mp, C, K, beta, theta, u_r, st);
-      lif_replay_repair_launch(I + r0, up, U + r0, S + r0, reinterpret_cast<float*>(wp + L.STARTS),
-                               reinterpret_cast<float*>(wp + L.ENDS),
-                               reinterpret_cast<int*>(wp + L.LIST0),
-                               reinterpret_cast<int*>(wp + L.LIST1),
-                               reinterpret_cast<WsHeader*>(wp), N, Mp, C, Mp, beta, theta, u_r, st);
+      const ReplayInto rp{U + r0, S + r0, reinterpret_cast<float*>(wp + L.ENDS),
+                          reinterpret_cast<int*>(wp + L.LIST1)};
+      const bool done = lif_carry_launch(I + r0, up, wp, L, N, Mp, C, K, beta, theta, u_r, st, &rp);
+      replay_repair(I + r0, U + r0, S + r0, reinterpret_cast<float*>(wp + L.STARTS),
+                    reinterpret_cast<float*>(wp + L.ENDS), reinterpret_cast<int*>(wp + L.LIST0),
+                    reinterpret_cast<int*>(wp + L.LIST1), reinterpret_cast<WsHeader*>(wp), N, Mp,
+                    C, Mp, beta, theta, u_r, st,
+                    done ? reinterpret_cast<const int*>(wp + L.LIST1) : nullptr);
     }
   }
   if (!ok) return LSH_ERR_HIP;

@@ -1210,10 +1210,10 @@ int lif_build_launch(const float* I, const float* u0, char* ws, const lsh_v3_lay
 
 // Replay of every chunk from its carried start (but the blocks flagged in done, which the
 // carry replayed), then the device repair rounds.
-static void replay_repair(const float* I, float* U, float* S, float* starts, float* ends,
-                          int* list0, int* list1, WsHeader* hdr, int64_t N, int M, int C,
-                          int64_t repair, float beta, float theta, float u_r, hipStream_t st,
-                          const int* done) {
+void lif_replay_repair_done_launch(const float* I, float* U, float* S, float* starts, float* ends,
+                                   int* list0, int* list1, WsHeader* hdr, int64_t N, int M, int C,
+                                   int64_t repair, float beta, float theta, float u_r,
+                                   hipStream_t st, const int* done) {
   launch_fwd_auto(I, starts, U, S, ends, N, C, M, beta, theta, u_r, st, done);
   lif_repair_launch(I, U, S, starts, ends, list0, list1, hdr, N, M, C, repair, beta, theta, u_r,
                     st);
@@ -1223,8 +1223,8 @@ void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* 
                               float* ends, int* list0, int* list1, WsHeader* hdr, int64_t N, int M,
                               int C, int64_t repair, float beta, float theta, float u_r,
                               hipStream_t st) {
-  replay_repair(I, U, S, starts, ends, list0, list1, hdr, N, M, C, repair, beta, theta, u_r, st,
-                nullptr);
+  lif_replay_repair_done_launch(I, U, S, starts, ends, list0, list1, hdr, N, M, C, repair, beta,
+                                theta, u_r, st, nullptr);
 }
 
 // The segmented ordered repair (k_lif_repair_seg): from this many chunks, with fewer neurons
@@ -1410,10 +1410,11 @@ static int scan2_fwd(const float* I, const float* u0, const float* lo_neuron, fl
     done = launch_build_carry<32>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st, RP);
   else
     done = launch_build_carry<64>(I, u0, lo_neuron, w, L, N, M, C, K, beta, theta, u_r, st, RP);
-  replay_repair(I, U, S, reinterpret_cast<float*>(w + L.STARTS),
-                reinterpret_cast<float*>(w + L.ENDS), reinterpret_cast<int*>(w + L.LIST0),
-                reinterpret_cast<int*>(w + L.LIST1), reinterpret_cast<WsHeader*>(w), N, M, C, repair,
-                beta, theta, u_r, st, done ? reinterpret_cast<const int*>(w + L.LIST1) : nullptr);
+  lif_replay_repair_done_launch(
+      I, U, S, reinterpret_cast<float*>(w + L.STARTS), reinterpret_cast<float*>(w + L.ENDS),
+      reinterpret_cast<int*>(w + L.LIST0), reinterpret_cast<int*>(w + L.LIST1),
+      reinterpret_cast<WsHeader*>(w), N, M, C, repair, beta, theta, u_r, st,
+      done ? reinterpret_cast<const int*>(w + L.LIST1) : nullptr);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }
@@ -1519,11 +1520,11 @@ extern "C" int lsh_lif_scan_v3_pieces_fwd(const float* I, const float* u0, float
       const ReplayInto rp{U + r0, S + r0, reinterpret_cast<float*>(wp + L.ENDS),
                           reinterpret_cast<int*>(wp + L.LIST1)};
       const bool done = lif_carry_launch(I + r0, up, wp, L, N, Mp, C, K, beta, theta, u_r, st, &rp);
-      replay_repair(I + r0, U + r0, S + r0, reinterpret_cast<float*>(wp + L.STARTS),
-                    reinterpret_cast<float*>(wp + L.ENDS), reinterpret_cast<int*>(wp + L.LIST0),
-                    reinterpret_cast<int*>(wp + L.LIST1), reinterpret_cast<WsHeader*>(wp), N, Mp,
-                    C, Mp, beta, theta, u_r, st,
-                    done ? reinterpret_cast<const int*>(wp + L.LIST1) : nullptr);
+      lif_replay_repair_done_launch(
+          I + r0, U + r0, S + r0, reinterpret_cast<float*>(wp + L.STARTS),
+          reinterpret_cast<float*>(wp + L.ENDS), reinterpret_cast<int*>(wp + L.LIST0),
+          reinterpret_cast<int*>(wp + L.LIST1), reinterpret_cast<WsHeader*>(wp), N, Mp, C, Mp, beta,
+          theta, u_r, st, done ? reinterpret_cast<const int*>(wp + L.LIST1) : nullptr);
     }
   }
   if (!ok) return LSH_ERR_HIP;

@@ -617,12 +617,18 @@ __global__ __launch_bounds__(64) void k_map_carry_wave(
   }
 }
 
+// done (converged calls only; else null): as the v3 lane carries, a wave whose chunk
+// overflows in any lane replays that chunk for all its lanes from their starts, writing U, S
+// and the end, and flags the (chunk, 64-neuron block) for the replay to skip; every later
+// chunk of the group then starts from the exact state of the group's start.
 template <int KMAX>
 __global__ __launch_bounds__(64) void k_lif_carry_inner(
     const float* __restrict__ I, const float* __restrict__ sstarts, const float* __restrict__ MA,
     const float* __restrict__ MB, const int* __restrict__ MN, const int* __restrict__ OVF,
     const float* __restrict__ MX, const float* __restrict__ MC, float* __restrict__ starts,
-    int64_t N, int NB, int G, int C, int K, float beta, float theta, float u_r) {
+    int64_t N, int NB, int G, int C, int K, float beta, float theta, float u_r,
+    float* __restrict__ U, float* __restrict__ S, float* __restrict__ ends,
+    int* __restrict__ done) {
   const int64_t s = blockIdx.x / NB;
   const int nb = (int)(blockIdx.x - s * NB);
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
@@ -639,7 +645,25 @@ __global__ __launch_bounds__(64) void k_lif_carry_inner(
       cd[i] = i < K ? MC[((size_t)m * K + i) * N + n] : 0.0f;
     }
     float nu = eval_slots<KMAX>(xd, cd, MN[o], MA[o], MB[o], u);
-    if (OVF[o]) nu = serial_rows(I, N, n, m * C, C, u, beta, theta, u_r);
+    const bool ovf = OVF[o] != 0;
+    if (done) {
+      const bool fb = __ballot(ovf) != 0ull;
+      if (fb) {
+        float w = u;
+        const size_t base = (size_t)m * C * N + n;
+        stream_rows<32>(I + base, (size_t)N, C, [&](int64_t j, float x) {
+          bool sp;
+          w = lif_step(w, x, beta, theta, u_r, sp);
+          st_nt(U + base + (size_t)j * N, w);
+          st_nt(S + base + (size_t)j * N, sp ? 1.0f : 0.0f);
+        });
+        ends[o] = w;
+        nu = w;
+      }
+      if (threadIdx.x == 0) done[(size_t)m * NB + nb] = fb ? 1 : 0;
+    } else if (ovf) {
+      nu = serial_rows(I, N, n, m * C, C, u, beta, theta, u_r);
+    }
     u = nu;
   }
 }
@@ -648,6 +672,10 @@ __global__ __launch_bounds__(64) void k_lif_carry_inner(
 // entry point plumbing (the build, replay and repair kernels live in lif_kernels.hip)
 int lif_build_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L, int64_t N,
                      int M, int C, int K, float beta, float theta, float u_r, hipStream_t st);
+void lif_replay_repair_done_launch(const float* I, float* U, float* S, float* starts, float* ends,
+                                   int* list0, int* list1, WsHeader* hdr, int64_t N, int M, int C,
+                                   int64_t repair, float beta, float theta, float u_r,
+                                   hipStream_t st, const int* done);
 void lif_replay_repair_launch(const float* I, const float* u0, float* U, float* S, float* starts,
                               float* ends, int* list0, int* list1, WsHeader* hdr, int64_t N, int M,
                               int C, int64_t repair, float beta, float theta, float u_r,
@@ -716,15 +744,18 @@ static void launch_chunk_kernels(const float* I, const float* u0, char* w, const
                      reinterpret_cast<WsHeader*>(w), N, NB, M, MB, K);
 }
 
+// done: converged calls only (see k_lif_carry_inner), else null.
 template <int KMAX>
 static void launch_inner(const float* I, char* w, const lsh_v4_layout& L, int64_t N, int M2, int G,
-                         int C, int K, float beta, float theta, float u_r, hipStream_t st) {
+                         int C, int K, float beta, float theta, float u_r, hipStream_t st,
+                         float* U, float* S, int* done) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
   hipLaunchKernelGGL((k_lif_carry_inner<KMAX>), dim3((unsigned)((int64_t)M2 * NB)), dim3(WAVE), 0, st,
                      I, F(L.SSTARTS), F(L.v3.MA), F(L.v3.MB), Iq(L.v3.MN), Iq(L.v3.OVF), F(L.v3.MX),
-                     F(L.v3.MC), F(L.v3.STARTS), N, NB, G, C, K, beta, theta, u_r);
+                     F(L.v3.MC), F(L.v3.STARTS), N, NB, G, C, K, beta, theta, u_r, U, S,
+                     F(L.v3.ENDS), done);
 }
 
 template <int K2MAX, int KW>
@@ -866,17 +897,20 @@ extern "C" int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, fl
     case 32: launch_super_carry<32>(I, u0, w, L, N, M2, K2, G, C, K, walk, beta, theta, u_r, st); break;
     default: launch_super_carry<64>(I, u0, w, L, N, M2, K2, G, C, K, walk, beta, theta, u_r, st); break;
   }
+  // converged without statistics (repair -1): exact fallbacks in the inner carry, the block
+  // flags in the second repair list (the Jacobi rounds refill their lists from scratch)
+  int* done = repair < 0 ? reinterpret_cast<int*>(w + L.v3.LIST1) : nullptr;
   switch (kcap(K)) {
-    case 4: launch_inner<4>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st); break;
-    case 8: launch_inner<8>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st); break;
-    case 16: launch_inner<16>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st); break;
-    default: launch_inner<32>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st); break;
+    case 4: launch_inner<4>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st, U, S, done); break;
+    case 8: launch_inner<8>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st, U, S, done); break;
+    case 16: launch_inner<16>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st, U, S, done); break;
+    default: launch_inner<32>(I, w, L, N, M2, G, C, K, beta, theta, u_r, st, U, S, done); break;
   }
-  lif_replay_repair_launch(I, u0, U, S, reinterpret_cast<float*>(w + L.v3.STARTS),
-                           reinterpret_cast<float*>(w + L.v3.ENDS),
-                           reinterpret_cast<int*>(w + L.v3.LIST0),
-                           reinterpret_cast<int*>(w + L.v3.LIST1), h, N, M, C, repair, beta, theta,
-                           u_r, st);
+  lif_replay_repair_done_launch(I, U, S, reinterpret_cast<float*>(w + L.v3.STARTS),
+                                reinterpret_cast<float*>(w + L.v3.ENDS),
+                                reinterpret_cast<int*>(w + L.v3.LIST0),
+                                reinterpret_cast<int*>(w + L.v3.LIST1), h, N, M, C, repair, beta,
+                                theta, u_r, st, done);
   LSH_CHECK_LAUNCH();
   return LSH_OK;
 }

@@ -272,7 +272,8 @@ __global__ __launch_bounds__(64) void k_lif_build(
     const float* __restrict__ I, const float* __restrict__ u0, float* __restrict__ EC,
     float* __restrict__ EA, float* __restrict__ EB, float* __restrict__ MA, float* __restrict__ MB,
     int* __restrict__ CNT, int* __restrict__ OVFRAW, float* __restrict__ MX, float* __restrict__ MC,
-    int64_t N, int C, int NB, int K, float beta, float theta, float u_r) {
+    int64_t N, int C, int NB, int K, float beta, float theta, float u_r,
+    float* __restrict__ XT = nullptr, float* __restrict__ CT = nullptr) {
   const int64_t m = blockIdx.x / NB;
   const int nb = (int)(blockIdx.x - m * NB);
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
@@ -373,6 +374,16 @@ __global__ __launch_bounds__(64) void k_lif_build(
       const size_t os = ((size_t)m * K + i) * N + n;
       MX[os] = xd[i];
       MC[os] = cd[i];
+    }
+  }
+  if (XT) {  // a neuron's K slots contiguous ([M, N, K]), for walks with one wave per neuron
+#pragma unroll
+    for (int i = 0; i < KMAX; ++i) {
+      if (i < K) {
+        const size_t ot = ((size_t)m * N + n) * K + i;
+        XT[ot] = xd[i];
+        CT[ot] = cd[i];
+      }
     }
   }
 }
@@ -1093,18 +1104,18 @@ void v3_layout_fill(int64_t T, int64_t N, int C, int K, lsh_v3_layout* L) {
 template <int KMAX>
 static void launch_build(const float* I, const float* u0, char* ws, const lsh_v3_layout& L,
                          int64_t N, int M, int C, int K, float beta, float theta, float u_r,
-                         hipStream_t st) {
+                         hipStream_t st, float* XT = nullptr, float* CT = nullptr) {
   const int NB = (int)((N + WAVE - 1) / WAVE);
   auto F = [&](size_t off) { return reinterpret_cast<float*>(ws + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(ws + off); };
   if (C >= 16)
     hipLaunchKernelGGL((k_lif_build<KMAX, 8>), dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, u0,
                        F(L.EC), F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
-                       F(L.MC), N, C, NB, K, beta, theta, u_r);
+                       F(L.MC), N, C, NB, K, beta, theta, u_r, XT, CT);
   else
     hipLaunchKernelGGL((k_lif_build<KMAX, 1>), dim3((unsigned)(M * NB)), dim3(WAVE), 0, st, I, u0,
                        F(L.EC), F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),
-                       F(L.MC), N, C, NB, K, beta, theta, u_r);
+                       F(L.MC), N, C, NB, K, beta, theta, u_r, XT, CT);
 }
 
 // The carry over the M chunk maps from u0 (the envelope seed and the first start).
@@ -1198,13 +1209,23 @@ static hipStream_t side_stream() {
 }
 
 // Build kernel alone (used by the three-level scan).
+int lif_build_t_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L,
+                       int64_t N, int M, int C, int K, float beta, float theta, float u_r,
+                       hipStream_t st, float* XT, float* CT);
 int lif_build_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L, int64_t N,
                      int M, int C, int K, float beta, float theta, float u_r, hipStream_t st) {
-  if (K <= 4) launch_build<4>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
-  else if (K <= 8) launch_build<8>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
-  else if (K <= 16) launch_build<16>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
-  else if (K <= 32) launch_build<32>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
-  else launch_build<64>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st);
+  return lif_build_t_launch(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st, nullptr, nullptr);
+}
+
+// The same, also writing the maps' slots transposed ([M, N, K]) into XT, CT when given.
+int lif_build_t_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L,
+                       int64_t N, int M, int C, int K, float beta, float theta, float u_r,
+                       hipStream_t st, float* XT, float* CT) {
+  if (K <= 4) launch_build<4>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st, XT, CT);
+  else if (K <= 8) launch_build<8>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st, XT, CT);
+  else if (K <= 16) launch_build<16>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st, XT, CT);
+  else if (K <= 32) launch_build<32>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st, XT, CT);
+  else launch_build<64>(I, u0, ws, L, N, M, C, K, beta, theta, u_r, st, XT, CT);
   return LSH_OK;
 }
 

@@ -376,6 +376,8 @@ struct ChunkMaps {
   const float* MX;
   const float* MC;
   int K, G, C, walk;
+  const float* XT;  // the slots transposed ([M, N, K]) for the one-wave walk, or null
+  const float* CT;
 };
 
 template <int KMAX>
@@ -535,8 +537,13 @@ __device__ __forceinline__ float wave_walk_chunk_maps(const float* __restrict__ 
 #pragma unroll
     for (int v = 0; v < NV; ++v) {
       const size_t m = (size_t)(c0 + j0 + min(v * CPV + row, nb - 1));
-      xv[v] = cm.MX[(m * cm.K + sl) * N + n];
-      cv[v] = cm.MC[(m * cm.K + sl) * N + n];
+      if (cm.XT) {  // a chunk's slots in one segment: one line per row of the load
+        xv[v] = cm.XT[(m * N + n) * cm.K + sl];
+        cv[v] = cm.CT[(m * N + n) * cm.K + sl];
+      } else {  // one line per lane
+        xv[v] = cm.MX[(m * cm.K + sl) * N + n];
+        cv[v] = cm.MC[(m * cm.K + sl) * N + n];
+      }
     }
     const size_t ms = (size_t)(c0 + j0 + min(lane, nb - 1)) * N + n;
     const float av = cm.MA[ms], bv = cm.MB[ms];
@@ -670,6 +677,9 @@ __global__ __launch_bounds__(64) void k_lif_carry_inner(
 
 // ---------------------------------------------------------------------------------------
 // entry point plumbing (the build, replay and repair kernels live in lif_kernels.hip)
+int lif_build_t_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L,
+                       int64_t N, int M, int C, int K, float beta, float theta, float u_r,
+                       hipStream_t st, float* XT, float* CT);
 int lif_build_launch(const float* I, const float* u0, char* ws, const lsh_v3_layout& L, int64_t N,
                      int M, int C, int K, float beta, float theta, float u_r, hipStream_t st);
 void lif_replay_repair_done_launch(const float* I, float* U, float* S, float* starts, float* ends,
@@ -778,8 +788,9 @@ static void launch_super_carry(const float* I, const float* u0, char* w, const l
                                float beta, float theta, float u_r, hipStream_t st) {
   auto F = [&](size_t off) { return reinterpret_cast<float*>(w + off); };
   auto Iq = [&](size_t off) { return reinterpret_cast<int*>(w + off); };
+  const bool xt = L.XT != L.CT;  // the transposed slots exist (a wave per neuron)
   const ChunkMaps cm{F(L.v3.MA), F(L.v3.MB), Iq(L.v3.MN), Iq(L.v3.OVF), F(L.v3.MX), F(L.v3.MC),
-                     K, G, C, walk};
+                     K, G, C, walk, xt ? F(L.XT) : nullptr, xt ? F(L.CT) : nullptr};
   const int64_t Lsteps = (int64_t)C * G;
   if (K2MAX <= 32 && N <= LSH_V4_WAVE_MAX_N) {
     hipLaunchKernelGGL(k_map_carry_wave, dim3((unsigned)N), dim3(WAVE), 0, st, I, u0, F(L.SA),
@@ -824,6 +835,11 @@ static void v4_layout(int64_t T, int64_t N, int C, int G, int K, int K2, lsh_v4_
   L->SX = c.take(sn * (size_t)K2);
   L->SC = c.take(sn * (size_t)K2);
   L->SSTARTS = c.take(sn);
+  // the chunk maps' slots transposed, for the one-wave super carry's walk over an overflowed
+  // super map's chunk maps (a chunk's slots then share cache lines instead of one line each)
+  const size_t xt = N <= LSH_V4_WAVE_MAX_N ? (size_t)(T / C) * (size_t)N * (size_t)K * 4 : 0;
+  L->XT = c.take(xt);
+  L->CT = c.take(xt);
   L->total = c.off;
 }
 
@@ -869,7 +885,10 @@ extern "C" int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, fl
   }
   const int M = (int)(T / C);
   const int M2 = M / G;
-  int r = lif_build_launch(I, u0, w, L.v3, N, M, C, K, beta, theta, u_r, st);
+  const bool xt = walk && L.XT != L.CT;  // transposed slots for the one-wave walk
+  int r = lif_build_t_launch(I, u0, w, L.v3, N, M, C, K, beta, theta, u_r, st,
+                             xt ? reinterpret_cast<float*>(w + L.XT) : nullptr,
+                             xt ? reinterpret_cast<float*>(w + L.CT) : nullptr);
   if (r != LSH_OK) return r;
   switch (kcap(K)) {
     case 4:

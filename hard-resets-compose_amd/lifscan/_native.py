@@ -15,7 +15,7 @@ from . import _build
 _LIB = None
 
 # LSH_ABI_VERSION of include/lifscan_hip.h that these signatures bind
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 LSH_OK = 0
 LSH_ERR_ARG = -1
@@ -57,7 +57,7 @@ class V3Layout(ctypes.Structure):
 
 class V4Layout(ctypes.Structure):
     _fields_ = [("v3", V3Layout)] + [(n, ctypes.c_size_t) for n in (
-        "SA", "SB", "SN", "SOVF", "SX", "SC", "SSTARTS", "total")]
+        "SA", "SB", "SN", "SOVF", "SX", "SC", "SSTARTS", "XT", "CT", "total")]
 
 
 class AffLayout(ctypes.Structure):

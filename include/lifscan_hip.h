@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define LSH_ABI_VERSION 3
+#define LSH_ABI_VERSION 4
 
 #define LSH_OK 0
 #define LSH_ERR_ARG (-1)          /* null pointer or bad scalar argument */
@@ -204,6 +204,9 @@ typedef struct lsh_v4_layout {
   size_t SA, SB, SN, SOVF; /* super maps [M/G, N] */
   size_t SX, SC;        /* super breakpoints / constants [M/G, K2, N] */
   size_t SSTARTS;       /* super-chunk entry states [M/G, N] */
+  size_t XT, CT;        /* chunk breakpoints / constants transposed [M, N, K], written with
+                           super_walk = 1 for the one-wave-per-neuron super carry (N <= 2048;
+                           empty, XT == CT, above) */
   size_t total;
 } lsh_v4_layout;
 size_t lsh_lif_scan_v4_workspace(int64_t T, int64_t N, int C, int G, int K, int K2);

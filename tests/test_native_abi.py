@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol():
 def test_identity_and_status_strings():
     from lifscan import _native
     L = _native.lib()
-    assert L.lsh_abi_version() == 3
+    assert L.lsh_abi_version() == 4
     assert L.lsh_arch() == b"gfx950"
     for rc in (0, -1, -2, -3, -4, -5):
         assert len(L.lsh_status_string(rc)) > 0

@@ -1186,6 +1186,8 @@ class LIFAuto(torch.autograd.Function):
 
 def lif_auto(I, u0, beta=0.9, theta=1.0, u_r=0.0, alpha=4.0, K=16, repair=0):
     fwd, bwd = auto_modes(I.shape[1], I.shape[0])
+    if fwd == bwd:  # one mode for both passes: lif_tuned's path (the same kernels and bits)
+        return lif_tuned(I, u0, beta, theta, u_r, alpha, mode=fwd, K=K, repair=repair)
     return LIFAuto.apply(I, u0, beta, theta, u_r, alpha, K, repair, fwd, bwd)
 
 

@@ -978,6 +978,9 @@ __global__ __launch_bounds__(64) void k_lif_repair_seg(const float* __restrict__
     }
     const bool dirty = valid && !same_bits(ue, s0);
     if (__ballot(dirty) == 0ull) {
+      // after round 0 the segment is consistent from chunk to chunk, and a later round only
+      // changes a run from its start: the first chunk that needs nothing ends that run
+      if (round > 0) break;
       ue = e0;
       continue;
     }

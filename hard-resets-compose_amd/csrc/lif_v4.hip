@@ -368,6 +368,10 @@ __global__ __launch_bounds__(64) void k_lif_compose_wave(
 
 // The chunk maps behind the super maps (truncated counts and overflow flags, as the inner
 // carry reads them), for the fallback of an overflowed super map; walk = 0: serial steps.
+// ChunkMaps::walk, the fallback of an overflowed super map: 0 its C*G serial steps, 1 the walk
+// over its G chunk maps, kSuperAsStored none: the map as stored (converged calls only, where
+// the repair replaces a start it got wrong).
+constexpr int kSuperAsStored = 2;
 struct ChunkMaps {
   const float* MA;
   const float* MB;
@@ -451,7 +455,7 @@ __global__ __launch_bounds__(64) void k_map_carry(
       const SuperMap<KMAX>& d = mr[ph];
       if (valid) starts[(size_t)m * N + nn] = u;
       float nu = eval_slots<KMAX>(d.xd, d.cd, d.cnt, d.a, d.b, u);
-      if (d.ovf)
+      if (d.ovf && cm.walk != kSuperAsStored)
         nu = cm.walk ? walk_chunk_maps<KW>(I, cm, N, nn, m, u, beta, theta, u_r)
                      : serial_rows(I, N, nn, (int64_t)m * L, L, u, beta, theta, u_r);
       u = nu;
@@ -607,7 +611,8 @@ __global__ __launch_bounds__(64) void k_map_carry_wave(
         float nu = k == cnt ? __fadd_rn(__fmul_rn(lane_f(cur.a, c), u), lane_f(cur.b, c))
                             : lane_f(cur.cd[g], 32 * h + min(k, 31));
         if (lane == c) st_o = u;
-        if (__builtin_amdgcn_readlane(cur.ovf, c) != 0) {  // fallback through the map
+        if (cm.walk != kSuperAsStored && __builtin_amdgcn_readlane(cur.ovf, c) != 0) {
+          // fallback through the map
           const int64_t sm = (int64_t)w * 64 + c;
           if (!cm.walk)
             nu = wave_serial_rows(I, N, n, sm * L, L, u, beta, theta, u_r);
@@ -868,7 +873,8 @@ extern "C" int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, fl
                                    int K, int K2, int super_walk, int64_t repair, void* ws,
                                    size_t ws_bytes, void* stream) {
   if (bad_ptr(I) || bad_ptr(u0) || bad_ptr(U) || bad_ptr(S) || bad_ptr(ws)) return LSH_ERR_ARG;
-  if (repair < -1 || (super_walk != 0 && super_walk != 1)) return LSH_ERR_ARG;
+  if (repair < -1 || super_walk < 0 || super_walk > kSuperAsStored) return LSH_ERR_ARG;
+  if (super_walk == kSuperAsStored && repair != -1) return LSH_ERR_ARG;
   const int walk = super_walk;
   const int rc = v4_check(T, N, C, G, K, K2);
   if (rc != LSH_OK) return rc;
@@ -885,7 +891,7 @@ extern "C" int lsh_lif_scan_v4_fwd(const float* I, const float* u0, float* U, fl
   }
   const int M = (int)(T / C);
   const int M2 = M / G;
-  const bool xt = walk && L.XT != L.CT;  // transposed slots for the one-wave walk
+  const bool xt = walk == 1 && L.XT != L.CT;  // transposed slots for the one-wave walk
   int r = lif_build_t_launch(I, u0, w, L.v3, N, M, C, K, beta, theta, u_r, st,
                              xt ? reinterpret_cast<float*>(w + L.XT) : nullptr,
                              xt ? reinterpret_cast<float*>(w + L.CT) : nullptr);

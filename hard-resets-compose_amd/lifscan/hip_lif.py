@@ -622,16 +622,18 @@ class _ScanRunV4(_ScanRun):
 
 
 def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=1, BNg=16, nwg=1,
-                    BNc=16, nwc=1, BNr=32, D=8, nwr=1, repair=0, stats=None, super_fallback="chunks"):
+                    BNc=16, nwc=1, BNr=32, D=8, nwr=1, repair=0, stats=None, super_fallback="auto"):
     """Three-level exact scan (triton_lif.py:935-983) -> (U, S).  T must be divisible by C*G
     (ValueError, the reference asserts).  stats receives repair_iters, overflow_frac,
     super_overflow_frac, mean_pieces, super_mean_pieces, super_max_pieces (:976-982).
     super_fallback: how the super-map carry passes an overflowed super map: "chunks" walks its
     G chunk maps (as the inner carry does; an overflowed chunk map runs its C steps serially),
-    "serial" runs its C*G steps serially (the reference's carry, triton_lif.py:958-963).  With
-    the repair budget at least T/C and no stats requested, the result is the serial recurrence
-    and the fastest exact path computes it, as in scan_forward_v3 (scan_forward_v4_maps runs
-    the three-level pipeline itself)."""
+    "serial" runs its C*G steps serially (the reference's carry, triton_lif.py:958-963), "none"
+    evaluates it as stored (a start the repair replaces where it is wrong: only with the repair
+    budget at least T/C and no stats), "auto" is "none" there and "chunks" otherwise.  With the
+    repair budget at least T/C and no stats requested, the result is the serial recurrence and
+    the fastest exact path computes it, as in scan_forward_v3 (scan_forward_v4_maps runs the
+    three-level pipeline itself)."""
     I = _input(I)
     T = I.shape[0]
     if int(C) >= 1 and int(G) >= 1 and T % int(C) == 0 and (T // int(C)) % int(G) == 0:
@@ -643,14 +645,14 @@ def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=
 
 
 def scan_forward_v4_maps(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, repair=0, stats=None,
-                         super_fallback="chunks"):
+                         super_fallback="auto"):
     """The three-level pipeline of scan_forward_v4 itself (envelope, chunk maps, group
     composition, super-map carry, inner carry, replay, device repair) -> (U, S), also where
     scan_forward_v4 would compute its converged result by a faster exact path.  For measuring
     the three-level scan."""
     global _LAST_RUN
-    if super_fallback not in ("chunks", "serial"):
-        raise ValueError('super_fallback must be "chunks" or "serial"')
+    if super_fallback not in ("auto", "chunks", "serial", "none"):
+        raise ValueError('super_fallback must be "auto", "chunks", "serial" or "none"')
     I = _input(I)
     T, N = I.shape
     u0 = _vec(u0, N, I)
@@ -659,6 +661,12 @@ def scan_forward_v4_maps(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, repai
         raise ValueError(f"T={T} must be divisible by C*G={C * G}")
     if not (1 <= K <= 32 and K <= K2 <= 64):
         raise ValueError("three-level scan needs 1 <= K <= 32 and K <= K2 <= 64")
+    rep = _repair_arg(repair, T // C, stats)
+    if super_fallback == "auto":
+        super_fallback = "none" if rep == -1 else "chunks"
+    if super_fallback == "none" and rep != -1:
+        raise ValueError('super_fallback="none" needs repair >= T/C and no stats (the repair '
+                         'replaces the starts it gets wrong)')
     L = _n.lib()
     nbytes = L.lsh_lif_scan_v4_workspace(T, N, C, G, K, K2)
     if nbytes == 0:
@@ -669,8 +677,8 @@ def scan_forward_v4_maps(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, repai
     with _n.on_device(I):
         _n.check(L.lsh_lif_scan_v4_fwd(_n.ptr(I), _n.ptr(u0), _n.ptr(U), _n.ptr(S), T, N,
                                        _f32(beta), _f32(theta), _f32(u_r), C, G, K, K2,
-                                       1 if super_fallback == "chunks" else 0,
-                                       _repair_arg(repair, T // C, stats), _n.ptr(ws), nbytes,
+                                       {"serial": 0, "chunks": 1, "none": 2}[super_fallback],
+                                       rep, _n.ptr(ws), nbytes,
                                        _n.stream_of(I)),
                  "lsh_lif_scan_v4_fwd")
     _LAST_RUN = _ScanRunV4(ws, T, N, C, G, K, K2)

@@ -197,7 +197,8 @@ int lsh_lif_scan_v3_layout(int64_t T, int64_t N, int C, int K, lsh_v3_layout* ou
  * (scan_forward_v4), :829-899 (compose_group_kernel), :903-932 (carry_inner_kernel).
  * super_walk = 0: an overflowed super map runs its C*G steps serially (the reference's carry,
  * triton_lif.py:958-963); 1: it walks its G chunk maps as the inner carry does (an overflowed
- * chunk map runs its C steps serially).  Either way the repair gives the serial recurrence.
+ * chunk map runs its C steps serially); 2: it is evaluated as stored, a start that may be wrong
+ * (only with repair = -1, else LSH_ERR_ARG).  Each way the repair gives the serial recurrence.
  * Requires T % C == 0, (T / C) % G == 0, 1 <= K <= K2, K <= 32, K2 <= 64. */
 typedef struct lsh_v4_layout {
   lsh_v3_layout v3;     /* chunk-level arrays, as for lsh_lif_scan_v3_fwd */

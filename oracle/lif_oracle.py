@@ -392,9 +392,12 @@ def carry_super(I, u0, SA, SB, SX, SC, SN, SOVF, A, B, xd, cd, n, ovf, beta, the
     length C*G).  An overflowed super map is passed with fallback "serial" by its C*G serial steps
     (the reference), with "chunks" by evaluating its G chunk maps in turn from the super's start
     exactly as carry_inner does (an overflowed chunk map by its C serial steps), so that the
-    next super's start is the value the inner carry reaches at the end of this one."""
+    next super's start is the value the inner carry reaches at the end of this one, and with
+    "none" by evaluating it as stored (a start that may be wrong, for repair to convergence)."""
     if fallback == "serial":
         return carry(I, u0, SA, SB, SX, SC, SN, SOVF, beta, theta, u_r, C * G)
+    if fallback == "none":
+        return carry(I, u0, SA, SB, SX, SC, SN, np.zeros_like(SOVF), beta, theta, u_r, C * G)
     M2, N = SA.shape
     u = np.array(u0, dtype=f32).reshape(N).copy()
     sstarts = np.empty((M2, N), dtype=f32)

@@ -82,7 +82,8 @@ def test_cfg4_scan_v4_equals_serial(dev):
     scan_forward_v4 with repair at the reference default (C 64, G 16, K 16, K2 32; most super maps
     overflow, passed by walking their chunk maps or by their serial steps) and at C 2048, G 4,
     K 32, K2 64 returns the serial forward bit for bit, with statistics (the Jacobi rounds) and
-    without (the segmented ordered repair); 64 columns of the serial forward equal the oracle's."""
+    without (the segmented ordered repair; there also with the super maps passed as stored, the
+    converged default); 64 columns of the serial forward equal the oracle's."""
     from lifscan import hip_lif as L
     T, N, I, u0 = _cfg4_inputs(dev)
     Us, Ss = L.serial_forward(I, 0.99, 1.0, 0.0, u0)
@@ -97,6 +98,10 @@ def test_cfg4_scan_v4_equals_serial(dev):
         U, S = L.scan_forward_v4_maps(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2, repair=10 ** 6,
                                       super_fallback=fb)
         assert torch.equal(U, Us) and torch.equal(S, Ss)
+        if fb == "chunks":  # the default of converged calls: overflowed super maps as stored
+            U, S = L.scan_forward_v4_maps(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=K, K2=K2,
+                                          repair=10 ** 6, super_fallback="none")
+            assert torch.equal(U, Us) and torch.equal(S, Ss)
         del U, S
         torch.cuda.empty_cache()
     U, S = L.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=64, G=16, K=16, K2=32, repair=10 ** 6)

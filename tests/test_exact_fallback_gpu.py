@@ -50,7 +50,7 @@ def test_converged_v4_inner_carry_exact_fallbacks(dev, N, C, G, K, K2):
     Ig, u0g = gpu(I, dev), gpu(u0, dev)
     print(f"converged v4 exact fallbacks N={N} C={C} G={G} K={K} K2={K2}", flush=True)
     Us, Ss = O.serial_forward(I, beta, 1.0, 0.0, u0)
-    for fb in ("chunks", "serial"):
+    for fb in ("chunks", "serial", "none"):
         U, S = L.scan_forward_v4_maps(Ig, beta, 1.0, 0.0, u0g, C=C, G=G, K=K, K2=K2,
                                       repair=10 ** 6, super_fallback=fb)
         assert np.array_equal(host(U), Us) and np.array_equal(host(S), Ss), fb

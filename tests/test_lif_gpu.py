@@ -409,6 +409,12 @@ def test_scan_v4_matches_oracle(L, dev, beta, mu, sd, fallback):
         U2, S2 = L.scan_forward_v4_maps(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, repair=10 ** 6,
                                         super_fallback=fallback)
         assert np.array_equal(host(U2), Us) and np.array_equal(host(S2), Ss)
+        # converged default: overflowed super maps passed as stored, the repair fixes the starts
+        U2, S2 = L.scan_forward_v4_maps(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
+        assert np.array_equal(host(U2), Us) and np.array_equal(host(S2), Ss)
+        with pytest.raises(ValueError):
+            L.scan_forward_v4_maps(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, repair=1,
+                                   super_fallback="none")
         U2, S2 = L.scan_forward_v4(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, repair=10 ** 6)
         assert np.array_equal(host(U2), Us) and np.array_equal(host(S2), Ss)
 

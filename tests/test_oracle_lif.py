@@ -487,3 +487,23 @@ def test_carry_super_chunks_continues_the_inner_carry():
             bad = keep["SOVF"][s_] > 0
             want = end if fallback == "chunks" else full
             assert np.array_equal(ss[s_ + 1][bad], want[bad]), (fallback, s_)
+
+
+def test_carry_super_as_stored_then_repair_is_serial():
+    """Fallback "none" passes an overflowed super map as stored: its next start is the stored
+    map's value (a start that may be wrong), and with repair to convergence the scan is the
+    serial recurrence all the same."""
+    T, N, C, G = 4096, 96, 64, 8
+    I = normal(T, N, 0.012, 0.08, 35)
+    u0 = uniform(N, 0.0, 1.0, 36)
+    keep = {}
+    U, S = O.scan_forward_v4(I, 0.99, 1.0, 0.0, u0, C=C, G=G, K=4, K2=8, repair=T // C, keep=keep,
+                             super_fallback="none")
+    assert keep["SOVF"].mean() > 0.2
+    ss = keep["sstarts"]
+    for s_ in range(ss.shape[0] - 1):
+        want = O.eval_map(keep["SA"][s_], keep["SB"][s_], keep["SX"][s_], keep["SC"][s_],
+                          keep["SN"][s_], ss[s_])
+        assert np.array_equal(ss[s_ + 1], want), s_
+    Us, Ss = O.serial_forward(I, 0.99, 1.0, 0.0, u0)
+    assert np.array_equal(U, Us) and np.array_equal(S, Ss)

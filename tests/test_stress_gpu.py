@@ -85,7 +85,10 @@ def test_stress_exact_paths_equal_serial(L, dev, row):
         "warm-started": lambda: L.scan_forward_warm(Ig, beta, 1.0, 0.0, z, C=256),
         "single pass": lambda: L.scan_forward_exact(Ig, beta, 1.0, 0.0, z),
         "single pass maps": lambda: L.scan_forward_exact(Ig, beta, 1.0, 0.0, z, C=32, K=8, maps=True),
-        "three-level": lambda: L.scan_forward_v4_maps(Ig, beta, 1.0, 0.0, z, C=64, G=16, K=16, K2=32, repair=R),
+        "three-level": lambda: L.scan_forward_v4_maps(Ig, beta, 1.0, 0.0, z, C=64, G=16, K=16, K2=32, repair=R,
+                                                      super_fallback="chunks"),
+        "three-level as stored": lambda: L.scan_forward_v4_maps(Ig, beta, 1.0, 0.0, z, C=64, G=16, K=16,
+                                                                K2=32, repair=R),
         "three-level serial fallback": lambda: L.scan_forward_v4_maps(
             Ig, beta, 1.0, 0.0, z, C=64, G=16, K=16, K2=32, repair=R, super_fallback="serial"),
     }

@@ -1135,6 +1135,8 @@ struct ReplayInto {
   float *U, *S, *ends;
   int* done;
 };
+constexpr int kStagedCarryMaxBlocks = 256;  // one staged block per CU of the MI355X
+
 template <int KMAX>
 static bool launch_carry(const float* I, const float* u0, const float* lo_neuron, char* ws,
                          const lsh_v3_layout& L, int64_t N, int M, int C, int K, float beta,
@@ -1163,7 +1165,11 @@ static bool launch_carry(const float* I, const float* u0, const float* lo_neuron
                        reinterpret_cast<WsHeader*>(ws), N, M, C, K, beta, theta, u_r);
     return false;
   }
-  if (M >= 4 * CarryStage<KMAX>::R && KMAX <= 32) {
+  // The staged carry's LDS (two stages of R chunk maps, ~130 KB at K 8) leaves one block per CU,
+  // so beyond one block per CU its walks run in rounds while the lane carry keeps every walk
+  // resident.  Measured at cfg2 (N 65536, 1024 blocks), the map scan at C 32 / 64 (K 8): beta
+  // 0.9 1.97 / 1.50 -> 1.72 / 1.33 ms, beta 0.99 2.34 / 1.85 -> 1.49 / 1.29 ms with the lane carry.
+  if (M >= 4 * CarryStage<KMAX>::R && KMAX <= 32 && NB <= kStagedCarryMaxBlocks) {
     // long chunk sequences: map reads staged through LDS by three loader waves
     hipLaunchKernelGGL((k_lif_carry_staged<KMAX>), dim3((unsigned)NB), dim3(256), 0, st, I, u0,
                        F(L.EC), F(L.EA), F(L.EB), F(L.MA), F(L.MB), Iq(L.CNT), Iq(L.OVFRAW), F(L.MX),

@@ -630,7 +630,8 @@ def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=
     G chunk maps (as the inner carry does; an overflowed chunk map runs its C steps serially),
     "serial" runs its C*G steps serially (the reference's carry, triton_lif.py:958-963), "none"
     evaluates it as stored (a start the repair replaces where it is wrong: only with the repair
-    budget at least T/C and no stats), "auto" is "none" there and "chunks" otherwise.  With the
+    budget at least T/C and no stats), "auto" is "none" there for groups of 16 chunks or more
+    (AUTO_V4_AS_STORED_MIN_G) and "chunks" otherwise.  With the
     repair budget at least T/C and no stats requested, the result is the serial recurrence and
     the fastest exact path computes it, as in scan_forward_v3 (scan_forward_v4_maps runs the
     three-level pipeline itself)."""
@@ -642,6 +643,17 @@ def scan_forward_v4(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, BN=32, nw=
             return out
     return scan_forward_v4_maps(I, beta, theta, u_r, u0, C=C, G=G, K=K, K2=K2, repair=repair,
                                 stats=stats, super_fallback=super_fallback)
+
+
+# Converged calls pass an overflowed super map as stored ("none") from groups of this many
+# chunks: the walk over a group's chunk maps grows with G, the repair of the starts the stored
+# map gets wrong does not.  Measured on MI355X, scan_forward_v4_maps with repair to
+# convergence, K 16, K2 32, beta 0.99, "none" against "chunks" (ms): G 16 (C 64): cfg4 15.6 /
+# 18.5; N 128 / 1024, T 2^18, x ~ N(0.15, 0.4^2) 1.12 / 1.17, 2.94 / 3.07; N 4096 / 16384 at
+# N*T = 2^28, x ~ N(0.012, 0.08^2) 8.35 / 9.73, 4.31 / 4.66; N 128 / 1024, T 65536 1.02 / 0.92,
+# 2.12 / 2.05.  G 8 (C 128): 0.77 / 0.77, 2.51 / 2.53; 8.01 / 7.53, 3.90 / 3.72; 1.35 / 0.91,
+# 2.59 / 1.74.
+AUTO_V4_AS_STORED_MIN_G = 16
 
 
 def scan_forward_v4_maps(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, repair=0, stats=None,
@@ -663,7 +675,7 @@ def scan_forward_v4_maps(I, beta, theta, u_r, u0, C=64, G=16, K=16, K2=32, repai
         raise ValueError("three-level scan needs 1 <= K <= 32 and K <= K2 <= 64")
     rep = _repair_arg(repair, T // C, stats)
     if super_fallback == "auto":
-        super_fallback = "none" if rep == -1 else "chunks"
+        super_fallback = "none" if rep == -1 and G >= AUTO_V4_AS_STORED_MIN_G else "chunks"
     if super_fallback == "none" and rep != -1:
         raise ValueError('super_fallback="none" needs repair >= T/C and no stats (the repair '
                          'replaces the starts it gets wrong)')

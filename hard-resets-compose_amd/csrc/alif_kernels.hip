@@ -313,9 +313,10 @@ constexpr int kAlifTS = 32;   // steps per tile (LDS: 5 x 16 neurons x 33 floats
 
 // Waves per SIMD the build is compiled for (registers <= 512 / WPE per lane).  Measured at cfg5
 // (N 16384, T 4096, BN 4, dw 0.1q / 0.3q) with the per-wave tile phases: 6 (80 VGPRs) 1.68 /
-// 2.13 ms, 7 (72 VGPRs, more spilled) 1.88 / 2.32 ms.  The kernel is VALU-bound (at cfg5 its
-// 8566 VALU instructions per wave, at 4 cycles each, fill the SIMDs' issue cycles over the
-// launch), so a seventh wave hides nothing and its extra spills cost instructions.
+// 2.13 ms, 7 (72 VGPRs, more spilled) 1.88 / 2.32 ms.  The kernel is bound by instruction issue
+// (at cfg5 7321 VALU and 5127 scalar instructions per wave; the VALU ones at 4 cycles each fill
+// 89 % of the SIMDs' cycles over the launch, the rest waits on the chains between compares, mask
+// logic and selects), so a seventh wave hides little and its extra spills cost instructions.
 #ifndef LSH_ALIF_BUILD_WPE
 #define LSH_ALIF_BUILD_WPE 6
 #endif
@@ -458,38 +459,46 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
       const float wlo = sLo[ln][k], whi = sHi[ln][k];
       const float lwl = sLwl[ln][k], lwh = sLwh[ln][k];
       // does any neuron of the wave hold pieces in register 1 (slots 16..31)?
-      const bool hi_p = __ballot(npc > 16) != 0ull;
+      const bool hi_p = wave_ballot(npc > 16) != 0ull;
       // 1. advance the post-spike pieces; a piece spikes for x <= (v - theta0 - pof)/pa.  Every
       // piece first takes the update of an uncut piece, in place; a split below rebuilds the
       // fields of the cut neurons from these updated fields and from v, rho*pof and z.  Slots
       // from npc on hold no piece: their tests are false, and their (u, a, of), advanced with
       // the others, are never read (a slot that receives a piece gets every field written).
-      const bool va0 = i < npc;
+      // The tests are kept as wave masks (a lane's test is its bit): a mask is the compare's
+      // own result, where a per-lane bool combined with another is turned into a 0/1 value
+      // and compared again for each ballot and each use in another block.
       const float v0 = lif_v(pu[0], x, beta);
       const float rr0 = (v0 - theta0) - pof[0];
       const float pa0 = pa[0];
-      const bool es0 = va0 & (rr0 > pa0 * pxl[0]);
-      const bool en0 = va0 & (rr0 < pa0 * pxr[0]);
+      const unsigned long long va0m = wave_ballot(i < npc);
+      const unsigned long long es0m = va0m & wave_ballot(rr0 > pa0 * pxl[0]);
+      const unsigned long long en0m = va0m & wave_ballot(rr0 < pa0 * pxr[0]);
+      const bool es0 = __builtin_amdgcn_inverse_ballot_w64(es0m);
+      const bool en0 = __builtin_amdgcn_inverse_ballot_w64(en0m);
       const float ro0 = rho * pof[0];
       pu[0] = es0 ? u_r : v0;
       pof[0] = es0 ? ro0 + q : ro0;
       pa[0] = rho * pa0;
-      unsigned long long cb = __ballot(es0 & en0);
-      bool es1 = false, en1 = false;
-      float v1 = 0.0f, rr1 = 0.0f, pa1 = 1.0f, ro1 = 0.0f;
+      unsigned long long cb = es0m & en0m;
+      unsigned long long es1m = 0ull, en1m = 0ull;
+      float v1, rr1, pa1, ro1;  // read only where hi_p
       if (hi_p) {
-        const bool va1 = 16 + i < npc;
         v1 = lif_v(pu[1], x, beta);
         rr1 = (v1 - theta0) - pof[1];
         pa1 = pa[1];
-        es1 = va1 & (rr1 > pa1 * pxl[1]);
-        en1 = va1 & (rr1 < pa1 * pxr[1]);
+        const unsigned long long va1m = wave_ballot(16 + i < npc);
+        es1m = va1m & wave_ballot(rr1 > pa1 * pxl[1]);
+        en1m = va1m & wave_ballot(rr1 < pa1 * pxr[1]);
+        const bool es1_ = __builtin_amdgcn_inverse_ballot_w64(es1m);
         ro1 = rho * pof[1];
-        pu[1] = es1 ? u_r : v1;
-        pof[1] = es1 ? ro1 + q : ro1;
+        pu[1] = es1_ ? u_r : v1;
+        pof[1] = es1_ ? ro1 + q : ro1;
         pa[1] = rho * pa1;
-        cb |= __ballot(es1 & en1);
+        cb |= es1m & en1m;
       }
+      const bool es1 = __builtin_amdgcn_inverse_ballot_w64(es1m);
+      const bool en1 = __builtin_amdgcn_inverse_ballot_w64(en1m);
       unsigned long long cutm;  // lanes of the neurons whose block has a cut
       if (GW == 1) {
         cutm = block_lanes<BLK>(cb);
@@ -536,11 +545,11 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
           if (ntot > K2) ovf = 1;
         }
         __builtin_amdgcn_wave_barrier();
-        const bool hi_o = __ballot(cut && n_new > 16) != 0ull;
+        const bool hi_o = wave_ballot(cut && n_new > 16) != 0ull;
         // every gather first, then each field replaced once: a kept part of source piece s has
         // bounds from s's and z, u = u_r (spiking part) or v_s, a = rho*a_s (s's updated a),
         // of = rho*of_s (+ q for the spiking part)
-        auto gather = [&](float f0, float f1, int sl, bool s1) {
+        auto gather = [&](float f0, const float& f1, int sl, bool s1) {  // f1 read where hi_p
           const float a0 = __shfl(f0, sl, WAVE);
           const float a1 = hi_p ? __shfl(f1, sl, WAVE) : 0.0f;
           return s1 ? a1 : a0;
@@ -597,12 +606,13 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
         npc = cut ? n_new : npc;
       }
       // 2. first-spike line of this step: added unless a line dominates it on [wlo, whi]
-      const bool hi_l = __ballot(nl > 16) != 0ull;
-      unsigned long long bl =
-          __ballot((i < nl) & (ls[0] * wlo + lc[0] <= lwl) & (ls[0] * whi + lc[0] <= lwh));
+      const bool hi_l = wave_ballot(nl > 16) != 0ull;
+      unsigned long long bl = wave_ballot(i < nl) & wave_ballot(ls[0] * wlo + lc[0] <= lwl) &
+                              wave_ballot(ls[0] * whi + lc[0] <= lwh);
       if (hi_l)
-        bl |= __ballot((16 + i < nl) & (ls[1] * wlo + lc[1] <= lwl) & (ls[1] * whi + lc[1] <= lwh));
-      const unsigned long long newm = __ballot(wlo < whi) & ~block_lanes<1>(bl) & vmask;
+        bl |= wave_ballot(16 + i < nl) & wave_ballot(ls[1] * wlo + lc[1] <= lwl) &
+              wave_ballot(ls[1] * whi + lc[1] <= lwh);
+      const unsigned long long newm = wave_ballot(wlo < whi) & ~block_lanes<1>(bl) & vmask;
       if (newm != 0ull) {
         // the new line goes to slot nl and its piece to slot npc, written by selects on both
         // registers so the slots stay in registers; the whole block is skipped on the (most)

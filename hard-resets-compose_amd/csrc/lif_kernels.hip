@@ -318,17 +318,21 @@ __global__ __launch_bounds__(64) void k_lif_build(
     const float num = (theta - x) - beta * B;
     const float den = beta * A;
     const float z = den == 0.0f ? (num > 0.0f ? INFINITY : -INFINITY) : num / den;
-    bool nw = (z < xmin) && (z <= hi);
-    if (nw && cnt >= K) ovf = true;
-    nw = nw && (cnt < K);
-    if (__ballot(nw) != 0ull) {  // few steps add a breakpoint anywhere in the wave
+    // the tests as wave masks (each a compare's own result; a combination of per-lane bools
+    // would be ballotted through a 0/1 value and another compare)
+    const unsigned long long nw0m = wave_ballot(z < xmin) & wave_ballot(z <= hi);
+    const unsigned long long fullm = wave_ballot(cnt >= K);
+    if (__builtin_amdgcn_inverse_ballot_w64(nw0m & fullm)) ovf = true;
+    const unsigned long long nwm = nw0m & ~fullm;
+    const bool nw = __builtin_amdgcn_inverse_ballot_w64(nwm);
+    if (nwm != 0ull) {  // few steps add a breakpoint anywhere in the wave
 #pragma unroll
       for (int i = 0; i < KMAX; ++i) {
         const bool put = nw && (i == cnt);
         xd[i] = put ? z : xd[i];
         cd[i] = put ? u_r : cd[i];
       }
-      if (__ballot(nw && cnt == wc) != 0ull) ++wcnt;
+      if ((nwm & wave_ballot(cnt == wc)) != 0ull) ++wcnt;
     }
     cnt += nw ? 1 : 0;
     xmin = nw ? z : xmin;
@@ -566,10 +570,10 @@ __global__ __launch_bounds__(64) void k_lif_carry_wave(
         const float lo = lo_neuron ? lo_n : l - margin * (fabsf(l) + 1.0f);
         l = fminf(ec, __fadd_rn(__fmul_rn(ea, l), eb));
         const bool in_row = row == r;
-        const int gt = __popcll(__ballot(in_row && slot < cnt && cur.xd[g] > lo));
+        const int gt = __popcll(wave_ballot(in_row && slot < cnt && cur.xd[g] > lo));
         const int ne = min(cnt, gt + 1);
         const bool ovf = ovfr && gt == cnt;
-        const int k = __popcll(__ballot(in_row && slot < ne && cur.xd[g] > u));
+        const int k = __popcll(wave_ballot(in_row && slot < ne && cur.xd[g] > u));
         const float cval = lane_f(cur.cd[g], RW * r + min(k, RW - 1));
         float nu = (k == ne)
                        ? __fadd_rn(__fmul_rn(lane_f(cur.ma, c), u), lane_f(cur.mb, c))

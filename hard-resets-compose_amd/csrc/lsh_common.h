@@ -228,6 +228,12 @@ __device__ __forceinline__ bool stream_rows_until(const float* __restrict__ p,
   return false;
 }
 
+// Ballot of a bool over the active lanes: the lanes' compare mask itself (__ballot(int) goes
+// through a 0/1 value in a VGPR and a compare, two VALU instructions more).
+__device__ __forceinline__ unsigned long long wave_ballot(bool p) {
+  return __builtin_amdgcn_ballot_w64(p);
+}
+
 __device__ __forceinline__ int wave_max_i(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, WAVE));

@@ -104,6 +104,36 @@ def test_scan_v3_matches_oracle(L, dev, beta, mu, sd):
         assert st2["repair_iters"] == sto2["repair_iters"]
 
 
+@pytest.mark.parametrize("C,beta,mu,sd", [(512, 0.99, 0.012, 0.08), (2048, 0.99, 0.012, 0.08),
+                                          (1024, 0.9, 0.15, 0.4), (256, 0.5, 0.15, 0.4)])
+def test_scan_v3_long_chunks_32_slots_match_oracle(L, dev, C, beta, mu, sd):
+    """Long chunks with 32 slots (cfg4's chunk lengths, up to 33 pieces a map at beta 0.99):
+    U, S, starts, the kept breakpoints and constants, overflow flags and stats equal the oracle's
+    bit for bit at repair = 0 (N = 130, a ragged second wave)."""
+    T, N, K = 4096, 130, 32
+    I = normal(T, N, mu, sd, 41)
+    u0 = uniform(N, 0.0, 1.0, 42)
+    print(f"v3 long chunks C={C} beta={beta} K=32", flush=True)
+    st, sto, keep = {}, {}, {}
+    U, S = L.scan_forward_v3(gpu(I, dev), beta, 1.0, 0.0, gpu(u0, dev), C=C, K=K, stats=st)
+    run = L.last_scan_run()
+    Uo, So = O.scan_forward_v3(I, beta, 1.0, 0.0, u0, C=C, K=K, stats=sto, keep=keep)
+    assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+    assert np.array_equal(host(run.view("LO")), keep["Lo"])
+    assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+    n = host(run.view("MN", torch.int32))
+    assert np.array_equal(n, keep["n"])
+    assert np.array_equal(host(run.view("OVF", torch.int32)), keep["ovf"])
+    assert np.array_equal(host(run.view("MA")), keep["A"])
+    assert np.array_equal(host(run.view("MB")), keep["B"])
+    valid = np.arange(K)[None, :, None] < n[:, None, :]
+    assert np.array_equal(host(run.view("MX"))[valid], keep["xd"][valid])
+    assert np.array_equal(host(run.view("MC"))[valid], keep["cd"][valid])
+    assert st["mean_pieces"] == pytest.approx(sto["mean_pieces"], rel=1e-12)
+    assert st["max_pieces"] == sto["max_pieces"]
+    print(f"  max pieces {sto['max_pieces']}, mean {sto['mean_pieces']:.2f}", flush=True)
+
+
 @pytest.mark.parametrize("K", [4, 8, 16, 32])
 def test_scan_v3_long_sequence_wave_carry(L, dev, K):
     """Many chunks per neuron (M = 1024) with few neurons (N = 130: the carry takes one wave per

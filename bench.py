@@ -894,7 +894,7 @@ def counters_workload(torch, dev):
     statistics (k_alif_repair); cfg2's map scan at C = 128, K = 8
     (k_lif_build<8,8>, k_lif_carry<8>); at cfg4: the converged forward (k_lif_fwd_warm,
     k_lif_repair_wide), the long-chunk map scan in pieces (k_lif_build<32,8>,
-    k_lif_carry_staged<32>) and with the associative carry (k_map_scan), v4 at C 2048 / G 4 /
+    k_lif_carry_wave<32>) and with the associative carry (k_map_scan), v4 at C 2048 / G 4 /
     K 32 / K2 64 and at the reference default (k_lif_compose, k_map_carry; with 1024 neurons the
     one-wave-per-neuron walks k_lif_env_lo_wave, k_map_carry_wave) and the look-back adjoint
     (k_lif_bwd_lookback<16,16,...>); with few neurons (N = 128, T = 65536): the map scan at C 256,

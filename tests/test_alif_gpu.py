@@ -205,8 +205,9 @@ def test_alif_box_scan_converged_few_chunks(AL, dev, M):
     (Ur, Wr, Sr), preds = _preds(I, beta, rho, q, u0, w0, C)
     for tag in ("oracle", "bad"):
         print(f"alif converged M={M} pred={tag}", flush=True)
-        U, W, S = AL.alif_scan_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev),
-                                       gpu(preds[tag], dev), 0.1 * q, C=C, K1=32, K2=32, BN=4, repair=10 ** 6)
+        U, W, S = AL.alif_scan_forward_maps(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev),
+                                            gpu(w0, dev), gpu(preds[tag], dev), 0.1 * q, C=C, K1=32,
+                                            K2=32, BN=4, repair=10 ** 6)
         assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), tag
         assert np.array_equal(host(S), Sr), tag
 
@@ -234,8 +235,9 @@ def test_alif_box_scan_chunk_not_multiple_of_16(AL, dev):
             assert np.array_equal(host(run.view(g)), keep[g]), (tag, g)
         assert np.array_equal(host(run.view("MISS", torch.int32)), keep["MISS"]), tag
         assert np.array_equal(host(U), Uo) and np.array_equal(host(W), Wo) and np.array_equal(host(S), So)
-        U, W, S = AL.alif_scan_forward(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev), gpu(w0, dev),
-                                       gpu(Wp, dev), 0.1 * q, C=C, K1=16, K2=32, BN=4, repair=10 ** 6)
+        U, W, S = AL.alif_scan_forward_maps(gpu(I, dev), beta, rho, q, 1.0, 0.0, gpu(u0, dev),
+                                            gpu(w0, dev), gpu(Wp, dev), 0.1 * q, C=C, K1=16, K2=32, BN=4,
+                                            repair=10 ** 6)
         assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), tag
         assert np.array_equal(host(S), Sr), tag
 
@@ -260,16 +262,52 @@ def test_alif_box_scan_with_repair_equals_serial(AL, dev, name, beta, rho, q, mf
                                            C=C, K1=16, K2=32, BN=block, repair=10 ** 6, stats=st)
             assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), (tag, block)
             assert np.array_equal(host(S), Sr), (tag, block)
-            # without stats the converged repair is the ordered chain pass: the same result
-            U, W, S = AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, gpu(Wp, dev), 0.1 * q,
-                                           C=C, K1=16, K2=32, BN=block, repair=10 ** 6)
+            # without stats the pipeline's converged repair is the ordered chain pass: the same
+            # result; alif_scan_forward itself then takes the serial forward
+            U, W, S = AL.alif_scan_forward_maps(Ig, beta, rho, q, 1.0, 0.0, ug, wg, gpu(Wp, dev),
+                                                0.1 * q, C=C, K1=16, K2=32, BN=block, repair=10 ** 6)
             assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), (tag, block, "chain")
             assert np.array_equal(host(S), Sr), (tag, block, "chain")
+            U, W, S = AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, gpu(Wp, dev), 0.1 * q,
+                                           C=C, K1=16, K2=32, BN=block, repair=10 ** 6)
+            assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr), (tag, block, "dispatch")
+            assert np.array_equal(host(S), Sr), (tag, block, "dispatch")
             if T * N <= 4096 * 200 and block == 4 and tag in ("oracle", "bad"):
                 A.scan_forward(I, beta, rho, q, 1.0, 0.0, u0, w0, Wp, 0.1 * q, C=C, K1=16, K2=32,
                                block=block, repair=10 ** 6, stats=sto)
                 assert st["repair_iters"] == sto["repair_iters"]
                 assert st["miss_frac"] == pytest.approx(sto["miss_frac"], abs=1e-12)
+
+
+def test_alif_converged_dispatch(AL, dev):
+    """alif_scan_forward with the repair budget at least T/C and neither stats nor phases computes
+    the serial recurrence by the serial forward (the same bits as the box-scan pipeline's
+    converged call), keeps the pipeline's argument checks, and runs the pipeline when phases or
+    stats are asked for or the budget is finite."""
+    beta, rho, q = 0.95, 0.995, 0.9
+    T, N, C = 1024, 70, 128
+    I = _inputs(beta, 2.0, T, N, 19)
+    u0 = np.zeros(N, np.float32)
+    w0 = uniform(N, 0.0, 0.1, 20)
+    (Ur, Wr, Sr), preds = _preds(I, beta, rho, q, u0, w0, C)
+    Ig, ug, wg, Wp = gpu(I, dev), gpu(u0, dev), gpu(w0, dev), gpu(preds["warm4"], dev)
+    print("alif converged dispatch", flush=True)
+    AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, Wp, 0.1 * q, C=C, repair=0)
+    before = AL.last_alif_run()
+    U, W, S = AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, Wp, 0.1 * q, C=C, repair=10 ** 6)
+    assert AL.last_alif_run() is before  # no box-scan pipeline ran
+    assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr) and np.array_equal(host(S), Sr)
+    ph = {}
+    U, W, S = AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, Wp, 0.1 * q, C=C, repair=10 ** 6,
+                                   phases=ph)
+    assert AL.last_alif_run() is not before and set(ph) == {"envelope", "build", "carry", "replay"}
+    assert np.array_equal(host(U), Ur) and np.array_equal(host(W), Wr) and np.array_equal(host(S), Sr)
+    with pytest.raises(ValueError):
+        AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, Wp, 0.1 * q, C=100, repair=10 ** 6)
+    with pytest.raises(ValueError):
+        AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, Wp[1:], 0.1 * q, C=C, repair=10 ** 6)
+    with pytest.raises(ValueError):
+        AL.alif_scan_forward(Ig, beta, rho, q, 1.0, 0.0, ug, wg, Wp, 0.1 * q, C=C, K2=24, repair=10 ** 6)
 
 
 @pytest.mark.parametrize("R", [1, 2, 5])

@@ -205,9 +205,12 @@ def test_cfg5_box_scan_with_repair_equals_serial(dev):
                                               BN=4, repair=10 ** 6, stats=st)
             assert torch.equal(U2, U) and torch.equal(W2, W) and torch.equal(S2, S), (name, dwq, st)
             print(f"  stats {st}", flush=True)
-            U2, W2, S2 = AL.alif_scan_forward(I, b, r, q, 1.0, 0.0, z, z, WP, dwq * q, C=C, K1=32, K2=32,
-                                              BN=4, repair=10 ** 6)  # no stats: the ordered chain
+            U2, W2, S2 = AL.alif_scan_forward_maps(I, b, r, q, 1.0, 0.0, z, z, WP, dwq * q, C=C, K1=32,
+                                                   K2=32, BN=4, repair=10 ** 6)  # no stats: the ordered chain
             assert torch.equal(U2, U) and torch.equal(W2, W) and torch.equal(S2, S), (name, dwq, "chain")
+            U2, W2, S2 = AL.alif_scan_forward(I, b, r, q, 1.0, 0.0, z, z, WP, dwq * q, C=C, K1=32, K2=32,
+                                              BN=4, repair=10 ** 6)  # the converged dispatch
+            assert torch.equal(U2, U) and torch.equal(W2, W) and torch.equal(S2, S), (name, dwq, "dispatch")
             del U2, W2, S2
     del I, U, W, S
     torch.cuda.empty_cache()

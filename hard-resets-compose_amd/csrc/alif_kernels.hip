@@ -605,14 +605,20 @@ __attribute__((amdgpu_waves_per_eu(LSH_ALIF_BUILD_WPE))) void k_alif_build(
         __builtin_amdgcn_wave_barrier();
         npc = cut ? n_new : npc;
       }
-      // 2. first-spike line of this step: added unless a line dominates it on [wlo, whi]
-      const bool hi_l = wave_ballot(nl > 16) != 0ull;
-      unsigned long long bl = wave_ballot(i < nl) & wave_ballot(ls[0] * wlo + lc[0] <= lwl) &
-                              wave_ballot(ls[0] * whi + lc[0] <= lwh);
-      if (hi_l)
-        bl |= wave_ballot(16 + i < nl) & wave_ballot(ls[1] * wlo + lc[1] <= lwl) &
-              wave_ballot(ls[1] * whi + lc[1] <= lwh);
-      const unsigned long long newm = wave_ballot(wlo < whi) & ~block_lanes<1>(bl) & vmask;
+      // 2. first-spike line of this step: added unless a line dominates it on [wlo, whi].  A
+      // step has a candidate line (wlo < whi) in some row of the wave on about a fifth of the
+      // steps at cfg5, so the dominance tests run only then.
+      const unsigned long long candm = wave_ballot(wlo < whi) & vmask;
+      unsigned long long newm = 0ull;
+      if (candm != 0ull) {
+        const bool hi_l = wave_ballot(nl > 16) != 0ull;
+        unsigned long long bl = wave_ballot(i < nl) & wave_ballot(ls[0] * wlo + lc[0] <= lwl) &
+                                wave_ballot(ls[0] * whi + lc[0] <= lwh);
+        if (hi_l)
+          bl |= wave_ballot(16 + i < nl) & wave_ballot(ls[1] * wlo + lc[1] <= lwl) &
+                wave_ballot(ls[1] * whi + lc[1] <= lwh);
+        newm = candm & ~block_lanes<1>(bl);
+      }
       if (newm != 0ull) {
         // the new line goes to slot nl and its piece to slot npc, written by selects on both
         // registers so the slots stay in registers; the whole block is skipped on the (most)

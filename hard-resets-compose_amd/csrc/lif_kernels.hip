@@ -280,7 +280,10 @@ __global__ __launch_bounds__(64) void k_lif_build(
   const bool valid = n < N;
   const int64_t nn = valid ? n : 0;  // invalid lanes run on neuron 0 and store nothing
   const float hi = fmaxf(u0[nn], fmaxf(theta, u_r));
-  float ec = INFINITY, ea = 1.0f, eb = 0.0f;
+  // the envelope's affine part (a, b) starts at (1, 0) and takes the step of the map's affine
+  // part (A, B) (a <- beta*a, b <- fl(fl(beta*b) + x)), so it is (A, B) itself: only its
+  // constant c is carried apart
+  float ec = INFINITY;
   float A = 1.0f, B = 0.0f, xmin = INFINITY;
   int cnt = 0;
   bool ovf = false;
@@ -294,10 +297,8 @@ __global__ __launch_bounds__(64) void k_lif_build(
   const float* __restrict__ Ip = I + (size_t)m * C * N + nn;
 
   auto step = [&](float x) {
-    // (a) envelope
+    // (a) envelope constant
     ec = fminf(u_r, lif_v(ec, x, beta));
-    ea = beta * ea;
-    eb = lif_v(eb, x, beta);
     // (b) existing constants pushed through the step (same arithmetic as the serial step).
     // wcnt is the same on every lane (it grows through a ballot): slots go in groups of 8
     // behind one scalar branch per group, with no per-slot masks; a slot above a lane's cnt
@@ -366,8 +367,8 @@ __global__ __launch_bounds__(64) void k_lif_build(
   if (!valid) return;
   const size_t o = (size_t)m * N + n;
   EC[o] = ec;
-  EA[o] = ea;
-  EB[o] = eb;
+  EA[o] = A;
+  EB[o] = B;
   MA[o] = A;
   MB[o] = B;
   CNT[o] = cnt;

@@ -165,8 +165,9 @@ def envelope_carry(u0, EC, EA, EB, margin=1e-5):
 
 
 def _safe_div(num, den):
-    """num/den with den == 0 -> +inf if num > 0 else -inf (fast.py:94-99, triton_lif.py:761)."""
-    with np.errstate(divide="ignore", invalid="ignore"):
+    """num/den with den == 0 -> +inf if num > 0 else -inf (fast.py:94-99, triton_lif.py:761); a
+    quotient beyond the float32 range rounds to +-inf, as the IEEE division on the device does."""
+    with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
         q = num / den
     return np.where(den == 0, np.where(num > 0, INF, -INF), q).astype(f32)
 

@@ -288,6 +288,10 @@ __global__ __launch_bounds__(64) void k_lif_build(
   int cnt = 0;
   bool ovf = false;
   int wcnt = 0;  // wave-uniform upper bound of cnt
+  // the lane's breakpoints newest first (register r holds breakpoint cnt-1-r): a new one shifts
+  // the others up by one register with a select on the lane's (wave-uniform mask) add flag,
+  // where writing it at register cnt would take a per-register compare with cnt as well; the
+  // stores below put them back in insertion order
   float xd[KMAX], cd[KMAX];
 #pragma unroll
   for (int i = 0; i < KMAX; ++i) {
@@ -327,11 +331,17 @@ __global__ __launch_bounds__(64) void k_lif_build(
     const unsigned long long nwm = nw0m & ~fullm;
     const bool nw = __builtin_amdgcn_inverse_ballot_w64(nwm);
     if (nwm != 0ull) {  // few steps add a breakpoint anywhere in the wave
+      // registers above wc hold no breakpoint in any lane (+inf, shifted onto +inf), so the
+      // shift stops at wc's group
 #pragma unroll
-      for (int i = 0; i < KMAX; ++i) {
-        const bool put = nw && (i == cnt);
-        xd[i] = put ? z : xd[i];
-        cd[i] = put ? u_r : cd[i];
+      for (int g = KMAX - G; g >= 0; g -= G) {
+        if (g <= wc) {
+#pragma unroll
+          for (int i = g + G - 1; i >= g; --i) {
+            xd[i] = nw ? (i == 0 ? z : xd[i - 1]) : xd[i];
+            cd[i] = nw ? (i == 0 ? u_r : cd[i - 1]) : cd[i];
+          }
+        }
       }
       if ((nwm & wave_ballot(cnt == wc)) != 0ull) ++wcnt;
     }
@@ -373,21 +383,25 @@ __global__ __launch_bounds__(64) void k_lif_build(
   MB[o] = B;
   CNT[o] = cnt;
   OVFRAW[o] = ovf ? 1 : 0;
+  // register r goes to slot cnt-1-r (insertion order, breakpoints descending) below cnt and to
+  // slot r above it (+inf and unused constants), each slot written once
 #pragma unroll
-  for (int i = 0; i < KMAX; ++i) {
-    if (i < K) {
-      const size_t os = ((size_t)m * K + i) * N + n;
-      MX[os] = xd[i];
-      MC[os] = cd[i];
+  for (int r = 0; r < KMAX; ++r) {
+    if (r < K) {
+      const int sl = r < cnt ? cnt - 1 - r : r;
+      const size_t os = ((size_t)m * K + sl) * N + n;
+      MX[os] = xd[r];
+      MC[os] = cd[r];
     }
   }
   if (XT) {  // a neuron's K slots contiguous ([M, N, K]), for walks with one wave per neuron
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i) {
-      if (i < K) {
-        const size_t ot = ((size_t)m * N + n) * K + i;
-        XT[ot] = xd[i];
-        CT[ot] = cd[i];
+    for (int r = 0; r < KMAX; ++r) {
+      if (r < K) {
+        const int sl = r < cnt ? cnt - 1 - r : r;
+        const size_t ot = ((size_t)m * N + n) * K + sl;
+        XT[ot] = xd[r];
+        CT[ot] = cd[r];
       }
     }
   }

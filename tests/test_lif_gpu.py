@@ -450,6 +450,39 @@ def test_scan_v4_matches_oracle(L, dev, beta, mu, sd, fallback):
         assert np.array_equal(host(U2), Us) and np.array_equal(host(S2), Ss)
 
 
+@pytest.mark.parametrize("beta,mu,sd", [(0.9, 0.15, 0.4), (0.99, 0.012, 0.08), (0.5, -0.1, 0.6)])
+def test_scan_v4_lane_compose_matches_oracle(L, dev, beta, mu, sd):
+    """The group composition with one lane per neuron (k_lif_compose; the test above has too few
+    neurons and super maps for it and takes the one-wave-per-neuron composition): N = 4160 with
+    four super maps gives 260 waves.  Super maps, starts, U and S equal the oracle bit for bit at
+    repair = 0, for K2 above, at and below twice K."""
+    T, N, C, G = 2048, 4160, 64, 8
+    I = normal(T, N, mu, sd, 27)
+    u0 = uniform(N, -0.3, 0.3, 28)
+    Ig, u0g = gpu(I, dev), gpu(u0, dev)
+    for K, K2 in ((16, 32), (8, 16), (8, 8)):
+        print(f"v4 lane compose beta={beta} mu={mu} K={K} K2={K2}", flush=True)
+        st, sto, keep = {}, {}, {}
+        U, S = L.scan_forward_v4(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, stats=st,
+                                 super_fallback="chunks")
+        run = L.last_scan_run()
+        Uo, So = O.scan_forward_v4(I, beta, 1.0, -0.1, u0, C=C, G=G, K=K, K2=K2, stats=sto, keep=keep,
+                                   super_fallback="chunks")
+        SN = host(run.view("SN", torch.int32))
+        assert np.array_equal(SN, keep["SN"])
+        assert np.array_equal(host(run.view("SOVF", torch.int32)), keep["SOVF"])
+        assert np.array_equal(host(run.view("SA")), keep["SA"])
+        assert np.array_equal(host(run.view("SB")), keep["SB"])
+        valid = np.arange(K2)[None, :, None] < SN[:, None, :]
+        assert np.array_equal(host(run.view("SX"))[valid], keep["SX"][valid])
+        assert np.array_equal(host(run.view("SC"))[valid], keep["SC"][valid])
+        assert np.array_equal(host(run.view("SSTARTS")), keep["sstarts"])
+        assert np.array_equal(host(run.view("STARTS")), keep["starts"])
+        assert np.array_equal(host(U), Uo) and np.array_equal(host(S), So)
+        print(f"  super pieces mean {sto['super_mean_pieces'] if 'super_mean_pieces' in sto else '-'}, "
+              f"super overflow {st.get('super_overflow_frac')}", flush=True)
+
+
 def test_scan_v4_rejects_bad_shapes(L, dev):
     I = torch.zeros(64 * 5, 8, device=dev)
     u0 = torch.zeros(8, device=dev)

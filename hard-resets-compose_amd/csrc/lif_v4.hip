@@ -171,14 +171,16 @@ __global__ __launch_bounds__(64) void k_lif_compose(
   float xmin = INFINITY;
 #pragma unroll
   for (int i = 0; i < K2MAX; ++i) xmin = (i < nH) ? fminf(xmin, X[i]) : xmin;
-  int wnH = wave_max_i(nH);
+  // the wave's largest slot counts, as scalars (the guards below are then scalar branches, where
+  // a lane-reduced value in a vector register would make each one an exec-mask update)
+  int wnH = __builtin_amdgcn_readfirstlane(wave_max_i(nH));
   for (int jj = 1; jj < G; ++jj) {
     const int64_t m = m0 + jj;
     const size_t o = (size_t)m * N + nn;
     const float Ag = MA[o], Bg = MB[o];
     const int ng = MN[o];
     ov |= OVF[o];
-    const int wng = wave_max_i(ng);
+    const int wng = __builtin_amdgcn_readfirstlane(wave_max_i(ng));
     float yd[KMAX], dd[KMAX];
 #pragma unroll
     for (int j = 0; j < KMAX; ++j) {
@@ -190,18 +192,22 @@ __global__ __launch_bounds__(64) void k_lif_compose(
         dd[j] = 0.0f;
       }
     }
-    // (1) the left map's constants pushed through the right map
+    // (1) the left map's constants pushed through the right map: c = #{j < ng : yd[j] > C}, a
+    // prefix of the strictly descending breakpoints, so the constant dd[c] is the one after the
+    // last breakpoint above C (dd[0] if none), picked up in the same pass
 #pragma unroll
     for (int i = 0; i < K2MAX; ++i) {
       if (i < wnH) {
         int c = 0;
+        float gc = dd[0];
 #pragma unroll
-        for (int j = 0; j < KMAX; ++j)
-          if (j < wng) c += (j < ng && yd[j] > Cc[i]) ? 1 : 0;
-        float gc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < KMAX; ++j)
-          if (j < wng) gc = (c == j) ? dd[j] : gc;
+        for (int j = 0; j < KMAX; ++j) {
+          if (j < wng) {
+            const bool gt = j < ng && yd[j] > Cc[i];
+            c += gt ? 1 : 0;
+            if (j + 1 < KMAX) gc = gt ? dd[j + 1] : gc;
+          }
+        }
         Cc[i] = (c == ng) ? __fadd_rn(__fmul_rn(Ag, Cc[i]), Bg) : gc;
       }
     }
@@ -214,17 +220,19 @@ __global__ __launch_bounds__(64) void k_lif_compose(
         bool nw = (j < ng) && (z < xmin) && (z <= hi) && (xmin > lo);
         if (nw && nH >= K2) ov = 1;
         nw = nw && (nH < K2);
+        if (__ballot(nw) != 0ull) {  // skipped where no lane of the wave keeps the breakpoint
 #pragma unroll
-        for (int i = 0; i < K2MAX; ++i) {
-          if (i <= wnH) {
-            const bool put = nw && (i == nH);
-            X[i] = put ? z : X[i];
-            Cc[i] = put ? dd[j] : Cc[i];
+          for (int i = 0; i < K2MAX; ++i) {
+            if (i <= wnH) {
+              const bool put = nw && (i == nH);
+              X[i] = put ? z : X[i];
+              Cc[i] = put ? dd[j] : Cc[i];
+            }
           }
+          if (__ballot(nw && nH == wnH) != 0ull) ++wnH;
+          nH += nw ? 1 : 0;
+          xmin = nw ? z : xmin;
         }
-        if (__ballot(nw && nH == wnH) != 0ull) ++wnH;
-        nH += nw ? 1 : 0;
-        xmin = nw ? z : xmin;
       }
     }
     // (3) affine parts

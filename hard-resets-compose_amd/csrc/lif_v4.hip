@@ -526,7 +526,7 @@ __global__ __launch_bounds__(64) void k_lif_env_lo_wave(const float* __restrict_
 struct SuperWindow {
   float a, b;  // lane j: map j of the window
   int cnt, ovf;
-  float xd[32], cd[32];  // VGPR g, lane 32h + s: slot s of map 2g + h
+  float xd[32], cd[32];  // VGPR g, lane RW h + s: slot s of map SPR g + h (k_map_carry_wave<RW>)
 };
 
 // The G chunk maps of super map s from u, with one wave per neuron (walk_chunk_maps's values):
@@ -578,50 +578,56 @@ __device__ __forceinline__ float wave_walk_chunk_maps(const float* __restrict__ 
   return u;
 }
 
+// RW lanes a super map (RW = 32 for K2 <= 32: two maps a register and windows of 64 maps;
+// RW = 64 for K2 <= 64: one map a register and windows of 32).
+template <int RW>
 __global__ __launch_bounds__(64) void k_map_carry_wave(
     const float* __restrict__ I, const float* __restrict__ u0, const float* __restrict__ MA,
     const float* __restrict__ MB, const int* __restrict__ MN, const int* __restrict__ OVF,
     const float* __restrict__ MX, const float* __restrict__ MC, float* __restrict__ starts,
     int64_t N, int M, int K, int64_t L, float beta, float theta, float u_r, ChunkMaps cm) {
+  static_assert(RW == 32 || RW == 64, "a super map takes a half or a whole wave");
+  constexpr int SPR = WAVE / RW;  // super maps a register
+  constexpr int WS = 32 * SPR;    // super maps a window
   if (M <= 0) return;
   const int64_t n = xcd_neuron(blockIdx.x, N);
   const int lane = threadIdx.x;
-  const int half = lane >> 5, slot = lane & 31;
+  const int half = lane / RW, slot = lane % RW;
   const int sl = min(slot, K - 1);
   auto load = [&](int w, SuperWindow& d) {
-    const size_t o = (size_t)min(w * 64 + lane, M - 1) * N + n;
+    const size_t o = (size_t)min(w * WS + lane, M - 1) * N + n;
     d.a = MA[o];
     d.b = MB[o];
     d.cnt = MN[o];
     d.ovf = OVF[o];
 #pragma unroll
     for (int g = 0; g < 32; ++g) {
-      const size_t os = ((size_t)min(w * 64 + 2 * g + half, M - 1) * K + sl) * N + n;
+      const size_t os = ((size_t)min(w * WS + SPR * g + half, M - 1) * K + sl) * N + n;
       d.xd[g] = MX[os];
       d.cd[g] = MC[os];
     }
   };
   float u = u0[n];
-  const int NW = (M + 63) / 64;
+  const int NW = (M + WS - 1) / WS;
   SuperWindow cur, nxt;
   load(0, cur);
   for (int w = 0; w < NW; ++w) {
     load(min(w + 1, NW - 1), nxt);
-    const int nc = min(64, M - w * 64);
+    const int nc = min(WS, M - w * WS);
     float st_o = 0.0f;
 #pragma unroll
     for (int g = 0; g < 32; ++g) {
-      for (int h = 0; h < 2; ++h) {
-        const int c = 2 * g + h;
+      for (int h = 0; h < SPR; ++h) {
+        const int c = SPR * g + h;
         if (c >= nc) break;
         const int cnt = __builtin_amdgcn_readlane(cur.cnt, c);
         const int k = __popcll(__ballot(half == h && slot < cnt && cur.xd[g] > u));
         float nu = k == cnt ? __fadd_rn(__fmul_rn(lane_f(cur.a, c), u), lane_f(cur.b, c))
-                            : lane_f(cur.cd[g], 32 * h + min(k, 31));
+                            : lane_f(cur.cd[g], RW * h + min(k, RW - 1));
         if (lane == c) st_o = u;
         if (cm.walk != kSuperAsStored && __builtin_amdgcn_readlane(cur.ovf, c) != 0) {
           // fallback through the map
-          const int64_t sm = (int64_t)w * 64 + c;
+          const int64_t sm = (int64_t)w * WS + c;
           if (!cm.walk)
             nu = wave_serial_rows(I, N, n, sm * L, L, u, beta, theta, u_r);
           else if (cm.K <= 16)
@@ -632,7 +638,7 @@ __global__ __launch_bounds__(64) void k_map_carry_wave(
         u = nu;
       }
     }
-    if (lane < nc) starts[(size_t)(w * 64 + lane) * N + n] = st_o;
+    if (lane < nc) starts[(size_t)(w * WS + lane) * N + n] = st_o;
     cur = nxt;
   }
 }
@@ -805,10 +811,11 @@ static void launch_super_carry(const float* I, const float* u0, char* w, const l
   const ChunkMaps cm{F(L.v3.MA), F(L.v3.MB), Iq(L.v3.MN), Iq(L.v3.OVF), F(L.v3.MX), F(L.v3.MC),
                      K, G, C, walk, xt ? F(L.XT) : nullptr, xt ? F(L.CT) : nullptr};
   const int64_t Lsteps = (int64_t)C * G;
-  if (K2MAX <= 32 && N <= LSH_V4_WAVE_MAX_N) {
-    hipLaunchKernelGGL(k_map_carry_wave, dim3((unsigned)N), dim3(WAVE), 0, st, I, u0, F(L.SA),
-                       F(L.SB), Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC), F(L.SSTARTS), N, M2, K2,
-                       Lsteps, beta, theta, u_r, cm);
+  if (K2 <= 64 && N <= LSH_V4_WAVE_MAX_N) {
+    auto kern = K2 <= 32 ? k_map_carry_wave<32> : k_map_carry_wave<64>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)N), dim3(WAVE), 0, st, I, u0, F(L.SA), F(L.SB),
+                       Iq(L.SN), Iq(L.SOVF), F(L.SX), F(L.SC), F(L.SSTARTS), N, M2, K2, Lsteps,
+                       beta, theta, u_r, cm);
     return;
   }
   // the chunk maps' slot capacity (K <= K2)

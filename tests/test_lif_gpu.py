@@ -412,7 +412,8 @@ def test_scan_v4_matches_oracle(L, dev, beta, mu, sd, fallback):
     u0 = uniform(N, -0.3, 0.3, 26)
     Ig, u0g = gpu(I, dev), gpu(u0, dev)
     Us, Ss = O.serial_forward(I, beta, 1.0, -0.1, u0)
-    for K, K2 in ((16, 32), (8, 16), (4, 4)):
+    # K2 = 64: the one-wave super carry with a whole wave per super map
+    for K, K2 in ((16, 32), (8, 16), (4, 4), (32, 64)):
         print(f"v4 beta={beta} mu={mu} K={K} K2={K2} fallback={fallback}", flush=True)
         st, sto, keep = {}, {}, {}
         U, S = L.scan_forward_v4(Ig, beta, 1.0, -0.1, u0g, C=C, G=G, K=K, K2=K2, stats=st,

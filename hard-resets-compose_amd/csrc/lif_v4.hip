@@ -520,9 +520,10 @@ __global__ __launch_bounds__(64) void k_lif_env_lo_wave(const float* __restrict_
   }
 }
 
-// Super-map carry (K2 <= 32): VGPR g holds super maps 2g and 2g + 1 of the window, lane 32h + s
-// slot s of map 2g + h; k = #{s < n : xd[s] > u} is a ballot over the map's half-wave and the
-// constant a lane read.  An overflowed map reads its L rows 64 at a time, one per lane.
+// Super-map carry with one wave per neuron (K2 <= 64): for K2 <= 32 VGPR g holds super maps 2g
+// and 2g + 1 of the window, lane 32h + s slot s of map 2g + h; for K2 <= 64 VGPR g holds map g on
+// the whole wave.  k = #{s < n : xd[s] > u} is a ballot over the map's lanes and the constant a
+// lane read.  An overflowed map reads its L rows 64 at a time, one per lane.
 struct SuperWindow {
   float a, b;  // lane j: map j of the window
   int cnt, ovf;

@@ -502,9 +502,10 @@ __global__ __launch_bounds__(64) void k_lif_env_lo_wave(const float* __restrict_
     float c1, a1, b1;
     load(min(w + 1, NW - 1), c1, a1, b1);
     const int nc = min(64, M - w * 64);
-    float lo_o = 0.0f;
+    // lane c keeps chunk c's entry bound l; the margin is applied to the window at once
+    float l_o = 0.0f;
     auto step = [&](int c) {
-      if (lane == c) lo_o = l - margin * (fabsf(l) + 1.0f);
+      l_o = lane == c ? l : l_o;
       l = fminf(lane_f(c0, c), __fadd_rn(__fmul_rn(lane_f(a0, c), l), lane_f(b0, c)));
     };
     if (nc == 64) {  // a full window, unrolled so that the lane reads run ahead of the chain
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(64) void k_lif_env_lo_wave(const float* __restrict_
     } else {
       for (int c = 0; c < nc; ++c) step(c);
     }
-    if (lane < nc) LO[(size_t)(w * 64 + lane) * N + n] = lo_o;
+    if (lane < nc) LO[(size_t)(w * 64 + lane) * N + n] = l_o - margin * (fabsf(l_o) + 1.0f);
     c0 = c1;
     a0 = a1;
     b0 = b1;

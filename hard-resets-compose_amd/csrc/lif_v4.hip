@@ -114,22 +114,39 @@ __global__ __launch_bounds__(64) void k_lif_trunc(const float* __restrict__ LO,
   const int64_t n = (int64_t)nb * WAVE + threadIdx.x;
   unsigned long long ovf_acc = 0, pcs_acc = 0;
   int pmax = 0;
-  if (n < N) {
-    for (int m = mb; m < M; m += MB) {
+  if (n < N && mb < M) {
+    // a chunk's loads do not wait for its count (every slot is read, the index clamped below
+    // K; the count masks the compares), and the next chunk's are issued before this one is
+    // counted (the last chunk reloads itself), so the walk waits on one load latency a chunk
+    struct Row {
+      float lo;
+      int cnt, ovr;
+      float x[KMAX];
+    };
+    auto load = [&](int m, Row& r) {
       const size_t o = (size_t)m * N + n;
-      const float lo = LO[o];
-      const int cnt = CNT[o];
+      r.lo = LO[o];
+      r.cnt = CNT[o];
+      r.ovr = OVFRAW[o];
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i) r.x[i] = MX[((size_t)m * K + min(i, K - 1)) * N + n];
+    };
+    Row cur, nxt;
+    load(mb, cur);
+    for (int m = mb; m < M; m += MB) {
+      load(m + MB < M ? m + MB : m, nxt);
       int gt = 0;
 #pragma unroll
-      for (int i = 0; i < KMAX; ++i)
-        if (i < K && i < cnt) gt += MX[((size_t)m * K + i) * N + n] > lo ? 1 : 0;
-      const int ne = min(cnt, gt + 1);
-      const bool ovf = OVFRAW[o] != 0 && gt == cnt;
+      for (int i = 0; i < KMAX; ++i) gt += (i < K && i < cur.cnt && cur.x[i] > cur.lo) ? 1 : 0;
+      const int ne = min(cur.cnt, gt + 1);
+      const bool ovf = cur.ovr != 0 && gt == cur.cnt;
+      const size_t o = (size_t)m * N + n;
       MN[o] = ne;
       OVF[o] = ovf ? 1 : 0;
       ovf_acc += ovf ? 1ull : 0ull;
       pcs_acc += (unsigned long long)ne;
       pmax = max(pmax, ne);
+      cur = nxt;
     }
   }
   ovf_acc = wave_sum_u64(ovf_acc);
